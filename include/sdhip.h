@@ -1,0 +1,177 @@
+/*
+ * sdhip.h -- the C ABI of the MI355X (gfx950) form of the operations that
+ * stable-diffusion.assembly takes over from ggml's CPU backend.
+ *
+ * The reference offers its operations to ggml through sources/sdasm.h
+ * (sdasm_compute_nodes, sdasm_work_size, sdasm_forget) and, inside, through
+ * one supported / work_size / compute triple per operation (sources/ops.h:26-62).
+ * This header is the same surface with ggml's types taken out: a tensor is a
+ * plain descriptor (ggml's type number, extents ne[4], strides nb[4] in bytes,
+ * a DEVICE pointer), the chain of element-wise nodes after an operation is a
+ * plain array of steps, and every compute call takes the caller's device work
+ * buffer (as ggml hands its wdata, sized by sdasm_work_size) and a HIP stream.
+ *
+ * Nothing here allocates device memory: the caller owns every tensor and the
+ * work buffer, as ggml owns them for the reference (SURVEY: ownership).
+ *
+ * Errors.  SDHIP_UNSUPPORTED is the reference's "not taken" (false / 0 from
+ * sdasm_compute_nodes, hooks.cc:29-55): the caller computes the node itself.
+ * SDHIP_ERROR is a programming error or a failed launch; sdhip_last_error()
+ * says which.  The reference aborts on those (SDASM_REQUIRE, memory.h:68-77);
+ * a library returns instead.
+ */
+#ifndef SDHIP_H
+#define SDHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types, numbered as ggml numbers them (GGML_TYPE_F32 = 0,
+ * GGML_TYPE_F16 = 1); the only two the reference's operations take
+ * (mul_mat.cc:181-194, conv2d.cc:320-331, attention.cc:828-845). */
+enum { SDHIP_TYPE_F32 = 0, SDHIP_TYPE_F16 = 1 };
+
+typedef enum { SDHIP_OK = 0, SDHIP_UNSUPPORTED = 1, SDHIP_ERROR = 2 } sdhip_status;
+
+/* A tensor as ggml_tensor describes its memory: ne[] extents, nb[] strides in
+ * bytes (nb[0] the element size for the layouts taken), data on the device. */
+typedef struct sdhip_tensor {
+    int32_t type;
+    int64_t ne[4];
+    int64_t nb[4];
+    void *data;
+} sdhip_tensor;
+
+/* One node of the chain after an operation (sources/fusion.h:51-61): an
+ * addition or a multiplication by `operand`, broadcast along each dimension
+ * whose extent is 1, in place on the operation's output; or SiLU of it. */
+enum { SDHIP_STEP_ADD = 0, SDHIP_STEP_MUL = 1, SDHIP_STEP_SILU = 2 };
+
+typedef struct sdhip_step {
+    int32_t kind;
+    sdhip_tensor operand; /* f32, nb[0] = 4; unused for SILU */
+} sdhip_step;
+
+#define SDHIP_MAX_STEPS 6
+
+/* The chain (sources/fusion.h:63-108, Epilogue): `count` steps applied in
+ * order to each output element while it is still on chip.  With `redirect`
+ * the operation writes into that tensor (same extents and strides as its own
+ * output) instead of its own -- a residual connection that ends the chain;
+ * with `from_redirect` its sum begins from what `redirect` holds (the
+ * residual already there), as Epilogue::from_redirect does. */
+typedef struct sdhip_epilogue {
+    int32_t count;
+    sdhip_step steps[SDHIP_MAX_STEPS];
+    const sdhip_tensor *redirect;
+    int32_t from_redirect;
+} sdhip_epilogue;
+
+/* ---------------------------------------------------------------- library */
+
+/* Makes `device` current for the calls of this thread and checks that it is
+ * a gfx950; returns SDHIP_ERROR on any other. */
+sdhip_status sdhip_init(int device);
+
+/* The text of the last SDHIP_ERROR or SDHIP_UNSUPPORTED of this thread. */
+const char *sdhip_last_error(void);
+
+/* The tuning that changes what is computed, in the reference's SDASM_TUNE
+ * syntax "name=value,..." (sources/kernels.h:91-135, parsed by cpu.cc:121-212):
+ * bits, input_bits, group, weight_group, quantize, winograd,
+ * winograd_positions, winograd4_positions, winograd_small_tiles, fuse.
+ * Returns SDHIP_ERROR naming the first unknown name.  "" resets the defaults. */
+sdhip_status sdhip_set_tuning(const char *text);
+/* The value of one tuning field, or -1 if it has no such name. */
+int sdhip_get_tuning(const char *name);
+
+/* Forgets what the library keeps derived from device memory in
+ * [begin, begin + size) -- the reference's sdasm_forget (sdasm.h:56-60,
+ * store.cc:241-266), called when that memory is about to change. */
+void sdhip_forget(const void *begin, size_t size);
+
+/* ---------------------------------------------------------------- MUL_MAT */
+
+/* GGML_OP_MUL_MAT of one weight matrix w (F16/F32, ne = [K, N, 1, 1]) by
+ * x (F32 contiguous, ne = [K, M1, M2, M3]) into y (F32 contiguous,
+ * ne = [N, M1, M2, M3]): y[n, m] = sum_k w[k, n] x[k, m].
+ * Replaces mul_mat_supported / mul_mat_work_size / mul_mat_compute
+ * (sources/ops.h:40-44; mul_mat.cc:181-194, 205-215, 1175-1196). */
+int sdhip_mul_mat_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y);
+size_t sdhip_mul_mat_work_size(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y);
+sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
+                           const sdhip_epilogue *chain, void *work, size_t work_size, void *stream);
+
+/* The same product with the GEGLU after it (fusion.h:110-127, fusion.cc:347-394):
+ * P = the product with its chain, split into halves along dimension 0;
+ * out[j, m] = P[j, m] * GELU(P[half + j, m]); the product itself (y) is never
+ * written.  Replaces mul_mat_gated_supported / mul_mat_compute_gated
+ * (ops.h:45-49; mul_mat.cc:1128-1173). */
+int sdhip_mul_mat_gated_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
+                                  const sdhip_tensor *out);
+sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
+                                 const sdhip_epilogue *chain, const sdhip_tensor *out, void *work, size_t work_size,
+                                 void *stream);
+
+/* ---------------------------------------------------------------- CONV_2D */
+
+/* GGML_OP_CONV_2D (ggml_conv_2d_direct): kernel ne = [KW, KH, IC, OC]
+ * (F16/F32 contiguous), input ne = [IW, IH, IC, N] (F32, nb[0] = 4), y
+ * ne = [OW, OH, OC, N] (F32 contiguous), op_params = {s0, s1, p0, p1, d0, d1}.
+ * The library takes it by Winograd F(4x4,3x3) / F(2x2,3x3) where the
+ * reference would (winograd_supported, four, small; winograd.cc:194-196,
+ * 1204-1206, 2107-2123) and directly otherwise (conv2d_supported,
+ * conv2d.cc:320-331).  Replaces conv2d_* and winograd_* of ops.h:26-38. */
+int sdhip_conv2d_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                           const int32_t op_params[6]);
+/* Which path a supported convolution takes: 0 direct, 2 Winograd F(2x2,3x3),
+ * 4 Winograd F(4x4,3x3); -1 if not supported. */
+int sdhip_conv2d_path(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                      const int32_t op_params[6]);
+size_t sdhip_conv2d_work_size(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                              const int32_t op_params[6]);
+sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                          const int32_t op_params[6], const sdhip_epilogue *chain, void *work, size_t work_size,
+                          void *stream);
+
+/* ---------------------------------------------------------------- FLASH_ATTN_EXT */
+
+/* GGML_OP_FLASH_ATTN_EXT without a mask (attention.cc:828-845): q ne =
+ * [d, lq, h, b] F32 (any strides, nb[0] = 4), k ne = [d, lk, hk, b] and v ne =
+ * [dv, lk, hk, b] F32 or F16, y ne = [dv, h, lq, b] F32 contiguous; head h
+ * reads key head h / (h / hk).  scale, max_bias and softcap are op_params[0..2];
+ * only max_bias = softcap = 0 is taken.  Replaces attention_supported /
+ * attention_work_size / attention_compute (ops.h:51-56). */
+int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                              const sdhip_tensor *y, float max_bias, float softcap);
+size_t sdhip_attention_work_size(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                                 const sdhip_tensor *y);
+sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                             const sdhip_tensor *y, float scale, float max_bias, float softcap, void *work,
+                             size_t work_size, void *stream);
+
+/* ---------------------------------------------------------------- GROUP_NORM, NORM */
+
+/* GGML_OP_GROUP_NORM (norm.cc:100-140): x, y F32 contiguous of one shape,
+ * `groups` groups of ceil(ne2 / groups) channels over ne[2], per image ne[3];
+ * then the chain (scale, shift, SiLU).  Replaces group_norm_supported /
+ * group_norm_compute (ops.h:58-61). */
+int sdhip_group_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y, int groups);
+sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
+                              const sdhip_epilogue *chain, void *stream);
+
+/* GGML_OP_NORM over ne[0] (norm.cc:148-175), then the chain.  Replaces
+ * norm_supported / norm_compute (ops.h:62-63). */
+int sdhip_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y);
+sdhip_status sdhip_norm(const sdhip_tensor *x, const sdhip_tensor *y, float eps, const sdhip_epilogue *chain,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,424 @@
+/*
+ * The oracle (oracle.h): TEST INFRASTRUCTURE, never part of the library.
+ * Built with -ffp-contract=off, so that each operation rounds as written.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ scalar math */
+
+/* sources/scalar_math.h:34-51: x clamped, n = round(x / ln 2) by the sum with
+ * 1.5 * 2^23, r = x - n ln 2 in two fused steps, Cephes' expf polynomial,
+ * 2^n from the exponent bits. */
+float oracle_exponential(float x) {
+    x = fminf(fmaxf(x, -87.3f), 88.73f);
+    const float magic = 12582912.0f;
+    const float z = fmaf(x, 1.44269504088896341f, magic);
+    const float n = z - magic;
+    float r = fmaf(n, -0.693359375f, x);
+    r = fmaf(n, 2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = fmaf(p, r, 1.3981999507e-3f);
+    p = fmaf(p, r, 8.3334519073e-3f);
+    p = fmaf(p, r, 4.1665795894e-2f);
+    p = fmaf(p, r, 1.6666665459e-1f);
+    p = fmaf(p, r, 5.0000001201e-1f);
+    p = fmaf(p * r, r, r) + 1.0f;
+    int32_t zi;
+    memcpy(&zi, &z, 4);
+    const uint32_t e = (uint32_t)(zi - 0x4b400000 + 127) << 23;
+    float two;
+    memcpy(&two, &e, 4);
+    return p * two;
+}
+
+/* scalar_math.h:54-56 */
+float oracle_silu(float x) { return x / (1.0f + oracle_exponential(-x)); }
+
+void oracle_silu_array(float *x, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = oracle_silu(x[i]);
+}
+
+/* scalar_math.h:58-63 */
+float oracle_gelu(float x) {
+    const float y = x * fmaf(0.044715f * x, x, 1.0f);
+    return x / (1.0f + oracle_exponential(-1.5957691216057308f * y));
+}
+
+/* ------------------------------------------------------------------ float64 */
+
+void oracle_exact_mul_mat(const float *w, int64_t ldw, const float *x, int64_t ldx, int64_t M, int64_t N,
+                          int64_t K, double *y, double *mag) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            double s = 0.0, a = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                const double p = (double)w[n * ldw + k] * (double)x[m * ldx + k];
+                s += p;
+                a += fabs(p);
+            }
+            y[m * N + n] = s;
+            mag[m * N + n] = a;
+        }
+    }
+}
+
+void oracle_exact_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
+                         int64_t kh, int64_t kw, int s0, int s1, int p0, int p1, int d0, int d1, int64_t oh,
+                         int64_t ow, double *y, double *mag) {
+    for (int64_t b = 0; b < n; ++b) {
+        for (int64_t o = 0; o < oc; ++o) {
+            for (int64_t oy = 0; oy < oh; ++oy) {
+                for (int64_t ox = 0; ox < ow; ++ox) {
+                    double s = 0.0, a = 0.0;
+                    for (int64_t c = 0; c < ic; ++c) {
+                        for (int64_t ky = 0; ky < kh; ++ky) {
+                            const int64_t yy = oy * s1 + ky * d1 - p1;
+                            if (yy < 0 || yy >= ih) continue;
+                            for (int64_t kx = 0; kx < kw; ++kx) {
+                                const int64_t xx = ox * s0 + kx * d0 - p0;
+                                if (xx < 0 || xx >= iw) continue;
+                                const double p = (double)w[((o * ic + c) * kh + ky) * kw + kx] *
+                                                 (double)x[((b * ic + c) * ih + yy) * iw + xx];
+                                s += p;
+                                a += fabs(p);
+                            }
+                        }
+                    }
+                    const int64_t at = ((b * oc + o) * oh + oy) * ow + ox;
+                    y[at] = s;
+                    mag[at] = a;
+                }
+            }
+        }
+    }
+}
+
+void oracle_exact_conv2d_at(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w,
+                            int64_t oc, int64_t kh, int64_t kw, int s0, int s1, int p0, int p1, int d0, int d1,
+                            int64_t oh, int64_t ow, const int64_t *index, int64_t count, double *y, double *mag) {
+    (void)n;
+    for (int64_t t = 0; t < count; ++t) {
+        const int64_t at = index[t];
+        const int64_t ox = at % ow;
+        const int64_t oy = (at / ow) % oh;
+        const int64_t o = (at / (ow * oh)) % oc;
+        const int64_t b = at / (ow * oh * oc);
+        double s = 0.0, a = 0.0;
+        for (int64_t c = 0; c < ic; ++c) {
+            for (int64_t ky = 0; ky < kh; ++ky) {
+                const int64_t yy = oy * s1 + ky * d1 - p1;
+                if (yy < 0 || yy >= ih) continue;
+                for (int64_t kx = 0; kx < kw; ++kx) {
+                    const int64_t xx = ox * s0 + kx * d0 - p0;
+                    if (xx < 0 || xx >= iw) continue;
+                    const double p = (double)w[((o * ic + c) * kh + ky) * kw + kx] *
+                                     (double)x[((b * ic + c) * ih + yy) * iw + xx];
+                    s += p;
+                    a += fabs(p);
+                }
+            }
+        }
+        y[t] = s;
+        mag[t] = a;
+    }
+}
+
+void oracle_exact_attention(const float *q, const float *k, const float *v, int64_t d, int64_t dv, int64_t lq,
+                            int64_t lk, int64_t h, int64_t hk, int64_t b, float scale, double *y, double *mag) {
+    double *w = (double *)malloc((size_t)lk * sizeof(double));
+    const int64_t group = h / hk;
+    for (int64_t bi = 0; bi < b; ++bi) {
+        for (int64_t hi = 0; hi < h; ++hi) {
+            const int64_t kh = hi / group;
+            for (int64_t i = 0; i < lq; ++i) {
+                const float *qi = q + ((bi * lq + i) * h + hi) * d;
+                double max = -HUGE_VAL;
+                for (int64_t j = 0; j < lk; ++j) {
+                    const float *kj = k + ((bi * lk + j) * hk + kh) * d;
+                    double s = 0.0;
+                    for (int64_t e = 0; e < d; ++e) s += (double)qi[e] * (double)kj[e];
+                    w[j] = s * (double)scale;
+                    if (w[j] > max) max = w[j];
+                }
+                double total = 0.0;
+                for (int64_t j = 0; j < lk; ++j) {
+                    w[j] = exp(w[j] - max);
+                    total += w[j];
+                }
+                for (int64_t e = 0; e < dv; ++e) {
+                    double s = 0.0, a = 0.0;
+                    for (int64_t j = 0; j < lk; ++j) {
+                        const double p = w[j] / total * (double)v[((bi * lk + j) * hk + kh) * dv + e];
+                        s += p;
+                        a += fabs(p);
+                    }
+                    const int64_t at = ((bi * lq + i) * h + hi) * dv + e;
+                    y[at] = s;
+                    mag[at] = a;
+                }
+            }
+        }
+    }
+    free(w);
+}
+
+void oracle_exact_attention_at(const float *q, const float *k, const float *v, int64_t d, int64_t dv, int64_t lq,
+                               int64_t lk, int64_t h, int64_t hk, int64_t b, float scale, const int64_t *query,
+                               int64_t count, double *y, double *mag) {
+    (void)b;
+    double *w = (double *)malloc((size_t)lk * sizeof(double));
+    const int64_t group = h / hk;
+    for (int64_t t = 0; t < count; ++t) {
+        const int64_t i = query[t] % lq;
+        const int64_t hi = (query[t] / lq) % h;
+        const int64_t bi = query[t] / (lq * h);
+        const int64_t kh = hi / group;
+        const float *qi = q + ((bi * lq + i) * h + hi) * d;
+        double max = -HUGE_VAL;
+        for (int64_t j = 0; j < lk; ++j) {
+            const float *kj = k + ((bi * lk + j) * hk + kh) * d;
+            double s = 0.0;
+            for (int64_t e = 0; e < d; ++e) s += (double)qi[e] * (double)kj[e];
+            w[j] = s * (double)scale;
+            if (w[j] > max) max = w[j];
+        }
+        double total = 0.0;
+        for (int64_t j = 0; j < lk; ++j) {
+            w[j] = exp(w[j] - max);
+            total += w[j];
+        }
+        for (int64_t e = 0; e < dv; ++e) {
+            double s = 0.0, a = 0.0;
+            for (int64_t j = 0; j < lk; ++j) {
+                const double p = w[j] / total * (double)v[((bi * lk + j) * hk + kh) * dv + e];
+                s += p;
+                a += fabs(p);
+            }
+            y[t * dv + e] = s;
+            mag[t * dv + e] = a;
+        }
+    }
+    free(w);
+}
+
+static double gelu64(double v) { return 0.5 * v * (1.0 + tanh(0.79788456080286535587989211986876 * (v + 0.044715 * v * v * v))); }
+
+void oracle_exact_gated(const float *w, const float *x, const float *bias, int64_t M, int64_t half, int64_t K,
+                        double *y, double *mag) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t j = 0; j < half; ++j) {
+            double sum[2], a[2];
+            for (int side = 0; side < 2; ++side) {
+                const int64_t n = side * half + j;
+                sum[side] = bias ? (double)bias[n] : 0.0;
+                a[side] = fabs(sum[side]);
+                for (int64_t e = 0; e < K; ++e) {
+                    const double p = (double)w[n * K + e] * (double)x[m * K + e];
+                    sum[side] += p;
+                    a[side] += fabs(p);
+                }
+            }
+            /* d/dv of GELU(v) lies within [-0.13, 1.13] (ops_test.cc:761-764). */
+            y[m * half + j] = sum[0] * gelu64(sum[1]);
+            mag[m * half + j] = a[0] * fabs(gelu64(sum[1])) + fabs(sum[0]) * 1.13 * a[1];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ chain */
+
+void oracle_apply_chain(float *out, const int64_t ne[4], int count, const int *kinds, const float *const *operands,
+                        const int64_t *nb) {
+    for (int64_t i3 = 0; i3 < ne[3]; ++i3)
+        for (int64_t i2 = 0; i2 < ne[2]; ++i2)
+            for (int64_t i1 = 0; i1 < ne[1]; ++i1)
+                for (int64_t i0 = 0; i0 < ne[0]; ++i0) {
+                    float *o = out + ((i3 * ne[2] + i2) * ne[1] + i1) * ne[0] + i0;
+                    float v = *o;
+                    for (int s = 0; s < count; ++s) {
+                        if (kinds[s] == 2) {
+                            v = oracle_silu(v);
+                            continue;
+                        }
+                        const int64_t *b = nb + 4 * s;
+                        const float op = operands[s][i0 * b[0] + i1 * b[1] + i2 * b[2] + i3 * b[3]];
+                        v = kinds[s] == 0 ? v + op : v * op;
+                    }
+                    *o = v;
+                }
+}
+
+/* ------------------------------------------------------------------ norms */
+
+/* The sum of a row in double, in 8 lanes (norm.cc:44-62). */
+static double row_sum(const float *x, int64_t n) {
+    double part[8] = {0};
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) part[l] += (double)x[i + l];
+    double s = 0.0;
+    for (; i < n; ++i) s += (double)x[i];
+    for (int l = 0; l < 8; ++l) s += part[l];
+    return s;
+}
+
+/* The squares of (x - mean) in single precision summed in double (norm.cc:64-84). */
+static double row_squares(const float *x, int64_t n, float mean) {
+    double part[8] = {0};
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) {
+            const float v = x[i + l] - mean;
+            part[l] += (double)(v * v);
+        }
+    double s = 0.0;
+    for (; i < n; ++i) {
+        const float v = x[i] - mean;
+        s += (double)(v * v);
+    }
+    for (int l = 0; l < 8; ++l) s += part[l];
+    return s;
+}
+
+void oracle_group_norm(const float *x, float *y, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int groups,
+                       float eps) {
+    const int64_t per = (ne2 + groups - 1) / groups;
+    const int64_t plane = ne0 * ne1;
+    for (int64_t i3 = 0; i3 < ne3; ++i3) {
+        for (int64_t g = 0; g < groups; ++g) {
+            const int64_t c0 = g * per;
+            const int64_t c1 = c0 + per < ne2 ? c0 + per : ne2;
+            if (c0 >= c1) continue;
+            const int64_t count = plane * (c1 - c0);
+            const float *in = x + (i3 * ne2 + c0) * plane;
+            float *out = y + (i3 * ne2 + c0) * plane;
+            const float mean = (float)(row_sum(in, count) / (double)count);
+            const float variance = (float)(row_squares(in, count, mean) / (double)count);
+            const float scale = 1.0f / sqrtf(variance + eps);
+            for (int64_t i = 0; i < count; ++i) out[i] = (in[i] - mean) * scale;
+        }
+    }
+}
+
+void oracle_norm(const float *x, float *y, int64_t ne0, int64_t rows, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *in = x + r * ne0;
+        float *out = y + r * ne0;
+        const float mean = (float)(row_sum(in, ne0) / (double)ne0);
+        const float variance = (float)(row_squares(in, ne0, mean) / (double)ne0);
+        const float scale = 1.0f / sqrtf(variance + eps);
+        for (int64_t i = 0; i < ne0; ++i) out[i] = (in[i] - mean) * scale;
+    }
+}
+
+/* ------------------------------------------------------------------ bits mode */
+
+static float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* quant.cc:282-315: least and greatest with 0 between them, scale (hi - lo) /
+ * levels, the inverse 0 for a scale of 0, the zero point rounded to the
+ * nearest-even, each byte rint(x * inverse) + zero clamped to [0, levels];
+ * the group's tail the zero point. */
+void oracle_quantize_input_row(const float *x, int64_t n, int64_t group, int levels, uint8_t *dst, float *scale,
+                               float *offset) {
+    float least = 0.0f, greatest = 0.0f;
+    for (int64_t e = 0; e < n; ++e) {
+        least = fminf(least, x[e]);
+        greatest = fmaxf(greatest, x[e]);
+    }
+    const float s = (greatest - least) / (float)levels;
+    const float inverse = s > 0.0f ? 1.0f / s : 0.0f;
+    const float zero = nearbyintf(-least * inverse);
+    const float top = (float)levels;
+    int64_t e = 0;
+    for (; e < n; ++e) dst[e] = (uint8_t)clampf(nearbyintf(x[e] * inverse) + zero, 0.0f, top);
+    for (; e < group; ++e) dst[e] = (uint8_t)zero;
+    *scale = s;
+    *offset = s * zero;
+}
+
+/* quant.cc:204-243 with quantize_weight_group (186-199): the scale of the
+ * group's (or with weight_groups = 0, the whole row's) greatest magnitude over
+ * weight_max; each weight rint(w * inverse) clamped to +-weight_max; the
+ * offset the scale times the group's integer sum; zeros past k. */
+void oracle_quantize_weights(const float *w, int64_t ld, int64_t rows, int64_t k, int64_t group, int weight_max,
+                             int weight_groups, int8_t *q, float *scale, float *offset, int32_t *sums) {
+    const int64_t groups = (k + group - 1) / group;
+    const float max = (float)weight_max;
+    for (int64_t r = 0; r < rows; ++r) {
+        float row_max = 0.0f;
+        if (!weight_groups) {
+            for (int64_t e = 0; e < k; ++e) row_max = fmaxf(row_max, fabsf(w[r * ld + e]));
+        }
+        for (int64_t g = 0; g < groups; ++g) {
+            const int64_t n = k - g * group < group ? k - g * group : group;
+            float m = row_max;
+            if (weight_groups) {
+                for (int64_t e = 0; e < n; ++e) m = fmaxf(m, fabsf(w[r * ld + g * group + e]));
+            }
+            const float s = m / max;
+            const float inverse = s > 0.0f ? 1.0f / s : 0.0f;
+            int32_t sum = 0;
+            int8_t *dst = q + r * groups * group + g * group;
+            for (int64_t e = 0; e < group; ++e) {
+                const float v = e < n ? w[r * ld + g * group + e] : 0.0f;
+                const int32_t qv = (int32_t)clampf(nearbyintf(v * inverse), -max, max);
+                dst[e] = (int8_t)qv;
+                sum += qv;
+            }
+            scale[r * groups + g] = s;
+            offset[r * groups + g] = s * (float)sum;
+            sums[r * groups + g] = sum;
+        }
+    }
+}
+
+void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t N, int64_t K, int64_t group,
+                              int input_levels, int weight_max, int weight_groups, const float *init, float *y,
+                              uint8_t *xq, float *xscale, float *xoffset, int8_t *wq, float *wscale, float *woffset,
+                              int32_t *wsums) {
+    const int64_t groups = (K + group - 1) / group;
+    const int64_t kp = groups * group;
+    uint8_t *qx = xq ? xq : (uint8_t *)malloc((size_t)(M * kp));
+    float *sa = xscale ? xscale : (float *)malloc((size_t)(M * groups) * sizeof(float));
+    float *oa = xoffset ? xoffset : (float *)malloc((size_t)(M * groups) * sizeof(float));
+    int8_t *qw = wq ? wq : (int8_t *)malloc((size_t)(N * kp));
+    float *sb = wscale ? wscale : (float *)malloc((size_t)(N * groups) * sizeof(float));
+    float *ob = woffset ? woffset : (float *)malloc((size_t)(N * groups) * sizeof(float));
+    int32_t *qs = wsums ? wsums : (int32_t *)malloc((size_t)(N * groups) * sizeof(int32_t));
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t g = 0; g < groups; ++g) {
+            const int64_t n = K - g * group < group ? K - g * group : group;
+            oracle_quantize_input_row(x + m * K + g * group, n, group, input_levels, qx + m * kp + g * group,
+                                      &sa[m * groups + g], &oa[m * groups + g]);
+        }
+    }
+    oracle_quantize_weights(w, K, N, K, group, weight_max, weight_groups, qw, sb, ob, qs);
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float t = init ? init[m * N + n] : 0.0f;
+            for (int64_t g = 0; g < groups; ++g) {
+                int32_t s = 0;
+                const uint8_t *a = qx + m * kp + g * group;
+                const int8_t *b = qw + n * kp + g * group;
+                for (int64_t e = 0; e < group; ++e) s += (int32_t)a[e] * (int32_t)b[e];
+                const float ab = sa[m * groups + g] * sb[n * groups + g];
+                t = fmaf(ab, (float)s, t);
+                t = fmaf(-oa[m * groups + g], ob[n * groups + g], t);
+            }
+            y[m * N + n] = t;
+        }
+    }
+    if (!xq) free(qx);
+    if (!xscale) free(sa);
+    if (!xoffset) free(oa);
+    if (!wq) free(qw);
+    if (!wscale) free(sb);
+    if (!woffset) free(ob);
+    if (!wsums) free(qs);
+}

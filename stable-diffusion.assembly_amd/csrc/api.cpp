@@ -1,0 +1,232 @@
+// The C ABI of sdhip.h: the descriptors checked as the reference's
+// *_supported predicates check ggml's nodes, the path chosen as hooks.cc and
+// the ops choose it, and the kernels launched on the caller's stream.
+
+#include "../../include/sdhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "host.h"
+#include "kernels.h"
+
+namespace sdhip {
+
+namespace {
+
+thread_local std::string g_error;
+
+}  // namespace
+
+sdhip_status fail(sdhip_status s, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return s;
+}
+
+sdhip_status launched(hipError_t e, const char *what) {
+    if (e != hipSuccess) {
+        return fail(SDHIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+    }
+    return SDHIP_OK;
+}
+
+// ------------------------------------------------------------------ tuning
+
+Tuning &tuning() {
+    static Tuning t;
+    return t;
+}
+
+namespace {
+
+struct Field {
+    const char *name;
+    int Tuning::*member;
+};
+
+const Field kFields[] = {
+    {"bits", &Tuning::bits},
+    {"input_bits", &Tuning::input_bits},
+    {"group", &Tuning::group},
+    {"weight_group", &Tuning::weight_group},
+    {"quantize", &Tuning::quantize},
+    {"winograd", &Tuning::winograd},
+    {"winograd_positions", &Tuning::winograd_positions},
+    {"winograd4_positions", &Tuning::winograd4_positions},
+    {"winograd_small_tiles", &Tuning::winograd_small_tiles},
+    {"fuse", &Tuning::fuse},
+};
+
+}  // namespace
+
+// ------------------------------------------------------------------ descriptors
+
+bool holds_f32(const sdhip_tensor *t) { return t != nullptr && t->type == SDHIP_TYPE_F32 && t->nb[0] == 4; }
+bool holds_f16(const sdhip_tensor *t) { return t != nullptr && t->type == SDHIP_TYPE_F16 && t->nb[0] == 2; }
+
+bool contiguous(const sdhip_tensor *t) {
+    const int64_t size = t->type == SDHIP_TYPE_F16 ? 2 : 4;
+    return t->nb[0] == size && t->nb[1] == t->nb[0] * t->ne[0] && t->nb[2] == t->nb[1] * t->ne[1] &&
+           t->nb[3] == t->nb[2] * t->ne[2];
+}
+
+bool same_shape(const sdhip_tensor *a, const sdhip_tensor *b) {
+    for (int k = 0; k < 4; ++k) {
+        if (a->ne[k] != b->ne[k]) return false;
+    }
+    return true;
+}
+
+bool same_layout(const sdhip_tensor *a, const sdhip_tensor *b) {
+    if (!same_shape(a, b)) return false;
+    for (int k = 0; k < 4; ++k) {
+        if (a->nb[k] != b->nb[k]) return false;
+    }
+    return a->type == b->type;
+}
+
+int64_t nelements(const sdhip_tensor *t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }
+
+// The chain for an output of extents `ne`: each operand F32, nb[0] = 4, and
+// of the output's extent or 1 along each dimension (the broadcast ggml's ADD
+// and MUL take, fusion.cc:174-186).
+sdhip_status device_chain(const sdhip_epilogue *e, const int64_t ne[4], DevChain &c) {
+    c = DevChain{};
+    if (e == nullptr) return SDHIP_OK;
+    if (e->count < 0 || e->count > kMaxSteps) {
+        return fail(SDHIP_ERROR, "chain of %d steps (at most %d)", e->count, kMaxSteps);
+    }
+    for (int s = 0; s < e->count; ++s) {
+        const sdhip_step &st = e->steps[s];
+        DevStep &d = c.steps[s];
+        d.kind = st.kind;
+        if (st.kind == SDHIP_STEP_SILU) {
+            continue;
+        }
+        if (st.kind != SDHIP_STEP_ADD && st.kind != SDHIP_STEP_MUL) {
+            return fail(SDHIP_ERROR, "chain step %d of unknown kind %d", s, st.kind);
+        }
+        if (!holds_f32(&st.operand) || st.operand.data == nullptr) {
+            return fail(SDHIP_ERROR, "chain step %d: operand is not single precision with nb[0] = 4", s);
+        }
+        d.operand = static_cast<const float *>(st.operand.data);
+        for (int k = 0; k < 4; ++k) {
+            if (st.operand.ne[k] != ne[k] && st.operand.ne[k] != 1) {
+                return fail(SDHIP_ERROR, "chain step %d: operand extent %lld along %d is neither %lld nor 1", s,
+                            static_cast<long long>(st.operand.ne[k]), k, static_cast<long long>(ne[k]));
+            }
+            if (st.operand.nb[k] % 4 != 0) {
+                return fail(SDHIP_ERROR, "chain step %d: stride not a multiple of 4 bytes", s);
+            }
+            d.nb[k] = st.operand.ne[k] == 1 ? 0 : st.operand.nb[k] / 4;
+        }
+    }
+    c.count = e->count;
+    return SDHIP_OK;
+}
+
+// The tensor the operation writes: its own, or the chain's redirect, which
+// must have the output's extents and strides (fusion.cc:227-240).
+sdhip_status output_of(const sdhip_tensor *y, const sdhip_epilogue *e, float *&out, int32_t &from_redirect) {
+    out = static_cast<float *>(y->data);
+    from_redirect = 0;
+    if (e == nullptr || e->redirect == nullptr) {
+        if (e != nullptr && e->from_redirect) {
+            return fail(SDHIP_ERROR, "from_redirect without a redirect");
+        }
+        return SDHIP_OK;
+    }
+    const sdhip_tensor *r = e->redirect;
+    for (int k = 0; k < 4; ++k) {
+        if (r->ne[k] != y->ne[k] || r->nb[k] != y->nb[k]) {
+            return fail(SDHIP_ERROR, "redirect of another layout than the output");
+        }
+    }
+    if (r->type != SDHIP_TYPE_F32 || r->data == nullptr) {
+        return fail(SDHIP_ERROR, "redirect is not single precision");
+    }
+    out = static_cast<float *>(r->data);
+    from_redirect = e->from_redirect ? 1 : 0;
+    return SDHIP_OK;
+}
+
+}  // namespace sdhip
+
+using namespace sdhip;
+
+extern "C" {
+
+sdhip_status sdhip_init(int device) {
+    if (hipSetDevice(device) != hipSuccess) {
+        return fail(SDHIP_ERROR, "hipSetDevice(%d) failed", device);
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        return fail(SDHIP_ERROR, "hipGetDeviceProperties(%d) failed", device);
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        return fail(SDHIP_ERROR, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    }
+    return SDHIP_OK;
+}
+
+const char *sdhip_last_error(void) { return g_error.c_str(); }
+
+sdhip_status sdhip_set_tuning(const char *text) {
+    Tuning t;  // the defaults; the text changes them
+    if (text != nullptr) {
+        std::string s(text);
+        size_t at = 0;
+        while (at < s.size()) {
+            size_t end = s.find(',', at);
+            if (end == std::string::npos) end = s.size();
+            const std::string item = s.substr(at, end - at);
+            at = end + 1;
+            if (item.empty()) continue;
+            const size_t eq = item.find('=');
+            if (eq == std::string::npos) {
+                return fail(SDHIP_ERROR, "tuning item '%s' is not name=value", item.c_str());
+            }
+            const std::string name = item.substr(0, eq);
+            const std::string value = item.substr(eq + 1);
+            char *stop = nullptr;
+            const long v = std::strtol(value.c_str(), &stop, 10);
+            if (value.empty() || stop == nullptr || *stop != '\0') {
+                return fail(SDHIP_ERROR, "tuning value '%s' of %s is not a number", value.c_str(), name.c_str());
+            }
+            bool known = false;
+            for (const Field &f : kFields) {
+                if (name == f.name) {
+                    t.*(f.member) = static_cast<int>(v);
+                    known = true;
+                }
+            }
+            if (!known) {
+                return fail(SDHIP_ERROR, "unknown tuning name '%s'", name.c_str());
+            }
+        }
+    }
+    tuning() = t;
+    return SDHIP_OK;
+}
+
+int sdhip_get_tuning(const char *name) {
+    if (name == nullptr) return -1;
+    for (const Field &f : kFields) {
+        if (std::strcmp(name, f.name) == 0) return tuning().*(f.member);
+    }
+    return -1;
+}
+
+void sdhip_forget(const void *begin, size_t size) { store_forget(begin, size); }
+
+}  // extern "C"

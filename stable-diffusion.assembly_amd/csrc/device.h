@@ -1,0 +1,128 @@
+// Device-side pieces shared by every kernel of the library: vector types of
+// the MFMA operands, the split of a single-precision number into two FP16
+// parts, the element-wise chain an operation applies to its output while it
+// is still in registers, and the single-precision functions the chain and the
+// gated GELU compute with.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sdhip {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ split
+
+// The single-precision operand is scaled by 2^-4 before it is split, so that
+// numbers up to 65504 * 16 ~ 1.05e6 stay finite in FP16, and the product is
+// scaled back by 2^4 (both exact).  x * 2^-4 = hi + lo + r with hi =
+// fp16(x * 2^-4), lo = fp16(x * 2^-4 - hi) (the difference is exact in single
+// precision) and |r| <= 2^-22 |x * 2^-4| while lo is normal, 2^-25 once it is
+// subnormal: 22 bits of x, against 11 in ggml's own rounding of x to FP16.
+// FP16 weights are exact in FP16, so w * x = w hi + w lo + w r, and the two
+// products are exact in the MFMA's single-precision sums.
+constexpr float kSplitDown = 0.0625f;
+constexpr float kSplitUp = 16.0f;
+
+__device__ __forceinline__ void split2(float x, _Float16 &hi, _Float16 &lo) {
+    const float s = x * kSplitDown;
+    hi = static_cast<_Float16>(s);
+    lo = static_cast<_Float16>(s - static_cast<float>(hi));
+}
+
+// ------------------------------------------------------------------ scalar math
+
+// exp(x) by Cephes' expf method, as the reference's exponential()
+// (sources/scalar_math.h:34-51) computes it, so that the chain's SiLU and the
+// gated GELU round as the reference's do: x clamped to [-87.3, 88.73], n =
+// round(x / ln 2) by the sum with 1.5 * 2^23, r = x - n ln 2 in two steps,
+// exp(r) by Cephes' minimax polynomial, 2^n built in the exponent field.
+__device__ __forceinline__ float cephes_exp(float x) {
+    x = fminf(fmaxf(x, -87.3f), 88.73f);
+    const float magic = 12582912.0f;  // 1.5 * 2^23
+    const float z = __builtin_fmaf(x, 1.44269504088896341f, magic);
+    const float n = z - magic;
+    float r = __builtin_fmaf(n, -0.693359375f, x);
+    r = __builtin_fmaf(n, 2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    p = __builtin_fmaf(p * r, r, r) + 1.0f;
+    const uint32_t e = static_cast<uint32_t>(__float_as_int(z) - 0x4b400000 + 127) << 23;
+    return p * __uint_as_float(e);
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + cephes_exp(-x)); }
+
+// GELU by its tanh form, 0.5 x (1 + tanh(y)) = x / (1 + exp(-2y)),
+// y = sqrt(2/pi) (x + 0.044715 x^3) (scalar_math.h:58-63).
+__device__ __forceinline__ float gelu(float x) {
+    const float y = x * __builtin_fmaf(0.044715f * x, x, 1.0f);
+    return x / (1.0f + cephes_exp(-1.5957691216057308f * y));
+}
+
+// ------------------------------------------------------------------ chain
+
+enum StepKind : int32_t { kAdd = 0, kMul = 1, kSilu = 2 };
+
+struct DevStep {
+    int32_t kind;
+    const float *operand;
+    int64_t nb[4];  // elements; 0 along a broadcast dimension
+};
+
+constexpr int kMaxSteps = 6;
+
+struct DevChain {
+    int32_t count;
+    DevStep steps[kMaxSteps];
+};
+
+// The chain applied to the output element at coordinates (i0, i1, i2, i3) of
+// the output, in the order of the graph (fusion.cc:77-99), in single
+// precision: no contraction of an addition into a multiplication before it.
+__device__ __forceinline__ float apply_chain(const DevChain &c, float v, int64_t i0, int64_t i1, int64_t i2,
+                                             int64_t i3) {
+#pragma unroll 1
+    for (int s = 0; s < c.count; ++s) {
+        const DevStep &st = c.steps[s];
+        if (st.kind == kSilu) {
+            v = silu(v);
+            continue;
+        }
+        const float o = st.operand[i0 * st.nb[0] + i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3]];
+        if (st.kind == kAdd) {
+            v = __fadd_rn(v, o);
+        } else {
+            v = __fmul_rn(v, o);
+        }
+    }
+    return v;
+}
+
+// ------------------------------------------------------------------ grid
+
+// The 8 XCDs of an MI355X each take every 8th workgroup of a launch, and each
+// has its own L2.  A launch whose neighbouring blocks share an operand panel
+// maps hardware block b to logical block so that the blocks of one XCD are
+// consecutive logical blocks.  Blocks past the last multiple of 8 keep their
+// number.
+__device__ __forceinline__ uint32_t xcd_swizzle(uint32_t b, uint32_t nblocks) {
+    const uint32_t whole = nblocks / 8u * 8u;
+    if (b >= whole) {
+        return b;
+    }
+    return (b % 8u) * (whole / 8u) + b / 8u;
+}
+
+}  // namespace sdhip

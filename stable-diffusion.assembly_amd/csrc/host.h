@@ -1,0 +1,48 @@
+// Host-side helpers shared by the operations of the C ABI.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/sdhip.h"
+#include "device.h"
+
+namespace sdhip {
+
+// The fields of the reference's Tuning that change what is computed
+// (sources/kernels.h:91-135), with its defaults.
+struct Tuning {
+    int bits = 0;                    // 0 single precision; 2..8 quantized products (quant.h)
+    int input_bits = 8;              // the inputs' bits, unsigned with a zero point
+    int group = 64;                  // numbers of k sharing a scale, a multiple of 4
+    int weight_group = 1;            // the weights' scale per group: 1; per whole row of k: 0
+    int quantize = 7;                // with bits: 1 linear, 2 convolution, 4 attention
+    int winograd = 2;                // 2: F(2x2) and F(4x4); 1: F(2x2) alone; 0: direct
+    int winograd_positions = 1024;   // the least outputs of an image Winograd is used for
+    int winograd4_positions = 256;   // the least outputs of an image F(4x4) is used for
+    int winograd_small_tiles = 256;  // the most tiles of all images taken as small images
+    int fuse = 1;                    // chains fused: 1; the caller computes them apart: 0
+};
+
+Tuning &tuning();
+
+sdhip_status fail(sdhip_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+sdhip_status launched(hipError_t e, const char *what);
+
+bool holds_f32(const sdhip_tensor *t);
+bool holds_f16(const sdhip_tensor *t);
+bool contiguous(const sdhip_tensor *t);
+bool same_shape(const sdhip_tensor *a, const sdhip_tensor *b);
+bool same_layout(const sdhip_tensor *a, const sdhip_tensor *b);
+int64_t nelements(const sdhip_tensor *t);
+
+sdhip_status device_chain(const sdhip_epilogue *e, const int64_t ne[4], DevChain &c);
+sdhip_status output_of(const sdhip_tensor *y, const sdhip_epilogue *e, float *&out, int32_t &from_redirect);
+
+// The device store of derived weights (none kept yet): forget a range.
+void store_forget(const void *begin, size_t size);
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+}  // namespace sdhip

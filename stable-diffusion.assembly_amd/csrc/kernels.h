@@ -1,0 +1,54 @@
+// The launchers of the library's kernels and the argument blocks they take,
+// shared by the host code (api.cpp) and the kernels (*.hip).  Strides here
+// are in elements, not bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device.h"
+
+namespace sdhip {
+
+// MUL_MAT: y[m][n] = sum_k x[m][k] w[n][k]; m over M = ne1 * ne2 * ne3 rows.
+struct MulMatArgs {
+    const float *x;
+    int64_t ldx;
+    const _Float16 *w;
+    int64_t ldw;
+    float *y;  // the output, or the redirect, or the gated output
+    int64_t ldy;
+    int64_t M, N, K;
+    int64_t ne1, ne2;  // the output's rows and matrices, for the chain's coordinates
+    int64_t half;      // gated: N / 2
+    int64_t col_blocks;
+    int32_t from_redirect;
+    DevChain chain;
+};
+
+hipError_t launch_mul_mat(const MulMatArgs &p, hipStream_t stream);
+hipError_t launch_mul_mat_gated(const MulMatArgs &p, hipStream_t stream);
+
+// The direct convolution: y[n][oc][oy][ox] = sum over (ic, kh, kw).
+struct ConvArgs {
+    const float *x;  // [N][IC][IH][IW], strides xnb1..3
+    int64_t xnb1, xnb2, xnb3;
+    int64_t iw, ih, ic, n;
+    const _Float16 *w;  // [OC][IC * KH * KW], contiguous
+    int64_t kw, kh, oc;
+    float *y;  // [N][OC][OH][OW], strides ynb1..3
+    int64_t ynb1, ynb2, ynb3;
+    int64_t ow, oh;
+    int32_t s0, s1, p0, p1, d0, d1;
+    int64_t K;      // ic * kh * kw
+    int64_t taps;   // kh * kw
+    int64_t plane;  // oh * ow
+    int64_t P;      // n * plane
+    int64_t oc_blocks;
+    int32_t from_redirect;
+    DevChain chain;
+};
+
+hipError_t launch_conv_direct(const ConvArgs &c, hipStream_t stream);
+
+}  // namespace sdhip

@@ -1,0 +1,202 @@
+// CONV_2D on the device: the predicates of conv2d_supported
+// (conv2d.cc:320-331) and winograd_supported (winograd.cc:2107-2123), the
+// choice between F(4x4, 3x3), F(2x2, 3x3) and the direct convolution that
+// hooks.cc:36-41 and winograd.cc:1204-1206, 194-196 make, and the launch.
+
+#include <hip/hip_runtime.h>
+
+#include "host.h"
+#include "kernels.h"
+#include "winograd.h"
+
+namespace sdhip {
+
+namespace {
+
+struct Geometry {
+    int64_t iw, ih, ic, n, kw, kh, oc, ow, oh;
+    int32_t s0, s1, p0, p1, d0, d1;
+};
+
+Geometry geometry(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                  const int32_t *op) {
+    Geometry g{};
+    g.iw = input->ne[0];
+    g.ih = input->ne[1];
+    g.ic = input->ne[2];
+    g.n = input->ne[3];
+    g.kw = kernel->ne[0];
+    g.kh = kernel->ne[1];
+    g.oc = kernel->ne[3];
+    g.ow = y->ne[0];
+    g.oh = y->ne[1];
+    g.s0 = op[0];
+    g.s1 = op[1];
+    g.p0 = op[2];
+    g.p1 = op[3];
+    g.d0 = op[4];
+    g.d1 = op[5];
+    return g;
+}
+
+// The output extent of a convolution along one dimension (ggml_calc_conv_output_size).
+int64_t out_size(int64_t in, int64_t k, int32_t s, int32_t p, int32_t d) {
+    return (in + 2 * p - d * (k - 1) - 1) / s + 1;
+}
+
+bool direct_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
+    if (kernel == nullptr || input == nullptr || y == nullptr || op == nullptr) return false;
+    // FP16 kernels only: single-precision ones are left to the caller.
+    const bool weights = holds_f16(kernel) && contiguous(kernel);
+    if (!(weights && holds_f32(input) && holds_f32(y) && contiguous(y) && kernel->ne[2] == input->ne[2] &&
+          op[0] > 0 && op[1] > 0 && op[4] > 0 && op[5] > 0 && op[2] >= 0 && op[3] >= 0)) {
+        return false;
+    }
+    return y->ne[0] == out_size(input->ne[0], kernel->ne[0], op[0], op[2], op[4]) &&
+           y->ne[1] == out_size(input->ne[1], kernel->ne[1], op[1], op[3], op[5]) && y->ne[2] == kernel->ne[3] &&
+           y->ne[3] == input->ne[3] && input->nb[1] % 4 == 0 && input->nb[2] % 4 == 0 && input->nb[3] % 4 == 0;
+}
+
+// Small images: every tile of every image in one block (winograd.cc:194-196).
+bool small(const Geometry &g) {
+    return g.n * ((g.ow + 1) / 2) * ((g.oh + 1) / 2) <= tuning().winograd_small_tiles;
+}
+
+bool winograd_taken(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
+    if (tuning().winograd == 0 || !direct_supported(kernel, input, y, op)) return false;
+    const Geometry g = geometry(kernel, input, y, op);
+    if (!(g.kw == 3 && g.kh == 3 && g.s0 == 1 && g.s1 == 1 && g.d0 == 1 && g.d1 == 1 && g.p0 <= 2 && g.p1 <= 2)) {
+        return false;
+    }
+    return g.ow * g.oh >= tuning().winograd_positions || small(g);
+}
+
+// F(4x4, 3x3) for FP16 kernels and images of winograd4_positions outputs and
+// more (winograd.cc:1204-1206).
+bool four(const Geometry &g) {
+    return tuning().winograd == 2 && g.ow * g.oh >= tuning().winograd4_positions;
+}
+
+int path_of(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
+    if (!direct_supported(kernel, input, y, op)) return -1;
+    if (winograd_taken(kernel, input, y, op)) {
+        return four(geometry(kernel, input, y, op)) ? 4 : 2;
+    }
+    return 0;
+}
+
+WinogradArgs winograd_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                           const int32_t *op, int m) {
+    WinogradArgs a{};
+    a.m = m;
+    a.x = static_cast<const float *>(input->data);
+    a.xnb1 = input->nb[1] / 4;
+    a.xnb2 = input->nb[2] / 4;
+    a.xnb3 = input->nb[3] / 4;
+    a.iw = input->ne[0];
+    a.ih = input->ne[1];
+    a.ic = input->ne[2];
+    a.n = input->ne[3];
+    a.w = static_cast<const _Float16 *>(kernel->data);
+    a.oc = kernel->ne[3];
+    a.ow = y->ne[0];
+    a.oh = y->ne[1];
+    a.ynb1 = y->nb[1] / 4;
+    a.ynb2 = y->nb[2] / 4;
+    a.ynb3 = y->nb[3] / 4;
+    a.p0 = op[2];
+    a.p1 = op[3];
+    a.tw = ceil_div(a.ow, m);
+    a.th = ceil_div(a.oh, m);
+    a.tiles = a.n * a.tw * a.th;
+    return a;
+}
+
+}  // namespace
+
+}  // namespace sdhip
+
+using namespace sdhip;
+
+extern "C" {
+
+int sdhip_conv2d_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                           const int32_t op_params[6]) {
+    return direct_supported(kernel, input, y, op_params) ? 1 : 0;
+}
+
+int sdhip_conv2d_path(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                      const int32_t op_params[6]) {
+    return path_of(kernel, input, y, op_params);
+}
+
+size_t sdhip_conv2d_work_size(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                              const int32_t op_params[6]) {
+    const int path = path_of(kernel, input, y, op_params);
+    if (path == 2 || path == 4) {
+        return winograd_work_size(winograd_args(kernel, input, y, op_params, path));
+    }
+    return 0;
+}
+
+sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                          const int32_t op_params[6], const sdhip_epilogue *chain, void *work, size_t work_size,
+                          void *stream) {
+    const int path = path_of(kernel, input, y, op_params);
+    if (path < 0) {
+        return fail(SDHIP_UNSUPPORTED, "conv2d: operands not taken");
+    }
+    DevChain dc;
+    sdhip_status s = device_chain(chain, y->ne, dc);
+    if (s != SDHIP_OK) return s;
+    float *out = nullptr;
+    int32_t from_redirect = 0;
+    s = output_of(y, chain, out, from_redirect);
+    if (s != SDHIP_OK) return s;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (path == 2 || path == 4) {
+        WinogradArgs a = winograd_args(kernel, input, y, op_params, path);
+        a.y = out;
+        a.from_redirect = from_redirect;
+        a.chain = dc;
+        const size_t need = winograd_work_size(a);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        return winograd(a, work, st);
+    }
+    ConvArgs c{};
+    c.x = static_cast<const float *>(input->data);
+    c.xnb1 = input->nb[1] / 4;
+    c.xnb2 = input->nb[2] / 4;
+    c.xnb3 = input->nb[3] / 4;
+    c.iw = input->ne[0];
+    c.ih = input->ne[1];
+    c.ic = input->ne[2];
+    c.n = input->ne[3];
+    c.w = static_cast<const _Float16 *>(kernel->data);
+    c.kw = kernel->ne[0];
+    c.kh = kernel->ne[1];
+    c.oc = kernel->ne[3];
+    c.y = out;
+    c.ynb1 = y->nb[1] / 4;
+    c.ynb2 = y->nb[2] / 4;
+    c.ynb3 = y->nb[3] / 4;
+    c.ow = y->ne[0];
+    c.oh = y->ne[1];
+    c.s0 = op_params[0];
+    c.s1 = op_params[1];
+    c.p0 = op_params[2];
+    c.p1 = op_params[3];
+    c.d0 = op_params[4];
+    c.d1 = op_params[5];
+    c.K = c.ic * c.kh * c.kw;
+    c.taps = c.kh * c.kw;
+    c.plane = c.oh * c.ow;
+    c.P = c.n * c.plane;
+    c.from_redirect = from_redirect;
+    c.chain = dc;
+    return launched(launch_conv_direct(c, st), "conv2d direct");
+}
+
+}  // extern "C"

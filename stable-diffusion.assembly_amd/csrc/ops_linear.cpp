@@ -1,0 +1,156 @@
+// MUL_MAT and MUL_MAT with the gated GELU after it (mul_mat.cc), on the
+// device: the predicates of mul_mat_supported (mul_mat.cc:181-194) and
+// mul_mat_gated_supported (mul_mat.cc:1128-1151), then the split-FP16 MFMA
+// product (gemm.hip) or, with bits, the quantized one (quant.hip).
+
+#include <hip/hip_runtime.h>
+
+#include "host.h"
+#include "kernels.h"
+#include "quant.h"
+
+namespace sdhip {
+
+namespace {
+
+bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
+    const char *pa = static_cast<const char *>(a);
+    const char *pb = static_cast<const char *>(b);
+    return pa < pb + bn && pb < pa + an;
+}
+
+size_t nbytes(const sdhip_tensor *t) {
+    // The span of memory a tensor of these strides reaches (ggml_nbytes).
+    size_t n = t->type == SDHIP_TYPE_F16 ? 2 : 4;
+    for (int k = 0; k < 4; ++k) {
+        if (t->ne[k] <= 0) return 0;
+        n += static_cast<size_t>((t->ne[k] - 1) * t->nb[k]);
+    }
+    return n;
+}
+
+MulMatArgs args_of(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y) {
+    MulMatArgs a{};
+    a.x = static_cast<const float *>(x->data);
+    a.ldx = x->nb[1] / 4;
+    a.w = static_cast<const _Float16 *>(w->data);
+    a.ldw = w->nb[1] / 2;
+    a.K = w->ne[0];
+    a.N = w->ne[1];
+    a.M = x->ne[1] * x->ne[2] * x->ne[3];
+    a.ne1 = y->ne[1];
+    a.ne2 = y->ne[2];
+    a.ldy = y->nb[1] / 4;
+    return a;
+}
+
+}  // namespace
+
+// Whether the product is quantized (mul_mat.cc:95-105): bits asks for the
+// linear layers, and the product is of 256 rows or more.
+bool mul_mat_quantized(const sdhip_tensor *x) {
+    const Tuning &t = tuning();
+    const int64_t m = x->ne[1] * x->ne[2] * x->ne[3];
+    return t.bits >= 2 && t.bits <= 8 && (t.quantize & 1) != 0 && m >= 256;
+}
+
+}  // namespace sdhip
+
+using namespace sdhip;
+
+extern "C" {
+
+int sdhip_mul_mat_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y) {
+    if (w == nullptr || x == nullptr || y == nullptr) return 0;
+    // The weights are one matrix of FP16, the other operand and the result
+    // contiguous single precision, the products large enough to pay for the
+    // launch (mul_mat.cc:181-194).  Single-precision weights are not taken:
+    // the caller computes them (not taken, as ggml computes what the
+    // reference does not take).
+    const bool weights = holds_f16(w) && w->ne[2] == 1 && w->ne[3] == 1;
+    const bool shapes = x->ne[0] == w->ne[0] && y->ne[0] == w->ne[1] && y->ne[1] == x->ne[1] &&
+                        y->ne[2] == x->ne[2] && y->ne[3] == x->ne[3];
+    return weights && shapes && holds_f32(x) && contiguous(x) && holds_f32(y) && contiguous(y) &&
+           x->ne[1] * x->ne[2] * x->ne[3] >= 16 && w->ne[0] >= 16;
+}
+
+size_t sdhip_mul_mat_work_size(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y) {
+    if (!sdhip_mul_mat_supported(w, x, y)) return 0;
+    if (mul_mat_quantized(x)) {
+        return quantized_linear_work_size(w->ne[0], w->ne[1], x->ne[1] * x->ne[2] * x->ne[3]);
+    }
+    return 0;
+}
+
+sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
+                           const sdhip_epilogue *chain, void *work, size_t work_size, void *stream) {
+    if (!sdhip_mul_mat_supported(w, x, y)) {
+        return fail(SDHIP_UNSUPPORTED, "mul_mat: operands not taken");
+    }
+    MulMatArgs a = args_of(w, x, y);
+    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    if (s != SDHIP_OK) return s;
+    s = output_of(y, chain, a.y, a.from_redirect);
+    if (s != SDHIP_OK) return s;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (mul_mat_quantized(x)) {
+        const size_t need = quantized_linear_work_size(a.K, a.N, a.M);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        return quantized_linear(a, false, work, st);
+    }
+    return launched(launch_mul_mat(a, st), "mul_mat");
+}
+
+int sdhip_mul_mat_gated_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
+                                  const sdhip_tensor *out) {
+    if (!sdhip_mul_mat_supported(w, x, y) || out == nullptr || y->ne[0] % 2 != 0) return 0;
+    const int64_t half = y->ne[0] / 2;
+    // Quantized, each half's columns begin a panel (mul_mat.cc:1129-1132).
+    if (mul_mat_quantized(x) && half % 16 != 0) return 0;
+    // What the result is written to is not what the product reads
+    // (mul_mat.cc:1133-1149).
+    const size_t on = nbytes(out);
+    if (overlaps(out->data, on, w->data, nbytes(w)) || overlaps(out->data, on, x->data, nbytes(x)) ||
+        overlaps(out->data, on, y->data, nbytes(y))) {
+        return 0;
+    }
+    return holds_f32(out) && contiguous(out) && out->ne[0] == half && out->ne[1] == y->ne[1] &&
+           out->ne[2] == y->ne[2] && out->ne[3] == y->ne[3];
+}
+
+sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
+                                 const sdhip_epilogue *chain, const sdhip_tensor *out, void *work, size_t work_size,
+                                 void *stream) {
+    if (!sdhip_mul_mat_gated_supported(w, x, y, out)) {
+        return fail(SDHIP_UNSUPPORTED, "mul_mat_gated: operands not taken");
+    }
+    if (chain != nullptr && chain->redirect != nullptr) {
+        return fail(SDHIP_UNSUPPORTED, "mul_mat_gated: a chain with a residual redirect is not gated");
+    }
+    MulMatArgs a = args_of(w, x, y);
+    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    if (s != SDHIP_OK) return s;
+    const size_t on = nbytes(out);
+    for (int i = 0; chain != nullptr && i < chain->count; ++i) {
+        const sdhip_tensor &op = chain->steps[i].operand;
+        if (chain->steps[i].kind != SDHIP_STEP_SILU && overlaps(out->data, on, op.data, nbytes(&op))) {
+            return fail(SDHIP_UNSUPPORTED, "mul_mat_gated: the output overlaps a chain operand");
+        }
+    }
+    a.y = static_cast<float *>(out->data);
+    a.ldy = out->nb[1] / 4;
+    a.half = y->ne[0] / 2;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (mul_mat_quantized(x)) {
+        const size_t need = quantized_linear_work_size(a.K, a.N, a.M);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "mul_mat_gated: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        return quantized_linear(a, true, work, st);
+    }
+    return launched(launch_mul_mat_gated(a, st), "mul_mat_gated");
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// GROUP_NORM and NORM on the device: the predicates of group_norm_supported
+// (norm.cc:93-98) and norm_supported (norm.cc:142-146), and the launch.
+
+#include <hip/hip_runtime.h>
+
+#include "host.h"
+#include "norm.h"
+
+using namespace sdhip;
+
+extern "C" {
+
+int sdhip_group_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y, int groups) {
+    if (x == nullptr || y == nullptr) return 0;
+    return holds_f32(x) && holds_f32(y) && contiguous(x) && contiguous(y) && same_shape(x, y) && groups > 0;
+}
+
+sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
+                              const sdhip_epilogue *chain, void *stream) {
+    if (!sdhip_group_norm_supported(x, y, groups)) {
+        return fail(SDHIP_UNSUPPORTED, "group_norm: operands not taken");
+    }
+    if (chain != nullptr && chain->redirect != nullptr) {
+        return fail(SDHIP_UNSUPPORTED, "group_norm: no residual redirect after a normalisation");
+    }
+    GroupNormArgs a{};
+    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    if (s != SDHIP_OK) return s;
+    a.x = static_cast<const float *>(x->data);
+    a.y = static_cast<float *>(y->data);
+    a.ne0 = x->ne[0];
+    a.ne1 = x->ne[1];
+    a.ne2 = x->ne[2];
+    a.ne3 = x->ne[3];
+    a.xnb2 = x->nb[2] / 4;
+    a.xnb3 = x->nb[3] / 4;
+    a.ynb2 = y->nb[2] / 4;
+    a.ynb3 = y->nb[3] / 4;
+    a.groups = groups;
+    a.per_group = ceil_div(a.ne2, groups);
+    a.eps = eps;
+    return launched(launch_group_norm(a, static_cast<hipStream_t>(stream)), "group_norm");
+}
+
+int sdhip_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y) {
+    if (x == nullptr || y == nullptr) return 0;
+    return holds_f32(x) && holds_f32(y) && same_shape(x, y) && x->nb[1] % 4 == 0 && x->nb[2] % 4 == 0 &&
+           x->nb[3] % 4 == 0 && y->nb[1] % 4 == 0 && y->nb[2] % 4 == 0 && y->nb[3] % 4 == 0;
+}
+
+sdhip_status sdhip_norm(const sdhip_tensor *x, const sdhip_tensor *y, float eps, const sdhip_epilogue *chain,
+                        void *stream) {
+    if (!sdhip_norm_supported(x, y)) {
+        return fail(SDHIP_UNSUPPORTED, "norm: operands not taken");
+    }
+    if (chain != nullptr && chain->redirect != nullptr) {
+        return fail(SDHIP_UNSUPPORTED, "norm: no residual redirect after a normalisation");
+    }
+    NormArgs a{};
+    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    if (s != SDHIP_OK) return s;
+    a.x = static_cast<const float *>(x->data);
+    a.y = static_cast<float *>(y->data);
+    a.ne0 = x->ne[0];
+    a.ne1 = x->ne[1];
+    a.ne2 = x->ne[2];
+    a.rows = x->ne[1] * x->ne[2] * x->ne[3];
+    a.xnb1 = x->nb[1] / 4;
+    a.xnb2 = x->nb[2] / 4;
+    a.xnb3 = x->nb[3] / 4;
+    a.ynb1 = y->nb[1] / 4;
+    a.ynb2 = y->nb[2] / 4;
+    a.ynb3 = y->nb[3] / 4;
+    a.eps = eps;
+    return launched(launch_norm(a, static_cast<hipStream_t>(stream)), "norm");
+}
+
+}  // extern "C"

@@ -1,0 +1,205 @@
+"""numpy front end of the C oracle (oracle/oracle.h) for the tests.
+
+The oracle is the checker: these functions compute the float64 references and
+the single-precision restatements the tests compare the HIP library with.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "liboracle.so")
+
+_f = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_d = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i64 = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_i32 = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u8 = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_s8 = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+_L = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"{ORACLE_SO} is missing: make -C oracle")
+        L = ctypes.CDLL(ORACLE_SO)
+        L.oracle_exponential.restype = _F
+        L.oracle_exponential.argtypes = [_F]
+        L.oracle_silu.restype = _F
+        L.oracle_silu.argtypes = [_F]
+        L.oracle_gelu.restype = _F
+        L.oracle_gelu.argtypes = [_F]
+        L.oracle_silu_array.argtypes = [_f, _L]
+        L.oracle_exact_mul_mat.argtypes = [_f, _L, _f, _L, _L, _L, _L, _d, _d]
+        L.oracle_exact_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L, _d, _d]
+        L.oracle_exact_conv2d_at.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L,
+                                             _i64, _L, _d, _d]
+        L.oracle_exact_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _d, _d]
+        L.oracle_exact_attention_at.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _i64, _L, _d, _d]
+        L.oracle_exact_gated.argtypes = [_f, _f, ctypes.c_void_p, _L, _L, _L, _d, _d]
+        L.oracle_group_norm.argtypes = [_f, _f, _L, _L, _L, _L, _I, _F]
+        L.oracle_norm.argtypes = [_f, _f, _L, _L, _F]
+        L.oracle_quantize_input_row.argtypes = [_f, _L, _L, _I, _u8, ctypes.POINTER(_F), ctypes.POINTER(_F)]
+        L.oracle_quantize_weights.argtypes = [_f, _L, _L, _L, _L, _I, _I, _s8, _f, _f, _i32]
+        L.oracle_quantized_mul_mat.argtypes = [_f, _f, _L, _L, _L, _L, _I, _I, _I, ctypes.c_void_p, _f,
+                                               _u8, _f, _f, _s8, _f, _f, _i32]
+        _lib = L
+    return _lib
+
+
+def c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def metric(y, exact, mag):
+    """The reference's measure (tests/ops_test.cc:173-211): the largest
+    |y - exact| / (sum of product magnitudes, or 1 where that is 0)."""
+    y = np.asarray(y, dtype=np.float64).reshape(-1)
+    exact = np.asarray(exact, dtype=np.float64).reshape(-1)
+    mag = np.asarray(mag, dtype=np.float64).reshape(-1)
+    scale = np.where(mag > 0, mag, 1.0)
+    e = np.abs(y - exact) / scale
+    if not np.all(np.isfinite(e)):
+        return float("inf")
+    return float(e.max()) if e.size else 0.0
+
+
+def exact_mul_mat(w, x):
+    """w [N, K] (float, FP16 widened), x [M, K] -> (y, mag) [M, N] float64."""
+    w, x = c32(w), c32(x)
+    N, K = w.shape
+    M = x.shape[0]
+    y = np.empty((M, N), np.float64)
+    mag = np.empty((M, N), np.float64)
+    lib().oracle_exact_mul_mat(w, K, x, K, M, N, K, y, mag)
+    return y, mag
+
+
+def exact_conv2d(x, w, s0, s1, p0, p1, d0, d1, index=None):
+    """x [n, ic, ih, iw], w [oc, ic, kh, kw] -> (y, mag) [n, oc, oh, ow], or at
+    the flat indices `index` of that layout."""
+    x, w = c32(x), c32(w)
+    n, ic, ih, iw = x.shape
+    oc, _, kh, kw = w.shape
+    oh = (ih + 2 * p1 - d1 * (kh - 1) - 1) // s1 + 1
+    ow = (iw + 2 * p0 - d0 * (kw - 1) - 1) // s0 + 1
+    if index is None:
+        y = np.empty((n, oc, oh, ow), np.float64)
+        mag = np.empty_like(y)
+        lib().oracle_exact_conv2d(x, n, ic, ih, iw, w, oc, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, y, mag)
+        return y, mag
+    index = np.ascontiguousarray(index, dtype=np.int64)
+    y = np.empty(index.size, np.float64)
+    mag = np.empty(index.size, np.float64)
+    lib().oracle_exact_conv2d_at(x, n, ic, ih, iw, w, oc, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, index, index.size,
+                                 y, mag)
+    return y, mag
+
+
+def exact_attention(q, k, v, scale, queries=None):
+    """q [b, lq, h, d], k [b, lk, hk, d], v [b, lk, hk, dv] -> (y, mag)
+    [b, lq, h, dv], or [count, dv] for the flat queries (bi * h + hi) * lq + i."""
+    q, k, v = c32(q), c32(k), c32(v)
+    b, lq, h, d = q.shape
+    _, lk, hk, dv = v.shape
+    if queries is None:
+        y = np.empty((b, lq, h, dv), np.float64)
+        mag = np.empty_like(y)
+        lib().oracle_exact_attention(q, k, v, d, dv, lq, lk, h, hk, b, scale, y, mag)
+        return y, mag
+    queries = np.ascontiguousarray(queries, dtype=np.int64)
+    y = np.empty((queries.size, dv), np.float64)
+    mag = np.empty_like(y)
+    lib().oracle_exact_attention_at(q, k, v, d, dv, lq, lk, h, hk, b, scale, queries, queries.size, y, mag)
+    return y, mag
+
+
+def exact_gated(w, x, bias):
+    """w [2 half, K], x [M, K], bias [2 half] or None -> (y, mag) [M, half]."""
+    w, x = c32(w), c32(x)
+    M, K = x.shape
+    half = w.shape[0] // 2
+    y = np.empty((M, half), np.float64)
+    mag = np.empty_like(y)
+    bp = None
+    if bias is not None:
+        bias = c32(bias)
+        bp = bias.ctypes.data_as(ctypes.c_void_p)
+    lib().oracle_exact_gated(w, x, bp, M, half, K, y, mag)
+    return y, mag
+
+
+def group_norm(x, groups, eps):
+    """x [ne3, ne2, ne1, ne0] -> the reference's single-precision GROUP_NORM."""
+    x = c32(x)
+    y = np.empty_like(x)
+    ne3, ne2, ne1, ne0 = x.shape
+    lib().oracle_group_norm(x, y, ne0, ne1, ne2, ne3, groups, eps)
+    return y
+
+
+def norm(x, eps):
+    x = c32(x)
+    y = np.empty_like(x)
+    ne0 = x.shape[-1]
+    lib().oracle_norm(x, y, ne0, x.size // ne0, eps)
+    return y
+
+
+def silu(v):
+    """SiLU with the reference's exponential (scalar_math.h:54-56)."""
+    out = np.array(v, dtype=np.float32, copy=True, order="C")
+    lib().oracle_silu_array(out, out.size)
+    return out
+
+
+def quantize_input_row(x, group, levels):
+    x = c32(x)
+    dst = np.zeros(group, np.uint8)
+    s, o = _F(), _F()
+    lib().oracle_quantize_input_row(x, x.size, group, levels, dst, ctypes.byref(s), ctypes.byref(o))
+    return dst, np.float32(s.value), np.float32(o.value)
+
+
+def quantize_weights(w, group, weight_max, weight_groups):
+    w = c32(w)
+    rows, k = w.shape
+    groups = (k + group - 1) // group
+    q = np.zeros((rows, groups * group), np.int8)
+    sc = np.zeros((rows, groups), np.float32)
+    of = np.zeros((rows, groups), np.float32)
+    su = np.zeros((rows, groups), np.int32)
+    lib().oracle_quantize_weights(w, k, rows, k, group, weight_max, weight_groups, q, sc, of, su)
+    return q, sc, of, su
+
+
+def quantized_mul_mat(w, x, group=64, input_levels=255, weight_max=127, weight_groups=1, init=None):
+    """The reference's bits-mode MUL_MAT, bit for bit: (y, xq, xs, xo, wq, ws, wo, wsum)."""
+    w, x = c32(w), c32(x)
+    N, K = w.shape
+    M = x.shape[0]
+    groups = (K + group - 1) // group
+    kp = groups * group
+    y = np.zeros((M, N), np.float32)
+    xq = np.zeros((M, kp), np.uint8)
+    xs = np.zeros((M, groups), np.float32)
+    xo = np.zeros((M, groups), np.float32)
+    wq = np.zeros((N, kp), np.int8)
+    ws = np.zeros((N, groups), np.float32)
+    wo = np.zeros((N, groups), np.float32)
+    wsum = np.zeros((N, groups), np.int32)
+    ip = None
+    if init is not None:
+        init = c32(init)
+        ip = init.ctypes.data_as(ctypes.c_void_p)
+    lib().oracle_quantized_mul_mat(w, x, M, N, K, group, input_levels, weight_max, weight_groups, ip, y, xq, xs, xo,
+                                   wq, ws, wo, wsum)
+    return y, xq, xs, xo, wq, ws, wo, wsum

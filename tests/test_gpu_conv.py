@@ -1,0 +1,156 @@
+"""CONV_2D on the device -- direct, Winograd F(2x2, 3x3) and F(4x4, 3x3) --
+against the float64 oracle by the reference's metric, at the reference's
+test shapes (ops_test.cc:801-819, FP16 kernels) and the SD1.5 configurations
+of the bench (at full size the oracle checks a sample of the outputs)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as orc
+import sdhip
+from helpers import dev, normal, rng, uniform, unwritten, weights_f16
+
+BOUND = 2e-5
+
+# w, h, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n  (ops_test.cc:801-819, FP16 ones)
+CASES = [
+    (64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+    (16, 16, 96, 64, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+    (8, 8, 96, 64, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+    (32, 32, 64, 40, 1, 1, 1, 1, 0, 0, 1, 1, 2),
+    (33, 33, 24, 30, 3, 3, 2, 2, 1, 1, 1, 1, 1),
+    (100, 3, 20, 25, 3, 3, 1, 1, 0, 1, 1, 1, 1),
+    (512, 4, 16, 3, 3, 3, 1, 1, 1, 1, 1, 1, 1),
+    (65, 33, 24, 20, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+    (64, 20, 13, 11, 3, 3, 1, 1, 0, 0, 1, 1, 1),
+    (128, 128, 8, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1),
+    (40, 9, 7, 13, 5, 3, 1, 2, 2, 0, 2, 1, 1),
+    (17, 13, 5, 7, 3, 3, 1, 1, 1, 1, 1, 1, 3),
+]
+
+
+def out_size(i, k, s, p, d):
+    return (i + 2 * p - d * (k - 1) - 1) // s + 1
+
+
+def conv_case(gpu, c, seed, chain_steps=(), redirect=None, from_redirect=False, tuning=""):
+    w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
+    r = rng(seed)
+    kh16, k32 = weights_f16(r, (oc, ic, kh, kw))
+    x = uniform(r, (n, ic, h_, w_), 1.0)
+    oh, ow = out_size(h_, kh, s1, p1, d1), out_size(w_, kw, s0, p0, d0)
+    k_d, x_d = dev(kh16, gpu), dev(x, gpu)
+    y_d = unwritten((n, oc, oh, ow), gpu)
+    params = sdhip.conv_params(s0, s1, p0, p1, d0, d1)
+    sdhip.set_tuning(tuning)
+    try:
+        path = sdhip.conv2d_path(k_d, x_d, y_d, params)
+        sdhip.conv2d(k_d, x_d, y_d, params, sdhip.epilogue(chain_steps, redirect, from_redirect))
+        torch.cuda.synchronize()
+    finally:
+        sdhip.set_tuning("")
+    return x, k32, y_d, path, (s0, s1, p0, p1, d0, d1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("tuning", ["", "winograd=1", "winograd=0"])
+def test_conv2d(gpu, c, tuning):
+    x, k32, y, path, p = conv_case(gpu, c, seed=sum(c), tuning=tuning)
+    exact, mag = orc.exact_conv2d(x, k32, *p)
+    err = orc.metric(y.cpu().numpy(), exact, mag)
+    print(f"conv {c} path {path} [{tuning}]: {err:.3g}")
+    assert err <= BOUND
+
+
+@pytest.mark.gpu
+def test_path_selection(gpu):
+    """The paths the reference's predicates choose (winograd.cc:194-196,
+    1204-1206, 2107-2123; hooks.cc:36-41)."""
+    def path(w_, h_, ic, oc, kk, s, p, n, tuning=""):
+        k = torch.zeros((oc, ic, kk, kk), dtype=torch.float16, device=gpu)
+        x = torch.zeros((n, ic, h_, w_), dtype=torch.float32, device=gpu)
+        oh, ow = out_size(h_, kk, s, p, 1), out_size(w_, kk, s, p, 1)
+        y = torch.zeros((n, oc, oh, ow), dtype=torch.float32, device=gpu)
+        sdhip.set_tuning(tuning)
+        try:
+            return sdhip.conv2d_path(k, x, y, sdhip.conv_params(s, s, p, p, 1, 1))
+        finally:
+            sdhip.set_tuning("")
+    assert path(64, 64, 320, 320, 3, 1, 1, 2) == 4      # F(4x4): >= 1024 outputs
+    assert path(8, 8, 1280, 1280, 3, 1, 1, 2) == 2      # F(2x2): small, 32 tiles
+    assert path(16, 16, 1280, 1280, 3, 1, 1, 2) == 4    # small (128 tiles) and 256 outputs: F(4x4)
+    assert path(32, 32, 640, 1280, 1, 1, 0, 2) == 0     # 1x1: direct
+    assert path(33, 33, 24, 30, 3, 2, 1, 1) == 0        # stride 2: direct
+    assert path(64, 64, 320, 320, 3, 1, 1, 2, "winograd=1") == 2
+    assert path(64, 64, 320, 320, 3, 1, 1, 2, "winograd=0") == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [
+    (40, 36, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2),   # Winograd F(4x4), 1440 outputs
+    (66, 40, 16, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1),   # Winograd F(4x4), odd tiles
+    (15, 9, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2),    # small images, F(2x2)
+    (40, 36, 96, 40, 1, 1, 1, 1, 0, 0, 1, 1, 2),   # 1x1
+])
+@pytest.mark.parametrize("mode", ["bias", "residual", "from_redirect"])
+def test_conv2d_chain(gpu, c, mode):
+    """conv + bias, + residual not in place, or begun from the residual in its
+    own memory (ops_test.cc:952-1061)."""
+    w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
+    oh, ow = out_size(h_, kh, s1, p1, d1), out_size(w_, kw, s0, p0, d0)
+    r = rng(99)
+    bias = uniform(r, (1, oc, 1, 1), 1.0)
+    res = uniform(r, (n, oc, oh, ow), 1.0)
+    b_d, res_d = dev(bias, gpu), dev(res, gpu)
+    if mode == "bias":
+        x, k32, y, path, p = conv_case(gpu, c, 7, [("add", b_d)])
+        out = y
+        add = np.broadcast_to(bias, res.shape).astype(np.float64)
+    elif mode == "residual":
+        out = unwritten(res.shape, gpu)
+        x, k32, y, path, p = conv_case(gpu, c, 7, [("add", b_d), ("add", res_d)], redirect=out)
+        add = bias.astype(np.float64) + res
+    else:
+        out = res_d.clone()
+        x, k32, y, path, p = conv_case(gpu, c, 7, [("add", b_d)], redirect=out, from_redirect=True)
+        add = bias.astype(np.float64) + res
+    exact, mag = orc.exact_conv2d(x, k32, *p)
+    err = orc.metric(out.cpu().numpy(), exact + add, mag + np.abs(add))
+    print(f"conv chain {mode} {c} path {path}: {err:.3g}")
+    assert err <= BOUND
+
+
+def sampled(gpu, shape, k, s, p, seed, count=3000, chain=None):
+    n, ic, h_, w_ = shape
+    oc = k[0]
+    r = rng(seed)
+    kh16 = (0.02 * r.standard_normal(size=k)).astype(np.float16)
+    x = normal(r, shape)
+    k_d, x_d = dev(kh16, gpu), dev(x, gpu)
+    kk = k[2]
+    oh, ow = out_size(h_, kk, s, p, 1), out_size(w_, kk, s, p, 1)
+    y = unwritten((n, oc, oh, ow), gpu)
+    params = sdhip.conv_params(s, s, p, p, 1, 1)
+    path = sdhip.conv2d_path(k_d, x_d, y, params)
+    sdhip.conv2d(k_d, x_d, y, params)
+    torch.cuda.synchronize()
+    yy = y.cpu().numpy().reshape(-1)
+    assert np.isfinite(yy).all(), "every output written"
+    index = r.choice(yy.size, size=count, replace=False)
+    exact, mag = orc.exact_conv2d(x, kh16.astype(np.float32), s, s, p, p, 1, 1, index=index)
+    return orc.metric(yy[index], exact, mag), path
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,shape,k,s,p,want", [
+    ("cfg2 F(4x4) 64x64x320", (2, 320, 64, 64), (320, 320, 3, 3), 1, 1, 4),
+    ("cfg3a F(2x2) 8x8x1280", (2, 1280, 8, 8), (1280, 1280, 3, 3), 1, 1, 2),
+    ("cfg3b 1x1 32x32 640->1280", (2, 640, 32, 32), (1280, 640, 1, 1), 1, 0, 0),
+])
+def test_conv2d_bench_shapes(gpu, name, shape, k, s, p, want):
+    err, path = sampled(gpu, shape, k, s, p, seed=len(name))
+    print(f"{name}: path {path}, sampled error {err:.3g}")
+    assert path == want
+    assert err <= BOUND

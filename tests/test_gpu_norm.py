@@ -1,0 +1,70 @@
+"""GROUP_NORM and NORM with their chains on the device against the oracle's
+restatement of norm.cc (the same statistics in the same precisions), and
+against float64 for the normalisation itself."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as orc
+import sdhip
+from helpers import dev, normal, rng, uniform, unwritten
+
+# Fused and apart within 1e-6 of the largest output, as the reference's
+# fusion tests hold them (ops_test.cc:567-637); the statistics here are the
+# reference's own, so the outputs agree to a few units in the last place.
+CLOSE = 1e-6
+
+
+def chain_ref(y, gamma, beta, silu):
+    out = y * gamma
+    out = out + beta
+    if silu:
+        out = orc.silu(out)
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,groups,eps,silu", [
+    ((2, 64, 20, 36), 32, 1e-6, True),     # ops_test.cc:1062-1075
+    ((1, 30, 7, 13), 10, 1e-5, True),      # rows of no multiple of eight
+    ((2, 1280, 8, 8), 32, 1e-5, True),     # cfg3a's GroupNorm + SiLU
+    ((2, 1280, 32, 32), 32, 1e-5, True),   # cfg3b's
+    ((1, 30, 7, 13), 7, 1e-5, False),      # groups of ceil(30/7) = 5 channels, the last of none
+])
+def test_group_norm(gpu, shape, groups, eps, silu):
+    r = rng(sum(shape) + groups)
+    x = uniform(r, shape, 3.0)
+    c = shape[1]
+    gamma = normal(r, (1, c, 1, 1), 1.0, 0.1)
+    beta = normal(r, (1, c, 1, 1), 0.0, 0.1)
+    x_d, g_d, b_d = dev(x, gpu), dev(gamma, gpu), dev(beta, gpu)
+    y = unwritten(shape, gpu)
+    steps = [("mul", g_d), ("add", b_d)] + ([("silu", None)] if silu else [])
+    sdhip.group_norm(x_d, y, groups, eps, sdhip.epilogue(steps))
+    torch.cuda.synchronize()
+    want = chain_ref(orc.group_norm(x, groups, eps), gamma, beta, silu)
+    got = y.cpu().numpy()
+    assert np.isfinite(got).all()
+    diff = np.abs(got - want).max() / np.abs(want).max()
+    print(f"group_norm {shape}/{groups}: {diff:.3g} of the largest")
+    assert diff <= CLOSE
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(2, 77, 320), (2, 988, 1280), (3, 5, 33)])
+def test_norm(gpu, shape):
+    r = rng(sum(shape))
+    x = uniform(r, shape, 3.0)
+    n = shape[-1]
+    gamma = normal(r, (n,), 1.0, 0.1)
+    beta = normal(r, (n,), 0.0, 0.1)
+    x_d, g_d, b_d = dev(x, gpu), dev(gamma, gpu), dev(beta, gpu)
+    y = unwritten(shape, gpu)
+    sdhip.norm(x_d, y, 1e-5, sdhip.epilogue([("mul", g_d), ("add", b_d)]))
+    torch.cuda.synchronize()
+    want = chain_ref(orc.norm(x, 1e-5), gamma, beta, False)
+    got = y.cpu().numpy()
+    diff = np.abs(got - want).max() / np.abs(want).max()
+    print(f"norm {shape}: {diff:.3g} of the largest")
+    assert diff <= CLOSE
