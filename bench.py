@@ -1,0 +1,301 @@
+"""Benchmark of the MI355X form of stable-diffusion.assembly's hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+
+A step is one pass of the hot path over one batch of synthetic input: the
+configuration BASELINE.json's metric is quoted on, configs[1] -- the SD1.5
+ResNet 3x3 convolution [2, 320, 64, 64] -> 320 by Winograd F(4x4, 3x3) with
+its bias and residual add fused -- with inputs resident in HBM.  `value` is
+TFLOP/s counted in direct-convolution FLOPs (2 * N * OC * OH * OW * IC * 9),
+as the metric asks.  The other configurations are timed the same way and
+reported under "configs"; the roofline object is that of the workload's
+dominant kernel, timed with HIP events on its own stream; cpu_baseline is the
+oracle's single-precision restatement of the same F(4x4) algorithm on this
+host's cores (oracle/port.c).
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "stable-diffusion.assembly_amd"))
+
+METRIC = "TFLOP/s per op (direct-conv-equiv) + SD1.5 UNet step ms, 1 MI355X"
+PEAK_FP32_MFMA = 157.3  # TFLOP/s, dense
+PEAK_FP16_MFMA = 2500.0
+PEAK_HBM = 8000.0  # GB/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--only-main", action="store_true")
+    return p.parse_args()
+
+
+def timed(fn, steps, warmup):
+    """ms per call of fn over `steps` calls after `warmup`, bracketed by
+    synchronisations, with HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def kernel_times(fn, steps):
+    """{kernel: (ms per launch, launches per call)} over `steps` calls."""
+    import torch
+
+    import sdhip
+
+    torch.cuda.synchronize()
+    sdhip.profile_reset()
+    sdhip.profile_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    sdhip.profile_enable(False)
+    out = {}
+    for name, (ms, n) in sdhip.profile_collect().items():
+        out[name] = (ms / n, n / steps)
+    return out
+
+
+def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupnorm=False, seed=0):
+    """The convolution of a configuration with its chain, ready to run."""
+    import torch
+
+    import sdhip
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn((n, ic, h, w), generator=g, device=dev, dtype=torch.float32)
+    kern = (0.02 * torch.randn((oc, ic, k, k), generator=g, device=dev)).to(torch.float16)
+    oh, ow = h + 2 * pad - k + 1, w + 2 * pad - k + 1
+    y = torch.empty((n, oc, oh, ow), device=dev, dtype=torch.float32)
+    steps = []
+    if bias:
+        b = 0.01 * torch.randn((1, oc, 1, 1), generator=g, device=dev)
+        steps.append(("add", b))
+    if residual:
+        r = torch.randn((n, oc, oh, ow), generator=g, device=dev)
+        steps.append(("add", r))
+    chain = sdhip.epilogue(steps)
+    params = sdhip.conv_params(1, 1, pad, pad, 1, 1)
+    lib = sdhip.load()
+    dk, dx, dy = sdhip.desc(kern), sdhip.desc(x), sdhip.desc(y)
+    size = lib.sdhip_conv2d_work_size(dk, dx, dy, params)
+    work = torch.empty(max(size, 1), dtype=torch.uint8, device=dev)
+    path = lib.sdhip_conv2d_path(dk, dx, dy, params)
+    gn = None
+    if groupnorm:
+        gamma = 1.0 + 0.1 * torch.randn((1, oc, 1, 1), generator=g, device=dev)
+        beta = 0.1 * torch.randn((1, oc, 1, 1), generator=g, device=dev)
+        out = torch.empty_like(y)
+        gn = (out, sdhip.epilogue([("mul", gamma), ("add", beta), ("silu", None)]), sdhip.desc(out))
+    stream = sdhip.stream_handle()
+    keep = (x, kern, y, steps, work)
+
+    def run():
+        sdhip.check(lib.sdhip_conv2d(dk, dx, dy, params, ctypes.byref(chain), ctypes.c_void_p(work.data_ptr()),
+                                     size, stream), "conv2d")
+        if gn is not None:
+            sdhip.check(lib.sdhip_group_norm(dy, gn[2], 32, 1e-5, ctypes.byref(gn[1]), stream), "group_norm")
+
+    flops = 2.0 * n * oc * oh * ow * ic * k * k
+    run.keep = keep
+    return run, flops, path
+
+
+def linear_workload(dev, k, nout, m, batch, seed=0):
+    import torch
+
+    import sdhip
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = (0.02 * torch.randn((nout, k), generator=g, device=dev)).to(torch.float16)
+    x = torch.randn((batch, m, k), generator=g, device=dev)
+    b = 0.01 * torch.randn((nout,), generator=g, device=dev)
+    y = torch.empty((batch, m, nout), device=dev)
+    chain = sdhip.epilogue([("add", b)])
+    lib = sdhip.load()
+    dw, dx, dy = sdhip.desc(w), sdhip.desc(x), sdhip.desc(y)
+    size = lib.sdhip_mul_mat_work_size(dw, dx, dy)
+    work = torch.empty(max(size, 1), dtype=torch.uint8, device=dev)
+    stream = sdhip.stream_handle()
+
+    def run():
+        sdhip.check(lib.sdhip_mul_mat(dw, dx, dy, ctypes.byref(chain), ctypes.c_void_p(work.data_ptr()), size,
+                                      stream), "mul_mat")
+
+    run.keep = (w, x, b, y, work)
+    return run, 2.0 * k * nout * m * batch
+
+
+def attention_workload(dev, b, h, lq, lk, d, seed=0):
+    """cfg4: Q [b, h, lq, d], K/V [b, h, lk, d] ~N(0,1), ggml's head layout."""
+    import torch
+
+    import sdhip
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn((b, lq, h, d), generator=g, device=dev)
+    k = torch.randn((b, lk, h, d), generator=g, device=dev)
+    v = torch.randn((b, lk, h, d), generator=g, device=dev)
+    y = torch.empty((b, lq, h, d), device=dev)
+    lib = sdhip.load()
+    dq, dk, dv, dy = (sdhip.desc(q.permute(0, 2, 1, 3)), sdhip.desc(k.permute(0, 2, 1, 3)),
+                      sdhip.desc(v.permute(0, 2, 1, 3)), sdhip.desc(y))
+    scale = 1.0 / d ** 0.5
+    stream = sdhip.stream_handle()
+
+    def run():
+        sdhip.check(lib.sdhip_attention(dq, dk, dv, dy, scale, 0.0, 0.0, None, 0, stream), "attention")
+
+    run.keep = (q, k, v, y)
+    return run, 4.0 * b * h * lq * lk * d
+
+
+def cpu_baseline(seconds):
+    """The oracle's F(4x4) restatement on this host's cores, on the full
+    configs[1] convolution, repeated for about `seconds`; the best rate."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as orc
+
+    lib = orc.lib()
+    f = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+    L, I = ctypes.c_int64, ctypes.c_int
+    lib.oracle_port_winograd4.argtypes = [f, L, L, L, L, f, L, I, I, f, f, f, I]
+    n, ic, h, w, oc = 2, 320, 64, 64, 320
+    r = np.random.default_rng(1)
+    x = r.standard_normal((n, ic, h, w)).astype(np.float32)
+    k = (0.02 * r.standard_normal((oc, ic, 3, 3))).astype(np.float16).astype(np.float32)
+    bias = (0.01 * r.standard_normal(oc)).astype(np.float32)
+    res = r.standard_normal((n, oc, h, w)).astype(np.float32)
+    y = np.empty((n, oc, h, w), np.float32)
+    cores = min(16, os.cpu_count() or 1)
+    flops = 2.0 * n * oc * h * w * ic * 9
+    best, runs, t_end = None, 0, time.time() + seconds
+    while time.time() < t_end or runs < 2:
+        t = time.perf_counter()
+        lib.oracle_port_winograd4(x, n, ic, h, w, k, oc, 1, 1, bias, res, y, cores)
+        dt = time.perf_counter() - t
+        runs += 1
+        if runs > 1:  # the first run is not counted (tools/bench.cc:427-451)
+            best = dt if best is None else min(best, dt)
+    return {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"the whole configs[1] convolution (F(4x4), bias + residual) in single precision, "
+                      f"best of {runs - 1} runs after one uncounted, {cores} OpenMP threads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported in this build "
+              f"(every operation of the path shards without exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import sdhip
+
+    dev = torch.device("cuda", 0)
+    sdhip.check(sdhip.load().sdhip_init(0), "init")
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    # The headline: configs[1], F(4x4) with bias and residual fused.
+    run, flops, path = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2)
+    assert path == 4, f"configs[1] takes path {path}, not F(4x4)"
+    ms = timed(run, args.steps, args.warmup)
+    value = flops / ms / 1e9
+    log(f"cfg2 F(4x4) 64x64x320: {ms * 1e3:.1f} us, {value:.1f} TFLOP/s direct-eq")
+    kt = kernel_times(run, args.steps)
+    dominant = max(kt, key=lambda n: kt[n][0] * kt[n][1])
+    dom_ms = kt[dominant][0]
+    # The products: 36 GEMMs of OC x IC x tiles, 2 FLOP per multiply-add.
+    tiles = 2 * 16 * 16
+    alg = 2.0 * 36 * 320 * 320 * tiles
+    roof = {"kernel": dominant, "bound": "mfma", "achieved": round(alg / dom_ms / 1e9, 2), "peak": PEAK_FP32_MFMA,
+            "unit": "TFLOP/s", "frac": round(alg / dom_ms / 1e9 / PEAK_FP32_MFMA, 4), "traffic": None,
+            "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kt.items()}}
+    log(f"kernels: {roof['kernels_us']}")
+
+    configs = {"cfg2_winograd4": {"ms": round(ms, 5), "tflops": round(value, 2)}}
+    if not args.only_main:
+        run1, f1 = linear_workload(dev, 320, 320, 4096, 2, seed=1)
+        m1 = timed(run1, args.steps, args.warmup)
+        configs["cfg1_linear"] = {"ms": round(m1, 5), "tflops": round(f1 / m1 / 1e9, 2),
+                                  "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kernel_times(run1, 10).items()}}
+        log(f"cfg1 linear: {m1 * 1e3:.1f} us")
+        run3a, f3a, p3a = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True,
+                                        seed=3)
+        m3a = timed(run3a, args.steps, args.warmup)
+        configs["cfg3a_winograd2_gn_silu"] = {"ms": round(m3a, 5), "tflops": round(f3a / m3a / 1e9, 2), "path": p3a,
+                                              "kernels_us": {k: round(v[0] * 1e3, 2)
+                                                             for k, v in kernel_times(run3a, 10).items()}}
+        log(f"cfg3a F(2x2)+GN+SiLU: {m3a * 1e3:.1f} us")
+        run3b, f3b, p3b = conv_workload(dev, 2, 640, 32, 32, 1280, 1, 0, bias=True, residual=False, groupnorm=True,
+                                        seed=4)
+        m3b = timed(run3b, args.steps, args.warmup)
+        configs["cfg3b_pointwise_gn_silu"] = {"ms": round(m3b, 5), "tflops": round(f3b / m3b / 1e9, 2),
+                                              "path": p3b,
+                                              "kernels_us": {k: round(v[0] * 1e3, 2)
+                                                             for k, v in kernel_times(run3b, 10).items()}}
+        log(f"cfg3b 1x1+GN+SiLU: {m3b * 1e3:.1f} us")
+        for name, lk in (("cfg4_self_attention", 4096), ("cfg4_cross_attention", 77)):
+            run4, f4 = attention_workload(dev, 2, 8, 4096, lk, 40, seed=5)
+            m4 = timed(run4, args.steps, args.warmup)
+            configs[name] = {"ms": round(m4, 5), "tflops": round(f4 / m4 / 1e9, 2),
+                             "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kernel_times(run4, 5).items()}}
+            log(f"{name}: {m4 * 1e3:.1f} us, {f4 / m4 / 1e9:.1f} TFLOP/s")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: SD1.5 ResNet 3x3 conv [2,320,64,64]->320, pad 1, Winograd F(4x4,3x3), "
+                               "FP16 weights ~N(0,0.02), fused bias + residual add",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+        "configs": configs,
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -94,6 +94,16 @@ int sdhip_get_tuning(const char *name);
  * store.cc:241-266), called when that memory is about to change. */
 void sdhip_forget(const void *begin, size_t size);
 
+/* The profile of the kernels (the reference's sdasm_profile_*, sdasm.h:63-76,
+ * profile.cc): with profiling on, each kernel launch is bracketed by HIP
+ * events on its own stream; sdhip_profile_collect() waits for them and adds
+ * the times up per kernel name, returning how many names there are, and
+ * sdhip_profile_entry() reads entry i (total milliseconds, launches). */
+void sdhip_profile_enable(int on);
+void sdhip_profile_reset(void);
+int sdhip_profile_collect(void);
+int sdhip_profile_entry(int i, const char **name, double *total_ms, int64_t *launches);
+
 /* ---------------------------------------------------------------- MUL_MAT */
 
 /* GGML_OP_MUL_MAT of one weight matrix w (F16/F32, ne = [K, N, 1, 1]) by

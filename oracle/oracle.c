@@ -49,6 +49,10 @@ float oracle_gelu(float x) {
     return x / (1.0f + oracle_exponential(-1.5957691216057308f * y));
 }
 
+void oracle_gated_gelu_array(const float *x, const float *gate, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] * oracle_gelu(gate[i]);
+}
+
 /* ------------------------------------------------------------------ float64 */
 
 void oracle_exact_mul_mat(const float *w, int64_t ldw, const float *x, int64_t ldx, int64_t M, int64_t N,

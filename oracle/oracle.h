@@ -36,6 +36,8 @@ float oracle_silu(float x);
 float oracle_gelu(float x);
 /* SiLU of n numbers in place. */
 void oracle_silu_array(float *x, int64_t n);
+/* out = x * GELU(gate) of n numbers (fusion.cc:290-310). */
+void oracle_gated_gelu_array(const float *x, const float *gate, float *out, int64_t n);
 
 /* ---- float64 references (tests/ops_test.cc) */
 
@@ -108,6 +110,17 @@ void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t
                               int input_levels, int weight_max, int weight_groups, const float *init, float *y,
                               uint8_t *xq, float *xscale, float *xoffset, int8_t *wq, float *wscale, float *woffset,
                               int32_t *wsums);
+
+/* ---- CPU-baseline restatements (port.c), threads OpenMP threads */
+
+/* Winograd F(4x4, 3x3) of winograd.cc:1548-1613 with bias and residual:
+ * x [n][ic][ih][iw], w [oc][ic][3][3] widened, y [n][oc][oh][ow]. */
+void oracle_port_winograd4(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
+                           int p0, int p1, const float *bias, const float *residual, float *y, int threads);
+
+/* MUL_MAT in single precision: y[m][n] = sum_k x[m][k] w[n][k] (+ bias[n]). */
+void oracle_port_mul_mat(const float *w, const float *x, const float *bias, int64_t M, int64_t N, int64_t K, float *y,
+                         int threads);
 
 #ifdef __cplusplus
 }

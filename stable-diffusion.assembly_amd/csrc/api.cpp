@@ -129,6 +129,8 @@ sdhip_status device_chain(const sdhip_epilogue *e, const int64_t ne[4], DevChain
             }
             d.nb[k] = st.operand.ne[k] == 1 ? 0 : st.operand.nb[k] / 4;
         }
+        d.flat01 = d.nb[1] == ne[0] * d.nb[0] ? 1 : 0;
+        d.flat123 = d.nb[2] == ne[1] * d.nb[1] && d.nb[3] == ne[2] * d.nb[2] ? 1 : 0;
     }
     c.count = e->count;
     return SDHIP_OK;

@@ -1,0 +1,33 @@
+// FLASH_ATTN_EXT (attention.cc) on the device.  Strides in elements.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sdhip {
+
+struct AttentionArgs {
+    const float *q;
+    int64_t qnb1, qnb2, qnb3;
+    const void *k;  // F32 or F16 (khalf)
+    int64_t knb1, knb2, knb3;
+    const void *v;
+    int64_t vnb1, vnb2, vnb3;
+    float *y;  // [b][lq][h][dv]
+    int64_t ynb1, ynb2, ynb3;
+    int64_t d, dv, lq, lk, h, hk, b;
+    float scale;
+    int32_t khalf, vhalf;
+    // Set by the launcher.
+    int32_t dp, ldq, ldk, ldv;
+    int64_t qblocks;
+};
+
+// The most dimensions of a head the kernel takes (queries, keys and values).
+constexpr int64_t kAttentionMaxDims = 256;
+
+size_t attention_lds_bytes(int64_t d, int64_t dv);
+hipError_t launch_attention(AttentionArgs a, hipStream_t stream);
+
+}  // namespace sdhip

@@ -77,6 +77,11 @@ enum StepKind : int32_t { kAdd = 0, kMul = 1, kSilu = 2 };
 
 struct DevStep {
     int32_t kind;
+    // flat01: nb[1] = ne[0] nb[0], so i0 nb[0] + i1 nb[1] = (i1 ne0 + i0) nb[0];
+    // flat123: nb[2] = ne[1] nb[1] and nb[3] = ne[2] nb[2], so that
+    // i1 nb[1] + i2 nb[2] + i3 nb[3] = (row of the output) nb[1].  Either lets
+    // an epilogue index the operand without dividing.
+    int32_t flat01, flat123;
     const float *operand;
     int64_t nb[4];  // elements; 0 along a broadcast dimension
 };
@@ -88,26 +93,44 @@ struct DevChain {
     DevStep steps[kMaxSteps];
 };
 
-// The chain applied to the output element at coordinates (i0, i1, i2, i3) of
-// the output, in the order of the graph (fusion.cc:77-99), in single
-// precision: no contraction of an addition into a multiplication before it.
-__device__ __forceinline__ float apply_chain(const DevChain &c, float v, int64_t i0, int64_t i1, int64_t i2,
-                                             int64_t i3) {
+// The chain (fusion.cc:77-99) applied to E values at once, in the order of
+// the graph and in single precision (no contraction of an addition into a
+// multiplication before it), step after step: the operands of a step are all
+// loaded before any is used and nothing is stored meanwhile, so that the
+// loads go out together rather than one round trip per element.  off(s, e)
+// gives the offset of element e in the operand of step s.
+template <int E, class Off>
+__device__ __forceinline__ void apply_chain_block(const DevChain &c, float (&v)[E], Off off) {
 #pragma unroll 1
     for (int s = 0; s < c.count; ++s) {
         const DevStep &st = c.steps[s];
-        if (st.kind == kSilu) {
-            v = silu(v);
+        if (st.kind == 2) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[e] = silu(v[e]);
             continue;
         }
-        const float o = st.operand[i0 * st.nb[0] + i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3]];
-        if (st.kind == kAdd) {
-            v = __fadd_rn(v, o);
+        float o[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = st.operand[off(s, e)];
+        if (st.kind == 0) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[e] = __fadd_rn(v[e], o[e]);
         } else {
-            v = __fmul_rn(v, o);
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[e] = __fmul_rn(v[e], o[e]);
         }
     }
-    return v;
+}
+
+// Row r of an output of ne1 rows and ne2 matrices as (i1, i2, i3), in 32-bit
+// unsigned division (the host keeps every extent below 2^31): 64-bit division
+// is a long software sequence on the GPU.
+__device__ __forceinline__ void split_index(uint32_t r, uint32_t ne1, uint32_t ne2, uint32_t &i1, uint32_t &i2,
+                                            uint32_t &i3) {
+    const uint32_t q = r / ne1;
+    i1 = r - q * ne1;
+    i3 = q / ne2;
+    i2 = q - i3 * ne2;
 }
 
 // ------------------------------------------------------------------ grid

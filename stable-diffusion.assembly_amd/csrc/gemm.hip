@@ -25,6 +25,7 @@
 
 #include "device.h"
 #include "kernels.h"
+#include "profile.h"
 
 namespace sdhip {
 
@@ -244,35 +245,68 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
         __syncthreads();
     }
 
-    // The epilogue: rows m of the tile, column (feature) lane % 32.
+    // The epilogue: rows m of the tile, column (feature) lane % 32; a tile's
+    // 16 values of the lane at a time, their loads before their stores.
     const int col = lane & 31;
+    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
+    const auto row_off = [&](const DevStep &st, int64_t m) -> int64_t {
+        if (st.flat123) return m * st.nb[1];
+        uint32_t i1, i2, i3;
+        split_index(static_cast<uint32_t>(m), ne1, ne2, i1, i2, i3);
+        return i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+    };
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        const int64_t mbase = m0 + wr * 32 * TM + 32 * i;
+        // Rows past M read the last row and are not stored.
+        const auto row = [&](int e) -> int64_t {
+            const int64_t m = mbase + acc_row(e, lane);
+            return m < p.M ? m : p.M - 1;
+        };
+        if (GATED) {
+            const int64_t f = n0 + 32 * wc + col;
+            const int64_t fc = f < p.half ? f : p.half - 1;
+            float xv[16], gv[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int64_t m = m0 + wr * 32 * TM + 32 * i + acc_row(e, lane);
-            if (m >= p.M) continue;
-            const int64_t i1 = m % p.ne1;
-            const int64_t i2 = (m / p.ne1) % p.ne2;
-            const int64_t i3 = m / (p.ne1 * p.ne2);
-            if (GATED) {
-                const int64_t f = n0 + 32 * wc + col;
-                if (f >= p.half) continue;
-                float xv = acc[i][0][e] * kSplitUp;
-                float gv = acc[i][1][e] * kSplitUp;
-                xv = apply_chain(p.chain, xv, f, i1, i2, i3);
-                gv = apply_chain(p.chain, gv, p.half + f, i1, i2, i3);
-                p.y[m * p.ldy + f] = xv * gelu(gv);
-            } else {
+            for (int e = 0; e < 16; ++e) {
+                xv[e] = acc[i][0][e] * kSplitUp;
+                gv[e] = acc[i][1][e] * kSplitUp;
+            }
+            apply_chain_block(p.chain, xv, [&](int s, int e) {
+                return fc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+            });
+            apply_chain_block(p.chain, gv, [&](int s, int e) {
+                return (p.half + fc) * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+            });
+            if (f >= p.half) continue;
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int64_t n = n0 + wc * 32 * TN + 32 * j + col;
-                    if (n >= p.N) continue;
-                    float v = acc[i][j][e] * kSplitUp;
-                    float *out = p.y + m * p.ldy + n;
-                    if (p.from_redirect) v = __fadd_rn(*out, v);
-                    v = apply_chain(p.chain, v, n, i1, i2, i3);
-                    *out = v;
+            for (int e = 0; e < 16; ++e) {
+                const int64_t m = mbase + acc_row(e, lane);
+                if (m < p.M) p.y[m * p.ldy + f] = xv[e] * gelu(gv[e]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int64_t n = n0 + wc * 32 * TN + 32 * j + col;
+                const int64_t nc = n < p.N ? n : p.N - 1;
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+                if (p.from_redirect) {
+                    float r[16];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) r[e] = p.y[row(e) * p.ldy + nc];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(r[e], v[e]);
+                }
+                apply_chain_block(p.chain, v, [&](int s, int e) {
+                    return nc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+                });
+                if (n >= p.N) continue;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int64_t m = mbase + acc_row(e, lane);
+                    if (m < p.M) p.y[m * p.ldy + n] = v[e];
                 }
             }
         }
@@ -290,41 +324,59 @@ template <int BN, bool POINTWISE>
 struct ColumnsTile {
     static constexpr int kLoads = BN * kBK / 4 / 256;
     float v[kLoads][4];
+    // Per load slot, fixed over K: the image's first element (or -1 past the
+    // last position) and the position's first input row and column.
+    int64_t base[kLoads];
+    int32_t iy0[kLoads], ix0[kLoads];
 
-    __device__ void load(const ConvArgs &c, int64_t p0, int64_t k0, int tid) {
+    __device__ void init(const ConvArgs &c, int64_t p0, int tid) {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int idx = tid + 256 * i;
-            const int pl = idx % BN;
+            const int64_t pos = p0 + idx % BN;
+            base[i] = -1;
+            if (pos >= c.P) continue;
+            uint32_t ox, oy, n;
+            split_index(static_cast<uint32_t>(pos), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy,
+                        n);
+            base[i] = static_cast<int64_t>(n) * c.xnb3;
+            if (POINTWISE) {
+                base[i] += static_cast<int64_t>(oy) * c.xnb1 + ox;
+            } else {
+                iy0[i] = static_cast<int32_t>(oy) * c.s1 - c.p1;
+                ix0[i] = static_cast<int32_t>(ox) * c.s0 - c.p0;
+            }
+        }
+    }
+
+    __device__ void load(const ConvArgs &c, int64_t k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int idx = tid + 256 * i;
             const int kq = (idx / BN) * 4;
-            const int64_t pos = p0 + pl;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[i][e] = 0.0f;
-            if (pos >= c.P) continue;
-            const int64_t n = pos / c.plane;
-            const int64_t rem = pos - n * c.plane;
-            const int64_t oy = rem / c.ow;
-            const int64_t ox = rem - oy * c.ow;
-            const float *img = c.x + n * c.xnb3;
+            if (base[i] < 0) continue;
+            const float *img = c.x + base[i];
             if (POINTWISE) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int64_t k = k0 + kq + e;
-                    if (k < c.K) v[i][e] = img[k * c.xnb2 + oy * c.xnb1 + ox];
+                    if (k < c.K) v[i][e] = img[k * c.xnb2];
                 }
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int64_t k = k0 + kq + e;
+                    const uint32_t k = static_cast<uint32_t>(k0 + kq + e);
                     if (k >= c.K) continue;
-                    const int64_t ic = k / c.taps;
-                    const int64_t t = k - ic * c.taps;
-                    const int64_t kh = t / c.kw;
-                    const int64_t kw = t - kh * c.kw;
-                    const int64_t iy = oy * c.s1 + kh * c.d1 - c.p1;
-                    const int64_t ix = ox * c.s0 + kw * c.d0 - c.p0;
+                    const uint32_t ic = k / static_cast<uint32_t>(c.taps);
+                    const uint32_t t = k - ic * static_cast<uint32_t>(c.taps);
+                    const uint32_t kh = t / static_cast<uint32_t>(c.kw);
+                    const uint32_t kw = t - kh * static_cast<uint32_t>(c.kw);
+                    const int32_t iy = iy0[i] + static_cast<int32_t>(kh) * c.d1;
+                    const int32_t ix = ix0[i] + static_cast<int32_t>(kw) * c.d0;
                     if (iy >= 0 && iy < c.ih && ix >= 0 && ix < c.iw) {
-                        v[i][e] = img[ic * c.xnb2 + iy * c.xnb1 + ix];
+                        v[i][e] = img[static_cast<int64_t>(ic) * c.xnb2 + static_cast<int64_t>(iy) * c.xnb1 + ix];
                     }
                 }
             }
@@ -381,8 +433,9 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     F16RowsTile<BM, VECW> wa;
     ColumnsTile<BN, POINTWISE> xb;
     const int64_t steps = (c.K + kBK - 1) / kBK;
+    xb.init(c, p0, tid);
     wa.load(c.w, c.K, w_row, 0, c.K, tid);
-    xb.load(c, p0, 0, tid);
+    xb.load(c, 0, tid);
     wa.store(lds[0], tid);
     xb.store(lds[0] + BM * kLdk, lds[0] + (BM + BN) * kLdk, tid);
     __syncthreads();
@@ -390,7 +443,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
         const int cur = s & 1;
         if (s + 1 < steps) {
             wa.load(c.w, c.K, w_row, (s + 1) * kBK, c.K, tid);
-            xb.load(c, p0, (s + 1) * kBK, tid);
+            xb.load(c, (s + 1) * kBK, tid);
         }
         const _Float16 *base = lds[cur];
         mfma_step<TM, TN, false>(acc, base + (wr * 32 * TM) * kLdk, nullptr, base + (BM + wc * 32 * TN) * kLdk,
@@ -407,21 +460,38 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     for (int j = 0; j < TN; ++j) {
         const int64_t pos = p0 + wc * 32 * TN + 32 * j + col;
         if (pos >= c.P) continue;
-        const int64_t n = pos / c.plane;
-        const int64_t rem = pos - n * c.plane;
-        const int64_t oy = rem / c.ow;
-        const int64_t ox = rem - oy * c.ow;
+        uint32_t ox, oy, n;
+        split_index(static_cast<uint32_t>(pos), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
+        const int64_t at = static_cast<int64_t>(n) * c.ynb3 + static_cast<int64_t>(oy) * c.ynb1 + ox;
+        const int64_t in_image = static_cast<int64_t>(oy) * c.ow + ox;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
+            const int64_t obase = oc0 + wr * 32 * TM + 32 * i;
+            // Channels past OC read the last and are not stored.
+            const auto chan = [&](int e) -> int64_t {
+                const int64_t oc = obase + acc_row(e, lane);
+                return oc < c.oc ? oc : c.oc - 1;
+            };
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+            if (c.from_redirect) {
+                float r[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) r[e] = c.y[at + chan(e) * c.ynb2];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(r[e], v[e]);
+            }
+            apply_chain_block(c.chain, v, [&](int s, int e) {
+                const DevStep &st = c.chain.steps[s];
+                const int64_t xy = st.flat01 ? in_image * st.nb[0]
+                                             : static_cast<int64_t>(ox) * st.nb[0] + static_cast<int64_t>(oy) * st.nb[1];
+                return xy + chan(e) * st.nb[2] + static_cast<int64_t>(n) * st.nb[3];
+            });
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int64_t oc = oc0 + wr * 32 * TM + 32 * i + acc_row(e, lane);
-                if (oc >= c.oc) continue;
-                float v = acc[i][j][e] * kSplitUp;
-                float *out = c.y + n * c.ynb3 + oc * c.ynb2 + oy * c.ynb1 + ox;
-                if (c.from_redirect) v = __fadd_rn(*out, v);
-                v = apply_chain(c.chain, v, ox, oy, oc, n);
-                *out = v;
+                const int64_t oc = obase + acc_row(e, lane);
+                if (oc < c.oc) c.y[at + oc * c.ynb2] = v[e];
             }
         }
     }
@@ -438,6 +508,7 @@ hipError_t launch_mul_mat_t(const MulMatArgs &p, hipStream_t stream) {
     const bool vx = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0;
     const bool vw = p.ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+    KernelScope scope(GATED ? "mul_mat_gated" : "mul_mat", stream);
     if (vx && vw) {
         hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true>), grid, block, 0, stream, a);
     } else if (vx) {
@@ -459,6 +530,7 @@ hipError_t launch_conv_t(const ConvArgs &c, hipStream_t stream) {
     const int64_t blocks = ((c.P + BN - 1) / BN) * a.oc_blocks;
     const bool vw = c.K % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+    KernelScope scope(POINTWISE ? "conv_direct_pointwise" : "conv_direct", stream);
     if (vw) {
         hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true>), grid, block, 0, stream, a);
     } else {

@@ -8,6 +8,7 @@
 
 #include "host.h"
 #include "norm.h"
+#include "profile.h"
 
 namespace sdhip {
 
@@ -21,8 +22,10 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// The sum of a block's values, every thread receiving it.
-__device__ double block_sum(double v, double *scratch) {
+constexpr int kGroupThreads = 1024;
+
+// The sum of a block of kGroupThreads' values, every thread receiving it.
+__device__ double group_block_sum(double v, double *scratch) {
     v = wave_sum(v);
     const int wave = threadIdx.x >> 6;
     __syncthreads();
@@ -30,14 +33,17 @@ __device__ double block_sum(double v, double *scratch) {
     __syncthreads();
     double s = 0.0;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s += scratch[w];
+    for (int w = 0; w < kGroupThreads / 64; ++w) s += scratch[w];
     return s;
 }
 
-// One block per (image, group): the group's channels are consecutive planes,
-// ne0 * ne1 * channels numbers one after another.
-__global__ __launch_bounds__(kThreads) void group_norm_kernel(GroupNormArgs a) {
-    __shared__ double scratch[kThreads / 64];
+// One block of 16 waves per (image, group): the group's channels are
+// consecutive planes, ne0 * ne1 * channels numbers one after another, read
+// four at a time where they are aligned.  The output goes channel by channel,
+// so that a position's coordinates need no division unless the chain reads
+// operands along the rows.
+__global__ __launch_bounds__(kGroupThreads) void group_norm_kernel(GroupNormArgs a) {
+    __shared__ double scratch[kGroupThreads / 64];
     const int64_t item = blockIdx.x;
     const int64_t i3 = item / a.groups;
     const int64_t g = item % a.groups;
@@ -47,23 +53,71 @@ __global__ __launch_bounds__(kThreads) void group_norm_kernel(GroupNormArgs a) {
     const int64_t plane = a.ne0 * a.ne1;
     const int64_t count = plane * (c1 - c0);
     const float *x = a.x + i3 * a.xnb3 + c0 * a.xnb2;
+    const bool vec = count % 4 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+    const int tid = threadIdx.x;
     double s = 0.0;
-    for (int64_t i = threadIdx.x; i < count; i += kThreads) s += static_cast<double>(x[i]);
-    const float mean = static_cast<float>(block_sum(s, scratch) / static_cast<double>(count));
-    double q = 0.0;
-    for (int64_t i = threadIdx.x; i < count; i += kThreads) {
-        const float d = x[i] - mean;
-        q += static_cast<double>(__fmul_rn(d, d));
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        for (int64_t i = tid; i < count / 4; i += kGroupThreads) {
+            const float4 v = x4[i];
+            s += static_cast<double>(v.x);
+            s += static_cast<double>(v.y);
+            s += static_cast<double>(v.z);
+            s += static_cast<double>(v.w);
+        }
+    } else {
+        for (int64_t i = tid; i < count; i += kGroupThreads) s += static_cast<double>(x[i]);
     }
-    const float variance = static_cast<float>(block_sum(q, scratch) / static_cast<double>(count));
+    const float mean = static_cast<float>(group_block_sum(s, scratch) / static_cast<double>(count));
+    double q = 0.0;
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        for (int64_t i = tid; i < count / 4; i += kGroupThreads) {
+            const float4 v = x4[i];
+            const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+            q += static_cast<double>(__fmul_rn(d0, d0));
+            q += static_cast<double>(__fmul_rn(d1, d1));
+            q += static_cast<double>(__fmul_rn(d2, d2));
+            q += static_cast<double>(__fmul_rn(d3, d3));
+        }
+    } else {
+        for (int64_t i = tid; i < count; i += kGroupThreads) {
+            const float d = x[i] - mean;
+            q += static_cast<double>(__fmul_rn(d, d));
+        }
+    }
+    const float variance = static_cast<float>(group_block_sum(q, scratch) / static_cast<double>(count));
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
     float *y = a.y + i3 * a.ynb3 + c0 * a.ynb2;
-    for (int64_t i = threadIdx.x; i < count; i += kThreads) {
-        const int64_t c = i / plane;
-        const int64_t r = (i - c * plane) / a.ne0;
-        const int64_t i0 = i - c * plane - r * a.ne0;
-        const float v = __fmul_rn(x[i] - mean, scale);
-        y[i] = apply_chain(a.chain, v, i0, r, c0 + c, i3);
+    // Four numbers of a thread at a time, their chain's loads before their
+    // stores; those past the plane read its last and are not stored.
+    constexpr int kU = 4;
+    for (int64_t c = c0; c < c1; ++c) {
+        const float *xc = x + (c - c0) * plane;
+        float *yc = y + (c - c0) * plane;
+        for (int64_t i = tid; i < plane; i += kGroupThreads * kU) {
+            const auto at = [&](int u) -> int64_t {
+                const int64_t j = i + static_cast<int64_t>(u) * kGroupThreads;
+                return j < plane ? j : plane - 1;
+            };
+            float v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = __fmul_rn(xc[at(u)] - mean, scale);
+            apply_chain_block(a.chain, v, [&](int s, int u) {
+                const DevStep &st = a.chain.steps[s];
+                int64_t xy = at(u) * st.nb[0];
+                if (!st.flat01) {
+                    const uint32_t r = static_cast<uint32_t>(at(u)) / static_cast<uint32_t>(a.ne0);
+                    xy = (at(u) - static_cast<int64_t>(r) * a.ne0) * st.nb[0] + static_cast<int64_t>(r) * st.nb[1];
+                }
+                return xy + c * st.nb[2] + i3 * st.nb[3];
+            });
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int64_t j = i + static_cast<int64_t>(u) * kGroupThreads;
+                if (j < plane) yc[j] = v[u];
+            }
+        }
     }
 }
 
@@ -87,20 +141,36 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(NormArgs a) {
     }
     const float variance = static_cast<float>(wave_sum(q) / static_cast<double>(a.ne0));
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
-    for (int64_t i = lane; i < a.ne0; i += 64) {
-        const float v = __fmul_rn(x[i] - mean, scale);
-        y[i] = apply_chain(a.chain, v, i, i1, i2, i3);
+    constexpr int kU = 4;
+    for (int64_t i = lane; i < a.ne0; i += 64 * kU) {
+        const auto at = [&](int u) -> int64_t {
+            const int64_t j = i + 64 * u;
+            return j < a.ne0 ? j : a.ne0 - 1;
+        };
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = __fmul_rn(x[at(u)] - mean, scale);
+        apply_chain_block(a.chain, v, [&](int s, int u) {
+            const DevStep &st = a.chain.steps[s];
+            return at(u) * st.nb[0] + i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+        });
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            if (i + 64 * u < a.ne0) y[i + 64 * u] = v[u];
+        }
     }
 }
 
 }  // namespace
 
 hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL(group_norm_kernel, dim3(a.groups * a.ne3), dim3(kThreads), 0, stream, a);
+    KernelScope scope("group_norm", stream);
+    hipLaunchKernelGGL(group_norm_kernel, dim3(a.groups * a.ne3), dim3(kGroupThreads), 0, stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_norm(const NormArgs &a, hipStream_t stream) {
+    KernelScope scope("norm", stream);
     hipLaunchKernelGGL(norm_kernel, dim3(ceil_div(a.rows, kThreads / 64)), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }

@@ -1,13 +1,38 @@
-// FLASH_ATTN_EXT on the device (attention.cc): placeholder until the kernel lands.
+// FLASH_ATTN_EXT on the device: the predicate of attention_supported
+// (attention.cc:828-845) and the launch.
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "attention.h"
 #include "host.h"
 
 using namespace sdhip;
 
+namespace {
+
+bool kv_type(const sdhip_tensor *t) { return holds_f32(t) || holds_f16(t); }
+
+}  // namespace
+
 extern "C" {
 
-int sdhip_attention_supported(const sdhip_tensor *, const sdhip_tensor *, const sdhip_tensor *, const sdhip_tensor *,
-                              float, float) {
-    return 0;
+int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                              const sdhip_tensor *y, float max_bias, float softcap) {
+    if (q == nullptr || k == nullptr || v == nullptr || y == nullptr) return 0;
+    // No mask, ALiBi or soft cap; q single precision, k and v single
+    // precision or FP16, each of elements one after another along ne[0]; the
+    // heads of q a multiple of those of k (attention.cc:828-845).  Heads of
+    // more than kAttentionMaxDims dimensions are left to the caller.
+    const bool shapes = q->ne[0] == k->ne[0] && k->ne[1] == v->ne[1] && k->ne[2] == v->ne[2] && k->ne[2] > 0 &&
+                        q->ne[2] % k->ne[2] == 0 && q->ne[3] == k->ne[3] && q->ne[3] == v->ne[3] && k->ne[1] >= 1 &&
+                        y->ne[0] == v->ne[0] && y->ne[1] == q->ne[2] && y->ne[2] == q->ne[1] && y->ne[3] == q->ne[3];
+    return max_bias == 0.0f && softcap == 0.0f && holds_f32(q) && kv_type(k) && kv_type(v) && holds_f32(y) &&
+           contiguous(y) && shapes && q->ne[0] <= kAttentionMaxDims && v->ne[0] <= kAttentionMaxDims &&
+           q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 && q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 &&
+           k->nb[2] % k->nb[0] == 0 && k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 &&
+           v->nb[2] % v->nb[0] == 0 && v->nb[3] % v->nb[0] == 0;
 }
 
 size_t sdhip_attention_work_size(const sdhip_tensor *, const sdhip_tensor *, const sdhip_tensor *,
@@ -15,9 +40,40 @@ size_t sdhip_attention_work_size(const sdhip_tensor *, const sdhip_tensor *, con
     return 0;
 }
 
-sdhip_status sdhip_attention(const sdhip_tensor *, const sdhip_tensor *, const sdhip_tensor *, const sdhip_tensor *,
-                             float, float, float, void *, size_t, void *) {
-    return fail(SDHIP_UNSUPPORTED, "attention: not built yet");
+sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                             const sdhip_tensor *y, float scale, float max_bias, float softcap, void *, size_t,
+                             void *stream) {
+    if (!sdhip_attention_supported(q, k, v, y, max_bias, softcap)) {
+        return fail(SDHIP_UNSUPPORTED, "attention: operands not taken");
+    }
+    AttentionArgs a{};
+    a.q = static_cast<const float *>(q->data);
+    a.qnb1 = q->nb[1] / 4;
+    a.qnb2 = q->nb[2] / 4;
+    a.qnb3 = q->nb[3] / 4;
+    a.k = k->data;
+    a.khalf = k->type == SDHIP_TYPE_F16;
+    a.knb1 = k->nb[1] / k->nb[0];
+    a.knb2 = k->nb[2] / k->nb[0];
+    a.knb3 = k->nb[3] / k->nb[0];
+    a.v = v->data;
+    a.vhalf = v->type == SDHIP_TYPE_F16;
+    a.vnb1 = v->nb[1] / v->nb[0];
+    a.vnb2 = v->nb[2] / v->nb[0];
+    a.vnb3 = v->nb[3] / v->nb[0];
+    a.y = static_cast<float *>(y->data);
+    a.ynb1 = y->nb[1] / 4;
+    a.ynb2 = y->nb[2] / 4;
+    a.ynb3 = y->nb[3] / 4;
+    a.d = q->ne[0];
+    a.dv = v->ne[0];
+    a.lq = q->ne[1];
+    a.lk = k->ne[1];
+    a.h = q->ne[2];
+    a.hk = k->ne[2];
+    a.b = q->ne[3];
+    a.scale = scale;
+    return launched(launch_attention(a, static_cast<hipStream_t>(stream)), "attention");
 }
 
 }  // extern "C"

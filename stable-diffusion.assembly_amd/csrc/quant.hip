@@ -1,12 +1,468 @@
+// The bits mode of the linear layers (quant.h, quant.cc, mul_mat.cc:378-646)
+// on gfx950's integer MFMA.
+//
+// Quantization, bit for bit as the reference's C++ form does it:
+//   inputs, per (row, group of k) (quant.cc:282-315): lo = min(0, min x),
+//     hi = max(0, max x), s = (hi - lo) / levels, inv = s > 0 ? 1 / s : 0,
+//     z = rint(-lo * inv), q = clamp(rint(x * inv) + z, 0, levels), the
+//     group's tail the zero point z; offset = s * z;
+//   weights, per (column, group) or per whole column (quant.cc:204-243):
+//     s = max |w| / wmax, inv = s > 0 ? 1 / s : 0,
+//     q = clamp(rint(w * inv), -wmax, wmax); offset = s * sum(q).
+// Every operation is an IEEE one (correctly rounded division, round to
+// nearest-even), so the bytes, scales and offsets are the reference's.
+//
+// Products: the MFMA multiplies signed bytes, so the inputs are stored as
+// q - 128 and the group's integer sum restored exactly as
+// S = sum((q - 128) w) + 128 sum(w).  Each group then adds to the output, in
+// the reference's order and roundings (quant.cc:150-155):
+//     t = fma(sa * sb, float(S), t);  t = fma(-oa, ob, t)
+// so that the result is the reference's C++ result, bit for bit, when the
+// sum starts from the same number (0, or the residual with from_redirect).
+//
+// Layout in the work buffer: each group of k padded to a slot of 64 bytes
+// (the MFMA's k), inputs [M][groups][slot] and weights [N][groups][slot],
+// then the scales, offsets and (weights) integer sums [rows][groups].
+
 #include "host.h"
+#include "profile.h"
 #include "quant.h"
 
 namespace sdhip {
 
-size_t quantized_linear_work_size(int64_t, int64_t, int64_t) { return 0; }
+namespace {
 
-sdhip_status quantized_linear(const MulMatArgs &, bool, void *, hipStream_t) {
-    return fail(SDHIP_UNSUPPORTED, "quantized products are not built yet");
+struct Quant {
+    int group;  // numbers of k sharing a scale
+    int levels;
+    int wmax;
+    int weight_groups;
+};
+
+Quant quant_of(const Tuning &t) {
+    Quant q;
+    int quads = t.group / 4;
+    quads = quads < 1 ? 1 : (quads > 256 ? 256 : quads);
+    q.group = 4 * quads;
+    const int ib = t.input_bits < 2 ? 2 : (t.input_bits > 8 ? 8 : t.input_bits);
+    const int wb = t.bits < 2 ? 2 : (t.bits > 8 ? 8 : t.bits);
+    q.levels = (1 << ib) - 1;
+    q.wmax = (1 << (wb - 1)) - 1;
+    q.weight_groups = t.weight_group != 0;
+    return q;
+}
+
+struct Layout {
+    int64_t groups, slot, kp;  // groups of k, bytes a group takes, bytes a row takes
+    size_t xq, xs, xo, wq, ws, wo, wsum, total;
+};
+
+Layout layout_of(int64_t K, int64_t N, int64_t M, const Quant &q) {
+    Layout l{};
+    l.groups = ceil_div(K, q.group);
+    l.slot = round_up(q.group, 64);
+    l.kp = l.groups * l.slot;
+    size_t at = 0;
+    const auto take = [&](size_t bytes) {
+        const size_t here = at;
+        at += static_cast<size_t>(round_up(static_cast<int64_t>(bytes), 256));
+        return here;
+    };
+    l.xq = take(static_cast<size_t>(M * l.kp));
+    l.xs = take(static_cast<size_t>(M * l.groups) * 4);
+    l.xo = take(static_cast<size_t>(M * l.groups) * 4);
+    l.wq = take(static_cast<size_t>(N * l.kp));
+    l.ws = take(static_cast<size_t>(N * l.groups) * 4);
+    l.wo = take(static_cast<size_t>(N * l.groups) * 4);
+    l.wsum = take(static_cast<size_t>(N * l.groups) * 4);
+    l.total = at;
+    return l;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// ------------------------------------------------------------------ inputs
+
+// One wave per (row, group): the group's least and greatest (with 0), its
+// scale and zero point, and its bytes, stored as q - 128.
+__global__ __launch_bounds__(256) void quantize_inputs_kernel(const float *__restrict__ x, int64_t ldx, int64_t M,
+                                                              int64_t K, Quant q, Layout l, int8_t *__restrict__ xq,
+                                                              float *__restrict__ xs, float *__restrict__ xo) {
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= M * l.groups) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t m = item / l.groups;
+    const int64_t g = item - m * l.groups;
+    const int64_t k0 = g * q.group;
+    const int64_t n = K - k0 < q.group ? K - k0 : q.group;
+    const float *row = x + m * ldx + k0;
+    float lo = 0.0f, hi = 0.0f;
+    for (int64_t e = lane; e < n; e += 64) {
+        lo = fminf(lo, row[e]);
+        hi = fmaxf(hi, row[e]);
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    const float levels = static_cast<float>(q.levels);
+    const float s = __fdiv_rn(__fsub_rn(hi, lo), levels);
+    const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+    const float zero = rintf(__fmul_rn(-lo, inverse));
+    int8_t *dst = xq + m * l.kp + g * l.slot;
+    for (int64_t e = lane; e < l.slot; e += 64) {
+        float v = 0.0f;
+        if (e < n) {
+            v = clampf(__fadd_rn(rintf(__fmul_rn(row[e], inverse)), zero), 0.0f, levels);
+        } else if (e < q.group) {
+            v = zero;  // the group's tail stands for zeros
+        } else {
+            v = 128.0f;  // the slot's padding: 0 after the shift, times a weight of 0
+        }
+        dst[e] = static_cast<int8_t>(static_cast<int>(v) - 128);
+    }
+    if (lane == 0) {
+        xs[m * l.groups + g] = s;
+        xo[m * l.groups + g] = __fmul_rn(s, zero);
+    }
+}
+
+// ------------------------------------------------------------------ weights
+
+// One wave per column (a row of W): the whole row's greatest magnitude when
+// the weights have one scale a row, then group by group the scale, the
+// bytes and their sum.
+__global__ __launch_bounds__(256) void quantize_weights_kernel(const _Float16 *__restrict__ w, int64_t ldw, int64_t N,
+                                                               int64_t K, Quant q, Layout l, int8_t *__restrict__ wq,
+                                                               float *__restrict__ ws, float *__restrict__ wo,
+                                                               int32_t *__restrict__ wsum) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const int lane = threadIdx.x & 63;
+    const _Float16 *row = w + n * ldw;
+    float row_max = 0.0f;
+    if (!q.weight_groups) {
+        for (int64_t e = lane; e < K; e += 64) row_max = fmaxf(row_max, fabsf(static_cast<float>(row[e])));
+        row_max = wave_max(row_max);
+    }
+    const float wmax = static_cast<float>(q.wmax);
+    for (int64_t g = 0; g < l.groups; ++g) {
+        const int64_t k0 = g * q.group;
+        const int64_t cnt = K - k0 < q.group ? K - k0 : q.group;
+        float m = row_max;
+        if (q.weight_groups) {
+            float mm = 0.0f;
+            for (int64_t e = lane; e < cnt; e += 64) mm = fmaxf(mm, fabsf(static_cast<float>(row[k0 + e])));
+            m = wave_max(mm);
+        }
+        const float s = __fdiv_rn(m, wmax);
+        const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+        int8_t *dst = wq + n * l.kp + g * l.slot;
+        int sum = 0;
+        for (int64_t e = lane; e < l.slot; e += 64) {
+            int v = 0;
+            if (e < cnt) {
+                v = static_cast<int>(clampf(rintf(__fmul_rn(static_cast<float>(row[k0 + e]), inverse)), -wmax, wmax));
+            }
+            dst[e] = static_cast<int8_t>(v);
+            sum += v;
+        }
+        sum = wave_isum(sum);
+        if (lane == 0) {
+            ws[n * l.groups + g] = s;
+            wo[n * l.groups + g] = __fmul_rn(s, static_cast<float>(sum));
+            wsum[n * l.groups + g] = sum;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ products
+
+// A block of 64 rows (tokens) by 64 columns (features) by 4 waves of 32 x 32,
+// each 2 x 2 tiles of 16 x 16 on v_mfma_i32_16x16x64_i8; k a group's slot at
+// a time through LDS, double-buffered.  After each group the lane's 16
+// integer sums are scaled into its 16 single-precision outputs.  GATED: the
+// block's 64 columns are 32 features of the first half and the same 32 of
+// the second, each wave's two column tiles a pair (x, gate).
+constexpr int kQB = 64;
+constexpr int kQLd = 64 + 16;  // bytes per LDS row
+
+struct QgemmArgs {
+    const int8_t *xq, *wq;
+    const float *xs, *xo, *ws, *wo;
+    const int32_t *wsum;
+    float *y;
+    int64_t ldy;
+    int64_t M, N, half;
+    int64_t ne1, ne2;
+    int64_t groups, slot, kp;
+    int64_t col_blocks;
+    int32_t from_redirect;
+    DevChain chain;
+};
+
+template <bool GATED>
+__global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
+    __shared__ __attribute__((aligned(16))) int8_t la[2][kQB * kQLd];
+    __shared__ __attribute__((aligned(16))) int8_t lb[2][kQB * kQLd];
+    __shared__ float sa[2][kQB], oa[2][kQB], sb[2][kQB], ob[2][kQB];
+    __shared__ int32_t qs[2][kQB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int lr = lane & 15, lg = lane >> 4;
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t mb = b / p.col_blocks;
+    const int64_t nb = b % p.col_blocks;
+    const int64_t m0 = mb * kQB;
+    const int64_t n0 = nb * (GATED ? kQB / 2 : kQB);
+    // The global row of W that LDS row r of the block holds, or -1.
+    const auto w_row = [&](int r) -> int64_t {
+        if (GATED) {
+            const int side = (r >> 4) & 1;
+            const int64_t f = n0 + 16 * (r >> 5) + (r & 15);
+            return f < p.half ? side * p.half + f : -1;
+        }
+        return n0 + r < p.N ? n0 + r : -1;
+    };
+
+    // Global loads: 64 rows x 64 bytes of each operand = 256 x 16 bytes, one
+    // a thread each; the group's scales by the first threads.
+    const int lrow = tid >> 2, lq = (tid & 3) * 16;
+    const int64_t arow = m0 + lrow < p.M ? m0 + lrow : -1;
+    const int64_t brow = w_row(lrow);
+    int4v ra, rb;
+    float rsa = 0.f, roa = 0.f, rsb = 0.f, rob = 0.f;
+    int32_t rqs = 0;
+    const auto load = [&](int64_t g, int64_t sub) {
+        const int64_t off = g * p.slot + sub * 64 + lq;
+        ra = arow >= 0 ? *reinterpret_cast<const int4v *>(p.xq + arow * p.kp + off) : int4v{};
+        rb = brow >= 0 ? *reinterpret_cast<const int4v *>(p.wq + brow * p.kp + off) : int4v{};
+        if (tid < kQB) {
+            const int64_t r = m0 + tid;
+            rsa = r < p.M ? p.xs[r * p.groups + g] : 0.0f;
+            roa = r < p.M ? p.xo[r * p.groups + g] : 0.0f;
+        } else if (tid < 2 * kQB) {
+            const int64_t c = w_row(tid - kQB);
+            rsb = c >= 0 ? p.ws[c * p.groups + g] : 0.0f;
+            rob = c >= 0 ? p.wo[c * p.groups + g] : 0.0f;
+            rqs = c >= 0 ? p.wsum[c * p.groups + g] : 0;
+        }
+    };
+    const auto store = [&](int buf) {
+        *reinterpret_cast<int4v *>(&la[buf][lrow * kQLd + lq]) = ra;
+        *reinterpret_cast<int4v *>(&lb[buf][lrow * kQLd + lq]) = rb;
+        if (tid < kQB) {
+            sa[buf][tid] = rsa;
+            oa[buf][tid] = roa;
+        } else if (tid < 2 * kQB) {
+            sb[buf][tid - kQB] = rsb;
+            ob[buf][tid - kQB] = rob;
+            qs[buf][tid - kQB] = rqs;
+        }
+    };
+
+    // The outputs: tile (i, j) of the wave, lane rows 4 lg + e, column lr.
+    float t[2][2][4];
+    if (!GATED && p.from_redirect) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t n = n0 + wc * 32 + 16 * j + lr;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t m = m0 + wr * 32 + 16 * i + 4 * lg + e;
+                    t[i][j][e] = (m < p.M && n < p.N) ? p.y[m * p.ldy + n] : 0.0f;
+                }
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[i][j][e] = 0.0f;
+    }
+
+    const int64_t subs = p.slot / 64;
+    const int64_t steps = p.groups * subs;
+    load(0, 0);
+    store(0);
+    __syncthreads();
+    int4v acc[2][2];
+    for (int64_t s = 0; s < steps; ++s) {
+        const int cur = s & 1;
+        const int64_t g = s / subs, sub = s - g * subs;
+        if (s + 1 < steps) load((s + 1) / subs, (s + 1) % subs);
+        if (sub == 0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = int4v{};
+        }
+        int4v a[2], bv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            a[i] = *reinterpret_cast<const int4v *>(&la[cur][(wr * 32 + 16 * i + lr) * kQLd + 16 * lg]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            bv[j] = *reinterpret_cast<const int4v *>(&lb[cur][(wc * 32 + 16 * j + lr) * kQLd + 16 * lg]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bv[j], acc[i][j], 0, 0, 0);
+        if (sub == subs - 1) {
+            // The group's sums into the outputs, as quant.cc:150-155 does.
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = wc * 32 + 16 * j + lr;
+                const float cs = sb[cur][col], co = ob[cur][col];
+                const int32_t shift = 128 * qs[cur][col];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = wr * 32 + 16 * i + 4 * lg + e;
+                        const float ab = __fmul_rn(sa[cur][row], cs);
+                        const float sum = static_cast<float>(acc[i][j][e] + shift);
+                        float v = __builtin_fmaf(ab, sum, t[i][j][e]);
+                        t[i][j][e] = __builtin_fmaf(-oa[cur][row], co, v);
+                    }
+            }
+        }
+        if (s + 1 < steps) store(cur ^ 1);
+        __syncthreads();
+    }
+
+    // The chain, then the stores (or the gated GELU of the pair).
+    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
+    const auto row_off = [&](const DevStep &st, int64_t m) -> int64_t {
+        if (st.flat123) return m * st.nb[1];
+        uint32_t i1, i2, i3;
+        split_index(static_cast<uint32_t>(m), ne1, ne2, i1, i2, i3);
+        return i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t mbase = m0 + wr * 32 + 16 * i + 4 * lg;
+        const auto row = [&](int e) -> int64_t { return mbase + e < p.M ? mbase + e : p.M - 1; };
+        if (GATED) {
+            const int64_t f = n0 + 16 * wc + lr;
+            const int64_t fc = f < p.half ? f : p.half - 1;
+            float xv[4], gv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xv[e] = t[i][0][e];
+                gv[e] = t[i][1][e];
+            }
+            apply_chain_block(p.chain, xv, [&](int s, int e) {
+                return fc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+            });
+            apply_chain_block(p.chain, gv, [&](int s, int e) {
+                return (p.half + fc) * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+            });
+            if (f >= p.half) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (mbase + e < p.M) p.y[(mbase + e) * p.ldy + f] = xv[e] * gelu(gv[e]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t n = n0 + wc * 32 + 16 * j + lr;
+                const int64_t nc = n < p.N ? n : p.N - 1;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = t[i][j][e];
+                apply_chain_block(p.chain, v, [&](int s, int e) {
+                    return nc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+                });
+                if (n >= p.N) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (mbase + e < p.M) p.y[(mbase + e) * p.ldy + n] = v[e];
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+size_t quantized_linear_work_size(int64_t K, int64_t N, int64_t M) {
+    return layout_of(K, N, M, quant_of(tuning())).total;
+}
+
+sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipStream_t stream) {
+    const Quant q = quant_of(tuning());
+    const Layout l = layout_of(a.K, a.N, a.M, q);
+    char *base = static_cast<char *>(work);
+    int8_t *xq = reinterpret_cast<int8_t *>(base + l.xq);
+    float *xs = reinterpret_cast<float *>(base + l.xs);
+    float *xo = reinterpret_cast<float *>(base + l.xo);
+    int8_t *wq = reinterpret_cast<int8_t *>(base + l.wq);
+    float *ws = reinterpret_cast<float *>(base + l.ws);
+    float *wo = reinterpret_cast<float *>(base + l.wo);
+    int32_t *wsum = reinterpret_cast<int32_t *>(base + l.wsum);
+    {
+        KernelScope scope("quantize_inputs", stream);
+        hipLaunchKernelGGL(quantize_inputs_kernel, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream, a.x,
+                           a.ldx, a.M, a.K, q, l, xq, xs, xo);
+    }
+    {
+        KernelScope scope("quantize_weights", stream);
+        hipLaunchKernelGGL(quantize_weights_kernel, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w, a.ldw, a.N,
+                           a.K, q, l, wq, ws, wo, wsum);
+    }
+    QgemmArgs p{};
+    p.xq = xq;
+    p.wq = wq;
+    p.xs = xs;
+    p.xo = xo;
+    p.ws = ws;
+    p.wo = wo;
+    p.wsum = wsum;
+    p.y = a.y;
+    p.ldy = a.ldy;
+    p.M = a.M;
+    p.N = a.N;
+    p.half = a.half;
+    p.ne1 = a.ne1;
+    p.ne2 = a.ne2;
+    p.groups = l.groups;
+    p.slot = l.slot;
+    p.kp = l.kp;
+    p.from_redirect = a.from_redirect;
+    p.chain = a.chain;
+    const int64_t cols = gated ? a.half : a.N;
+    p.col_blocks = ceil_div(cols, gated ? kQB / 2 : kQB);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(a.M, kQB) * p.col_blocks));
+    KernelScope scope(gated ? "qgemm_gated" : "qgemm", stream);
+    if (gated) {
+        hipLaunchKernelGGL(qgemm_kernel<true>, grid, dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
+    }
+    return launched(hipGetLastError(), gated ? "quantized mul_mat_gated" : "quantized mul_mat");
 }
 
 }  // namespace sdhip

@@ -18,6 +18,7 @@
 //      chain says so and the chain after, one thread per (oc, tile).
 
 #include "host.h"
+#include "profile.h"
 #include "winograd.h"
 
 namespace sdhip {
@@ -98,18 +99,15 @@ __global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict
 template <int M>
 __global__ __launch_bounds__(256) void inputs_kernel(WinogradArgs a, float *__restrict__ v) {
     constexpr int A = Mat<M>::A;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= a.tiles * a.ic) return;
-    const int64_t tile = t % a.tiles;
-    const int64_t c = t / a.tiles;
-    const int64_t per_image = a.tw * a.th;
-    const int64_t n = tile / per_image;
-    const int64_t rem = tile - n * per_image;
-    const int64_t ty = rem / a.tw;
-    const int64_t tx = rem - ty * a.tw;
-    const int64_t y0 = ty * M - a.p1;
-    const int64_t x0 = tx * M - a.p0;
-    const float *plane = a.x + n * a.xnb3 + c * a.xnb2;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= static_cast<uint32_t>(a.tiles * a.ic)) return;
+    const uint32_t c = t / static_cast<uint32_t>(a.tiles);
+    const uint32_t tile = t - c * static_cast<uint32_t>(a.tiles);
+    uint32_t tx, ty, n;
+    split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
+    const int64_t y0 = static_cast<int64_t>(ty) * M - a.p1;
+    const int64_t x0 = static_cast<int64_t>(tx) * M - a.p0;
+    const float *plane = a.x + static_cast<int64_t>(n) * a.xnb3 + static_cast<int64_t>(c) * a.xnb2;
     float d[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i) {
@@ -139,7 +137,7 @@ __global__ __launch_bounds__(256) void inputs_kernel(WinogradArgs a, float *__re
             float x = 0.0f;
 #pragma unroll
             for (int j = 0; j < A; ++j) x += bd[r][j] * Mat<M>::bt(s, j);
-            v[(r * A + s) * plane_v + c * a.tiles + tile] = x;
+            v[(r * A + s) * plane_v + static_cast<int64_t>(c) * a.tiles + tile] = x;
         }
 }
 
@@ -282,21 +280,18 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
 template <int M>
 __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod) {
     constexpr int A = Mat<M>::A;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= a.tiles * a.oc) return;
-    const int64_t tile = t % a.tiles;
-    const int64_t oc = t / a.tiles;
-    const int64_t per_image = a.tw * a.th;
-    const int64_t n = tile / per_image;
-    const int64_t rem = tile - n * per_image;
-    const int64_t ty = rem / a.tw;
-    const int64_t tx = rem - ty * a.tw;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= static_cast<uint32_t>(a.tiles * a.oc)) return;
+    const uint32_t oc = t / static_cast<uint32_t>(a.tiles);
+    const uint32_t tile = t - oc * static_cast<uint32_t>(a.tiles);
+    uint32_t tx, ty, n;
+    split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     const int64_t plane = a.oc * a.tiles;
     float m[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
-        for (int j = 0; j < A; ++j) m[i][j] = prod[(i * A + j) * plane + oc * a.tiles + tile];
+        for (int j = 0; j < A; ++j) m[i][j] = prod[(i * A + j) * plane + static_cast<int64_t>(oc) * a.tiles + tile];
     float am[M][A];
 #pragma unroll
     for (int i = 0; i < M; ++i)
@@ -307,22 +302,45 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
             for (int x = 0; x < A; ++x) s += Mat<M>::at(i, x) * m[x][j];
             am[i][j] = s;
         }
-    float *out = a.y + n * a.ynb3 + oc * a.ynb2;
+    // The tile's M x M outputs, their loads (the residual, the chain's
+    // operands) all before their stores; outputs past the image's edge read
+    // its last row or column and are not stored.
+    float v[M * M];
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-        const int64_t yy = ty * M + i;
-        if (yy >= a.oh) continue;
+    for (int i = 0; i < M; ++i)
 #pragma unroll
         for (int jj = 0; jj < M; ++jj) {
-            const int64_t xx = tx * M + jj;
-            if (xx >= a.ow) continue;
-            float v = 0.0f;
+            float s = 0.0f;
 #pragma unroll
-            for (int j = 0; j < A; ++j) v += am[i][j] * Mat<M>::at(jj, j);
-            float *o = out + yy * a.ynb1 + xx;
-            if (a.from_redirect) v = __fadd_rn(*o, v);
-            *o = apply_chain(a.chain, v, xx, yy, oc, n);
+            for (int j = 0; j < A; ++j) s += am[i][j] * Mat<M>::at(jj, j);
+            v[i * M + jj] = s;
         }
+    const auto yy = [&](int e) -> int64_t {
+        const int64_t y = static_cast<int64_t>(ty) * M + e / M;
+        return y < a.oh ? y : a.oh - 1;
+    };
+    const auto xx = [&](int e) -> int64_t {
+        const int64_t x = static_cast<int64_t>(tx) * M + e % M;
+        return x < a.ow ? x : a.ow - 1;
+    };
+    float *out = a.y + static_cast<int64_t>(n) * a.ynb3 + static_cast<int64_t>(oc) * a.ynb2;
+    if (a.from_redirect) {
+        float r[M * M];
+#pragma unroll
+        for (int e = 0; e < M * M; ++e) r[e] = out[yy(e) * a.ynb1 + xx(e)];
+#pragma unroll
+        for (int e = 0; e < M * M; ++e) v[e] = __fadd_rn(r[e], v[e]);
+    }
+    apply_chain_block(a.chain, v, [&](int s, int e) {
+        const DevStep &st = a.chain.steps[s];
+        const int64_t xy = st.flat01 ? (yy(e) * a.ow + xx(e)) * st.nb[0] : xx(e) * st.nb[0] + yy(e) * st.nb[1];
+        return xy + static_cast<int64_t>(oc) * st.nb[2] + static_cast<int64_t>(n) * st.nb[3];
+    });
+#pragma unroll
+    for (int e = 0; e < M * M; ++e) {
+        const int64_t y = static_cast<int64_t>(ty) * M + e / M;
+        const int64_t x = static_cast<int64_t>(tx) * M + e % M;
+        if (y < a.oh && x < a.ow) out[y * a.ynb1 + x] = v[e];
     }
 }
 
@@ -352,14 +370,26 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     float *v = reinterpret_cast<float *>(base + l.v);
     float *m = reinterpret_cast<float *>(base + l.m);
     const int64_t nw = a.oc * a.ic;
-    hipLaunchKernelGGL((weights_kernel<M>), dim3(ceil_div(nw, 256)), dim3(256), 0, stream, a.w, u, a.oc, a.ic);
-    const int64_t ni = a.tiles * a.ic;
-    hipLaunchKernelGGL((inputs_kernel<M>), dim3(ceil_div(ni, 256)), dim3(256), 0, stream, a, v);
-    const int64_t mb = ceil_div(a.oc, kGBM), nb = ceil_div(a.tiles, kGBN);
-    hipLaunchKernelGGL(batched_gemm_f32, dim3(A * A * mb * nb), dim3(256), 0, stream, u, v, m, a.oc, a.tiles, a.ic,
-                       mb, nb);
-    const int64_t no = a.tiles * a.oc;
-    hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(no, 256)), dim3(256), 0, stream, a, m);
+    {
+        KernelScope scope(M == 4 ? "winograd4.weights" : "winograd2.weights", stream);
+        hipLaunchKernelGGL((weights_kernel<M>), dim3(ceil_div(nw, 256)), dim3(256), 0, stream, a.w, u, a.oc, a.ic);
+    }
+    {
+        KernelScope scope(M == 4 ? "winograd4.inputs" : "winograd2.inputs", stream);
+        const int64_t ni = a.tiles * a.ic;
+        hipLaunchKernelGGL((inputs_kernel<M>), dim3(ceil_div(ni, 256)), dim3(256), 0, stream, a, v);
+    }
+    {
+        KernelScope scope(M == 4 ? "winograd4.products" : "winograd2.products", stream);
+        const int64_t mb = ceil_div(a.oc, kGBM), nb = ceil_div(a.tiles, kGBN);
+        hipLaunchKernelGGL(batched_gemm_f32, dim3(A * A * mb * nb), dim3(256), 0, stream, u, v, m, a.oc, a.tiles,
+                           a.ic, mb, nb);
+    }
+    {
+        KernelScope scope(M == 4 ? "winograd4.outputs" : "winograd2.outputs", stream);
+        const int64_t no = a.tiles * a.oc;
+        hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(no, 256)), dim3(256), 0, stream, a, m);
+    }
     return launched(hipGetLastError(), "winograd");
 }
 

@@ -56,6 +56,11 @@ SIGNATURES = [
     ("sdhip_set_tuning", ctypes.c_int, [ctypes.c_char_p]),
     ("sdhip_get_tuning", ctypes.c_int, [ctypes.c_char_p]),
     ("sdhip_forget", None, [_P, _SZ]),
+    ("sdhip_profile_enable", None, [ctypes.c_int]),
+    ("sdhip_profile_reset", None, []),
+    ("sdhip_profile_collect", ctypes.c_int, []),
+    ("sdhip_profile_entry", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
     ("sdhip_mul_mat_supported", ctypes.c_int, [_T, _T, _T]),
     ("sdhip_mul_mat_work_size", _SZ, [_T, _T, _T]),
     ("sdhip_mul_mat", ctypes.c_int, [_T, _T, _T, _E, _P, _SZ, _P]),
@@ -241,3 +246,25 @@ def group_norm(x, y, groups, eps, chain=None):
 def norm(x, y, eps, chain=None):
     check(load().sdhip_norm(desc(x), desc(y), eps, ctypes.byref(chain) if chain else None, stream_handle()),
           "norm")
+
+
+def profile_enable(on=True):
+    load().sdhip_profile_enable(1 if on else 0)
+
+
+def profile_reset():
+    load().sdhip_profile_reset()
+
+
+def profile_collect():
+    """{kernel name: (total ms, launches)} of the launches since the reset."""
+    lib = load()
+    count = lib.sdhip_profile_collect()
+    out = {}
+    for i in range(count):
+        name = ctypes.c_char_p()
+        ms = ctypes.c_double()
+        n = ctypes.c_int64()
+        if lib.sdhip_profile_entry(i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)):
+            out[name.value.decode()] = (ms.value, n.value)
+    return out

@@ -38,6 +38,7 @@ def lib():
         L.oracle_gelu.restype = _F
         L.oracle_gelu.argtypes = [_F]
         L.oracle_silu_array.argtypes = [_f, _L]
+        L.oracle_gated_gelu_array.argtypes = [_f, _f, _f, _L]
         L.oracle_exact_mul_mat.argtypes = [_f, _L, _f, _L, _L, _L, _L, _d, _d]
         L.oracle_exact_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L, _d, _d]
         L.oracle_exact_conv2d_at.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L,
@@ -158,6 +159,14 @@ def silu(v):
     """SiLU with the reference's exponential (scalar_math.h:54-56)."""
     out = np.array(v, dtype=np.float32, copy=True, order="C")
     lib().oracle_silu_array(out, out.size)
+    return out
+
+
+def gated_gelu(x, gate):
+    """x * GELU(gate) with the reference's GELU (fusion.cc:290-310)."""
+    x, gate = c32(x), c32(gate)
+    out = np.empty_like(x)
+    lib().oracle_gated_gelu_array(x, gate, out, out.size)
     return out
 
 

@@ -1,0 +1,87 @@
+"""FLASH_ATTN_EXT on the device against the float64 oracle (the textbook
+softmax in double, ops_test.cc:517-553) by the reference's metric, at the
+reference's own cases (ops_test.cc:925-938) and the SD1.5 attention of the
+bench configuration (at full size, a sample of the queries)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as orc
+import sdhip
+from helpers import dev, rng, uniform, unwritten
+
+BOUND = 1e-6  # attention, |error| / sum |products| against float64
+
+# d, lq, lk, h, hk, b, FP16 keys and values
+CASES = [
+    (40, 300, 4096, 2, 2, 2, False),   # SD1.5 self-attention at 64x64, fewer queries and heads
+    (40, 200, 77, 2, 2, 2, False),     # its cross-attention: 77 tokens
+    (80, 100, 1024, 2, 2, 1, False),
+    (160, 64, 256, 2, 2, 2, False),
+    (13, 37, 29, 4, 2, 3, False),      # edges: no multiple of a tile, heads sharing keys
+    (64, 50, 100, 2, 1, 1, True),      # FP16 keys and values
+    (64, 988, 988, 2, 2, 1, False),    # SDXL's heads of 64
+]
+
+
+def attention_case(gpu, d, lq, lk, h, hk, b, half, seed, dist="uniform"):
+    r = rng(seed)
+    if dist == "uniform":
+        q = uniform(r, (b, lq, h, d), 1.0)
+        k = uniform(r, (b, lk, hk, d), 1.0)
+        v = uniform(r, (b, lk, hk, d), 1.0)
+    else:
+        q = r.standard_normal((b, lq, h, d)).astype(np.float32)
+        k = r.standard_normal((b, lk, hk, d)).astype(np.float32)
+        v = r.standard_normal((b, lk, hk, d)).astype(np.float32)
+    if half:
+        k = k.astype(np.float16)
+        v = v.astype(np.float16)
+    q_d, k_d, v_d = dev(q, gpu), dev(k, gpu), dev(v, gpu)
+    y = unwritten((b, lq, h, d), gpu)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    # ggml's views: ne = [d, lq, h, b] with the heads interleaved in memory.
+    sdhip.attention(q_d.permute(0, 2, 1, 3), k_d.permute(0, 2, 1, 3), v_d.permute(0, 2, 1, 3), y, scale)
+    torch.cuda.synchronize()
+    return q, k.astype(np.float32), v.astype(np.float32), y.cpu().numpy(), scale
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_attention(gpu, c):
+    d, lq, lk, h, hk, b, half = c
+    q, k, v, y, scale = attention_case(gpu, *c, seed=d + lq + lk)
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    print(f"attention {c}: {err:.3g}")
+    assert np.isfinite(y).all()
+    assert err <= BOUND
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,lk", [("cfg4 self", 4096), ("cfg4 cross", 77)])
+def test_attention_bench_shapes(gpu, name, lk):
+    """cfg4: Q [2, 8, 4096, 40] ~N(0,1) against 4096 or 77 keys; a sample of
+    400 queries checked against float64."""
+    b, h, lq, d = 2, 8, 4096, 40
+    q, k, v, y, scale = attention_case(gpu, d, lq, lk, h, h, b, False, seed=lk, dist="normal")
+    r = rng(7)
+    queries = r.choice(b * h * lq, size=400, replace=False)
+    exact, mag = orc.exact_attention(q, k, v, scale, queries=queries)
+    bi, hi, i = queries // (h * lq), (queries // lq) % h, queries % lq
+    got = y[bi, i, hi, :]
+    err = orc.metric(got, exact, mag)
+    print(f"{name}: sampled error {err:.3g}")
+    assert np.isfinite(y).all()
+    assert err <= BOUND
+
+
+@pytest.mark.gpu
+def test_attention_not_taken(gpu):
+    """Heads of 512 (the VAE's) are left to the caller; so is a soft cap."""
+    q = torch.zeros((1, 40, 1, 512), device=gpu)
+    y = torch.zeros((1, 40, 1, 512), device=gpu)
+    with pytest.raises(sdhip.SdhipError) as e:
+        sdhip.attention(q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), y, 0.05)
+    assert e.value.status == sdhip.UNSUPPORTED
