@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only-main", action="store_true")
+    p.add_argument("--workload", default="", help="run one workload alone (cfg1 cfg2 cfg3a cfg3b cfg4_self "
+                                                  "cfg4_cross copy), for a profiler")
     return p.parse_args()
 
 
@@ -178,6 +180,44 @@ def attention_workload(dev, b, h, lq, lk, d, seed=0):
     return run, 4.0 * b * h * lq * lk * d
 
 
+def copy_workload(dev, mib=256):
+    """A plain device copy of known size: the scale for the HBM byte counters
+    (FETCH_SIZE, WRITE_SIZE) a profiler reads for the other kernels."""
+    import torch
+
+    src = torch.ones(mib << 18, device=dev)
+    dst = torch.empty_like(src)
+
+    def run():
+        dst.copy_(src)
+
+    run.keep = (src, dst)
+    return run, 0.0
+
+
+def make_workload(dev, name):
+    """(run, FLOPs) of a named workload: the BASELINE.json configurations."""
+    if name == "cfg1":
+        return linear_workload(dev, 320, 320, 4096, 2, seed=1)
+    if name == "cfg2":
+        run, flops, _ = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2)
+        return run, flops
+    if name == "cfg3a":
+        run, flops, _ = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True, seed=3)
+        return run, flops
+    if name == "cfg3b":
+        run, flops, _ = conv_workload(dev, 2, 640, 32, 32, 1280, 1, 0, bias=True, residual=False, groupnorm=True,
+                                      seed=4)
+        return run, flops
+    if name == "cfg4_self":
+        return attention_workload(dev, 2, 8, 4096, 4096, 40, seed=5)
+    if name == "cfg4_cross":
+        return attention_workload(dev, 2, 8, 4096, 77, 40, seed=5)
+    if name == "copy":
+        return copy_workload(dev)
+    raise SystemExit(f"unknown workload {name}")
+
+
 def cpu_baseline(seconds):
     """The oracle's F(4x4) restatement on this host's cores, on the full
     configs[1] convolution, repeated for about `seconds`; the best rate."""
@@ -225,6 +265,14 @@ def main():
     dev = torch.device("cuda", 0)
     sdhip.check(sdhip.load().sdhip_init(0), "init")
     log(f"device: {torch.cuda.get_device_name(0)}")
+
+    if args.workload:
+        # One workload alone, for a profiler: warmup + steps calls, one line.
+        run, flops = make_workload(dev, args.workload)
+        ms = timed(run, args.steps, args.warmup)
+        print(json.dumps({"workload": args.workload, "ms": round(ms, 5),
+                          "tflops": round(flops / ms / 1e9, 3) if flops else None}), flush=True)
+        return
 
     # The headline: configs[1], F(4x4) with bias and residual fused.
     run, flops, path = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2)

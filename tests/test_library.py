@@ -1,0 +1,138 @@
+"""The library's host side, on the CPU: it loads, exports every entry point
+include/sdhip.h declares, parses the tuning as the reference's SDASM_TUNE
+does, and takes or leaves operations by the reference's predicates
+(hooks.cc:29-55 and the *_supported functions) -- none of which touches a
+device.  No compute call is made here."""
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+import sdhip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "sdhip.h")).read()
+    return sorted(set(re.findall(r"\b(sdhip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    lib = sdhip.load()
+    names = declared()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in sdhip.h but not exported"
+    bound = {n for n, _, _ in sdhip.SIGNATURES}
+    assert set(names) == bound, "the Python binding and the header list the same entry points"
+
+
+def test_tuning_parses_like_sdasm_tune():
+    try:
+        sdhip.set_tuning("bits=8,group=128,weight_group=0,winograd=1")
+        assert sdhip.get_tuning("bits") == 8
+        assert sdhip.get_tuning("group") == 128
+        assert sdhip.get_tuning("weight_group") == 0
+        assert sdhip.get_tuning("winograd") == 1
+        assert sdhip.get_tuning("no_such") == -1
+        with pytest.raises(sdhip.SdhipError):
+            sdhip.set_tuning("no_such=1")
+        with pytest.raises(sdhip.SdhipError):
+            sdhip.set_tuning("bits=eight")
+    finally:
+        sdhip.set_tuning("")
+    # The reference's defaults (sources/kernels.h:91-135).
+    for name, value in (("bits", 0), ("input_bits", 8), ("group", 64), ("weight_group", 1), ("quantize", 7),
+                        ("winograd", 2), ("winograd_positions", 1024), ("winograd4_positions", 256),
+                        ("winograd_small_tiles", 256), ("fuse", 1)):
+        assert sdhip.get_tuning(name) == value
+
+
+FAKE = 1 << 20  # a data pointer the predicates never dereference
+
+
+def tensor(dtype, shape, data=FAKE):
+    """A contiguous descriptor of a torch-ordered shape."""
+    size = 4 if dtype == sdhip.TYPE_F32 else 2
+    ne = list(reversed(shape)) + [1] * (4 - len(shape))
+    nb = [size]
+    for k in range(1, 4):
+        nb.append(nb[k - 1] * ne[k - 1])
+    return sdhip.view_desc(data, dtype, ne, nb)
+
+
+F32, F16 = sdhip.TYPE_F32, sdhip.TYPE_F16
+
+
+def test_mul_mat_predicate():
+    lib = sdhip.load()
+    w, x, y = tensor(F16, (320, 320)), tensor(F32, (2, 4096, 320)), tensor(F32, (2, 4096, 320))
+    assert lib.sdhip_mul_mat_supported(w, x, y)
+    assert lib.sdhip_mul_mat_work_size(w, x, y) == 0
+    # Fewer than 16 rows, or K under 16, are left to the caller (mul_mat.cc:192-193).
+    assert not lib.sdhip_mul_mat_supported(w, tensor(F32, (15, 320)), tensor(F32, (15, 320)))
+    assert not lib.sdhip_mul_mat_supported(tensor(F16, (8, 8)), tensor(F32, (40, 8)), tensor(F32, (40, 8)))
+    # Single-precision weights are not taken by this form.
+    assert not lib.sdhip_mul_mat_supported(tensor(F32, (320, 320)), x, y)
+    try:
+        sdhip.set_tuning("bits=8")
+        assert lib.sdhip_mul_mat_work_size(w, x, y) > 0
+        small = tensor(F32, (255, 320))
+        assert lib.sdhip_mul_mat_work_size(w, small, small) == 0  # under 256 rows: not quantized
+    finally:
+        sdhip.set_tuning("")
+
+
+def conv_path(w_, h_, ic, oc, k, s, p, n, tuning=""):
+    lib = sdhip.load()
+    oh, ow = (h_ + 2 * p - k) // s + 1, (w_ + 2 * p - k) // s + 1
+    kern = tensor(F16, (oc, ic, k, k))
+    x = tensor(F32, (n, ic, h_, w_))
+    y = tensor(F32, (n, oc, oh, ow))
+    sdhip.set_tuning(tuning)
+    try:
+        return lib.sdhip_conv2d_path(kern, x, y, sdhip.conv_params(s, s, p, p, 1, 1))
+    finally:
+        sdhip.set_tuning("")
+
+
+def test_conv2d_path_selection():
+    """winograd_supported, four, small (winograd.cc:194-196, 1204-1206,
+    2107-2123) and the direct fallback (hooks.cc:36-41)."""
+    assert conv_path(64, 64, 320, 320, 3, 1, 1, 2) == 4    # configs[1]: F(4x4)
+    assert conv_path(8, 8, 1280, 1280, 3, 1, 1, 2) == 2    # configs[2]: F(2x2), small images
+    assert conv_path(32, 32, 640, 1280, 1, 1, 0, 2) == 0   # 1x1: direct
+    assert conv_path(33, 33, 24, 30, 3, 2, 1, 1) == 0      # stride 2: direct
+    assert conv_path(40, 20, 8, 8, 3, 1, 1, 1) == 4        # 800 outputs, 200 tiles: small, >= 256 outputs: F(4x4)
+    assert conv_path(15, 9, 8, 8, 3, 1, 1, 2) == 2         # 135 outputs, 80 tiles: small, F(2x2)
+    assert conv_path(80, 40, 8, 8, 3, 1, 1, 1) == 4        # 3200 outputs: F(4x4), not small
+    assert conv_path(64, 64, 320, 320, 3, 1, 1, 2, "winograd=1") == 2
+    assert conv_path(64, 64, 320, 320, 3, 1, 1, 2, "winograd=0") == 0
+    assert conv_path(64, 64, 320, 320, 3, 1, 3, 2) == 0    # padding 3: not Winograd
+
+
+def test_attention_and_norm_predicates():
+    lib = sdhip.load()
+    q = tensor(F32, (2, 8, 4096, 40))
+    y = tensor(F32, (2, 4096, 8, 40))
+    assert lib.sdhip_attention_supported(q, q, q, y, 0.0, 0.0)
+    assert not lib.sdhip_attention_supported(q, q, q, y, 0.0, 30.0)   # a soft cap
+    assert not lib.sdhip_attention_supported(q, q, q, y, 8.0, 0.0)    # ALiBi
+    big = tensor(F32, (1, 1, 4096, 512))
+    assert not lib.sdhip_attention_supported(big, big, big, tensor(F32, (1, 4096, 1, 512)), 0.0, 0.0)
+    x = tensor(F32, (2, 1280, 8, 8))
+    assert lib.sdhip_group_norm_supported(x, x, 32)
+    assert not lib.sdhip_group_norm_supported(x, x, 0)
+    assert lib.sdhip_norm_supported(tensor(F32, (2, 988, 1280)), tensor(F32, (2, 988, 1280)))
+
+
+def test_bench_refuses_several_gpus():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr

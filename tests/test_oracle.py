@@ -1,0 +1,277 @@
+"""Pins of the oracle, on the CPU.  Each restated function is checked against
+something that fixes it independently: a closed form, a library routine of
+the textbook case, a brute-force recomputation, or invariants a plausible
+mistake (a dropped term, a wrong sign or index, a transposed operand) breaks.
+The reference keeps no golden vectors for this path (its tests compare every
+form with float64 recomputations, tests/ops_test.cc:154-211)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as orc
+from helpers import rng, uniform
+
+# ------------------------------------------------------------------ scalar math
+
+
+def test_exponential_against_exp():
+    """scalar_math.h:34-51 is within two units in the last place of exp over
+    its range, and clamps beyond it."""
+    xs = np.concatenate([np.linspace(-87.0, 88.0, 20001, dtype=np.float32),
+                         np.float32([0.0, -0.0, 1e-8, -1e-8, 0.5, -0.5, 10.0, -20.0])])
+    L = orc.lib()
+    worst = 0.0
+    for x in xs:
+        got = L.oracle_exponential(float(x))
+        want = math.exp(float(x))
+        worst = max(worst, abs(got - want) / want)
+    assert worst <= 2.5 * 2.0 ** -24
+    assert L.oracle_exponential(-1000.0) == pytest.approx(math.exp(-87.3), rel=1e-6)
+    assert L.oracle_exponential(0.0) == 1.0
+
+
+def test_silu_and_gelu_closed_forms():
+    L = orc.lib()
+    for x in np.linspace(-10, 10, 401, dtype=np.float32):
+        x = float(x)
+        assert L.oracle_silu(x) == pytest.approx(x / (1.0 + math.exp(-x)), rel=1e-6, abs=1e-7)
+        g = 0.5 * x * (1.0 + math.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)))
+        assert L.oracle_gelu(x) == pytest.approx(g, rel=1e-6, abs=1e-7)
+    v = uniform(rng(1), (1000,), 8.0)
+    assert np.allclose(orc.silu(v), v / (1 + np.exp(-v.astype(np.float64))), rtol=1e-6, atol=1e-7)
+    g = uniform(rng(2), (1000,), 6.0)
+    want = v * (0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g.astype(np.float64) ** 3))))
+    assert np.allclose(orc.gated_gelu(v, g), want, rtol=2e-6, atol=1e-6)
+
+# ------------------------------------------------------------------ float64 references
+
+
+def test_exact_mul_mat_is_the_matrix_product():
+    r = rng(3)
+    w = uniform(r, (17, 33), 0.25)
+    x = uniform(r, (29, 33), 1.0)
+    y, mag = orc.exact_mul_mat(w, x)
+    w64, x64 = w.astype(np.float64), x.astype(np.float64)
+    assert np.allclose(y, x64 @ w64.T, rtol=0, atol=1e-13)
+    assert np.allclose(mag, np.abs(x64) @ np.abs(w64).T, rtol=0, atol=1e-13)
+
+
+@pytest.mark.parametrize("c", [
+    (9, 7, 3, 4, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+    (11, 8, 2, 3, 5, 3, 1, 2, 2, 0, 2, 1, 1),
+    (10, 10, 4, 2, 1, 1, 1, 1, 0, 0, 1, 1, 2),
+    (12, 9, 3, 5, 3, 3, 2, 2, 1, 1, 1, 1, 1),
+])
+def test_exact_conv2d_is_torch_conv2d(c):
+    """ggml's CONV_2D layouts and op_params (s0, s1, p0, p1, d0, d1) against
+    torch's float64 conv2d (a cross-correlation, as ggml's is)."""
+    w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
+    r = rng(sum(c))
+    x = uniform(r, (n, ic, h_, w_), 1.0)
+    k = uniform(r, (oc, ic, kh, kw), 0.25)
+    y, mag = orc.exact_conv2d(x, k, s0, s1, p0, p1, d0, d1)
+    t = torch.nn.functional.conv2d(torch.from_numpy(x).double(), torch.from_numpy(k).double(), stride=(s1, s0),
+                                   padding=(p1, p0), dilation=(d1, d0))
+    assert y.shape == tuple(t.shape)
+    assert np.allclose(y, t.numpy(), rtol=0, atol=1e-12)
+    tm = torch.nn.functional.conv2d(torch.from_numpy(np.abs(x)).double(), torch.from_numpy(np.abs(k)).double(),
+                                    stride=(s1, s0), padding=(p1, p0), dilation=(d1, d0))
+    assert np.allclose(mag, tm.numpy(), rtol=0, atol=1e-12)
+    index = np.array([0, y.size // 3, y.size - 1])
+    ys, ms = orc.exact_conv2d(x, k, s0, s1, p0, p1, d0, d1, index=index)
+    assert np.array_equal(ys, y.reshape(-1)[index]) and np.array_equal(ms, mag.reshape(-1)[index])
+
+
+def test_exact_attention_is_softmax():
+    """ggml's head layout (q [b][lq][h][d], heads sharing keys h / (h / hk))
+    against a float64 softmax written with numpy."""
+    r = rng(5)
+    b, lq, lk, h, hk, d = 2, 5, 7, 4, 2, 3
+    q, k, v = uniform(r, (b, lq, h, d), 1.0), uniform(r, (b, lk, hk, d), 1.0), uniform(r, (b, lk, hk, d), 1.0)
+    scale = 0.4
+    y, mag = orc.exact_attention(q, k, v, scale)
+    for bi in range(b):
+        for hi in range(h):
+            kh = hi // (h // hk)
+            s = q[bi, :, hi, :].astype(np.float64) @ k[bi, :, kh, :].astype(np.float64).T * scale
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            vv = v[bi, :, kh, :].astype(np.float64)
+            assert np.allclose(y[bi, :, hi, :], p @ vv, atol=1e-14)
+            assert np.allclose(mag[bi, :, hi, :], p @ np.abs(vv), atol=1e-14)
+    queries = np.array([0, 7, 39])
+    ys, _ = orc.exact_attention(q, k, v, scale, queries=queries)
+    for t, qq in enumerate(queries):
+        bi, hi, i = qq // (h * lq), (qq // lq) % h, qq % lq
+        assert np.array_equal(ys[t], y[bi, i, hi])
+
+
+def test_exact_gated():
+    r = rng(6)
+    K, half, M = 9, 4, 3
+    w, x, b = uniform(r, (2 * half, K), 0.25), uniform(r, (M, K), 1.0), uniform(r, (2 * half,), 1.0)
+    y, _ = orc.exact_gated(w, x, b)
+    p = x.astype(np.float64) @ w.astype(np.float64).T + b
+    g = p[:, half:]
+    gelu = 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3)))
+    assert np.allclose(y, p[:, :half] * gelu, atol=1e-13)
+
+
+def test_winograd_matrices_compute_the_convolution():
+    """The F(2x2,3x3) and F(4x4,3x3) matrices of winograd.cc:19-22,
+    1155-1183, 1259-1264 (the ones oracle/port.c and the device use) satisfy
+    A^T [(G g G^T) * (B^T d B)] A = the 3x3 cross-correlation of d and g."""
+    BT4 = np.array([[1, 1.5, -2, -1.5, 1, 0], [0, -1, -2.5, -.5, 1, 0], [0, 1, .5, -2.5, 1, 0],
+                    [0, -.5, -1, .5, 1, 0], [0, 2, -1, -2, 1, 0], [0, 1, 1.5, -2, -1.5, 1]])
+    G4 = np.array([[1, 0, 0], [-1 / 3, -1 / 3, -1 / 3], [1 / 3, -1 / 3, 1 / 3], [1 / 15, 2 / 15, 4 / 15],
+                   [-16 / 15, 8 / 15, -4 / 15], [0, 0, 1]])
+    AT4 = np.array([[1, 1, 1, 1, 1, 0], [0, 1, -1, 2, -.5, 0], [0, 1, 1, 4, .25, 0], [0, 1, -1, 8, -.125, 1]])
+    BT2 = np.array([[1, 0, -1, 0], [0, 1, 1, 0], [0, -1, 1, 0], [0, 1, 0, -1]])
+    G2 = np.array([[1, 0, 0], [.5, .5, .5], [.5, -.5, .5], [0, 0, 1]])
+    AT2 = np.array([[1, 1, 1, 0], [0, 1, -1, -1]])
+    r = rng(7)
+    for BT, G, AT, m in ((BT4, G4, AT4, 4), (BT2, G2, AT2, 2)):
+        d = r.standard_normal((m + 2, m + 2))
+        g = r.standard_normal((3, 3))
+        y = AT @ ((G @ g @ G.T) * (BT @ d @ BT.T)) @ AT.T
+        want = np.array([[np.sum(d[i:i + 3, j:j + 3] * g) for j in range(m)] for i in range(m)])
+        assert np.allclose(y, want, atol=1e-13)
+
+
+def test_port_winograd4_within_the_reference_bound():
+    """oracle/port.c's F(4x4) (the CPU baseline) against float64: within the
+    reference's published 5-11e-7 class, and the 2e-5 bound."""
+    import ctypes
+
+    L = orc.lib()
+    f = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+    I64, I = ctypes.c_int64, ctypes.c_int
+    L.oracle_port_winograd4.argtypes = [f, I64, I64, I64, I64, f, I64, I, I, ctypes.c_void_p, ctypes.c_void_p, f, I]
+    r = rng(8)
+    n, ic, h, w, oc = 2, 13, 18, 22, 11
+    x = uniform(r, (n, ic, h, w), 1.0)
+    k = uniform(r, (oc, ic, 3, 3), 0.25).astype(np.float16).astype(np.float32)
+    y = np.zeros((n, oc, h, w), np.float32)
+    L.oracle_port_winograd4(x, n, ic, h, w, k, oc, 1, 1, None, None, y, 2)
+    exact, mag = orc.exact_conv2d(x, k, 1, 1, 1, 1, 1, 1)
+    assert orc.metric(y, exact, mag) <= 2e-6
+
+# ------------------------------------------------------------------ norms
+
+
+@pytest.mark.parametrize("shape,groups", [((2, 64, 20, 36), 32), ((1, 30, 7, 13), 10), ((1, 30, 7, 13), 7)])
+def test_group_norm_against_float64(shape, groups):
+    """norm.cc's statistics in single precision agree with float64 group
+    normalisation to single precision, groups of ceil(C / G) channels."""
+    x = uniform(rng(9), shape, 3.0)
+    y = orc.group_norm(x, groups, 1e-5)
+    per = -(-shape[1] // groups)
+    want = np.empty(shape)
+    for b in range(shape[0]):
+        for c0 in range(0, shape[1], per):
+            blk = x[b, c0:c0 + per].astype(np.float64)
+            want[b, c0:c0 + per] = (blk - blk.mean()) / np.sqrt(blk.var() + 1e-5)
+    assert np.abs(y - want).max() <= 2e-6 * np.abs(want).max()
+
+
+def test_norm_against_float64():
+    x = uniform(rng(10), (3, 7, 130), 3.0)
+    y = orc.norm(x, 1e-5)
+    x64 = x.astype(np.float64)
+    want = (x64 - x64.mean(-1, keepdims=True)) / np.sqrt(x64.var(-1, keepdims=True) + 1e-5)
+    assert np.abs(y - want).max() <= 2e-6 * np.abs(want).max()
+
+
+def test_apply_chain_broadcasts_as_numpy():
+    import ctypes
+
+    L = orc.lib()
+    r = rng(11)
+    out = uniform(r, (2, 3, 4, 5), 1.0)
+    bias = uniform(r, (1, 3, 1, 1), 1.0)
+    res = uniform(r, (2, 3, 4, 5), 1.0)
+    ne = (ctypes.c_int64 * 4)(5, 4, 3, 2)
+    kinds = (ctypes.c_int * 3)(1, 0, 2)
+    ops = (ctypes.c_void_p * 3)(bias.ctypes.data, res.ctypes.data, None)
+    nb = (ctypes.c_int64 * 12)(0, 0, 1, 0, 1, 5, 20, 60, 0, 0, 0, 0)
+    L.oracle_apply_chain.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+    got = out.copy()
+    L.oracle_apply_chain(got.ctypes.data, ne, 3, kinds, ops, nb)
+    want = orc.silu((out * bias + res).astype(np.float32))
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+
+# ------------------------------------------------------------------ bits mode
+
+
+@pytest.mark.parametrize("levels", [255, 127])
+def test_input_quantization_invariants(levels):
+    """quant.cc:282-315: bytes in [0, levels]; 0 maps to the zero point
+    exactly; the scale is (hi - lo) / levels of the group's range with 0; each
+    number is reconstructed within half a step; the tail is the zero point."""
+    r = rng(12)
+    for trial in range(50):
+        n = int(r.integers(1, 64))
+        x = uniform(r, (n,), float(r.uniform(0.1, 5.0)))
+        if trial % 5 == 0:
+            x = np.abs(x)  # all of one sign: the range still holds 0
+        x[0] = 0.0
+        q, s, o = orc.quantize_input_row(x, 64, levels)
+        lo, hi = min(0.0, x.min()), max(0.0, x.max())
+        assert s == np.float32(np.float32(hi - lo) / np.float32(levels))
+        z = int(q[0])
+        assert o == np.float32(s * np.float32(z))
+        assert np.all(q[n:] == z)
+        assert q.max() <= levels
+        recon = s * (q[:n].astype(np.float64) - z)
+        assert np.all(np.abs(recon - x) <= 0.5 * s * (1 + 1e-5) + 1e-7)
+
+
+@pytest.mark.parametrize("weight_groups", [1, 0])
+def test_weight_quantization_invariants(weight_groups):
+    """quant.cc:186-243: |q| <= wmax, the greatest magnitude of the group (or
+    the row) reaching wmax, each weight within half a step, the offset the
+    scale times the integer sum."""
+    r = rng(13)
+    w = uniform(r, (6, 150), 0.25)
+    q, s, o, su = orc.quantize_weights(w, 64, 127, weight_groups)
+    groups = 3
+    assert np.abs(q).max() <= 127
+    for row in range(6):
+        if not weight_groups:
+            assert np.all(s[row] == s[row, 0])
+            assert s[row, 0] == np.float32(np.abs(w[row]).max() / np.float32(127))
+        for g in range(groups):
+            seg = w[row, 64 * g:64 * (g + 1)]
+            qs = q[row, 64 * g:64 * g + seg.size].astype(np.int64)
+            assert np.all(q[row, 64 * g + seg.size:64 * (g + 1)] == 0)
+            assert su[row, g] == qs.sum()
+            assert o[row, g] == np.float32(s[row, g] * np.float32(qs.sum()))
+            assert np.all(np.abs(s[row, g] * qs - seg) <= 0.5 * s[row, g] * (1 + 1e-5))
+            if weight_groups:
+                assert np.abs(qs).max() == 127
+
+
+def test_quantized_product_against_its_own_integers_and_float64():
+    """The quantized MUL_MAT: the output agrees with a float64 recomputation
+    from the oracle's own bytes, scales and offsets (pins the integer sums,
+    their indexing and the dequantisation's signs), and with the exact product
+    within the reference's bound kQuantized = 1e-2 (ops_test.cc:213-223)."""
+    r = rng(14)
+    N, K, M = 9, 150, 7
+    w = uniform(r, (N, K), 0.25).astype(np.float16).astype(np.float32)
+    x = uniform(r, (M, K), 1.0)
+    y, xq, xs, xo, wq, ws, wo, wsum = orc.quantized_mul_mat(w, x)
+    groups = 3
+    S = np.einsum("mgk,ngk->mng", xq.reshape(M, groups, 64).astype(np.int64),
+                  wq.reshape(N, groups, 64).astype(np.int64))
+    recon = (xs[:, None, :] * ws[None, :, :] * S - xo[:, None, :] * wo[None, :, :]).sum(-1)
+    assert np.allclose(y, recon, rtol=1e-5, atol=1e-5)
+    exact, mag = orc.exact_mul_mat(w, x)
+    assert orc.metric(y, exact, mag) <= 1e-2
+    init = uniform(r, (M, N), 1.0)
+    y2 = orc.quantized_mul_mat(w, x, init=init)[0]
+    assert np.allclose(y2, y + init, atol=1e-5)
