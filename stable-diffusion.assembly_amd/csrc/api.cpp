@@ -64,6 +64,8 @@ const Field kFields[] = {
     {"winograd4_positions", &Tuning::winograd4_positions},
     {"winograd_small_tiles", &Tuning::winograd_small_tiles},
     {"fuse", &Tuning::fuse},
+    {"winograd_fp32", &Tuning::winograd_fp32},
+    {"gemm_stages", &Tuning::gemm_stages},
 };
 
 }  // namespace

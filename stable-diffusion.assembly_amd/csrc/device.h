@@ -122,6 +122,68 @@ __device__ __forceinline__ void apply_chain_block(const DevChain &c, float (&v)[
     }
 }
 
+// x, which the compiler may not see through: what is computed from it is
+// computed where it is used, not hoisted out of loops into registers held for
+// their whole length.
+template <class T>
+__device__ __forceinline__ T opaque(T x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// The row, within a 32 x 32 MFMA result tile, of register e (of 16) of a lane
+// of the first half of the wave; the second half's are 4 further down.
+__device__ __forceinline__ constexpr int tile_row(int e) { return 8 * (e >> 2) + (e & 3); }
+
+// The chain over the 16 values a lane holds of a 32 x 32 MFMA result tile,
+// one column of it.  Where the tile lies wholly inside the output (`full`) and
+// a step's operand is strided along the tile's rows (stride(s) >= 0), its
+// values are at base(s) + tile_row(e) * stride(s) -- one broadcast load when
+// the stride is 0; elsewhere (the edges, operands broadcast over only some of
+// the row's dimensions) general(s, e) gives each offset.  The operands of a
+// step are all loaded before any is used.
+template <class Base, class Stride, class General>
+__device__ __forceinline__ void apply_chain_tile(const DevChain &c, float (&v)[16], bool full, Base base,
+                                                 Stride stride, General general) {
+#pragma unroll 1
+    for (int s = 0; s < c.count; ++s) {
+        const DevStep &st = c.steps[s];
+        if (st.kind == 2) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = silu(v[e]);
+            continue;
+        }
+        float o[16];
+        const int64_t rs = stride(s);
+        if (full && rs == 0) {
+            const float b = st.operand[base(s)];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[e] = b;
+        } else if (full && rs > 0) {
+            const float *p = st.operand + base(s);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[e] = p[tile_row(e) * rs];
+        } else {
+            // Four at a time, so that the offsets of all sixteen are not held
+            // at once: this path's registers count for the whole kernel.
+#pragma unroll
+            for (int g = 0; g < 16; g += 4) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int e = g; e < g + 4; ++e) o[e] = st.operand[general(s, e)];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (st.kind == 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(v[e], o[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = __fmul_rn(v[e], o[e]);
+        }
+    }
+}
+
 // Row r of an output of ne1 rows and ne2 matrices as (i1, i2, i3), in 32-bit
 // unsigned division (the host keeps every extent below 2^31): 64-bit division
 // is a long software sequence on the GPU.

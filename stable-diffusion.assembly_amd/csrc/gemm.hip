@@ -1,7 +1,8 @@
 // The products of FP16 weights by single-precision activations on gfx950's
 // FP16 MFMA (v_mfma_f32_32x32x16_f16): MUL_MAT (mul_mat.cc), MUL_MAT with the
-// gated GELU after it (mul_mat.cc:889-1058) and the direct convolution
-// (conv2d.cc), each with its chain applied while the output tile is in
+// gated GELU after it (mul_mat.cc:889-1058), the direct convolution
+// (conv2d.cc), and the alpha^2 products of Winograd's convolution
+// (winograd.cc), each with its chain applied while the output tile is in
 // registers.
 //
 // Precision.  The weights are FP16 and so exact as FP16 MFMA operands; each
@@ -9,19 +10,25 @@
 // product is taken as w*hi + w*lo, two MFMAs into the same single-precision
 // accumulator: 22 bits of x, as the reference's AMX-FP16 form takes it
 // (x86_64/amx_fp16.S: the weights exact, x in two FP16 parts), where ggml
-// rounds x to FP16 (11 bits).  Measured by the reference's metric, |error| /
-// sum |products| against float64, the result is within a few 1e-7.
+// rounds x to FP16 (11 bits).  Winograd's transformed weights are not FP16
+// numbers: both operands are split there and the products taken as
+// a_hi b_hi + a_hi b_lo + a_lo b_hi, three MFMAs (the fourth, a_lo b_lo, is
+// below 2^-22 of the product).
 //
-// Shape.  A workgroup of 4 waves computes a block of BM x BN of C = A B^T,
-// A and B both K-contiguous rows, in steps of BK = 32 of K: the rows of both
-// operands go from global memory into registers, are split (the single-
-// precision one) and written to LDS as FP16, double-buffered, and each wave
-// computes its TM x TN tiles of 32 x 32 from LDS, 2 K-steps of 16 per BK.
-//   MUL_MAT:     A = x (tokens, split), B = W (features):  C[token][feature]
+// Shape.  A workgroup of 4 waves (2 x 2) computes a block of BM x BN of
+// C = A B^T, A and B both K-contiguous rows, in steps of BK = 32 of K.  The
+// rows go from global memory into registers two steps ahead of the MFMAs
+// (two register stages, two LDS buffers), are split where they are single
+// precision and written to LDS as FP16; each wave computes its TM x TN tiles
+// of 32 x 32 from LDS, two K-steps of 16 a step.
+//   MUL_MAT:     A = x (tokens, split), B = W (features): C[token][feature]
 //   convolution: A = W (output channels), B = the image's columns (split),
 //                C[channel][position]
+//   Winograd:    A = U[xi] (output channels), B = V[xi] (tiles), both split
 // so that the output's contiguous dimension is always C's column, lane % 32
 // of the MFMA's result, and a wave's stores are 128-byte rows.
+
+#include <type_traits>
 
 #include "device.h"
 #include "kernels.h"
@@ -34,12 +41,18 @@ namespace {
 constexpr int kBK = 32;
 constexpr int kLdk = kBK + 8;  // halves per LDS row: 80 bytes, 16-byte aligned, skewed across banks
 
+// Which operands are single precision, split into two FP16 planes.
+enum Split { kSplitA = 0, kSplitB = 1, kSplitBoth = 2 };
+
+constexpr int planes_a(int mode) { return mode == kSplitB ? 1 : 2; }
+constexpr int planes_b(int mode) { return mode == kSplitA ? 1 : 2; }
+
 // ------------------------------------------------------------------ MFMA core
 
-// acc[i][j] += A rows (32 i ..) x B cols (32 j ..) over one BK step held in
-// LDS.  `a_hi/a_lo` and `b_hi/b_lo`: when an operand is not split its lo
-// plane is null and one MFMA is made per tile and K-step instead of two.
-template <int TM, int TN, bool SPLIT_A>
+// acc[i][j] += A rows (32 i ..) x B rows (32 j ..) over one BK step held in
+// LDS: two MFMAs per tile and K-step of 16 with one operand split, three
+// with both.
+template <int TM, int TN, int MODE>
 __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float16 *a_hi, const _Float16 *a_lo,
                                           const _Float16 *b_hi, const _Float16 *b_lo, int lane) {
     const int r = lane & 31;
@@ -50,25 +63,22 @@ __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float1
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             a[i] = *reinterpret_cast<const half8 *>(a_hi + (32 * i + r) * kLdk + ks + kh);
-            if (SPLIT_A) {
-                al[i] = *reinterpret_cast<const half8 *>(a_lo + (32 * i + r) * kLdk + ks + kh);
-            }
+            if (MODE != kSplitB) al[i] = *reinterpret_cast<const half8 *>(a_lo + (32 * i + r) * kLdk + ks + kh);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             b[j] = *reinterpret_cast<const half8 *>(b_hi + (32 * j + r) * kLdk + ks + kh);
-            if (!SPLIT_A) {
-                bl[j] = *reinterpret_cast<const half8 *>(b_lo + (32 * j + r) * kLdk + ks + kh);
-            }
+            if (MODE != kSplitA) bl[j] = *reinterpret_cast<const half8 *>(b_lo + (32 * j + r) * kLdk + ks + kh);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-                if (SPLIT_A) {
+                if (MODE != kSplitB) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
-                } else {
+                }
+                if (MODE != kSplitA) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
                 }
             }
@@ -76,31 +86,50 @@ __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float1
     }
 }
 
-// Row of the MFMA result held in register e (of 16) of a lane, within a 32 x 32
-// tile: the column is lane % 32.
-__device__ __forceinline__ int acc_row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
-
 // ------------------------------------------------------------------ loaders
 
-// BR rows x BK of K-contiguous single-precision rows (row stride ld elements),
-// split into hi and lo planes of LDS.  Rows at or past `rows`, and k at or
-// past K, are zeros.  VEC: every row start and ld are multiples of 4 floats.
-template <int BR, bool VEC>
-struct F32RowsTile {
-    static constexpr int kQuads = BR * kBK / 4 / 256;  // float4 per thread
-    float4 v[kQuads];
+// Every loader takes BR rows x BK of K into registers (load) and writes them
+// to LDS as FP16 (store), one or two planes; a thread's rows are fixed over K,
+// so their first elements are found once (init).
 
-    __device__ void load(const float *base, int64_t ld, int64_t row0, int64_t rows, int64_t k0, int64_t K, int tid) {
+// K-contiguous single-precision rows, split into hi and lo planes.  Rows at or
+// past `rows`, and k at or past K, are zeros.  VEC: every row start and ld are
+// multiples of 4 floats.  FULL (with VEC): K a multiple of BK, and rows past
+// the end read the block's first row instead, whose products are never
+// stored -- the loads then have no conditions, and so no branches that would
+// wait on the loads before them.
+template <int BR, bool VEC, bool FULL>
+struct F32Rows {
+    static constexpr int kQuads = BR * kBK / 4 / 256;  // float4 per thread
+    static_assert(kQuads >= 1, "tile too small for 256 threads");
+    static_assert(!FULL || VEC, "FULL loads are vector loads");
+    float4 v[kQuads];
+    const float *row[kQuads];
+    int64_t K;
+
+    template <class RowOf>
+    __device__ void init(const float *base, int64_t ld, RowOf row_of, int64_t k_, int tid) {
+        K = k_;
 #pragma unroll
         for (int i = 0; i < kQuads; ++i) {
             const int idx = tid + 256 * i;
-            const int r = idx / (kBK / 4);
-            const int kq = (idx % (kBK / 4)) * 4;
-            const int64_t row = row0 + r;
-            const int64_t k = k0 + kq;
+            int64_t r = row_of(idx / (kBK / 4));
+            if (FULL && r < 0) r = row_of(0);
+            row[i] = r >= 0 ? base + r * ld + (idx % (kBK / 4)) * 4 : nullptr;
+        }
+    }
+
+    __device__ void load(int64_t k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < kQuads; ++i) {
+            if (FULL) {
+                v[i] = *reinterpret_cast<const float4 *>(row[i] + k0);
+                continue;
+            }
+            const int64_t k = k0 + ((tid + 256 * i) % (kBK / 4)) * 4;
             float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (row < rows) {
-                const float *p = base + row * ld + k;
+            if (row[i] != nullptr) {
+                const float *p = row[i] + k0;
                 if (VEC && k + 4 <= K) {
                     x = *reinterpret_cast<const float4 *>(p);
                 } else {
@@ -132,251 +161,146 @@ struct F32RowsTile {
     }
 };
 
-// BR rows x BK of K-contiguous FP16 (or single-precision, rounded... no:
-// single-precision weights are split like activations, see F32RowsTile) rows
-// into one LDS plane.  `row_of(r)` gives the global row of LDS row r, or -1.
-template <int BR, bool VEC>
-struct F16RowsTile {
+// K-contiguous 16-bit rows into LDS, PLANES of them at once (one, or the two
+// parts hi and lo of a split operand, `ld_plane` elements apart); `row_of(r)`
+// gives the global row of LDS row r, or -1.  FULL as for F32Rows.
+template <int BR, bool VEC, bool FULL, int PLANES = 1>
+struct F16Rows {
     static constexpr int kOcts = BR * kBK / 8 / 256;  // 8 halves per load
     static_assert(kOcts >= 1, "tile too small for 256 threads");
-    half8 v[kOcts];
+    static_assert(!FULL || VEC, "FULL loads are vector loads");
+    half8 v[PLANES][kOcts];
+    const _Float16 *row[kOcts];
+    int64_t K, plane;
 
     template <class RowOf>
-    __device__ void load(const _Float16 *base, int64_t ld, RowOf row_of, int64_t k0, int64_t K, int tid) {
+    __device__ void init(const _Float16 *base, int64_t ld, RowOf row_of, int64_t k_, int tid, int64_t ld_plane = 0) {
+        K = k_;
+        plane = ld_plane;
 #pragma unroll
         for (int i = 0; i < kOcts; ++i) {
             const int idx = tid + 256 * i;
-            const int r = idx / (kBK / 8);
-            const int kq = (idx % (kBK / 8)) * 8;
-            const int64_t row = row_of(r);
-            const int64_t k = k0 + kq;
-            half8 x = {};
-            if (row >= 0) {
-                const _Float16 *p = base + row * ld + k;
-                if (VEC && k + 8 <= K) {
-                    x = *reinterpret_cast<const half8 *>(p);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        if (k + e < K) x[e] = p[e];
-                    }
-                }
-            }
-            v[i] = x;
+            int64_t r = row_of(idx / (kBK / 8));
+            if (FULL && r < 0) r = row_of(0);
+            row[i] = r >= 0 ? base + r * ld + (idx % (kBK / 8)) * 8 : nullptr;
         }
     }
 
-    __device__ void store(_Float16 *dst, int tid) const {
+    __device__ void load(int64_t k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < kOcts; ++i) {
+#pragma unroll
+            for (int q = 0; q < PLANES; ++q) {
+                if (FULL) {
+                    v[q][i] = *reinterpret_cast<const half8 *>(row[i] + q * plane + k0);
+                    continue;
+                }
+                const int64_t k = k0 + ((tid + 256 * i) % (kBK / 8)) * 8;
+                half8 x = {};
+                if (row[i] != nullptr) {
+                    const _Float16 *p = row[i] + q * plane + k0;
+                    if (VEC && k + 8 <= K) {
+                        x = *reinterpret_cast<const half8 *>(p);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            if (k + e < K) x[e] = p[e];
+                        }
+                    }
+                }
+                v[q][i] = x;
+            }
+        }
+    }
+
+    __device__ void store(_Float16 *dst, _Float16 *dst_lo, int tid) const {
 #pragma unroll
         for (int i = 0; i < kOcts; ++i) {
             const int idx = tid + 256 * i;
             const int r = idx / (kBK / 8);
             const int kq = (idx % (kBK / 8)) * 8;
-            *reinterpret_cast<half8 *>(dst + r * kLdk + kq) = v[i];
+            *reinterpret_cast<half8 *>(dst + r * kLdk + kq) = v[0][i];
+            if (PLANES == 2) *reinterpret_cast<half8 *>(dst_lo + r * kLdk + kq) = v[PLANES - 1][i];
         }
     }
 };
-
-// ------------------------------------------------------------------ MUL_MAT
-
-// C[m][n] = sum_k x[m][k] W[n][k] for rows m of x (single precision, split)
-// and rows n of W (FP16), the chain applied, into y[m * ldy + n].  With GATED,
-// the block's 128 rows of W are 64 features of the first half and the same 64
-// of the second (the gate), each wave's two column tiles a pair, and the
-// block writes out[m * ldo + j] = P[m][j] GELU(P[m][half + j]).
-template <int TM, int TN, bool GATED, bool VECX, bool VECW>
-__global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
-    constexpr int BM = 64 * TM;
-    constexpr int BN = 64 * TN;
-    static_assert(!GATED || TN == 2, "the gated form pairs two column tiles");
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2][(2 * BM + BN) * kLdk];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wr = wave >> 1;  // wave row (0, 1)
-    const int wc = wave & 1;   // wave column
-
-    const uint32_t nblocks = gridDim.x;
-    const uint32_t b = xcd_swizzle(blockIdx.x, nblocks);
-    const int64_t mb = b / p.col_blocks;
-    const int64_t nb = b % p.col_blocks;
-    const int64_t m0 = mb * BM;
-    const int64_t n0 = nb * (GATED ? BN / 2 : BN);
-
-    const auto w_row = [&](int r) -> int64_t {
-        if (GATED) {
-            const int wq = r / 64;
-            const int side = (r / 32) & 1;
-            const int64_t f = n0 + 32 * wq + (r & 31);
-            return f < p.half ? side * p.half + f : -1;
-        }
-        const int64_t f = n0 + r;
-        return f < p.N ? f : -1;
-    };
-
-    float16v acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
-
-    F32RowsTile<BM, VECX> xa;
-    F16RowsTile<BN, VECW> wb;
-    const int64_t steps = (p.K + kBK - 1) / kBK;
-    xa.load(p.x, p.ldx, m0, p.M, 0, p.K, tid);
-    wb.load(p.w, p.ldw, w_row, 0, p.K, tid);
-    xa.store(lds[0], lds[0] + BM * kLdk, tid);
-    wb.store(lds[0] + 2 * BM * kLdk, tid);
-    __syncthreads();
-    for (int64_t s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < steps) {
-            xa.load(p.x, p.ldx, m0, p.M, (s + 1) * kBK, p.K, tid);
-            wb.load(p.w, p.ldw, w_row, (s + 1) * kBK, p.K, tid);
-        }
-        const _Float16 *base = lds[cur];
-        mfma_step<TM, TN, true>(acc, base + (wr * 32 * TM) * kLdk, base + BM * kLdk + (wr * 32 * TM) * kLdk,
-                                base + 2 * BM * kLdk + (wc * 32 * TN) * kLdk, nullptr, lane);
-        if (s + 1 < steps) {
-            xa.store(lds[cur ^ 1], lds[cur ^ 1] + BM * kLdk, tid);
-            wb.store(lds[cur ^ 1] + 2 * BM * kLdk, tid);
-        }
-        __syncthreads();
-    }
-
-    // The epilogue: rows m of the tile, column (feature) lane % 32; a tile's
-    // 16 values of the lane at a time, their loads before their stores.
-    const int col = lane & 31;
-    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
-    const auto row_off = [&](const DevStep &st, int64_t m) -> int64_t {
-        if (st.flat123) return m * st.nb[1];
-        uint32_t i1, i2, i3;
-        split_index(static_cast<uint32_t>(m), ne1, ne2, i1, i2, i3);
-        return i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
-    };
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int64_t mbase = m0 + wr * 32 * TM + 32 * i;
-        // Rows past M read the last row and are not stored.
-        const auto row = [&](int e) -> int64_t {
-            const int64_t m = mbase + acc_row(e, lane);
-            return m < p.M ? m : p.M - 1;
-        };
-        if (GATED) {
-            const int64_t f = n0 + 32 * wc + col;
-            const int64_t fc = f < p.half ? f : p.half - 1;
-            float xv[16], gv[16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                xv[e] = acc[i][0][e] * kSplitUp;
-                gv[e] = acc[i][1][e] * kSplitUp;
-            }
-            apply_chain_block(p.chain, xv, [&](int s, int e) {
-                return fc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
-            });
-            apply_chain_block(p.chain, gv, [&](int s, int e) {
-                return (p.half + fc) * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
-            });
-            if (f >= p.half) continue;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int64_t m = mbase + acc_row(e, lane);
-                if (m < p.M) p.y[m * p.ldy + f] = xv[e] * gelu(gv[e]);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int64_t n = n0 + wc * 32 * TN + 32 * j + col;
-                const int64_t nc = n < p.N ? n : p.N - 1;
-                float v[16];
-#pragma unroll
-                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
-                if (p.from_redirect) {
-                    float r[16];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) r[e] = p.y[row(e) * p.ldy + nc];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(r[e], v[e]);
-                }
-                apply_chain_block(p.chain, v, [&](int s, int e) {
-                    return nc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
-                });
-                if (n >= p.N) continue;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int64_t m = mbase + acc_row(e, lane);
-                    if (m < p.M) p.y[m * p.ldy + n] = v[e];
-                }
-            }
-        }
-    }
-}
-
-// ------------------------------------------------------------------ direct convolution
 
 // The columns of the image for BN positions p (of all images, n * OH * OW +
 // oy * OW + ox) by BK of K = (ic, kh, kw), read from the image where im2col
 // would have put them, split, into LDS as [position][k].  A thread takes one
 // position and 4 consecutive k: consecutive threads read consecutive
-// positions, which are consecutive in a row of the image at stride 1.
-template <int BN, bool POINTWISE>
-struct ColumnsTile {
+// positions, which are consecutive in a row of the image at stride 1.  FULL
+// (1x1 kernels, K = IC a multiple of BK): positions past the last read the
+// block's first, never stored, and the loads have no conditions.
+template <int BN, bool POINTWISE, bool FULL>
+struct Columns {
     static constexpr int kLoads = BN * kBK / 4 / 256;
+    static_assert(!FULL || POINTWISE, "FULL columns are those of 1x1 kernels");
     float v[kLoads][4];
+    const ConvArgs *c;
     // Per load slot, fixed over K: the image's first element (or -1 past the
     // last position) and the position's first input row and column.
     int64_t base[kLoads];
     int32_t iy0[kLoads], ix0[kLoads];
 
-    __device__ void init(const ConvArgs &c, int64_t p0, int tid) {
+    __device__ void init(const ConvArgs &args, int64_t p0, int tid) {
+        c = &args;
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int idx = tid + 256 * i;
-            const int64_t pos = p0 + idx % BN;
+            int64_t pos = p0 + idx % BN;
             base[i] = -1;
-            if (pos >= c.P) continue;
+            if (pos >= args.P) {
+                if (!FULL) continue;
+                pos = p0;
+            }
             uint32_t ox, oy, n;
-            split_index(static_cast<uint32_t>(pos), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy,
-                        n);
-            base[i] = static_cast<int64_t>(n) * c.xnb3;
+            split_index(static_cast<uint32_t>(pos), static_cast<uint32_t>(args.ow), static_cast<uint32_t>(args.oh), ox,
+                        oy, n);
+            base[i] = static_cast<int64_t>(n) * args.xnb3;
             if (POINTWISE) {
-                base[i] += static_cast<int64_t>(oy) * c.xnb1 + ox;
+                base[i] += static_cast<int64_t>(oy) * args.xnb1 + ox;
             } else {
-                iy0[i] = static_cast<int32_t>(oy) * c.s1 - c.p1;
-                ix0[i] = static_cast<int32_t>(ox) * c.s0 - c.p0;
+                iy0[i] = static_cast<int32_t>(oy) * args.s1 - args.p1;
+                ix0[i] = static_cast<int32_t>(ox) * args.s0 - args.p0;
             }
         }
     }
 
-    __device__ void load(const ConvArgs &c, int64_t k0, int tid) {
+    __device__ void load(int64_t k0, int tid) {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int idx = tid + 256 * i;
             const int kq = (idx / BN) * 4;
+            if (FULL) {
+                const float *img = c->x + base[i] + (k0 + kq) * c->xnb2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = img[e * c->xnb2];
+                continue;
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[i][e] = 0.0f;
             if (base[i] < 0) continue;
-            const float *img = c.x + base[i];
+            const float *img = c->x + base[i];
             if (POINTWISE) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int64_t k = k0 + kq + e;
-                    if (k < c.K) v[i][e] = img[k * c.xnb2];
+                    if (k < c->K) v[i][e] = img[k * c->xnb2];
                 }
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t k = static_cast<uint32_t>(k0 + kq + e);
-                    if (k >= c.K) continue;
-                    const uint32_t ic = k / static_cast<uint32_t>(c.taps);
-                    const uint32_t t = k - ic * static_cast<uint32_t>(c.taps);
-                    const uint32_t kh = t / static_cast<uint32_t>(c.kw);
-                    const uint32_t kw = t - kh * static_cast<uint32_t>(c.kw);
-                    const int32_t iy = iy0[i] + static_cast<int32_t>(kh) * c.d1;
-                    const int32_t ix = ix0[i] + static_cast<int32_t>(kw) * c.d0;
-                    if (iy >= 0 && iy < c.ih && ix >= 0 && ix < c.iw) {
-                        v[i][e] = img[static_cast<int64_t>(ic) * c.xnb2 + static_cast<int64_t>(iy) * c.xnb1 + ix];
+                    if (k >= c->K) continue;
+                    const uint32_t ic = k / static_cast<uint32_t>(c->taps);
+                    const uint32_t t = k - ic * static_cast<uint32_t>(c->taps);
+                    const uint32_t kh = t / static_cast<uint32_t>(c->kw);
+                    const uint32_t kw = t - kh * static_cast<uint32_t>(c->kw);
+                    const int32_t iy = iy0[i] + static_cast<int32_t>(kh) * c->d1;
+                    const int32_t ix = ix0[i] + static_cast<int32_t>(kw) * c->d0;
+                    if (iy >= 0 && iy < c->ih && ix >= 0 && ix < c->iw) {
+                        v[i][e] = img[static_cast<int64_t>(ic) * c->xnb2 + static_cast<int64_t>(iy) * c->xnb1 + ix];
                     }
                 }
             }
@@ -403,13 +327,270 @@ struct ColumnsTile {
     }
 };
 
+// Columns of a k-major operand already split into two FP16 planes (hi, then
+// lo `plane` elements after): rows of k, `ld` apart, each BC consecutive
+// columns n read 8 at a time and written to LDS transposed, [n][k], as the
+// MFMA reads them.  `ld` is a multiple of 8; columns at or past it read
+// column 0, never stored.  FULL: K a multiple of BK.
+template <int BC, bool FULL>
+struct SplitCols {
+    static constexpr int kChunks = BC * kBK / 8 / 256;
+    static_assert(kChunks >= 1, "tile too small for 256 threads");
+    half8 v[2][kChunks];
+    const _Float16 *col[kChunks];
+    int64_t ld, plane, K;
+
+    __device__ void init(const _Float16 *base, int64_t ld_, int64_t plane_, int64_t n0, int64_t k_, int tid) {
+        ld = ld_;
+        plane = plane_;
+        K = k_;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int idx = tid + 256 * i;
+            const int64_t n = n0 + (idx % (BC / 8)) * 8;
+            const int kr = idx / (BC / 8);
+            col[i] = base + (n < ld ? n : 0) + kr * ld;
+        }
+    }
+
+    __device__ void load(int64_t k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int kr = (tid + 256 * i) / (BC / 8);
+            const bool in = FULL || k0 + kr < K;
+            const _Float16 *p = col[i] + k0 * ld;
+            v[0][i] = in ? *reinterpret_cast<const half8 *>(p) : half8{};
+            v[1][i] = in ? *reinterpret_cast<const half8 *>(p + plane) : half8{};
+        }
+    }
+
+    __device__ void store(_Float16 *hi, _Float16 *lo, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int idx = tid + 256 * i;
+            const int cq = (idx % (BC / 8)) * 8;
+            const int kr = idx / (BC / 8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                hi[(cq + j) * kLdk + kr] = v[0][i][j];
+                lo[(cq + j) * kLdk + kr] = v[1][i][j];
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ main loop
+
+// The K loop of a block: loads NS steps ahead of the MFMAs, through NS
+// register stages (la[], lb[], stage q holding the steps s = q mod NS) and two
+// LDS buffers (step s in buffer s % 2).  After the MFMAs of step t, the data
+// of step t + 1 goes from its stage into the other buffer, and past the
+// barrier that stage's loads of step t + 1 + NS go out.  Every load and store
+// is unconditional -- past the last step they repeat it, into a buffer no wave
+// reads again -- so that the compiler counts the loads in flight exactly and
+// waits only for the ones a store needs; only the MFMAs of steps past the
+// last are skipped, by a branch uniform over the block.
+template <int TM, int TN, int MODE, int NS, class LA, class LB>
+__device__ __forceinline__ void main_loop(float16v (&acc)[TM][TN], LA (&la)[NS], LB (&lb)[NS], _Float16 *lds,
+                                          int64_t steps, int tid, int lane, int wr, int wc) {
+    static_assert(NS % 2 == 0, "stages pair with the two LDS buffers");
+    constexpr int BM = 64 * TM, BN = 64 * TN;
+    constexpr int PA = planes_a(MODE), PB = planes_b(MODE);
+    constexpr int kBuf = (PA * BM + PB * BN) * kLdk;
+    _Float16 *buf[2] = {lds, lds + kBuf};
+    const auto a_hi = [&](int b) { return buf[b]; };
+    const auto a_lo = [&](int b) { return buf[b] + BM * kLdk; };
+    const auto b_hi = [&](int b) { return buf[b] + PA * BM * kLdk; };
+    const auto b_lo = [&](int b) { return buf[b] + (PA * BM + BN) * kLdk; };
+    const auto compute = [&](int b) {
+        mfma_step<TM, TN, MODE>(acc, a_hi(b) + wr * 32 * TM * kLdk, a_lo(b) + wr * 32 * TM * kLdk,
+                                b_hi(b) + wc * 32 * TN * kLdk, b_lo(b) + wc * 32 * TN * kLdk, lane);
+    };
+    const auto store = [&](int stage, int b) {
+        la[stage].store(a_hi(b), a_lo(b), tid);
+        lb[stage].store(b_hi(b), b_lo(b), tid);
+    };
+    // The scheduler keeps the loads where they are written: issued as early
+    // as the registers allow, not moved down to the stores that use them.
+    const auto load = [&](int stage, int64_t s) {
+        __builtin_amdgcn_sched_barrier(0);
+        la[stage].load(s * kBK, tid);
+        lb[stage].load(s * kBK, tid);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const int64_t last = steps - 1;
+    const auto at = [&](int64_t s) { return s < last ? s : last; };
+
+#pragma unroll
+    for (int q = 0; q < NS; ++q) load(q, at(q));
+    store(0, 0);
+    __syncthreads();
+    load(0, at(NS));
+    // At the top of each pass: buffer 0 holds step s, stages 1 .. NS - 1 steps
+    // s + 1 .. s + NS - 1, stage 0 step s + NS on its way.  One exit, at the
+    // top, so that every path into the loop has the same loads in flight.
+    for (int64_t s = 0; s < steps; s += NS) {
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+            if (s + q < steps) compute(q & 1);
+            store((q + 1) % NS, (q + 1) & 1);
+            __syncthreads();
+            load((q + 1) % NS, at(s + q + 1 + NS));
+        }
+    }
+}
+
+template <int TM, int TN, int MODE>
+constexpr int lds_halves() {
+    return 2 * (planes_a(MODE) * 64 * TM + planes_b(MODE) * 64 * TN) * kLdk;
+}
+
+// ------------------------------------------------------------------ MUL_MAT
+
+// C[m][n] = sum_k x[m][k] W[n][k] for rows m of x (single precision, split)
+// and rows n of W (FP16), the chain applied, into y[m * ldy + n].  With GATED,
+// the block's 128 rows of W are 64 features of the first half and the same 64
+// of the second (the gate), each wave's two column tiles a pair, and the
+// block writes out[m * ldo + j] = P[m][j] GELU(P[m][half + j]).
+template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS>
+__global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
+    constexpr int BM = 64 * TM;
+    constexpr int BN = 64 * TN;
+    static_assert(!GATED || TN == 2, "the gated form pairs two column tiles");
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, kSplitA>()];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave >> 1;  // wave row (0, 1)
+    const int wc = wave & 1;   // wave column
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t mb = b / p.col_blocks;
+    const int64_t nb = b % p.col_blocks;
+    const int64_t m0 = mb * BM;
+    const int64_t n0 = nb * (GATED ? BN / 2 : BN);
+
+    const auto x_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : -1; };
+    const auto w_row = [&](int r) -> int64_t {
+        if (GATED) {
+            const int wq = r / 64;
+            const int side = (r / 32) & 1;
+            const int64_t f = n0 + 32 * wq + (r & 31);
+            return f < p.half ? side * p.half + f : -1;
+        }
+        const int64_t f = n0 + r;
+        return f < p.N ? f : -1;
+    };
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+
+    F32Rows<BM, VECX, FULL> xa[NS];
+    F16Rows<BN, VECW, FULL> wb[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        xa[s].init(p.x, p.ldx, x_row, p.K, tid);
+        wb[s].init(p.w, p.ldw, w_row, p.K, tid);
+    }
+    main_loop<TM, TN, kSplitA, NS>(acc, xa, wb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
+
+    // The epilogue: rows m of the tile, column (feature) lane % 32; a tile's
+    // 16 values of the lane at a time, their loads before their stores.  A
+    // tile wholly inside the output addresses its rows as a stride from its
+    // first; at the last rows, rows past M read the last row and are not
+    // stored.
+    const int col = lane & 31;
+    const int64_t lane_row = 4 * (lane >> 5);
+    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
+    const auto row_off = [&](const DevStep &st, int64_t m) -> int64_t {
+        if (st.flat123) return m * st.nb[1];
+        uint32_t i1, i2, i3;
+        split_index(static_cast<uint32_t>(m), ne1, ne2, i1, i2, i3);
+        return i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+    };
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int64_t tile0 = m0 + wr * 32 * TM + 32 * i;
+        const int64_t mbase = tile0 + lane_row;
+        const bool full = tile0 + 32 <= p.M;
+        // The tile's rows all of one matrix (i2, i3): every operand strided by
+        // nb[1] along them, from the offset of the lane's first row.
+        const bool one_matrix = static_cast<uint64_t>(tile0 % p.ne1) + 32 <= static_cast<uint64_t>(p.ne1);
+        const auto stride = [&](int s) -> int64_t {
+            const DevStep &st = p.chain.steps[s];
+            return st.flat123 || one_matrix ? st.nb[1] : -1;
+        };
+        const auto first = [&](int s) -> int64_t { return row_off(p.chain.steps[s], mbase); };
+        // Rows past M read the last row; computed where used, per element.
+        const auto row = [&](int e) -> int64_t {
+            const int64_t m = opaque(mbase) + tile_row(e);
+            return m < p.M ? m : p.M - 1;
+        };
+        if (GATED) {
+            const int64_t f = n0 + 32 * wc + col;
+            const int64_t fc = f < p.half ? f : p.half - 1;
+            float xv[16], gv[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                xv[e] = acc[i][0][e] * kSplitUp;
+                gv[e] = acc[i][1][e] * kSplitUp;
+            }
+            apply_chain_tile(
+                p.chain, xv, full, [&](int s) { return fc * p.chain.steps[s].nb[0] + first(s); }, stride,
+                [&](int s, int e) { return fc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e)); });
+            apply_chain_tile(
+                p.chain, gv, full, [&](int s) { return (p.half + fc) * p.chain.steps[s].nb[0] + first(s); }, stride,
+                [&](int s, int e) {
+                    return (p.half + fc) * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+                });
+            if (f >= p.half) continue;
+            float *out = p.y + mbase * p.ldy + f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                if (full || mbase + tile_row(e) < p.M) out[tile_row(e) * p.ldy] = xv[e] * gelu(gv[e]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int64_t n = n0 + wc * 32 * TN + 32 * j + col;
+                const int64_t nc = n < p.N ? n : p.N - 1;
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+                float *out = p.y + mbase * p.ldy + nc;
+                if (p.from_redirect) {
+                    float r[16];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) r[e] = full ? out[tile_row(e) * p.ldy] : p.y[row(e) * p.ldy + nc];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(r[e], v[e]);
+                }
+                apply_chain_tile(
+                    p.chain, v, full, [&](int s) { return nc * p.chain.steps[s].nb[0] + first(s); }, stride,
+                    [&](int s, int e) { return nc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e)); });
+                if (n >= p.N) continue;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    if (full || mbase + tile_row(e) < p.M) out[tile_row(e) * p.ldy] = v[e];
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ direct convolution
+
 // y[n][oc][pos] = sum_k W[oc][k] columns[k][pos], the chain applied; W rows
 // K-contiguous FP16 (the kernel as ggml holds it, [OC][IC][KH][KW]).
-template <int TM, int TN, bool POINTWISE, bool VECW>
+template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     constexpr int BM = 64 * TM;  // output channels
     constexpr int BN = 64 * TN;  // positions
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2][(BM + 2 * BN) * kLdk];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, kSplitB>()];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -430,32 +611,19 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    F16RowsTile<BM, VECW> wa;
-    ColumnsTile<BN, POINTWISE> xb;
-    const int64_t steps = (c.K + kBK - 1) / kBK;
-    xb.init(c, p0, tid);
-    wa.load(c.w, c.K, w_row, 0, c.K, tid);
-    xb.load(c, 0, tid);
-    wa.store(lds[0], tid);
-    xb.store(lds[0] + BM * kLdk, lds[0] + (BM + BN) * kLdk, tid);
-    __syncthreads();
-    for (int64_t s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < steps) {
-            wa.load(c.w, c.K, w_row, (s + 1) * kBK, c.K, tid);
-            xb.load(c, (s + 1) * kBK, tid);
-        }
-        const _Float16 *base = lds[cur];
-        mfma_step<TM, TN, false>(acc, base + (wr * 32 * TM) * kLdk, nullptr, base + (BM + wc * 32 * TN) * kLdk,
-                                 base + (BM + BN + wc * 32 * TN) * kLdk, lane);
-        if (s + 1 < steps) {
-            wa.store(lds[cur ^ 1], tid);
-            xb.store(lds[cur ^ 1] + BM * kLdk, lds[cur ^ 1] + (BM + BN) * kLdk, tid);
-        }
-        __syncthreads();
+    F16Rows<BM, VECW, FULL> wa[NS];
+    Columns<BN, POINTWISE, FULL> xb[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        wa[s].init(c.w, c.K, w_row, c.K, tid);
+        xb[s].init(c, p0, tid);
     }
+    main_loop<TM, TN, kSplitB, NS>(acc, wa, xb, lds, (c.K + kBK - 1) / kBK, tid, lane, wr, wc);
 
+    // The epilogue: output channels oc down the tile, position lane % 32 across;
+    // a tile wholly inside OC addresses its channels as a stride from its first.
     const int col = lane & 31;
+    const int64_t lane_row = 4 * (lane >> 5);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int64_t pos = p0 + wc * 32 * TN + 32 * j + col;
@@ -464,41 +632,115 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
         split_index(static_cast<uint32_t>(pos), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
         const int64_t at = static_cast<int64_t>(n) * c.ynb3 + static_cast<int64_t>(oy) * c.ynb1 + ox;
         const int64_t in_image = static_cast<int64_t>(oy) * c.ow + ox;
+        const auto xyn = [&](const DevStep &st) -> int64_t {
+            const int64_t xy =
+                st.flat01 ? in_image * st.nb[0] : static_cast<int64_t>(ox) * st.nb[0] + static_cast<int64_t>(oy) * st.nb[1];
+            return xy + static_cast<int64_t>(n) * st.nb[3];
+        };
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            const int64_t obase = oc0 + wr * 32 * TM + 32 * i;
+            const int64_t tile0 = oc0 + wr * 32 * TM + 32 * i;
+            const int64_t obase = tile0 + lane_row;
+            const bool full = tile0 + 32 <= c.oc;
             // Channels past OC read the last and are not stored.
             const auto chan = [&](int e) -> int64_t {
-                const int64_t oc = obase + acc_row(e, lane);
+                const int64_t oc = opaque(obase) + tile_row(e);
                 return oc < c.oc ? oc : c.oc - 1;
             };
             float v[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+            float *out = c.y + at + obase * c.ynb2;
             if (c.from_redirect) {
                 float r[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) r[e] = c.y[at + chan(e) * c.ynb2];
+                for (int e = 0; e < 16; ++e) r[e] = full ? out[tile_row(e) * c.ynb2] : c.y[at + chan(e) * c.ynb2];
 #pragma unroll
                 for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(r[e], v[e]);
             }
-            apply_chain_block(c.chain, v, [&](int s, int e) {
-                const DevStep &st = c.chain.steps[s];
-                const int64_t xy = st.flat01 ? in_image * st.nb[0]
-                                             : static_cast<int64_t>(ox) * st.nb[0] + static_cast<int64_t>(oy) * st.nb[1];
-                return xy + chan(e) * st.nb[2] + static_cast<int64_t>(n) * st.nb[3];
-            });
+            apply_chain_tile(
+                c.chain, v, full,
+                [&](int s) { return xyn(c.chain.steps[s]) + obase * c.chain.steps[s].nb[2]; },
+                [&](int s) { return c.chain.steps[s].nb[2]; },
+                [&](int s, int e) { return xyn(c.chain.steps[s]) + chan(e) * c.chain.steps[s].nb[2]; });
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int64_t oc = obase + acc_row(e, lane);
-                if (oc < c.oc) c.y[at + oc * c.ynb2] = v[e];
+                if (full || obase + tile_row(e) < c.oc) out[tile_row(e) * c.ynb2] = v[e];
             }
         }
     }
 }
 
+// ------------------------------------------------------------------ Winograd's products
+
+// C[b][m][n] = sum_k A[b][m][k] B[b][k][n] for the batches b, both operands
+// already split into two FP16 planes: A K-contiguous rows, B k-major rows of
+// columns (transposed on the way into LDS); three MFMAs a product.
+template <int TM, int TN, bool FULL, int NS>
+__global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) {
+    constexpr int BM = 64 * TM;
+    constexpr int BN = 64 * TN;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, kSplitBoth>()];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave >> 1;
+    const int wc = wave & 1;
+
+    const int64_t per_batch = p.m_blocks * p.n_blocks;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t batch = bid / per_batch;
+    const int64_t rem = bid - batch * per_batch;
+    const int64_t mb = rem / p.n_blocks;
+    const int64_t nb = rem - mb * p.n_blocks;
+    const int64_t m0 = mb * BM, n0 = nb * BN;
+    const _Float16 *A = p.a + batch * p.a_batch;
+    const _Float16 *B = p.b + batch * p.b_batch;
+    float *C = p.c + batch * p.c_batch;
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+
+    F16Rows<BM, true, FULL, 2> la[NS];
+    SplitCols<BN, FULL> lb[NS];
+    const auto a_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : -1; };
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        la[s].init(A, p.K, a_row, p.K, tid, p.a_plane);
+        lb[s].init(B, p.ldb, p.b_plane, n0, p.K, tid);
+    }
+    main_loop<TM, TN, kSplitBoth, NS>(acc, la, lb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
+
+    // Both operands were scaled by 2^-4 in the split: the product by 2^-8.
+    const int col = lane & 31;
+    const int64_t lane_row = 4 * (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + wc * 32 * TN + 32 * j + col;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int64_t tile0 = m0 + wr * 32 * TM + 32 * i;
+            const bool full = tile0 + 32 <= p.M;
+            float *out = C + (tile0 + lane_row) * p.N + n;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                if (full || tile0 + lane_row + tile_row(e) < p.M) {
+                    out[tile_row(e) * p.N] = acc[i][j][e] * (kSplitUp * kSplitUp);
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ launchers
+
 template <int TM, int TN, bool GATED>
-hipError_t launch_mul_mat_t(const MulMatArgs &p, hipStream_t stream) {
+hipError_t launch_mul_mat_t(const MulMatArgs &p, int stages, hipStream_t stream) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
     MulMatArgs a = p;
@@ -507,62 +749,103 @@ hipError_t launch_mul_mat_t(const MulMatArgs &p, hipStream_t stream) {
     const int64_t blocks = ((p.M + BM - 1) / BM) * a.col_blocks;
     const bool vx = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0;
     const bool vw = p.ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
+    const bool full = vx && vw && p.K % kBK == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(GATED ? "mul_mat_gated" : "mul_mat", stream);
-    if (vx && vw) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true>), grid, block, 0, stream, a);
+    if (full && stages == 4) {
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 4>), grid, block, 0, stream, a);
+    } else if (full) {
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 2>), grid, block, 0, stream, a);
+    } else if (vx && vw) {
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, false, 2>), grid, block, 0, stream, a);
     } else if (vx) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, false, false, 2>), grid, block, 0, stream, a);
     } else if (vw) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, true, false, 2>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, false, false, 2>), grid, block, 0, stream, a);
     }
     return hipGetLastError();
 }
 
 template <int TM, int TN, bool POINTWISE>
-hipError_t launch_conv_t(const ConvArgs &c, hipStream_t stream) {
+hipError_t launch_conv_t(const ConvArgs &c, int stages, hipStream_t stream) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
     ConvArgs a = c;
     a.oc_blocks = (c.oc + BM - 1) / BM;
     const int64_t blocks = ((c.P + BN - 1) / BN) * a.oc_blocks;
     const bool vw = c.K % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0;
+    const bool full = POINTWISE && vw && c.K % kBK == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(POINTWISE ? "conv_direct_pointwise" : "conv_direct", stream);
-    if (vw) {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true>), grid, block, 0, stream, a);
+    if (full && stages == 4) {
+        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 4>), grid, block, 0, stream, a);
+    } else if (full) {
+        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2>), grid, block, 0, stream, a);
+    } else if (vw) {
+        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2>), grid, block, 0, stream, a);
     }
     return hipGetLastError();
 }
 
+template <int TM, int TN>
+hipError_t launch_split_t(SplitBatchedArgs p, int stages, hipStream_t stream) {
+    p.m_blocks = (p.M + 64 * TM - 1) / (64 * TM);
+    p.n_blocks = (p.N + 64 * TN - 1) / (64 * TN);
+    dim3 grid(static_cast<uint32_t>(p.batches * p.m_blocks * p.n_blocks)), block(256);
+    if (stages == 4) {
+        hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 4>), grid, block, 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 2>), grid, block, 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+// Blocks of 64 TM x 64 TN: the largest tiles that still give each CU two
+// blocks or more, down to 64 x 64.
+template <class Launch>
+hipError_t pick_tiles(int64_t rows, int64_t cols, int64_t batches, Launch launch) {
+    const auto blocks = [&](int tm, int tn) {
+        return batches * ((rows + 64 * tm - 1) / (64 * tm)) * ((cols + 64 * tn - 1) / (64 * tn));
+    };
+    if (blocks(2, 2) >= 512) return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
+    if (blocks(2, 1) >= 512) return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
+    return launch(std::integral_constant<int, 1>(), std::integral_constant<int, 1>());
+}
+
 }  // namespace
 
-hipError_t launch_mul_mat(const MulMatArgs &p, hipStream_t stream) {
-    // Blocks of 128 rows; of 128 features where that still gives every CU a
-    // block, of 64 otherwise.
-    const int64_t rows = (p.M + 127) / 128;
-    if (rows * ((p.N + 127) / 128) >= 256) {
-        return launch_mul_mat_t<2, 2, false>(p, stream);
-    }
-    return launch_mul_mat_t<2, 1, false>(p, stream);
+hipError_t launch_mul_mat(const MulMatArgs &p, int stages, hipStream_t stream) {
+    return pick_tiles(p.M, p.N, 1, [&](auto tm, auto tn) {
+        return launch_mul_mat_t<decltype(tm)::value, decltype(tn)::value, false>(p, stages, stream);
+    });
 }
 
-hipError_t launch_mul_mat_gated(const MulMatArgs &p, hipStream_t stream) {
-    return launch_mul_mat_t<2, 2, true>(p, stream);
+hipError_t launch_mul_mat_gated(const MulMatArgs &p, int stages, hipStream_t stream) {
+    return launch_mul_mat_t<2, 2, true>(p, stages, stream);
 }
 
-hipError_t launch_conv_direct(const ConvArgs &c, hipStream_t stream) {
+hipError_t launch_conv_direct(const ConvArgs &c, int stages, hipStream_t stream) {
     const bool pointwise = c.kw == 1 && c.kh == 1 && c.s0 == 1 && c.s1 == 1 && c.p0 == 0 && c.p1 == 0;
-    const int64_t pblocks = (c.P + 127) / 128;
-    const bool wide = pblocks * ((c.oc + 127) / 128) >= 256;
-    if (pointwise) {
-        return wide ? launch_conv_t<2, 2, true>(c, stream) : launch_conv_t<1, 2, true>(c, stream);
-    }
-    return wide ? launch_conv_t<2, 2, false>(c, stream) : launch_conv_t<1, 2, false>(c, stream);
+    return pick_tiles(c.oc, c.P, 1, [&](auto tm, auto tn) {
+        constexpr int TM = decltype(tm)::value, TN = decltype(tn)::value;
+        return pointwise ? launch_conv_t<TM, TN, true>(c, stages, stream)
+                         : launch_conv_t<TM, TN, false>(c, stages, stream);
+    });
+}
+
+hipError_t launch_split_batched(const SplitBatchedArgs &p, int stages, hipStream_t stream) {
+    // The operands' layout is the caller's own: K padded to whole steps, rows
+    // of B to whole chunks of 8, every plane 16-byte aligned.
+    const bool aligned = (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 &&
+                         p.a_batch % 8 == 0 && p.a_plane % 8 == 0 && p.b_batch % 8 == 0 && p.b_plane % 8 == 0;
+    if (p.K % kBK != 0 || p.ldb % 8 != 0 || p.ldb < p.N || !aligned) return hipErrorInvalidValue;
+    // Both operands split: two planes each, so 128 x 64 at the most in 64 KB of LDS.
+    const int64_t blocks = p.batches * ((p.M + 127) / 128) * ((p.N + 63) / 64);
+    return blocks >= 512 ? launch_split_t<2, 1>(p, stages, stream) : launch_split_t<1, 1>(p, stages, stream);
 }
 
 }  // namespace sdhip

@@ -22,6 +22,13 @@ struct Tuning {
     int winograd4_positions = 256;   // the least outputs of an image F(4x4) is used for
     int winograd_small_tiles = 256;  // the most tiles of all images taken as small images
     int fuse = 1;                    // chains fused: 1; the caller computes them apart: 0
+    // This library's own: Winograd's products on the single-precision MFMA
+    // (1) instead of split FP16 parts (0), for comparison; results agree
+    // within the same bound.
+    int winograd_fp32 = 0;
+    // This library's own: the K steps a product's loads run ahead of its
+    // MFMAs, 2 or 4.
+    int gemm_stages = 2;
 };
 
 Tuning &tuning();

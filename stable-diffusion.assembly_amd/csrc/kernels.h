@@ -26,8 +26,10 @@ struct MulMatArgs {
     DevChain chain;
 };
 
-hipError_t launch_mul_mat(const MulMatArgs &p, hipStream_t stream);
-hipError_t launch_mul_mat_gated(const MulMatArgs &p, hipStream_t stream);
+// `stages`: the K steps the loads run ahead of the products, 2 or 4 (the
+// library's gemm_stages tuning).
+hipError_t launch_mul_mat(const MulMatArgs &p, int stages, hipStream_t stream);
+hipError_t launch_mul_mat_gated(const MulMatArgs &p, int stages, hipStream_t stream);
 
 // The direct convolution: y[n][oc][oy][ox] = sum over (ic, kh, kw).
 struct ConvArgs {
@@ -49,6 +51,23 @@ struct ConvArgs {
     DevChain chain;
 };
 
-hipError_t launch_conv_direct(const ConvArgs &c, hipStream_t stream);
+hipError_t launch_conv_direct(const ConvArgs &c, int stages, hipStream_t stream);
+
+// Batched products of operands already split into two FP16 planes (hi, and
+// lo `*_plane` elements after it): c[b][m][n] = sum_k a[b][m][k] b[b][k][n],
+// a's rows K-contiguous, b's rows of k `ldb` apart (a multiple of 8, at least
+// N), c's rows N apart.  Strides between batches in elements.  The caller
+// pads: K a multiple of 32, a and b 16-byte aligned, a_batch, a_plane, b_batch
+// and b_plane multiples of 8; hipErrorInvalidValue otherwise.
+struct SplitBatchedArgs {
+    const _Float16 *a;
+    const _Float16 *b;
+    float *c;
+    int64_t a_batch, a_plane, b_batch, b_plane, ldb, c_batch;
+    int64_t M, N, K, batches;
+    int64_t m_blocks, n_blocks;
+};
+
+hipError_t launch_split_batched(const SplitBatchedArgs &p, int stages, hipStream_t stream);
 
 }  // namespace sdhip

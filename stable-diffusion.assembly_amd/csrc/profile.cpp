@@ -49,8 +49,7 @@ hipEvent_t take_event(Profile &p) {
         return e;
     }
     hipEvent_t e = nullptr;
-    hipEventCreate(&e);
-    return e;
+    return hipEventCreate(&e) == hipSuccess ? e : nullptr;
 }
 
 }  // namespace
@@ -63,13 +62,13 @@ KernelScope::KernelScope(const char *name, hipStream_t stream) : name_(name), st
     std::lock_guard<std::mutex> g(p.lock);
     start_ = take_event(p);
     stop_ = take_event(p);
-    hipEventRecord(start_, stream_);
+    if (start_ == nullptr || stop_ == nullptr || hipEventRecord(start_, stream_) != hipSuccess) start_ = nullptr;
 }
 
 KernelScope::~KernelScope() {
     if (start_ == nullptr) return;
     Profile &p = profile();
-    hipEventRecord(stop_, stream_);
+    if (hipEventRecord(stop_, stream_) != hipSuccess) return;
     std::lock_guard<std::mutex> g(p.lock);
     p.pending.push_back({name_, start_, stop_});
 }
@@ -92,9 +91,9 @@ int sdhip_profile_collect(void) {
     Profile &p = profile();
     std::lock_guard<std::mutex> g(p.lock);
     for (Pending &e : p.pending) {
-        hipEventSynchronize(e.stop);
         float ms = 0.0f;
-        hipEventElapsedTime(&ms, e.start, e.stop);
+        if (hipEventSynchronize(e.stop) != hipSuccess || hipEventElapsedTime(&ms, e.start, e.stop) != hipSuccess)
+            ms = 0.0f;
         Totals &t = p.totals[e.name];
         t.ms += ms;
         t.launches += 1;

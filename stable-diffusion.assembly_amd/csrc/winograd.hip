@@ -6,18 +6,29 @@
 // F(2x2, 3x3) with the matrices of winograd.cc:19-22 and F(4x4, 3x3) with the
 // points 0, 1, -1, 2, -1/2, infinity of winograd.cc:1146-1183, 1259-1264.
 //
-// On the device, in four launches:
-//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi], single precision;
-//   2. the inputs,  V[xi][ic][tile] = (B^T d B)[xi], one thread per (tile, ic);
-//   3. the alpha^2 products M[xi] = U[xi] V[xi] on the single-precision MFMA
-//      (v_mfma_f32_16x16x4_f32), so that the sums are as exact as the
-//      reference's single-precision ones and the transforms' rounding is all
-//      that Winograd adds -- FP16 parts would not hold the transformed
-//      numbers (1/3, 1/15 of F(4x4)'s G) exactly;
-//   4. the outputs, A^T M A, with the sum begun from the residual when the
-//      chain says so and the chain after, one thread per (oc, tile).
+// On the device, in five launches:
+//   0. each input channel's exponent e_ic: its greatest |x| times the
+//      transform's gain (49 for F(4x4), 4 for F(2x2)) below 2^17 * 2^e_ic;
+//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi] * 2^(e_ic + a_oc), a_oc the
+//      output channel's own exponent, which brings its greatest transformed
+//      weight into [2^16, 2^17);
+//   2. the inputs,  V[xi][ic][tile] = (B^T d B)[xi] * 2^-e_ic;
+//      both written as two FP16 parts (device.h, split2), hi and lo, each a
+//      plane of its own, IC padded with zeros to a multiple of 32 and a row
+//      of tiles to a multiple of 8;
+//   3. the alpha^2 products M[xi] = U[xi] V[xi]: three MFMAs a product
+//      (gemm.hip), so that the sums are those of 22-bit operands where FP16
+//      would hold 11 -- the scales are powers of two, exact, and keep every
+//      part inside FP16's range;
+//   4. the outputs, A^T M A * 2^-a_oc, with the sum begun from the residual
+//      when the chain says so and the chain after, one thread per (oc, tile).
+// The scales cancel: sum_ic (U 2^(e_ic + a)) (V 2^-e_ic) = 2^a sum_ic U V.
+//
+// With winograd_fp32=1 the products go to the single-precision MFMA instead
+// (v_mfma_f32_16x16x4_f32), unscaled: a sixteenth of the rate, for comparison.
 
 #include "host.h"
+#include "kernels.h"
 #include "profile.h"
 #include "winograd.h"
 
@@ -50,6 +61,7 @@ struct Mat;
 template <>
 struct Mat<2> {
     static constexpr int A = 4;
+    static constexpr float kGain = 4.0f;  // the largest row sum of |B^T|, squared
     __device__ static float bt(int i, int j) { return kBT2[i][j]; }
     __device__ static float g(int i, int j) { return kG2[i][j]; }
     __device__ static float at(int i, int j) { return kAT2[i][j]; }
@@ -57,52 +69,167 @@ struct Mat<2> {
 template <>
 struct Mat<4> {
     static constexpr int A = 6;
+    static constexpr float kGain = 49.0f;
     __device__ static float bt(int i, int j) { return kBT4[i][j]; }
     __device__ static float g(int i, int j) { return kG4[i][j]; }
     __device__ static float at(int i, int j) { return kAT4[i][j]; }
 };
 
+// The exponent k of v = m 2^k, m in [0.5, 1): v < 2^k.
+__device__ __forceinline__ int exponent_above(float v) {
+    int k = 0;
+    frexpf(v, &k);
+    return k;
+}
+
+constexpr int kTop = 17;  // scaled operands below 2^17: below 2^13 once split2 takes 2^-4
+
+__device__ __forceinline__ float block_max(float v, float *scratch) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+}
+
+// ------------------------------------------------------------------ 0. input exponents
+
+// One block per input channel: its greatest |x| over every image, four
+// independent loads in flight per thread where the rows are contiguous.
+template <int M>
+__global__ __launch_bounds__(256) void channel_exponent_kernel(WinogradArgs a, int32_t *__restrict__ e) {
+    __shared__ float scratch[4];
+    const int64_t c = blockIdx.x;
+    const int64_t plane = a.ih * a.iw;
+    float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+    for (int64_t n = 0; n < a.n; ++n) {
+        const float *p = a.x + n * a.xnb3 + c * a.xnb2;
+        if (a.xnb1 == a.iw && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            const float4 *q = reinterpret_cast<const float4 *>(p);
+            const int64_t quads = plane / 4;
+            int64_t i = threadIdx.x;
+            for (; i + 768 < quads; i += 1024) {
+                const float4 v0 = q[i], v1 = q[i + 256], v2 = q[i + 512], v3 = q[i + 768];
+                m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
+                m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+                m2 = fmaxf(m2, fmaxf(fmaxf(fabsf(v2.x), fabsf(v2.y)), fmaxf(fabsf(v2.z), fabsf(v2.w))));
+                m3 = fmaxf(m3, fmaxf(fmaxf(fabsf(v3.x), fabsf(v3.y)), fmaxf(fabsf(v3.z), fabsf(v3.w))));
+            }
+            for (; i < quads; i += 256) {
+                const float4 v0 = q[i];
+                m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
+            }
+            for (int64_t j = quads * 4 + threadIdx.x; j < plane; j += 256) m1 = fmaxf(m1, fabsf(p[j]));
+        } else {
+            for (int64_t i = threadIdx.x; i < plane; i += 256) {
+                const int64_t y = i / a.iw;
+                m0 = fmaxf(m0, fabsf(p[y * a.xnb1 + (i - y * a.iw)]));
+            }
+        }
+    }
+    const float m = block_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)), scratch);
+    if (threadIdx.x == 0) e[c] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : 0;
+}
+
 // ------------------------------------------------------------------ 1. weights
 
-// U[xi][oc][ic] = (G g G^T)[xi]: G g a column at a time, then (G g) G^T a row
-// at a time (winograd.cc:1281-1300), one thread per (oc, ic).
-template <int M>
-__global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict__ w, float *__restrict__ u, int64_t oc,
-                                                      int64_t ic) {
-    constexpr int A = Mat<M>::A;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= oc * ic) return;
-    float g[3][3];
+__device__ __forceinline__ void load_g(const _Float16 *w, float (&g)[3][3]) {
 #pragma unroll
-    for (int i = 0; i < 9; ++i) g[i / 3][i % 3] = static_cast<float>(w[t * 9 + i]);
+    for (int i = 0; i < 9; ++i) g[i / 3][i % 3] = static_cast<float>(w[i]);
+}
+
+// (G g G^T) of one kernel: G g a column at a time, then (G g) G^T a row at a
+// time (winograd.cc:1281-1300).
+template <int M>
+__device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[Mat<M>::A][Mat<M>::A]) {
+    constexpr int A = Mat<M>::A;
     float gg[A][3];
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j)
             gg[i][j] = Mat<M>::g(i, 0) * g[0][j] + Mat<M>::g(i, 1) * g[1][j] + Mat<M>::g(i, 2) * g[2][j];
-    const int64_t plane = oc * ic;
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
         for (int j = 0; j < A; ++j)
-            u[(i * A + j) * plane + t] =
-                gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
+            u[i][j] = gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
+}
+
+// One block per output channel: the channel's exponent a_oc from its
+// greatest |U| 2^e_ic, then U * 2^(e_ic + a_oc) split into its two FP16
+// planes, u[xi][part][oc][kp], zeros for the channels from IC to kp.
+template <int M>
+__global__ __launch_bounds__(256) void weights_scaled_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
+                                                             int64_t kp, const int32_t *__restrict__ e,
+                                                             _Float16 *__restrict__ u, int32_t *__restrict__ a_oc) {
+    constexpr int A = Mat<M>::A;
+    __shared__ float scratch[4];
+    const int64_t o = blockIdx.x;
+    float m = 0.0f;
+    for (int64_t c = threadIdx.x; c < ic; c += 256) {
+        float g[3][3], t[A][A];
+        load_g(w + (o * ic + c) * 9, g);
+        transform_g<M>(g, t);
+        float tm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < A; ++j) tm = fmaxf(tm, fabsf(t[i][j]));
+        m = fmaxf(m, ldexpf(tm, e[c]));
+    }
+    m = block_max(m, scratch);
+    const int a = m > 0.0f ? kTop - exponent_above(m) : 0;
+    if (threadIdx.x == 0) a_oc[o] = a;
+    const int64_t part = oc * kp;
+    _Float16 *row = u + o * kp;
+    for (int64_t c = threadIdx.x; c < kp; c += 256) {
+        float t[A][A] = {};
+        if (c < ic) {
+            float g[3][3];
+            load_g(w + (o * ic + c) * 9, g);
+            transform_g<M>(g, t);
+        }
+        const int s = c < ic ? e[c] + a : 0;
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < A; ++j) {
+                _Float16 hi, lo;
+                split2(ldexpf(t[i][j], s), hi, lo);
+                row[(2 * (i * A + j)) * part + c] = hi;
+                row[(2 * (i * A + j) + 1) * part + c] = lo;
+            }
+    }
+}
+
+// Unscaled U[xi][oc][ic], one thread per (oc, ic), for the single-precision products.
+template <int M>
+__global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict__ w, float *__restrict__ u, int64_t oc,
+                                                      int64_t ic) {
+    constexpr int A = Mat<M>::A;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= oc * ic) return;
+    float g[3][3], v[A][A];
+    load_g(w + t * 9, g);
+    transform_g<M>(g, v);
+    const int64_t plane = oc * ic;
+#pragma unroll
+    for (int i = 0; i < A; ++i)
+#pragma unroll
+        for (int j = 0; j < A; ++j) u[(i * A + j) * plane + t] = v[i][j];
 }
 
 // ------------------------------------------------------------------ 2. inputs
 
-// V[xi][ic][tile] = (B^T d B)[xi] of the alpha x alpha inputs of the tile,
-// zeros outside the image: B^T d (a row r of B^T takes its combination of the
-// rows of d), then each of those times B.  One thread per (tile, ic),
-// consecutive threads consecutive tiles.
+// (B^T d B) of the alpha x alpha inputs of a tile, zeros outside the image:
+// B^T d (a row r of B^T takes its combination of the rows of d), then each of
+// those times B.
 template <int M>
-__global__ __launch_bounds__(256) void inputs_kernel(WinogradArgs a, float *__restrict__ v) {
+__device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile, uint32_t c,
+                                            float (&v)[Mat<M>::A][Mat<M>::A]) {
     constexpr int A = Mat<M>::A;
-    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-    if (t >= static_cast<uint32_t>(a.tiles * a.ic)) return;
-    const uint32_t c = t / static_cast<uint32_t>(a.tiles);
-    const uint32_t tile = t - c * static_cast<uint32_t>(a.tiles);
     uint32_t tx, ty, n;
     split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     const int64_t y0 = static_cast<int64_t>(ty) * M - a.p1;
@@ -129,7 +256,6 @@ __global__ __launch_bounds__(256) void inputs_kernel(WinogradArgs a, float *__re
             for (int i = 0; i < A; ++i) s += Mat<M>::bt(r, i) * d[i][j];
             bd[r][j] = s;
         }
-    const int64_t plane_v = a.ic * a.tiles;
 #pragma unroll
     for (int r = 0; r < A; ++r)
 #pragma unroll
@@ -137,11 +263,59 @@ __global__ __launch_bounds__(256) void inputs_kernel(WinogradArgs a, float *__re
             float x = 0.0f;
 #pragma unroll
             for (int j = 0; j < A; ++j) x += bd[r][j] * Mat<M>::bt(s, j);
-            v[(r * A + s) * plane_v + static_cast<int64_t>(c) * a.tiles + tile] = x;
+            v[r][s] = x;
         }
 }
 
-// ------------------------------------------------------------------ 3. products
+// V[xi][ic][tile] * 2^-e_ic split into its two FP16 planes,
+// v[xi][part][kp][tp], one thread per (ic, tile), consecutive threads
+// consecutive tiles; zeros for the channels from IC to kp.
+template <int M>
+__global__ __launch_bounds__(256) void inputs_scaled_kernel(WinogradArgs a, int64_t kp, int64_t tp,
+                                                            const int32_t *__restrict__ e, _Float16 *__restrict__ v) {
+    constexpr int A = Mat<M>::A;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= static_cast<uint32_t>(a.tiles * kp)) return;
+    const uint32_t c = t / static_cast<uint32_t>(a.tiles);
+    const uint32_t tile = t - c * static_cast<uint32_t>(a.tiles);
+    float x[A][A] = {};
+    int s = 0;
+    if (c < a.ic) {
+        transform_d<M>(a, tile, c, x);
+        s = -e[c];
+    }
+    const int64_t part = kp * tp;
+    _Float16 *out = v + static_cast<int64_t>(c) * tp + tile;
+#pragma unroll
+    for (int r = 0; r < A; ++r)
+#pragma unroll
+        for (int q = 0; q < A; ++q) {
+            _Float16 hi, lo;
+            split2(ldexpf(x[r][q], s), hi, lo);
+            out[(2 * (r * A + q)) * part] = hi;
+            out[(2 * (r * A + q) + 1) * part] = lo;
+        }
+}
+
+// Unscaled V[xi][ic][tile], for the single-precision products: consecutive
+// threads consecutive tiles.
+template <int M>
+__global__ __launch_bounds__(256) void inputs_kernel(WinogradArgs a, float *__restrict__ v) {
+    constexpr int A = Mat<M>::A;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= static_cast<uint32_t>(a.tiles * a.ic)) return;
+    const uint32_t c = t / static_cast<uint32_t>(a.tiles);
+    const uint32_t tile = t - c * static_cast<uint32_t>(a.tiles);
+    float x[A][A];
+    transform_d<M>(a, tile, c, x);
+    const int64_t plane = a.ic * a.tiles;
+#pragma unroll
+    for (int r = 0; r < A; ++r)
+#pragma unroll
+        for (int q = 0; q < A; ++q) v[(r * A + q) * plane + t] = x[r][q];
+}
+
+// ------------------------------------------------------------------ 3. single-precision products
 
 // C[b][m][n] = sum_k A[b][m][k] B[b][k][n] for the alpha^2 batches b, A rows
 // K-contiguous (U: [oc][ic]), B rows N-contiguous (V: [ic][tile]), on
@@ -175,7 +349,6 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
     const bool vec_a = (K % 4) == 0;
     const bool vec_b = (N % 4) == 0;
 
-    // Global loads: A 64 x 16 = 256 float4 (one a thread), B 16 x 128 = 512 (two).
     float4 ra, rb[2];
     const auto load = [&](int64_t k0) {
         {
@@ -259,7 +432,6 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
         if (s + 1 < steps) store(cur ^ 1);
         __syncthreads();
     }
-    // Row 4 (lane / 16) + e, column lane % 16 of each 16 x 16 tile.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -274,11 +446,12 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
 
 // ------------------------------------------------------------------ 4. outputs
 
-// Y = A^T M A of the tile's alpha^2 products, then the sum begun from the
-// residual (from_redirect) and the chain, one thread per (oc, tile),
-// consecutive threads consecutive tiles.
+// Y = A^T M A * 2^-a_oc of the tile's alpha^2 products, then the sum begun from
+// the residual (from_redirect) and the chain, one thread per (oc, tile),
+// consecutive threads consecutive tiles.  a_oc null: no scale.
 template <int M>
-__global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod) {
+__global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod,
+                                                      const int32_t *__restrict__ a_oc) {
     constexpr int A = Mat<M>::A;
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
     if (t >= static_cast<uint32_t>(a.tiles * a.oc)) return;
@@ -287,11 +460,13 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
     uint32_t tx, ty, n;
     split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     const int64_t plane = a.oc * a.tiles;
+    const int unscale = a_oc != nullptr ? -a_oc[oc] : 0;
     float m[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
-        for (int j = 0; j < A; ++j) m[i][j] = prod[(i * A + j) * plane + static_cast<int64_t>(oc) * a.tiles + tile];
+        for (int j = 0; j < A; ++j)
+            m[i][j] = ldexpf(prod[(i * A + j) * plane + static_cast<int64_t>(oc) * a.tiles + tile], unscale);
     float am[M][A];
 #pragma unroll
     for (int i = 0; i < M; ++i)
@@ -344,52 +519,108 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
     }
 }
 
+// ------------------------------------------------------------------ host
+
 struct WorkLayout {
-    size_t u, v, m, total;  // byte offsets of U, V, M and the whole
+    int64_t kp, tp;                // IC padded to whole steps of K, tiles to whole chunks of 8
+    size_t e, a, u, v, m, total;  // byte offsets
 };
 
 WorkLayout work_layout(const WinogradArgs &a) {
     const int64_t alpha2 = (a.m + 2) * (a.m + 2);
     WorkLayout l{};
-    const size_t u = static_cast<size_t>(alpha2 * a.oc * a.ic) * 4;
-    const size_t v = static_cast<size_t>(alpha2 * a.ic * a.tiles) * 4;
-    const size_t m = static_cast<size_t>(alpha2 * a.oc * a.tiles) * 4;
-    l.u = 0;
-    l.v = round_up(static_cast<int64_t>(u), 256);
-    l.m = l.v + round_up(static_cast<int64_t>(v), 256);
-    l.total = l.m + round_up(static_cast<int64_t>(m), 256);
+    l.kp = round_up(a.ic, 32);
+    l.tp = round_up(a.tiles, 8);
+    size_t at = 0;
+    const auto take = [&](int64_t bytes) {
+        const size_t here = at;
+        at += static_cast<size_t>(round_up(bytes, 256));
+        return here;
+    };
+    // Either form: two FP16 planes of the padded sizes, or single precision
+    // of the unpadded ones.
+    l.e = take(a.ic * 4);
+    l.a = take(a.oc * 4);
+    l.u = take(alpha2 * a.oc * l.kp * 4);
+    l.v = take(alpha2 * l.kp * l.tp * 4);
+    l.m = take(alpha2 * a.oc * a.tiles * 4);
+    l.total = at;
     return l;
 }
 
 template <int M>
 sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     constexpr int A = Mat<M>::A;
+    const char *tag = M == 4 ? "winograd4" : "winograd2";
     const WorkLayout l = work_layout(a);
     char *base = static_cast<char *>(work);
+    int32_t *e = reinterpret_cast<int32_t *>(base + l.e);
+    int32_t *a_oc = reinterpret_cast<int32_t *>(base + l.a);
     float *u = reinterpret_cast<float *>(base + l.u);
     float *v = reinterpret_cast<float *>(base + l.v);
     float *m = reinterpret_cast<float *>(base + l.m);
-    const int64_t nw = a.oc * a.ic;
+    const std::string names[] = {std::string(tag) + ".exponents", std::string(tag) + ".weights",
+                                 std::string(tag) + ".inputs", std::string(tag) + ".products",
+                                 std::string(tag) + ".outputs"};
+    if (tuning().winograd_fp32) {
+        const int64_t n_in = a.tiles * a.ic;
+        {
+            KernelScope scope(names[1].c_str(), stream);
+            hipLaunchKernelGGL((weights_kernel<M>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0, stream, a.w, u,
+                               a.oc, a.ic);
+        }
+        {
+            KernelScope scope(names[2].c_str(), stream);
+            hipLaunchKernelGGL((inputs_kernel<M>), dim3(ceil_div(n_in, 256)), dim3(256), 0, stream, a, v);
+        }
+        {
+            KernelScope scope(names[3].c_str(), stream);
+            const int64_t mb = ceil_div(a.oc, kGBM), nb = ceil_div(a.tiles, kGBN);
+            hipLaunchKernelGGL(batched_gemm_f32, dim3(A * A * mb * nb), dim3(256), 0, stream, u, v, m, a.oc, a.tiles,
+                               a.ic, mb, nb);
+        }
+        KernelScope scope(names[4].c_str(), stream);
+        hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
+                           nullptr);
+        return launched(hipGetLastError(), "winograd");
+    }
+    _Float16 *uh = reinterpret_cast<_Float16 *>(u);
+    _Float16 *vh = reinterpret_cast<_Float16 *>(v);
     {
-        KernelScope scope(M == 4 ? "winograd4.weights" : "winograd2.weights", stream);
-        hipLaunchKernelGGL((weights_kernel<M>), dim3(ceil_div(nw, 256)), dim3(256), 0, stream, a.w, u, a.oc, a.ic);
+        KernelScope scope(names[0].c_str(), stream);
+        hipLaunchKernelGGL((channel_exponent_kernel<M>), dim3(a.ic), dim3(256), 0, stream, a, e);
     }
     {
-        KernelScope scope(M == 4 ? "winograd4.inputs" : "winograd2.inputs", stream);
-        const int64_t ni = a.tiles * a.ic;
-        hipLaunchKernelGGL((inputs_kernel<M>), dim3(ceil_div(ni, 256)), dim3(256), 0, stream, a, v);
+        KernelScope scope(names[1].c_str(), stream);
+        hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(a.oc), dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, uh,
+                           a_oc);
     }
     {
-        KernelScope scope(M == 4 ? "winograd4.products" : "winograd2.products", stream);
-        const int64_t mb = ceil_div(a.oc, kGBM), nb = ceil_div(a.tiles, kGBN);
-        hipLaunchKernelGGL(batched_gemm_f32, dim3(A * A * mb * nb), dim3(256), 0, stream, u, v, m, a.oc, a.tiles,
-                           a.ic, mb, nb);
+        KernelScope scope(names[2].c_str(), stream);
+        hipLaunchKernelGGL((inputs_scaled_kernel<M>), dim3(ceil_div(a.tiles * l.kp, 256)), dim3(256), 0, stream, a, l.kp,
+                           l.tp, e, vh);
     }
     {
-        KernelScope scope(M == 4 ? "winograd4.outputs" : "winograd2.outputs", stream);
-        const int64_t no = a.tiles * a.oc;
-        hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(no, 256)), dim3(256), 0, stream, a, m);
+        KernelScope scope(names[3].c_str(), stream);
+        SplitBatchedArgs p{};
+        p.a = uh;
+        p.a_plane = a.oc * l.kp;
+        p.a_batch = 2 * p.a_plane;
+        p.b = vh;
+        p.b_plane = l.kp * l.tp;
+        p.b_batch = 2 * p.b_plane;
+        p.ldb = l.tp;
+        p.c = m;
+        p.c_batch = a.oc * a.tiles;
+        p.M = a.oc;
+        p.N = a.tiles;
+        p.K = l.kp;
+        p.batches = A * A;
+        const hipError_t err = launch_split_batched(p, tuning().gemm_stages, stream);
+        if (err != hipSuccess) return launched(err, "winograd products");
     }
+    KernelScope scope(names[4].c_str(), stream);
+    hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, a_oc);
     return launched(hipGetLastError(), "winograd");
 }
 

@@ -55,7 +55,7 @@ def conv_case(gpu, c, seed, chain_steps=(), redirect=None, from_redirect=False, 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("c", CASES, ids=lambda c: "x".join(map(str, c)))
-@pytest.mark.parametrize("tuning", ["", "winograd=1", "winograd=0"])
+@pytest.mark.parametrize("tuning", ["", "winograd=1", "winograd=0", "winograd_fp32=1"])
 def test_conv2d(gpu, c, tuning):
     x, k32, y, path, p = conv_case(gpu, c, seed=sum(c), tuning=tuning)
     exact, mag = orc.exact_conv2d(x, k32, *p)
@@ -119,6 +119,34 @@ def test_conv2d_chain(gpu, c, mode):
     exact, mag = orc.exact_conv2d(x, k32, *p)
     err = orc.metric(out.cpu().numpy(), exact + add, mag + np.abs(add))
     print(f"conv chain {mode} {c} path {path}: {err:.3g}")
+    assert err <= BOUND
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [
+    (40, 36, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2),   # F(4x4)
+    (15, 9, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2),    # F(2x2)
+])
+def test_winograd_wide_range(gpu, c):
+    """Input channels 2^-30 .. 2^30 apart and output channels' weights 2^-12 ..
+    2^4: the split products scale each channel into FP16's range by powers of
+    two, so the bound holds at any scale an FP32 input takes."""
+    w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
+    r = rng(5)
+    x = uniform(r, (n, ic, h_, w_), 1.0) * np.exp2(r.integers(-30, 31, size=(1, ic, 1, 1))).astype(np.float32)
+    k = (r.uniform(-1, 1, size=(oc, ic, kh, kw)) * np.exp2(r.integers(-12, 5, size=(oc, 1, 1, 1))))
+    k16 = k.astype(np.float16)
+    k_d, x_d = dev(k16, gpu), dev(x.astype(np.float32), gpu)
+    oh, ow = out_size(h_, kh, s1, p1, d1), out_size(w_, kw, s0, p0, d0)
+    y = unwritten((n, oc, oh, ow), gpu)
+    params = sdhip.conv_params(s0, s1, p0, p1, d0, d1)
+    path = sdhip.conv2d_path(k_d, x_d, y, params)
+    sdhip.conv2d(k_d, x_d, y, params)
+    torch.cuda.synchronize()
+    exact, mag = orc.exact_conv2d(x.astype(np.float32), k16.astype(np.float32), s0, s1, p0, p1, d0, d1)
+    err = orc.metric(y.cpu().numpy(), exact, mag)
+    print(f"wide range {c} path {path}: {err:.3g}")
+    assert path in (2, 4)
     assert err <= BOUND
 
 
