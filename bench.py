@@ -256,7 +256,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported in this build "
-              f"(every operation of the path shards without exchange; see DESIGN.md)", file=sys.stderr)
+              f"(each operation of the path shards by images, rows or heads without exchange)", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -12,7 +12,7 @@
  * buffer (as ggml hands its wdata, sized by sdasm_work_size) and a HIP stream.
  *
  * Nothing here allocates device memory: the caller owns every tensor and the
- * work buffer, as ggml owns them for the reference (SURVEY: ownership).
+ * work buffer, as ggml owns them for the reference (sdasm.h:51-54).
  *
  * Errors.  SDHIP_UNSUPPORTED is the reference's "not taken" (false / 0 from
  * sdasm_compute_nodes, hooks.cc:29-55): the caller computes the node itself.
