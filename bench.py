@@ -116,7 +116,9 @@ def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupn
         gamma = 1.0 + 0.1 * torch.randn((1, oc, 1, 1), generator=g, device=dev)
         beta = 0.1 * torch.randn((1, oc, 1, 1), generator=g, device=dev)
         out = torch.empty_like(y)
-        gn = (out, sdhip.epilogue([("mul", gamma), ("add", beta), ("silu", None)]), sdhip.desc(out))
+        gn_size = lib.sdhip_group_norm_work_size(sdhip.desc(y), sdhip.desc(out), 32)
+        gn_work = torch.empty(max(gn_size, 8), dtype=torch.uint8, device=dev)
+        gn = (out, sdhip.epilogue([("mul", gamma), ("add", beta), ("silu", None)]), sdhip.desc(out), gn_work, gn_size)
     stream = sdhip.stream_handle()
     keep = (x, kern, y, steps, work)
 
@@ -124,7 +126,8 @@ def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupn
         sdhip.check(lib.sdhip_conv2d(dk, dx, dy, params, ctypes.byref(chain), ctypes.c_void_p(work.data_ptr()),
                                      size, stream), "conv2d")
         if gn is not None:
-            sdhip.check(lib.sdhip_group_norm(dy, gn[2], 32, 1e-5, ctypes.byref(gn[1]), stream), "group_norm")
+            sdhip.check(lib.sdhip_group_norm(dy, gn[2], 32, 1e-5, ctypes.byref(gn[1]), ctypes.c_void_p(gn[3].data_ptr()),
+                                             gn[4], stream), "group_norm")
 
     flops = 2.0 * n * oc * oh * ow * ic * k * k
     run.keep = keep

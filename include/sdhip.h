@@ -169,10 +169,14 @@ sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const
 /* GGML_OP_GROUP_NORM (norm.cc:100-140): x, y F32 contiguous of one shape,
  * `groups` groups of ceil(ne2 / groups) channels over ne[2], per image ne[3];
  * then the chain (scale, shift, SiLU).  Replaces group_norm_supported /
- * group_norm_compute (ops.h:58-61). */
+ * group_norm_compute (ops.h:58-61).  The work buffer (8-byte aligned) holds
+ * the partial sums of the group's slices: the bytes sdasm_work_size would
+ * report for the node (sdasm.h:51-54), where the reference's own form needs
+ * none. */
 int sdhip_group_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y, int groups);
+size_t sdhip_group_norm_work_size(const sdhip_tensor *x, const sdhip_tensor *y, int groups);
 sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
-                              const sdhip_epilogue *chain, void *stream);
+                              const sdhip_epilogue *chain, void *work, size_t work_size, void *stream);
 
 /* GGML_OP_NORM over ne[0] (norm.cc:148-175), then the chain.  Replaces
  * norm_supported / norm_compute (ops.h:62-63). */

@@ -66,6 +66,7 @@ const Field kFields[] = {
     {"fuse", &Tuning::fuse},
     {"winograd_fp32", &Tuning::winograd_fp32},
     {"gemm_stages", &Tuning::gemm_stages},
+    {"gemm_tiles", &Tuning::gemm_tiles},
 };
 
 }  // namespace

@@ -24,7 +24,8 @@
 //   MUL_MAT:     A = x (tokens, split), B = W (features): C[token][feature]
 //   convolution: A = W (output channels), B = the image's columns (split),
 //                C[channel][position]
-//   Winograd:    A = U[xi] (output channels), B = V[xi] (tiles), both split
+//   Winograd:    A = U[xi] (output channels, split by the transform),
+//                B = V[xi] (tiles, split here)
 // so that the output's contiguous dimension is always C's column, lane % 32
 // of the MFMA's result, and a wave's stores are 128-byte rows.
 
@@ -327,58 +328,6 @@ struct Columns {
     }
 };
 
-// Columns of a k-major operand already split into two FP16 planes (hi, then
-// lo `plane` elements after): rows of k, `ld` apart, each BC consecutive
-// columns n read 8 at a time and written to LDS transposed, [n][k], as the
-// MFMA reads them.  `ld` is a multiple of 8; columns at or past it read
-// column 0, never stored.  FULL: K a multiple of BK.
-template <int BC, bool FULL>
-struct SplitCols {
-    static constexpr int kChunks = BC * kBK / 8 / 256;
-    static_assert(kChunks >= 1, "tile too small for 256 threads");
-    half8 v[2][kChunks];
-    const _Float16 *col[kChunks];
-    int64_t ld, plane, K;
-
-    __device__ void init(const _Float16 *base, int64_t ld_, int64_t plane_, int64_t n0, int64_t k_, int tid) {
-        ld = ld_;
-        plane = plane_;
-        K = k_;
-#pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
-            const int idx = tid + 256 * i;
-            const int64_t n = n0 + (idx % (BC / 8)) * 8;
-            const int kr = idx / (BC / 8);
-            col[i] = base + (n < ld ? n : 0) + kr * ld;
-        }
-    }
-
-    __device__ void load(int64_t k0, int tid) {
-#pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
-            const int kr = (tid + 256 * i) / (BC / 8);
-            const bool in = FULL || k0 + kr < K;
-            const _Float16 *p = col[i] + k0 * ld;
-            v[0][i] = in ? *reinterpret_cast<const half8 *>(p) : half8{};
-            v[1][i] = in ? *reinterpret_cast<const half8 *>(p + plane) : half8{};
-        }
-    }
-
-    __device__ void store(_Float16 *hi, _Float16 *lo, int tid) const {
-#pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
-            const int idx = tid + 256 * i;
-            const int cq = (idx % (BC / 8)) * 8;
-            const int kr = idx / (BC / 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                hi[(cq + j) * kLdk + kr] = v[0][i][j];
-                lo[(cq + j) * kLdk + kr] = v[1][i][j];
-            }
-        }
-    }
-};
-
 // ------------------------------------------------------------------ main loop
 
 // The K loop of a block: loads NS steps ahead of the MFMAs, through NS
@@ -673,9 +622,9 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
 
 // ------------------------------------------------------------------ Winograd's products
 
-// C[b][m][n] = sum_k A[b][m][k] B[b][k][n] for the batches b, both operands
-// already split into two FP16 planes: A K-contiguous rows, B k-major rows of
-// columns (transposed on the way into LDS); three MFMAs a product.
+// C[b][m][n] = sum_k A[b][m][k] B[b][n][k] for the batches b: A already split
+// into two FP16 planes, B single precision split on its way into LDS, both
+// K-contiguous rows; three MFMAs a product.
 template <int TM, int TN, bool FULL, int NS>
 __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) {
     constexpr int BM = 64 * TM;
@@ -696,7 +645,7 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
     const int64_t nb = rem - mb * p.n_blocks;
     const int64_t m0 = mb * BM, n0 = nb * BN;
     const _Float16 *A = p.a + batch * p.a_batch;
-    const _Float16 *B = p.b + batch * p.b_batch;
+    const float *B = p.b + batch * p.b_batch;
     float *C = p.c + batch * p.c_batch;
 
     float16v acc[TM][TN];
@@ -706,12 +655,13 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
     F16Rows<BM, true, FULL, 2> la[NS];
-    SplitCols<BN, FULL> lb[NS];
+    F32Rows<BN, true, FULL> lb[NS];
     const auto a_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : -1; };
+    const auto b_row = [&](int r) -> int64_t { return n0 + r < p.N ? n0 + r : -1; };
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         la[s].init(A, p.K, a_row, p.K, tid, p.a_plane);
-        lb[s].init(B, p.ldb, p.b_plane, n0, p.K, tid);
+        lb[s].init(B, p.K, b_row, p.K, tid);
     }
     main_loop<TM, TN, kSplitBoth, NS>(acc, la, lb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
 
@@ -807,45 +757,51 @@ hipError_t launch_split_t(SplitBatchedArgs p, int stages, hipStream_t stream) {
 // Blocks of 64 TM x 64 TN: the largest tiles that still give each CU two
 // blocks or more, down to 64 x 64.
 template <class Launch>
-hipError_t pick_tiles(int64_t rows, int64_t cols, int64_t batches, Launch launch) {
+hipError_t pick_tiles(int64_t rows, int64_t cols, int64_t batches, int forced, Launch launch) {
     const auto blocks = [&](int tm, int tn) {
         return batches * ((rows + 64 * tm - 1) / (64 * tm)) * ((cols + 64 * tn - 1) / (64 * tn));
     };
-    if (blocks(2, 2) >= 512) return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
-    if (blocks(2, 1) >= 512) return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
+    if (forced == 22 || (forced == 0 && blocks(2, 2) >= 512)) {
+        return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
+    }
+    if (forced == 21 || (forced == 0 && blocks(2, 1) >= 512)) {
+        return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
+    }
     return launch(std::integral_constant<int, 1>(), std::integral_constant<int, 1>());
 }
 
 }  // namespace
 
-hipError_t launch_mul_mat(const MulMatArgs &p, int stages, hipStream_t stream) {
-    return pick_tiles(p.M, p.N, 1, [&](auto tm, auto tn) {
-        return launch_mul_mat_t<decltype(tm)::value, decltype(tn)::value, false>(p, stages, stream);
+hipError_t launch_mul_mat(const MulMatArgs &p, GemmShape g, hipStream_t stream) {
+    return pick_tiles(p.M, p.N, 1, g.tiles, [&](auto tm, auto tn) {
+        return launch_mul_mat_t<decltype(tm)::value, decltype(tn)::value, false>(p, g.stages, stream);
     });
 }
 
-hipError_t launch_mul_mat_gated(const MulMatArgs &p, int stages, hipStream_t stream) {
-    return launch_mul_mat_t<2, 2, true>(p, stages, stream);
+hipError_t launch_mul_mat_gated(const MulMatArgs &p, GemmShape g, hipStream_t stream) {
+    return launch_mul_mat_t<2, 2, true>(p, g.stages, stream);
 }
 
-hipError_t launch_conv_direct(const ConvArgs &c, int stages, hipStream_t stream) {
+hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream) {
     const bool pointwise = c.kw == 1 && c.kh == 1 && c.s0 == 1 && c.s1 == 1 && c.p0 == 0 && c.p1 == 0;
-    return pick_tiles(c.oc, c.P, 1, [&](auto tm, auto tn) {
+    const int stages = g.stages;
+    return pick_tiles(c.oc, c.P, 1, g.tiles, [&](auto tm, auto tn) {
         constexpr int TM = decltype(tm)::value, TN = decltype(tn)::value;
         return pointwise ? launch_conv_t<TM, TN, true>(c, stages, stream)
                          : launch_conv_t<TM, TN, false>(c, stages, stream);
     });
 }
 
-hipError_t launch_split_batched(const SplitBatchedArgs &p, int stages, hipStream_t stream) {
-    // The operands' layout is the caller's own: K padded to whole steps, rows
-    // of B to whole chunks of 8, every plane 16-byte aligned.
+hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream) {
+    // The operands' layout is the caller's own: K padded to whole steps, every
+    // row 16-byte aligned.
     const bool aligned = (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 &&
-                         p.a_batch % 8 == 0 && p.a_plane % 8 == 0 && p.b_batch % 8 == 0 && p.b_plane % 8 == 0;
-    if (p.K % kBK != 0 || p.ldb % 8 != 0 || p.ldb < p.N || !aligned) return hipErrorInvalidValue;
-    // Both operands split: two planes each, so 128 x 64 at the most in 64 KB of LDS.
-    const int64_t blocks = p.batches * ((p.M + 127) / 128) * ((p.N + 63) / 64);
-    return blocks >= 512 ? launch_split_t<2, 1>(p, stages, stream) : launch_split_t<1, 1>(p, stages, stream);
+                         p.a_batch % 8 == 0 && p.a_plane % 8 == 0 && p.b_batch % 4 == 0;
+    if (p.K % kBK != 0 || !aligned) return hipErrorInvalidValue;
+    // Both operands split, two planes each: 80 KB of LDS at 128 x 128.
+    return pick_tiles(p.M, p.N, p.batches, g.tiles, [&](auto tm, auto tn) {
+        return launch_split_t<decltype(tm)::value, decltype(tn)::value>(p, g.stages, stream);
+    });
 }
 
 }  // namespace sdhip

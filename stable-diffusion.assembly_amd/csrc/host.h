@@ -6,6 +6,7 @@
 
 #include "../../include/sdhip.h"
 #include "device.h"
+#include "kernels.h"
 
 namespace sdhip {
 
@@ -29,9 +30,14 @@ struct Tuning {
     // This library's own: the K steps a product's loads run ahead of its
     // MFMAs, 2 or 4.
     int gemm_stages = 2;
+    // This library's own: a product's block of 64 TM x 64 TN as TM TN (11,
+    // 21, 22), or 0 to choose by the size.
+    int gemm_tiles = 0;
 };
 
 Tuning &tuning();
+
+inline GemmShape gemm_shape() { return GemmShape{tuning().gemm_stages, tuning().gemm_tiles}; }
 
 sdhip_status fail(sdhip_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 sdhip_status launched(hipError_t e, const char *what);

@@ -26,10 +26,17 @@ struct MulMatArgs {
     DevChain chain;
 };
 
-// `stages`: the K steps the loads run ahead of the products, 2 or 4 (the
-// library's gemm_stages tuning).
-hipError_t launch_mul_mat(const MulMatArgs &p, int stages, hipStream_t stream);
-hipError_t launch_mul_mat_gated(const MulMatArgs &p, int stages, hipStream_t stream);
+// The shape of a product's launch: `stages`, the K steps its loads run ahead
+// of its MFMAs (2 or 4; the gemm_stages tuning); `tiles`, its block of
+// 64 TM x 64 TN given as TM TN (11, 21, 22), or 0 to choose by the size (the
+// gemm_tiles tuning).
+struct GemmShape {
+    int stages;
+    int tiles;
+};
+
+hipError_t launch_mul_mat(const MulMatArgs &p, GemmShape g, hipStream_t stream);
+hipError_t launch_mul_mat_gated(const MulMatArgs &p, GemmShape g, hipStream_t stream);
 
 // The direct convolution: y[n][oc][oy][ox] = sum over (ic, kh, kw).
 struct ConvArgs {
@@ -51,23 +58,23 @@ struct ConvArgs {
     DevChain chain;
 };
 
-hipError_t launch_conv_direct(const ConvArgs &c, int stages, hipStream_t stream);
+hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream);
 
-// Batched products of operands already split into two FP16 planes (hi, and
-// lo `*_plane` elements after it): c[b][m][n] = sum_k a[b][m][k] b[b][k][n],
-// a's rows K-contiguous, b's rows of k `ldb` apart (a multiple of 8, at least
-// N), c's rows N apart.  Strides between batches in elements.  The caller
-// pads: K a multiple of 32, a and b 16-byte aligned, a_batch, a_plane, b_batch
-// and b_plane multiples of 8; hipErrorInvalidValue otherwise.
+// Batched products c[b][m][n] = sum_k a[b][m][k] b[b][n][k]: a already split
+// into two FP16 planes (hi, and lo `a_plane` elements after it), b single
+// precision, both K-contiguous rows of K elements; c's rows N apart.  Strides
+// between batches in elements.  The caller pads: K a multiple of 32, a and b
+// 16-byte aligned, a_batch and a_plane multiples of 8, b_batch of 4;
+// hipErrorInvalidValue otherwise.
 struct SplitBatchedArgs {
     const _Float16 *a;
-    const _Float16 *b;
+    const float *b;
     float *c;
-    int64_t a_batch, a_plane, b_batch, b_plane, ldb, c_batch;
+    int64_t a_batch, a_plane, b_batch, c_batch;
     int64_t M, N, K, batches;
     int64_t m_blocks, n_blocks;
 };
 
-hipError_t launch_split_batched(const SplitBatchedArgs &p, int stages, hipStream_t stream);
+hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream);
 
 }  // namespace sdhip

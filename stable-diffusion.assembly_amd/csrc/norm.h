@@ -14,9 +14,19 @@ struct GroupNormArgs {
     int64_t ne0, ne1, ne2, ne3;
     int64_t xnb2, xnb3, ynb2, ynb3;
     int64_t groups, per_group;
+    int64_t chunk, slices;  // numbers of a slice; slices of a group
+    double *partials;       // [2][ne3 * groups][slices]: sums of x, then of (x - mean)^2
     float eps;
     DevChain chain;
 };
+
+// How a group norm of these extents splits, and its work buffer's bytes.
+struct GroupNormShape {
+    int64_t chunk, slices;
+    size_t work;
+};
+
+GroupNormShape group_norm_shape(int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int64_t groups);
 
 struct NormArgs {
     const float *x;

@@ -22,102 +22,182 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-constexpr int kGroupThreads = 1024;
+// GROUP_NORM in three launches over blocks of (image, group, slice), the
+// slices `chunk` consecutive numbers of the group's channels (consecutive
+// planes, ne0 * ne1 numbers each): the partial sums of x; from their total
+// the mean, and the partial sums of (x - mean)^2; from both totals the scale,
+// and the output with its chain.  Each sum of a slice goes to the work buffer
+// and is added up, in the order of the slices, by each block that needs the
+// total.
 
-// The sum of a block of kGroupThreads' values, every thread receiving it.
-__device__ double group_block_sum(double v, double *scratch) {
+struct GroupView {
+    int64_t item, slice, i3, c0, count, e0, e1;
+};
+
+__device__ __forceinline__ GroupView group_view(const GroupNormArgs &a) {
+    GroupView v;
+    v.item = blockIdx.x / a.slices;
+    v.slice = blockIdx.x - v.item * a.slices;
+    v.i3 = v.item / a.groups;
+    const int64_t g = v.item - v.i3 * a.groups;
+    v.c0 = g * a.per_group;
+    const int64_t c1 = v.c0 + a.per_group < a.ne2 ? v.c0 + a.per_group : a.ne2;
+    v.count = v.c0 < c1 ? (c1 - v.c0) * a.ne0 * a.ne1 : 0;
+    v.e0 = v.slice * a.chunk;
+    v.e1 = v.e0 + a.chunk < v.count ? v.e0 + a.chunk : v.count;
+    return v;
+}
+
+__device__ __forceinline__ double block_sum(double v, double *scratch) {
     v = wave_sum(v);
-    const int wave = threadIdx.x >> 6;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
     double s = 0.0;
 #pragma unroll
-    for (int w = 0; w < kGroupThreads / 64; ++w) s += scratch[w];
+    for (int w = 0; w < kThreads / 64; ++w) s += scratch[w];
     return s;
 }
 
-// One block of 16 waves per (image, group): the group's channels are
-// consecutive planes, ne0 * ne1 * channels numbers one after another, read
-// four at a time where they are aligned.  The output goes channel by channel,
-// so that a position's coordinates need no division unless the chain reads
-// operands along the rows.
-__global__ __launch_bounds__(kGroupThreads) void group_norm_kernel(GroupNormArgs a) {
-    __shared__ double scratch[kGroupThreads / 64];
-    const int64_t item = blockIdx.x;
-    const int64_t i3 = item / a.groups;
-    const int64_t g = item % a.groups;
-    const int64_t c0 = g * a.per_group;
-    const int64_t c1 = c0 + a.per_group < a.ne2 ? c0 + a.per_group : a.ne2;
-    if (c0 >= c1) return;
-    const int64_t plane = a.ne0 * a.ne1;
-    const int64_t count = plane * (c1 - c0);
-    const float *x = a.x + i3 * a.xnb3 + c0 * a.xnb2;
-    const bool vec = count % 4 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+// The total over the slices of an item, in their order.
+__device__ __forceinline__ double total(const double *partials, int64_t item, int64_t slices) {
+    double t = 0.0;
+    for (int64_t q = 0; q < slices; ++q) t += partials[item * slices + q];
+    return t;
+}
+
+// PASS 0: the sum of x over the block's slice; PASS 1: of (x - mean)^2, each
+// difference and square in single precision (norm.cc:44-90).
+template <int PASS>
+__device__ __forceinline__ double term(float x, float mean) {
+    if (PASS == 0) return static_cast<double>(x);
+    const float d = x - mean;
+    return static_cast<double>(__fmul_rn(d, d));
+}
+
+template <int PASS>
+__global__ __launch_bounds__(kThreads) void group_sums_kernel(GroupNormArgs a) {
+    __shared__ double scratch[kThreads / 64];
+    __shared__ float shared_mean;
+    const GroupView g = group_view(a);
     const int tid = threadIdx.x;
-    double s = 0.0;
-    if (vec) {
-        const float4 *x4 = reinterpret_cast<const float4 *>(x);
-        for (int64_t i = tid; i < count / 4; i += kGroupThreads) {
-            const float4 v = x4[i];
-            s += static_cast<double>(v.x);
-            s += static_cast<double>(v.y);
-            s += static_cast<double>(v.z);
-            s += static_cast<double>(v.w);
+    float mean = 0.0f;
+    if (PASS == 1) {
+        if (tid == 0 && g.count > 0) {
+            shared_mean = static_cast<float>(total(a.partials, g.item, a.slices) / static_cast<double>(g.count));
         }
-    } else {
-        for (int64_t i = tid; i < count; i += kGroupThreads) s += static_cast<double>(x[i]);
+        __syncthreads();
+        mean = shared_mean;
     }
-    const float mean = static_cast<float>(group_block_sum(s, scratch) / static_cast<double>(count));
-    double q = 0.0;
-    if (vec) {
+    const float *x = a.x + g.i3 * a.xnb3 + g.c0 * a.xnb2;
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        // a.chunk is a multiple of 4: the slice's quads start at e0 / 4.
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
-        for (int64_t i = tid; i < count / 4; i += kGroupThreads) {
-            const float4 v = x4[i];
-            const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
-            q += static_cast<double>(__fmul_rn(d0, d0));
-            q += static_cast<double>(__fmul_rn(d1, d1));
-            q += static_cast<double>(__fmul_rn(d2, d2));
-            q += static_cast<double>(__fmul_rn(d3, d3));
+        const int64_t q1 = g.e1 / 4;
+        int64_t i = g.e0 / 4 + tid;
+        for (; i + 3 * kThreads < q1; i += 4 * kThreads) {
+            const float4 v0 = x4[i], v1 = x4[i + kThreads], v2 = x4[i + 2 * kThreads], v3 = x4[i + 3 * kThreads];
+            s0 += term<PASS>(v0.x, mean) + term<PASS>(v0.y, mean) + term<PASS>(v0.z, mean) + term<PASS>(v0.w, mean);
+            s1 += term<PASS>(v1.x, mean) + term<PASS>(v1.y, mean) + term<PASS>(v1.z, mean) + term<PASS>(v1.w, mean);
+            s2 += term<PASS>(v2.x, mean) + term<PASS>(v2.y, mean) + term<PASS>(v2.z, mean) + term<PASS>(v2.w, mean);
+            s3 += term<PASS>(v3.x, mean) + term<PASS>(v3.y, mean) + term<PASS>(v3.z, mean) + term<PASS>(v3.w, mean);
         }
+        for (; i < q1; i += kThreads) {
+            const float4 v0 = x4[i];
+            s0 += term<PASS>(v0.x, mean) + term<PASS>(v0.y, mean) + term<PASS>(v0.z, mean) + term<PASS>(v0.w, mean);
+        }
+        for (int64_t e = q1 * 4 + tid; e < g.e1; e += kThreads) s1 += term<PASS>(x[e], mean);
     } else {
-        for (int64_t i = tid; i < count; i += kGroupThreads) {
-            const float d = x[i] - mean;
-            q += static_cast<double>(__fmul_rn(d, d));
-        }
+        for (int64_t e = g.e0 + tid; e < g.e1; e += kThreads) s0 += term<PASS>(x[e], mean);
     }
-    const float variance = static_cast<float>(group_block_sum(q, scratch) / static_cast<double>(count));
-    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
-    float *y = a.y + i3 * a.ynb3 + c0 * a.ynb2;
-    // Four numbers of a thread at a time, their chain's loads before their
-    // stores; those past the plane read its last and are not stored.
-    constexpr int kU = 4;
-    for (int64_t c = c0; c < c1; ++c) {
-        const float *xc = x + (c - c0) * plane;
-        float *yc = y + (c - c0) * plane;
-        for (int64_t i = tid; i < plane; i += kGroupThreads * kU) {
-            const auto at = [&](int u) -> int64_t {
-                const int64_t j = i + static_cast<int64_t>(u) * kGroupThreads;
-                return j < plane ? j : plane - 1;
-            };
-            float v[kU];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = __fmul_rn(xc[at(u)] - mean, scale);
-            apply_chain_block(a.chain, v, [&](int s, int u) {
+    const double sum = block_sum((s0 + s1) + (s2 + s3), scratch);
+    if (tid == 0) a.partials[(PASS * a.ne3 * a.groups + g.item) * a.slices + g.slice] = sum;
+}
+
+// The output of the block's slice, (x - mean) * scale and the chain, four
+// consecutive numbers of a thread at a time where the planes allow (the four
+// then share their channel); all loads of a step before its stores.
+__global__ __launch_bounds__(kThreads) void group_apply_kernel(GroupNormArgs a) {
+    __shared__ float shared[2];
+    const GroupView g = group_view(a);
+    const int tid = threadIdx.x;
+    if (tid == 0 && g.count > 0) {
+        const double n = static_cast<double>(g.count);
+        const float mean = static_cast<float>(total(a.partials, g.item, a.slices) / n);
+        const float variance =
+            static_cast<float>(total(a.partials + a.ne3 * a.groups * a.slices, g.item, a.slices) / n);
+        shared[0] = mean;
+        shared[1] = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
+    }
+    __syncthreads();
+    const float mean = shared[0], scale = shared[1];
+    const int64_t plane = a.ne0 * a.ne1;
+    const float *x = a.x + g.i3 * a.xnb3 + g.c0 * a.xnb2;
+    float *y = a.y + g.i3 * a.ynb3 + g.c0 * a.ynb2;
+    // A step whose operand is one number per channel (and image) reads one.
+    bool per_channel = true;
+    for (int s = 0; s < a.chain.count; ++s) {
+        const DevStep &st = a.chain.steps[s];
+        if (st.kind != 2 && (st.nb[0] != 0 || st.nb[1] != 0)) per_channel = false;
+    }
+    const auto offset = [&](const DevStep &st, int64_t c, int64_t p) -> int64_t {
+        const int64_t c_part = (g.c0 + c) * st.nb[2] + g.i3 * st.nb[3];
+        if (per_channel) return c_part;
+        const uint32_t r = static_cast<uint32_t>(p) / static_cast<uint32_t>(a.ne0);
+        return (p - static_cast<int64_t>(r) * a.ne0) * st.nb[0] + static_cast<int64_t>(r) * st.nb[1] + c_part;
+    };
+    const bool quads = plane % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    if (quads) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        float4 *y4 = reinterpret_cast<float4 *>(y);
+        for (int64_t i = g.e0 / 4 + tid; i < g.e1 / 4; i += kThreads) {
+            const float4 q = x4[i];
+            const int64_t e = i * 4;
+            const uint32_t c = static_cast<uint32_t>(e) / static_cast<uint32_t>(plane);
+            const int64_t p = e - static_cast<int64_t>(c) * plane;
+            float v[4] = {__fmul_rn(q.x - mean, scale), __fmul_rn(q.y - mean, scale), __fmul_rn(q.z - mean, scale),
+                          __fmul_rn(q.w - mean, scale)};
+#pragma unroll 1
+            for (int s = 0; s < a.chain.count; ++s) {
                 const DevStep &st = a.chain.steps[s];
-                int64_t xy = at(u) * st.nb[0];
-                if (!st.flat01) {
-                    const uint32_t r = static_cast<uint32_t>(at(u)) / static_cast<uint32_t>(a.ne0);
-                    xy = (at(u) - static_cast<int64_t>(r) * a.ne0) * st.nb[0] + static_cast<int64_t>(r) * st.nb[1];
-                }
-                return xy + c * st.nb[2] + i3 * st.nb[3];
-            });
+                if (st.kind == 2) {
 #pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int64_t j = i + static_cast<int64_t>(u) * kGroupThreads;
-                if (j < plane) yc[j] = v[u];
+                    for (int u = 0; u < 4; ++u) v[u] = silu(v[u]);
+                    continue;
+                }
+                float o[4];
+                if (per_channel) {
+                    const float b = st.operand[offset(st, c, p)];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) o[u] = b;
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) o[u] = st.operand[offset(st, c, p + u)];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = st.kind == 0 ? __fadd_rn(v[u], o[u]) : __fmul_rn(v[u], o[u]);
             }
+            y4[i] = make_float4(v[0], v[1], v[2], v[3]);
         }
+        return;
+    }
+    for (int64_t e = g.e0 + tid; e < g.e1; e += kThreads) {
+        const uint32_t c = static_cast<uint32_t>(e) / static_cast<uint32_t>(plane);
+        const int64_t p = e - static_cast<int64_t>(c) * plane;
+        float v = __fmul_rn(x[e] - mean, scale);
+#pragma unroll 1
+        for (int s = 0; s < a.chain.count; ++s) {
+            const DevStep &st = a.chain.steps[s];
+            if (st.kind == 2) {
+                v = silu(v);
+                continue;
+            }
+            const float o = st.operand[offset(st, c, p)];
+            v = st.kind == 0 ? __fadd_rn(v, o) : __fmul_rn(v, o);
+        }
+        y[e] = v;
     }
 }
 
@@ -163,9 +243,35 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(NormArgs a) {
 
 }  // namespace
 
+GroupNormShape group_norm_shape(int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int64_t groups) {
+    GroupNormShape g{};
+    const int64_t per_group = ceil_div(ne2, groups);
+    const int64_t count = per_group * ne0 * ne1;
+    const int64_t items = ne3 * groups;
+    // About 1024 blocks in all, each of 4096 numbers or more, a slice a
+    // multiple of 4 numbers so that every slice's quads start aligned.
+    const int64_t want = ceil_div(1024, items);
+    g.chunk = round_up(ceil_div(count, want), 4);
+    if (g.chunk < 4096) g.chunk = round_up(count < 4096 ? count : 4096, 4);
+    if (g.chunk < 4) g.chunk = 4;
+    g.slices = ceil_div(count, g.chunk);
+    if (g.slices < 1) g.slices = 1;
+    g.work = static_cast<size_t>(2 * items * g.slices) * sizeof(double);
+    return g;
+}
+
 hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream) {
-    KernelScope scope("group_norm", stream);
-    hipLaunchKernelGGL(group_norm_kernel, dim3(a.groups * a.ne3), dim3(kGroupThreads), 0, stream, a);
+    const dim3 grid(static_cast<uint32_t>(a.ne3 * a.groups * a.slices));
+    {
+        KernelScope scope("group_norm.sums", stream);
+        hipLaunchKernelGGL(group_sums_kernel<0>, grid, dim3(kThreads), 0, stream, a);
+    }
+    {
+        KernelScope scope("group_norm.squares", stream);
+        hipLaunchKernelGGL(group_sums_kernel<1>, grid, dim3(kThreads), 0, stream, a);
+    }
+    KernelScope scope("group_norm.apply", stream);
+    hipLaunchKernelGGL(group_apply_kernel, grid, dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -196,7 +196,7 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
     c.P = c.n * c.plane;
     c.from_redirect = from_redirect;
     c.chain = dc;
-    return launched(launch_conv_direct(c, tuning().gemm_stages, st), "conv2d direct");
+    return launched(launch_conv_direct(c, gemm_shape(), st), "conv2d direct");
 }
 
 }  // extern "C"

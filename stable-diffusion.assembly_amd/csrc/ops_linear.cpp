@@ -100,7 +100,7 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
         }
         return quantized_linear(a, false, work, st);
     }
-    return launched(launch_mul_mat(a, tuning().gemm_stages, st), "mul_mat");
+    return launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
 }
 
 int sdhip_mul_mat_gated_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
@@ -150,7 +150,7 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
         }
         return quantized_linear(a, true, work, st);
     }
-    return launched(launch_mul_mat_gated(a, tuning().gemm_stages, st), "mul_mat_gated");
+    return launched(launch_mul_mat_gated(a, gemm_shape(), st), "mul_mat_gated");
 }
 
 }  // extern "C"

@@ -12,11 +12,18 @@ extern "C" {
 
 int sdhip_group_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y, int groups) {
     if (x == nullptr || y == nullptr) return 0;
-    return holds_f32(x) && holds_f32(y) && contiguous(x) && contiguous(y) && same_shape(x, y) && groups > 0;
+    if (!(holds_f32(x) && holds_f32(y) && contiguous(x) && contiguous(y) && same_shape(x, y) && groups > 0)) return 0;
+    // A group's numbers are indexed in 32 bits.
+    return ceil_div(x->ne[2], groups) * x->ne[0] * x->ne[1] < (int64_t(1) << 31);
+}
+
+size_t sdhip_group_norm_work_size(const sdhip_tensor *x, const sdhip_tensor *y, int groups) {
+    if (!sdhip_group_norm_supported(x, y, groups)) return 0;
+    return group_norm_shape(x->ne[0], x->ne[1], x->ne[2], x->ne[3], groups).work;
 }
 
 sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
-                              const sdhip_epilogue *chain, void *stream) {
+                              const sdhip_epilogue *chain, void *work, size_t work_size, void *stream) {
     if (!sdhip_group_norm_supported(x, y, groups)) {
         return fail(SDHIP_UNSUPPORTED, "group_norm: operands not taken");
     }
@@ -39,6 +46,16 @@ sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int 
     a.groups = groups;
     a.per_group = ceil_div(a.ne2, groups);
     a.eps = eps;
+    const GroupNormShape shape = group_norm_shape(a.ne0, a.ne1, a.ne2, a.ne3, groups);
+    if (work == nullptr || work_size < shape.work) {
+        return fail(SDHIP_ERROR, "group_norm: work buffer of %zu bytes, %zu needed", work_size, shape.work);
+    }
+    if ((reinterpret_cast<uintptr_t>(work) & 7) != 0) {
+        return fail(SDHIP_ERROR, "group_norm: work buffer not 8-byte aligned");
+    }
+    a.chunk = shape.chunk;
+    a.slices = shape.slices;
+    a.partials = static_cast<double *>(work);
     return launched(launch_group_norm(a, static_cast<hipStream_t>(stream)), "group_norm");
 }
 

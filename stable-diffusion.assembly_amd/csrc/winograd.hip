@@ -7,22 +7,27 @@
 // points 0, 1, -1, 2, -1/2, infinity of winograd.cc:1146-1183, 1259-1264.
 //
 // On the device, in five launches:
-//   0. each input channel's exponent e_ic: its greatest |x| times the
-//      transform's gain (49 for F(4x4), 4 for F(2x2)) below 2^17 * 2^e_ic;
-//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi] * 2^(e_ic + a_oc), a_oc the
-//      output channel's own exponent, which brings its greatest transformed
-//      weight into [2^16, 2^17);
-//   2. the inputs,  V[xi][ic][tile] = (B^T d B)[xi] * 2^-e_ic;
-//      both written as two FP16 parts (device.h, split2), hi and lo, each a
-//      plane of its own, IC padded with zeros to a multiple of 32 and a row
-//      of tiles to a multiple of 8;
-//   3. the alpha^2 products M[xi] = U[xi] V[xi]: three MFMAs a product
-//      (gemm.hip), so that the sums are those of 22-bit operands where FP16
-//      would hold 11 -- the scales are powers of two, exact, and keep every
-//      part inside FP16's range;
-//   4. the outputs, A^T M A * 2^-a_oc, with the sum begun from the residual
-//      when the chain says so and the chain after, one thread per (oc, tile).
-// The scales cancel: sum_ic (U 2^(e_ic + a)) (V 2^-e_ic) = 2^a sum_ic U V.
+//   0. the scales, exact powers of two: each input channel's e_c, its
+//      greatest |x| times the input transform's gain (49 for F(4x4), 4 for
+//      F(2x2)) below 2^(17 + e_c); each output channel's a_o, its greatest
+//      FP16 weight times the weight transform's gain ((28/15)^2, 1.5^2)
+//      below 2^(17 - a_o);
+//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi] * 2^(a_o + e_c - E), E the
+//      greatest e_c, as two FP16 parts (device.h, split2), hi and lo, each a
+//      plane of its own, [xi][part][oc][kp], IC padded with zeros to kp, a
+//      multiple of 32;
+//   2. the inputs, V[xi][tile][ic] = (B^T d B)[xi] * 2^-e_c, single
+//      precision, [xi][tile][kp];
+//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: V split on its way into
+//      LDS, three MFMAs a product (gemm.hip), so that the sums are those of
+//      22-bit operands where FP16 would hold 11 -- the scales keep every part
+//      inside FP16's range: |U| 2^(a_o + e_c - E) and |V| 2^-e_c below 2^17;
+//   4. the outputs, A^T M A * 2^(E - a_o), with the sum begun from the
+//      residual when the chain says so and the chain after, one thread per
+//      (oc, tile).
+// The scales cancel: sum_c (U 2^(a + e_c - E)) (V 2^-e_c) = 2^(a - E) sum_c U V.
+// The weights and the inputs go out through LDS, so that their stores are
+// whole rows of IC rather than scattered halves.
 //
 // With winograd_fp32=1 the products go to the single-precision MFMA instead
 // (v_mfma_f32_16x16x4_f32), unscaled: a sixteenth of the rate, for comparison.
@@ -61,7 +66,8 @@ struct Mat;
 template <>
 struct Mat<2> {
     static constexpr int A = 4;
-    static constexpr float kGain = 4.0f;  // the largest row sum of |B^T|, squared
+    static constexpr float kGain = 4.0f;       // the largest row sum of |B^T|, squared
+    static constexpr float kWeightGain = 2.25f;  // the largest row sum of |G|, squared
     __device__ static float bt(int i, int j) { return kBT2[i][j]; }
     __device__ static float g(int i, int j) { return kG2[i][j]; }
     __device__ static float at(int i, int j) { return kAT2[i][j]; }
@@ -70,9 +76,22 @@ template <>
 struct Mat<4> {
     static constexpr int A = 6;
     static constexpr float kGain = 49.0f;
+    static constexpr float kWeightGain = 3.4844445f;  // (28 / 15)^2, rounded up
     __device__ static float bt(int i, int j) { return kBT4[i][j]; }
     __device__ static float g(int i, int j) { return kG4[i][j]; }
     __device__ static float at(int i, int j) { return kAT4[i][j]; }
+};
+
+// A row of a tile's outputs as one vector.
+template <int M>
+struct RowOf;
+template <>
+struct RowOf<2> {
+    using type = float __attribute__((ext_vector_type(2)));
+};
+template <>
+struct RowOf<4> {
+    using type = float __attribute__((ext_vector_type(4)));
 };
 
 // The exponent k of v = m 2^k, m in [0.5, 1): v < 2^k.
@@ -83,6 +102,7 @@ __device__ __forceinline__ int exponent_above(float v) {
 }
 
 constexpr int kTop = 17;  // scaled operands below 2^17: below 2^13 once split2 takes 2^-4
+constexpr int kZeroChannel = -126;  // the exponent of an input channel of zeros
 
 __device__ __forceinline__ float block_max(float v, float *scratch) {
 #pragma unroll
@@ -93,43 +113,72 @@ __device__ __forceinline__ float block_max(float v, float *scratch) {
     return fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
 }
 
-// ------------------------------------------------------------------ 0. input exponents
+// ------------------------------------------------------------------ 0. scales
 
-// One block per input channel: its greatest |x| over every image, four
-// independent loads in flight per thread where the rows are contiguous.
+constexpr int kScaleThreads = 1024;
+
+__device__ __forceinline__ float block_max_wide(float v, float *scratch) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = scratch[0];
+#pragma unroll
+    for (int i = 1; i < kScaleThreads / 64; ++i) m = fmaxf(m, scratch[i]);
+    return m;
+}
+
+__device__ __forceinline__ float abs_max4(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Blocks [0, IC): input channel c's greatest |x| over every image, four
+// independent loads in flight per thread where the rows are contiguous, and
+// its exponent e[c] (zero channels: the least, so that they scale to zero).
+// Blocks [IC, IC + OC): output channel o's greatest FP16 weight and a[o].
 template <int M>
-__global__ __launch_bounds__(256) void channel_exponent_kernel(WinogradArgs a, int32_t *__restrict__ e) {
-    __shared__ float scratch[4];
-    const int64_t c = blockIdx.x;
-    const int64_t plane = a.ih * a.iw;
+__global__ __launch_bounds__(kScaleThreads) void scales_kernel(WinogradArgs a, int32_t *__restrict__ e,
+                                                               int32_t *__restrict__ amax) {
+    __shared__ float scratch[kScaleThreads / 64];
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x;
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
-    for (int64_t n = 0; n < a.n; ++n) {
-        const float *p = a.x + n * a.xnb3 + c * a.xnb2;
-        if (a.xnb1 == a.iw && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-            const float4 *q = reinterpret_cast<const float4 *>(p);
-            const int64_t quads = plane / 4;
-            int64_t i = threadIdx.x;
-            for (; i + 768 < quads; i += 1024) {
-                const float4 v0 = q[i], v1 = q[i + 256], v2 = q[i + 512], v3 = q[i + 768];
-                m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
-                m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
-                m2 = fmaxf(m2, fmaxf(fmaxf(fabsf(v2.x), fabsf(v2.y)), fmaxf(fabsf(v2.z), fabsf(v2.w))));
-                m3 = fmaxf(m3, fmaxf(fmaxf(fabsf(v3.x), fabsf(v3.y)), fmaxf(fabsf(v3.z), fabsf(v3.w))));
-            }
-            for (; i < quads; i += 256) {
-                const float4 v0 = q[i];
-                m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
-            }
-            for (int64_t j = quads * 4 + threadIdx.x; j < plane; j += 256) m1 = fmaxf(m1, fabsf(p[j]));
-        } else {
-            for (int64_t i = threadIdx.x; i < plane; i += 256) {
-                const int64_t y = i / a.iw;
-                m0 = fmaxf(m0, fabsf(p[y * a.xnb1 + (i - y * a.iw)]));
+    if (b < a.ic) {
+        const int64_t plane = a.ih * a.iw;
+        for (int64_t n = 0; n < a.n; ++n) {
+            const float *p = a.x + n * a.xnb3 + b * a.xnb2;
+            if (a.xnb1 == a.iw && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+                const float4 *q = reinterpret_cast<const float4 *>(p);
+                const int64_t quads = plane / 4;
+                int64_t i = tid;
+                for (; i + 3 * kScaleThreads < quads; i += 4 * kScaleThreads) {
+                    const float4 v0 = q[i], v1 = q[i + kScaleThreads], v2 = q[i + 2 * kScaleThreads],
+                                 v3 = q[i + 3 * kScaleThreads];
+                    m0 = fmaxf(m0, abs_max4(v0));
+                    m1 = fmaxf(m1, abs_max4(v1));
+                    m2 = fmaxf(m2, abs_max4(v2));
+                    m3 = fmaxf(m3, abs_max4(v3));
+                }
+                for (; i < quads; i += kScaleThreads) m0 = fmaxf(m0, abs_max4(q[i]));
+                for (int64_t j = quads * 4 + tid; j < plane; j += kScaleThreads) m1 = fmaxf(m1, fabsf(p[j]));
+            } else {
+                for (int64_t i = tid; i < plane; i += kScaleThreads) {
+                    const int64_t y = i / a.iw;
+                    m0 = fmaxf(m0, fabsf(p[y * a.xnb1 + (i - y * a.iw)]));
+                }
             }
         }
+        const float m = block_max_wide(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)), scratch);
+        if (tid == 0) e[b] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : kZeroChannel;
+    } else {
+        const int64_t o = b - a.ic;
+        const int64_t count = a.ic * 9;
+        const _Float16 *p = a.w + o * count;
+        for (int64_t i = tid; i < count; i += kScaleThreads) m0 = fmaxf(m0, fabsf(static_cast<float>(p[i])));
+        const float m = block_max_wide(m0, scratch);
+        if (tid == 0) amax[o] = m > 0.0f ? kTop - exponent_above(m * Mat<M>::kWeightGain) : 0;
     }
-    const float m = block_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)), scratch);
-    if (threadIdx.x == 0) e[c] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : 0;
 }
 
 // ------------------------------------------------------------------ 1. weights
@@ -157,50 +206,57 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
             u[i][j] = gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
 }
 
-// One block per output channel: the channel's exponent a_oc from its
-// greatest |U| 2^e_ic, then U * 2^(e_ic + a_oc) split into its two FP16
-// planes, u[xi][part][oc][kp], zeros for the channels from IC to kp.
+// One block per output channel o: E, the greatest e_c, and shift[o] = E - a_o
+// for the outputs; then, 256 channels at a time, U * 2^(a_o + e_c - E) split
+// into its two FP16 parts, staged in LDS as [xi][part][channel] and written
+// out as rows of channels, u[xi][part][oc][kp], zeros from IC to kp.
+constexpr int kWeightChunk = 256;
+
 template <int M>
-__global__ __launch_bounds__(256) void weights_scaled_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
-                                                             int64_t kp, const int32_t *__restrict__ e,
-                                                             _Float16 *__restrict__ u, int32_t *__restrict__ a_oc) {
+__global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
+                                                            int64_t kp, const int32_t *__restrict__ e,
+                                                            const int32_t *__restrict__ amax, _Float16 *__restrict__ u,
+                                                            int32_t *__restrict__ shift) {
     constexpr int A = Mat<M>::A;
+    constexpr int kRows = 2 * A * A;
     __shared__ float scratch[4];
+    __shared__ __attribute__((aligned(16))) _Float16 stage[kRows][kWeightChunk];
     const int64_t o = blockIdx.x;
-    float m = 0.0f;
-    for (int64_t c = threadIdx.x; c < ic; c += 256) {
-        float g[3][3], t[A][A];
-        load_g(w + (o * ic + c) * 9, g);
-        transform_g<M>(g, t);
-        float tm = 0.0f;
-#pragma unroll
-        for (int i = 0; i < A; ++i)
-#pragma unroll
-            for (int j = 0; j < A; ++j) tm = fmaxf(tm, fabsf(t[i][j]));
-        m = fmaxf(m, ldexpf(tm, e[c]));
-    }
-    m = block_max(m, scratch);
-    const int a = m > 0.0f ? kTop - exponent_above(m) : 0;
-    if (threadIdx.x == 0) a_oc[o] = a;
-    const int64_t part = oc * kp;
-    _Float16 *row = u + o * kp;
-    for (int64_t c = threadIdx.x; c < kp; c += 256) {
+    const int tid = threadIdx.x;
+    int emax = kZeroChannel;
+    for (int64_t c = tid; c < ic; c += 256) emax = max(emax, e[c]);
+    const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
+    const int ao = amax[o];
+    if (tid == 0) shift[o] = E - ao;
+    for (int64_t c0 = 0; c0 < kp; c0 += kWeightChunk) {
+        const int64_t c = c0 + tid;
         float t[A][A] = {};
+        int s = 0;
         if (c < ic) {
             float g[3][3];
             load_g(w + (o * ic + c) * 9, g);
             transform_g<M>(g, t);
+            s = ao + e[c] - E;
         }
-        const int s = c < ic ? e[c] + a : 0;
 #pragma unroll
         for (int i = 0; i < A; ++i)
 #pragma unroll
             for (int j = 0; j < A; ++j) {
                 _Float16 hi, lo;
                 split2(ldexpf(t[i][j], s), hi, lo);
-                row[(2 * (i * A + j)) * part + c] = hi;
-                row[(2 * (i * A + j) + 1) * part + c] = lo;
+                stage[2 * (i * A + j)][tid] = hi;
+                stage[2 * (i * A + j) + 1][tid] = lo;
             }
+        __syncthreads();
+        // kRows rows of `width` halves, 8 at a time.
+        const int width = static_cast<int>(kp - c0 < kWeightChunk ? kp - c0 : kWeightChunk);
+        const int per_row = width / 8;
+        for (int q = tid; q < kRows * per_row; q += 256) {
+            const int r = q / per_row;
+            const int k = (q - r * per_row) * 8;
+            *reinterpret_cast<half8 *>(u + (r * oc + o) * kp + c0 + k) = *reinterpret_cast<const half8 *>(&stage[r][k]);
+        }
+        __syncthreads();
     }
 }
 
@@ -267,34 +323,49 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
         }
 }
 
-// V[xi][ic][tile] * 2^-e_ic split into its two FP16 planes,
-// v[xi][part][kp][tp], one thread per (ic, tile), consecutive threads
-// consecutive tiles; zeros for the channels from IC to kp.
+// V[xi][tile][ic] * 2^-e_c in single precision, v[xi][tile][kp], zeros for
+// the channels from IC to kp.  A block takes 8 consecutive tiles by 32
+// channels, one (tile, channel) a thread, consecutive threads consecutive
+// tiles (so that the reads of a channel are rows of the image); the results
+// are staged in LDS as [xi][tile][channel] and written out as rows of 32
+// channels.
+constexpr int kInTiles = 8, kInChannels = 32;
+
 template <int M>
-__global__ __launch_bounds__(256) void inputs_scaled_kernel(WinogradArgs a, int64_t kp, int64_t tp,
-                                                            const int32_t *__restrict__ e, _Float16 *__restrict__ v) {
+__global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
+                                                           float *__restrict__ v) {
     constexpr int A = Mat<M>::A;
-    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-    if (t >= static_cast<uint32_t>(a.tiles * kp)) return;
-    const uint32_t c = t / static_cast<uint32_t>(a.tiles);
-    const uint32_t tile = t - c * static_cast<uint32_t>(a.tiles);
+    // Rows of a tile 40 floats apart: 16-byte aligned, and the 64 lanes of a
+    // wave (8 tiles by 8 channels) in at most two to a bank.
+    __shared__ __attribute__((aligned(16))) float stage[A * A][kInTiles][kInChannels + 8];
+    const int tid = threadIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kInTiles;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kInChannels;
+    const int tl = tid % kInTiles, cl = tid / kInTiles;
+    const int64_t tile = t0 + tl, c = c0 + cl;
     float x[A][A] = {};
-    int s = 0;
-    if (c < a.ic) {
-        transform_d<M>(a, tile, c, x);
-        s = -e[c];
+    if (c < a.ic && tile < a.tiles) {
+        transform_d<M>(a, static_cast<uint32_t>(tile), static_cast<uint32_t>(c), x);
+        const int s = -e[c];
+#pragma unroll
+        for (int r = 0; r < A; ++r)
+#pragma unroll
+            for (int q = 0; q < A; ++q) x[r][q] = ldexpf(x[r][q], s);
     }
-    const int64_t part = kp * tp;
-    _Float16 *out = v + static_cast<int64_t>(c) * tp + tile;
 #pragma unroll
     for (int r = 0; r < A; ++r)
 #pragma unroll
-        for (int q = 0; q < A; ++q) {
-            _Float16 hi, lo;
-            split2(ldexpf(x[r][q], s), hi, lo);
-            out[(2 * (r * A + q)) * part] = hi;
-            out[(2 * (r * A + q) + 1) * part] = lo;
-        }
+        for (int q = 0; q < A; ++q) stage[r * A + q][tl][cl] = x[r][q];
+    __syncthreads();
+    // A * A * kInTiles rows of 32 floats, 4 at a time.
+    for (int q = tid; q < A * A * kInTiles * (kInChannels / 4); q += 256) {
+        const int row = q / (kInChannels / 4);
+        const int k = (q % (kInChannels / 4)) * 4;
+        const int xi = row / kInTiles, t = row % kInTiles;
+        if (t0 + t >= a.tiles) continue;
+        *reinterpret_cast<float4 *>(v + (xi * a.tiles + t0 + t) * kp + c0 + k) =
+            *reinterpret_cast<const float4 *>(&stage[xi][t][k]);
+    }
 }
 
 // Unscaled V[xi][ic][tile], for the single-precision products: consecutive
@@ -446,12 +517,12 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
 
 // ------------------------------------------------------------------ 4. outputs
 
-// Y = A^T M A * 2^-a_oc of the tile's alpha^2 products, then the sum begun from
-// the residual (from_redirect) and the chain, one thread per (oc, tile),
-// consecutive threads consecutive tiles.  a_oc null: no scale.
+// Y = A^T M A * 2^shift[oc] of the tile's alpha^2 products, then the sum
+// begun from the residual (from_redirect) and the chain, one thread per
+// (oc, tile), consecutive threads consecutive tiles.  shift null: no scale.
 template <int M>
 __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod,
-                                                      const int32_t *__restrict__ a_oc) {
+                                                      const int32_t *__restrict__ shift) {
     constexpr int A = Mat<M>::A;
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
     if (t >= static_cast<uint32_t>(a.tiles * a.oc)) return;
@@ -460,7 +531,7 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
     uint32_t tx, ty, n;
     split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     const int64_t plane = a.oc * a.tiles;
-    const int unscale = a_oc != nullptr ? -a_oc[oc] : 0;
+    const int unscale = shift != nullptr ? shift[oc] : 0;
     float m[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i)
@@ -478,8 +549,9 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
             am[i][j] = s;
         }
     // The tile's M x M outputs, their loads (the residual, the chain's
-    // operands) all before their stores; outputs past the image's edge read
-    // its last row or column and are not stored.
+    // operands) all before their stores.  A tile inside the image whose rows
+    // are aligned (`vec`) moves whole rows of M; at the edges, outputs past
+    // the image read its last row or column and are not stored.
     float v[M * M];
 #pragma unroll
     for (int i = 0; i < M; ++i)
@@ -490,59 +562,113 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
             for (int j = 0; j < A; ++j) s += am[i][j] * Mat<M>::at(jj, j);
             v[i * M + jj] = s;
         }
+    using Row = typename RowOf<M>::type;
+    const int64_t y0 = static_cast<int64_t>(ty) * M, x0 = static_cast<int64_t>(tx) * M;
+    const bool full = y0 + M <= a.oh && x0 + M <= a.ow;
     const auto yy = [&](int e) -> int64_t {
-        const int64_t y = static_cast<int64_t>(ty) * M + e / M;
+        const int64_t y = y0 + e / M;
         return y < a.oh ? y : a.oh - 1;
     };
     const auto xx = [&](int e) -> int64_t {
-        const int64_t x = static_cast<int64_t>(tx) * M + e % M;
+        const int64_t x = x0 + e % M;
         return x < a.ow ? x : a.ow - 1;
     };
+    const auto aligned = [&](const void *p, int64_t nb1, int64_t nb2, int64_t nb3) {
+        return (reinterpret_cast<uintptr_t>(p) % (4 * M)) == 0 && nb1 % M == 0 && nb2 % M == 0 && nb3 % M == 0;
+    };
     float *out = a.y + static_cast<int64_t>(n) * a.ynb3 + static_cast<int64_t>(oc) * a.ynb2;
+    const bool vec = full && aligned(a.y, a.ynb1, a.ynb2, a.ynb3);
     if (a.from_redirect) {
         float r[M * M];
+        if (vec) {
 #pragma unroll
-        for (int e = 0; e < M * M; ++e) r[e] = out[yy(e) * a.ynb1 + xx(e)];
+            for (int i = 0; i < M; ++i) {
+                const Row q = *reinterpret_cast<const Row *>(out + (y0 + i) * a.ynb1 + x0);
+#pragma unroll
+                for (int j = 0; j < M; ++j) r[i * M + j] = q[j];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < M * M; ++e) r[e] = out[yy(e) * a.ynb1 + xx(e)];
+        }
 #pragma unroll
         for (int e = 0; e < M * M; ++e) v[e] = __fadd_rn(r[e], v[e]);
     }
-    apply_chain_block(a.chain, v, [&](int s, int e) {
+#pragma unroll 1
+    for (int s = 0; s < a.chain.count; ++s) {
         const DevStep &st = a.chain.steps[s];
-        const int64_t xy = st.flat01 ? (yy(e) * a.ow + xx(e)) * st.nb[0] : xx(e) * st.nb[0] + yy(e) * st.nb[1];
-        return xy + static_cast<int64_t>(oc) * st.nb[2] + static_cast<int64_t>(n) * st.nb[3];
-    });
+        if (st.kind == 2) {
 #pragma unroll
-    for (int e = 0; e < M * M; ++e) {
-        const int64_t y = static_cast<int64_t>(ty) * M + e / M;
-        const int64_t x = static_cast<int64_t>(tx) * M + e % M;
-        if (y < a.oh && x < a.ow) out[y * a.ynb1 + x] = v[e];
+            for (int e = 0; e < M * M; ++e) v[e] = silu(v[e]);
+            continue;
+        }
+        const float *base = st.operand + static_cast<int64_t>(oc) * st.nb[2] + static_cast<int64_t>(n) * st.nb[3];
+        float o[M * M];
+        if (st.nb[0] == 0 && st.nb[1] == 0) {
+            const float b = *base;
+#pragma unroll
+            for (int e = 0; e < M * M; ++e) o[e] = b;
+        } else if (full && st.nb[0] == 1 && aligned(st.operand, st.nb[1], st.nb[2], st.nb[3])) {
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                const Row q = *reinterpret_cast<const Row *>(base + (y0 + i) * st.nb[1] + x0);
+#pragma unroll
+                for (int j = 0; j < M; ++j) o[i * M + j] = q[j];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < M * M; ++e) o[e] = base[xx(e) * st.nb[0] + yy(e) * st.nb[1]];
+        }
+        if (st.kind == 0) {
+#pragma unroll
+            for (int e = 0; e < M * M; ++e) v[e] = __fadd_rn(v[e], o[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < M * M; ++e) v[e] = __fmul_rn(v[e], o[e]);
+        }
+    }
+    if (vec) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            Row q;
+#pragma unroll
+            for (int j = 0; j < M; ++j) q[j] = v[i * M + j];
+            *reinterpret_cast<Row *>(out + (y0 + i) * a.ynb1 + x0) = q;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < M * M; ++e) {
+            const int64_t y = y0 + e / M;
+            const int64_t x = x0 + e % M;
+            if (y < a.oh && x < a.ow) out[y * a.ynb1 + x] = v[e];
+        }
     }
 }
 
 // ------------------------------------------------------------------ host
 
 struct WorkLayout {
-    int64_t kp, tp;                // IC padded to whole steps of K, tiles to whole chunks of 8
-    size_t e, a, u, v, m, total;  // byte offsets
+    int64_t kp;                          // IC padded to whole steps of K
+    size_t e, a, shift, u, v, m, total;  // byte offsets
 };
 
 WorkLayout work_layout(const WinogradArgs &a) {
     const int64_t alpha2 = (a.m + 2) * (a.m + 2);
     WorkLayout l{};
     l.kp = round_up(a.ic, 32);
-    l.tp = round_up(a.tiles, 8);
     size_t at = 0;
     const auto take = [&](int64_t bytes) {
         const size_t here = at;
         at += static_cast<size_t>(round_up(bytes, 256));
         return here;
     };
-    // Either form: two FP16 planes of the padded sizes, or single precision
-    // of the unpadded ones.
+    // Either form: U as two FP16 planes or in single precision, V in single
+    // precision, [xi][tile][kp] or [xi][ic][tile].
     l.e = take(a.ic * 4);
     l.a = take(a.oc * 4);
+    l.shift = take(a.oc * 4);
     l.u = take(alpha2 * a.oc * l.kp * 4);
-    l.v = take(alpha2 * l.kp * l.tp * 4);
+    l.v = take(alpha2 * l.kp * a.tiles * 4);
     l.m = take(alpha2 * a.oc * a.tiles * 4);
     l.total = at;
     return l;
@@ -556,10 +682,11 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     char *base = static_cast<char *>(work);
     int32_t *e = reinterpret_cast<int32_t *>(base + l.e);
     int32_t *a_oc = reinterpret_cast<int32_t *>(base + l.a);
+    int32_t *shift = reinterpret_cast<int32_t *>(base + l.shift);
     float *u = reinterpret_cast<float *>(base + l.u);
     float *v = reinterpret_cast<float *>(base + l.v);
     float *m = reinterpret_cast<float *>(base + l.m);
-    const std::string names[] = {std::string(tag) + ".exponents", std::string(tag) + ".weights",
+    const std::string names[] = {std::string(tag) + ".scales", std::string(tag) + ".weights",
                                  std::string(tag) + ".inputs", std::string(tag) + ".products",
                                  std::string(tag) + ".outputs"};
     if (tuning().winograd_fp32) {
@@ -585,20 +712,19 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         return launched(hipGetLastError(), "winograd");
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
-    _Float16 *vh = reinterpret_cast<_Float16 *>(v);
     {
         KernelScope scope(names[0].c_str(), stream);
-        hipLaunchKernelGGL((channel_exponent_kernel<M>), dim3(a.ic), dim3(256), 0, stream, a, e);
+        hipLaunchKernelGGL((scales_kernel<M>), dim3(a.ic + a.oc), dim3(kScaleThreads), 0, stream, a, e, a_oc);
     }
     {
         KernelScope scope(names[1].c_str(), stream);
-        hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(a.oc), dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, uh,
-                           a_oc);
+        hipLaunchKernelGGL((weights_split_kernel<M>), dim3(a.oc), dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, a_oc,
+                           uh, shift);
     }
     {
         KernelScope scope(names[2].c_str(), stream);
-        hipLaunchKernelGGL((inputs_scaled_kernel<M>), dim3(ceil_div(a.tiles * l.kp, 256)), dim3(256), 0, stream, a, l.kp,
-                           l.tp, e, vh);
+        hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
+                           stream, a, l.kp, e, v);
     }
     {
         KernelScope scope(names[3].c_str(), stream);
@@ -606,21 +732,19 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         p.a = uh;
         p.a_plane = a.oc * l.kp;
         p.a_batch = 2 * p.a_plane;
-        p.b = vh;
-        p.b_plane = l.kp * l.tp;
-        p.b_batch = 2 * p.b_plane;
-        p.ldb = l.tp;
+        p.b = v;
+        p.b_batch = a.tiles * l.kp;
         p.c = m;
         p.c_batch = a.oc * a.tiles;
         p.M = a.oc;
         p.N = a.tiles;
         p.K = l.kp;
         p.batches = A * A;
-        const hipError_t err = launch_split_batched(p, tuning().gemm_stages, stream);
+        const hipError_t err = launch_split_batched(p, gemm_shape(), stream);
         if (err != hipSuccess) return launched(err, "winograd products");
     }
     KernelScope scope(names[4].c_str(), stream);
-    hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, a_oc);
+    hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, shift);
     return launched(hipGetLastError(), "winograd");
 }
 

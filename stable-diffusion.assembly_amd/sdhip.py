@@ -75,7 +75,8 @@ SIGNATURES = [
     ("sdhip_attention", ctypes.c_int,
      [_T, _T, _T, _T, ctypes.c_float, ctypes.c_float, ctypes.c_float, _P, _SZ, _P]),
     ("sdhip_group_norm_supported", ctypes.c_int, [_T, _T, ctypes.c_int]),
-    ("sdhip_group_norm", ctypes.c_int, [_T, _T, ctypes.c_int, ctypes.c_float, _E, _P]),
+    ("sdhip_group_norm_work_size", _SZ, [_T, _T, ctypes.c_int]),
+    ("sdhip_group_norm", ctypes.c_int, [_T, _T, ctypes.c_int, ctypes.c_float, _E, _P, _SZ, _P]),
     ("sdhip_norm_supported", ctypes.c_int, [_T, _T]),
     ("sdhip_norm", ctypes.c_int, [_T, _T, ctypes.c_float, _E, _P]),
 ]
@@ -238,9 +239,17 @@ def attention(q, k, v, y, scale, work=None):
     return buf
 
 
-def group_norm(x, y, groups, eps, chain=None):
-    check(load().sdhip_group_norm(desc(x), desc(y), groups, eps, ctypes.byref(chain) if chain else None,
-                                  stream_handle()), "group_norm")
+def group_norm(x, y, groups, eps, chain=None, work=None):
+    lib = load()
+    dx, dy = desc(x), desc(y)
+    size = lib.sdhip_group_norm_work_size(dx, dy, groups)
+    buf = work
+    if buf is None:
+        buf, _ = _work(size, x.device)
+    ptr = buf.data_ptr() if buf is not None else None
+    check(lib.sdhip_group_norm(dx, dy, groups, eps, ctypes.byref(chain) if chain else None, ptr, size,
+                               stream_handle()), "group_norm")
+    return buf
 
 
 def norm(x, y, eps, chain=None):

@@ -31,6 +31,7 @@ def chain_ref(y, gamma, beta, silu):
     ((2, 1280, 8, 8), 32, 1e-5, True),     # cfg3a's GroupNorm + SiLU
     ((2, 1280, 32, 32), 32, 1e-5, True),   # cfg3b's
     ((1, 30, 7, 13), 7, 1e-5, False),      # groups of ceil(30/7) = 5 channels, the last of none
+    ((1, 128, 128, 128), 32, 1e-6, True),  # groups of many slices
 ])
 def test_group_norm(gpu, shape, groups, eps, silu):
     r = rng(sum(shape) + groups)
@@ -48,6 +49,27 @@ def test_group_norm(gpu, shape, groups, eps, silu):
     assert np.isfinite(got).all()
     diff = np.abs(got - want).max() / np.abs(want).max()
     print(f"group_norm {shape}/{groups}: {diff:.3g} of the largest")
+    assert diff <= CLOSE
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(2, 64, 32, 32), (1, 30, 7, 13)])
+def test_group_norm_operand_per_position(gpu, shape):
+    """A chain operand that varies along the rows (a residual of the output's
+    shape, and one broadcast over channels): the per-element path."""
+    r = rng(7 + sum(shape))
+    x = uniform(r, shape, 2.0)
+    res = uniform(r, shape, 1.0)
+    rows = uniform(r, (1, 1, shape[2], shape[3]), 1.0)
+    x_d, res_d, rows_d = dev(x, gpu), dev(res, gpu), dev(rows, gpu)
+    y = unwritten(shape, gpu)
+    sdhip.group_norm(x_d, y, 16 if shape[1] % 16 == 0 else 10, 1e-5,
+                     sdhip.epilogue([("add", res_d), ("mul", rows_d)]))
+    torch.cuda.synchronize()
+    want = (orc.group_norm(x, 16 if shape[1] % 16 == 0 else 10, 1e-5) + res) * rows
+    got = y.cpu().numpy()
+    diff = np.abs(got - want).max() / np.abs(want).max()
+    print(f"group_norm per position {shape}: {diff:.3g}")
     assert diff <= CLOSE
 
 
