@@ -86,6 +86,20 @@ def kernel_times(fn, steps):
     return out
 
 
+def profiled_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` in `workload`, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs summarised in profiles/hbm_traffic.md, or
+    None where that table has no such row."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == workload and cells[1] == kernel:
+            return int(cells[4])
+    return None
+
+
 def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupnorm=False, seed=0):
     """The convolution of a configuration with its chain, ready to run."""
     import torch
@@ -286,11 +300,18 @@ def main():
     kt = kernel_times(run, args.steps)
     dominant = max(kt, key=lambda n: kt[n][0] * kt[n][1])
     dom_ms = kt[dominant][0]
-    # The products: 36 GEMMs of OC x IC x tiles, 2 FLOP per multiply-add.
+    # The products: 36 GEMMs of OC x IC x tiles, 2 FLOP per multiply-add,
+    # each product taken as three FP16 MFMA products of its split parts, so
+    # the instruction's peak is the FP16 one and a third of it the ceiling.
     tiles = 2 * 16 * 16
     alg = 2.0 * 36 * 320 * 320 * tiles
-    roof = {"kernel": dominant, "bound": "mfma", "achieved": round(alg / dom_ms / 1e9, 2), "peak": PEAK_FP32_MFMA,
-            "unit": "TFLOP/s", "frac": round(alg / dom_ms / 1e9 / PEAK_FP32_MFMA, 4), "traffic": None,
+    fp32 = sdhip.get_tuning("winograd_fp32") == 1
+    peak = PEAK_FP32_MFMA if fp32 else PEAK_FP16_MFMA
+    roof = {"kernel": dominant, "bound": "mfma", "achieved": round(alg / dom_ms / 1e9, 2), "peak": peak,
+            "unit": "TFLOP/s", "frac": round(alg / dom_ms / 1e9 / peak, 4),
+            "traffic": profiled_traffic("cfg2", dominant),
+            "mfma": "v_mfma_f32_16x16x4_f32" if fp32 else "v_mfma_f32_32x32x16_f16, 3 per product (split FP16)",
+            "effective_peak": peak if fp32 else round(PEAK_FP16_MFMA / 3, 1),
             "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kt.items()}}
     log(f"kernels: {roof['kernels_us']}")
 
