@@ -45,7 +45,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only-main", action="store_true")
     p.add_argument("--workload", default="", help="run one workload alone (cfg1 cfg2 cfg3a cfg3b cfg4_self "
-                                                  "cfg4_cross copy), for a profiler")
+                                                  "cfg4_cross unet copy), for a profiler")
+    p.add_argument("--no-unet", action="store_true", help="leave out the UNet step")
     return p.parse_args()
 
 
@@ -212,6 +213,15 @@ def copy_workload(dev, mib=256):
     return run, 0.0
 
 
+def unet_workload(dev, seed=7):
+    """The synthetic SD1.5 UNet step (unet_step.py) at 512x512, batch 2,
+    captured in a HIP graph."""
+    import unet_step
+
+    model = unet_step.Model(unet_step.Config(), dev, seed=seed)
+    return unet_step.Step(model, unet_step.HipOps(dev), model.inputs(seed=seed + 1))
+
+
 def make_workload(dev, name):
     """(run, FLOPs) of a named workload: the BASELINE.json configurations."""
     if name == "cfg1":
@@ -232,6 +242,9 @@ def make_workload(dev, name):
         return attention_workload(dev, 2, 8, 4096, 77, 40, seed=5)
     if name == "copy":
         return copy_workload(dev)
+    if name == "unet":
+        step = unet_workload(dev)
+        return step.run, step.flops
     raise SystemExit(f"unknown workload {name}")
 
 
@@ -267,6 +280,33 @@ def cpu_baseline(seconds):
     return {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"the whole configs[1] convolution (F(4x4), bias + residual) in single precision, "
                       f"best of {runs - 1} runs after one uncounted, {cores} OpenMP threads"}
+
+
+def unet_step_line(dev, args):
+    """The SD1.5 UNet step in ms: the graph replayed `steps` times after
+    `warmup`; the eager step (the same launches from Python) beside it, and
+    where the kernels' time goes, by the library's kernel profile of one
+    eager step."""
+    import torch
+
+    log("unet step: building the model and capturing the graph ...")
+    step = unet_workload(dev)
+    ms = timed(step.run, max(5, args.steps // 5), max(2, args.warmup // 5))
+    eager_ms = timed(step.eager, 3, 1)
+    kt = kernel_times(step.eager, 1)
+    lib_ms = sum(v[0] * v[1] for v in kt.values())
+    torch.cuda.synchronize()
+    log(f"unet step: {ms:.2f} ms (graph), {eager_ms:.2f} ms eager, library kernels {lib_ms:.2f} ms")
+    return {"ms": round(ms, 3), "tflops": round(step.flops / ms / 1e9, 2),
+            "gflop": round(step.flops / 1e9, 2), "nodes": step.nodes,
+            "gflop_by_class": {k: round(v / 1e9, 2) for k, v in step.by_class.items()},
+            "eager_ms": round(eager_ms, 3), "library_kernels_ms": round(lib_ms, 3),
+            "kernels_ms": {k: round(v[0] * v[1], 3) for k, v in sorted(kt.items(), key=lambda kv: -kv[1][0] * kv[1][1])},
+            "workload": "SD1.5 UNet at 512x512 (latent 64x64), batch 2 (CFG), context 77x768, random weights "
+                        "(FP16 ~N(0,0.02)); the nodes ggml keeps (concat, upsample, permutes, timestep embedding, "
+                        "two-row linears) by torch on the same stream; one HIP graph",
+            "reference_published_ms": {"i7-1360P 12 threads": 3540, "note": "README.md:29-34: 70.8 s for 20 steps; "
+                                       "other hardware, context only"}}
 
 
 def main():
@@ -363,6 +403,8 @@ def main():
         "roofline": roof,
         "configs": configs,
     }
+    if not args.no_unet:
+        line["unet_step"] = unet_step_line(dev, args)
     if not args.no_cpu:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
