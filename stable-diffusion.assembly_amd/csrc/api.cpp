@@ -67,6 +67,7 @@ const Field kFields[] = {
     {"winograd_fp32", &Tuning::winograd_fp32},
     {"gemm_stages", &Tuning::gemm_stages},
     {"gemm_tiles", &Tuning::gemm_tiles},
+    {"attention_generic", &Tuning::attention_generic},
 };
 
 }  // namespace

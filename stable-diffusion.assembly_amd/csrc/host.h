@@ -33,6 +33,10 @@ struct Tuning {
     // This library's own: a product's block of 64 TM x 64 TN as TM TN (11,
     // 21, 22), or 0 to choose by the size.
     int gemm_tiles = 0;
+    // This library's own: attention by its generic form (1) even where the
+    // fast one takes the operands (0), for comparison; results agree within
+    // the same bound.
+    int attention_generic = 0;
 };
 
 Tuning &tuning();

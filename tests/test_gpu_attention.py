@@ -22,6 +22,11 @@ CASES = [
     (13, 37, 29, 4, 2, 3, False),      # edges: no multiple of a tile, heads sharing keys
     (64, 50, 100, 2, 1, 1, True),      # FP16 keys and values
     (64, 988, 988, 2, 2, 1, False),    # SDXL's heads of 64
+    (32, 130, 200, 3, 3, 1, False),    # the fast form's other head sizes, ragged queries and keys
+    (96, 129, 65, 2, 1, 2, False),
+    (128, 70, 300, 2, 2, 1, False),
+    (64, 257, 1000, 4, 2, 1, False),   # heads sharing keys in the fast form
+    (40, 1, 1, 1, 1, 1, False),        # one query, one key
 ]
 
 
@@ -85,3 +90,19 @@ def test_attention_not_taken(gpu):
     with pytest.raises(sdhip.SdhipError) as e:
         sdhip.attention(q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), y, 0.05)
     assert e.value.status == sdhip.UNSUPPORTED
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [c for c in CASES if not c[6] and c[0] in (40, 64, 80)], ids=lambda c: "x".join(map(str, c)))
+def test_attention_generic_form(gpu, c):
+    """The generic kernel (attention_generic=1) on the cases the fast one
+    takes, so that both stay checked."""
+    sdhip.set_tuning("attention_generic=1")
+    try:
+        q, k, v, y, scale = attention_case(gpu, *c, seed=c[0] + 11)
+    finally:
+        sdhip.set_tuning("")
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    print(f"attention generic {c}: {err:.3g}")
+    assert err <= BOUND
