@@ -426,3 +426,87 @@ void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t
     if (!woffset) free(ob);
     if (!wsums) free(qs);
 }
+
+/* attention.cc:612-824 (compute_quantized), with the quantizers above:
+ * over_dims (the keys and queries: one group of 4 ceil(d / 4) over the
+ * dimensions, attention.cc:632-637) and over_keys (the values and
+ * exponentials: groups of `group` keys, 639-643); key_block the stretch of
+ * the exponentials, a multiple of the group (663-664). */
+void oracle_quantized_attention(const float *q, const float *k, const float *v, int64_t d, int64_t dv, int64_t lq,
+                                int64_t lk, int64_t h, int64_t hk, int64_t b, float scale, int64_t group,
+                                int input_levels, int weight_max, int64_t key_block, float *y) {
+    const int64_t gd = (d + 3) / 4 * 4;
+    const int64_t groups = (lk + group - 1) / group;
+    int8_t *kq = (int8_t *)malloc((size_t)(lk * gd));
+    float *ks = (float *)malloc((size_t)lk * sizeof(float)), *ko = (float *)malloc((size_t)lk * sizeof(float));
+    int32_t *ksum = (int32_t *)malloc((size_t)lk * sizeof(int32_t));
+    float *vt = (float *)malloc((size_t)(dv * lk) * sizeof(float));
+    int8_t *vq = (int8_t *)malloc((size_t)(dv * groups * group));
+    float *vs = (float *)malloc((size_t)(dv * groups) * sizeof(float));
+    float *vo = (float *)malloc((size_t)(dv * groups) * sizeof(float));
+    int32_t *vsum = (int32_t *)malloc((size_t)(dv * groups) * sizeof(int32_t));
+    float *krow = (float *)malloc((size_t)(lk * d) * sizeof(float));
+    float *scores = (float *)malloc((size_t)lk * sizeof(float));
+    uint8_t *qq = (uint8_t *)malloc((size_t)gd);
+    uint8_t *eq = (uint8_t *)malloc((size_t)group);
+    float *t = (float *)malloc((size_t)dv * sizeof(float));
+    for (int64_t bi = 0; bi < b; ++bi) {
+        for (int64_t kh = 0; kh < hk; ++kh) {
+            /* The head's keys, rows of d, and its values by dimension. */
+            for (int64_t j = 0; j < lk; ++j)
+                for (int64_t e = 0; e < d; ++e) krow[j * d + e] = k[((bi * lk + j) * hk + kh) * d + e];
+            for (int64_t c = 0; c < dv; ++c)
+                for (int64_t j = 0; j < lk; ++j) vt[c * lk + j] = v[((bi * lk + j) * hk + kh) * dv + c];
+            oracle_quantize_weights(krow, d, lk, d, gd, weight_max, 1, kq, ks, ko, ksum);
+            oracle_quantize_weights(vt, lk, dv, lk, group, weight_max, 1, vq, vs, vo, vsum);
+            for (int64_t hh = 0; hh < h; ++hh) {
+                if (hh / (h / hk) != kh) continue;
+                for (int64_t i = 0; i < lq; ++i) {
+                    const float *qrow = q + ((bi * lq + i) * h + hh) * d;
+                    float qs, qo;
+                    oracle_quantize_input_row(qrow, d, gd, input_levels, qq, &qs, &qo);
+                    qs = qs * scale; /* attention.cc:754-764 */
+                    qo = qo * scale;
+                    float top = -INFINITY;
+                    for (int64_t j = 0; j < lk; ++j) {
+                        int32_t s = 0;
+                        for (int64_t e = 0; e < gd; ++e) s += (int32_t)kq[j * gd + e] * (int32_t)qq[e];
+                        float x = fmaf(ks[j] * qs, (float)s, 0.0f);
+                        x = fmaf(-ko[j], qo, x);
+                        scores[j] = x;
+                        top = fmaxf(top, x);
+                    }
+                    double total = 0.0;
+                    for (int64_t c = 0; c < dv; ++c) t[c] = 0.0f;
+                    for (int64_t j0 = 0; j0 < lk; j0 += key_block) {
+                        const int64_t j1 = j0 + key_block < lk ? j0 + key_block : lk;
+                        const int64_t whole = j0 + (j1 - j0) / 8 * 8;
+                        for (int64_t j = j0; j < j1; ++j) {
+                            const float e = j < whole ? oracle_exponential(scores[j] - top) : expf(scores[j] - top);
+                            scores[j] = e;
+                            total += (double)e;
+                        }
+                        for (int64_t g0 = j0; g0 < j1; g0 += group) {
+                            const int64_t n = j1 - g0 < group ? j1 - g0 : group;
+                            float es, eo;
+                            oracle_quantize_input_row(scores + g0, n, group, input_levels, eq, &es, &eo);
+                            const int64_t g = g0 / group;
+                            for (int64_t c = 0; c < dv; ++c) {
+                                int32_t s = 0;
+                                const int8_t *row = vq + (c * groups + g) * group;
+                                for (int64_t e = 0; e < group; ++e) s += (int32_t)row[e] * (int32_t)eq[e];
+                                t[c] = fmaf(vs[c * groups + g] * es, (float)s, t[c]);
+                                t[c] = fmaf(-vo[c * groups + g], eo, t[c]);
+                            }
+                        }
+                    }
+                    const float reciprocal = (float)(1.0 / total);
+                    float *out = y + ((bi * lq + i) * h + hh) * dv;
+                    for (int64_t c = 0; c < dv; ++c) out[c] = t[c] * reciprocal;
+                }
+            }
+        }
+    }
+    free(kq); free(ks); free(ko); free(ksum); free(vt); free(vq); free(vs); free(vo); free(vsum);
+    free(krow); free(scores); free(qq); free(eq); free(t);
+}

@@ -111,6 +111,20 @@ void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t
                               uint8_t *xq, float *xscale, float *xoffset, int8_t *wq, float *wscale, float *woffset,
                               int32_t *wsums);
 
+/* Self-attention with quantized products (attention.cc:612-824): keys
+ * signed, one group over the head's d dimensions (group 4 ceil(d / 4)),
+ * queries unsigned with a zero point likewise, the softmax scale folded into
+ * their scales and offsets; the scores' maximum per query; then stretches of
+ * key_block keys: the exponentials of the stretch (exponential() for its
+ * multiples of 8 keys, expf for the rest, attention.cc:288-301), their sum in
+ * double in key order, each query's quantized unsigned per `group` keys; the
+ * values signed per (dimension, group of keys); the output summed group by
+ * group as quant.cc:150-155 does and multiplied by float(1 / sum).
+ * q [b][lq][h][d], k [b][lk][hk][d], v [b][lk][hk][dv]; y [b][lq][h][dv]. */
+void oracle_quantized_attention(const float *q, const float *k, const float *v, int64_t d, int64_t dv, int64_t lq,
+                                int64_t lk, int64_t h, int64_t hk, int64_t b, float scale, int64_t group,
+                                int input_levels, int weight_max, int64_t key_block, float *y);
+
 /* ---- CPU-baseline restatements (port.c), threads OpenMP threads */
 
 /* Winograd F(4x4, 3x3) of winograd.cc:1548-1613 with bias and residual:

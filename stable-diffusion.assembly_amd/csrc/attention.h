@@ -27,6 +27,37 @@ struct AttentionArgs {
 // The most dimensions of a head the kernel takes (queries, keys and values).
 constexpr int64_t kAttentionMaxDims = 256;
 
+// The bits mode of self-attention (qattention.hip): the operands, the
+// quantization (levels, wmax, group), the stretch of keys of the
+// exponentials, and the work buffer's parts, set by qattention_layout.
+struct QAttentionArgs {
+    const float *q;
+    int64_t qnb1, qnb2, qnb3;
+    const void *k;
+    int64_t knb1, knb2, knb3;
+    const void *v;
+    int64_t vnb1, vnb2, vnb3;
+    float *y;
+    int64_t ynb1, ynb2, ynb3;
+    int64_t d, dv, lq, lk, h, hk, b;
+    float scale;
+    int32_t khalf, vhalf;
+    int32_t levels, wmax;
+    int64_t group, key_block;
+    // Set by qattention_layout.
+    int64_t gd, sd, lkp, lqp, groups, slot, dvp, tail_from, qblocks;
+    int8_t *kq, *vq, *qq;
+    float *ks, *ko, *vs, *vo, *qs, *qo;
+    int32_t *ksum, *vsum;
+};
+
+struct QAttentionLayout {
+    size_t kq, ks, ko, ksum, vq, vs, vo, vsum, qq, qs, qo, total;
+};
+
+QAttentionLayout qattention_layout(QAttentionArgs &a);
+hipError_t launch_quantized_attention(QAttentionArgs a, void *work, hipStream_t stream);
+
 size_t attention_lds_bytes(int64_t d, int64_t dv);
 hipError_t launch_attention(AttentionArgs a, hipStream_t stream);
 

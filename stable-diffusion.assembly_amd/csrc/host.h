@@ -37,6 +37,9 @@ struct Tuning {
     // fast one takes the operands (0), for comparison; results agree within
     // the same bound.
     int attention_generic = 0;
+    // The keys of a stretch of attention's second product (kernels.h:107):
+    // with bits, it sets where the exponentials switch to std::exp.
+    int attention_keys = 256;
 };
 
 Tuning &tuning();

@@ -14,6 +14,58 @@ namespace {
 
 bool kv_type(const sdhip_tensor *t) { return holds_f32(t) || holds_f16(t); }
 
+// Whether the attention is computed with quantized products
+// (quantized_attention, attention.cc:622-624): bits asks for attention, and
+// there are kQuantizedKeys keys and more.
+bool quantized_attention(const sdhip_tensor *k) {
+    const Tuning &t = tuning();
+    return t.bits >= 2 && t.bits <= 8 && (t.quantize & 4) != 0 && k->ne[1] >= 256;
+}
+
+QAttentionArgs qargs_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v, const sdhip_tensor *y,
+                        float scale) {
+    const Tuning &t = tuning();
+    QAttentionArgs a{};
+    a.q = static_cast<const float *>(q->data);
+    a.qnb1 = q->nb[1] / 4;
+    a.qnb2 = q->nb[2] / 4;
+    a.qnb3 = q->nb[3] / 4;
+    a.k = k->data;
+    a.khalf = k->type == SDHIP_TYPE_F16;
+    a.knb1 = k->nb[1] / k->nb[0];
+    a.knb2 = k->nb[2] / k->nb[0];
+    a.knb3 = k->nb[3] / k->nb[0];
+    a.v = v->data;
+    a.vhalf = v->type == SDHIP_TYPE_F16;
+    a.vnb1 = v->nb[1] / v->nb[0];
+    a.vnb2 = v->nb[2] / v->nb[0];
+    a.vnb3 = v->nb[3] / v->nb[0];
+    a.y = static_cast<float *>(y->data);
+    a.ynb1 = y->nb[1] / 4;
+    a.ynb2 = y->nb[2] / 4;
+    a.ynb3 = y->nb[3] / 4;
+    a.d = q->ne[0];
+    a.dv = v->ne[0];
+    a.lq = q->ne[1];
+    a.lk = k->ne[1];
+    a.h = q->ne[2];
+    a.hk = k->ne[2];
+    a.b = q->ne[3];
+    a.scale = scale;
+    // quant() and over_keys() (quant.cc:59-67; attention.cc:639-643).
+    int quads = t.group / 4;
+    quads = quads < 1 ? 1 : (quads > 256 ? 256 : quads);
+    a.group = 4 * quads;
+    const int ib = t.input_bits < 2 ? 2 : (t.input_bits > 8 ? 8 : t.input_bits);
+    const int wb = t.bits < 2 ? 2 : (t.bits > 8 ? 8 : t.bits);
+    a.levels = (1 << ib) - 1;
+    a.wmax = (1 << (wb - 1)) - 1;
+    // The stretch of the exponentials (attention.cc:154, 663-664).
+    const int64_t keys = t.attention_keys / 8 * 8 > 8 ? t.attention_keys / 8 * 8 : 8;
+    a.key_block = keys / a.group * a.group > a.group ? keys / a.group * a.group : a.group;
+    return a;
+}
+
 }  // namespace
 
 extern "C" {
@@ -35,16 +87,32 @@ int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, cons
            v->nb[2] % v->nb[0] == 0 && v->nb[3] % v->nb[0] == 0;
 }
 
-size_t sdhip_attention_work_size(const sdhip_tensor *, const sdhip_tensor *, const sdhip_tensor *,
-                                 const sdhip_tensor *) {
-    return 0;
+size_t sdhip_attention_work_size(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                                 const sdhip_tensor *y) {
+    if (!sdhip_attention_supported(q, k, v, y, 0.0f, 0.0f) || !quantized_attention(k)) return 0;
+    QAttentionArgs a = qargs_of(q, k, v, y, 1.0f);
+    return qattention_layout(a).total;
 }
 
 sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
-                             const sdhip_tensor *y, float scale, float max_bias, float softcap, void *, size_t,
-                             void *stream) {
+                             const sdhip_tensor *y, float scale, float max_bias, float softcap, void *work,
+                             size_t work_size, void *stream) {
     if (!sdhip_attention_supported(q, k, v, y, max_bias, softcap)) {
         return fail(SDHIP_UNSUPPORTED, "attention: operands not taken");
+    }
+    if (quantized_attention(k)) {
+        QAttentionArgs qa = qargs_of(q, k, v, y, scale);
+        if (qa.group % 16 != 0 || qa.group > 256) {
+            return fail(SDHIP_UNSUPPORTED, "attention: quantized groups of %lld keys (a multiple of 16 up to 256 "
+                                           "is taken)", static_cast<long long>(qa.group));
+        }
+        const size_t need = qattention_layout(qa).total;
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "attention: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        if (qa.lq == 0 || qa.h == 0 || qa.b == 0) return SDHIP_OK;
+        return launched(launch_quantized_attention(qa, work, static_cast<hipStream_t>(stream)),
+                        "quantized attention");
     }
     AttentionArgs a{};
     a.q = static_cast<const float *>(q->data);

@@ -1,0 +1,494 @@
+// Self-attention with quantized products, the bits mode of FLASH_ATTN_EXT
+// (attention.cc:597-824), on gfx950's integer MFMA, v_mfma_i32_16x16x64_i8.
+//
+// Quantization, bit for bit as the reference's C++ form does it (quant.cc):
+//   keys, signed, one group over the head's dimensions (over_dims,
+//     attention.cc:632-637: 4 ceil(d / 4) numbers): s = max |k| / wmax,
+//     q = clamp(rint(k / s), -wmax, wmax), offset = s * sum(q);
+//   queries, unsigned with a zero point, one group likewise; their scale and
+//     offset then multiplied by the softmax's scale (attention.cc:754-764);
+//   values, signed, per (dimension, group of keys) (over_keys, 639-643);
+//   exponentials, unsigned with a zero point, per (query, group of keys).
+// The scores are the quantized products scaled back as quant.cc:150-155 does,
+// t = fma(sa sb, S, 0), t = fma(-oa, ob, t); their maximum per query over
+// every key (the first pass); then, group by group in key order (the second
+// pass), the scores again (the same integers and roundings), their
+// exponentials exp(s - max) -- Cephes' form (scalar_math.h:34-51), and for
+// the keys past the last multiple of 8 of the last stretch of key_block keys,
+// the correctly rounded exp the reference's std::exp gives (attention.cc:288-
+// 301) -- summed in double, quantized, and the group's product with the
+// values added to the output, t = fma(sa sb, S, t), t = fma(-oa, ob, t).  The
+// output is t * float(1 / sum).
+//
+// The MFMA multiplies signed bytes: the unsigned operands (queries,
+// exponentials) are stored as q - 128 and the integer sums restored exactly
+// as S = sum((q - 128) w) + 128 sum(w), sum(w) the signed operand's integer
+// sum over the group.
+//
+// A workgroup of 4 waves takes 64 queries of one head, a wave 16.  The
+// scores are computed transposed, keys by queries: lane (query lr, lg) holds
+// keys 16 kt + 4 lg + r of each tile of 16.  The exponentials' bytes of a
+// group are then already where the product with the values wants them, as
+// operand B of 64 keys: lane lg's 16 bytes are positions 16 lg + 4 kt + r --
+// the values' bytes are stored in that order (position p = 64 c + 16 kg +
+// 4 kt + r holds key 64 c + 16 kt + 4 kg + r of the group).
+
+#include "attention.h"
+#include "host.h"
+#include "profile.h"
+
+namespace sdhip {
+
+namespace {
+
+__device__ __forceinline__ float qa_clamp(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+__device__ __forceinline__ float qa_wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float qa_wave_min(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ int qa_wave_sum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float load_num(const void *p, int64_t at, bool half) {
+    if (half) return static_cast<float>(static_cast<const _Float16 *>(p)[at]);
+    return static_cast<const float *>(p)[at];
+}
+
+// ------------------------------------------------------------------ keys
+
+// One wave per (image, key head, key): the key's bytes over its sd slot (zeros
+// past d), its scale, offset and integer sum.  Keys from lk to lkp: zeros.
+__global__ __launch_bounds__(256) void qa_keys_kernel(QAttentionArgs a) {
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= a.b * a.hk * a.lkp) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t j = item % a.lkp;
+    const int64_t head = item / a.lkp;  // bi * hk + kh
+    const int64_t bi = head / a.hk, kh = head % a.hk;
+    const bool valid = j < a.lk;
+    const int64_t base = bi * a.knb3 + kh * a.knb2 + (valid ? j : 0) * a.knb1;
+    float m = 0.0f;
+    for (int64_t e = lane; e < a.d; e += 64) m = fmaxf(m, valid ? fabsf(load_num(a.k, base + e, a.khalf)) : 0.0f);
+    m = qa_wave_max(m);
+    const float wmax = static_cast<float>(a.wmax);
+    const float s = __fdiv_rn(m, wmax);
+    const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+    int sum = 0;
+    int8_t *dst = a.kq + item * a.sd;
+    for (int64_t e = lane; e < a.sd; e += 64) {
+        int q = 0;
+        if (valid && e < a.d) {
+            q = static_cast<int>(qa_clamp(rintf(__fmul_rn(load_num(a.k, base + e, a.khalf), inverse)), -wmax, wmax));
+        }
+        dst[e] = static_cast<int8_t>(q);
+        sum += q;
+    }
+    sum = qa_wave_sum(sum);
+    if (lane == 0) {
+        a.ks[item] = s;
+        a.ko[item] = __fmul_rn(s, static_cast<float>(sum));
+        a.ksum[item] = sum;
+    }
+}
+
+// ------------------------------------------------------------------ values
+
+// One wave per (image, key head, group of keys, dimension): the group's bytes
+// in the order of operand A (above), its scale, offset and integer sum,
+// stored [head][group][dvp].  Keys past lk and dimensions past dv: zeros.
+__global__ __launch_bounds__(256) void qa_values_kernel(QAttentionArgs a) {
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= a.b * a.hk * a.groups * a.dvp) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t c = item % a.dvp;
+    const int64_t rest = item / a.dvp;
+    const int64_t g = rest % a.groups;
+    const int64_t head = rest / a.groups;
+    const int64_t bi = head / a.hk, kh = head % a.hk;
+    const int64_t base = bi * a.vnb3 + kh * a.vnb2 + c;
+    // Position p of the slot holds key w of the group (or nothing).
+    const auto key_of = [&](int64_t p) -> int64_t {
+        const int64_t chunk = p >> 6, kg = (p >> 4) & 3, kt = (p >> 2) & 3, r = p & 3;
+        return 64 * chunk + 16 * kt + 4 * kg + r;
+    };
+    const auto value_at = [&](int64_t w) -> float {
+        const int64_t key = g * a.group + w;
+        return (w < a.group && key < a.lk && c < a.dv) ? load_num(a.v, base + key * a.vnb1, a.vhalf) : 0.0f;
+    };
+    float m = 0.0f;
+    for (int64_t p = lane; p < a.slot; p += 64) m = fmaxf(m, fabsf(value_at(key_of(p))));
+    m = qa_wave_max(m);
+    const float wmax = static_cast<float>(a.wmax);
+    const float s = __fdiv_rn(m, wmax);
+    const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+    int sum = 0;
+    int8_t *dst = a.vq + ((head * a.dvp + c) * a.groups + g) * a.slot;
+    for (int64_t p = lane; p < a.slot; p += 64) {
+        const int q = static_cast<int>(qa_clamp(rintf(__fmul_rn(value_at(key_of(p)), inverse)), -wmax, wmax));
+        dst[p] = static_cast<int8_t>(q);
+        sum += q;
+    }
+    sum = qa_wave_sum(sum);
+    if (lane == 0) {
+        const int64_t at = (head * a.groups + g) * a.dvp + c;
+        a.vs[at] = s;
+        a.vo[at] = __fmul_rn(s, static_cast<float>(sum));
+        a.vsum[at] = sum;
+    }
+}
+
+// ------------------------------------------------------------------ queries
+
+// One wave per (image, head, query): the query's bytes as q - 128 over its sd
+// slot (the group's tail past d its zero point, the slot past the group 0:
+// the keys' bytes there are 0), its scale and offset times the softmax's
+// scale.  Queries from lq to lqp: zeros.
+__global__ __launch_bounds__(256) void qa_queries_kernel(QAttentionArgs a) {
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= a.b * a.h * a.lqp) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t i = item % a.lqp;
+    const int64_t head = item / a.lqp;  // bi * h + hh
+    const int64_t bi = head / a.h, hh = head % a.h;
+    const bool valid = i < a.lq;
+    const float *row = a.q + bi * a.qnb3 + hh * a.qnb2 + (valid ? i : 0) * a.qnb1;
+    float lo = 0.0f, hi = 0.0f;
+    for (int64_t e = lane; e < a.d; e += 64) {
+        const float x = valid ? row[e] : 0.0f;
+        lo = fminf(lo, x);
+        hi = fmaxf(hi, x);
+    }
+    lo = qa_wave_min(lo);
+    hi = qa_wave_max(hi);
+    const float levels = static_cast<float>(a.levels);
+    const float s = __fdiv_rn(__fsub_rn(hi, lo), levels);
+    const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+    const float zero = rintf(__fmul_rn(-lo, inverse));
+    int8_t *dst = a.qq + item * a.sd;
+    for (int64_t e = lane; e < a.sd; e += 64) {
+        float q = 128.0f;
+        if (e < a.d) {
+            q = qa_clamp(__fadd_rn(rintf(__fmul_rn(valid ? row[e] : 0.0f, inverse)), zero), 0.0f, levels);
+        } else if (e < a.gd) {
+            q = zero;
+        }
+        dst[e] = static_cast<int8_t>(static_cast<int>(q) - 128);
+    }
+    if (lane == 0) {
+        a.qs[item] = __fmul_rn(s, a.scale);
+        a.qo[item] = __fmul_rn(__fmul_rn(s, zero), a.scale);
+    }
+}
+
+// ------------------------------------------------------------------ attention
+
+// The most 16-byte steps of the scores' k (sd <= 256), of 16-key tiles of a
+// group (group <= 256), and of 16-dimension tiles of the output (dv <= 256).
+constexpr int kQaSteps = 4;
+constexpr int kQaTiles = 16;
+
+// The scores of key tile kt (keys 16 kt + 4 lg + r) for the lane's query:
+// the integer products over the sd bytes, restored, and scaled back.
+template <int SUBS>
+__device__ __forceinline__ float4v qa_scores(const QAttentionArgs &a, const int8_t *kq, const float *ks,
+                                             const float *ko, const int32_t *ksum, const int4v (&qb)[kQaSteps],
+                                             float qs, float qo, int64_t kt, int lr, int lg) {
+    int4v acc = int4v{};
+    const int8_t *krow = kq + (16 * kt + lr) * a.sd + 16 * lg;
+#pragma unroll
+    for (int sub = 0; sub < SUBS; ++sub) {
+        const int4v av = *reinterpret_cast<const int4v *>(krow + 64 * sub);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qb[sub], acc, 0, 0, 0);
+    }
+    const int64_t j = 16 * kt + 4 * lg;
+    const float4v s4 = *reinterpret_cast<const float4v *>(ks + j);
+    const float4v o4 = *reinterpret_cast<const float4v *>(ko + j);
+    const int4v n4 = *reinterpret_cast<const int4v *>(ksum + j);
+    float4v out;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float sum = static_cast<float>(acc[r] + 128 * n4[r]);
+        float t = __builtin_fmaf(__fmul_rn(s4[r], qs), sum, 0.0f);
+        out[r] = __builtin_fmaf(-o4[r], qo, t);
+    }
+    return out;
+}
+
+template <int SUBS, int NDV, int GT>
+__global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+
+    const uint32_t blk = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t qb_ = blk % static_cast<uint32_t>(a.qblocks);
+    const uint32_t bh = blk / static_cast<uint32_t>(a.qblocks);
+    const int64_t hh = bh % a.h;
+    const int64_t bi = bh / a.h;
+    const int64_t kh = hh / (a.h / a.hk);
+    const int64_t head_k = bi * a.hk + kh;
+    const int64_t i0 = static_cast<int64_t>(qb_) * 64 + wave * 16;  // the wave's first query
+    const int64_t qrow = (bi * a.h + hh) * a.lqp + i0 + lr;        // the lane's query, in qq / qs / qo
+
+    // Operand B of the scores: the lane's query, bytes 64 sub + 16 lg.
+    int4v qbv[kQaSteps];
+#pragma unroll
+    for (int sub = 0; sub < kQaSteps; ++sub)
+        qbv[sub] = sub < SUBS ? *reinterpret_cast<const int4v *>(a.qq + qrow * a.sd + 64 * sub + 16 * lg) : int4v{};
+    const float qs = a.qs[qrow], qo = a.qo[qrow];
+
+    const int8_t *kq = a.kq + head_k * a.lkp * a.sd;
+    const float *ks = a.ks + head_k * a.lkp;
+    const float *ko = a.ko + head_k * a.lkp;
+    const int32_t *ksum = a.ksum + head_k * a.lkp;
+
+    // First pass: the greatest score of each query over the keys.
+    float top = -INFINITY;
+    for (int64_t kt = 0; kt < a.lkp / 16; ++kt) {
+        const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, kt, lr, lg);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (16 * kt + 4 * lg + r < a.lk) top = fmaxf(top, sc[r]);
+    }
+    top = fmaxf(top, __shfl_xor(top, 16, 64));
+    top = fmaxf(top, __shfl_xor(top, 32, 64));
+
+    // Second pass, group by group.  NDV is the most tiles of 16 dimensions
+    // the instance takes; ndv those the values have.
+    const int ndv = static_cast<int>(a.dvp / 16);
+    float t[NDV][4];
+#pragma unroll
+    for (int c = 0; c < NDV; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[c][r] = 0.0f;
+    double total = 0.0;
+    const float levels = static_cast<float>(a.levels);
+    const int8_t *vq = a.vq + head_k * a.dvp * a.groups * a.slot;
+    const float *vs = a.vs + head_k * a.groups * a.dvp;
+    const float *vo = a.vo + head_k * a.groups * a.dvp;
+    const int32_t *vsum = a.vsum + head_k * a.groups * a.dvp;
+    for (int64_t g = 0; g < a.groups; ++g) {
+        // The group's exponentials: tile kt of the group, keys 16 kt + 4 lg + r.
+        float e[GT][4];
+        float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < GT; ++kt) {
+            const int64_t j0 = g * a.group + 16 * kt;  // the tile's first key
+            if (16 * kt >= a.group || j0 >= a.lk) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e[kt][r] = 0.0f;
+                continue;
+            }
+            const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, j0 / 16, lr, lg);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t j = j0 + 4 * lg + r;
+                float x = 0.0f;
+                if (j < a.lk) {
+                    const float arg = __fsub_rn(sc[r], top);
+                    x = j < a.tail_from ? cephes_exp(arg) : static_cast<float>(exp(static_cast<double>(arg)));
+                    total += static_cast<double>(x);
+                    lo = fminf(lo, x);
+                    hi = fmaxf(hi, x);
+                }
+                e[kt][r] = x;
+            }
+        }
+        lo = fminf(lo, __shfl_xor(lo, 16, 64));
+        lo = fminf(lo, __shfl_xor(lo, 32, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, 16, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, 32, 64));
+        const float es = __fdiv_rn(__fsub_rn(hi, lo), levels);
+        const float inverse = es > 0.0f ? __fdiv_rn(1.0f, es) : 0.0f;
+        const float zero = rintf(__fmul_rn(-lo, inverse));
+        const float eo = __fmul_rn(es, zero);
+
+        // The group's product with the values, 64 keys (four tiles) at a time,
+        // over the group's slot.
+        int4v acc[NDV];
+#pragma unroll
+        for (int c = 0; c < NDV; ++c) acc[c] = int4v{};
+#pragma unroll
+        for (int chunk = 0; chunk < (GT + 3) / 4; ++chunk) {
+            if (64 * chunk >= a.slot) continue;
+            int4v bv;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kt = 4 * chunk + w;
+                    float q = 0.0f;
+                    if (kt < GT) q = qa_clamp(__fadd_rn(rintf(__fmul_rn(e[kt][r], inverse)), zero), 0.0f, levels);
+                    const uint32_t byte = static_cast<uint32_t>(static_cast<int>(q) - 128) & 0xffu;
+                    word |= byte << (8 * r);
+                }
+                bv[w] = static_cast<int>(word);
+            }
+            // Tiles of the group past its keys: positions with no key, whose
+            // values' bytes are 0; the -128 there multiplies them.
+#pragma unroll
+            for (int c = 0; c < NDV; ++c) {
+                if (c >= ndv) continue;
+                const int4v av = *reinterpret_cast<const int4v *>(
+                    vq + ((16 * c + lr) * a.groups + g) * a.slot + 64 * chunk + 16 * lg);
+                acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[c], 0, 0, 0);
+            }
+        }
+        // Scaled back into the output, dimensions 16 c + 4 lg + r.
+#pragma unroll
+        for (int c = 0; c < NDV; ++c) {
+            if (c >= ndv) continue;
+            const int64_t at = g * a.dvp + 16 * c + 4 * lg;
+            const float4v s4 = *reinterpret_cast<const float4v *>(vs + at);
+            const float4v o4 = *reinterpret_cast<const float4v *>(vo + at);
+            const int4v n4 = *reinterpret_cast<const int4v *>(vsum + at);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float sum = static_cast<float>(acc[c][r] + 128 * n4[r]);
+                t[c][r] = __builtin_fmaf(__fmul_rn(s4[r], es), sum, t[c][r]);
+                t[c][r] = __builtin_fmaf(-o4[r], eo, t[c][r]);
+            }
+        }
+    }
+
+    total += __shfl_xor(total, 16, 64);
+    total += __shfl_xor(total, 32, 64);
+    const float reciprocal = static_cast<float>(1.0 / total);
+    const int64_t i = i0 + lr;
+    if (i >= a.lq) return;
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hh * a.ynb1;
+#pragma unroll
+    for (int c = 0; c < NDV; ++c) {
+        if (c >= ndv) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t dim = 16 * c + 4 * lg + r;
+            if (dim < a.dv) out[dim] = __fmul_rn(t[c][r], reciprocal);
+        }
+    }
+}
+
+template <int SUBS, int NDV>
+hipError_t launch_qa_gt(const QAttentionArgs &a, hipStream_t stream, dim3 grid) {
+    const int gt = static_cast<int>(a.group / 16);
+    if (gt <= 4) {
+        hipLaunchKernelGGL((qa_attention_kernel<SUBS, NDV, 4>), grid, dim3(256), 0, stream, a);
+    } else if (gt <= 8) {
+        hipLaunchKernelGGL((qa_attention_kernel<SUBS, NDV, 8>), grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((qa_attention_kernel<SUBS, NDV, 16>), grid, dim3(256), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+template <int SUBS>
+hipError_t launch_qa_ndv(const QAttentionArgs &a, hipStream_t stream, dim3 grid) {
+    switch (a.dvp / 16) {
+    case 1: return launch_qa_gt<SUBS, 1>(a, stream, grid);
+    case 2: return launch_qa_gt<SUBS, 2>(a, stream, grid);
+    case 3: return launch_qa_gt<SUBS, 3>(a, stream, grid);
+    case 4: return launch_qa_gt<SUBS, 4>(a, stream, grid);
+    case 5: return launch_qa_gt<SUBS, 5>(a, stream, grid);
+    case 6:
+    case 7:
+    case 8: return launch_qa_gt<SUBS, 8>(a, stream, grid);
+    case 9:
+    case 10: return launch_qa_gt<SUBS, 10>(a, stream, grid);
+    default: return launch_qa_gt<SUBS, 16>(a, stream, grid);
+    }
+}
+
+}  // namespace
+
+QAttentionLayout qattention_layout(QAttentionArgs &a) {
+    a.gd = round_up(a.d, 4);
+    a.sd = round_up(a.gd, 64);
+    a.lkp = round_up(a.lk, 16);
+    a.lqp = round_up(a.lq, 64);
+    a.groups = ceil_div(a.lk, a.group);
+    a.slot = round_up(a.group, 64);
+    a.dvp = round_up(a.dv, 16);
+    // Stretches of key_block keys (attention.cc:663-664); the keys past the
+    // last multiple of 8 of the last one take std::exp (attention.cc:288-301).
+    const int64_t last = (a.lk - 1) / a.key_block * a.key_block;
+    a.tail_from = last + (a.lk - last) / 8 * 8;
+    a.qblocks = ceil_div(a.lq, 64);
+    QAttentionLayout l{};
+    size_t at = 0;
+    const auto take = [&](int64_t bytes) {
+        const size_t here = at;
+        at += static_cast<size_t>(round_up(bytes, 256));
+        return here;
+    };
+    const int64_t heads_k = a.b * a.hk, heads = a.b * a.h;
+    l.kq = take(heads_k * a.lkp * a.sd);
+    l.ks = take(heads_k * a.lkp * 4);
+    l.ko = take(heads_k * a.lkp * 4);
+    l.ksum = take(heads_k * a.lkp * 4);
+    l.vq = take(heads_k * a.dvp * a.groups * a.slot);
+    l.vs = take(heads_k * a.groups * a.dvp * 4);
+    l.vo = take(heads_k * a.groups * a.dvp * 4);
+    l.vsum = take(heads_k * a.groups * a.dvp * 4);
+    l.qq = take(heads * a.lqp * a.sd);
+    l.qs = take(heads * a.lqp * 4);
+    l.qo = take(heads * a.lqp * 4);
+    l.total = at;
+    return l;
+}
+
+hipError_t launch_quantized_attention(QAttentionArgs a, void *work, hipStream_t stream) {
+    const QAttentionLayout l = qattention_layout(a);
+    char *base = static_cast<char *>(work);
+    a.kq = reinterpret_cast<int8_t *>(base + l.kq);
+    a.ks = reinterpret_cast<float *>(base + l.ks);
+    a.ko = reinterpret_cast<float *>(base + l.ko);
+    a.ksum = reinterpret_cast<int32_t *>(base + l.ksum);
+    a.vq = reinterpret_cast<int8_t *>(base + l.vq);
+    a.vs = reinterpret_cast<float *>(base + l.vs);
+    a.vo = reinterpret_cast<float *>(base + l.vo);
+    a.vsum = reinterpret_cast<int32_t *>(base + l.vsum);
+    a.qq = reinterpret_cast<int8_t *>(base + l.qq);
+    a.qs = reinterpret_cast<float *>(base + l.qs);
+    a.qo = reinterpret_cast<float *>(base + l.qo);
+    {
+        KernelScope scope("qattention.keys", stream);
+        hipLaunchKernelGGL(qa_keys_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.lkp, 4))), dim3(256), 0,
+                           stream, a);
+    }
+    {
+        KernelScope scope("qattention.values", stream);
+        hipLaunchKernelGGL(qa_values_kernel,
+                           dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.groups * a.dvp, 4))), dim3(256), 0,
+                           stream, a);
+    }
+    {
+        KernelScope scope("qattention.queries", stream);
+        hipLaunchKernelGGL(qa_queries_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lqp, 4))), dim3(256),
+                           0, stream, a);
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    KernelScope scope("qattention", stream);
+    const dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b));
+    switch (a.sd / 64) {
+    case 1: return launch_qa_ndv<1>(a, stream, grid);
+    case 2: return launch_qa_ndv<2>(a, stream, grid);
+    case 3: return launch_qa_ndv<3>(a, stream, grid);
+    default: return launch_qa_ndv<4>(a, stream, grid);
+    }
+}
+
+}  // namespace sdhip

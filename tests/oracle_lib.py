@@ -52,6 +52,7 @@ def lib():
         L.oracle_quantize_weights.argtypes = [_f, _L, _L, _L, _L, _I, _I, _s8, _f, _f, _i32]
         L.oracle_quantized_mul_mat.argtypes = [_f, _f, _L, _L, _L, _L, _I, _I, _I, ctypes.c_void_p, _f,
                                                _u8, _f, _f, _s8, _f, _f, _i32]
+        L.oracle_quantized_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _L, _I, _I, _L, _f]
         _lib = L
     return _lib
 
@@ -212,3 +213,17 @@ def quantized_mul_mat(w, x, group=64, input_levels=255, weight_max=127, weight_g
     lib().oracle_quantized_mul_mat(w, x, M, N, K, group, input_levels, weight_max, weight_groups, ip, y, xq, xs, xo,
                                    wq, ws, wo, wsum)
     return y, xq, xs, xo, wq, ws, wo, wsum
+
+
+def quantized_attention(q, k, v, scale, group=64, input_levels=255, weight_max=127, key_block=256):
+    """The reference's bits-mode self-attention (attention.cc:612-824):
+    q [b, lq, h, d], k [b, lk, hk, d], v [b, lk, hk, dv] -> y [b, lq, h, dv].
+    key_block: the reference's stretch of keys, max(group, attention_keys
+    rounded down to 8 then to the group)."""
+    q, k, v = c32(q), c32(k), c32(v)
+    b, lq, h, d = q.shape
+    _, lk, hk, dv = v.shape
+    y = np.zeros((b, lq, h, dv), np.float32)
+    lib().oracle_quantized_attention(q, k, v, d, dv, lq, lk, h, hk, b, scale, group, input_levels, weight_max,
+                                     key_block, y)
+    return y

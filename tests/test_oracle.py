@@ -275,3 +275,57 @@ def test_quantized_product_against_its_own_integers_and_float64():
     init = uniform(r, (M, N), 1.0)
     y2 = orc.quantized_mul_mat(w, x, init=init)[0]
     assert np.allclose(y2, y + init, atol=1e-5)
+
+
+# ------------------------------------------------------------------ quantized attention
+
+K_QUANTIZED = 1e-2  # tests/ops_test.cc:221
+
+
+def quantized_bound(levels, wmax):
+    """The reference's bound for a quantized form against float64
+    (ops_test.cc:213-240): kQuantized scaled by (2/L + 1/W)."""
+    return K_QUANTIZED * (2.0 / levels + 1.0 / wmax) / (2.0 / 255 + 1.0 / 127)
+
+
+@pytest.mark.parametrize("c,levels,wmax", [
+    ((40, 120, 700, 2, 2, 1), 255, 127),
+    ((13, 37, 290, 4, 2, 3), 255, 127),    # the reference's edge case (ops_test.cc:920)
+    ((80, 60, 1024, 2, 1, 1), 255, 127),
+    ((40, 50, 500, 2, 2, 1), 255, 63),     # weights of 7 bits
+    ((40, 50, 500, 2, 2, 1), 127, 127),    # inputs of 7 bits
+])
+def test_quantized_attention_within_the_reference_bound(c, levels, wmax):
+    """The bits-mode self-attention against the float64 softmax, by the
+    reference's metric and its own bound for quantized forms."""
+    d, lq, lk, h, hk, b = c
+    r = rng(d + lk)
+    q, k, v = (uniform(r, (b, n, hh, d), 1.0) for n, hh in ((lq, h), (lk, hk), (lk, hk)))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    y = orc.quantized_attention(q, k, v, scale, input_levels=levels, weight_max=wmax)
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    assert err <= quantized_bound(levels, wmax), err
+    assert err > 1e-5  # quantized, not single precision
+
+
+def test_quantized_attention_groups_exactly():
+    """Keys of zeros make every score 0 and every exponential 1, so each
+    output is the mean of the dequantized values; values that are integers
+    times a power of two per (dimension, group of 64 keys), with +-127 of them
+    in each group, dequantize exactly.  The output is then the plain mean to
+    single-precision rounding: a group misplaced against the stretches or the
+    keys, a wrong scale or offset, or a dropped term would be off by a step
+    of a byte."""
+    b, lq, h, d, lk = 1, 5, 2, 16, 300
+    r = rng(11)
+    q = uniform(r, (b, lq, h, d), 1.0)
+    k = np.zeros((b, lk, h, d), np.float32)
+    ints = r.integers(-127, 128, size=(b, lk, h, d)).astype(np.float32)
+    ints[:, ::64] = 127.0  # each group's greatest
+    powers = np.float32(2.0) ** -r.integers(0, 12, size=((lk + 63) // 64, h, d)).astype(np.float32)
+    v = ints * np.repeat(powers, 64, axis=0)[None, :lk]
+    y = orc.quantized_attention(q, k, v.astype(np.float32), 0.25)
+    mean = v.astype(np.float64).mean(axis=1)  # [b, h, d]
+    want = np.broadcast_to(mean[:, None], y.shape)
+    assert np.max(np.abs(y - want) / np.abs(v).max()) < 1e-6
