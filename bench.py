@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only-main", action="store_true")
     p.add_argument("--workload", default="", help="run one workload alone (cfg1 cfg2 cfg3a cfg3b cfg4_self "
-                                                  "cfg4_cross unet copy), for a profiler")
+                                                  "cfg4_cross cfg5 unet copy), for a profiler")
     p.add_argument("--no-unet", action="store_true", help="leave out the UNet step")
     return p.parse_args()
 
@@ -222,6 +222,32 @@ def unet_workload(dev, seed=7):
     return unet_step.Step(model, unet_step.HipOps(dev), model.inputs(seed=seed + 1))
 
 
+def sdxl_block_workload(dev, tuning="bits=8,weight_group=0", seed=9):
+    """the SDXL transformer block at 988 tokens (26x38), batch 2,
+    1280 channels, 20 heads of 64, in the bits mode (weights int8 per output
+    row), captured in a HIP graph with the tuning in effect."""
+    import torch
+
+    import sdhip
+    import unet_step
+
+    block = unet_step.SdxlBlock(dev, seed=seed)
+    g = torch.Generator(device=dev).manual_seed(seed + 1)
+    x = torch.randn((2, 988, 1280), generator=g, device=dev)
+    ops = unet_step.HipOps(dev)
+
+    def fn():
+        sdhip.set_tuning(tuning)
+        try:
+            return block.forward(ops, x)
+        finally:
+            sdhip.set_tuning("")
+
+    graph = unet_step.Graph(fn, ops)
+    graph.keep = (block, x)
+    return graph
+
+
 def make_workload(dev, name):
     """(run, FLOPs) of a named workload: the BASELINE.json configurations."""
     if name == "cfg1":
@@ -242,6 +268,9 @@ def make_workload(dev, name):
         return attention_workload(dev, 2, 8, 4096, 77, 40, seed=5)
     if name == "copy":
         return copy_workload(dev)
+    if name == "cfg5":
+        graph = sdxl_block_workload(dev)
+        return graph.run, graph.flops
     if name == "unet":
         step = unet_workload(dev)
         return step.run, step.flops
@@ -377,6 +406,13 @@ def main():
                                               "kernels_us": {k: round(v[0] * 1e3, 2)
                                                              for k, v in kernel_times(run3b, 10).items()}}
         log(f"cfg3b 1x1+GN+SiLU: {m3b * 1e3:.1f} us")
+        g5 = sdxl_block_workload(dev)
+        m5 = timed(g5.run, args.steps, args.warmup)
+        configs["cfg5_sdxl_block_bits8"] = {
+            "ms": round(m5, 5), "tops": round(g5.flops / m5 / 1e9, 2), "gop": round(g5.flops / 1e9, 2),
+            "tuning": "bits=8,weight_group=0",
+            "kernels_us": {k: round(v[0] * v[1] * 1e3, 2) for k, v in kernel_times(g5.eager, 5).items()}}
+        log(f"cfg5 SDXL block bits=8: {m5 * 1e3:.1f} us, {g5.flops / m5 / 1e9:.1f} TOPS")
         for name, lk in (("cfg4_self_attention", 4096), ("cfg4_cross_attention", 77)):
             run4, f4 = attention_workload(dev, 2, 8, 4096, lk, 40, seed=5)
             m4 = timed(run4, args.steps, args.warmup)

@@ -435,15 +435,15 @@ class Model:
         return ref
 
 
-class Step:
-    """The step on the GPU, captured once in a HIP graph (torch.cuda.graph)
-    after an eager pass that sizes the work buffer; `run()` replays it."""
+class Graph:
+    """`fn()` on the GPU, captured once in a HIP graph (torch.cuda.graph)
+    after an eager call that sizes the work buffer of `ops`; `run()` replays
+    it, `eager()` calls `fn` again."""
 
-    def __init__(self, model, ops, inputs):
-        self.model, self.ops = model, ops
-        self.x, self.t, self.ctx = inputs
+    def __init__(self, fn, ops):
+        self.fn, self.ops = fn, ops
         ops.reset()
-        self.out = model.forward(ops, self.x, self.t, self.ctx)  # eager: sizes the work buffer
+        self.out = fn()  # eager: sizes the work buffer
         self.flops, self.by_class, self.nodes = ops.flops, dict(ops.by_class), dict(ops.nodes)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
@@ -452,13 +452,53 @@ class Step:
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
             with torch.cuda.graph(self.graph, stream=stream):
-                self.out = model.forward(ops, self.x, self.t, self.ctx)
+                self.out = fn()
         torch.cuda.current_stream().wait_stream(stream)
         torch.cuda.synchronize()
+        ops.frozen = False
 
     def run(self):
         self.graph.replay()
         return self.out
 
     def eager(self):
-        return self.model.forward(self.ops, self.x, self.t, self.ctx)
+        return self.fn()
+
+
+class Step(Graph):
+    """The UNet step of `model` on `inputs` (x, t, context), as a Graph."""
+
+    def __init__(self, model, ops, inputs):
+        self.model = model
+        self.x, self.t, self.ctx = inputs
+        super().__init__(lambda: model.forward(ops, self.x, self.t, self.ctx), ops)
+
+
+class SdxlBlock:
+    """The transformer block of the SDXL configuration: LayerNorm, Q/K/V
+    projections (no bias), self-attention over `heads` heads, the output
+    projection with its bias and the residual, LayerNorm, the GEGLU FF
+    (C -> 2 x 4C with bias, gated) and its projection back with bias and the
+    residual; FP16 weights ~N(0, 0.02), biases ~N(0, 0.01), norms ~N(1, 0.1) /
+    ~N(0, 0.1).  `forward(ops, x)` for tokens x [b, L, C]."""
+
+    def __init__(self, device, channels=1280, heads=20, seed=0):
+        m = object.__new__(Model)
+        m.device = device
+        gdev = device if torch.device(device).type == "cuda" else "cpu"
+        m.gen = torch.Generator(device=gdev).manual_seed(seed)
+        m.gdev = gdev
+        c = channels
+        self.heads = heads
+        self.ln1, self.ln2 = m._norm(c), m._norm(c)
+        self.wq, self.wk, self.wv = (m._w(c, c) for _ in range(3))
+        self.wo = m._lin(c, c)
+        self.ff1 = m._lin(8 * c, c)
+        self.ff2 = m._lin(c, 4 * c)
+
+    def forward(self, ops, x):
+        n = ops.layer_norm(x, 1e-5, *self.ln1)
+        q, k, v = (ops.linear(n, w) for w in (self.wq, self.wk, self.wv))
+        x = ops.linear(ops.attention(q, k, v, self.heads), *self.wo, add=(x,))
+        n = ops.layer_norm(x, 1e-5, *self.ln2)
+        return ops.linear(ops.geglu(n, *self.ff1), *self.ff2, add=(x,))

@@ -38,3 +38,32 @@ def test_unet_graph_replays_equal_eager(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs from the eager step"
         assert torch.equal(other, eager)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tuning,low,high", [("", 0.0, 1e-5), ("bits=8,weight_group=0", 1e-5, 1e-2),
+                                             ("bits=8", 1e-5, 1e-2)])
+def test_sdxl_block(gpu, tuning, low, high):
+    """The SDXL transformer block at a reduced size -- 300
+    tokens, so that its self-attention is quantized too -- against float64
+    torch: in single precision within 1e-5 of the output's norm, in the bits
+    mode within the quantization's error (and measurably quantized)."""
+    import sdhip
+
+    block = u.SdxlBlock(gpu, channels=256, heads=4, seed=2)
+    x = torch.randn((1, 300, 256), generator=torch.Generator(device=gpu).manual_seed(3), device=gpu)
+    ops = u.HipOps(gpu)
+    sdhip.set_tuning(tuning)
+    try:
+        y = block.forward(ops, x)
+        torch.cuda.synchronize()
+    finally:
+        sdhip.set_tuning("")
+    ref = u.SdxlBlock("cpu", channels=256, heads=4, seed=2)
+    for name in ("ln1", "ln2", "wq", "wk", "wv", "wo", "ff1", "ff2"):
+        setattr(ref, name, tuple(t.cpu() for t in getattr(block, name)) if isinstance(getattr(block, name), tuple)
+                else getattr(block, name).cpu())
+    y64 = ref.forward(u.TorchOps(torch.float64), x.cpu().double())
+    err = ((y.cpu().double() - y64).norm() / y64.norm()).item()
+    print(f"sdxl block [{tuning or 'single precision'}]: relative L2 error {err:.3g}")
+    assert low <= err <= high
