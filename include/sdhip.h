@@ -83,8 +83,11 @@ const char *sdhip_last_error(void);
 /* The tuning that changes what is computed, in the reference's SDASM_TUNE
  * syntax "name=value,..." (sources/kernels.h:91-135, parsed by cpu.cc:121-212):
  * bits, input_bits, group, weight_group, quantize, winograd,
- * winograd_positions, winograd4_positions, winograd_small_tiles, fuse.
- * Returns SDHIP_ERROR naming the first unknown name.  "" resets the defaults. */
+ * winograd_positions, winograd4_positions, winograd_small_tiles, fuse,
+ * attention_keys; and this library's own: winograd_fp32, gemm_stages,
+ * gemm_tiles, attention_generic (forms to compare, same results within the
+ * bounds).  Returns SDHIP_ERROR naming the first unknown name.  "" resets
+ * the defaults. */
 sdhip_status sdhip_set_tuning(const char *text);
 /* The value of one tuning field, or -1 if it has no such name. */
 int sdhip_get_tuning(const char *name);
@@ -93,6 +96,22 @@ int sdhip_get_tuning(const char *name);
  * [begin, begin + size) -- the reference's sdasm_forget (sdasm.h:56-60,
  * store.cc:241-266), called when that memory is about to change. */
 void sdhip_forget(const void *begin, size_t size);
+
+/* The device store of the forms the library derives from weights and keeps
+ * from one call to the next -- the reference's store (sources/store.h,
+ * store.cc), whose quantized layouts are kept by default within a budget
+ * (store.cc:64-99).  Here the budget is memory the caller gives: `arena`,
+ * `bytes` of device memory, 256-byte aligned, that the library places its
+ * entries in (the quantized weights of the bits mode's MUL_MATs: bytes,
+ * scales, offsets and sums).  A NULL arena or 0 bytes keeps nothing (the
+ * default); a new arena forgets every entry of the last.  An entry is filled
+ * by the first call that needs it, on that call's stream, and read by later
+ * calls: they must be ordered after it on the device (one stream, or an
+ * event), and no entry is made while a stream is captured into a graph.
+ * sdhip_forget drops the entries derived from the memory it names. */
+void sdhip_store_arena(void *arena, size_t bytes);
+/* The bytes of the arena in use, and (if not NULL) how many entries. */
+size_t sdhip_store_used(size_t *entries);
 
 /* The profile of the kernels (the reference's sdasm_profile_*, sdasm.h:63-76,
  * profile.cc): with profiling on, each kernel launch is bracketed by HIP

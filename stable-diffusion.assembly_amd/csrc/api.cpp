@@ -236,4 +236,8 @@ int sdhip_get_tuning(const char *name) {
 
 void sdhip_forget(const void *begin, size_t size) { store_forget(begin, size); }
 
+void sdhip_store_arena(void *arena, size_t bytes) { store_arena(arena, bytes); }
+
+size_t sdhip_store_used(size_t *entries) { return store_used(entries); }
+
 }  // extern "C"

@@ -59,8 +59,18 @@ int64_t nelements(const sdhip_tensor *t);
 sdhip_status device_chain(const sdhip_epilogue *e, const int64_t ne[4], DevChain &c);
 sdhip_status output_of(const sdhip_tensor *y, const sdhip_epilogue *e, float *&out, int32_t &from_redirect);
 
-// The device store of derived weights (none kept yet): forget a range.
+// The device store of derived weights (store.cpp).  store_entry: the entry of
+// `bytes` for the form `layout`/`variant` of the tensor at `begin` (of
+// `source` bytes), made if the arena has room and the stream is not being
+// captured, or null; `ready` whether an earlier call filled it.  The call that
+// gets an entry not ready fills it on its stream, then store_publish()es it.
+enum StoreLayout : int32_t { kStoreQuantizedLinear = 1 };
+void *store_entry(const void *begin, int32_t type, const int64_t ne[4], const int64_t nb[4], int32_t layout,
+                  uint64_t variant, size_t source, size_t bytes, hipStream_t stream, bool &ready);
+void store_publish(const void *entry);
 void store_forget(const void *begin, size_t size);
+void store_arena(void *arena, size_t bytes);
+size_t store_used(size_t *entries);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }

@@ -419,19 +419,33 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     int8_t *xq = reinterpret_cast<int8_t *>(base + l.xq);
     float *xs = reinterpret_cast<float *>(base + l.xs);
     float *xo = reinterpret_cast<float *>(base + l.xo);
-    int8_t *wq = reinterpret_cast<int8_t *>(base + l.wq);
-    float *ws = reinterpret_cast<float *>(base + l.ws);
-    float *wo = reinterpret_cast<float *>(base + l.wo);
-    int32_t *wsum = reinterpret_cast<int32_t *>(base + l.wsum);
+    // The quantized weights: kept in the store when it has room for them
+    // (quantized layouts are kept by default, store.cc:64-99), else derived
+    // into the work buffer at every call.
+    const size_t wbytes = l.total - l.wq;
+    const int64_t ne[4] = {a.K, a.N, 1, 1};
+    const int64_t nb[4] = {2, 2 * a.ldw, 2 * a.ldw * a.N, 2 * a.ldw * a.N};
+    const uint64_t variant = static_cast<uint64_t>(q.group) | static_cast<uint64_t>(q.wmax) << 16 |
+                             static_cast<uint64_t>(q.weight_groups) << 24;
+    bool ready = false;
+    char *kept = static_cast<char *>(store_entry(a.w, SDHIP_TYPE_F16, ne, nb, kStoreQuantizedLinear, variant,
+                                                 static_cast<size_t>(2 * (a.ldw * (a.N - 1) + a.K)), wbytes, stream,
+                                                 ready));
+    char *wbase = kept != nullptr ? kept : base + l.wq;  // the weights' parts, at their offsets from l.wq
+    int8_t *wq = reinterpret_cast<int8_t *>(wbase);
+    float *ws = reinterpret_cast<float *>(wbase + (l.ws - l.wq));
+    float *wo = reinterpret_cast<float *>(wbase + (l.wo - l.wq));
+    int32_t *wsum = reinterpret_cast<int32_t *>(wbase + (l.wsum - l.wq));
     {
         KernelScope scope("quantize_inputs", stream);
         hipLaunchKernelGGL(quantize_inputs_kernel, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream, a.x,
                            a.ldx, a.M, a.K, q, l, xq, xs, xo);
     }
-    {
+    if (!ready) {
         KernelScope scope("quantize_weights", stream);
         hipLaunchKernelGGL(quantize_weights_kernel, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w, a.ldw, a.N,
                            a.K, q, l, wq, ws, wo, wsum);
+        if (kept != nullptr) store_publish(kept);
     }
     QgemmArgs p{};
     p.xq = xq;

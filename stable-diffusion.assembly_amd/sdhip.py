@@ -56,6 +56,8 @@ SIGNATURES = [
     ("sdhip_set_tuning", ctypes.c_int, [ctypes.c_char_p]),
     ("sdhip_get_tuning", ctypes.c_int, [ctypes.c_char_p]),
     ("sdhip_forget", None, [_P, _SZ]),
+    ("sdhip_store_arena", None, [_P, _SZ]),
+    ("sdhip_store_used", _SZ, [ctypes.POINTER(_SZ)]),
     ("sdhip_profile_enable", None, [ctypes.c_int]),
     ("sdhip_profile_reset", None, []),
     ("sdhip_profile_collect", ctypes.c_int, []),
@@ -277,3 +279,22 @@ def profile_collect():
         if lib.sdhip_profile_entry(i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)):
             out[name.value.decode()] = (ms.value, n.value)
     return out
+
+
+def store_arena(buf):
+    """Give the library `buf` (a uint8 device tensor, or None) as its store."""
+    if buf is None:
+        load().sdhip_store_arena(None, 0)
+    else:
+        load().sdhip_store_arena(ctypes.c_void_p(buf.data_ptr()), buf.numel())
+
+
+def store_used():
+    n = ctypes.c_size_t()
+    used = load().sdhip_store_used(ctypes.byref(n))
+    return used, n.value
+
+
+def forget(t):
+    """sdhip_forget over the memory of tensor t."""
+    load().sdhip_forget(ctypes.c_void_p(t.data_ptr()), t.numel() * t.element_size())

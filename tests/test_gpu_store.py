@@ -1,0 +1,153 @@
+"""The device store (sdhip_store_arena): the bits mode's quantized weights
+kept from one call to the next, as the reference keeps its quantized layouts
+(store.h, store.cc:64-99), and forgotten by sdhip_forget as sdasm_forget
+forgets them (store.cc:241-266)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as orc
+import sdhip
+from helpers import dev, rng, uniform, unwritten, weights_f16
+
+
+def product(gpu, w_d, x_d, tuning="bits=8"):
+    y = unwritten((x_d.shape[0], w_d.shape[0]), gpu)
+    sdhip.set_tuning(tuning)
+    try:
+        sdhip.mul_mat(w_d, x_d, y)
+        torch.cuda.synchronize()
+    finally:
+        sdhip.set_tuning("")
+    return y.cpu().numpy()
+
+
+@pytest.fixture
+def arena(gpu):
+    buf = torch.empty(64 << 20, dtype=torch.uint8, device=gpu)
+    sdhip.store_arena(buf)
+    yield buf
+    sdhip.store_arena(None)
+
+
+def kernels_of(fn):
+    sdhip.profile_reset()
+    sdhip.profile_enable(True)
+    fn()
+    torch.cuda.synchronize()
+    sdhip.profile_enable(False)
+    return sdhip.profile_collect()
+
+
+@pytest.mark.gpu
+def test_kept_weights_give_the_same_products(gpu, arena):
+    K, N, M = 640, 384, 300
+    r = rng(1)
+    wh, w32 = weights_f16(r, (N, K))
+    x = uniform(r, (M, K), 1.0)
+    w_d, x_d = dev(wh, gpu), dev(x, gpu)
+    want = orc.quantized_mul_mat(w32, x)[0]
+    first = product(gpu, w_d, x_d)
+    used, entries = sdhip.store_used()
+    assert entries == 1 and used > 0
+    second = kernels_of(lambda: product(gpu, w_d, x_d))
+    assert "quantize_weights" not in second and "quantize_inputs" in second
+    again = product(gpu, w_d, x_d)
+    assert np.array_equal(first.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+    # Another variant of the same weights (per-row scales) is another entry.
+    rows = product(gpu, w_d, x_d, "bits=8,weight_group=0")
+    assert sdhip.store_used()[1] == 2
+    assert np.array_equal(rows.view(np.uint32), orc.quantized_mul_mat(w32, x, weight_groups=0)[0].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_gated_product_shares_the_entry(gpu, arena):
+    K, half, M = 256, 640, 300
+    r = rng(2)
+    wh, w32 = weights_f16(r, (2 * half, K))
+    x = uniform(r, (M, K), 1.0)
+    w_d, x_d = dev(wh, gpu), dev(x, gpu)
+    product(gpu, w_d, x_d)
+    out = unwritten((M, half), gpu)
+    y = unwritten((M, 2 * half), gpu)
+    sdhip.set_tuning("bits=8")
+    try:
+        k = kernels_of(lambda: sdhip.mul_mat_gated(w_d, x_d, y, out))
+    finally:
+        sdhip.set_tuning("")
+    assert "quantize_weights" not in k
+    p = orc.quantized_mul_mat(w32, x)[0]
+    want = orc.gated_gelu(p[:, :half], p[:, half:])
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_forget_drops_the_entry(gpu, arena):
+    K, N, M = 320, 320, 256
+    r = rng(3)
+    wh, w32 = weights_f16(r, (N, K))
+    x = uniform(r, (M, K), 1.0)
+    w_d, x_d = dev(wh, gpu), dev(x, gpu)
+    product(gpu, w_d, x_d)
+    # New weights written into the same memory: kept until forgotten.
+    wh2, w322 = weights_f16(rng(4), (N, K))
+    w_d.copy_(torch.from_numpy(wh2).to(gpu))
+    stale = product(gpu, w_d, x_d)
+    assert np.array_equal(stale.view(np.uint32), orc.quantized_mul_mat(w32, x)[0].view(np.uint32))
+    sdhip.forget(w_d[1:2])  # any byte of the weights
+    assert sdhip.store_used()[1] == 0
+    fresh = product(gpu, w_d, x_d)
+    assert np.array_equal(fresh.view(np.uint32), orc.quantized_mul_mat(w322, x)[0].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_small_arena_keeps_nothing(gpu):
+    buf = torch.empty(4096, dtype=torch.uint8, device=gpu)
+    sdhip.store_arena(buf)
+    try:
+        K, N, M = 640, 384, 300
+        r = rng(5)
+        wh, w32 = weights_f16(r, (N, K))
+        x = uniform(r, (M, K), 1.0)
+        y = product(gpu, dev(wh, gpu), dev(x, gpu))
+        assert sdhip.store_used() == (0, 0)
+        assert np.array_equal(y.view(np.uint32), orc.quantized_mul_mat(w32, x)[0].view(np.uint32))
+    finally:
+        sdhip.store_arena(None)
+
+
+@pytest.mark.gpu
+def test_no_entry_made_under_capture(gpu, arena):
+    """A product captured into a graph before its weights are kept derives
+    them in its work buffer; replays after the weights are kept by an eager
+    call stay right, and every replay equals the eager result."""
+    K, N, M = 320, 256, 300
+    r = rng(6)
+    wh, w32 = weights_f16(r, (N, K))
+    x = uniform(r, (M, K), 1.0)
+    w_d, x_d = dev(wh, gpu), dev(x, gpu)
+    y = torch.empty((M, N), device=gpu)
+    work = torch.empty(1 << 22, dtype=torch.uint8, device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    sdhip.set_tuning("bits=8")
+    try:
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                sdhip.mul_mat(w_d, x_d, y, work=work)
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        assert sdhip.store_used()[1] == 0
+        want = orc.quantized_mul_mat(w32, x)[0]
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+            eager = product(gpu, w_d, x_d)  # makes the entry, then reads it
+            assert np.array_equal(eager.view(np.uint32), want.view(np.uint32))
+        assert sdhip.store_used()[1] == 1
+    finally:
+        sdhip.set_tuning("")
