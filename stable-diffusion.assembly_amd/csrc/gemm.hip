@@ -755,16 +755,19 @@ hipError_t launch_split_t(SplitBatchedArgs p, int stages, hipStream_t stream) {
 }
 
 // Blocks of 64 TM x 64 TN: the largest tiles that still give each CU two
-// blocks or more, down to 64 x 64.
+// blocks or more, down to 64 x 64 -- and 64 rows wherever 128 would leave a
+// part of the last block idle (OC = 320 fills 64-row blocks, not 128-row
+// ones: a sixth of the MFMAs would be on padding).
 template <class Launch>
 hipError_t pick_tiles(int64_t rows, int64_t cols, int64_t batches, int forced, Launch launch) {
     const auto blocks = [&](int tm, int tn) {
         return batches * ((rows + 64 * tm - 1) / (64 * tm)) * ((cols + 64 * tn - 1) / (64 * tn));
     };
-    if (forced == 22 || (forced == 0 && blocks(2, 2) >= 512)) {
+    const bool rows128 = rows % 128 == 0 || rows % 128 > 64;
+    if (forced == 22 || (forced == 0 && rows128 && blocks(2, 2) >= 512)) {
         return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
     }
-    if (forced == 21 || (forced == 0 && blocks(2, 1) >= 512)) {
+    if (forced == 21 || (forced == 0 && rows128 && blocks(2, 1) >= 512)) {
         return launch(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
     }
     return launch(std::integral_constant<int, 1>(), std::integral_constant<int, 1>());

@@ -115,69 +115,70 @@ __device__ __forceinline__ float block_max(float v, float *scratch) {
 
 // ------------------------------------------------------------------ 0. scales
 
-constexpr int kScaleThreads = 1024;
+__device__ __forceinline__ float abs_max4(float4v v) {
+    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+}
 
-__device__ __forceinline__ float block_max_wide(float v, float *scratch) {
+__device__ __forceinline__ float wave_max64(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = scratch[0];
-#pragma unroll
-    for (int i = 1; i < kScaleThreads / 64; ++i) m = fmaxf(m, scratch[i]);
-    return m;
+    return v;
 }
 
-__device__ __forceinline__ float abs_max4(float4 v) {
-    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-}
-
-// Blocks [0, IC): input channel c's greatest |x| over every image, four
-// independent loads in flight per thread where the rows are contiguous, and
-// its exponent e[c] (zero channels: the least, so that they scale to zero).
-// Blocks [IC, IC + OC): output channel o's greatest FP16 weight and a[o].
+// One wave per channel: waves [0, IC) input channel c's greatest |x| over
+// every image, four independent float4 loads in flight per lane where the
+// rows are contiguous, and its exponent e[c] (zero channels: the least, so
+// that they scale to zero); waves [IC, IC + OC) output channel o's greatest
+// FP16 weight, eight at a time, and a[o].
 template <int M>
-__global__ __launch_bounds__(kScaleThreads) void scales_kernel(WinogradArgs a, int32_t *__restrict__ e,
-                                                               int32_t *__restrict__ amax) {
-    __shared__ float scratch[kScaleThreads / 64];
-    const int64_t b = blockIdx.x;
-    const int tid = threadIdx.x;
+__global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__restrict__ e,
+                                                     int32_t *__restrict__ amax) {
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (w >= a.ic + a.oc) return;
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
-    if (b < a.ic) {
+    if (w < a.ic) {
         const int64_t plane = a.ih * a.iw;
         for (int64_t n = 0; n < a.n; ++n) {
-            const float *p = a.x + n * a.xnb3 + b * a.xnb2;
+            const float *p = a.x + n * a.xnb3 + w * a.xnb2;
             if (a.xnb1 == a.iw && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-                const float4 *q = reinterpret_cast<const float4 *>(p);
+                const float4v *q = reinterpret_cast<const float4v *>(p);
                 const int64_t quads = plane / 4;
-                int64_t i = tid;
-                for (; i + 3 * kScaleThreads < quads; i += 4 * kScaleThreads) {
-                    const float4 v0 = q[i], v1 = q[i + kScaleThreads], v2 = q[i + 2 * kScaleThreads],
-                                 v3 = q[i + 3 * kScaleThreads];
+                int64_t i = lane;
+                for (; i + 192 < quads; i += 256) {
+                    const float4v v0 = q[i], v1 = q[i + 64], v2 = q[i + 128], v3 = q[i + 192];
                     m0 = fmaxf(m0, abs_max4(v0));
                     m1 = fmaxf(m1, abs_max4(v1));
                     m2 = fmaxf(m2, abs_max4(v2));
                     m3 = fmaxf(m3, abs_max4(v3));
                 }
-                for (; i < quads; i += kScaleThreads) m0 = fmaxf(m0, abs_max4(q[i]));
-                for (int64_t j = quads * 4 + tid; j < plane; j += kScaleThreads) m1 = fmaxf(m1, fabsf(p[j]));
+                for (; i < quads; i += 64) m0 = fmaxf(m0, abs_max4(q[i]));
+                for (int64_t j = quads * 4 + lane; j < plane; j += 64) m1 = fmaxf(m1, fabsf(p[j]));
             } else {
-                for (int64_t i = tid; i < plane; i += kScaleThreads) {
+                for (int64_t i = lane; i < plane; i += 64) {
                     const int64_t y = i / a.iw;
                     m0 = fmaxf(m0, fabsf(p[y * a.xnb1 + (i - y * a.iw)]));
                 }
             }
         }
-        const float m = block_max_wide(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)), scratch);
-        if (tid == 0) e[b] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : kZeroChannel;
+        const float m = wave_max64(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
+        if (lane == 0) e[w] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : kZeroChannel;
     } else {
-        const int64_t o = b - a.ic;
+        const int64_t o = w - a.ic;
         const int64_t count = a.ic * 9;
         const _Float16 *p = a.w + o * count;
-        for (int64_t i = tid; i < count; i += kScaleThreads) m0 = fmaxf(m0, fabsf(static_cast<float>(p[i])));
-        const float m = block_max_wide(m0, scratch);
-        if (tid == 0) amax[o] = m > 0.0f ? kTop - exponent_above(m * Mat<M>::kWeightGain) : 0;
+        if (count % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            const half8 *q = reinterpret_cast<const half8 *>(p);
+            for (int64_t i = lane; i < count / 8; i += 64) {
+                const half8 v = q[i];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) m0 = fmaxf(m0, fabsf(static_cast<float>(v[k])));
+            }
+        } else {
+            for (int64_t i = lane; i < count; i += 64) m0 = fmaxf(m0, fabsf(static_cast<float>(p[i])));
+        }
+        const float m = wave_max64(m0);
+        if (lane == 0) amax[o] = m > 0.0f ? kTop - exponent_above(m * Mat<M>::kWeightGain) : 0;
     }
 }
 
@@ -206,11 +207,13 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
             u[i][j] = gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
 }
 
-// One block per output channel o: E, the greatest e_c, and shift[o] = E - a_o
-// for the outputs; then, 256 channels at a time, U * 2^(a_o + e_c - E) split
-// into its two FP16 parts, staged in LDS as [xi][part][channel] and written
-// out as rows of channels, u[xi][part][oc][kp], zeros from IC to kp.
-constexpr int kWeightChunk = 256;
+// A block per 4 output channels by 64 input channels, a thread per kernel:
+// E, the greatest e_c (each block reduces e itself), and shift[o] = E - a_o
+// for the outputs (blocks of the first channels); U * 2^(a_o + e_c - E) split
+// into its two FP16 parts, staged in LDS as [xi][part][o][channel] and
+// written out as rows of 64 channels, u[xi][part][oc][kp], zeros from IC to
+// kp.
+constexpr int kWeightOc = 4, kWeightIc = 64;
 
 template <int M>
 __global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
@@ -220,43 +223,47 @@ __global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__re
     constexpr int A = Mat<M>::A;
     constexpr int kRows = 2 * A * A;
     __shared__ float scratch[4];
-    __shared__ __attribute__((aligned(16))) _Float16 stage[kRows][kWeightChunk];
-    const int64_t o = blockIdx.x;
+    __shared__ __attribute__((aligned(16))) _Float16 stage[kRows][kWeightOc][kWeightIc];
     const int tid = threadIdx.x;
+    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kWeightOc;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kWeightIc;
     int emax = kZeroChannel;
     for (int64_t c = tid; c < ic; c += 256) emax = max(emax, e[c]);
     const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
-    const int ao = amax[o];
-    if (tid == 0) shift[o] = E - ao;
-    for (int64_t c0 = 0; c0 < kp; c0 += kWeightChunk) {
-        const int64_t c = c0 + tid;
-        float t[A][A] = {};
-        int s = 0;
+    const int ol = tid / kWeightIc, cl = tid % kWeightIc;
+    const int64_t o = o0 + ol, c = c0 + cl;
+    float t[A][A] = {};
+    int s = 0;
+    if (o < oc) {
+        const int ao = amax[o];
+        if (blockIdx.y == 0 && cl == 0) shift[o] = E - ao;
         if (c < ic) {
             float g[3][3];
             load_g(w + (o * ic + c) * 9, g);
             transform_g<M>(g, t);
             s = ao + e[c] - E;
         }
+    }
 #pragma unroll
-        for (int i = 0; i < A; ++i)
+    for (int i = 0; i < A; ++i)
 #pragma unroll
-            for (int j = 0; j < A; ++j) {
-                _Float16 hi, lo;
-                split2(ldexpf(t[i][j], s), hi, lo);
-                stage[2 * (i * A + j)][tid] = hi;
-                stage[2 * (i * A + j) + 1][tid] = lo;
-            }
-        __syncthreads();
-        // kRows rows of `width` halves, 8 at a time.
-        const int width = static_cast<int>(kp - c0 < kWeightChunk ? kp - c0 : kWeightChunk);
-        const int per_row = width / 8;
-        for (int q = tid; q < kRows * per_row; q += 256) {
-            const int r = q / per_row;
-            const int k = (q - r * per_row) * 8;
-            *reinterpret_cast<half8 *>(u + (r * oc + o) * kp + c0 + k) = *reinterpret_cast<const half8 *>(&stage[r][k]);
+        for (int j = 0; j < A; ++j) {
+            _Float16 hi, lo;
+            split2(ldexpf(t[i][j], s), hi, lo);
+            stage[2 * (i * A + j)][ol][cl] = hi;
+            stage[2 * (i * A + j) + 1][ol][cl] = lo;
         }
-        __syncthreads();
+    __syncthreads();
+    // kRows x kWeightOc rows of `width` halves, 8 at a time.
+    const int width = static_cast<int>(kp - c0 < kWeightIc ? kp - c0 : kWeightIc);
+    const int per_row = width / 8;
+    for (int q = tid; q < kRows * kWeightOc * per_row; q += 256) {
+        const int row = q / per_row;
+        const int k = (q - row * per_row) * 8;
+        const int r = row / kWeightOc, oo = row % kWeightOc;
+        if (o0 + oo >= oc) continue;
+        *reinterpret_cast<half8 *>(u + (r * oc + o0 + oo) * kp + c0 + k) =
+            *reinterpret_cast<const half8 *>(&stage[r][oo][k]);
     }
 }
 
@@ -714,12 +721,15 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
     {
         KernelScope scope(names[0].c_str(), stream);
-        hipLaunchKernelGGL((scales_kernel<M>), dim3(a.ic + a.oc), dim3(kScaleThreads), 0, stream, a, e, a_oc);
+        hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.ic + a.oc, 4))), dim3(256), 0,
+                           stream, a, e, a_oc);
     }
     {
         KernelScope scope(names[1].c_str(), stream);
-        hipLaunchKernelGGL((weights_split_kernel<M>), dim3(a.oc), dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, a_oc,
-                           uh, shift);
+        hipLaunchKernelGGL((weights_split_kernel<M>),
+                           dim3(static_cast<uint32_t>(ceil_div(a.oc, kWeightOc)),
+                                static_cast<uint32_t>(ceil_div(l.kp, kWeightIc))),
+                           dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, a_oc, uh, shift);
     }
     {
         KernelScope scope(names[2].c_str(), stream);
