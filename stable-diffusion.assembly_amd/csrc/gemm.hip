@@ -233,7 +233,7 @@ struct F16Rows {
 // positions, which are consecutive in a row of the image at stride 1.  FULL
 // (1x1 kernels, K = IC a multiple of BK): positions past the last read the
 // block's first, never stored, and the loads have no conditions.
-template <int BN, bool POINTWISE, bool FULL>
+template <int BN, bool POINTWISE, bool FULL, bool K3 = false>
 struct Columns {
     static constexpr int kLoads = BN * kBK / 4 / 256;
     static_assert(!FULL || POINTWISE, "FULL columns are those of 1x1 kernels");
@@ -294,10 +294,13 @@ struct Columns {
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t k = static_cast<uint32_t>(k0 + kq + e);
                     if (k >= c->K) continue;
-                    const uint32_t ic = k / static_cast<uint32_t>(c->taps);
-                    const uint32_t t = k - ic * static_cast<uint32_t>(c->taps);
-                    const uint32_t kh = t / static_cast<uint32_t>(c->kw);
-                    const uint32_t kw = t - kh * static_cast<uint32_t>(c->kw);
+                    // K3: 3x3 kernels, the divisions by constants.
+                    const uint32_t taps = K3 ? 9u : static_cast<uint32_t>(c->taps);
+                    const uint32_t kwidth = K3 ? 3u : static_cast<uint32_t>(c->kw);
+                    const uint32_t ic = k / taps;
+                    const uint32_t t = k - ic * taps;
+                    const uint32_t kh = t / kwidth;
+                    const uint32_t kw = t - kh * kwidth;
                     const int32_t iy = iy0[i] + static_cast<int32_t>(kh) * c->d1;
                     const int32_t ix = ix0[i] + static_cast<int32_t>(kw) * c->d0;
                     if (iy >= 0 && iy < c->ih && ix >= 0 && ix < c->iw) {
@@ -535,7 +538,7 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
 
 // y[n][oc][pos] = sum_k W[oc][k] columns[k][pos], the chain applied; W rows
 // K-contiguous FP16 (the kernel as ggml holds it, [OC][IC][KH][KW]).
-template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS>
+template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS, bool K3 = false>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     constexpr int BM = 64 * TM;  // output channels
     constexpr int BN = 64 * TN;  // positions
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
     F16Rows<BM, VECW, FULL> wa[NS];
-    Columns<BN, POINTWISE, FULL> xb[NS];
+    Columns<BN, POINTWISE, FULL, K3> xb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         wa[s].init(c.w, c.K, w_row, c.K, tid);
@@ -733,6 +736,8 @@ hipError_t launch_conv_t(const ConvArgs &c, int stages, hipStream_t stream) {
         hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 4>), grid, block, 0, stream, a);
     } else if (full) {
         hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2>), grid, block, 0, stream, a);
+    } else if (vw && !POINTWISE && c.kh == 3 && c.kw == 3) {
+        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, false, true, false, 2, true>), grid, block, 0, stream, a);
     } else if (vw) {
         hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2>), grid, block, 0, stream, a);
     } else {

@@ -201,6 +201,128 @@ __global__ __launch_bounds__(kThreads) void group_apply_kernel(GroupNormArgs a) 
     }
 }
 
+// GROUP_NORM of small groups in one launch: a block of 1024 threads per
+// (image, group) holds the group's count <= kResident numbers in registers,
+// four consecutive numbers of one channel a thread at a time (planes of a
+// multiple of 4), and takes the same statistics as the three launches above
+// -- float(sum / n) with the sum in double, then float(sum of the single-
+// precision squares of x - mean / n) -- with x read once.
+constexpr int kResidentThreads = 1024;
+constexpr int kResidentQuads = 4;  // float4 a thread
+constexpr int64_t kResident = int64_t(kResidentThreads) * 4 * kResidentQuads;
+
+__device__ __forceinline__ double block_sum_wide(double v, double *scratch) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double s = 0.0;
+#pragma unroll
+    for (int w = 0; w < kResidentThreads / 64; ++w) s += scratch[w];
+    return s;
+}
+
+__global__ __launch_bounds__(kResidentThreads) void group_norm_resident_kernel(GroupNormArgs a) {
+    __shared__ double scratch[kResidentThreads / 64];
+    const int tid = threadIdx.x;
+    const int64_t item = blockIdx.x;
+    const int64_t i3 = item / a.groups;
+    const int64_t g = item - i3 * a.groups;
+    const int64_t c0 = g * a.per_group;
+    const int64_t c1 = c0 + a.per_group < a.ne2 ? c0 + a.per_group : a.ne2;
+    const int64_t count = c0 < c1 ? (c1 - c0) * a.ne0 * a.ne1 : 0;
+    const int64_t plane = a.ne0 * a.ne1;
+    const float4v *x4 = reinterpret_cast<const float4v *>(a.x + i3 * a.xnb3 + c0 * a.xnb2);
+    float4v v[kResidentQuads];
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < kResidentQuads; ++u) {
+        const int64_t q = tid + kResidentThreads * u;
+        v[u] = 4 * q < count ? x4[q] : float4v{};
+        s += (static_cast<double>(v[u][0]) + static_cast<double>(v[u][1])) +
+             (static_cast<double>(v[u][2]) + static_cast<double>(v[u][3]));
+    }
+    const double n = static_cast<double>(count);
+    const float mean = static_cast<float>(block_sum_wide(s, scratch) / n);
+    double t = 0.0;
+#pragma unroll
+    for (int u = 0; u < kResidentQuads; ++u) {
+        if (4 * (tid + kResidentThreads * u) >= count) continue;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float d = v[u][k] - mean;
+            t += static_cast<double>(__fmul_rn(d, d));
+        }
+    }
+    const float variance = static_cast<float>(block_sum_wide(t, scratch) / n);
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
+    float4v *y4 = reinterpret_cast<float4v *>(a.y + i3 * a.ynb3 + c0 * a.ynb2);
+#pragma unroll
+    for (int u = 0; u < kResidentQuads; ++u) {
+        const int64_t q = tid + kResidentThreads * u;
+        if (4 * q >= count) continue;
+        const int64_t e = 4 * q;
+        const uint32_t c = static_cast<uint32_t>(e) / static_cast<uint32_t>(plane);
+        const int64_t p = e - static_cast<int64_t>(c) * plane;
+        float w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = __fmul_rn(v[u][k] - mean, scale);
+        apply_chain_block(a.chain, w, [&](int st_i, int k) {
+            const DevStep &st = a.chain.steps[st_i];
+            const int64_t pk = p + k;
+            const uint32_t r = static_cast<uint32_t>(pk) / static_cast<uint32_t>(a.ne0);
+            return (pk - static_cast<int64_t>(r) * a.ne0) * st.nb[0] + static_cast<int64_t>(r) * st.nb[1] +
+                   (c0 + c) * st.nb[2] + i3 * st.nb[3];
+        });
+        y4[q] = float4v{w[0], w[1], w[2], w[3]};
+    }
+}
+
+// NORM with the row in registers: one wave per row of ne0 <= 64 E, E numbers
+// a lane (lane + 64 u), x read once; the same statistics as norm_kernel.
+template <int E>
+__global__ __launch_bounds__(kThreads) void norm_resident_kernel(NormArgs a) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= a.rows) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t i1 = row % a.ne1;
+    const int64_t i2 = (row / a.ne1) % a.ne2;
+    const int64_t i3 = row / (a.ne1 * a.ne2);
+    const float *x = a.x + i1 * a.xnb1 + i2 * a.xnb2 + i3 * a.xnb3;
+    float *y = a.y + i1 * a.ynb1 + i2 * a.ynb2 + i3 * a.ynb3;
+    const auto at = [&](int u) -> int64_t {
+        const int64_t j = lane + 64 * u;
+        return j < a.ne0 ? j : a.ne0 - 1;
+    };
+    float v[E];
+#pragma unroll
+    for (int u = 0; u < E; ++u) v[u] = x[at(u)];
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < E; ++u)
+        if (lane + 64 * u < a.ne0) s += static_cast<double>(v[u]);
+    const float mean = static_cast<float>(wave_sum(s) / static_cast<double>(a.ne0));
+    double q = 0.0;
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+        if (lane + 64 * u >= a.ne0) continue;
+        const float d = v[u] - mean;
+        q += static_cast<double>(__fmul_rn(d, d));
+    }
+    const float variance = static_cast<float>(wave_sum(q) / static_cast<double>(a.ne0));
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
+#pragma unroll
+    for (int u = 0; u < E; ++u) v[u] = __fmul_rn(v[u] - mean, scale);
+    apply_chain_block(a.chain, v, [&](int s, int u) {
+        const DevStep &st = a.chain.steps[s];
+        return at(u) * st.nb[0] + i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+    });
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+        if (lane + 64 * u < a.ne0) y[lane + 64 * u] = v[u];
+    }
+}
+
 // One wave per row of ne0.
 __global__ __launch_bounds__(kThreads) void norm_kernel(NormArgs a) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
@@ -261,6 +383,16 @@ GroupNormShape group_norm_shape(int64_t ne0, int64_t ne1, int64_t ne2, int64_t n
 }
 
 hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream) {
+    const int64_t plane = a.ne0 * a.ne1;
+    const bool resident = a.per_group * plane <= kResident && plane % 4 == 0 && a.xnb2 == plane &&
+                          a.ynb2 == plane && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                          (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.xnb3 % 4 == 0 && a.ynb3 % 4 == 0;
+    if (resident) {
+        KernelScope scope("group_norm", stream);
+        hipLaunchKernelGGL(group_norm_resident_kernel, dim3(static_cast<uint32_t>(a.ne3 * a.groups)),
+                           dim3(kResidentThreads), 0, stream, a);
+        return hipGetLastError();
+    }
     const dim3 grid(static_cast<uint32_t>(a.ne3 * a.groups * a.slices));
     {
         KernelScope scope("group_norm.sums", stream);
@@ -277,7 +409,16 @@ hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream) {
 
 hipError_t launch_norm(const NormArgs &a, hipStream_t stream) {
     KernelScope scope("norm", stream);
-    hipLaunchKernelGGL(norm_kernel, dim3(ceil_div(a.rows, kThreads / 64)), dim3(kThreads), 0, stream, a);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(a.rows, kThreads / 64)));
+    if (a.ne0 <= 64 * 8) {
+        hipLaunchKernelGGL(norm_resident_kernel<8>, grid, dim3(kThreads), 0, stream, a);
+    } else if (a.ne0 <= 64 * 16) {
+        hipLaunchKernelGGL(norm_resident_kernel<16>, grid, dim3(kThreads), 0, stream, a);
+    } else if (a.ne0 <= 64 * 32) {
+        hipLaunchKernelGGL(norm_resident_kernel<32>, grid, dim3(kThreads), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(norm_kernel, grid, dim3(kThreads), 0, stream, a);
+    }
     return hipGetLastError();
 }
 

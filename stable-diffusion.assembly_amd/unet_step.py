@@ -97,6 +97,7 @@ class HipOps(Ops):
         self.device = device
         self.work = torch.empty(1 << 20, dtype=torch.uint8, device=device)
         self.frozen = False  # under graph capture the work buffer may not grow
+        self.widened = {}  # the single-precision copies of ggml's two-row linear layers' weights
         self.reset()
 
     def _work(self, size):
@@ -153,8 +154,13 @@ class HipOps(Ops):
         m = x.numel() // k
         self.count_linear(x, w)
         if m < 16:
-            # Not taken by the reference (mul_mat.cc:181-194): ggml's node.
-            y = x.reshape(-1, k) @ w.float().t()
+            # Not taken by the reference (mul_mat.cc:181-194): ggml's node,
+            # with the weights widened once and kept, as ggml's CPU backend
+            # reads them without converting the tensor each time.
+            wide = self.widened.get(w.data_ptr())
+            if wide is None:
+                wide = self.widened[w.data_ptr()] = w.float().t().contiguous()
+            y = x.reshape(-1, k) @ wide
             if bias is not None:
                 y = y + bias
             for a in add:
@@ -306,6 +312,7 @@ class Model:
             self.up.append((blocks, up))
         self.out_norm = self._norm(ch)
         self.conv_out = self._conv(cfg.in_channels, ch, 3)
+        self._join_embeddings()
 
     # -- parameters
 
@@ -340,12 +347,34 @@ class Model:
                 "v2": self._lin(c, cd, False), "o2": self._lin(c, c),
                 "ln3": self._norm(c), "ff1": self._lin(8 * c, c), "ff2": self._lin(c, 4 * c)}
 
+    def _resblocks(self):
+        for blocks, _ in self.down:
+            for res, _ in blocks:
+                yield res
+        yield self.mid[0]
+        yield self.mid[2]
+        for blocks, _ in self.up:
+            for res, _ in blocks:
+                yield res
+
+    def _join_embeddings(self):
+        """The ResBlocks' embedding projections side by side, [sum oc, time
+        dim] and [sum oc]; each block keeps the slice of its columns."""
+        ws, bs, at = [], [], 0
+        for res in self._resblocks():
+            w, b = res["emb"]
+            res["emb_at"] = (slice(None), slice(at, at + w.shape[0]))
+            at += w.shape[0]
+            ws.append(w)
+            bs.append(b)
+        self.emb_all = (torch.cat(ws), torch.cat(bs))
+
     # -- blocks
 
-    def resblock(self, ops, p, x, emb_silu):
+    def resblock(self, ops, p, x, projections):
         g = self.cfg.groups
         h = ops.group_norm(x, g, 1e-5, *p["norm1"], silu=True)
-        e = ops.linear(emb_silu, *p["emb"])  # [b, oc], two rows: ggml's node
+        e = projections[p["emb_at"]]  # [b, oc]: this block's part of the embedding's projections
         oc = e.shape[1]
         h = ops.conv(h, *p["conv1"], add=(e.reshape(-1, oc, 1, 1),))
         h = ops.group_norm(h, g, 1e-5, *p["norm2"], silu=True)
@@ -378,11 +407,14 @@ class Model:
         emb = ops.linear(emb, *self.time[0])
         emb = ops.linear(emb * torch.sigmoid(emb), *self.time[1])
         emb_silu = emb * torch.sigmoid(emb)  # each ResBlock's emb_layers begin with SiLU
+        # Every ResBlock's projection of the embedding (two rows each: ggml's
+        # nodes) as one product over the blocks' weights side by side.
+        projections = ops.linear(emb_silu, *self.emb_all)
         h = ops.conv(x, *self.conv_in)
         hs = [h]
         for blocks, down in self.down:
             for res, st in blocks:
-                h = self.resblock(ops, res, h, emb_silu)
+                h = self.resblock(ops, res, h, projections)
                 if st is not None:
                     h = self.transformer(ops, st, h, context)
                 hs.append(h)
@@ -390,13 +422,13 @@ class Model:
                 h = ops.conv(h, *down, stride=2, pad=1)
                 hs.append(h)
         res1, st, res2 = self.mid
-        h = self.resblock(ops, res1, h, emb_silu)
+        h = self.resblock(ops, res1, h, projections)
         h = self.transformer(ops, st, h, context)
-        h = self.resblock(ops, res2, h, emb_silu)
+        h = self.resblock(ops, res2, h, projections)
         for blocks, up in self.up:
             for res, st in blocks:
                 h = torch.cat([h, hs.pop()], dim=1)  # ggml_concat
-                h = self.resblock(ops, res, h, emb_silu)
+                h = self.resblock(ops, res, h, projections)
                 if st is not None:
                     h = self.transformer(ops, st, h, context)
             if up is not None:
@@ -430,7 +462,7 @@ class Model:
                 return type(o)(move(v) for v in o)
             return o
 
-        for name in ("time", "conv_in", "down", "mid", "up", "out_norm", "conv_out"):
+        for name in ("time", "conv_in", "down", "mid", "up", "out_norm", "conv_out", "emb_all"):
             setattr(ref, name, move(getattr(self, name)))
         return ref
 

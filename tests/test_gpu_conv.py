@@ -27,6 +27,8 @@ CASES = [
     (128, 128, 8, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1),
     (40, 9, 7, 13, 5, 3, 1, 2, 2, 0, 2, 1, 1),
     (17, 13, 5, 7, 3, 3, 1, 1, 1, 1, 1, 1, 3),
+    (32, 32, 64, 64, 3, 3, 2, 2, 1, 1, 1, 1, 2),   # the UNet's downsampling, fewer channels
+    (20, 20, 16, 8, 3, 3, 1, 1, 2, 2, 2, 2, 1),    # 3x3 dilated: direct
 ]
 
 
