@@ -527,9 +527,13 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
 // Y = A^T M A * 2^shift[oc] of the tile's alpha^2 products, then the sum
 // begun from the residual (from_redirect) and the chain, one thread per
 // (oc, tile), consecutive threads consecutive tiles.  shift null: no scale.
+// The products may come in `splits` parts over the input channels (the small
+// images' path), each with its own scale, prod[s][xi][oc][ld] and
+// shift[s][oc]; they are added in the order of s.
 template <int M>
 __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod,
-                                                      const int32_t *__restrict__ shift) {
+                                                      const int32_t *__restrict__ shift, int64_t splits = 1,
+                                                      int64_t ld = 0) {
     constexpr int A = Mat<M>::A;
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
     if (t >= static_cast<uint32_t>(a.tiles * a.oc)) return;
@@ -537,14 +541,20 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
     const uint32_t tile = t - oc * static_cast<uint32_t>(a.tiles);
     uint32_t tx, ty, n;
     split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
-    const int64_t plane = a.oc * a.tiles;
-    const int unscale = shift != nullptr ? shift[oc] : 0;
+    if (ld == 0) ld = a.tiles;
+    const int64_t plane = a.oc * ld;
     float m[A][A];
+    for (int64_t sp = 0; sp < splits; ++sp) {
+        const int unscale = shift != nullptr ? shift[sp * a.oc + oc] : 0;
+        const float *part = prod + sp * A * A * plane + static_cast<int64_t>(oc) * ld + tile;
 #pragma unroll
-    for (int i = 0; i < A; ++i)
+        for (int i = 0; i < A; ++i)
 #pragma unroll
-        for (int j = 0; j < A; ++j)
-            m[i][j] = ldexpf(prod[(i * A + j) * plane + static_cast<int64_t>(oc) * a.tiles + tile], unscale);
+            for (int j = 0; j < A; ++j) {
+                const float v = ldexpf(part[(i * A + j) * plane], unscale);
+                m[i][j] = sp == 0 ? v : __fadd_rn(m[i][j], v);
+            }
+    }
     float am[M][A];
 #pragma unroll
     for (int i = 0; i < M; ++i)
@@ -652,12 +662,251 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
     }
 }
 
+// ------------------------------------------------------------------ small images
+
+// Images of few tiles (the deepest level of SD's UNet: 16x16 by F(4x4), 32
+// tiles for two images) take a path of their own, as the reference's small
+// path does (winograd.cc:1069-1144): the transformed weights are never written
+// out -- at this size they would be 4 times the FP16 weights, read back once
+// each -- but made in registers from the FP16 kernels, straight into the
+// MFMA's operands.
+//
+//   inputs:   V[xi][part][tile][kp] * 2^-e_c as two FP16 planes, tiles padded
+//             to tp (a multiple of 16) with zeros;
+//   products: a block of four waves per (64 output channels, row i of U, split
+//             of the input channels), each wave 16 output channels: V's rows
+//             of row i staged through LDS, double-buffered, 16 input channels
+//             at a time; each lane makes U[i][*] of its output channel for
+//             four input channels from their nine FP16 numbers (G g G^T, one
+//             row), scaled by 2^(a_os + e_c - E) -- a_os from the split's
+//             greatest weight, as a_o from the channel's (section 0) -- and
+//             split, the operand A of v_mfma_f32_16x16x16_f16, the three
+//             products of split parts into the tile's sums; each split's sums
+//             go to M[s][xi][oc][tp], and its scale shift[s][oc] = E - a_os;
+//   outputs:  the splits added in their order (outputs_kernel).
+constexpr int kSmallTilesMax = 32;
+
+template <int M>
+__global__ __launch_bounds__(256) void inputs_small_kernel(WinogradArgs a, int64_t kp, int64_t tp,
+                                                           const int32_t *__restrict__ e, _Float16 *__restrict__ v) {
+    constexpr int A = Mat<M>::A;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= tp * kp) return;
+    const int64_t tile = idx / kp, c = idx - tile * kp;
+    float x[A][A] = {};
+    if (c < a.ic && tile < a.tiles) {
+        transform_d<M>(a, static_cast<uint32_t>(tile), static_cast<uint32_t>(c), x);
+        const int s = -e[c];
+#pragma unroll
+        for (int r = 0; r < A; ++r)
+#pragma unroll
+            for (int q = 0; q < A; ++q) x[r][q] = ldexpf(x[r][q], s);
+    }
+    const int64_t plane = tp * kp;
+#pragma unroll
+    for (int r = 0; r < A; ++r)
+#pragma unroll
+        for (int q = 0; q < A; ++q) {
+            _Float16 hi, lo;
+            split2(x[r][q], hi, lo);
+            const int64_t xi = r * A + q;
+            v[(2 * xi) * plane + idx] = hi;
+            v[(2 * xi + 1) * plane + idx] = lo;
+        }
+}
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+// The nine numbers of kernel (o, c0 + 4 kg + jj), jj = 0..3: 36 consecutive
+// FP16 numbers, nine 8-byte loads (zeros past OC or IC).
+__device__ __forceinline__ void load_kernels4(const WinogradArgs &a, int64_t o, int64_t c, float (&g)[4][9]) {
+    if (o < a.oc && c + 3 < a.ic) {
+        const half4v *p = reinterpret_cast<const half4v *>(a.w + (o * a.ic + c) * 9);
+#pragma unroll
+        for (int q = 0; q < 9; ++q) {
+            const half4v h = p[q];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) g[(4 * q + k) / 9][(4 * q + k) % 9] = static_cast<float>(h[k]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int q = 0; q < 9; ++q)
+            g[jj][q] = (o < a.oc && c + jj < a.ic) ? static_cast<float>(a.w[(o * a.ic + c + jj) * 9 + q]) : 0.0f;
+}
+
+// A block of 4 waves: 64 output channels (16 a wave) of row `row` of U, over
+// the input channels of split sp; the tiles' FP16 parts of the row's A planes
+// of V for 16 input channels at a time shared through LDS, double-buffered,
+// the next 16 channels' kernels and inputs loaded while these are multiplied.
+constexpr int kSmallLd = 16 + 4;  // halves per LDS row of V (16 channels)
+
+template <int M, int NT>
+__global__ __launch_bounds__(256) void products_small_kernel(WinogradArgs a, int64_t kp, int64_t tp, int64_t split_len,
+                                                             const int32_t *__restrict__ e,
+                                                             const _Float16 *__restrict__ v, float *__restrict__ prod,
+                                                             int32_t *__restrict__ shift) {
+    constexpr int A = Mat<M>::A;
+    constexpr int TP = 16 * NT;                        // tiles held (tp <= TP)
+    constexpr int kRows = A * 2 * TP;                  // LDS rows of V: [j][part][tile]
+    constexpr int kLoads = (kRows * 2 + 255) / 256;    // 16-byte loads a thread (two a row)
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2][kRows * kSmallLd];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15, kg = lane >> 4;
+    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * 64 + wave * 16;
+    const int row = static_cast<int>(blockIdx.y % A);
+    const int64_t sp = blockIdx.y / A;
+    const int64_t c_begin = sp * split_len;
+    const int64_t c_end = c_begin + split_len < kp ? c_begin + split_len : kp;
+    const int64_t o = o0 + lr;
+
+    // E, the greatest e_c; the split's greatest weight of the lane's channel.
+    int emax = kZeroChannel;
+    for (int64_t c = lane; c < a.ic; c += 64) emax = max(emax, e[c]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) emax = max(emax, __shfl_xor(emax, off, 64));
+    float wm = 0.0f;
+    for (int64_t c0 = c_begin; c0 < c_end; c0 += 16) {
+        float g[4][9];
+        load_kernels4(a, o, c0 + 4 * kg, g);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+            for (int q = 0; q < 9; ++q) wm = fmaxf(wm, fabsf(g[jj][q]));
+    }
+    wm = fmaxf(wm, __shfl_xor(wm, 16, 64));
+    wm = fmaxf(wm, __shfl_xor(wm, 32, 64));
+    const int ao = wm > 0.0f ? kTop - exponent_above(wm * Mat<M>::kWeightGain) : 0;
+    if (row == 0 && kg == 0 && o < a.oc) shift[sp * a.oc + o] = emax - ao;
+
+    // V's rows for 16 channels from c0: LDS row r = (j * 2 + part) * TP + tile,
+    // two 16-byte halves each; tiles past tp read tile 0 (never used).
+    const int64_t plane = tp * kp;
+    int4v vr[kLoads];
+    const auto load_v = [&](int64_t c0) {
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) {
+            int idx = tid + 256 * q;
+            idx = idx < kRows * 2 ? idx : kRows * 2 - 1;
+            const int r = idx >> 1, h = idx & 1;
+            const int jp = r / TP;
+            int t = r - jp * TP;
+            t = t < tp ? t : 0;
+            const int64_t xi = row * A + (jp >> 1);
+            vr[q] = *reinterpret_cast<const int4v *>(v + (2 * xi + (jp & 1)) * plane + t * kp + c0 + 8 * h);
+        }
+    };
+    const auto store_v = [&](_Float16 *buf) {
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) {
+            const int idx = tid + 256 * q;
+            if (idx < kRows * 2) {
+                const int r = idx >> 1, h = idx & 1;
+                *reinterpret_cast<int4v *>(buf + r * kSmallLd + 8 * h) = vr[q];
+            }
+        }
+    };
+
+    float4v acc[A][NT];
+#pragma unroll
+    for (int j = 0; j < A; ++j)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[j][t] = float4v{};
+
+    float g[4][9];
+    load_kernels4(a, o, c_begin + 4 * kg, g);
+    load_v(c_begin);
+    store_v(lds[0]);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t c0 = c_begin; c0 < c_end; c0 += 16, buf ^= 1) {
+        const bool more = c0 + 16 < c_end;
+        float gn[4][9];
+        if (more) {
+            load_kernels4(a, o, c0 + 16 + 4 * kg, gn);
+            load_v(c0 + 16);
+        }
+        const int64_t c = c0 + 4 * kg;  // the lane's four input channels
+        // Row `row` of G g G^T of each of the four kernels, scaled and split.
+        half4v uh[A], ul[A];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            float gg[3];
+#pragma unroll
+            for (int b = 0; b < 3; ++b)
+                gg[b] = Mat<M>::g(row, 0) * g[jj][b] + Mat<M>::g(row, 1) * g[jj][3 + b] +
+                        Mat<M>::g(row, 2) * g[jj][6 + b];
+            const int sc = (c + jj < a.ic) ? ao + e[c + jj] - emax : 0;
+#pragma unroll
+            for (int j = 0; j < A; ++j) {
+                const float u = gg[0] * Mat<M>::g(j, 0) + gg[1] * Mat<M>::g(j, 1) + gg[2] * Mat<M>::g(j, 2);
+                _Float16 hi, lo;
+                split2(ldexpf(u, sc), hi, lo);
+                uh[j][jj] = hi;
+                ul[j][jj] = lo;
+            }
+        }
+        const _Float16 *cur = lds[buf];
+#pragma unroll
+        for (int j = 0; j < A; ++j)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int tile = 16 * t + lr;
+                const half4v bh = *reinterpret_cast<const half4v *>(cur + ((2 * j) * TP + tile) * kSmallLd + 4 * kg);
+                const half4v bl =
+                    *reinterpret_cast<const half4v *>(cur + ((2 * j + 1) * TP + tile) * kSmallLd + 4 * kg);
+                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(uh[j], bh, acc[j][t], 0, 0, 0);
+                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(uh[j], bl, acc[j][t], 0, 0, 0);
+                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ul[j], bh, acc[j][t], 0, 0, 0);
+            }
+        if (more) {
+            store_v(lds[buf ^ 1]);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int q = 0; q < 9; ++q) g[jj][q] = gn[jj][q];
+        }
+        __syncthreads();
+    }
+    // Lane holds the sums of channels o0 + 4 kg + r, tile 16 t + lr; both
+    // operands were scaled by 2^-4 in the split.
+    const int64_t oplane = a.oc * tp;
+#pragma unroll
+    for (int j = 0; j < A; ++j) {
+        float *out = prod + (sp * A * A + row * A + j) * oplane;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t oo = o0 + 4 * kg + r;
+                if (oo < a.oc && 16 * t + lr < tp) out[oo * tp + 16 * t + lr] = acc[j][t][r] * (kSplitUp * kSplitUp);
+            }
+    }
+}
+
 // ------------------------------------------------------------------ host
 
 struct WorkLayout {
     int64_t kp;                          // IC padded to whole steps of K
+    bool small;                          // the small images' path
+    int64_t tp, splits, split_len;       // its tiles padded to 16, splits of the input channels
     size_t e, a, shift, u, v, m, total;  // byte offsets
 };
+
+// The small images' path: F(4x4) on the reference's small images (few tiles
+// in all, winograd.cc:194-196) of at most 32 tiles, FP16 kernels whose rows of
+// four channels are 8-byte aligned; not with winograd_fp32.  (F(2x2)'s
+// transformed weights are 16/9 of the FP16 ones, not 4: there the batched
+// products over written-out weights measure faster.)
+bool small_path(const WinogradArgs &a) {
+    return !tuning().winograd_fp32 && a.m == 4 && a.tiles <= kSmallTilesMax &&
+           a.n * ((a.ow + 1) / 2) * ((a.oh + 1) / 2) <= tuning().winograd_small_tiles && a.ic % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(a.w) & 7) == 0;
+}
 
 WorkLayout work_layout(const WinogradArgs &a) {
     const int64_t alpha2 = (a.m + 2) * (a.m + 2);
@@ -669,6 +918,26 @@ WorkLayout work_layout(const WinogradArgs &a) {
         at += static_cast<size_t>(round_up(bytes, 256));
         return here;
     };
+    l.small = small_path(a);
+    if (l.small) {
+        // Splits enough for about 2048 waves of A lanes groups, at most 4, of
+        // 64 channels or more.
+        l.tp = round_up(a.tiles, 16);
+        const int64_t waves = ceil_div(a.oc, 16) * (a.m + 2);  // of all the splits' blocks, per split
+        int64_t sp = ceil_div(2048, waves);
+        sp = sp < 1 ? 1 : (sp > 4 ? 4 : sp);
+        while (sp > 1 && l.kp / sp < 64) --sp;
+        l.split_len = round_up(ceil_div(l.kp, sp), 16);
+        l.splits = ceil_div(l.kp, l.split_len);
+        l.e = take(a.ic * 4);
+        l.a = take(a.oc * 4);
+        l.shift = take(l.splits * a.oc * 4);
+        l.u = at;
+        l.v = take(alpha2 * 2 * l.tp * l.kp * 2);
+        l.m = take(l.splits * alpha2 * a.oc * l.tp * 4);
+        l.total = at;
+        return l;
+    }
     // Either form: U as two FP16 planes or in single precision, V in single
     // precision, [xi][tile][kp] or [xi][ic][tile].
     l.e = take(a.ic * 4);
@@ -717,6 +986,35 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
                            nullptr);
         return launched(hipGetLastError(), "winograd");
+    }
+    if (M == 4 && l.small) {
+        {
+            KernelScope scope(names[0].c_str(), stream);  // the inputs' exponents only
+            hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.ic, 4))), dim3(256), 0,
+                               stream, a, e, a_oc);
+        }
+        _Float16 *vh = reinterpret_cast<_Float16 *>(v);
+        {
+            KernelScope scope(names[2].c_str(), stream);
+            hipLaunchKernelGGL((inputs_small_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(l.tp * l.kp, 256))),
+                               dim3(256), 0, stream, a, l.kp, l.tp, e, vh);
+        }
+        {
+            KernelScope scope(names[3].c_str(), stream);
+            const dim3 grid(static_cast<uint32_t>(ceil_div(a.oc, 64)), static_cast<uint32_t>(A * l.splits));
+            const dim3 block(256);
+            if (l.tp <= 16) {
+                hipLaunchKernelGGL((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.tp, l.split_len, e,
+                                   vh, m, shift);
+            } else {
+                hipLaunchKernelGGL((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.tp, l.split_len, e,
+                                   vh, m, shift);
+            }
+        }
+        KernelScope scope(names[4].c_str(), stream);
+        hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, shift,
+                           l.splits, l.tp);
+        return launched(hipGetLastError(), "winograd (small images)");
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
     {
