@@ -192,10 +192,8 @@ __global__ __launch_bounds__(256) void qa_queries_kernel(QAttentionArgs a) {
 
 // ------------------------------------------------------------------ attention
 
-// The most 16-byte steps of the scores' k (sd <= 256), of 16-key tiles of a
-// group (group <= 256), and of 16-dimension tiles of the output (dv <= 256).
+// The most 16-byte steps of the scores' k (sd <= 256).
 constexpr int kQaSteps = 4;
-constexpr int kQaTiles = 16;
 
 // The scores of key tile kt (keys 16 kt + 4 lg + r) for the lane's query:
 // the integer products over the sd bytes, restored, and scaled back.

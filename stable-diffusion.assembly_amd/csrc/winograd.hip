@@ -129,7 +129,7 @@ __device__ __forceinline__ float wave_max64(float v) {
 // every image, four independent float4 loads in flight per lane where the
 // rows are contiguous, and its exponent e[c] (zero channels: the least, so
 // that they scale to zero); waves [IC, IC + OC) output channel o's greatest
-// FP16 weight, eight at a time, and a[o].
+// FP16 weight, four loads of eight in flight per lane, and a[o].
 template <int M>
 __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__restrict__ e,
                                                      int32_t *__restrict__ amax) {
@@ -169,7 +169,19 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
         const _Float16 *p = a.w + o * count;
         if (count % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
             const half8 *q = reinterpret_cast<const half8 *>(p);
-            for (int64_t i = lane; i < count / 8; i += 64) {
+            const int64_t octs = count / 8;
+            int64_t i = lane;
+            for (; i + 192 < octs; i += 256) {
+                const half8 v0 = q[i], v1 = q[i + 64], v2 = q[i + 128], v3 = q[i + 192];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    m0 = fmaxf(m0, fabsf(static_cast<float>(v0[k])));
+                    m1 = fmaxf(m1, fabsf(static_cast<float>(v1[k])));
+                    m2 = fmaxf(m2, fabsf(static_cast<float>(v2[k])));
+                    m3 = fmaxf(m3, fabsf(static_cast<float>(v3[k])));
+                }
+            }
+            for (; i < octs; i += 64) {
                 const half8 v = q[i];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) m0 = fmaxf(m0, fabsf(static_cast<float>(v[k])));
@@ -177,7 +189,7 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
         } else {
             for (int64_t i = lane; i < count; i += 64) m0 = fmaxf(m0, fabsf(static_cast<float>(p[i])));
         }
-        const float m = wave_max64(m0);
+        const float m = wave_max64(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
         if (lane == 0) amax[o] = m > 0.0f ? kTop - exponent_above(m * Mat<M>::kWeightGain) : 0;
     }
 }

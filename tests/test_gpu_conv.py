@@ -184,3 +184,42 @@ def test_conv2d_bench_shapes(gpu, name, shape, k, s, p, want):
     print(f"{name}: path {path}, sampled error {err:.3g}")
     assert path == want
     assert err <= BOUND
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [
+    (64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2),   # F(4x4)
+    (8, 8, 96, 64, 3, 3, 1, 1, 1, 1, 1, 1, 2),     # F(2x2)
+])
+def test_winograd_graph_replays(gpu, c):
+    """The Winograd path captured into a HIP graph and replayed with eager
+    convolutions between the replays: every replay equals the eager result
+    bit for bit."""
+    w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
+    r = rng(21)
+    kh16, _ = weights_f16(r, (oc, ic, kh, kw))
+    x = uniform(r, (n, ic, h_, w_), 1.0)
+    k_d, x_d = dev(kh16, gpu), dev(x, gpu)
+    oh, ow = out_size(h_, kh, s1, p1, d1), out_size(w_, kw, s0, p0, d0)
+    params = sdhip.conv_params(s0, s1, p0, p1, d0, d1)
+    eager = torch.empty((n, oc, oh, ow), device=gpu)
+    sdhip.conv2d(k_d, x_d, eager, params)
+    torch.cuda.synchronize()
+    want = eager.cpu().numpy()
+    y = torch.zeros((n, oc, oh, ow), device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            sdhip.conv2d(k_d, x_d, y, params)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        other = torch.empty_like(eager)
+        sdhip.conv2d(k_d, x_d, other, params)
+        torch.cuda.synchronize()
+        assert np.array_equal(other.cpu().numpy().view(np.uint32), want.view(np.uint32))
