@@ -190,11 +190,14 @@ def attention_workload(dev, b, h, lq, lk, d, seed=0):
                       sdhip.desc(v.permute(0, 2, 1, 3)), sdhip.desc(y))
     scale = 1.0 / d ** 0.5
     stream = sdhip.stream_handle()
+    size = lib.sdhip_attention_work_size(dq, dk, dv, dy)  # the keys' and values' split tiles
+    work = torch.empty(max(size, 1), dtype=torch.uint8, device=dev)
+    ptr = work.data_ptr()
 
     def run():
-        sdhip.check(lib.sdhip_attention(dq, dk, dv, dy, scale, 0.0, 0.0, None, 0, stream), "attention")
+        sdhip.check(lib.sdhip_attention(dq, dk, dv, dy, scale, 0.0, 0.0, ptr, size, stream), "attention")
 
-    run.keep = (q, k, v, y)
+    run.keep = (q, k, v, y, work)
     return run, 4.0 * b * h * lq * lk * d
 
 

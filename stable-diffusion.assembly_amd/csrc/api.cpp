@@ -68,6 +68,7 @@ const Field kFields[] = {
     {"gemm_stages", &Tuning::gemm_stages},
     {"gemm_tiles", &Tuning::gemm_tiles},
     {"attention_generic", &Tuning::attention_generic},
+    {"attention_fp32", &Tuning::attention_fp32},
     {"attention_keys", &Tuning::attention_keys},
 };
 

@@ -59,6 +59,9 @@ QAttentionLayout qattention_layout(QAttentionArgs &a);
 hipError_t launch_quantized_attention(QAttentionArgs a, void *work, hipStream_t stream);
 
 size_t attention_lds_bytes(int64_t d, int64_t dv);
-hipError_t launch_attention(AttentionArgs a, hipStream_t stream);
+// The work buffer the attention takes (the split form's tiles of the keys and
+// values; nothing for the other forms), and the launch, `work` at least that.
+size_t attention_work_bytes(const AttentionArgs &a);
+hipError_t launch_attention(AttentionArgs a, void *work, hipStream_t stream);
 
 }  // namespace sdhip

@@ -25,6 +25,8 @@
 // (attention.cc:287-301), and the output is multiplied at the end by the
 // reciprocal of the sum rounded to single precision (attention.cc:1055-1062).
 
+#include <type_traits>
+
 #include "attention.h"
 #include "host.h"
 #include "profile.h"
@@ -403,6 +405,466 @@ __global__ __launch_bounds__(256, 2) void attention_fast_kernel(AttentionArgs a)
     }
 }
 
+// ------------------------------------------------------------------ the split form
+//
+// The fast form's operands on the FP16 MFMA, v_mfma_f32_32x32x16_f16, the
+// default.  Every single-precision key, query (times scale log2(e)) and value
+// x is taken as two FP16 parts, h = fp16(x 2^-4) and l = fp16((x 2^-4 - h)
+// 2^11), and every product as h h' + 2^-11 (h l' + l h'): h h' into one
+// accumulator, the two others into a second, the two added once the sum is
+// done.  That is 22 bits of each operand, the part l scaled into FP16's normal
+// range so that it keeps its 11 bits for any |x| above 2^-20.  The
+// exponentials, computed 2^11 times their value, are split as h + l with l
+// the plain remainder, h h' + l h' into the first accumulator; the
+// reference's metric stays at single precision's.
+//
+// Two launches.  The first splits the keys and values once, into the work
+// buffer, as tiles of KB keys laid out as the second's LDS holds them: the
+// keys' parts [KB][kLdk] twice, then the values' parts transposed,
+// [kDvp][kLdv] twice, keys past lk and dimensions past D zero.  The second
+// takes 32 queries a wave, 128 of one head a workgroup, and goes through the
+// tiles in order, copying each whole from the work buffer into a ring of NS
+// LDS buffers (global_load_lds_dwordx4, 1 KB an instruction, NS - 2 tiles
+// ahead of the MFMAs; one barrier a tile).  S^T = K Q^T by tiles of 32 keys by
+// the wave's 32 queries: lane l holds query l % 32, keys 8 (e / 4) + 4 (l /
+// 32) + e % 4 of its accumulator element e.  Those are the operand B of O^T
+// += V^T P^T as they stand when the MFMA's k index 8 (l / 32) + j of a chunk
+// of 16 keys is taken for key 8 (j / 4) + 4 (l / 32) + j % 4; the values'
+// columns are stored in that order of keys, so that a lane's eight keys of
+// operand A are one 16-byte read.  The queries' parts stay in registers
+// (operand B of S^T).  LDS rows are an odd number of 16-byte units long -- D
+// padded to 16 and 8 halves more for the keys, KB + 8 halves for the values --
+// which the MFMAs' reads of 32 rows take without bank conflicts.
+
+template <int D, int KB>
+struct Split {
+    static constexpr int kDp = (D + 15) / 16 * 16;  // dimensions of the keys and queries, padded
+    static constexpr int kSteps = kDp / 16;
+    static constexpr int kDvp = (D + 31) / 32 * 32;  // of the values, whole tiles of 32
+    static constexpr int kDvt = kDvp / 32;
+    static constexpr int kTiles = KB / 32;           // tiles of 32 keys
+    static constexpr int kLdk = kDp + 8;             // halves
+    static constexpr int kLdv = KB + 8;              // halves
+    static constexpr int kPlaneK = KB * kLdk;
+    static constexpr int kPlaneV = kDvp * kLdv;
+    static constexpr int kHalves = 2 * kPlaneK + 2 * kPlaneV;          // of a tile
+    static constexpr int kRecord = (2 * kHalves + 1023) / 1024 * 1024;  // bytes of a tile, whole KB
+    static constexpr int kCopies = kRecord / 1024;                      // 1 KB copies of a tile
+    static constexpr int kPerWave = (kCopies + 3) / 4;
+    static constexpr int kQueries = 128;  // a workgroup's
+    static_assert(D % 8 == 0 && KB % 32 == 0, "shape");
+    static_assert((kLdk / 8) % 2 == 1 && (kLdv / 8) % 2 == 1, "rows of an odd number of 16-byte units");
+};
+
+constexpr float kPartUp = 2048.0f;  // the part l's scale, 2^11
+constexpr float kPartDown = 1.0f / 2048.0f;
+
+typedef _Float16 half4a __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split_part(float x, _Float16 &h, _Float16 &l) {
+    h = static_cast<_Float16>(x);
+    l = static_cast<_Float16>((x - static_cast<float>(h)) * kPartUp);
+}
+
+// The key of column c of a tile's values: within a chunk of 16 columns,
+// column 8 g + s holds key 8 (s / 4) + 4 g + s % 4.
+__device__ __forceinline__ int key_of_column(int c) {
+    const int g = (c >> 3) & 1, s = c & 7;
+    return (c & ~15) + 8 * (s >> 2) + 4 * g + (s & 3);
+}
+
+// The tiles of the keys and values of every (image, head of the keys), one
+// workgroup a tile: grid (tiles, b hk).
+template <int D, int KB>
+__global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _Float16 *__restrict__ tiles) {
+    using S = Split<D, KB>;
+    const int64_t kt = blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    const int64_t bi = bh / a.hk, kh = bh - bi * a.hk;
+    const int64_t nk = gridDim.x;
+    _Float16 *rec = tiles + (bh * nk + kt) * (S::kRecord / 2);
+    const float *kg = static_cast<const float *>(a.k) + bi * a.knb3 + kh * a.knb2;
+    const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
+    // The keys: a thread a key's four dimensions, float4 loads.
+    for (int idx = threadIdx.x; idx < KB * (S::kLdk / 4); idx += 256) {
+        const int j = idx / (S::kLdk / 4);
+        const int c4 = idx - j * (S::kLdk / 4);
+        const int64_t key = kt * KB + j;
+        float4v x = float4v{};
+        if (key < a.lk && 4 * c4 < D) x = *reinterpret_cast<const float4v *>(kg + key * a.knb1 + 4 * c4);
+        half4a h, l;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            _Float16 hh, ll;
+            split_part(x[r] * kSplitDown, hh, ll);
+            h[r] = hh;
+            l[r] = ll;
+        }
+        *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = h;
+        *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
+    }
+    // The values, transposed through LDS: rows read as float4, then a thread
+    // four columns (four consecutive keys) of a dimension, consecutive threads
+    // consecutive columns.
+    __shared__ __attribute__((aligned(16))) float vt[KB][D + 4];
+    for (int idx = threadIdx.x; idx < KB * (D / 4); idx += 256) {
+        const int j = idx / (D / 4);
+        const int c4 = idx - j * (D / 4);
+        const int64_t key = kt * KB + j;
+        float4v x = float4v{};
+        if (key < a.lk) x = *reinterpret_cast<const float4v *>(vg + key * a.vnb1 + 4 * c4);
+        *reinterpret_cast<float4v *>(&vt[j][4 * c4]) = x;
+    }
+    __syncthreads();
+    _Float16 *vh = rec + 2 * S::kPlaneK;
+    for (int idx = threadIdx.x; idx < S::kDvp * (S::kLdv / 4); idx += 256) {
+        const int dim = idx / (S::kLdv / 4);
+        const int c4 = idx - dim * (S::kLdv / 4);
+        half4a h, l;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = 4 * c4 + u;
+            const float x = c < KB && dim < D ? vt[key_of_column(c)][dim] : 0.0f;
+            _Float16 hh, ll;
+            split_part(x * kSplitDown, hh, ll);
+            h[u] = hh;
+            l[u] = ll;
+        }
+        *reinterpret_cast<half4a *>(vh + dim * S::kLdv + 4 * c4) = h;
+        *reinterpret_cast<half4a *>(vh + S::kPlaneV + dim * S::kLdv + 4 * c4) = l;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// One 16-byte piece a lane of a 1 KB copy from global memory into LDS; the
+// LDS address is the wave's (lane l's piece lands 16 l bytes past it).
+__device__ __forceinline__ void copy_lds(const void *src, char *lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
+// The online softmax of the wave's scores over KB keys, in base 2: the
+// accumulators hold the products of the keys by the queries times scale
+// log2(e), scaled by 2^-8 (the keys' and queries' 2^-4), as sh + 2^-11 sx;
+// with MASK, keys from `valid` on are masked.  The running maximum m, in that
+// scaled unit, moves only when a score passes it by more than 2^4 in
+// exponential, so that the output's accumulators are rescaled (by exp2(256
+// (old max - new max))) seldom, and only while some query's maximum moves.
+// The exponentials go to p as 2^11 exp2(256 (x - m)), below 2^15 -- the 2^11
+// so that their low FP16 parts stay normal down to exponentials of 2^-14,
+// below which they weigh less than the rounding of the sum -- and their sum
+// into l, taken 16 at a time as a tree in single precision and added in
+// double.
+template <bool MASK, int KT, int DVT>
+__device__ __forceinline__ void split_softmax(const float16v (&sh)[KT], const float16v (&sx)[KT], float (&p)[KT][16],
+                                              float &m, double &l, float16v (&oh)[DVT], float16v (&ol)[DVT],
+                                              int valid, int g) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float x = __builtin_fmaf(sx[t][e], kPartDown, sh[t][e]);
+            if (MASK && 32 * t + tile_row(e) + 4 * g >= valid) x = -INFINITY;
+            p[t][e] = x;
+            mx = fmaxf(mx, x);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = mx > m + 4.0f / 256.0f ? mx : m;
+    const float shift = mnew * 256.0f - 11.0f;
+    double part = 0.0;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) p[t][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][e], 256.0f, -shift));
+        float a8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a8[u] = p[t][2 * u] + p[t][2 * u + 1];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a8[u] = a8[2 * u] + a8[2 * u + 1];
+        part += static_cast<double>((a8[0] + a8[1]) + (a8[2] + a8[3]));
+    }
+    // The rescaling last, so that the work above shares its basic block with
+    // whatever the caller put before this (the test of the sum, always true
+    // but for a NaN, keeps the branch below the exponentials).
+    if (__ballot(mnew != m && part >= 0.0) != 0) {
+        const float alpha = __builtin_amdgcn_exp2f((m - mnew) * 256.0f);  // 0 while m is -inf
+        l *= static_cast<double>(alpha);
+#pragma unroll
+        for (int c = 0; c < DVT; ++c) {
+            oh[c] *= alpha;
+            ol[c] *= alpha;
+        }
+        m = mnew;
+    }
+    l += part;
+}
+
+template <int D, int KB, int NS, int OCC, bool PIPE>
+__global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs a, const char *__restrict__ tiles) {
+    using S = Split<D, KB>;
+    static_assert(NS >= 3 && (NS - 2) * S::kPerWave < 64, "stages");
+    extern __shared__ __attribute__((aligned(1024))) char sbuf[];  // NS tiles of S::kRecord bytes
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 31;  // the lane's query, or its row of operand A
+    const int g = lane >> 5;   // the lane's half of the wave
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t qb = b % static_cast<uint32_t>(a.qblocks);
+    const uint32_t bh = b / static_cast<uint32_t>(a.qblocks);
+    const int64_t hi = bh % a.h;
+    const int64_t bi = bh / a.h;
+    const int64_t kh = hi / (a.h / a.hk);
+    const int64_t q0 = static_cast<int64_t>(qb) * S::kQueries + wave * 32;
+    const int64_t nk = (a.lk + KB - 1) / KB;
+    const char *head = tiles + (bi * a.hk + kh) * nk * S::kRecord;
+
+    // Tile `t` into LDS buffer `stage`: the wave's kPerWave copies of 1 KB
+    // (those past the tile's last repeat it).
+    // The wave's index as a scalar, so that the copies' addresses are a
+    // scalar base and the lane's fixed 16-byte offset.
+    const int swave = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;
+    const auto issue = [&](int stage, int64_t t) {
+        const char *src = head + t * S::kRecord;
+#pragma unroll
+        for (int i = 0; i < S::kPerWave; ++i) {
+            int c = swave + 4 * i;
+            c = c < S::kCopies ? c : S::kCopies - 1;
+            copy_lds(src + c * 1024 + lane16, sbuf + stage * S::kRecord + c * 1024);
+        }
+    };
+    // The wave's queries, operand B of S^T: lane (query lr, half g) holds
+    // dimensions 16 st + 8 g .. + 7 at step st.  Queries past lq read the last.
+    half8 qh[S::kSteps], ql[S::kSteps];
+    const float qscale = a.scale * 1.44269504088896341f;  // scale log2(e), folded into the queries
+    {
+        int64_t i = q0 + lr;
+        i = i < a.lq ? i : a.lq - 1;
+        const float *qp = a.q + bi * a.qnb3 + hi * a.qnb2 + i * a.qnb1;
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int dim = 16 * st + 8 * g + j;
+                _Float16 h, l;
+                split_part(dim < D ? (qp[dim] * qscale) * kSplitDown : 0.0f, h, l);
+                qh[st][j] = h;
+                ql[st][j] = l;
+            }
+    }
+
+    float16v oh[S::kDvt], ol[S::kDvt];
+#pragma unroll
+    for (int c = 0; c < S::kDvt; ++c) {
+        oh[c] = float16v{};
+        ol[c] = float16v{};
+    }
+    float m = -INFINITY;
+    double l = 0.0;
+
+    // The ring: tile t in buffer t % NS.  With PIPE the scores of tile t + 1
+    // are taken while the exponentials of tile t are (the MFMAs of the one
+    // beside the VALU work of the other), so a buffer is free once the
+    // products by the values of the tile before the one being scored are
+    // done: tile t + NS - 2 is copied once tile t is in.  Without, tile t +
+    // NS - 1 is.
+    constexpr int kAhead = PIPE ? NS - 2 : NS - 1;
+    const auto sync = [&](int64_t t) {
+        // The wave's copies of tile t are done once at most kAhead - 1
+        // tiles' copies are outstanding after them (none, near the end);
+        // every wave's are, past the barrier, which also ends every wave's
+        // reads of the buffer the next copies go to.
+        if (t + kAhead - 1 < nk) {
+            wait_loads<(kAhead - 1) * S::kPerWave>();
+        } else {
+            wait_loads<0>();
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + kAhead < nk) issue(static_cast<int>((t + kAhead) % NS), t + kAhead);
+    };
+    // S^T of tile t.
+    const auto scores = [&](int64_t t, float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
+        const _Float16 *kbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord);
+#pragma unroll
+        for (int u = 0; u < S::kTiles; ++u) {
+            sh[u] = float16v{};
+            sx[u] = float16v{};
+        }
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st)
+#pragma unroll
+            for (int u = 0; u < S::kTiles; ++u) {
+                const _Float16 *kp = kbuf + (32 * u + lr) * S::kLdk + 16 * st + 8 * g;
+                const half8 ka = *reinterpret_cast<const half8 *>(kp);
+                const half8 kl = *reinterpret_cast<const half8 *>(kp + S::kPlaneK);
+                sh[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[st], sh[u], 0, 0, 0);
+                sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[st], sx[u], 0, 0, 0);
+                sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[st], sx[u], 0, 0, 0);
+            }
+    };
+    // O^T += V^T P^T of tile t, a chunk of 16 keys at a time: the lane's
+    // eight exponentials 8 c .. 8 c + 7 of a tile of 32 are its operand B.
+    const auto values = [&](int64_t t, const float (&p)[S::kTiles][16]) {
+        const _Float16 *vbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord) + 2 * S::kPlaneK;
+#pragma unroll
+        for (int u = 0; u < S::kTiles; ++u)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                // The exponentials (2^11 times, below 2^15) as two FP16 parts,
+                // the second the remainder of the first, in pairs.
+                half8 ph, pl;
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const float x0 = p[u][8 * c + j], x1 = p[u][8 * c + j + 1];
+                    const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+                    const auto r =
+                        __builtin_amdgcn_cvt_pkrtz(x0 - static_cast<float>(h[0]), x1 - static_cast<float>(h[1]));
+                    ph[j] = h[0];
+                    ph[j + 1] = h[1];
+                    pl[j] = r[0];
+                    pl[j + 1] = r[1];
+                }
+#pragma unroll
+                for (int dt = 0; dt < S::kDvt; ++dt) {
+                    const _Float16 *vp = vbuf + (32 * dt + lr) * S::kLdv + 32 * u + 16 * c + 8 * g;
+                    const half8 va = *reinterpret_cast<const half8 *>(vp);
+                    const half8 vl = *reinterpret_cast<const half8 *>(vp + S::kPlaneV);
+                    oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, oh[dt], 0, 0, 0);
+                    oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, oh[dt], 0, 0, 0);
+                    ol[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, ol[dt], 0, 0, 0);
+                }
+            }
+    };
+
+    // The first kAhead tiles on their way, once the queries are in; then
+    // every tile but the last (with PIPE, the next one's scores beside it),
+    // and the last, masked where it is not full.
+#pragma unroll
+    for (int st = 0; st < kAhead; ++st) {
+        if (st < nk) issue(st, st);
+    }
+    const auto last = [&](float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
+        float p[S::kTiles][16];
+        const int valid = static_cast<int>(a.lk - (nk - 1) * KB);
+        if (valid < KB) {
+            split_softmax<true, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, valid, g);
+        } else {
+            split_softmax<false, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+        }
+        values(nk - 1, p);
+    };
+    if constexpr (PIPE) {
+        // Two sets of scores, a and b, taking turns (no copies between them).
+        float16v sa[S::kTiles], xa[S::kTiles], sb[S::kTiles], xb[S::kTiles];
+        const auto step = [&](int64_t it, float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles],
+                              float16v (&nh)[S::kTiles], float16v (&nx)[S::kTiles]) {
+            sync(it + 1);
+            scores(it + 1, nh, nx);
+            float p[S::kTiles][16];
+            split_softmax<false, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+            values(it, p);
+        };
+        sync(0);
+        scores(0, sa, xa);
+        int64_t it = 0;
+        for (; it + 2 < nk; it += 2) {
+            step(it, sa, xa, sb, xb);
+            step(it + 1, sb, xb, sa, xa);
+        }
+        if (it + 1 < nk) {
+            step(it, sa, xa, sb, xb);
+            last(sb, xb);
+        } else {
+            last(sa, xa);
+        }
+    } else {
+        float16v sh[S::kTiles], sx[S::kTiles];
+        for (int64_t it = 0; it + 1 < nk; ++it) {
+            sync(it);
+            scores(it, sh, sx);
+            float p[S::kTiles][16];
+            split_softmax<false, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+            values(it, p);
+        }
+        sync(nk - 1);
+        scores(nk - 1, sh, sx);
+        last(sh, sx);
+    }
+
+    // The query's sum over its two lanes; lane holds O^T[32 dt + 8 (e / 4) +
+    // 4 g + e % 4][lr], and the values' 2^-4 comes back with the reciprocal.
+    double sum = l;
+    sum += __shfl_xor(sum, 32, 64);
+    const float reciprocal = static_cast<float>(1.0 / sum);
+    const int64_t i = q0 + lr;
+    if (i >= a.lq) return;
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
+#pragma unroll
+    for (int dt = 0; dt < S::kDvt; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const int dim = 32 * dt + 8 * e4 + 4 * g;
+            if (dim < D) {
+                float4v r;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    r[u] = ((oh[dt][4 * e4 + u] + ol[dt][4 * e4 + u] * kPartDown) * 16.0f) * reciprocal;
+                }
+                *reinterpret_cast<float4v *>(out + dim) = r;
+            }
+        }
+}
+
+// The split form's shape for head size D: its tiles' keys, the stages of its
+// ring, the workgroups a CU holds at least.
+template <int D>
+struct SplitShape {
+    static constexpr int kKeys = 32;
+    static constexpr int kStages = D <= 64 ? 4 : 3;
+    static constexpr int kOcc = D <= 96 ? 2 : 1;
+    static constexpr bool kPipe = D <= 64;  // registers for two sets of scores
+};
+
+template <int D>
+size_t split_work(const AttentionArgs &a) {
+    using S = Split<D, SplitShape<D>::kKeys>;
+    return static_cast<size_t>(a.b * a.hk) * static_cast<size_t>(ceil_div(a.lk, SplitShape<D>::kKeys)) * S::kRecord;
+}
+
+template <int D>
+hipError_t launch_split(AttentionArgs a, void *work, hipStream_t stream) {
+    using SH = SplitShape<D>;
+    using S = Split<D, SH::kKeys>;
+    const int64_t nk = ceil_div(a.lk, SH::kKeys);
+    {
+        KernelScope scope("attention.tiles", stream);
+        hipLaunchKernelGGL((attention_tiles_kernel<D, SH::kKeys>),
+                           dim3(static_cast<uint32_t>(nk), static_cast<uint32_t>(a.b * a.hk)), dim3(256), 0, stream,
+                           a, static_cast<_Float16 *>(work));
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+    }
+    a.qblocks = ceil_div(a.lq, S::kQueries);
+    const size_t lds = static_cast<size_t>(SH::kStages) * S::kRecord;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
+    dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
+    KernelScope scope("attention", stream);
+    hipLaunchKernelGGL((attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe>), grid, block, lds, stream, a,
+                       static_cast<const char *>(work));
+    return hipGetLastError();
+}
+
 template <int D, int QT, int KB>
 hipError_t launch_fast(AttentionArgs a, hipStream_t stream) {
     using F = Fast<D, QT, KB>;
@@ -423,6 +885,36 @@ bool fast_form(const AttentionArgs &a) {
     return size && a.d == a.dv && !a.khalf && !a.vhalf && aligned16(a.k) && aligned16(a.v) && aligned16(a.y) &&
            a.knb1 % 4 == 0 && a.knb2 % 4 == 0 && a.knb3 % 4 == 0 && a.vnb1 % 4 == 0 && a.vnb2 % 4 == 0 &&
            a.vnb3 % 4 == 0 && a.ynb1 % 4 == 0 && a.ynb2 % 4 == 0 && a.ynb3 % 4 == 0;
+}
+
+// Whether the split form takes the operands: the fast form's, unless the
+// tuning asks for another.
+bool split_form(const AttentionArgs &a) {
+    return fast_form(a) && a.lk > 0 && tuning().attention_generic == 0 && tuning().attention_fp32 == 0;
+}
+
+size_t split_form_work(const AttentionArgs &a) {
+    switch (a.d) {
+    case 32: return split_work<32>(a);
+    case 40: return split_work<40>(a);
+    case 64: return split_work<64>(a);
+    case 80: return split_work<80>(a);
+    case 96: return split_work<96>(a);
+    case 128: return split_work<128>(a);
+    default: return split_work<160>(a);
+    }
+}
+
+hipError_t launch_split_form(AttentionArgs a, void *work, hipStream_t stream) {
+    switch (a.d) {
+    case 32: return launch_split<32>(a, work, stream);
+    case 40: return launch_split<40>(a, work, stream);
+    case 64: return launch_split<64>(a, work, stream);
+    case 80: return launch_split<80>(a, work, stream);
+    case 96: return launch_split<96>(a, work, stream);
+    case 128: return launch_split<128>(a, work, stream);
+    default: return launch_split<160>(a, work, stream);
+    }
 }
 
 hipError_t launch_fast_form(AttentionArgs a, hipStream_t stream) {
@@ -461,8 +953,14 @@ size_t attention_lds_bytes(int64_t d, int64_t dv) {
     return sizeof(float) * static_cast<size_t>(kQueries * (dp + 1) + kKeys * (dp + 1) + kKeys * (16 * 16 + 4));
 }
 
-hipError_t launch_attention(AttentionArgs a, hipStream_t stream) {
+size_t attention_work_bytes(const AttentionArgs &a) {
+    if (a.lq == 0 || a.h == 0 || a.b == 0 || a.lk == 0) return 0;
+    return split_form(a) ? split_form_work(a) : 0;
+}
+
+hipError_t launch_attention(AttentionArgs a, void *work, hipStream_t stream) {
     if (a.lq == 0 || a.h == 0 || a.b == 0) return hipSuccess;  // no output
+    if (split_form(a)) return launch_split_form(a, work, stream);
     if (fast_form(a) && tuning().attention_generic == 0) return launch_fast_form(a, stream);
     a.dp = static_cast<int>(round_up(a.d, 4));
     a.ldq = a.dp + 1;

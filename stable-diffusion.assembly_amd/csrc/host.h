@@ -37,6 +37,10 @@ struct Tuning {
     // fast one takes the operands (0), for comparison; results agree within
     // the same bound.
     int attention_generic = 0;
+    // This library's own: attention's products on the single-precision MFMA
+    // (1) instead of split FP16 parts (0), for comparison; results agree
+    // within the same bound.
+    int attention_fp32 = 0;
     // The keys of a stretch of attention's second product (kernels.h:107):
     // with bits, it sets where the exponentials switch to std::exp.
     int attention_keys = 256;

@@ -66,54 +66,9 @@ QAttentionArgs qargs_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhi
     return a;
 }
 
-}  // namespace
-
-extern "C" {
-
-int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
-                              const sdhip_tensor *y, float max_bias, float softcap) {
-    if (q == nullptr || k == nullptr || v == nullptr || y == nullptr) return 0;
-    // No mask, ALiBi or soft cap; q single precision, k and v single
-    // precision or FP16, each of elements one after another along ne[0]; the
-    // heads of q a multiple of those of k (attention.cc:828-845).  Heads of
-    // more than kAttentionMaxDims dimensions are left to the caller.
-    const bool shapes = q->ne[0] == k->ne[0] && k->ne[1] == v->ne[1] && k->ne[2] == v->ne[2] && k->ne[2] > 0 &&
-                        q->ne[2] % k->ne[2] == 0 && q->ne[3] == k->ne[3] && q->ne[3] == v->ne[3] && k->ne[1] >= 1 &&
-                        y->ne[0] == v->ne[0] && y->ne[1] == q->ne[2] && y->ne[2] == q->ne[1] && y->ne[3] == q->ne[3];
-    return max_bias == 0.0f && softcap == 0.0f && holds_f32(q) && kv_type(k) && kv_type(v) && holds_f32(y) &&
-           contiguous(y) && shapes && q->ne[0] <= kAttentionMaxDims && v->ne[0] <= kAttentionMaxDims &&
-           q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 && q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 &&
-           k->nb[2] % k->nb[0] == 0 && k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 &&
-           v->nb[2] % v->nb[0] == 0 && v->nb[3] % v->nb[0] == 0;
-}
-
-size_t sdhip_attention_work_size(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
-                                 const sdhip_tensor *y) {
-    if (!sdhip_attention_supported(q, k, v, y, 0.0f, 0.0f) || !quantized_attention(k)) return 0;
-    QAttentionArgs a = qargs_of(q, k, v, y, 1.0f);
-    return qattention_layout(a).total;
-}
-
-sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
-                             const sdhip_tensor *y, float scale, float max_bias, float softcap, void *work,
-                             size_t work_size, void *stream) {
-    if (!sdhip_attention_supported(q, k, v, y, max_bias, softcap)) {
-        return fail(SDHIP_UNSUPPORTED, "attention: operands not taken");
-    }
-    if (quantized_attention(k)) {
-        QAttentionArgs qa = qargs_of(q, k, v, y, scale);
-        if (qa.group % 16 != 0 || qa.group > 256) {
-            return fail(SDHIP_UNSUPPORTED, "attention: quantized groups of %lld keys (a multiple of 16 up to 256 "
-                                           "is taken)", static_cast<long long>(qa.group));
-        }
-        const size_t need = qattention_layout(qa).total;
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "attention: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
-        if (qa.lq == 0 || qa.h == 0 || qa.b == 0) return SDHIP_OK;
-        return launched(launch_quantized_attention(qa, work, static_cast<hipStream_t>(stream)),
-                        "quantized attention");
-    }
+// The launch's description of the operands (ggml's ne and nb, in elements).
+AttentionArgs args_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v, const sdhip_tensor *y,
+                      float scale) {
     AttentionArgs a{};
     a.q = static_cast<const float *>(q->data);
     a.qnb1 = q->nb[1] / 4;
@@ -141,7 +96,64 @@ sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const
     a.hk = k->ne[2];
     a.b = q->ne[3];
     a.scale = scale;
-    return launched(launch_attention(a, static_cast<hipStream_t>(stream)), "attention");
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                              const sdhip_tensor *y, float max_bias, float softcap) {
+    if (q == nullptr || k == nullptr || v == nullptr || y == nullptr) return 0;
+    // No mask, ALiBi or soft cap; q single precision, k and v single
+    // precision or FP16, each of elements one after another along ne[0]; the
+    // heads of q a multiple of those of k (attention.cc:828-845).  Heads of
+    // more than kAttentionMaxDims dimensions are left to the caller.
+    const bool shapes = q->ne[0] == k->ne[0] && k->ne[1] == v->ne[1] && k->ne[2] == v->ne[2] && k->ne[2] > 0 &&
+                        q->ne[2] % k->ne[2] == 0 && q->ne[3] == k->ne[3] && q->ne[3] == v->ne[3] && k->ne[1] >= 1 &&
+                        y->ne[0] == v->ne[0] && y->ne[1] == q->ne[2] && y->ne[2] == q->ne[1] && y->ne[3] == q->ne[3];
+    return max_bias == 0.0f && softcap == 0.0f && holds_f32(q) && kv_type(k) && kv_type(v) && holds_f32(y) &&
+           contiguous(y) && shapes && q->ne[0] <= kAttentionMaxDims && v->ne[0] <= kAttentionMaxDims &&
+           q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 && q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 &&
+           k->nb[2] % k->nb[0] == 0 && k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 &&
+           v->nb[2] % v->nb[0] == 0 && v->nb[3] % v->nb[0] == 0;
+}
+
+size_t sdhip_attention_work_size(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                                 const sdhip_tensor *y) {
+    if (!sdhip_attention_supported(q, k, v, y, 0.0f, 0.0f)) return 0;
+    if (!quantized_attention(k)) return attention_work_bytes(args_of(q, k, v, y, 1.0f));
+    QAttentionArgs a = qargs_of(q, k, v, y, 1.0f);
+    return qattention_layout(a).total;
+}
+
+sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
+                             const sdhip_tensor *y, float scale, float max_bias, float softcap, void *work,
+                             size_t work_size, void *stream) {
+    if (!sdhip_attention_supported(q, k, v, y, max_bias, softcap)) {
+        return fail(SDHIP_UNSUPPORTED, "attention: operands not taken");
+    }
+    if (quantized_attention(k)) {
+        QAttentionArgs qa = qargs_of(q, k, v, y, scale);
+        if (qa.group % 16 != 0 || qa.group > 256) {
+            return fail(SDHIP_UNSUPPORTED, "attention: quantized groups of %lld keys (a multiple of 16 up to 256 "
+                                           "is taken)", static_cast<long long>(qa.group));
+        }
+        const size_t need = qattention_layout(qa).total;
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "attention: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        if (qa.lq == 0 || qa.h == 0 || qa.b == 0) return SDHIP_OK;
+        return launched(launch_quantized_attention(qa, work, static_cast<hipStream_t>(stream)),
+                        "quantized attention");
+    }
+    const AttentionArgs a = args_of(q, k, v, y, scale);
+    const size_t need = attention_work_bytes(a);
+    if (need > 0 && (work == nullptr || work_size < need)) {
+        return fail(SDHIP_ERROR, "attention: work buffer of %zu bytes, %zu needed", work_size, need);
+    }
+    return launched(launch_attention(a, work, static_cast<hipStream_t>(stream)), "attention");
 }
 
 }  // extern "C"

@@ -106,3 +106,22 @@ def test_attention_generic_form(gpu, c):
     err = orc.metric(y, exact, mag)
     print(f"attention generic {c}: {err:.3g}")
     assert err <= BOUND
+
+
+@pytest.mark.gpu
+def test_attention_work_buffer_checked(gpu):
+    """The split form's tiles of keys and values go to the work buffer: a
+    buffer short of sdhip_attention_work_size is an error, not a launch."""
+    lib = sdhip.load()
+    q = torch.zeros((1, 64, 2, 40), device=gpu)
+    y = torch.zeros((1, 64, 2, 40), device=gpu)
+    dq, dy = sdhip.desc(q.permute(0, 2, 1, 3)), sdhip.desc(y)
+    size = lib.sdhip_attention_work_size(dq, dq, dq, dy)
+    assert size > 0
+    work = torch.zeros(size, dtype=torch.uint8, device=gpu)
+    status = lib.sdhip_attention(dq, dq, dq, dy, 0.1, 0.0, 0.0, work.data_ptr(), size - 1, sdhip.stream_handle())
+    assert status == sdhip.ERROR
+    assert b"work buffer" in lib.sdhip_last_error()
+    sdhip.check(lib.sdhip_attention(dq, dq, dq, dy, 0.1, 0.0, 0.0, work.data_ptr(), size, sdhip.stream_handle()),
+                "attention")
+    torch.cuda.synchronize()

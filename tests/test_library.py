@@ -49,7 +49,8 @@ def test_tuning_parses_like_sdasm_tune():
     # The reference's defaults (sources/kernels.h:91-135).
     for name, value in (("bits", 0), ("input_bits", 8), ("group", 64), ("weight_group", 1), ("quantize", 7),
                         ("winograd", 2), ("winograd_positions", 1024), ("winograd4_positions", 256),
-                        ("winograd_small_tiles", 256), ("fuse", 1), ("attention_keys", 256)):
+                        ("winograd_small_tiles", 256), ("fuse", 1), ("attention_keys", 256),
+                        ("attention_fp32", 0), ("attention_generic", 0)):
         assert sdhip.get_tuning(name) == value
 
 
@@ -129,6 +130,29 @@ def test_attention_and_norm_predicates():
     assert lib.sdhip_group_norm_supported(x, x, 32)
     assert not lib.sdhip_group_norm_supported(x, x, 0)
     assert lib.sdhip_norm_supported(tensor(F32, (2, 988, 1280)), tensor(F32, (2, 988, 1280)))
+
+
+def test_attention_work_size():
+    """The split form takes the keys and values split into tiles of 32 keys in
+    the work buffer: per (image, head) and tile, the keys' two FP16 parts of
+    32 rows of 48 + 8 halves and the values' two parts of 64 rows of 32 + 8
+    halves at head size 40 -- 17408 bytes; the other forms take none."""
+    lib = sdhip.load()
+    q = tensor(F32, (2, 8, 4096, 40))
+    k = tensor(F32, (2, 8, 4096, 40))
+    y = tensor(F32, (2, 4096, 8, 40))
+    assert lib.sdhip_attention_work_size(q, k, k, y) == 2 * 8 * 128 * 17408
+    k77 = tensor(F32, (2, 8, 77, 40))
+    assert lib.sdhip_attention_work_size(q, k77, k77, y) == 2 * 8 * 3 * 17408
+    try:
+        sdhip.set_tuning("attention_fp32=1")
+        assert lib.sdhip_attention_work_size(q, k, k, y) == 0
+        sdhip.set_tuning("attention_generic=1")
+        assert lib.sdhip_attention_work_size(q, k, k, y) == 0
+    finally:
+        sdhip.set_tuning("")
+    k16 = tensor(F16, (2, 8, 4096, 40))
+    assert lib.sdhip_attention_work_size(q, k16, k16, y) == 0  # FP16 keys: the generic form
 
 
 def test_bench_refuses_several_gpus():
