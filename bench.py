@@ -101,6 +101,27 @@ def profiled_traffic(workload, kernel):
     return None
 
 
+_ARENA = None
+
+
+def fresh_store(dev, gib=6):
+    """The device store's arena, emptied: the derived forms of the weights
+    (Winograd's transformed weights, the bits mode's quantized ones) kept from
+    one call to the next, as the reference keeps them in its store by default
+    (store.cc:64-99, 8 GiB; winograd.cc:2147-2149) -- the first, untimed call
+    fills it.  Emptied per workload, so that no entry outlives the tensors it
+    was made from."""
+    import torch
+
+    import sdhip
+
+    global _ARENA
+    if _ARENA is None:
+        _ARENA = torch.empty(gib << 30, dtype=torch.uint8, device=dev)
+    sdhip.store_arena(_ARENA)
+    return _ARENA
+
+
 def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupnorm=False, seed=0):
     """The convolution of a configuration with its chain, ready to run."""
     import torch
@@ -135,7 +156,8 @@ def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupn
         gn_work = torch.empty(max(gn_size, 8), dtype=torch.uint8, device=dev)
         gn = (out, sdhip.epilogue([("mul", gamma), ("add", beta), ("silu", None)]), sdhip.desc(out), gn_work, gn_size)
     stream = sdhip.stream_handle()
-    keep = (x, kern, y, steps, work)
+    arena = fresh_store(dev)
+    keep = (x, kern, y, steps, work, arena)
 
     def run():
         sdhip.check(lib.sdhip_conv2d(dk, dx, dy, params, ctypes.byref(chain), ctypes.c_void_p(work.data_ptr()),
@@ -222,7 +244,10 @@ def unet_workload(dev, seed=7):
     import unet_step
 
     model = unet_step.Model(unet_step.Config(), dev, seed=seed)
-    return unet_step.Step(model, unet_step.HipOps(dev), model.inputs(seed=seed + 1))
+    arena = fresh_store(dev)
+    step = unet_step.Step(model, unet_step.HipOps(dev), model.inputs(seed=seed + 1))
+    step.keep = (model, arena)
+    return step
 
 
 def sdxl_block_workload(dev, tuning="bits=8,weight_group=0", seed=9):
@@ -240,8 +265,7 @@ def sdxl_block_workload(dev, tuning="bits=8,weight_group=0", seed=9):
     ops = unet_step.HipOps(dev)
     # The quantized weights kept from one step to the next, as the reference
     # keeps its quantized layouts by default (store.cc:64-99).
-    arena = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-    sdhip.store_arena(arena)
+    arena = fresh_store(dev)
 
     def fn():
         sdhip.set_tuning(tuning)

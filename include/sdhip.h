@@ -85,8 +85,8 @@ const char *sdhip_last_error(void);
  * bits, input_bits, group, weight_group, quantize, winograd,
  * winograd_positions, winograd4_positions, winograd_small_tiles, fuse,
  * attention_keys; and this library's own: winograd_fp32, gemm_stages,
- * gemm_tiles, attention_generic (forms to compare, same results within the
- * bounds).  Returns SDHIP_ERROR naming the first unknown name.  "" resets
+ * gemm_tiles, attention_generic, attention_fp32 (forms to compare, same
+ * results within the bounds).  Returns SDHIP_ERROR naming the first unknown name.  "" resets
  * the defaults. */
 sdhip_status sdhip_set_tuning(const char *text);
 /* The value of one tuning field, or -1 if it has no such name. */
@@ -173,7 +173,11 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
  * [d, lq, h, b] F32 (any strides, nb[0] = 4), k ne = [d, lk, hk, b] and v ne =
  * [dv, lk, hk, b] F32 or F16, y ne = [dv, h, lq, b] F32 contiguous; head h
  * reads key head h / (h / hk).  scale, max_bias and softcap are op_params[0..2];
- * only max_bias = softcap = 0 is taken.  Replaces attention_supported /
+ * only max_bias = softcap = 0 is taken.  The work buffer: in the bits mode
+ * the quantized operands; otherwise, for single-precision keys and values of
+ * the head sizes 32, 40, 64, 80, 96, 128 and 160, the keys and values split
+ * into FP16 parts, tile by tile (0 for the other forms).  A buffer short of
+ * sdhip_attention_work_size is SDHIP_ERROR.  Replaces attention_supported /
  * attention_work_size / attention_compute (ops.h:51-56). */
 int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
                               const sdhip_tensor *y, float max_bias, float softcap);

@@ -24,8 +24,8 @@
 //   MUL_MAT:     A = x (tokens, split), B = W (features): C[token][feature]
 //   convolution: A = W (output channels), B = the image's columns (split),
 //                C[channel][position]
-//   Winograd:    A = U[xi] (output channels, split by the transform),
-//                B = V[xi] (tiles, split here)
+//   Winograd:    A = U[xi] (output channels; single precision, each
+//                column scaled and split here), B = V[xi] (tiles, split here)
 // so that the output's contiguous dimension is always C's column, lane % 32
 // of the MFMA's result, and a wave's stores are 128-byte rows.
 
@@ -159,6 +159,39 @@ struct F32Rows {
             *reinterpret_cast<half4 *>(hi + r * kLdk + kq) = h;
             *reinterpret_cast<half4 *>(lo + r * kLdk + kq) = l;
         }
+    }
+};
+
+// F32Rows's rows with each column k multiplied by scale[k] before the split
+// (K a multiple of BK, every row start and ld multiples of 4 floats): a
+// thread's four columns are the same at every row it takes, so one float4 of
+// scales a step serves them all.
+template <int BR, bool FULL>
+struct ScaledF32Rows {
+    F32Rows<BR, true, FULL> rows;
+    const float *scale;
+    float4 f;
+
+    template <class RowOf>
+    __device__ void init(const float *base, int64_t ld, RowOf row_of, int64_t k_, int tid, const float *scale_) {
+        rows.init(base, ld, row_of, k_, tid);
+        scale = scale_ + (tid % (kBK / 4)) * 4;
+    }
+
+    __device__ void load(int64_t k0, int tid) {
+        rows.load(k0, tid);
+        f = *reinterpret_cast<const float4 *>(scale + k0);
+    }
+
+    __device__ void store(_Float16 *hi, _Float16 *lo, int tid) {
+#pragma unroll
+        for (int i = 0; i < F32Rows<BR, true, FULL>::kQuads; ++i) {
+            rows.v[i].x *= f.x;
+            rows.v[i].y *= f.y;
+            rows.v[i].z *= f.z;
+            rows.v[i].w *= f.w;
+        }
+        rows.store(hi, lo, tid);
     }
 };
 
@@ -626,9 +659,10 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
 // ------------------------------------------------------------------ Winograd's products
 
 // C[b][m][n] = sum_k A[b][m][k] B[b][n][k] for the batches b: A already split
-// into two FP16 planes, B single precision split on its way into LDS, both
-// K-contiguous rows; three MFMAs a product.
-template <int TM, int TN, bool FULL, int NS>
+// into two FP16 planes, or (SCALED) single precision with its columns scaled
+// and split on its way into LDS, B single precision split on its way into
+// LDS, both K-contiguous rows; three MFMAs a product.
+template <int TM, int TN, bool FULL, int NS, bool SCALED = false>
 __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
@@ -657,13 +691,18 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    F16Rows<BM, true, FULL, 2> la[NS];
+    using LA = std::conditional_t<SCALED, ScaledF32Rows<BM, FULL>, F16Rows<BM, true, FULL, 2>>;
+    LA la[NS];
     F32Rows<BN, true, FULL> lb[NS];
     const auto a_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : -1; };
     const auto b_row = [&](int r) -> int64_t { return n0 + r < p.N ? n0 + r : -1; };
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        la[s].init(A, p.K, a_row, p.K, tid, p.a_plane);
+        if constexpr (SCALED) {
+            la[s].init(p.a32 + batch * p.a_batch, p.K, a_row, p.K, tid, p.a_scale);
+        } else {
+            la[s].init(A, p.K, a_row, p.K, tid, p.a_plane);
+        }
         lb[s].init(B, p.K, b_row, p.K, tid);
     }
     main_loop<TM, TN, kSplitBoth, NS>(acc, la, lb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
@@ -751,7 +790,13 @@ hipError_t launch_split_t(SplitBatchedArgs p, int stages, hipStream_t stream) {
     p.m_blocks = (p.M + 64 * TM - 1) / (64 * TM);
     p.n_blocks = (p.N + 64 * TN - 1) / (64 * TN);
     dim3 grid(static_cast<uint32_t>(p.batches * p.m_blocks * p.n_blocks)), block(256);
-    if (stages == 4) {
+    if (p.a32 != nullptr) {
+        if (stages == 4) {
+            hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 4, true>), grid, block, 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 2, true>), grid, block, 0, stream, p);
+        }
+    } else if (stages == 4) {
         hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 4>), grid, block, 0, stream, p);
     } else {
         hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 2>), grid, block, 0, stream, p);
@@ -803,8 +848,11 @@ hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream
 hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream) {
     // The operands' layout is the caller's own: K padded to whole steps, every
     // row 16-byte aligned.
-    const bool aligned = (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 &&
-                         p.a_batch % 8 == 0 && p.a_plane % 8 == 0 && p.b_batch % 4 == 0;
+    const bool a_aligned = p.a32 != nullptr ? (reinterpret_cast<uintptr_t>(p.a32) % 16) == 0 &&
+                                                  (reinterpret_cast<uintptr_t>(p.a_scale) % 16) == 0
+                                            : (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && p.a_plane % 8 == 0;
+    const bool aligned = a_aligned && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 && p.a_batch % 8 == 0 &&
+                         p.b_batch % 4 == 0;
     if (p.K % kBK != 0 || !aligned) return hipErrorInvalidValue;
     // Both operands split, two planes each: 80 KB of LDS at 128 x 128.
     return pick_tiles(p.M, p.N, p.batches, g.tiles, [&](auto tm, auto tn) {

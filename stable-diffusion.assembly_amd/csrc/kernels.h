@@ -61,10 +61,11 @@ struct ConvArgs {
 hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream);
 
 // Batched products c[b][m][n] = sum_k a[b][m][k] b[b][n][k]: a already split
-// into two FP16 planes (hi, and lo `a_plane` elements after it), b single
-// precision, both K-contiguous rows of K elements; c's rows N apart.  Strides
-// between batches in elements.  The caller pads: K a multiple of 32, a and b
-// 16-byte aligned, a_batch and a_plane multiples of 8, b_batch of 4;
+// into two FP16 planes (hi, and lo `a_plane` elements after it), or single
+// precision with a scale per column (a32, a_scale), b single precision, both
+// K-contiguous rows of K elements; c's rows N apart.  Strides between batches
+// in elements.  The caller pads: K a multiple of 32, a (or a32, a_scale) and
+// b 16-byte aligned, a_batch and a_plane multiples of 8, b_batch of 4;
 // hipErrorInvalidValue otherwise.
 struct SplitBatchedArgs {
     const _Float16 *a;
@@ -73,6 +74,10 @@ struct SplitBatchedArgs {
     int64_t a_batch, a_plane, b_batch, c_batch;
     int64_t M, N, K, batches;
     int64_t m_blocks, n_blocks;
+    // Instead of a: A in single precision (a32, batches a_batch apart), each
+    // column k multiplied by a_scale[k] before the split.
+    const float *a32;
+    const float *a_scale;
 };
 
 hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream);

@@ -12,22 +12,26 @@
 //      F(2x2)) below 2^(17 + e_c); each output channel's a_o, its greatest
 //      FP16 weight times the weight transform's gain ((28/15)^2, 1.5^2)
 //      below 2^(17 - a_o);
-//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi] * 2^(a_o + e_c - E), E the
-//      greatest e_c, as two FP16 parts (device.h, split2), hi and lo, each a
-//      plane of its own, [xi][part][oc][kp], IC padded with zeros to kp, a
-//      multiple of 32;
+//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi] * 2^a_o in single
+//      precision, [xi][oc][kp], IC padded with zeros to kp, a multiple of 32:
+//      they depend on the weights alone, and the device store keeps them (with
+//      a_o) from one call to the next, as the reference's store keeps its
+//      transformed weights (winograd.cc:2147-2149); without a store they are
+//      made at every call in the work buffer;
 //   2. the inputs, V[xi][tile][ic] = (B^T d B)[xi] * 2^-e_c, single
-//      precision, [xi][tile][kp];
-//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: V split on its way into
-//      LDS, three MFMAs a product (gemm.hip), so that the sums are those of
-//      22-bit operands where FP16 would hold 11 -- the scales keep every part
-//      inside FP16's range: |U| 2^(a_o + e_c - E) and |V| 2^-e_c below 2^17;
+//      precision, [xi][tile][kp]; its first block also finds E, the greatest
+//      e_c, each channel's factor 2^(e_c - E) and each output's shift E - a_o;
+//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: U's column c times
+//      2^(e_c - E) and both operands split into two FP16 parts (device.h,
+//      split2) on their way into LDS, three MFMAs a product (gemm.hip), so
+//      that the sums are those of 22-bit operands where FP16 would hold 11 --
+//      the scales keep every part inside FP16's range: |U| 2^(a_o + e_c - E)
+//      and |V| 2^-e_c below 2^17;
 //   4. the outputs, A^T M A * 2^(E - a_o), with the sum begun from the
 //      residual when the chain says so and the chain after, one thread per
 //      (oc, tile).
 // The scales cancel: sum_c (U 2^(a + e_c - E)) (V 2^-e_c) = 2^(a - E) sum_c U V.
-// The weights and the inputs go out through LDS, so that their stores are
-// whole rows of IC rather than scattered halves.
+// The inputs go out through LDS, so that their stores are whole rows of IC.
 //
 // With winograd_fp32=1 the products go to the single-precision MFMA instead
 // (v_mfma_f32_16x16x4_f32), unscaled: a sixteenth of the rate, for comparison.
@@ -219,66 +223,6 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
             u[i][j] = gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
 }
 
-// A block per 4 output channels by 64 input channels, a thread per kernel:
-// E, the greatest e_c (each block reduces e itself), and shift[o] = E - a_o
-// for the outputs (blocks of the first channels); U * 2^(a_o + e_c - E) split
-// into its two FP16 parts, staged in LDS as [xi][part][o][channel] and
-// written out as rows of 64 channels, u[xi][part][oc][kp], zeros from IC to
-// kp.
-constexpr int kWeightOc = 4, kWeightIc = 64;
-
-template <int M>
-__global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
-                                                            int64_t kp, const int32_t *__restrict__ e,
-                                                            const int32_t *__restrict__ amax, _Float16 *__restrict__ u,
-                                                            int32_t *__restrict__ shift) {
-    constexpr int A = Mat<M>::A;
-    constexpr int kRows = 2 * A * A;
-    __shared__ float scratch[4];
-    __shared__ __attribute__((aligned(16))) _Float16 stage[kRows][kWeightOc][kWeightIc];
-    const int tid = threadIdx.x;
-    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kWeightOc;
-    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kWeightIc;
-    int emax = kZeroChannel;
-    for (int64_t c = tid; c < ic; c += 256) emax = max(emax, e[c]);
-    const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
-    const int ol = tid / kWeightIc, cl = tid % kWeightIc;
-    const int64_t o = o0 + ol, c = c0 + cl;
-    float t[A][A] = {};
-    int s = 0;
-    if (o < oc) {
-        const int ao = amax[o];
-        if (blockIdx.y == 0 && cl == 0) shift[o] = E - ao;
-        if (c < ic) {
-            float g[3][3];
-            load_g(w + (o * ic + c) * 9, g);
-            transform_g<M>(g, t);
-            s = ao + e[c] - E;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < A; ++i)
-#pragma unroll
-        for (int j = 0; j < A; ++j) {
-            _Float16 hi, lo;
-            split2(ldexpf(t[i][j], s), hi, lo);
-            stage[2 * (i * A + j)][ol][cl] = hi;
-            stage[2 * (i * A + j) + 1][ol][cl] = lo;
-        }
-    __syncthreads();
-    // kRows x kWeightOc rows of `width` halves, 8 at a time.
-    const int width = static_cast<int>(kp - c0 < kWeightIc ? kp - c0 : kWeightIc);
-    const int per_row = width / 8;
-    for (int q = tid; q < kRows * kWeightOc * per_row; q += 256) {
-        const int row = q / per_row;
-        const int k = (q - row * per_row) * 8;
-        const int r = row / kWeightOc, oo = row % kWeightOc;
-        if (o0 + oo >= oc) continue;
-        *reinterpret_cast<half8 *>(u + (r * oc + o0 + oo) * kp + c0 + k) =
-            *reinterpret_cast<const half8 *>(&stage[r][oo][k]);
-    }
-}
-
 // Unscaled U[xi][oc][ic], one thread per (oc, ic), for the single-precision products.
 template <int M>
 __global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict__ w, float *__restrict__ u, int64_t oc,
@@ -290,6 +234,35 @@ __global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict
     load_g(w + t * 9, g);
     transform_g<M>(g, v);
     const int64_t plane = oc * ic;
+#pragma unroll
+    for (int i = 0; i < A; ++i)
+#pragma unroll
+        for (int j = 0; j < A; ++j) u[(i * A + j) * plane + t] = v[i][j];
+}
+
+// U[xi][oc][kp] * 2^a_o in single precision, zeros from IC to kp, one thread
+// per (oc, channel): the transformed weights as the store keeps them, the
+// inputs' scales 2^(e_c - E) applied by the products as they read them.
+template <int M>
+__global__ __launch_bounds__(256) void weights_scaled_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
+                                                             int64_t kp, const int32_t *__restrict__ amax,
+                                                             float *__restrict__ u) {
+    constexpr int A = Mat<M>::A;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= oc * kp) return;
+    const int64_t o = t / kp, c = t - o * kp;
+    float v[A][A] = {};
+    if (c < ic) {
+        float g[3][3];
+        load_g(w + (o * ic + c) * 9, g);
+        transform_g<M>(g, v);
+        const int s = amax[o];
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < A; ++j) v[i][j] = ldexpf(v[i][j], s);
+    }
+    const int64_t plane = oc * kp;
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
@@ -352,8 +325,19 @@ constexpr int kInTiles = 8, kInChannels = 32;
 
 template <int M>
 __global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
-                                                           float *__restrict__ v) {
+                                                           float *__restrict__ v, const int32_t *__restrict__ amax,
+                                                           float *__restrict__ f, int32_t *__restrict__ shift) {
     constexpr int A = Mat<M>::A;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        // E, the greatest e_c; each channel's scale of the weights 2^(e_c -
+        // E) (zero past IC), and each output channel's shift E - a_o.
+        __shared__ float scratch[4];
+        int emax = kZeroChannel;
+        for (int64_t c = threadIdx.x; c < a.ic; c += 256) emax = max(emax, e[c]);
+        const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
+        for (int64_t c = threadIdx.x; c < kp; c += 256) f[c] = c < a.ic ? ldexpf(1.0f, e[c] - E) : 0.0f;
+        for (int64_t o = threadIdx.x; o < a.oc; o += 256) shift[o] = E - amax[o];
+    }
     // Rows of a tile 40 floats apart: 16-byte aligned, and the 64 lanes of a
     // wave (8 tiles by 8 channels) in at most two to a bank.
     __shared__ __attribute__((aligned(16))) float stage[A * A][kInTiles][kInChannels + 8];
@@ -906,7 +890,7 @@ struct WorkLayout {
     int64_t kp;                          // IC padded to whole steps of K
     bool small;                          // the small images' path
     int64_t tp, splits, split_len;       // its tiles padded to 16, splits of the input channels
-    size_t e, a, shift, u, v, m, total;  // byte offsets
+    size_t e, a, shift, f, u, v, m, total;  // byte offsets
 };
 
 // The small images' path: F(4x4) on the reference's small images (few tiles
@@ -950,11 +934,12 @@ WorkLayout work_layout(const WinogradArgs &a) {
         l.total = at;
         return l;
     }
-    // Either form: U as two FP16 planes or in single precision, V in single
-    // precision, [xi][tile][kp] or [xi][ic][tile].
+    // Either form: U in single precision, [xi][oc][kp] (scaled by 2^a_o) or
+    // [xi][oc][ic]; V in single precision, [xi][tile][kp] or [xi][ic][tile].
     l.e = take(a.ic * 4);
     l.a = take(a.oc * 4);
     l.shift = take(a.oc * 4);
+    l.f = take(l.kp * 4);
     l.u = take(alpha2 * a.oc * l.kp * 4);
     l.v = take(alpha2 * l.kp * a.tiles * 4);
     l.m = take(alpha2 * a.oc * a.tiles * 4);
@@ -1028,30 +1013,47 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
                            l.splits, l.tp);
         return launched(hipGetLastError(), "winograd (small images)");
     }
-    _Float16 *uh = reinterpret_cast<_Float16 *>(u);
+    // The transformed weights U 2^a_o and their exponents a_o: the store's
+    // when it keeps them (filled by the first call), else the work buffer's,
+    // made at every call.  They depend on the weights alone; the inputs'
+    // exponents come in as the products read U.
+    const int64_t wne[4] = {3, 3, a.ic, a.oc};
+    const int64_t wnb[4] = {2, 6, 18, 18 * a.ic};
+    const size_t a_bytes = static_cast<size_t>(round_up(a.oc * 4, 256));
+    const size_t u_bytes = static_cast<size_t>(A * A * a.oc * l.kp * 4);
+    bool ready = false;
+    char *kept = static_cast<char *>(store_entry(a.w, SDHIP_TYPE_F16, wne, wnb, kStoreWinograd, M,
+                                                 static_cast<size_t>(a.oc * a.ic * 18), a_bytes + u_bytes, stream,
+                                                 ready));
+    int32_t *a_kept = kept != nullptr ? reinterpret_cast<int32_t *>(kept) : a_oc;
+    float *u_kept = kept != nullptr ? reinterpret_cast<float *>(kept + a_bytes) : u;
+    float *f = reinterpret_cast<float *>(base + l.f);
     {
+        // The inputs' exponents, and the weights' while they are not kept.
         KernelScope scope(names[0].c_str(), stream);
-        hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.ic + a.oc, 4))), dim3(256), 0,
-                           stream, a, e, a_oc);
+        const int64_t waves = ready ? a.ic : a.ic + a.oc;
+        hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(waves, 4))), dim3(256), 0, stream,
+                           a, e, a_kept);
     }
-    {
+    if (!ready) {
         KernelScope scope(names[1].c_str(), stream);
-        hipLaunchKernelGGL((weights_split_kernel<M>),
-                           dim3(static_cast<uint32_t>(ceil_div(a.oc, kWeightOc)),
-                                static_cast<uint32_t>(ceil_div(l.kp, kWeightIc))),
-                           dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, a_oc, uh, shift);
+        hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256))),
+                           dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, a_kept, u_kept);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return launched(err, "winograd weights");
+        if (kept != nullptr) store_publish(kept);
     }
     {
         KernelScope scope(names[2].c_str(), stream);
         hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
-                           stream, a, l.kp, e, v);
+                           stream, a, l.kp, e, v, a_kept, f, shift);
     }
     {
         KernelScope scope(names[3].c_str(), stream);
         SplitBatchedArgs p{};
-        p.a = uh;
-        p.a_plane = a.oc * l.kp;
-        p.a_batch = 2 * p.a_plane;
+        p.a32 = u_kept;
+        p.a_scale = f;
+        p.a_batch = a.oc * l.kp;
         p.b = v;
         p.b_batch = a.tiles * l.kp;
         p.c = m;

@@ -151,3 +151,45 @@ def test_no_entry_made_under_capture(gpu, arena):
         assert sdhip.store_used()[1] == 1
     finally:
         sdhip.set_tuning("")
+
+
+def convolve(gpu, k_d, x_d, oh, ow):
+    y = unwritten((x_d.shape[0], k_d.shape[0], oh, ow), gpu)
+    sdhip.conv2d(k_d, x_d, y, sdhip.conv_params(1, 1, 1, 1, 1, 1))
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,path", [((2, 64, 40, 36), 4), ((2, 96, 8, 8), 2)])
+def test_kept_winograd_weights(gpu, arena, shape, path):
+    """Winograd's transformed weights (times 2^a_o) kept, as the reference
+    keeps its transformed weights (winograd.cc:2147-2149): the first call
+    fills the entry, later calls skip the weights' transform and give the
+    same outputs bit for bit as a call without a store; new inputs of other
+    magnitudes, same weights, agree with the oracle; sdhip_forget drops it."""
+    n, ic, h_, w_ = shape
+    oc = 48
+    r = rng(8)
+    kh16, k32 = weights_f16(r, (oc, ic, 3, 3))
+    x = uniform(r, shape, 1.0)
+    k_d, x_d = dev(kh16, gpu), dev(x, gpu)
+    assert sdhip.conv2d_path(k_d, x_d, unwritten((n, oc, h_, w_), gpu), sdhip.conv_params(1, 1, 1, 1, 1, 1)) == path
+    sdhip.store_arena(None)
+    plain = convolve(gpu, k_d, x_d, h_, w_)
+    sdhip.store_arena(arena)
+    first = convolve(gpu, k_d, x_d, h_, w_)
+    assert sdhip.store_used()[1] == 1
+    tag = "winograd4" if path == 4 else "winograd2"
+    second = kernels_of(lambda: convolve(gpu, k_d, x_d, h_, w_))
+    assert f"{tag}.weights" not in second and f"{tag}.products" in second
+    again = convolve(gpu, k_d, x_d, h_, w_)
+    assert np.array_equal(first.view(np.uint32), plain.view(np.uint32))
+    assert np.array_equal(again.view(np.uint32), plain.view(np.uint32))
+    # Inputs 2^10 larger in half the channels: the kept weights serve them.
+    x2 = (x * np.where(np.arange(ic) % 2 == 0, 1024.0, 1.0).reshape(1, ic, 1, 1)).astype(np.float32)
+    y2 = convolve(gpu, k_d, dev(x2, gpu), h_, w_)
+    exact, mag = orc.exact_conv2d(x2, k32, 1, 1, 1, 1, 1, 1)
+    assert orc.metric(y2, exact, mag) <= 2e-5
+    sdhip.forget(k_d)
+    assert sdhip.store_used() == (0, 0)
