@@ -44,8 +44,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only-main", action="store_true")
-    p.add_argument("--workload", default="", help="run one workload alone (cfg1 cfg2 cfg3a cfg3b cfg4_self "
-                                                  "cfg4_cross cfg5 unet copy), for a profiler")
+    p.add_argument("--workload", default="", help="run one workload alone (cfg1 cfg2 cfg2_kept cfg3a cfg3a_kept "
+                                                  "cfg3b cfg4_self cfg4_cross cfg5 unet unet_kept copy), for a "
+                                                  "profiler")
     p.add_argument("--no-unet", action="store_true", help="leave out the UNet step")
     return p.parse_args()
 
@@ -106,11 +107,12 @@ _ARENA = None
 
 def fresh_store(dev, gib=6):
     """The device store's arena, emptied: the derived forms of the weights
-    (Winograd's transformed weights, the bits mode's quantized ones) kept from
-    one call to the next, as the reference keeps them in its store by default
-    (store.cc:64-99, 8 GiB; winograd.cc:2147-2149) -- the first, untimed call
-    fills it.  Emptied per workload, so that no entry outlives the tensors it
-    was made from."""
+    kept from one call to the next -- the bits mode's quantized weights, as the
+    reference keeps them by default (store.cc:64-99, 8 GiB), and Winograd's
+    transformed weights, as it keeps them when SDASM_STORE_MB gives its store
+    a budget (winograd.cc:2147-2149; store.h:26-34: none by default) -- the
+    first, untimed call fills it.  Emptied per workload, so that no entry
+    outlives the tensors it was made from."""
     import torch
 
     import sdhip
@@ -122,7 +124,15 @@ def fresh_store(dev, gib=6):
     return _ARENA
 
 
-def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupnorm=False, seed=0):
+def no_store():
+    """No store: every call derives its weights' forms, the reference's
+    default for single-precision layouts."""
+    import sdhip
+
+    sdhip.store_arena(None)
+
+
+def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupnorm=False, seed=0, keep=False):
     """The convolution of a configuration with its chain, ready to run."""
     import torch
 
@@ -156,7 +166,7 @@ def conv_workload(dev, n, ic, h, w, oc, k, pad, bias=True, residual=True, groupn
         gn_work = torch.empty(max(gn_size, 8), dtype=torch.uint8, device=dev)
         gn = (out, sdhip.epilogue([("mul", gamma), ("add", beta), ("silu", None)]), sdhip.desc(out), gn_work, gn_size)
     stream = sdhip.stream_handle()
-    arena = fresh_store(dev)
+    arena = fresh_store(dev) if keep else no_store()
     keep = (x, kern, y, steps, work, arena)
 
     def run():
@@ -238,13 +248,14 @@ def copy_workload(dev, mib=256):
     return run, 0.0
 
 
-def unet_workload(dev, seed=7):
+def unet_workload(dev, seed=7, keep=False):
     """The synthetic SD1.5 UNet step (unet_step.py) at 512x512, batch 2,
-    captured in a HIP graph."""
+    captured in a HIP graph; with `keep`, Winograd's transformed weights kept
+    in the store."""
     import unet_step
 
     model = unet_step.Model(unet_step.Config(), dev, seed=seed)
-    arena = fresh_store(dev)
+    arena = fresh_store(dev) if keep else no_store()
     step = unet_step.Step(model, unet_step.HipOps(dev), model.inputs(seed=seed + 1))
     step.keep = (model, arena)
     return step
@@ -283,11 +294,12 @@ def make_workload(dev, name):
     """(run, FLOPs) of a named workload: the BASELINE.json configurations."""
     if name == "cfg1":
         return linear_workload(dev, 320, 320, 4096, 2, seed=1)
-    if name == "cfg2":
-        run, flops, _ = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2)
+    if name in ("cfg2", "cfg2_kept"):
+        run, flops, _ = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2, keep=name.endswith("kept"))
         return run, flops
-    if name == "cfg3a":
-        run, flops, _ = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True, seed=3)
+    if name in ("cfg3a", "cfg3a_kept"):
+        run, flops, _ = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True, seed=3,
+                                      keep=name.endswith("kept"))
         return run, flops
     if name == "cfg3b":
         run, flops, _ = conv_workload(dev, 2, 640, 32, 32, 1280, 1, 0, bias=True, residual=False, groupnorm=True,
@@ -302,8 +314,8 @@ def make_workload(dev, name):
     if name == "cfg5":
         graph = sdxl_block_workload(dev)
         return graph.run, graph.flops
-    if name == "unet":
-        step = unet_workload(dev)
+    if name in ("unet", "unet_kept"):
+        step = unet_workload(dev, keep=name.endswith("kept"))
         return step.run, step.flops
     raise SystemExit(f"unknown workload {name}")
 
@@ -357,9 +369,19 @@ def unet_step_line(dev, args):
     lib_ms = sum(v[0] * v[1] for v in kt.values())
     torch.cuda.synchronize()
     log(f"unet step: {ms:.2f} ms (graph), {eager_ms:.2f} ms eager, library kernels {lib_ms:.2f} ms")
-    return {"ms": round(ms, 3), "tflops": round(step.flops / ms / 1e9, 2),
-            "gflop": round(step.flops / 1e9, 2), "nodes": step.nodes,
-            "gflop_by_class": {k: round(v / 1e9, 2) for k, v in step.by_class.items()},
+    flops, nodes, by_class = step.flops, step.nodes, step.by_class
+    del step
+    # Beside it, Winograd's transformed weights kept from step to step, as the
+    # reference's store keeps them when given a budget.
+    kept = unet_workload(dev, keep=True)
+    kept_ms = timed(kept.run, max(5, args.steps // 5), max(2, args.warmup // 5))
+    del kept
+    no_store()
+    log(f"unet step, weights kept: {kept_ms:.2f} ms")
+    return {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 2),
+            "weights_kept": {"ms": round(kept_ms, 3), "tflops": round(flops / kept_ms / 1e9, 2)},
+            "gflop": round(flops / 1e9, 2), "nodes": nodes,
+            "gflop_by_class": {k: round(v / 1e9, 2) for k, v in by_class.items()},
             "eager_ms": round(eager_ms, 3), "library_kernels_ms": round(lib_ms, 3),
             "kernels_ms": {k: round(v[0] * v[1], 3) for k, v in sorted(kt.items(), key=lambda kv: -kv[1][0] * kv[1][1])},
             "workload": "SD1.5 UNet at 512x512 (latent 64x64), batch 2 (CFG), context 77x768, random weights "
@@ -416,6 +438,13 @@ def main():
     log(f"kernels: {roof['kernels_us']}")
 
     configs = {"cfg2_winograd4": {"ms": round(ms, 5), "tflops": round(value, 2)}}
+    # Beside it, the transformed weights kept from call to call, as the
+    # reference's store keeps them when given a budget (none by default).
+    run_k, _, _ = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2, keep=True)
+    ms_k = timed(run_k, args.steps, args.warmup)
+    configs["cfg2_winograd4"]["weights_kept"] = {"ms": round(ms_k, 5), "tflops": round(flops / ms_k / 1e9, 2)}
+    log(f"cfg2 weights kept: {ms_k * 1e3:.1f} us")
+    no_store()
     if not args.only_main:
         run1, f1 = linear_workload(dev, 320, 320, 4096, 2, seed=1)
         m1 = timed(run1, args.steps, args.warmup)
@@ -429,6 +458,12 @@ def main():
                                               "kernels_us": {k: round(v[0] * 1e3, 2)
                                                              for k, v in kernel_times(run3a, 10).items()}}
         log(f"cfg3a F(2x2)+GN+SiLU: {m3a * 1e3:.1f} us")
+        run3k, _, _ = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True, seed=3,
+                                    keep=True)
+        m3k = timed(run3k, args.steps, args.warmup)
+        configs["cfg3a_winograd2_gn_silu"]["weights_kept"] = {"ms": round(m3k, 5), "tflops": round(f3a / m3k / 1e9, 2)}
+        log(f"cfg3a weights kept: {m3k * 1e3:.1f} us")
+        no_store()
         run3b, f3b, p3b = conv_workload(dev, 2, 640, 32, 32, 1280, 1, 0, bias=True, residual=False, groupnorm=True,
                                         seed=4)
         m3b = timed(run3b, args.steps, args.warmup)

@@ -12,26 +12,27 @@
 //      F(2x2)) below 2^(17 + e_c); each output channel's a_o, its greatest
 //      FP16 weight times the weight transform's gain ((28/15)^2, 1.5^2)
 //      below 2^(17 - a_o);
-//   1. the weights, U[xi][oc][ic] = (G g G^T)[xi] * 2^a_o in single
-//      precision, [xi][oc][kp], IC padded with zeros to kp, a multiple of 32:
-//      they depend on the weights alone, and the device store keeps them (with
-//      a_o) from one call to the next, as the reference's store keeps its
-//      transformed weights (winograd.cc:2147-2149); without a store they are
-//      made at every call in the work buffer;
+//   1. the weights at every call, U[xi][oc][ic] = (G g G^T)[xi] * 2^(a_o +
+//      e_c - E), E the greatest e_c, as two FP16 parts (device.h, split2), hi
+//      and lo, each a plane of its own, [xi][part][oc][kp], IC padded with
+//      zeros to kp, a multiple of 32; or, where the device store keeps them
+//      (as the reference's store keeps its transformed weights when its
+//      budget allows, winograd.cc:2147-2149, store.h:26-34), U * 2^a_o in
+//      single precision, [xi][oc][kp], with a_o, made by the first call;
 //   2. the inputs, V[xi][tile][ic] = (B^T d B)[xi] * 2^-e_c, single
-//      precision, [xi][tile][kp]; its first block also finds E, the greatest
-//      e_c, each channel's factor 2^(e_c - E) and each output's shift E - a_o;
-//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: U's column c times
-//      2^(e_c - E) and both operands split into two FP16 parts (device.h,
-//      split2) on their way into LDS, three MFMAs a product (gemm.hip), so
-//      that the sums are those of 22-bit operands where FP16 would hold 11 --
-//      the scales keep every part inside FP16's range: |U| 2^(a_o + e_c - E)
-//      and |V| 2^-e_c below 2^17;
+//      precision, [xi][tile][kp]; with kept weights its first block also finds
+//      E, each channel's factor 2^(e_c - E) and each output's shift E - a_o;
+//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: V (and kept U, its column
+//      c times 2^(e_c - E)) split into two FP16 parts on their way into LDS,
+//      three MFMAs a product (gemm.hip), so that the sums are those of 22-bit
+//      operands where FP16 would hold 11 -- the scales keep every part inside
+//      FP16's range: |U| 2^(a_o + e_c - E) and |V| 2^-e_c below 2^17;
 //   4. the outputs, A^T M A * 2^(E - a_o), with the sum begun from the
 //      residual when the chain says so and the chain after, one thread per
 //      (oc, tile).
 // The scales cancel: sum_c (U 2^(a + e_c - E)) (V 2^-e_c) = 2^(a - E) sum_c U V.
-// The inputs go out through LDS, so that their stores are whole rows of IC.
+// The weights and the inputs go out through LDS, so that their stores are
+// whole rows of IC rather than scattered halves.
 //
 // With winograd_fp32=1 the products go to the single-precision MFMA instead
 // (v_mfma_f32_16x16x4_f32), unscaled: a sixteenth of the rate, for comparison.
@@ -223,6 +224,66 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
             u[i][j] = gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
 }
 
+// A block per 4 output channels by 64 input channels, a thread per kernel:
+// E, the greatest e_c (each block reduces e itself), and shift[o] = E - a_o
+// for the outputs (blocks of the first channels); U * 2^(a_o + e_c - E) split
+// into its two FP16 parts, staged in LDS as [xi][part][o][channel] and
+// written out as rows of 64 channels, u[xi][part][oc][kp], zeros from IC to
+// kp.
+constexpr int kWeightOc = 4, kWeightIc = 64;
+
+template <int M>
+__global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
+                                                            int64_t kp, const int32_t *__restrict__ e,
+                                                            const int32_t *__restrict__ amax, _Float16 *__restrict__ u,
+                                                            int32_t *__restrict__ shift) {
+    constexpr int A = Mat<M>::A;
+    constexpr int kRows = 2 * A * A;
+    __shared__ float scratch[4];
+    __shared__ __attribute__((aligned(16))) _Float16 stage[kRows][kWeightOc][kWeightIc];
+    const int tid = threadIdx.x;
+    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kWeightOc;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kWeightIc;
+    int emax = kZeroChannel;
+    for (int64_t c = tid; c < ic; c += 256) emax = max(emax, e[c]);
+    const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
+    const int ol = tid / kWeightIc, cl = tid % kWeightIc;
+    const int64_t o = o0 + ol, c = c0 + cl;
+    float t[A][A] = {};
+    int s = 0;
+    if (o < oc) {
+        const int ao = amax[o];
+        if (blockIdx.y == 0 && cl == 0) shift[o] = E - ao;
+        if (c < ic) {
+            float g[3][3];
+            load_g(w + (o * ic + c) * 9, g);
+            transform_g<M>(g, t);
+            s = ao + e[c] - E;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < A; ++i)
+#pragma unroll
+        for (int j = 0; j < A; ++j) {
+            _Float16 hi, lo;
+            split2(ldexpf(t[i][j], s), hi, lo);
+            stage[2 * (i * A + j)][ol][cl] = hi;
+            stage[2 * (i * A + j) + 1][ol][cl] = lo;
+        }
+    __syncthreads();
+    // kRows x kWeightOc rows of `width` halves, 8 at a time.
+    const int width = static_cast<int>(kp - c0 < kWeightIc ? kp - c0 : kWeightIc);
+    const int per_row = width / 8;
+    for (int q = tid; q < kRows * kWeightOc * per_row; q += 256) {
+        const int row = q / per_row;
+        const int k = (q - row * per_row) * 8;
+        const int r = row / kWeightOc, oo = row % kWeightOc;
+        if (o0 + oo >= oc) continue;
+        *reinterpret_cast<half8 *>(u + (r * oc + o0 + oo) * kp + c0 + k) =
+            *reinterpret_cast<const half8 *>(&stage[r][oo][k]);
+    }
+}
+
 // Unscaled U[xi][oc][ic], one thread per (oc, ic), for the single-precision products.
 template <int M>
 __global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict__ w, float *__restrict__ u, int64_t oc,
@@ -328,9 +389,10 @@ __global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64
                                                            float *__restrict__ v, const int32_t *__restrict__ amax,
                                                            float *__restrict__ f, int32_t *__restrict__ shift) {
     constexpr int A = Mat<M>::A;
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-        // E, the greatest e_c; each channel's scale of the weights 2^(e_c -
-        // E) (zero past IC), and each output channel's shift E - a_o.
+    if (f != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+        // With the weights kept: E, the greatest e_c; each channel's scale of
+        // the weights 2^(e_c - E) (zero past IC), and each output channel's
+        // shift E - a_o.
         __shared__ float scratch[4];
         int emax = kZeroChannel;
         for (int64_t c = threadIdx.x; c < a.ic; c += 256) emax = max(emax, e[c]);
@@ -934,8 +996,10 @@ WorkLayout work_layout(const WinogradArgs &a) {
         l.total = at;
         return l;
     }
-    // Either form: U in single precision, [xi][oc][kp] (scaled by 2^a_o) or
-    // [xi][oc][ic]; V in single precision, [xi][tile][kp] or [xi][ic][tile].
+    // Either form: U as two FP16 planes [xi][part][oc][kp] or in single
+    // precision [xi][oc][ic] (kept weights live in the store instead); V in
+    // single precision, [xi][tile][kp] or [xi][ic][tile]; the factors f of
+    // kept weights' columns.
     l.e = take(a.ic * 4);
     l.a = take(a.oc * 4);
     l.shift = take(a.oc * 4);
@@ -1013,10 +1077,12 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
                            l.splits, l.tp);
         return launched(hipGetLastError(), "winograd (small images)");
     }
-    // The transformed weights U 2^a_o and their exponents a_o: the store's
-    // when it keeps them (filled by the first call), else the work buffer's,
-    // made at every call.  They depend on the weights alone; the inputs'
-    // exponents come in as the products read U.
+    // The transformed weights U 2^a_o and their exponents a_o, kept in the
+    // store when it has room: they depend on the weights alone, and the
+    // inputs' exponents come in as the products read U.  Without the store
+    // (the reference keeps no single-precision transformed weights by
+    // default, store.h:26-34), U 2^(a_o + e_c - E) is made at every call
+    // already split into two FP16 planes, which the products read as they are.
     const int64_t wne[4] = {3, 3, a.ic, a.oc};
     const int64_t wnb[4] = {2, 6, 18, 18 * a.ic};
     const size_t a_bytes = static_cast<size_t>(round_up(a.oc * 4, 256));
@@ -1026,22 +1092,29 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
                                                  static_cast<size_t>(a.oc * a.ic * 18), a_bytes + u_bytes, stream,
                                                  ready));
     int32_t *a_kept = kept != nullptr ? reinterpret_cast<int32_t *>(kept) : a_oc;
-    float *u_kept = kept != nullptr ? reinterpret_cast<float *>(kept + a_bytes) : u;
-    float *f = reinterpret_cast<float *>(base + l.f);
+    float *u_kept = kept != nullptr ? reinterpret_cast<float *>(kept + a_bytes) : nullptr;
+    float *f = kept != nullptr ? reinterpret_cast<float *>(base + l.f) : nullptr;
     {
-        // The inputs' exponents, and the weights' while they are not kept.
+        // The inputs' exponents, and the weights' unless kept.
         KernelScope scope(names[0].c_str(), stream);
         const int64_t waves = ready ? a.ic : a.ic + a.oc;
         hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(waves, 4))), dim3(256), 0, stream,
                            a, e, a_kept);
     }
-    if (!ready) {
+    _Float16 *uh = reinterpret_cast<_Float16 *>(u);
+    if (kept == nullptr) {
+        KernelScope scope(names[1].c_str(), stream);
+        hipLaunchKernelGGL((weights_split_kernel<M>),
+                           dim3(static_cast<uint32_t>(ceil_div(a.oc, kWeightOc)),
+                                static_cast<uint32_t>(ceil_div(l.kp, kWeightIc))),
+                           dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, a_oc, uh, shift);
+    } else if (!ready) {
         KernelScope scope(names[1].c_str(), stream);
         hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256))),
                            dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, a_kept, u_kept);
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return launched(err, "winograd weights");
-        if (kept != nullptr) store_publish(kept);
+        store_publish(kept);
     }
     {
         KernelScope scope(names[2].c_str(), stream);
@@ -1051,9 +1124,15 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     {
         KernelScope scope(names[3].c_str(), stream);
         SplitBatchedArgs p{};
-        p.a32 = u_kept;
-        p.a_scale = f;
-        p.a_batch = a.oc * l.kp;
+        if (kept != nullptr) {
+            p.a32 = u_kept;
+            p.a_scale = f;
+            p.a_batch = a.oc * l.kp;
+        } else {
+            p.a = uh;
+            p.a_plane = a.oc * l.kp;
+            p.a_batch = 2 * p.a_plane;
+        }
         p.b = v;
         p.b_batch = a.tiles * l.kp;
         p.c = m;
