@@ -124,23 +124,17 @@ __device__ __forceinline__ float abs_max4(float4v v) {
     return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 }
 
-__device__ __forceinline__ float wave_max64(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// One wave per channel: waves [0, IC) input channel c's greatest |x| over
-// every image, four independent float4 loads in flight per lane where the
-// rows are contiguous, and its exponent e[c] (zero channels: the least, so
-// that they scale to zero); waves [IC, IC + OC) output channel o's greatest
-// FP16 weight, four loads of eight in flight per lane, and a[o].
+// One workgroup per channel: blocks [0, IC) input channel c's greatest |x|
+// over every image, four independent float4 loads in flight per thread where
+// the rows are contiguous, and its exponent e[c] (zero channels: the least,
+// so that they scale to zero); blocks [IC, IC + OC) output channel o's
+// greatest FP16 weight, four loads of eight in flight per thread, and a[o].
 template <int M>
 __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__restrict__ e,
                                                      int32_t *__restrict__ amax) {
-    const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (w >= a.ic + a.oc) return;
+    __shared__ float scratch[4];
+    const int64_t w = blockIdx.x;
+    const int tid = threadIdx.x;
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
     if (w < a.ic) {
         const int64_t plane = a.ih * a.iw;
@@ -149,25 +143,25 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
             if (a.xnb1 == a.iw && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
                 const float4v *q = reinterpret_cast<const float4v *>(p);
                 const int64_t quads = plane / 4;
-                int64_t i = lane;
-                for (; i + 192 < quads; i += 256) {
-                    const float4v v0 = q[i], v1 = q[i + 64], v2 = q[i + 128], v3 = q[i + 192];
+                int64_t i = tid;
+                for (; i + 768 < quads; i += 1024) {
+                    const float4v v0 = q[i], v1 = q[i + 256], v2 = q[i + 512], v3 = q[i + 768];
                     m0 = fmaxf(m0, abs_max4(v0));
                     m1 = fmaxf(m1, abs_max4(v1));
                     m2 = fmaxf(m2, abs_max4(v2));
                     m3 = fmaxf(m3, abs_max4(v3));
                 }
-                for (; i < quads; i += 64) m0 = fmaxf(m0, abs_max4(q[i]));
-                for (int64_t j = quads * 4 + lane; j < plane; j += 64) m1 = fmaxf(m1, fabsf(p[j]));
+                for (; i < quads; i += 256) m0 = fmaxf(m0, abs_max4(q[i]));
+                for (int64_t j = quads * 4 + tid; j < plane; j += 256) m1 = fmaxf(m1, fabsf(p[j]));
             } else {
-                for (int64_t i = lane; i < plane; i += 64) {
+                for (int64_t i = tid; i < plane; i += 256) {
                     const int64_t y = i / a.iw;
                     m0 = fmaxf(m0, fabsf(p[y * a.xnb1 + (i - y * a.iw)]));
                 }
             }
         }
-        const float m = wave_max64(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-        if (lane == 0) e[w] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : kZeroChannel;
+        const float m = block_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)), scratch);
+        if (tid == 0) e[w] = m > 0.0f ? exponent_above(m * Mat<M>::kGain) - kTop : kZeroChannel;
     } else {
         const int64_t o = w - a.ic;
         const int64_t count = a.ic * 9;
@@ -175,9 +169,9 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
         if (count % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
             const half8 *q = reinterpret_cast<const half8 *>(p);
             const int64_t octs = count / 8;
-            int64_t i = lane;
-            for (; i + 192 < octs; i += 256) {
-                const half8 v0 = q[i], v1 = q[i + 64], v2 = q[i + 128], v3 = q[i + 192];
+            int64_t i = tid;
+            for (; i + 768 < octs; i += 1024) {
+                const half8 v0 = q[i], v1 = q[i + 256], v2 = q[i + 512], v3 = q[i + 768];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     m0 = fmaxf(m0, fabsf(static_cast<float>(v0[k])));
@@ -186,16 +180,16 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
                     m3 = fmaxf(m3, fabsf(static_cast<float>(v3[k])));
                 }
             }
-            for (; i < octs; i += 64) {
+            for (; i < octs; i += 256) {
                 const half8 v = q[i];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) m0 = fmaxf(m0, fabsf(static_cast<float>(v[k])));
             }
         } else {
-            for (int64_t i = lane; i < count; i += 64) m0 = fmaxf(m0, fabsf(static_cast<float>(p[i])));
+            for (int64_t i = tid; i < count; i += 256) m0 = fmaxf(m0, fabsf(static_cast<float>(p[i])));
         }
-        const float m = wave_max64(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-        if (lane == 0) amax[o] = m > 0.0f ? kTop - exponent_above(m * Mat<M>::kWeightGain) : 0;
+        const float m = block_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)), scratch);
+        if (tid == 0) amax[o] = m > 0.0f ? kTop - exponent_above(m * Mat<M>::kWeightGain) : 0;
     }
 }
 
@@ -204,6 +198,16 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
 __device__ __forceinline__ void load_g(const _Float16 *w, float (&g)[3][3]) {
 #pragma unroll
     for (int i = 0; i < 9; ++i) g[i / 3][i % 3] = static_cast<float>(w[i]);
+}
+
+// c0 x0 + c1 x1 + c2 x2 with its roundings written out: the first product
+// rounded, the other two fused in turn.  Left to the compiler, the sum is
+// contracted by where its operands come from (a kernel that converts the FP16
+// weights in the same block fuses other pairs than one that converted them
+// earlier), and F(4x4)'s G (thirds, fifteenths) rounds differently each way;
+// written out, every kernel that transforms weights gets the same bits.
+__device__ __forceinline__ float dot3(float c0, float x0, float c1, float x1, float c2, float x2) {
+    return fmaf(c2, x2, fmaf(c1, x1, c0 * x0));
 }
 
 // (G g G^T) of one kernel: G g a column at a time, then (G g) G^T a row at a
@@ -216,12 +220,12 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
     for (int i = 0; i < A; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            gg[i][j] = Mat<M>::g(i, 0) * g[0][j] + Mat<M>::g(i, 1) * g[1][j] + Mat<M>::g(i, 2) * g[2][j];
+            gg[i][j] = dot3(Mat<M>::g(i, 0), g[0][j], Mat<M>::g(i, 1), g[1][j], Mat<M>::g(i, 2), g[2][j]);
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
         for (int j = 0; j < A; ++j)
-            u[i][j] = gg[i][0] * Mat<M>::g(j, 0) + gg[i][1] * Mat<M>::g(j, 1) + gg[i][2] * Mat<M>::g(j, 2);
+            u[i][j] = dot3(Mat<M>::g(j, 0), gg[i][0], Mat<M>::g(j, 1), gg[i][1], Mat<M>::g(j, 2), gg[i][2]);
 }
 
 // A block per 4 output channels by 64 input channels, a thread per kernel:
@@ -244,22 +248,27 @@ __global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__re
     const int tid = threadIdx.x;
     const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kWeightOc;
     const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kWeightIc;
-    int emax = kZeroChannel;
-    for (int64_t c = tid; c < ic; c += 256) emax = max(emax, e[c]);
-    const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
     const int ol = tid / kWeightIc, cl = tid % kWeightIc;
     const int64_t o = o0 + ol, c = c0 + cl;
+    // The thread's kernel and exponents first, so that their loads overlap
+    // those of E's reduction.
+    const bool live = o < oc && c < ic;
+    float g[3][3] = {};
+    int ao = 0, ec = 0;
+    if (o < oc) ao = amax[o];
+    if (live) {
+        load_g(w + (o * ic + c) * 9, g);
+        ec = e[c];
+    }
+    int emax = kZeroChannel;
+    for (int64_t k = tid; k < ic; k += 256) emax = max(emax, e[k]);
+    const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
+    if (o < oc && blockIdx.y == 0 && cl == 0) shift[o] = E - ao;
     float t[A][A] = {};
     int s = 0;
-    if (o < oc) {
-        const int ao = amax[o];
-        if (blockIdx.y == 0 && cl == 0) shift[o] = E - ao;
-        if (c < ic) {
-            float g[3][3];
-            load_g(w + (o * ic + c) * 9, g);
-            transform_g<M>(g, t);
-            s = ao + e[c] - E;
-        }
+    if (live) {
+        transform_g<M>(g, t);
+        s = ao + ec - E;
     }
 #pragma unroll
     for (int i = 0; i < A; ++i)
@@ -896,12 +905,12 @@ __global__ __launch_bounds__(256) void products_small_kernel(WinogradArgs a, int
             float gg[3];
 #pragma unroll
             for (int b = 0; b < 3; ++b)
-                gg[b] = Mat<M>::g(row, 0) * g[jj][b] + Mat<M>::g(row, 1) * g[jj][3 + b] +
-                        Mat<M>::g(row, 2) * g[jj][6 + b];
+                gg[b] = dot3(Mat<M>::g(row, 0), g[jj][b], Mat<M>::g(row, 1), g[jj][3 + b], Mat<M>::g(row, 2),
+                             g[jj][6 + b]);
             const int sc = (c + jj < a.ic) ? ao + e[c + jj] - emax : 0;
 #pragma unroll
             for (int j = 0; j < A; ++j) {
-                const float u = gg[0] * Mat<M>::g(j, 0) + gg[1] * Mat<M>::g(j, 1) + gg[2] * Mat<M>::g(j, 2);
+                const float u = dot3(Mat<M>::g(j, 0), gg[0], Mat<M>::g(j, 1), gg[1], Mat<M>::g(j, 2), gg[2]);
                 _Float16 hi, lo;
                 split2(ldexpf(u, sc), hi, lo);
                 uh[j][jj] = hi;
@@ -1051,8 +1060,8 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     if (M == 4 && l.small) {
         {
             KernelScope scope(names[0].c_str(), stream);  // the inputs' exponents only
-            hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.ic, 4))), dim3(256), 0,
-                               stream, a, e, a_oc);
+            hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(a.ic)), dim3(256), 0, stream, a, e,
+                               a_oc);
         }
         _Float16 *vh = reinterpret_cast<_Float16 *>(v);
         {
@@ -1098,8 +1107,8 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         // The inputs' exponents, and the weights' unless kept.
         KernelScope scope(names[0].c_str(), stream);
         const int64_t waves = ready ? a.ic : a.ic + a.oc;
-        hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(waves, 4))), dim3(256), 0, stream,
-                           a, e, a_kept);
+        hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(waves)), dim3(256), 0, stream, a, e,
+                           a_kept);
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
     if (kept == nullptr) {
