@@ -84,10 +84,10 @@ const char *sdhip_last_error(void);
  * syntax "name=value,..." (sources/kernels.h:91-135, parsed by cpu.cc:121-212):
  * bits, input_bits, group, weight_group, quantize, winograd,
  * winograd_positions, winograd4_positions, winograd_small_tiles, fuse,
- * attention_keys; and this library's own: winograd_fp32, gemm_stages,
- * gemm_tiles, attention_generic, attention_fp32 (forms to compare, same
- * results within the bounds).  Returns SDHIP_ERROR naming the first unknown name.  "" resets
- * the defaults. */
+ * attention_keys; and this library's own: winograd_fp32, winograd_splits,
+ * gemm_stages, gemm_tiles, attention_generic, attention_fp32 (forms to
+ * compare, same results within the bounds).  Returns SDHIP_ERROR naming the
+ * first unknown name.  "" resets the defaults. */
 sdhip_status sdhip_set_tuning(const char *text);
 /* The value of one tuning field, or -1 if it has no such name. */
 int sdhip_get_tuning(const char *name);

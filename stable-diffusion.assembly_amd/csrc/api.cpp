@@ -63,6 +63,7 @@ const Field kFields[] = {
     {"winograd_positions", &Tuning::winograd_positions},
     {"winograd4_positions", &Tuning::winograd4_positions},
     {"winograd_small_tiles", &Tuning::winograd_small_tiles},
+    {"winograd_splits", &Tuning::winograd_splits},
     {"fuse", &Tuning::fuse},
     {"winograd_fp32", &Tuning::winograd_fp32},
     {"gemm_stages", &Tuning::gemm_stages},

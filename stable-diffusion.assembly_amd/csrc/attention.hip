@@ -535,18 +535,6 @@ __global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _
     }
 }
 
-template <int N>
-__device__ __forceinline__ void wait_loads() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// One 16-byte piece a lane of a 1 KB copy from global memory into LDS; the
-// LDS address is the wave's (lane l's piece lands 16 l bytes past it).
-__device__ __forceinline__ void copy_lds(const void *src, char *lds) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
-}
-
 // The online softmax of the wave's scores over KB keys, in base 2: the
 // accumulators hold the products of the keys by the queries times scale
 // log2(e), scaled by 2^-8 (the keys' and queries' 2^-4), as sh + 2^-11 sx;

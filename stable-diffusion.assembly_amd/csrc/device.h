@@ -195,6 +195,22 @@ __device__ __forceinline__ void split_index(uint32_t r, uint32_t ne1, uint32_t n
     i2 = q - i3 * ne2;
 }
 
+// ------------------------------------------------------------------ copies into LDS
+
+// Waits until at most N of the wave's vector memory loads are in flight
+// (s_waitcnt vmcnt(N), the other counters left alone).
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// One 16-byte piece a lane of a 1 KB copy from global memory into LDS; the
+// LDS address is the wave's (lane l's piece lands 16 l bytes past it).
+__device__ __forceinline__ void copy_lds(const void *src, char *lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
 // ------------------------------------------------------------------ grid
 
 // The 8 XCDs of an MI355X each take every 8th workgroup of a launch, and each

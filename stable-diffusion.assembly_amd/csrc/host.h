@@ -22,6 +22,9 @@ struct Tuning {
     int winograd_positions = 1024;   // the least outputs of an image Winograd is used for
     int winograd4_positions = 256;   // the least outputs of an image F(4x4) is used for
     int winograd_small_tiles = 256;  // the most tiles of all images taken as small images
+    // This library's own: the splits of the input channels of the small
+    // images' Winograd products, or 0 to choose by the size.
+    int winograd_splits = 0;
     int fuse = 1;                    // chains fused: 1; the caller computes them apart: 0
     // This library's own: Winograd's products on the single-precision MFMA
     // (1) instead of split FP16 parts (0), for comparison; results agree

@@ -206,8 +206,21 @@ __device__ __forceinline__ void load_g(const _Float16 *w, float (&g)[3][3]) {
 // weights in the same block fuses other pairs than one that converted them
 // earlier), and F(4x4)'s G (thirds, fifteenths) rounds differently each way;
 // written out, every kernel that transforms weights gets the same bits.
+// Where the coefficients are the folded constants of G, a zero one is left
+// out (it would add nothing but the sign of a zero).
 __device__ __forceinline__ float dot3(float c0, float x0, float c1, float x1, float c2, float x2) {
-    return fmaf(c2, x2, fmaf(c1, x1, c0 * x0));
+    float s = 0.0f;
+    bool any = false;
+    if (c0 != 0.0f) {
+        s = c0 * x0;
+        any = true;
+    }
+    if (c1 != 0.0f) {
+        s = any ? fmaf(c1, x1, s) : c1 * x1;
+        any = true;
+    }
+    if (c2 != 0.0f) s = any ? fmaf(c2, x2, s) : c2 * x2;
+    return s;
 }
 
 // (G g G^T) of one kernel: G g a column at a time, then (G g) G^T a row at a
@@ -597,7 +610,7 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
 // The products may come in `splits` parts over the input channels (the small
 // images' path), each with its own scale, prod[s][xi][oc][ld] and
 // shift[s][oc]; they are added in the order of s.
-template <int M>
+template <int M, bool PAIRS = false>
 __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod,
                                                       const int32_t *__restrict__ shift, int64_t splits = 1,
                                                       int64_t ld = 0) {
@@ -610,17 +623,49 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
     split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     if (ld == 0) ld = a.tiles;
     const int64_t plane = a.oc * ld;
+    // The splits' sums added in their order; with PAIRS, the loads of two
+    // splits at once.
     float m[A][A];
-    for (int64_t sp = 0; sp < splits; ++sp) {
-        const int unscale = shift != nullptr ? shift[sp * a.oc + oc] : 0;
-        const float *part = prod + sp * A * A * plane + static_cast<int64_t>(oc) * ld + tile;
+    if constexpr (!PAIRS) {
+        for (int64_t sp = 0; sp < splits; ++sp) {
+            const int unscale = shift != nullptr ? shift[sp * a.oc + oc] : 0;
+            const float *part = prod + sp * A * A * plane + static_cast<int64_t>(oc) * ld + tile;
 #pragma unroll
-        for (int i = 0; i < A; ++i)
+            for (int i = 0; i < A; ++i)
 #pragma unroll
-            for (int j = 0; j < A; ++j) {
-                const float v = ldexpf(part[(i * A + j) * plane], unscale);
-                m[i][j] = sp == 0 ? v : __fadd_rn(m[i][j], v);
-            }
+                for (int j = 0; j < A; ++j) {
+                    const float v = ldexpf(part[(i * A + j) * plane], unscale);
+                    m[i][j] = sp == 0 ? v : __fadd_rn(m[i][j], v);
+                }
+        }
+    } else {
+        const auto part = [&](int64_t sp, float (&p)[A][A]) {
+            const int unscale = shift[sp * a.oc + oc];
+            const float *src = prod + sp * A * A * plane + static_cast<int64_t>(oc) * ld + tile;
+#pragma unroll
+            for (int i = 0; i < A; ++i)
+#pragma unroll
+                for (int j = 0; j < A; ++j) p[i][j] = ldexpf(src[(i * A + j) * plane], unscale);
+        };
+        part(0, m);
+        int64_t sp = 1;
+        for (; sp + 1 < splits; sp += 2) {
+            float p0[A][A], p1[A][A];
+            part(sp, p0);
+            part(sp + 1, p1);
+#pragma unroll
+            for (int i = 0; i < A; ++i)
+#pragma unroll
+                for (int j = 0; j < A; ++j) m[i][j] = __fadd_rn(__fadd_rn(m[i][j], p0[i][j]), p1[i][j]);
+        }
+        if (sp < splits) {
+            float p0[A][A];
+            part(sp, p0);
+#pragma unroll
+            for (int i = 0; i < A; ++i)
+#pragma unroll
+                for (int j = 0; j < A; ++j) m[i][j] = __fadd_rn(m[i][j], p0[i][j]);
+        }
     }
     float am[M][A];
 #pragma unroll
@@ -731,24 +776,26 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
 
 // ------------------------------------------------------------------ small images
 
-// Images of few tiles (the deepest level of SD's UNet: 16x16 by F(4x4), 32
-// tiles for two images) take a path of their own, as the reference's small
-// path does (winograd.cc:1069-1144): the transformed weights are never written
-// out -- at this size they would be 4 times the FP16 weights, read back once
-// each -- but made in registers from the FP16 kernels, straight into the
-// MFMA's operands.
+// Images of few tiles (the deepest levels of SD's UNet: 16x16 by F(4x4) and
+// 8x8 by F(2x2), 32 tiles for two images) take a path of their own, as the
+// reference's small path does (winograd.cc:1069-1144): the transformed
+// weights are never written out -- at this size they would be 16/9 or 4 times
+// the FP16 weights, read back once each -- but made in registers from the
+// FP16 kernels, straight into the MFMA's operands.
 //
-//   inputs:   V[xi][part][tile][kp] * 2^-e_c as two FP16 planes, tiles padded
-//             to tp (a multiple of 16) with zeros;
-//   products: a block of four waves per (64 output channels, row i of U, split
-//             of the input channels), each wave 16 output channels: V's rows
-//             of row i staged through LDS, double-buffered, 16 input channels
-//             at a time; each lane makes U[i][*] of its output channel for
-//             four input channels from their nine FP16 numbers (G g G^T, one
-//             row), scaled by 2^(a_os + e_c - E) -- a_os from the split's
-//             greatest weight, as a_o from the channel's (section 0) -- and
-//             split, the operand A of v_mfma_f32_16x16x16_f16, the three
-//             products of split parts into the tile's sums; each split's sums
+//   inputs:   V[xi][part][c / 32][tile][c % 32] * 2^-e_c as two FP16 planes,
+//             tiles padded to tp (16 or 32) with zeros;
+//   products: a block of A waves per (16 output channels, split of the input
+//             channels), wave i taking row i of U, so that each kernel is read
+//             once (and once more, from the caches, for the split's greatest
+//             weight, the waves taking its steps in turn).  A step is 32 input
+//             channels, eight a lane: the lane makes row i of G g of each of
+//             its kernels, scaled by 2^(a_os + e_c - E) -- a_os from the
+//             split's greatest weight of the output channel, as a_o from the
+//             channel's (section 0) -- then each of the row's A numbers of U
+//             in turn, split into the operand A of v_mfma_f32_16x16x32_f16,
+//             and V's parts of that point are its operand B: the three
+//             products of split parts into the tiles' sums.  Each split's sums
 //             go to M[s][xi][oc][tp], and its scale shift[s][oc] = E - a_os;
 //   outputs:  the splits added in their order (outputs_kernel).
 constexpr int kSmallTilesMax = 32;
@@ -769,7 +816,10 @@ __global__ __launch_bounds__(256) void inputs_small_kernel(WinogradArgs a, int64
 #pragma unroll
             for (int q = 0; q < A; ++q) x[r][q] = ldexpf(x[r][q], s);
     }
+    // [c / 32][tile][c % 32] in each plane: the 16 tiles by 32 channels a
+    // wave of the products reads at once are 1 KB in a row.
     const int64_t plane = tp * kp;
+    const int64_t at = ((c >> 5) * tp + tile) * 32 + (c & 31);
 #pragma unroll
     for (int r = 0; r < A; ++r)
 #pragma unroll
@@ -777,104 +827,105 @@ __global__ __launch_bounds__(256) void inputs_small_kernel(WinogradArgs a, int64
             _Float16 hi, lo;
             split2(x[r][q], hi, lo);
             const int64_t xi = r * A + q;
-            v[(2 * xi) * plane + idx] = hi;
-            v[(2 * xi + 1) * plane + idx] = lo;
+            v[(2 * xi) * plane + at] = hi;
+            v[(2 * xi + 1) * plane + at] = lo;
         }
 }
 
-typedef _Float16 half4v __attribute__((ext_vector_type(4)));
-
-// The nine numbers of kernel (o, c0 + 4 kg + jj), jj = 0..3: 36 consecutive
-// FP16 numbers, nine 8-byte loads (zeros past OC or IC).
-__device__ __forceinline__ void load_kernels4(const WinogradArgs &a, int64_t o, int64_t c, float (&g)[4][9]) {
-    if (o < a.oc && c + 3 < a.ic) {
-        const half4v *p = reinterpret_cast<const half4v *>(a.w + (o * a.ic + c) * 9);
-#pragma unroll
-        for (int q = 0; q < 9; ++q) {
-            const half4v h = p[q];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) g[(4 * q + k) / 9][(4 * q + k) % 9] = static_cast<float>(h[k]);
-        }
-        return;
-    }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int q = 0; q < 9; ++q)
-            g[jj][q] = (o < a.oc && c + jj < a.ic) ? static_cast<float>(a.w[(o * a.ic + c + jj) * 9 + q]) : 0.0f;
-}
-
-// A block of 4 waves: 64 output channels (16 a wave) of row `row` of U, over
-// the input channels of split sp; the tiles' FP16 parts of the row's A planes
-// of V for 16 input channels at a time shared through LDS, double-buffered,
-// the next 16 channels' kernels and inputs loaded while these are multiplied.
-constexpr int kSmallLd = 16 + 4;  // halves per LDS row of V (16 channels)
+typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
 
 template <int M, int NT>
-__global__ __launch_bounds__(256) void products_small_kernel(WinogradArgs a, int64_t kp, int64_t tp, int64_t split_len,
-                                                             const int32_t *__restrict__ e,
-                                                             const _Float16 *__restrict__ v, float *__restrict__ prod,
-                                                             int32_t *__restrict__ shift) {
+__global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(WinogradArgs a, int64_t kp, int64_t split_len,
+                                                                        int64_t oc_blocks, const int32_t *__restrict__ e,
+                                                                        const _Float16 *__restrict__ v,
+                                                                        float *__restrict__ prod,
+                                                                        int32_t *__restrict__ shift) {
     constexpr int A = Mat<M>::A;
-    constexpr int TP = 16 * NT;                        // tiles held (tp <= TP)
-    constexpr int kRows = A * 2 * TP;                  // LDS rows of V: [j][part][tile]
-    constexpr int kLoads = (kRows * 2 + 255) / 256;    // 16-byte loads a thread (two a row)
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2][kRows * kSmallLd];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    constexpr int TP = 16 * NT;  // tiles, padded
+    __shared__ float greatest[A][16];
+    const int lane = threadIdx.x & 63;
+    const int row = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, kg = lane >> 4;
-    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * 64 + wave * 16;
-    const int row = static_cast<int>(blockIdx.y % A);
-    const int64_t sp = blockIdx.y / A;
+    // Consecutive blocks on one XCD take one split, whose V its L2 keeps.
+    const int64_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t sp = b / oc_blocks;
+    const int64_t o0 = (b - sp * oc_blocks) * 16;
+    const int64_t o = o0 + lr;
+    const bool o_in = o < a.oc;
+    const int64_t og = o_in ? o : a.oc - 1;
     const int64_t c_begin = sp * split_len;
     const int64_t c_end = c_begin + split_len < kp ? c_begin + split_len : kp;
-    const int64_t o = o0 + lr;
 
-    // E, the greatest e_c; the split's greatest weight of the lane's channel.
     int emax = kZeroChannel;
-    for (int64_t c = lane; c < a.ic; c += 64) emax = max(emax, e[c]);
+#pragma unroll 4
+    for (int64_t c = 4 * lane; c < a.ic; c += 256) {
+        const int4v q = *reinterpret_cast<const int4v *>(e + c);
+        emax = max(emax, max(max(q[0], q[1]), max(q[2], q[3])));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) emax = max(emax, __shfl_xor(emax, off, 64));
-    float wm = 0.0f;
-    for (int64_t c0 = c_begin; c0 < c_end; c0 += 16) {
-        float g[4][9];
-        load_kernels4(a, o, c0 + 4 * kg, g);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-            for (int q = 0; q < 9; ++q) wm = fmaxf(wm, fabsf(g[jj][q]));
-    }
-    wm = fmaxf(wm, __shfl_xor(wm, 16, 64));
-    wm = fmaxf(wm, __shfl_xor(wm, 32, 64));
-    const int ao = wm > 0.0f ? kTop - exponent_above(wm * Mat<M>::kWeightGain) : 0;
-    if (row == 0 && kg == 0 && o < a.oc) shift[sp * a.oc + o] = emax - ao;
 
-    // V's rows for 16 channels from c0: LDS row r = (j * 2 + part) * TP + tile,
-    // two 16-byte halves each; tiles past tp read tile 0 (never used).
-    const int64_t plane = tp * kp;
-    int4v vr[kLoads];
-    const auto load_v = [&](int64_t c0) {
+    // Kernels (og, c .. c + 7): 144 consecutive bytes.  Past IC, the last
+    // eight instead, finite numbers that meet V's zeros there.
+    const auto load_g = [&](int64_t c, int4v(&q)[9]) {
+        const int64_t cc = c < a.ic ? c : a.ic - 8;
+        const int4v *p = reinterpret_cast<const int4v *>(a.w + (og * a.ic + cc) * 9);
 #pragma unroll
-        for (int q = 0; q < kLoads; ++q) {
-            int idx = tid + 256 * q;
-            idx = idx < kRows * 2 ? idx : kRows * 2 - 1;
-            const int r = idx >> 1, h = idx & 1;
-            const int jp = r / TP;
-            int t = r - jp * TP;
-            t = t < tp ? t : 0;
-            const int64_t xi = row * A + (jp >> 1);
-            vr[q] = *reinterpret_cast<const int4v *>(v + (2 * xi + (jp & 1)) * plane + t * kp + c0 + 8 * h);
-        }
+        for (int k = 0; k < 9; ++k) q[k] = p[k];
     };
-    const auto store_v = [&](_Float16 *buf) {
+
+    // The split's greatest |weight| of channel o: FP16 magnitudes compare as
+    // their bits, two to a register.
+    {
+        ushort2v big = {0, 0};
+        for (int64_t c0 = c_begin + 32 * row; c0 < c_end; c0 += 32 * A) {
+            const int64_t c = c0 + 8 * kg;
+            if (o_in && c < a.ic) {
+                int4v q[9];
+                load_g(c, q);
 #pragma unroll
-        for (int q = 0; q < kLoads; ++q) {
-            const int idx = tid + 256 * q;
-            if (idx < kRows * 2) {
-                const int r = idx >> 1, h = idx & 1;
-                *reinterpret_cast<int4v *>(buf + r * kSmallLd + 8 * h) = vr[q];
+                for (int k = 0; k < 9; ++k)
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        big = __builtin_elementwise_max(big, __builtin_bit_cast(ushort2v, q[k][w] & 0x7fff7fff));
             }
+        }
+        int bits = big.x > big.y ? big.x : big.y;
+        bits = max(bits, __shfl_xor(bits, 16, 64));
+        bits = max(bits, __shfl_xor(bits, 32, 64));
+        if (kg == 0) {
+            greatest[row][lr] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(bits)));
+        }
+    }
+    __syncthreads();
+    float wm = 0.0f;
+#pragma unroll
+    for (int r = 0; r < A; ++r) wm = fmaxf(wm, greatest[r][lr]);
+    const int ao = wm > 0.0f ? kTop - exponent_above(wm * Mat<M>::kWeightGain) : 0;
+    if (row == 0 && kg == 0 && o_in) shift[sp * a.oc + o] = emax - ao;
+
+    // The kernels of a step, 16 output channels by 32 input channels, copied
+    // into LDS (two stages) by the block: a channel's 32 kernels are 36
+    // pieces of 16 bytes, rows of 37 pieces (odd, so that the 16 rows a read
+    // takes fall in distinct banks).  Pieces past the weights' end read their
+    // last piece: finite numbers that meet V's zeros, as any past IC do.
+    constexpr int kRowPieces = 37;
+    constexpr int kCopies = (16 * kRowPieces + 63) / 64;
+    __shared__ __attribute__((aligned(16))) char gbuf[2][kCopies * 1024];
+    const int64_t w_last = a.oc * a.ic * 9 - 8;
+    const auto copy_g = [&](int64_t c0, int stage) {
+#pragma unroll
+        for (int r = 0; r < (kCopies + A - 1) / A; ++r) {
+            const int n = row + r * A;
+            if (n >= kCopies) break;
+            const int p = n * 64 + lane;
+            int orow = p / kRowPieces, k = p - orow * kRowPieces;
+            if (orow > 15) orow = 15;
+            if (k > 35) k = 35;
+            const int64_t oo = o0 + orow < a.oc ? o0 + orow : a.oc - 1;
+            int64_t hw = (oo * a.ic + c0) * 9 + 8 * k;
+            hw = hw < w_last ? hw : w_last;
+            copy_lds(a.w + hw, gbuf[stage] + n * 1024);
         }
     };
 
@@ -883,65 +934,100 @@ __global__ __launch_bounds__(256) void products_small_kernel(WinogradArgs a, int
     for (int j = 0; j < A; ++j)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[j][t] = float4v{};
-
-    float g[4][9];
-    load_kernels4(a, o, c_begin + 4 * kg, g);
-    load_v(c_begin);
-    store_v(lds[0]);
-    __syncthreads();
-    int buf = 0;
-    for (int64_t c0 = c_begin; c0 < c_end; c0 += 16, buf ^= 1) {
-        const bool more = c0 + 16 < c_end;
-        float gn[4][9];
-        if (more) {
-            load_kernels4(a, o, c0 + 16 + 4 * kg, gn);
-            load_v(c0 + 16);
-        }
-        const int64_t c = c0 + 4 * kg;  // the lane's four input channels
-        // Row `row` of G g G^T of each of the four kernels, scaled and split.
-        half4v uh[A], ul[A];
+    // Row `row` of G, the same for every lane of the wave.
+    const float r0 = Mat<M>::g(row, 0), r1 = Mat<M>::g(row, 1), r2 = Mat<M>::g(row, 2);
+    const int64_t plane = static_cast<int64_t>(TP) * kp;
+    const _Float16 *vrow = v + static_cast<int64_t>(row * A) * 2 * plane;  // the same for the wave
+    const uint32_t vlane = static_cast<uint32_t>(lr * 32 + 8 * kg);         // the lane's, in V's planes
+    // V's parts of point (row, j) at step c0, operand B; each point's are
+    // loaded again for the next step as soon as its MFMAs have them.
+    half8 vb[A][NT][2];
+    const auto load_v = [&](int j, int64_t c0) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            float gg[3];
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int b = 0; b < 3; ++b)
-                gg[b] = dot3(Mat<M>::g(row, 0), g[jj][b], Mat<M>::g(row, 1), g[jj][3 + b], Mat<M>::g(row, 2),
-                             g[jj][6 + b]);
-            const int sc = (c + jj < a.ic) ? ao + e[c + jj] - emax : 0;
+            for (int part = 0; part < 2; ++part) {
+                const _Float16 *base = vrow + (2 * j + part) * plane + (c0 >> 5) * (TP * 32) + 16 * t * 32;
+                vb[j][t][part] = *reinterpret_cast<const half8 *>(base + vlane);
+            }
+    };
+    // The exponents e_c of the lane's eight channels at step c0.
+    int4v e0, e1;
+    const auto load_e = [&](int64_t c0) {
+        const int64_t c = c0 + 8 * kg;
+        const int4v *ep = reinterpret_cast<const int4v *>(e + (c < a.ic ? c : a.ic - 8));
+        e0 = ep[0];
+        e1 = ep[1];
+    };
+    copy_g(c_begin, 0);
+    load_e(c_begin);
 #pragma unroll
-            for (int j = 0; j < A; ++j) {
-                const float u = dot3(Mat<M>::g(j, 0), gg[0], Mat<M>::g(j, 1), gg[1], Mat<M>::g(j, 2), gg[2]);
-                _Float16 hi, lo;
-                split2(ldexpf(u, sc), hi, lo);
-                uh[j][jj] = hi;
-                ul[j][jj] = lo;
+    for (int j = 0; j < A; ++j) load_v(j, c_begin);
+    int stage = 0;
+    for (int64_t c0 = c_begin; c0 < c_end; c0 += 32, stage ^= 1) {
+        const int64_t next = c0 + 32 < c_end ? c0 + 32 : c0;  // past the last step: this one again
+        // The step's kernels, exponents and V in (all loaded a step ahead);
+        // every wave past the step before, whose stage the next step's
+        // kernels now overwrite.
+        wait_loads<0>();
+        __syncthreads();
+        int4v q[9];
+        const char *gl = gbuf[stage] + (lr * kRowPieces + 9 * kg) * 16;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) q[k] = *reinterpret_cast<const int4v *>(gl + 16 * k);
+        if (c0 + 32 < c_end) copy_g(c0 + 32, stage ^ 1);
+        const int64_t c = c0 + 8 * kg;
+        const bool c_in = c < a.ic;
+        // Row `row` of G g of each kernel, times 2^(a_os + e_c - E) and the
+        // split's 2^-4 (zero past IC): the power of two goes into the row's
+        // coefficients, which changes no rounding, and each term is a fused
+        // multiply-add of an FP16 number as it is.
+        float gi[8][3];
+        const _Float16 *h = reinterpret_cast<const _Float16 *>(q);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const int ec = jj < 4 ? e0[jj] : e1[jj - 4];
+            const float f = c_in ? ldexpf(1.0f, ao + ec - emax - 4) : 0.0f;
+            const float s0 = r0 * f, s1 = r1 * f, s2 = r2 * f;
+#pragma unroll
+            for (int bb = 0; bb < 3; ++bb) {
+                const float x0 = static_cast<float>(h[9 * jj + bb]);
+                const float x1 = static_cast<float>(h[9 * jj + 3 + bb]);
+                const float x2 = static_cast<float>(h[9 * jj + 6 + bb]);
+                gi[jj][bb] = fmaf(s2, x2, fmaf(s1, x1, fmaf(s0, x0, 0.0f)));
             }
         }
-        const _Float16 *cur = lds[buf];
+        // The loads of the next step go out where they are written, each
+        // point's V as soon as its MFMAs have read it, so that a whole step
+        // covers their latency.
+        __builtin_amdgcn_sched_barrier(0);
+        load_e(next);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < A; ++j)
+        for (int j = 0; j < A; ++j) {
+            half8 uh, ul;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const float u =
+                    dot3(Mat<M>::g(j, 0), gi[jj][0], Mat<M>::g(j, 1), gi[jj][1], Mat<M>::g(j, 2), gi[jj][2]);
+                const _Float16 hi = static_cast<_Float16>(u);
+                uh[jj] = hi;
+                ul[jj] = static_cast<_Float16>(fmaf(-1.0f, static_cast<float>(hi), u));
+            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const int tile = 16 * t + lr;
-                const half4v bh = *reinterpret_cast<const half4v *>(cur + ((2 * j) * TP + tile) * kSmallLd + 4 * kg);
-                const half4v bl =
-                    *reinterpret_cast<const half4v *>(cur + ((2 * j + 1) * TP + tile) * kSmallLd + 4 * kg);
-                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(uh[j], bh, acc[j][t], 0, 0, 0);
-                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(uh[j], bl, acc[j][t], 0, 0, 0);
-                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ul[j], bh, acc[j][t], 0, 0, 0);
+                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(uh, vb[j][t][0], acc[j][t], 0, 0, 0);
+                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(uh, vb[j][t][1], acc[j][t], 0, 0, 0);
+                acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ul, vb[j][t][0], acc[j][t], 0, 0, 0);
             }
-        if (more) {
-            store_v(lds[buf ^ 1]);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                for (int q = 0; q < 9; ++q) g[jj][q] = gn[jj][q];
+            __builtin_amdgcn_sched_barrier(0);
+            load_v(j, next);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
     }
     // Lane holds the sums of channels o0 + 4 kg + r, tile 16 t + lr; both
-    // operands were scaled by 2^-4 in the split.
-    const int64_t oplane = a.oc * tp;
+    // operands were scaled by 2^-4 in their splits.
+    const int64_t oplane = a.oc * TP;
 #pragma unroll
     for (int j = 0; j < A; ++j) {
         float *out = prod + (sp * A * A + row * A + j) * oplane;
@@ -950,7 +1036,7 @@ __global__ __launch_bounds__(256) void products_small_kernel(WinogradArgs a, int
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t oo = o0 + 4 * kg + r;
-                if (oo < a.oc && 16 * t + lr < tp) out[oo * tp + 16 * t + lr] = acc[j][t][r] * (kSplitUp * kSplitUp);
+                if (oo < a.oc) out[oo * TP + 16 * t + lr] = acc[j][t][r] * (kSplitUp * kSplitUp);
             }
     }
 }
@@ -964,15 +1050,13 @@ struct WorkLayout {
     size_t e, a, shift, f, u, v, m, total;  // byte offsets
 };
 
-// The small images' path: F(4x4) on the reference's small images (few tiles
-// in all, winograd.cc:194-196) of at most 32 tiles, FP16 kernels whose rows of
-// four channels are 8-byte aligned; not with winograd_fp32.  (F(2x2)'s
-// transformed weights are 16/9 of the FP16 ones, not 4: there the batched
-// products over written-out weights measure faster.)
+// The small images' path: F(4x4) or F(2x2) on the reference's small images
+// (few tiles in all, winograd.cc:194-196) of at most 32 tiles, FP16 kernels
+// whose rows of eight channels are 16-byte aligned; not with winograd_fp32.
 bool small_path(const WinogradArgs &a) {
-    return !tuning().winograd_fp32 && a.m == 4 && a.tiles <= kSmallTilesMax &&
-           a.n * ((a.ow + 1) / 2) * ((a.oh + 1) / 2) <= tuning().winograd_small_tiles && a.ic % 4 == 0 &&
-           (reinterpret_cast<uintptr_t>(a.w) & 7) == 0;
+    return !tuning().winograd_fp32 && a.tiles <= kSmallTilesMax &&
+           a.n * ((a.ow + 1) / 2) * ((a.oh + 1) / 2) <= tuning().winograd_small_tiles && a.ic % 8 == 0 &&
+           (reinterpret_cast<uintptr_t>(a.w) & 15) == 0;
 }
 
 WorkLayout work_layout(const WinogradArgs &a) {
@@ -987,14 +1071,16 @@ WorkLayout work_layout(const WinogradArgs &a) {
     };
     l.small = small_path(a);
     if (l.small) {
-        // Splits enough for about 2048 waves of A lanes groups, at most 4, of
-        // 64 channels or more.
+        // Splits of the input channels for about 1152 waves in all, fewer
+        // where each split's sums cost more to add than its waves gain
+        // (measured: F(4x4) 1280 -> 1280 at 16x16 takes 2, F(2x2) at 8x8 4);
+        // winograd_splits: that many instead.  Two steps or more a split.
         l.tp = round_up(a.tiles, 16);
         const int64_t waves = ceil_div(a.oc, 16) * (a.m + 2);  // of all the splits' blocks, per split
-        int64_t sp = ceil_div(2048, waves);
-        sp = sp < 1 ? 1 : (sp > 4 ? 4 : sp);
-        while (sp > 1 && l.kp / sp < 64) --sp;
-        l.split_len = round_up(ceil_div(l.kp, sp), 16);
+        int64_t sp = tuning().winograd_splits > 0 ? tuning().winograd_splits : (1152 + waves / 2) / waves;
+        sp = sp < 1 ? 1 : (sp > l.kp / 64 ? l.kp / 64 : sp);
+        sp = sp < 1 ? 1 : sp;
+        l.split_len = round_up(ceil_div(l.kp, sp), 32);
         l.splits = ceil_div(l.kp, l.split_len);
         l.e = take(a.ic * 4);
         l.a = take(a.oc * 4);
@@ -1057,7 +1143,7 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
                            nullptr);
         return launched(hipGetLastError(), "winograd");
     }
-    if (M == 4 && l.small) {
+    if (l.small) {
         {
             KernelScope scope(names[0].c_str(), stream);  // the inputs' exponents only
             hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(a.ic)), dim3(256), 0, stream, a, e,
@@ -1071,19 +1157,20 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         }
         {
             KernelScope scope(names[3].c_str(), stream);
-            const dim3 grid(static_cast<uint32_t>(ceil_div(a.oc, 64)), static_cast<uint32_t>(A * l.splits));
-            const dim3 block(256);
+            const int64_t oc_blocks = ceil_div(a.oc, 16);
+            const dim3 grid(static_cast<uint32_t>(oc_blocks * l.splits));
+            const dim3 block(64 * A);
             if (l.tp <= 16) {
-                hipLaunchKernelGGL((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.tp, l.split_len, e,
-                                   vh, m, shift);
+                hipLaunchKernelGGL((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.split_len,
+                                   oc_blocks, e, vh, m, shift);
             } else {
-                hipLaunchKernelGGL((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.tp, l.split_len, e,
-                                   vh, m, shift);
+                hipLaunchKernelGGL((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.split_len,
+                                   oc_blocks, e, vh, m, shift);
             }
         }
         KernelScope scope(names[4].c_str(), stream);
-        hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, shift,
-                           l.splits, l.tp);
+        hipLaunchKernelGGL((outputs_kernel<M, true>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
+                           shift, l.splits, l.tp);
         return launched(hipGetLastError(), "winograd (small images)");
     }
     // The transformed weights U 2^a_o and their exponents a_o, kept in the

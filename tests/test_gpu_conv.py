@@ -67,6 +67,29 @@ def test_conv2d(gpu, c, tuning):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("c,tuning", [
+    ((8, 8, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2), ""),                  # F(2x2), IC % 16 = 8, OC % 16 = 8
+    ((6, 6, 40, 20, 3, 3, 1, 1, 1, 1, 1, 1, 1), ""),                  # F(2x2), 9 tiles: one tile group
+    ((16, 16, 72, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1), ""),                # F(4x4), 16 tiles
+    ((17, 18, 56, 36, 3, 3, 1, 1, 1, 1, 1, 1, 1), ""),                # F(4x4), 25 tiles, ragged edges
+    ((8, 8, 200, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), "winograd_splits=3"),  # splits of 96, 96 and 8 channels
+    ((16, 16, 264, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2), "winograd_splits=5"),  # three of 96, the last past IC
+    ((16, 16, 64, 32, 3, 3, 1, 1, 1, 1, 1, 1, 2), "winograd_splits=1"),
+])
+def test_winograd_small_images(gpu, c, tuning):
+    """The small images' path (every tile of all images in one group, the
+    transformed weights made in registers): channel counts that end partway
+    through a step of 32 or a group of 16 output channels, one group of 16
+    tiles, and splits of the input channels of unequal lengths."""
+    x, k32, y, path, p = conv_case(gpu, c, seed=sum(c) + 5, tuning=tuning)
+    exact, mag = orc.exact_conv2d(x, k32, *p)
+    err = orc.metric(y.cpu().numpy(), exact, mag)
+    print(f"small images {c} path {path} [{tuning}]: {err:.3g}")
+    assert path == (4 if c[0] * c[1] >= 256 else 2)
+    assert err <= BOUND
+
+
+@pytest.mark.gpu
 def test_path_selection(gpu):
     """The paths the reference's predicates choose (winograd.cc:194-196,
     1204-1206, 2107-2123; hooks.cc:36-41)."""

@@ -161,7 +161,7 @@ def convolve(gpu, k_d, x_d, oh, ow):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape,path", [((2, 64, 40, 36), 4), ((2, 96, 8, 8), 2)])
+@pytest.mark.parametrize("shape,path", [((2, 64, 40, 36), 4), ((4, 96, 8, 8), 2)])
 def test_kept_winograd_weights(gpu, arena, shape, path):
     """Winograd's transformed weights (times 2^a_o) kept, as the reference
     keeps its transformed weights (winograd.cc:2147-2149): the first call

@@ -50,7 +50,7 @@ def test_tuning_parses_like_sdasm_tune():
     for name, value in (("bits", 0), ("input_bits", 8), ("group", 64), ("weight_group", 1), ("quantize", 7),
                         ("winograd", 2), ("winograd_positions", 1024), ("winograd4_positions", 256),
                         ("winograd_small_tiles", 256), ("fuse", 1), ("attention_keys", 256),
-                        ("attention_fp32", 0), ("attention_generic", 0)):
+                        ("attention_fp32", 0), ("attention_generic", 0), ("winograd_splits", 0)):
         assert sdhip.get_tuning(name) == value
 
 
