@@ -656,6 +656,124 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     }
 }
 
+// ------------------------------------------------------------------ convolution by columns
+
+// The direct convolution of kernels other than 1x1 as an explicit im2col and
+// a product split along K: the columns gathered once (columns_kernel), the
+// split products of the FP16 weights by the split columns into partial sums
+// (conv_columns_kernel, as many splits as fill the chip when the output has
+// few blocks -- the deep, long-K layers), and the splits added in their
+// order with the chain applied (conv_sum_kernel).  K = IC KH KW a multiple
+// of the K-step.
+
+// cols[p][k] for positions p and k = (ic, kh, kw), zeros outside the image;
+// a thread four consecutive k of one position.
+template <bool K3>
+__global__ __launch_bounds__(256) void columns_kernel(ConvArgs c, float *__restrict__ cols) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t quads = c.K / 4;
+    if (t >= c.P * quads) return;
+    const int64_t p = t / quads;
+    const uint32_t k0 = static_cast<uint32_t>(t - p * quads) * 4;
+    uint32_t ox, oy, n;
+    split_index(static_cast<uint32_t>(p), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
+    const int32_t iy0 = static_cast<int32_t>(oy) * c.s1 - c.p1;
+    const int32_t ix0 = static_cast<int32_t>(ox) * c.s0 - c.p0;
+    const float *img = c.x + static_cast<int64_t>(n) * c.xnb3;
+    const uint32_t taps = K3 ? 9u : static_cast<uint32_t>(c.taps);
+    const uint32_t kwidth = K3 ? 3u : static_cast<uint32_t>(c.kw);
+    float4 v;
+    float *ve = reinterpret_cast<float *>(&v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t k = k0 + e;
+        const uint32_t ic = k / taps;
+        const uint32_t tap = k - ic * taps;
+        const uint32_t kh = tap / kwidth;
+        const uint32_t kw = tap - kh * kwidth;
+        const int32_t iy = iy0 + static_cast<int32_t>(kh) * c.d1;
+        const int32_t ix = ix0 + static_cast<int32_t>(kw) * c.d0;
+        ve[e] = (iy >= 0 && iy < c.ih && ix >= 0 && ix < c.iw)
+                    ? img[static_cast<int64_t>(ic) * c.xnb2 + static_cast<int64_t>(iy) * c.xnb1 + ix]
+                    : 0.0f;
+    }
+    *reinterpret_cast<float4 *>(cols + p * c.K + k0) = v;
+}
+
+// part[s][oc][p] = 16 sum over split s's k of W[oc][k] cols[p][k]: blocks of
+// 64 output channels by 64 positions, the splits of split_len (a multiple of
+// the K-step) one after the other in the grid.
+template <int NS>
+__global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const float *__restrict__ cols,
+                                                           int64_t split_len, int64_t p_blocks,
+                                                           float *__restrict__ part) {
+    constexpr int BM = 64, BN = 64;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<1, 1, kSplitB>()];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave >> 1;
+    const int wc = wave & 1;
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t per_split = c.oc_blocks * p_blocks;
+    const int64_t sp = b / per_split;
+    const int64_t rem = b - sp * per_split;
+    const int64_t pb = rem / c.oc_blocks;  // neighbouring blocks share positions
+    const int64_t ob = rem - pb * c.oc_blocks;
+    const int64_t oc0 = ob * BM, p0 = pb * BN;
+    const int64_t k_begin = sp * split_len;
+    const int64_t k_len = c.K - k_begin < split_len ? c.K - k_begin : split_len;
+
+    float16v acc[1][1];
+    acc[0][0] = float16v{};
+    F16Rows<BM, true, true> wa[NS];
+    F32Rows<BN, true, true> xb[NS];
+    const auto w_row = [&](int r) -> int64_t { return oc0 + r < c.oc ? oc0 + r : -1; };
+    const auto p_row = [&](int r) -> int64_t { return p0 + r < c.P ? p0 + r : -1; };
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        wa[q].init(c.w + k_begin, c.K, w_row, k_len, tid);
+        xb[q].init(cols + k_begin, c.K, p_row, k_len, tid);
+    }
+    main_loop<1, 1, kSplitB, NS>(acc, wa, xb, lds, k_len / kBK, tid, lane, wr, wc);
+
+    // The columns were scaled by 2^-4 in their split.
+    const int64_t pos = p0 + wc * 32 + (lane & 31);
+    if (pos >= c.P) return;
+    const int64_t obase = oc0 + wr * 32 + 4 * (lane >> 5);
+    float *out = part + sp * c.oc * c.P + pos;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int64_t oc = obase + tile_row(e);
+        if (oc < c.oc) out[oc * c.P] = acc[0][0][e] * kSplitUp;
+    }
+}
+
+// y = the splits' partial sums added in their order, from the redirect's
+// values if asked, and the chain (as the direct kernel's epilogue).
+__global__ __launch_bounds__(256) void conv_sum_kernel(ConvArgs c, const float *__restrict__ part, int64_t splits) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t plane = c.oc * c.P;
+    if (t >= plane) return;
+    const int64_t oc = t / c.P, p = t - oc * c.P;
+    float v = part[t];
+    for (int64_t sp = 1; sp < splits; ++sp) v = __fadd_rn(v, part[sp * plane + t]);
+    uint32_t ox, oy, n;
+    split_index(static_cast<uint32_t>(p), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
+    const int64_t at = static_cast<int64_t>(n) * c.ynb3 + oc * c.ynb2 + static_cast<int64_t>(oy) * c.ynb1 + ox;
+    if (c.from_redirect) v = __fadd_rn(c.y[at], v);
+    float vv[1] = {v};
+    const int64_t in_image = static_cast<int64_t>(oy) * c.ow + ox;
+    apply_chain_block<1>(c.chain, vv, [&](int s, int) -> int64_t {
+        const DevStep &st = c.chain.steps[s];
+        const int64_t xy =
+            st.flat01 ? in_image * st.nb[0] : static_cast<int64_t>(ox) * st.nb[0] + static_cast<int64_t>(oy) * st.nb[1];
+        return xy + static_cast<int64_t>(n) * st.nb[3] + oc * st.nb[2];
+    });
+    c.y[at] = vv[0];
+}
+
 // ------------------------------------------------------------------ Winograd's products
 
 // C[b][m][n] = sum_k A[b][m][k] B[b][n][k] for the batches b: A already split
@@ -843,6 +961,71 @@ hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream
         return pointwise ? launch_conv_t<TM, TN, true>(c, stages, stream)
                          : launch_conv_t<TM, TN, false>(c, stages, stream);
     });
+}
+
+namespace {
+
+struct ColumnsPlan {
+    int64_t p_blocks, blocks, splits, split_len;
+    size_t cols_bytes, total;
+};
+
+ColumnsPlan columns_plan(const ConvArgs &c) {
+    ColumnsPlan l{};
+    l.p_blocks = (c.P + 63) / 64;
+    l.blocks = ((c.oc + 63) / 64) * l.p_blocks;
+    // Splits for about 512 blocks in all, of four K-steps or more each.
+    const int64_t steps = c.K / kBK;
+    int64_t sp = (512 + l.blocks - 1) / l.blocks;
+    const int64_t most = steps / 4 > 1 ? steps / 4 : 1;
+    sp = sp < most ? sp : most;
+    l.split_len = (steps + sp - 1) / sp * kBK;
+    l.splits = (c.K + l.split_len - 1) / l.split_len;
+    l.cols_bytes = static_cast<size_t>((c.P * c.K * 4 + 255) / 256 * 256);
+    l.total = l.cols_bytes + static_cast<size_t>(l.splits * c.oc * c.P * 4);
+    return l;
+}
+
+}  // namespace
+
+bool conv_columns_taken(const ConvArgs &c) {
+    const bool pointwise = c.kw == 1 && c.kh == 1 && c.s0 == 1 && c.s1 == 1 && c.p0 == 0 && c.p1 == 0;
+    return !pointwise && c.K % kBK == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0 &&
+           c.P * c.K <= (int64_t{1} << 28) && c.P < (int64_t{1} << 31);
+}
+
+size_t conv_columns_work_size(const ConvArgs &c) { return columns_plan(c).total; }
+
+hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipStream_t stream) {
+    const ColumnsPlan l = columns_plan(c);
+    float *cols = static_cast<float *>(work);
+    float *part = reinterpret_cast<float *>(static_cast<char *>(work) + l.cols_bytes);
+    {
+        KernelScope scope("conv_direct.columns", stream);
+        const dim3 grid(static_cast<uint32_t>((c.P * (c.K / 4) + 255) / 256));
+        if (c.kh == 3 && c.kw == 3) {
+            hipLaunchKernelGGL((columns_kernel<true>), grid, dim3(256), 0, stream, c, cols);
+        } else {
+            hipLaunchKernelGGL((columns_kernel<false>), grid, dim3(256), 0, stream, c, cols);
+        }
+    }
+    {
+        KernelScope scope("conv_direct", stream);
+        ConvArgs a = c;
+        a.oc_blocks = (c.oc + 63) / 64;
+        const dim3 grid(static_cast<uint32_t>(l.blocks * l.splits));
+        if (g.stages == 4) {
+            hipLaunchKernelGGL((conv_columns_kernel<4>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
+                               part);
+        } else {
+            hipLaunchKernelGGL((conv_columns_kernel<2>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
+                               part);
+        }
+    }
+    KernelScope scope("conv_direct.sum", stream);
+    hipLaunchKernelGGL(conv_sum_kernel, dim3(static_cast<uint32_t>((c.oc * c.P + 255) / 256)), dim3(256), 0, stream, c,
+                       part, l.splits);
+    return hipGetLastError();
 }
 
 hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream) {

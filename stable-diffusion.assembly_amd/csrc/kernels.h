@@ -60,6 +60,14 @@ struct ConvArgs {
 
 hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream);
 
+// The direct convolution by columns (gemm.hip): taken for kernels other than
+// 1x1 whose K = IC KH KW is a multiple of 32 and whose FP16 weights are
+// 16-byte aligned, columns of at most 2^28 numbers; its work buffer holds the
+// columns and the splits' partial sums.
+bool conv_columns_taken(const ConvArgs &c);
+size_t conv_columns_work_size(const ConvArgs &c);
+hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipStream_t stream);
+
 // Batched products c[b][m][n] = sum_k a[b][m][k] b[b][n][k]: a already split
 // into two FP16 planes (hi, and lo `a_plane` elements after it), or single
 // precision with a scale per column (a32, a_scale), b single precision, both

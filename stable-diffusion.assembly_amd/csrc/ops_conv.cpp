@@ -85,6 +85,40 @@ int path_of(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_t
     return 0;
 }
 
+ConvArgs conv_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
+                   const int32_t *op) {
+    ConvArgs c{};
+    c.x = static_cast<const float *>(input->data);
+    c.xnb1 = input->nb[1] / 4;
+    c.xnb2 = input->nb[2] / 4;
+    c.xnb3 = input->nb[3] / 4;
+    c.iw = input->ne[0];
+    c.ih = input->ne[1];
+    c.ic = input->ne[2];
+    c.n = input->ne[3];
+    c.w = static_cast<const _Float16 *>(kernel->data);
+    c.kw = kernel->ne[0];
+    c.kh = kernel->ne[1];
+    c.oc = kernel->ne[3];
+    c.y = static_cast<float *>(y->data);
+    c.ynb1 = y->nb[1] / 4;
+    c.ynb2 = y->nb[2] / 4;
+    c.ynb3 = y->nb[3] / 4;
+    c.ow = y->ne[0];
+    c.oh = y->ne[1];
+    c.s0 = op[0];
+    c.s1 = op[1];
+    c.p0 = op[2];
+    c.p1 = op[3];
+    c.d0 = op[4];
+    c.d1 = op[5];
+    c.K = c.ic * c.kh * c.kw;
+    c.taps = c.kh * c.kw;
+    c.plane = c.oh * c.ow;
+    c.P = c.n * c.plane;
+    return c;
+}
+
 WinogradArgs winograd_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
                            const int32_t *op, int m) {
     WinogradArgs a{};
@@ -136,6 +170,10 @@ size_t sdhip_conv2d_work_size(const sdhip_tensor *kernel, const sdhip_tensor *in
     if (path == 2 || path == 4) {
         return winograd_work_size(winograd_args(kernel, input, y, op_params, path));
     }
+    if (path == 0) {
+        const ConvArgs c = conv_args(kernel, input, y, op_params);
+        if (conv_columns_taken(c)) return conv_columns_work_size(c);
+    }
     return 0;
 }
 
@@ -165,37 +203,17 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
         }
         return winograd(a, work, st);
     }
-    ConvArgs c{};
-    c.x = static_cast<const float *>(input->data);
-    c.xnb1 = input->nb[1] / 4;
-    c.xnb2 = input->nb[2] / 4;
-    c.xnb3 = input->nb[3] / 4;
-    c.iw = input->ne[0];
-    c.ih = input->ne[1];
-    c.ic = input->ne[2];
-    c.n = input->ne[3];
-    c.w = static_cast<const _Float16 *>(kernel->data);
-    c.kw = kernel->ne[0];
-    c.kh = kernel->ne[1];
-    c.oc = kernel->ne[3];
+    ConvArgs c = conv_args(kernel, input, y, op_params);
     c.y = out;
-    c.ynb1 = y->nb[1] / 4;
-    c.ynb2 = y->nb[2] / 4;
-    c.ynb3 = y->nb[3] / 4;
-    c.ow = y->ne[0];
-    c.oh = y->ne[1];
-    c.s0 = op_params[0];
-    c.s1 = op_params[1];
-    c.p0 = op_params[2];
-    c.p1 = op_params[3];
-    c.d0 = op_params[4];
-    c.d1 = op_params[5];
-    c.K = c.ic * c.kh * c.kw;
-    c.taps = c.kh * c.kw;
-    c.plane = c.oh * c.ow;
-    c.P = c.n * c.plane;
     c.from_redirect = from_redirect;
     c.chain = dc;
+    if (conv_columns_taken(c)) {
+        const size_t need = conv_columns_work_size(c);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        return launched(launch_conv_columns(c, work, gemm_shape(), st), "conv2d by columns");
+    }
     return launched(launch_conv_direct(c, gemm_shape(), st), "conv2d direct");
 }
 
