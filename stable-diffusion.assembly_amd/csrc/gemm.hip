@@ -567,6 +567,81 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ MUL_MAT split along K
+
+// Products of few output blocks and long K (the UNet's deepest level, 512
+// tokens by 1280 features): partial sums of splits of K in blocks of 64 x 64
+// (part[s][m][n]), then added in their order with the chain applied, as the
+// single-pass epilogue does.  Both operands as in mul_mat_kernel, whole
+// K-steps, rows 16-byte aligned.
+template <int NS>
+__global__ __launch_bounds__(256) void mul_mat_split_kernel(MulMatArgs p, int64_t split_len,
+                                                            float *__restrict__ part) {
+    constexpr int BM = 64, BN = 64;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<1, 1, kSplitA>()];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave >> 1;
+    const int wc = wave & 1;
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t per_split = ((p.M + BM - 1) / BM) * p.col_blocks;
+    const int64_t sp = b / per_split;
+    const int64_t rem = b - sp * per_split;
+    const int64_t mb = rem / p.col_blocks;  // neighbouring blocks share rows of x
+    const int64_t nb = rem - mb * p.col_blocks;
+    const int64_t m0 = mb * BM, n0 = nb * BN;
+    const int64_t k_begin = sp * split_len;
+    const int64_t k_len = p.K - k_begin < split_len ? p.K - k_begin : split_len;
+
+    float16v acc[1][1];
+    acc[0][0] = float16v{};
+    F32Rows<BM, true, true> xa[NS];
+    F16Rows<BN, true, true> wb[NS];
+    const auto x_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : -1; };
+    const auto w_row = [&](int r) -> int64_t { return n0 + r < p.N ? n0 + r : -1; };
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        xa[q].init(p.x + k_begin, p.ldx, x_row, k_len, tid);
+        wb[q].init(p.w + k_begin, p.ldw, w_row, k_len, tid);
+    }
+    main_loop<1, 1, kSplitA, NS>(acc, xa, wb, lds, k_len / kBK, tid, lane, wr, wc);
+
+    // x was scaled by 2^-4 in its split.
+    const int64_t n = n0 + wc * 32 + (lane & 31);
+    if (n >= p.N) return;
+    const int64_t mbase = m0 + wr * 32 + 4 * (lane >> 5);
+    float *out = part + sp * p.M * p.N + n;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int64_t m = mbase + tile_row(e);
+        if (m < p.M) out[m * p.N] = acc[0][0][e] * kSplitUp;
+    }
+}
+
+__global__ __launch_bounds__(256) void mul_mat_sum_kernel(MulMatArgs p, const float *__restrict__ part,
+                                                          int64_t splits) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t plane = p.M * p.N;
+    if (t >= plane) return;
+    const int64_t m = t / p.N, n = t - m * p.N;
+    float v = part[t];
+    for (int64_t sp = 1; sp < splits; ++sp) v = __fadd_rn(v, part[sp * plane + t]);
+    float *out = p.y + m * p.ldy + n;
+    if (p.from_redirect) v = __fadd_rn(*out, v);
+    float vv[1] = {v};
+    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
+    apply_chain_block<1>(p.chain, vv, [&](int s, int) -> int64_t {
+        const DevStep &st = p.chain.steps[s];
+        if (st.flat123) return n * st.nb[0] + m * st.nb[1];
+        uint32_t i1, i2, i3;
+        split_index(static_cast<uint32_t>(m), ne1, ne2, i1, i2, i3);
+        return n * st.nb[0] + i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+    });
+    *out = vv[0];
+}
+
 // ------------------------------------------------------------------ direct convolution
 
 // y[n][oc][pos] = sum_k W[oc][k] columns[k][pos], the chain applied; W rows
@@ -961,6 +1036,60 @@ hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream
         return pointwise ? launch_conv_t<TM, TN, true>(c, stages, stream)
                          : launch_conv_t<TM, TN, false>(c, stages, stream);
     });
+}
+
+namespace {
+
+struct MulMatSplitPlan {
+    int64_t blocks, splits, split_len;
+};
+
+// Splits of K for about 512 blocks where the output has fewer than 256 of
+// 64 x 64, each of 32 K-steps or more (shorter ones cost more in partial sums
+// than their blocks gain: measured at 512 x 1280 x 1280, two splits of 20
+// steps 19.7 us against 17.3 in one pass); one where that leaves no room.
+MulMatSplitPlan mul_mat_split_plan(const MulMatArgs &p) {
+    MulMatSplitPlan l{};
+    l.blocks = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+    const int64_t steps = p.K / kBK;
+    int64_t sp = l.blocks < 256 ? (512 + l.blocks - 1) / l.blocks : 1;
+    const int64_t most = steps / 32 > 1 ? steps / 32 : 1;
+    sp = sp < most ? sp : most;
+    l.split_len = (steps + sp - 1) / sp * kBK;
+    l.splits = steps > 0 ? (p.K + l.split_len - 1) / l.split_len : 1;
+    return l;
+}
+
+}  // namespace
+
+bool mul_mat_split_taken(const MulMatArgs &p) {
+    const bool aligned = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0 && p.ldw % 8 == 0 &&
+                         (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
+    return aligned && p.K % kBK == 0 && mul_mat_split_plan(p).splits > 1;
+}
+
+size_t mul_mat_split_work_size(const MulMatArgs &p) {
+    return static_cast<size_t>(mul_mat_split_plan(p).splits * p.M * p.N * 4);
+}
+
+hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hipStream_t stream) {
+    const MulMatSplitPlan l = mul_mat_split_plan(p);
+    float *part = static_cast<float *>(work);
+    MulMatArgs a = p;
+    a.col_blocks = (p.N + 63) / 64;
+    {
+        KernelScope scope("mul_mat", stream);
+        const dim3 grid(static_cast<uint32_t>(l.blocks * l.splits));
+        if (g.stages == 4) {
+            hipLaunchKernelGGL((mul_mat_split_kernel<4>), grid, dim3(256), 0, stream, a, l.split_len, part);
+        } else {
+            hipLaunchKernelGGL((mul_mat_split_kernel<2>), grid, dim3(256), 0, stream, a, l.split_len, part);
+        }
+    }
+    KernelScope scope("mul_mat.sum", stream);
+    hipLaunchKernelGGL(mul_mat_sum_kernel, dim3(static_cast<uint32_t>((p.M * p.N + 255) / 256)), dim3(256), 0, stream,
+                       a, part, l.splits);
+    return hipGetLastError();
 }
 
 namespace {

@@ -60,6 +60,14 @@ struct ConvArgs {
 
 hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream);
 
+// MUL_MAT split along K (gemm.hip): taken for products of fewer than 256
+// output blocks of 64 x 64 whose K (a multiple of 32) gives two splits of 32
+// K-steps or more, x and W rows 16-byte aligned; its work buffer holds the
+// splits' partial sums.
+bool mul_mat_split_taken(const MulMatArgs &p);
+size_t mul_mat_split_work_size(const MulMatArgs &p);
+hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hipStream_t stream);
+
 // The direct convolution by columns (gemm.hip): taken for kernels other than
 // 1x1 whose K = IC KH KW is a multiple of 32 and whose FP16 weights are
 // 16-byte aligned, columns of at most 2^28 numbers; its work buffer holds the

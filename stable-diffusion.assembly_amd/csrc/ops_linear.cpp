@@ -79,7 +79,8 @@ size_t sdhip_mul_mat_work_size(const sdhip_tensor *w, const sdhip_tensor *x, con
     if (mul_mat_quantized(x)) {
         return quantized_linear_work_size(w->ne[0], w->ne[1], x->ne[1] * x->ne[2] * x->ne[3]);
     }
-    return 0;
+    const MulMatArgs a = args_of(w, x, y);
+    return mul_mat_split_taken(a) ? mul_mat_split_work_size(a) : 0;
 }
 
 sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
@@ -99,6 +100,13 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
             return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
         }
         return quantized_linear(a, false, work, st);
+    }
+    if (mul_mat_split_taken(a)) {
+        const size_t need = mul_mat_split_work_size(a);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        return launched(launch_mul_mat_split(a, work, gemm_shape(), st), "mul_mat split along K");
     }
     return launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
 }

@@ -89,6 +89,36 @@ def test_mul_mat_residual(gpu, from_redirect):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("from_redirect", [False, True])
+def test_mul_mat_split_chain(gpu, from_redirect):
+    """A product of few output blocks and long K, split along K: the splits'
+    sums added with bias, a per-token scale and a residual (or begun from the
+    residual), the epilogue of the single pass."""
+    K, N, M, B = 4096, 200, 150, 2  # 20 blocks of 64 x 64: four splits of 1024
+    r = rng(13)
+    bias = dev(uniform(r, (N,), 1.0), gpu)
+    scale = dev(uniform(r, (B, M, 1), 1.0), gpu)
+    res = uniform(r, (B, M, N), 1.0)
+    res_d = dev(res, gpu)
+    b = bias.cpu().numpy().astype(np.float64)
+    s = scale.cpu().numpy().astype(np.float64)
+    if from_redirect:
+        out = res_d.clone()
+        y, exact, mag = run_mul_mat(gpu, K, N, M, B, 7, [("add", bias), ("mul", scale)], redirect=out,
+                                    from_redirect=True)
+        want = (res + exact + b) * s
+        m2 = (np.abs(res) + mag + np.abs(b)) * np.abs(s)
+    else:
+        out = unwritten((B, M, N), gpu)
+        y, exact, mag = run_mul_mat(gpu, K, N, M, B, 7, [("add", bias), ("mul", scale), ("add", res_d)],
+                                    redirect=out)
+        want = (exact + b) * s + res
+        m2 = (mag + np.abs(b)) * np.abs(s) + np.abs(res)
+    assert torch.isnan(y).all(), "the product's own tensor is not written under a redirect"
+    assert orc.metric(out.cpu().numpy(), want, m2) <= BOUND_SPLIT
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("K,half,M,B", [(320, 1280, 200, 2), (40, 100, 37, 1), (96, 2000, 300, 1),
                                         (1280, 5120, 64, 2)])
 def test_gated(gpu, K, half, M, B):
