@@ -223,6 +223,25 @@ __device__ __forceinline__ float dot3(float c0, float x0, float c1, float x1, fl
     return s;
 }
 
+// sum_i c(i) x(i) over N terms with its roundings written out, as dot3: the
+// first term of a nonzero coefficient rounded, the others fused in turn, the
+// zero coefficients of the folded tables left out -- the same bits in every
+// kernel that transforms the inputs.
+template <int N, class C, class X>
+__device__ __forceinline__ float dot_n(C c, X x) {
+    float s = 0.0f;
+    bool any = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float ci = c(i);
+        if (ci != 0.0f) {
+            s = any ? fmaf(ci, x(i), s) : ci * x(i);
+            any = true;
+        }
+    }
+    return s;
+}
+
 // (G g G^T) of one kernel: G g a column at a time, then (G g) G^T a row at a
 // time (winograd.cc:1281-1300).
 template <int M>
@@ -249,18 +268,24 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
 // kp.
 constexpr int kWeightOc = 4, kWeightIc = 64;
 
+// LDS of a block of weights_split: the 4 floats of the reduction, then the
+// staged parts.
 template <int M>
-__global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
-                                                            int64_t kp, const int32_t *__restrict__ e,
-                                                            const int32_t *__restrict__ amax, _Float16 *__restrict__ u,
-                                                            int32_t *__restrict__ shift) {
+constexpr int kWeightLds = 16 + 2 * Mat<M>::A * Mat<M>::A * kWeightOc * kWeightIc * 2;
+
+// Block (bx, by) of weights_split, its LDS at `lds`.
+template <int M>
+__device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__ w, int64_t oc, int64_t ic, int64_t kp,
+                                                    const int32_t *__restrict__ e, const int32_t *__restrict__ amax,
+                                                    _Float16 *__restrict__ u, int32_t *__restrict__ shift, int64_t bx,
+                                                    int64_t by, char *lds) {
     constexpr int A = Mat<M>::A;
     constexpr int kRows = 2 * A * A;
-    __shared__ float scratch[4];
-    __shared__ __attribute__((aligned(16))) _Float16 stage[kRows][kWeightOc][kWeightIc];
+    float *scratch = reinterpret_cast<float *>(lds);
+    auto stage = reinterpret_cast<_Float16(*)[kWeightOc][kWeightIc]>(lds + 16);
     const int tid = threadIdx.x;
-    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kWeightOc;
-    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kWeightIc;
+    const int64_t o0 = bx * kWeightOc;
+    const int64_t c0 = by * kWeightIc;
     const int ol = tid / kWeightIc, cl = tid % kWeightIc;
     const int64_t o = o0 + ol, c = c0 + cl;
     // The thread's kernel and exponents first, so that their loads overlap
@@ -276,7 +301,7 @@ __global__ __launch_bounds__(256) void weights_split_kernel(const _Float16 *__re
     int emax = kZeroChannel;
     for (int64_t k = tid; k < ic; k += 256) emax = max(emax, e[k]);
     const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
-    if (o < oc && blockIdx.y == 0 && cl == 0) shift[o] = E - ao;
+    if (o < oc && by == 0 && cl == 0) shift[o] = E - ao;
     float t[A][A] = {};
     int s = 0;
     if (live) {
@@ -381,21 +406,13 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
 #pragma unroll
     for (int r = 0; r < A; ++r)
 #pragma unroll
-        for (int j = 0; j < A; ++j) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < A; ++i) s += Mat<M>::bt(r, i) * d[i][j];
-            bd[r][j] = s;
-        }
+        for (int j = 0; j < A; ++j)
+            bd[r][j] = dot_n<A>([&](int i) { return Mat<M>::bt(r, i); }, [&](int i) { return d[i][j]; });
 #pragma unroll
     for (int r = 0; r < A; ++r)
 #pragma unroll
-        for (int s = 0; s < A; ++s) {
-            float x = 0.0f;
-#pragma unroll
-            for (int j = 0; j < A; ++j) x += bd[r][j] * Mat<M>::bt(s, j);
-            v[r][s] = x;
-        }
+        for (int s = 0; s < A; ++s)
+            v[r][s] = dot_n<A>([&](int j) { return Mat<M>::bt(s, j); }, [&](int j) { return bd[r][j]; });
 }
 
 // V[xi][tile][ic] * 2^-e_c in single precision, v[xi][tile][kp], zeros for
@@ -406,28 +423,21 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
 // channels.
 constexpr int kInTiles = 8, kInChannels = 32;
 
+// LDS of a block of inputs_split: the staged V, rows of a tile 40 floats
+// apart (16-byte aligned, and the 64 lanes of a wave -- 8 tiles by 8
+// channels -- in at most two to a bank).
 template <int M>
-__global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
-                                                           float *__restrict__ v, const int32_t *__restrict__ amax,
-                                                           float *__restrict__ f, int32_t *__restrict__ shift) {
+constexpr int kInputLds = Mat<M>::A * Mat<M>::A * kInTiles * (kInChannels + 8) * 4;
+
+// Block (bx, by) of inputs_split, its LDS at `lds`.
+template <int M>
+__device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_t kp, const int32_t *__restrict__ e,
+                                                   float *__restrict__ v, int64_t bx, int64_t by, char *lds) {
     constexpr int A = Mat<M>::A;
-    if (f != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
-        // With the weights kept: E, the greatest e_c; each channel's scale of
-        // the weights 2^(e_c - E) (zero past IC), and each output channel's
-        // shift E - a_o.
-        __shared__ float scratch[4];
-        int emax = kZeroChannel;
-        for (int64_t c = threadIdx.x; c < a.ic; c += 256) emax = max(emax, e[c]);
-        const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
-        for (int64_t c = threadIdx.x; c < kp; c += 256) f[c] = c < a.ic ? ldexpf(1.0f, e[c] - E) : 0.0f;
-        for (int64_t o = threadIdx.x; o < a.oc; o += 256) shift[o] = E - amax[o];
-    }
-    // Rows of a tile 40 floats apart: 16-byte aligned, and the 64 lanes of a
-    // wave (8 tiles by 8 channels) in at most two to a bank.
-    __shared__ __attribute__((aligned(16))) float stage[A * A][kInTiles][kInChannels + 8];
+    auto stage = reinterpret_cast<float(*)[kInTiles][kInChannels + 8]>(lds);
     const int tid = threadIdx.x;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kInTiles;
-    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kInChannels;
+    const int64_t t0 = bx * kInTiles;
+    const int64_t c0 = by * kInChannels;
     const int tl = tid % kInTiles, cl = tid / kInTiles;
     const int64_t tile = t0 + tl, c = c0 + cl;
     float x[A][A] = {};
@@ -452,6 +462,60 @@ __global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64
         if (t0 + t >= a.tiles) continue;
         *reinterpret_cast<float4 *>(v + (xi * a.tiles + t0 + t) * kp + c0 + k) =
             *reinterpret_cast<const float4 *>(&stage[xi][t][k]);
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
+                                                           float *__restrict__ v, const int32_t *__restrict__ amax,
+                                                           float *__restrict__ f, int32_t *__restrict__ shift) {
+    __shared__ __attribute__((aligned(16))) char lds[kInputLds<M>];
+    if (f != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+        // With the weights kept: E, the greatest e_c; each channel's scale of
+        // the weights 2^(e_c - E) (zero past IC), and each output channel's
+        // shift E - a_o.
+        float *scratch = reinterpret_cast<float *>(lds);
+        int emax = kZeroChannel;
+        for (int64_t c = threadIdx.x; c < a.ic; c += 256) emax = max(emax, e[c]);
+        const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
+        for (int64_t c = threadIdx.x; c < kp; c += 256) f[c] = c < a.ic ? ldexpf(1.0f, e[c] - E) : 0.0f;
+        for (int64_t o = threadIdx.x; o < a.oc; o += 256) shift[o] = E - amax[o];
+        __syncthreads();
+    }
+    inputs_split_block<M>(a, kp, e, v, blockIdx.x, blockIdx.y, lds);
+}
+
+// The weights' and the inputs' transforms of a call without kept weights in
+// one launch, wblocks of the weights' (wgx of them along OC) and the rest the
+// inputs' (igx along the tiles): neither waits for the other, and the
+// VALU-heavy weights share the chip with the memory-heavy inputs.
+template <int M>
+constexpr int kTransformLds = kWeightLds<M> > kInputLds<M> ? kWeightLds<M> : kInputLds<M>;
+
+template <int M>
+__global__ __launch_bounds__(256) void transforms_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
+                                                         const int32_t *__restrict__ amax, _Float16 *__restrict__ u,
+                                                         int32_t *__restrict__ shift, float *__restrict__ v,
+                                                         int64_t wgx, int64_t wblocks, int64_t igx) {
+    __shared__ __attribute__((aligned(16))) char lds[kTransformLds<M>];
+    // The two kinds alternate while both last, so that every CU gets some of
+    // each; the rest of the longer kind follows.
+    const int64_t b = blockIdx.x;
+    const int64_t iblocks = gridDim.x - wblocks;
+    const int64_t both = wblocks < iblocks ? wblocks : iblocks;
+    bool weights;
+    int64_t q;
+    if (b < 2 * both) {
+        weights = (b & 1) == 0;
+        q = b >> 1;
+    } else {
+        weights = wblocks > iblocks;
+        q = b - both;
+    }
+    if (weights) {
+        weights_split_block<M>(a.w, a.oc, a.ic, kp, e, amax, u, shift, q % wgx, q / wgx, lds);
+    } else {
+        inputs_split_block<M>(a, kp, e, v, q % igx, q / igx, lds);
     }
 }
 
@@ -1118,9 +1182,9 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     float *u = reinterpret_cast<float *>(base + l.u);
     float *v = reinterpret_cast<float *>(base + l.v);
     float *m = reinterpret_cast<float *>(base + l.m);
-    const std::string names[] = {std::string(tag) + ".scales", std::string(tag) + ".weights",
-                                 std::string(tag) + ".inputs", std::string(tag) + ".products",
-                                 std::string(tag) + ".outputs"};
+    const std::string names[] = {std::string(tag) + ".scales",   std::string(tag) + ".weights",
+                                 std::string(tag) + ".inputs",   std::string(tag) + ".products",
+                                 std::string(tag) + ".outputs",  std::string(tag) + ".transforms"};
     if (tuning().winograd_fp32) {
         const int64_t n_in = a.tiles * a.ic;
         {
@@ -1199,11 +1263,12 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
     if (kept == nullptr) {
-        KernelScope scope(names[1].c_str(), stream);
-        hipLaunchKernelGGL((weights_split_kernel<M>),
-                           dim3(static_cast<uint32_t>(ceil_div(a.oc, kWeightOc)),
-                                static_cast<uint32_t>(ceil_div(l.kp, kWeightIc))),
-                           dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, e, a_oc, uh, shift);
+        // Both transforms in one launch.
+        KernelScope scope(names[5].c_str(), stream);
+        const int64_t wgx = ceil_div(a.oc, kWeightOc), wblocks = wgx * ceil_div(l.kp, kWeightIc);
+        const int64_t igx = ceil_div(a.tiles, kInTiles), iblocks = igx * (l.kp / kInChannels);
+        hipLaunchKernelGGL((transforms_kernel<M>), dim3(static_cast<uint32_t>(wblocks + iblocks)), dim3(256), 0,
+                           stream, a, l.kp, e, a_oc, uh, shift, v, wgx, wblocks, igx);
     } else if (!ready) {
         KernelScope scope(names[1].c_str(), stream);
         hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256))),
@@ -1212,7 +1277,7 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         if (err != hipSuccess) return launched(err, "winograd weights");
         store_publish(kept);
     }
-    {
+    if (kept != nullptr) {
         KernelScope scope(names[2].c_str(), stream);
         hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
                            stream, a, l.kp, e, v, a_kept, f, shift);
