@@ -24,8 +24,9 @@
 //   MUL_MAT:     A = x (tokens, split), B = W (features): C[token][feature]
 //   convolution: A = W (output channels), B = the image's columns (split),
 //                C[channel][position]
-//   Winograd:    A = U[xi] (output channels; single precision, each
-//                column scaled and split here), B = V[xi] (tiles, split here)
+//   Winograd:    A = U[xi] (output channels; two FP16 planes, or single
+//                precision with each column scaled and split here), B = V[xi]
+//                (tiles; two FP16 planes, split by the inputs' transform)
 // so that the output's contiguous dimension is always C's column, lane % 32
 // of the MFMA's result, and a wave's stores are 128-byte rows.
 
@@ -197,20 +198,26 @@ struct ScaledF32Rows {
 
 // K-contiguous 16-bit rows into LDS, PLANES of them at once (one, or the two
 // parts hi and lo of a split operand, `ld_plane` elements apart); `row_of(r)`
-// gives the global row of LDS row r, or -1.  FULL as for F32Rows.
-template <int BR, bool VEC, bool FULL, int PLANES = 1>
+// gives the global row of LDS row r, or -1.  FULL as for F32Rows.  BLOCKED
+// (with FULL): the rows held in blocks of one K-step, [k / 32][row][k % 32],
+// `ld` then 32 and `step` elements from one block to the next, so that a
+// step's rows are whole cache lines in a row.
+template <int BR, bool VEC, bool FULL, int PLANES = 1, bool BLOCKED = false>
 struct F16Rows {
     static constexpr int kOcts = BR * kBK / 8 / 256;  // 8 halves per load
     static_assert(kOcts >= 1, "tile too small for 256 threads");
     static_assert(!FULL || VEC, "FULL loads are vector loads");
+    static_assert(!BLOCKED || FULL, "BLOCKED rows are FULL ones");
     half8 v[PLANES][kOcts];
     const _Float16 *row[kOcts];
-    int64_t K, plane;
+    int64_t K, plane, step;
 
     template <class RowOf>
-    __device__ void init(const _Float16 *base, int64_t ld, RowOf row_of, int64_t k_, int tid, int64_t ld_plane = 0) {
+    __device__ void init(const _Float16 *base, int64_t ld, RowOf row_of, int64_t k_, int tid, int64_t ld_plane = 0,
+                         int64_t step_ = 0) {
         K = k_;
         plane = ld_plane;
+        step = step_;
 #pragma unroll
         for (int i = 0; i < kOcts; ++i) {
             const int idx = tid + 256 * i;
@@ -226,7 +233,8 @@ struct F16Rows {
 #pragma unroll
             for (int q = 0; q < PLANES; ++q) {
                 if (FULL) {
-                    v[q][i] = *reinterpret_cast<const half8 *>(row[i] + q * plane + k0);
+                    const int64_t off = BLOCKED ? (k0 / kBK) * step : k0;
+                    v[q][i] = *reinterpret_cast<const half8 *>(row[i] + q * plane + off);
                     continue;
                 }
                 const int64_t k = k0 + ((tid + 256 * i) % (kBK / 8)) * 8;
@@ -852,9 +860,10 @@ __global__ __launch_bounds__(256) void conv_sum_kernel(ConvArgs c, const float *
 // ------------------------------------------------------------------ Winograd's products
 
 // C[b][m][n] = sum_k A[b][m][k] B[b][n][k] for the batches b: A already split
-// into two FP16 planes, or (SCALED) single precision with its columns scaled
-// and split on its way into LDS, B single precision split on its way into
-// LDS, both K-contiguous rows; three MFMAs a product.
+// into two FP16 planes held in blocks of 32 of K, [k / 32][m][k % 32], or
+// (SCALED) single precision K-contiguous rows with their columns scaled and
+// split on their way into LDS; B already split into two FP16 planes in
+// blocks, [k / 32][n][k % 32]; three MFMAs a product.
 template <int TM, int TN, bool FULL, int NS, bool SCALED = false>
 __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) {
     constexpr int BM = 64 * TM;
@@ -875,7 +884,7 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
     const int64_t nb = rem - mb * p.n_blocks;
     const int64_t m0 = mb * BM, n0 = nb * BN;
     const _Float16 *A = p.a + batch * p.a_batch;
-    const float *B = p.b + batch * p.b_batch;
+    const _Float16 *B = p.b + batch * p.b_batch;
     float *C = p.c + batch * p.c_batch;
 
     float16v acc[TM][TN];
@@ -884,9 +893,9 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    using LA = std::conditional_t<SCALED, ScaledF32Rows<BM, FULL>, F16Rows<BM, true, FULL, 2>>;
+    using LA = std::conditional_t<SCALED, ScaledF32Rows<BM, FULL>, F16Rows<BM, true, FULL, 2, true>>;
     LA la[NS];
-    F32Rows<BN, true, FULL> lb[NS];
+    F16Rows<BN, true, FULL, 2, true> lb[NS];
     const auto a_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : -1; };
     const auto b_row = [&](int r) -> int64_t { return n0 + r < p.N ? n0 + r : -1; };
 #pragma unroll
@@ -894,9 +903,9 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
         if constexpr (SCALED) {
             la[s].init(p.a32 + batch * p.a_batch, p.K, a_row, p.K, tid, p.a_scale);
         } else {
-            la[s].init(A, p.K, a_row, p.K, tid, p.a_plane);
+            la[s].init(A, kBK, a_row, p.K, tid, p.a_plane, p.M * kBK);
         }
-        lb[s].init(B, p.K, b_row, p.K, tid);
+        lb[s].init(B, kBK, b_row, p.K, tid, p.b_plane, p.N * kBK);
     }
     main_loop<TM, TN, kSplitBoth, NS>(acc, la, lb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
 
@@ -1164,7 +1173,7 @@ hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStrea
                                                   (reinterpret_cast<uintptr_t>(p.a_scale) % 16) == 0
                                             : (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && p.a_plane % 8 == 0;
     const bool aligned = a_aligned && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 && p.a_batch % 8 == 0 &&
-                         p.b_batch % 4 == 0;
+                         p.b_batch % 8 == 0 && p.b_plane % 8 == 0;
     if (p.K % kBK != 0 || !aligned) return hipErrorInvalidValue;
     // Both operands split, two planes each: 80 KB of LDS at 128 x 128.
     return pick_tiles(p.M, p.N, p.batches, g.tiles, [&](auto tm, auto tn) {

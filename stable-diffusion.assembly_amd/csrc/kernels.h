@@ -77,17 +77,19 @@ size_t conv_columns_work_size(const ConvArgs &c);
 hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipStream_t stream);
 
 // Batched products c[b][m][n] = sum_k a[b][m][k] b[b][n][k]: a already split
-// into two FP16 planes (hi, and lo `a_plane` elements after it), or single
-// precision with a scale per column (a32, a_scale), b single precision, both
-// K-contiguous rows of K elements; c's rows N apart.  Strides between batches
-// in elements.  The caller pads: K a multiple of 32, a (or a32, a_scale) and
-// b 16-byte aligned, a_batch and a_plane multiples of 8, b_batch of 4;
-// hipErrorInvalidValue otherwise.
+// into two FP16 planes (hi, and lo `a_plane` elements after it), each in
+// blocks of 32 of K, [k / 32][m][k % 32], or single precision with a scale
+// per column (a32, a_scale), K-contiguous rows of K elements; b already split
+// into two FP16 planes (b_plane apart) in blocks, [k / 32][n][k % 32]; c's
+// rows N apart.  Strides between batches in elements.  The caller pads: K a
+// multiple of 32, a (or a32, a_scale) and b 16-byte aligned, a_batch,
+// a_plane, b_batch and b_plane multiples of 8; hipErrorInvalidValue
+// otherwise.
 struct SplitBatchedArgs {
     const _Float16 *a;
-    const float *b;
+    const _Float16 *b;  // B already split: hi, and lo `b_plane` elements after it
     float *c;
-    int64_t a_batch, a_plane, b_batch, c_batch;
+    int64_t a_batch, a_plane, b_batch, b_plane, c_batch;
     int64_t M, N, K, batches;
     int64_t m_blocks, n_blocks;
     // Instead of a: A in single precision (a32, batches a_batch apart), each

@@ -14,17 +14,18 @@
 //      below 2^(17 - a_o);
 //   1. the weights at every call, U[xi][oc][ic] = (G g G^T)[xi] * 2^(a_o +
 //      e_c - E), E the greatest e_c, as two FP16 parts (device.h, split2), hi
-//      and lo, each a plane of its own, [xi][part][oc][kp], IC padded with
-//      zeros to kp, a multiple of 32; or, where the device store keeps them
+//      and lo, each a plane of its own, [xi][part][kp / 32][oc][32], IC
+//      padded with zeros to kp, a multiple of 32; or, where the device store keeps them
 //      (as the reference's store keeps its transformed weights when its
 //      budget allows, winograd.cc:2147-2149, store.h:26-34), U * 2^a_o in
 //      single precision, [xi][oc][kp], with a_o, made by the first call;
-//   2. the inputs, V[xi][tile][ic] = (B^T d B)[xi] * 2^-e_c, single
-//      precision, [xi][tile][kp]; with kept weights its first block also finds
-//      E, each channel's factor 2^(e_c - E) and each output's shift E - a_o;
-//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: V (and kept U, its column
-//      c times 2^(e_c - E)) split into two FP16 parts on their way into LDS,
-//      three MFMAs a product (gemm.hip), so that the sums are those of 22-bit
+//   2. the inputs, V[xi][tile][ic] = (B^T d B)[xi] * 2^-e_c, split into two
+//      FP16 parts, [xi][part][kp / 32][tile][32]; with kept weights its first
+//      block also finds E, each channel's factor 2^(e_c - E) and each
+//      output's shift E - a_o (without, 1. and 2. are one launch);
+//   3. the alpha^2 products M[xi] = U[xi] V[xi]^T: kept U (its column c times
+//      2^(e_c - E)) split into two FP16 parts on its way into LDS, three
+//      MFMAs a product (gemm.hip), so that the sums are those of 22-bit
 //      operands where FP16 would hold 11 -- the scales keep every part inside
 //      FP16's range: |U| 2^(a_o + e_c - E) and |V| 2^-e_c below 2^17;
 //   4. the outputs, A^T M A * 2^(E - a_o), with the sum begun from the
@@ -264,8 +265,8 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
 // E, the greatest e_c (each block reduces e itself), and shift[o] = E - a_o
 // for the outputs (blocks of the first channels); U * 2^(a_o + e_c - E) split
 // into its two FP16 parts, staged in LDS as [xi][part][o][channel] and
-// written out as rows of 64 channels, u[xi][part][oc][kp], zeros from IC to
-// kp.
+// written out in blocks of 32 channels, u[xi][part][kp / 32][oc][32], zeros
+// from IC to kp.
 constexpr int kWeightOc = 4, kWeightIc = 64;
 
 // LDS of a block of weights_split: the 4 floats of the reduction, then the
@@ -326,7 +327,8 @@ __device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__
         const int k = (q - row * per_row) * 8;
         const int r = row / kWeightOc, oo = row % kWeightOc;
         if (o0 + oo >= oc) continue;
-        *reinterpret_cast<half8 *>(u + (r * oc + o0 + oo) * kp + c0 + k) =
+        const int64_t c = c0 + k;
+        *reinterpret_cast<half8 *>(u + r * oc * kp + (c >> 5) * oc * 32 + (o0 + oo) * 32 + (c & 31)) =
             *reinterpret_cast<const half8 *>(&stage[r][oo][k]);
     }
 }
@@ -415,26 +417,28 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
             v[r][s] = dot_n<A>([&](int j) { return Mat<M>::bt(s, j); }, [&](int j) { return bd[r][j]; });
 }
 
-// V[xi][tile][ic] * 2^-e_c in single precision, v[xi][tile][kp], zeros for
-// the channels from IC to kp.  A block takes 8 consecutive tiles by 32
-// channels, one (tile, channel) a thread, consecutive threads consecutive
+// V[xi][tile][ic] * 2^-e_c split into two FP16 parts, in blocks of 32
+// channels, v[xi][part][c / 32][tile][c % 32], zeros for the channels from IC
+// to kp.  A block takes 8 consecutive tiles by
+// 32 channels, one (tile, channel) a thread, consecutive threads consecutive
 // tiles (so that the reads of a channel are rows of the image); the results
-// are staged in LDS as [xi][tile][channel] and written out as rows of 32
-// channels.
+// are staged in LDS as [xi][part][tile][channel] and written out as rows of
+// 32 channels.
 constexpr int kInTiles = 8, kInChannels = 32;
 
-// LDS of a block of inputs_split: the staged V, rows of a tile 40 floats
-// apart (16-byte aligned, and the 64 lanes of a wave -- 8 tiles by 8
-// channels -- in at most two to a bank).
+// LDS of a block of inputs_split: the staged parts of V, [xi][part][tile]
+// [channel], rows of a tile 40 halves apart (16-byte aligned).
 template <int M>
-constexpr int kInputLds = Mat<M>::A * Mat<M>::A * kInTiles * (kInChannels + 8) * 4;
+constexpr int kInputLds = 2 * Mat<M>::A * Mat<M>::A * kInTiles * (kInChannels + 8) * 2;
 
-// Block (bx, by) of inputs_split, its LDS at `lds`.
+// Block (bx, by) of inputs_split, its LDS at `lds`: V * 2^-e_c split into
+// its two FP16 parts (split2, the form the products take), written as
+// v[xi][part][c / 32][tile][c % 32].
 template <int M>
 __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_t kp, const int32_t *__restrict__ e,
-                                                   float *__restrict__ v, int64_t bx, int64_t by, char *lds) {
+                                                   _Float16 *__restrict__ v, int64_t bx, int64_t by, char *lds) {
     constexpr int A = Mat<M>::A;
-    auto stage = reinterpret_cast<float(*)[kInTiles][kInChannels + 8]>(lds);
+    auto stage = reinterpret_cast<_Float16(*)[kInTiles][kInChannels + 8]>(lds);
     const int tid = threadIdx.x;
     const int64_t t0 = bx * kInTiles;
     const int64_t c0 = by * kInChannels;
@@ -452,22 +456,27 @@ __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_
 #pragma unroll
     for (int r = 0; r < A; ++r)
 #pragma unroll
-        for (int q = 0; q < A; ++q) stage[r * A + q][tl][cl] = x[r][q];
+        for (int q = 0; q < A; ++q) {
+            _Float16 hi, lo;
+            split2(x[r][q], hi, lo);
+            stage[2 * (r * A + q)][tl][cl] = hi;
+            stage[2 * (r * A + q) + 1][tl][cl] = lo;
+        }
     __syncthreads();
-    // A * A * kInTiles rows of 32 floats, 4 at a time.
-    for (int q = tid; q < A * A * kInTiles * (kInChannels / 4); q += 256) {
-        const int row = q / (kInChannels / 4);
-        const int k = (q % (kInChannels / 4)) * 4;
-        const int xi = row / kInTiles, t = row % kInTiles;
+    // 2 A * A * kInTiles rows of 32 halves, 8 at a time.
+    for (int q = tid; q < 2 * A * A * kInTiles * (kInChannels / 8); q += 256) {
+        const int row = q / (kInChannels / 8);
+        const int k = (q % (kInChannels / 8)) * 8;
+        const int xp = row / kInTiles, t = row % kInTiles;
         if (t0 + t >= a.tiles) continue;
-        *reinterpret_cast<float4 *>(v + (xi * a.tiles + t0 + t) * kp + c0 + k) =
-            *reinterpret_cast<const float4 *>(&stage[xi][t][k]);
+        *reinterpret_cast<half8 *>(v + xp * a.tiles * kp + c0 * a.tiles + (t0 + t) * kInChannels + k) =
+            *reinterpret_cast<const half8 *>(&stage[xp][t][k]);
     }
 }
 
 template <int M>
 __global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
-                                                           float *__restrict__ v, const int32_t *__restrict__ amax,
+                                                           _Float16 *__restrict__ v, const int32_t *__restrict__ amax,
                                                            float *__restrict__ f, int32_t *__restrict__ shift) {
     __shared__ __attribute__((aligned(16))) char lds[kInputLds<M>];
     if (f != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
@@ -495,7 +504,7 @@ constexpr int kTransformLds = kWeightLds<M> > kInputLds<M> ? kWeightLds<M> : kIn
 template <int M>
 __global__ __launch_bounds__(256) void transforms_kernel(WinogradArgs a, int64_t kp, const int32_t *__restrict__ e,
                                                          const int32_t *__restrict__ amax, _Float16 *__restrict__ u,
-                                                         int32_t *__restrict__ shift, float *__restrict__ v,
+                                                         int32_t *__restrict__ shift, _Float16 *__restrict__ v,
                                                          int64_t wgx, int64_t wblocks, int64_t igx) {
     __shared__ __attribute__((aligned(16))) char lds[kTransformLds<M>];
     // The two kinds alternate while both last, so that every CU gets some of
@@ -1155,10 +1164,10 @@ WorkLayout work_layout(const WinogradArgs &a) {
         l.total = at;
         return l;
     }
-    // Either form: U as two FP16 planes [xi][part][oc][kp] or in single
-    // precision [xi][oc][ic] (kept weights live in the store instead); V in
-    // single precision, [xi][tile][kp] or [xi][ic][tile]; the factors f of
-    // kept weights' columns.
+    // Either form: U as two FP16 planes [xi][part][kp / 32][oc][32] or in single
+    // precision [xi][oc][ic] (kept weights live in the store instead); V as
+    // two FP16 planes [xi][part][kp / 32][tile][32], or in single precision
+    // [xi][ic][tile]; the factors f of kept weights' columns.
     l.e = take(a.ic * 4);
     l.a = take(a.oc * 4);
     l.shift = take(a.oc * 4);
@@ -1262,13 +1271,14 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
                            a_kept);
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
+    _Float16 *vh = reinterpret_cast<_Float16 *>(v);
     if (kept == nullptr) {
         // Both transforms in one launch.
         KernelScope scope(names[5].c_str(), stream);
         const int64_t wgx = ceil_div(a.oc, kWeightOc), wblocks = wgx * ceil_div(l.kp, kWeightIc);
         const int64_t igx = ceil_div(a.tiles, kInTiles), iblocks = igx * (l.kp / kInChannels);
         hipLaunchKernelGGL((transforms_kernel<M>), dim3(static_cast<uint32_t>(wblocks + iblocks)), dim3(256), 0,
-                           stream, a, l.kp, e, a_oc, uh, shift, v, wgx, wblocks, igx);
+                           stream, a, l.kp, e, a_oc, uh, shift, vh, wgx, wblocks, igx);
     } else if (!ready) {
         KernelScope scope(names[1].c_str(), stream);
         hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256))),
@@ -1280,7 +1290,7 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     if (kept != nullptr) {
         KernelScope scope(names[2].c_str(), stream);
         hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
-                           stream, a, l.kp, e, v, a_kept, f, shift);
+                           stream, a, l.kp, e, vh, a_kept, f, shift);
     }
     {
         KernelScope scope(names[3].c_str(), stream);
@@ -1294,8 +1304,9 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
             p.a_plane = a.oc * l.kp;
             p.a_batch = 2 * p.a_plane;
         }
-        p.b = v;
-        p.b_batch = a.tiles * l.kp;
+        p.b = vh;
+        p.b_plane = a.tiles * l.kp;
+        p.b_batch = 2 * p.b_plane;
         p.c = m;
         p.c_batch = a.oc * a.tiles;
         p.M = a.oc;
