@@ -48,6 +48,7 @@ def parse():
                                                   "cfg3b cfg4_self cfg4_cross cfg5 unet unet_kept copy), for a "
                                                   "profiler")
     p.add_argument("--no-unet", action="store_true", help="leave out the UNet step")
+    p.add_argument("--no-vae", action="store_true", help="leave out the VAE decoder's operations")
     return p.parse_args()
 
 
@@ -354,6 +355,31 @@ def cpu_baseline(seconds):
                       f"best of {runs - 1} runs after one uncounted, {cores} OpenMP threads"}
 
 
+# The VAE decoder's operations of the reference's bench (tools/bench.cc:146-153):
+# 3x3 convolutions (w, h, ic, oc) at batch 1 with their bias, and the
+# attention of its middle block (one head of 512 over 4096 positions).
+VAE_CONVS = [(64, 64, 512, 512), (128, 128, 512, 512), (256, 256, 256, 256), (256, 256, 512, 512),
+             (512, 512, 128, 128), (512, 512, 256, 256)]
+
+
+def vae_decoder_line(dev, args):
+    """Each of the VAE decoder's operations timed alone (synthetic inputs of
+    their shapes, weights ~N(0,0.02))."""
+    out = {}
+    steps, warmup = max(3, args.steps // 10), max(1, args.warmup // 5)
+    for (w, h, ic, oc) in VAE_CONVS:
+        run, flops, path = conv_workload(dev, 1, ic, h, w, oc, 3, 1, bias=True, residual=False, seed=w + ic)
+        ms = timed(run, steps, warmup)
+        out[f"conv {w}x{h} {ic}->{oc}"] = {"ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2), "path": path}
+        log(f"vae conv {w}x{h} {ic}->{oc}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s (path {path})")
+        del run
+    run, flops = attention_workload(dev, 1, 1, 4096, 4096, 512, seed=3)
+    ms = timed(run, steps, warmup)
+    out["attention 1x4096x4096x512"] = {"ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2)}
+    log(f"vae attention d=512: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s")
+    return out
+
+
 def unet_step_line(dev, args):
     """The SD1.5 UNet step in ms: the graph replayed `steps` times after
     `warmup`; the eager step (the same launches from Python) beside it, and
@@ -507,6 +533,8 @@ def main():
     }
     if not args.no_unet:
         line["unet_step"] = unet_step_line(dev, args)
+    if not args.no_vae:
+        line["vae_decoder"] = vae_decoder_line(dev, args)
     if not args.no_cpu:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -24,8 +24,9 @@ struct AttentionArgs {
     int64_t qblocks;
 };
 
-// The most dimensions of a head the kernel takes (queries, keys and values).
-constexpr int64_t kAttentionMaxDims = 256;
+// The most dimensions of a head the kernels take (queries, keys and values):
+// up to 256 in one pass, wider heads (the VAE's 512) by chunks of 128.
+constexpr int64_t kAttentionMaxDims = 512;
 
 // The bits mode of self-attention (qattention.hip): the operands, the
 // quantization (levels, wmax, group), the stretch of keys of the

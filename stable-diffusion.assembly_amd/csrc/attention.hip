@@ -167,6 +167,235 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
         }
 }
 
+// ------------------------------------------------------------------ wide heads
+//
+// Heads of more than 256 dimensions (the VAE's, 512): the generic form's
+// products, softmax and sums, with the queries and keys staged 128 dimensions
+// at a time -- the scores of a block of 32 keys summed over the chunks -- so
+// that LDS holds 64 queries and 32 keys of one chunk and the block's values
+// of NDV tiles of 16 dimensions (dv <= 16 NDV).
+constexpr int kWideChunk = 128;
+constexpr int kWideLd = kWideChunk + 1;
+
+// Whether the wide form takes the head: more than 256 dimensions of the
+// queries and keys or of the values.
+inline bool wide_form(const AttentionArgs &a) { return a.d > 256 || a.dv > 256; }
+
+// The splits of the keys: enough for about 512 blocks with the query blocks
+// of 64, of 256 keys or more each (a multiple of 32).
+struct WideSplits {
+    int64_t splits, key_len;
+};
+
+inline WideSplits wide_splits(const AttentionArgs &a) {
+    const int64_t blocks = ceil_div(a.lq, kQueries) * a.h * a.b;
+    int64_t sp = ceil_div(512, blocks);
+    const int64_t most = a.lk / 256 > 1 ? a.lk / 256 : 1;
+    sp = sp < most ? sp : most;
+    WideSplits w;
+    w.key_len = round_up(ceil_div(a.lk, sp), kKeys);
+    w.splits = ceil_div(a.lk, w.key_len);
+    return w;
+}
+
+// With `part`, a block takes the keys of one split of key_len (a multiple
+// of 32) and writes its queries' running maximum, sum and unnormalised output
+// there (WidePartial) for attention_combine_kernel.
+struct WidePartial {
+    float *m;    // [b h][split][lq]
+    double *l;   // [b h][split][lq]
+    float *o;    // [b h][split][lq][dv]
+};
+
+__host__ __device__ inline WidePartial wide_partial(void *work, const AttentionArgs &a, int64_t splits) {
+    const int64_t n = a.b * a.h * splits * a.lq;
+    char *p = static_cast<char *>(work);
+    WidePartial w;
+    w.l = reinterpret_cast<double *>(p);
+    w.m = reinterpret_cast<float *>(p + n * 8);
+    w.o = reinterpret_cast<float *>(p + n * 12);
+    return w;
+}
+
+template <int NDV, bool KHALF, bool VHALF>
+__global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, int64_t splits, int64_t key_len,
+                                                             WidePartial part) {
+    extern __shared__ float lds[];
+    float *qs = lds;                       // [64][kWideLd]
+    float *ks = qs + kQueries * kWideLd;   // [32][kWideLd]
+    float *vs = ks + kKeys * kWideLd;      // [32][ldv]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+
+    // Neighbouring blocks share a split's keys and values.
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t qb = b % static_cast<uint32_t>(a.qblocks);
+    const uint32_t rest = b / static_cast<uint32_t>(a.qblocks);
+    const int64_t sp = rest % splits;
+    const uint32_t bh = static_cast<uint32_t>(rest / splits);
+    const int64_t k_begin = sp * key_len;
+    const int64_t k_end = k_begin + key_len < a.lk ? k_begin + key_len : a.lk;
+    const int64_t hi = bh % a.h;
+    const int64_t bi = bh / a.h;
+    const int64_t kh = hi / (a.h / a.hk);
+    const int64_t q0 = static_cast<int64_t>(qb) * kQueries;
+    const int64_t qbase = bi * a.qnb3 + hi * a.qnb2;
+    const int64_t kbase = bi * a.knb3 + kh * a.knb2;
+    const int64_t vbase = bi * a.vnb3 + kh * a.vnb2;
+
+    float4v o[NDV];
+#pragma unroll
+    for (int t = 0; t < NDV; ++t) o[t] = float4v{};
+    float m = -INFINITY;
+    double l = 0.0;
+    const float *qw = qs + (wave * 16 + lr) * kWideLd + lg;
+
+    for (int64_t k0 = k_begin; k0 < k_end; k0 += kKeys) {
+        // S^T = K Q^T for two tiles of 16 keys, over the chunks of the
+        // dimensions: the lane's scores of its query lr, keys 16 t + 4 lg + r.
+        float4v s[2] = {float4v{}, float4v{}};
+        for (int e0 = 0; e0 < a.dp; e0 += kWideChunk) {
+            const int dc = a.dp - e0 < kWideChunk ? static_cast<int>(a.dp - e0) : kWideChunk;
+            __syncthreads();  // the last chunk's queries and keys are read
+            for (int idx = tid; idx < kQueries * dc; idx += 256) {
+                const int qi = idx / dc, e = idx - qi * dc;
+                const int64_t i = q0 + qi;
+                float x = 0.0f;
+                if (e0 + e < a.d && i < a.lq) x = a.q[qbase + i * a.qnb1 + e0 + e];
+                qs[qi * kWideLd + e] = x;
+            }
+            for (int idx = tid; idx < kKeys * dc; idx += 256) {
+                const int j = idx / dc, e = idx - j * dc;
+                const int64_t key = k0 + j;
+                ks[j * kWideLd + e] =
+                    (e0 + e < a.d && key < k_end) ? load_kv<KHALF>(a.k, kbase + key * a.knb1 + e0 + e) : 0.0f;
+            }
+            __syncthreads();
+            for (int e = 0; e < dc; e += 4) {
+                const float qv = qw[e];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const float kv = ks[(16 * t + lr) * kWideLd + e + lg];
+                    s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv, qv, s[t], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();  // the last block's values are read
+        for (int idx = tid; idx < kKeys * 16 * NDV; idx += 256) {
+            const int j = idx / (16 * NDV), e = idx - j * (16 * NDV);
+            const int64_t key = k0 + j;
+            vs[j * a.ldv + e] = (e < a.dv && key < k_end) ? load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e) : 0.0f;
+        }
+        __syncthreads();
+
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t key = k0 + 16 * t + 4 * lg + r;
+                const float x = key < k_end ? s[t][r] * a.scale : -INFINITY;
+                s[t][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float alpha = m == -INFINITY ? 0.0f : cephes_exp(m - mnew);
+        m = mnew;
+        double part = 0.0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = s[t][r] == -INFINITY ? 0.0f : cephes_exp(s[t][r] - mnew);
+                s[t][r] = p;
+                part += static_cast<double>(p);
+            }
+        l = l * static_cast<double>(alpha) + part;
+#pragma unroll
+        for (int t = 0; t < NDV; ++t) o[t] *= alpha;
+
+        // O^T += V^T P^T: k index 4 lg + r of each tile of 16 keys.
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float *vrow = vs + (16 * t + 4 * lg + r) * a.ldv + lr;
+#pragma unroll
+                for (int c = 0; c < NDV; ++c) {
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * c], s[t][r], o[c], 0, 0, 0);
+                }
+            }
+    }
+
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int64_t i = q0 + wave * 16 + lr;
+    if (i >= a.lq) return;
+    if (part.o != nullptr) {
+        const int64_t at = (static_cast<int64_t>(bh) * splits + sp) * a.lq + i;
+        if (lg == 0) {
+            part.m[at] = m;
+            part.l[at] = l;
+        }
+        float *po = part.o + at * a.dv;
+#pragma unroll
+        for (int c = 0; c < NDV; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int e = 16 * c + 4 * lg + r;
+                if (e < a.dv) po[e] = o[c][r];
+            }
+        return;
+    }
+    const float reciprocal = static_cast<float>(1.0 / l);
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
+#pragma unroll
+    for (int c = 0; c < NDV; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = 16 * c + 4 * lg + r;
+            if (e < a.dv) out[e] = o[c][r] * reciprocal;
+        }
+}
+
+// The splits of the keys of a query merged: each split's sum and output
+// rescaled by exp(its maximum - the greatest), as the single pass rescales
+// its running ones, the sum in double, the output times the reciprocal of
+// the sum rounded to single precision.  A wave per query.
+__global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a, int64_t splits, WidePartial part) {
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // (b h) lq + i
+    const int lane = threadIdx.x & 63;
+    if (item >= a.b * a.h * a.lq) return;
+    const int64_t bh = item / a.lq, i = item - bh * a.lq;
+    const int64_t hi = bh % a.h, bi = bh / a.h;
+    const int64_t first = bh * splits * a.lq + i;  // split 0 of the query
+    float mx = -INFINITY;
+    for (int64_t sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part.m[first + sp * a.lq]);
+    double l = 0.0;
+    for (int64_t sp = 0; sp < splits; ++sp) {
+        const float ms = part.m[first + sp * a.lq];
+        const float w = ms == -INFINITY ? 0.0f : cephes_exp(ms - mx);
+        l += part.l[first + sp * a.lq] * static_cast<double>(w);
+    }
+    const float reciprocal = static_cast<float>(1.0 / l);
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
+    for (int64_t e = lane; e < a.dv; e += 64) {
+        float acc = 0.0f;
+        for (int64_t sp = 0; sp < splits; ++sp) {
+            const float ms = part.m[first + sp * a.lq];
+            const float w = ms == -INFINITY ? 0.0f : cephes_exp(ms - mx);
+            acc = fmaf(part.o[(first + sp * a.lq) * a.dv + e], w, acc);
+        }
+        out[e] = acc * reciprocal;
+    }
+}
+
 // ------------------------------------------------------------------ the fast form
 //
 // Single-precision keys and values, heads of D = d = dv dimensions (a multiple
@@ -918,6 +1147,36 @@ hipError_t launch_fast_form(AttentionArgs a, hipStream_t stream) {
 }
 
 template <int NDV>
+hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
+    a.ldv = 16 * NDV + 4;
+    const WideSplits w = wide_splits(a);
+    const WidePartial part = w.splits > 1 ? wide_partial(work, a, w.splits) : WidePartial{nullptr, nullptr, nullptr};
+    const size_t lds = sizeof(float) * (kQueries * kWideLd + kKeys * kWideLd + kKeys * a.ldv);
+    dim3 grid(static_cast<uint32_t>(a.qblocks * w.splits * a.h * a.b)), block(256);
+    const auto launch = [&](auto kernel) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, a, w.splits, w.key_len, part);
+        return hipGetLastError();
+    };
+    hipError_t e;
+    if (a.khalf && a.vhalf) {
+        e = launch(attention_wide_kernel<NDV, true, true>);
+    } else if (a.khalf) {
+        e = launch(attention_wide_kernel<NDV, true, false>);
+    } else if (a.vhalf) {
+        e = launch(attention_wide_kernel<NDV, false, true>);
+    } else {
+        e = launch(attention_wide_kernel<NDV, false, false>);
+    }
+    if (e != hipSuccess || w.splits == 1) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lq, 4))),
+                       dim3(256), 0, stream, a, w.splits, part);
+    return hipGetLastError();
+}
+
+template <int NDV>
 hipError_t launch_ndv(AttentionArgs a, hipStream_t stream) {
     a.ldv = 16 * NDV + 4;
     const size_t lds = sizeof(float) * (kQueries * a.ldq + kKeys * a.ldk + kKeys * a.ldv);
@@ -943,7 +1202,12 @@ size_t attention_lds_bytes(int64_t d, int64_t dv) {
 
 size_t attention_work_bytes(const AttentionArgs &a) {
     if (a.lq == 0 || a.h == 0 || a.b == 0 || a.lk == 0) return 0;
-    return split_form(a) ? split_form_work(a) : 0;
+    if (split_form(a)) return split_form_work(a);
+    if (wide_form(a)) {
+        const WideSplits w = wide_splits(a);
+        return w.splits > 1 ? static_cast<size_t>(a.b * a.h * w.splits * a.lq * (12 + 4 * a.dv)) : 0;
+    }
+    return 0;
 }
 
 hipError_t launch_attention(AttentionArgs a, void *work, hipStream_t stream) {
@@ -956,6 +1220,11 @@ hipError_t launch_attention(AttentionArgs a, void *work, hipStream_t stream) {
     const int ndv = static_cast<int>(ceil_div(a.dv, 16));
     a.qblocks = ceil_div(a.lq, kQueries);
     KernelScope scope("attention", stream);
+    if (wide_form(a)) {
+        if (ndv <= 16) return launch_wide<16>(a, work, stream);
+        if (ndv <= 24) return launch_wide<24>(a, work, stream);
+        return launch_wide<32>(a, work, stream);
+    }
     switch (ndv) {
     case 1: return launch_ndv<1>(a, stream);
     case 2: return launch_ndv<2>(a, stream);

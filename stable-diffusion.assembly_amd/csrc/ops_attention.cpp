@@ -136,6 +136,9 @@ sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const
     }
     if (quantized_attention(k)) {
         QAttentionArgs qa = qargs_of(q, k, v, y, scale);
+        if (q->ne[0] > 256 || v->ne[0] > 256) {
+            return fail(SDHIP_UNSUPPORTED, "attention: quantized heads of more than 256 dimensions are not taken");
+        }
         if (qa.group % 16 != 0 || qa.group > 256) {
             return fail(SDHIP_UNSUPPORTED, "attention: quantized groups of %lld keys (a multiple of 16 up to 256 "
                                            "is taken)", static_cast<long long>(qa.group));

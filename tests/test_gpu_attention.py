@@ -27,6 +27,11 @@ CASES = [
     (128, 70, 300, 2, 2, 1, False),
     (64, 257, 1000, 4, 2, 1, False),   # heads sharing keys in the fast form
     (40, 1, 1, 1, 1, 1, False),        # one query, one key
+    (512, 100, 70, 1, 1, 1, False),    # the VAE's heads of 512, by chunks of the dimensions
+    (384, 65, 130, 2, 1, 2, True),     # wide heads sharing keys, FP16 keys and values
+    (300, 33, 47, 2, 2, 1, False),     # wide heads of no multiple of the chunk or of 16
+    (320, 64, 1000, 1, 1, 1, False),   # wide heads, the keys in three splits (the last ragged) merged
+    (288, 40, 700, 2, 1, 1, True),     # two splits, heads sharing FP16 keys and values
 ]
 
 
@@ -65,6 +70,22 @@ def test_attention(gpu, c):
 
 
 @pytest.mark.gpu
+def test_attention_vae_decoder(gpu):
+    """The VAE decoder's attention (tools/bench.cc:153): one head of 512
+    dimensions over 4096 positions, ~N(0,1); a sample of 200 queries checked
+    against float64."""
+    b, h, lq, d = 1, 1, 4096, 512
+    q, k, v, y, scale = attention_case(gpu, d, lq, lq, h, h, b, False, seed=512, dist="normal")
+    queries = rng(9).choice(b * h * lq, size=200, replace=False)
+    exact, mag = orc.exact_attention(q, k, v, scale, queries=queries)
+    got = y[0, queries % lq, 0, :]
+    err = orc.metric(got, exact, mag)
+    print(f"VAE attention: sampled error {err:.3g}")
+    assert np.isfinite(y).all()
+    assert err <= BOUND
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,lk", [("cfg4 self", 4096), ("cfg4 cross", 77)])
 def test_attention_bench_shapes(gpu, name, lk):
     """cfg4: Q [2, 8, 4096, 40] ~N(0,1) against 4096 or 77 keys; a sample of
@@ -84,9 +105,9 @@ def test_attention_bench_shapes(gpu, name, lk):
 
 @pytest.mark.gpu
 def test_attention_not_taken(gpu):
-    """Heads of 512 (the VAE's) are left to the caller; so is a soft cap."""
-    q = torch.zeros((1, 40, 1, 512), device=gpu)
-    y = torch.zeros((1, 40, 1, 512), device=gpu)
+    """Heads of more than 512 dimensions are left to the caller; so is a soft cap."""
+    q = torch.zeros((1, 40, 1, 640), device=gpu)
+    y = torch.zeros((1, 40, 1, 640), device=gpu)
     with pytest.raises(sdhip.SdhipError) as e:
         sdhip.attention(q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), y, 0.05)
     assert e.value.status == sdhip.UNSUPPORTED

@@ -201,6 +201,7 @@ def sampled(gpu, shape, k, s, p, seed, count=3000, chain=None):
     ("cfg2 F(4x4) 64x64x320", (2, 320, 64, 64), (320, 320, 3, 3), 1, 1, 4),
     ("cfg3a F(2x2) 8x8x1280", (2, 1280, 8, 8), (1280, 1280, 3, 3), 1, 1, 2),
     ("cfg3b 1x1 32x32 640->1280", (2, 640, 32, 32), (1280, 640, 1, 1), 1, 0, 0),
+    ("VAE decoder 128x128 512->512", (1, 512, 128, 128), (512, 512, 3, 3), 1, 1, 4),
 ])
 def test_conv2d_bench_shapes(gpu, name, shape, k, s, p, want):
     err, path = sampled(gpu, shape, k, s, p, seed=len(name))
