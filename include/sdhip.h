@@ -129,7 +129,10 @@ int sdhip_profile_entry(int i, const char **name, double *total_ms, int64_t *lau
 
 /* GGML_OP_MUL_MAT of one weight matrix w (F16/F32, ne = [K, N, 1, 1]) by
  * x (F32 contiguous, ne = [K, M1, M2, M3]) into y (F32 contiguous,
- * ne = [N, M1, M2, M3]): y[n, m] = sum_k w[k, n] x[k, m].
+ * ne = [N, M1, M2, M3]): y[n, m] = sum_k w[k, n] x[k, m].  The work buffer:
+ * in the bits mode the quantized operands; otherwise, for a product of few
+ * output blocks and long K (split along K), the splits' partial sums; 0
+ * else.  A buffer short of sdhip_mul_mat_work_size is SDHIP_ERROR.
  * Replaces mul_mat_supported / mul_mat_work_size / mul_mat_compute
  * (sources/ops.h:40-44; mul_mat.cc:181-194, 205-215, 1175-1196). */
 int sdhip_mul_mat_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y);
@@ -156,7 +159,11 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
  * The library takes it by Winograd F(4x4,3x3) / F(2x2,3x3) where the
  * reference would (winograd_supported, four, small; winograd.cc:194-196,
  * 1204-1206, 2107-2123) and directly otherwise (conv2d_supported,
- * conv2d.cc:320-331).  Replaces conv2d_* and winograd_* of ops.h:26-38. */
+ * conv2d.cc:320-331).  The work buffer: Winograd's exponents, transformed
+ * operands and products; for a direct convolution of a kernel other than
+ * 1x1 with IC KH KW a multiple of 32, its columns and the partial sums of
+ * its splits of K; 0 else.  A buffer short of sdhip_conv2d_work_size is
+ * SDHIP_ERROR.  Replaces conv2d_* and winograd_* of ops.h:26-38. */
 int sdhip_conv2d_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
                            const int32_t op_params[6]);
 /* Which path a supported convolution takes: 0 direct, 2 Winograd F(2x2,3x3),
@@ -175,10 +182,13 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
  * [d, lq, h, b] F32 (any strides, nb[0] = 4), k ne = [d, lk, hk, b] and v ne =
  * [dv, lk, hk, b] F32 or F16, y ne = [dv, h, lq, b] F32 contiguous; head h
  * reads key head h / (h / hk).  scale, max_bias and softcap are op_params[0..2];
- * only max_bias = softcap = 0 is taken.  The work buffer: in the bits mode
- * the quantized operands; otherwise, for single-precision keys and values of
- * the head sizes 32, 40, 64, 80, 96, 128 and 160, the keys and values split
- * into FP16 parts, tile by tile (0 for the other forms).  A buffer short of
+ * only max_bias = softcap = 0 is taken, heads of up to 512 dimensions (256
+ * in the bits mode: wider ones return SDHIP_UNSUPPORTED there).  The work
+ * buffer: in the bits mode the quantized operands; otherwise, for
+ * single-precision keys and values of the head sizes 32, 40, 64, 80, 96, 128
+ * and 160, the keys and values split into FP16 parts, tile by tile; for heads
+ * of more than 256 dimensions whose keys are split across blocks, each
+ * split's maximum, sum and output; 0 for the other forms.  A buffer short of
  * sdhip_attention_work_size is SDHIP_ERROR.  Replaces attention_supported /
  * attention_work_size / attention_compute (ops.h:51-56). */
 int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
