@@ -906,6 +906,7 @@ __global__ __launch_bounds__(256) void inputs_small_kernel(WinogradArgs a, int64
 }
 
 typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 
 template <int M, int NT>
 __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(WinogradArgs a, int64_t kp, int64_t split_len,
@@ -1039,10 +1040,12 @@ __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(Winograd
     int stage = 0;
     for (int64_t c0 = c_begin; c0 < c_end; c0 += 32, stage ^= 1) {
         const int64_t next = c0 + 32 < c_end ? c0 + 32 : c0;  // past the last step: this one again
-        // The step's kernels, exponents and V in (all loaded a step ahead);
-        // every wave past the step before, whose stage the next step's
-        // kernels now overwrite.
-        wait_loads<0>();
+        // The step's kernels in (copied a step ahead: loads complete in the
+        // order they were issued, and the exponents' two and V's 2 NT A
+        // loads of the step went out after them); every wave past the step
+        // before, whose stage the next step's kernels now overwrite.  The
+        // exponents and V are waited for where they are used.
+        wait_loads<2 + 2 * NT * A>();
         __syncthreads();
         int4v q[9];
         const char *gl = gbuf[stage] + (lr * kRowPieces + 9 * kg) * 16;
@@ -1078,14 +1081,22 @@ __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(Winograd
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < A; ++j) {
+            // U split two numbers at a time: the high parts rounded toward
+            // zero (the remainder u - hi then exact in single precision), the
+            // low parts from the remainders; hi + lo keeps 22 bits of u.
             half8 uh, ul;
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const float u =
+            for (int jj = 0; jj < 8; jj += 2) {
+                const float u0 =
                     dot3(Mat<M>::g(j, 0), gi[jj][0], Mat<M>::g(j, 1), gi[jj][1], Mat<M>::g(j, 2), gi[jj][2]);
-                const _Float16 hi = static_cast<_Float16>(u);
-                uh[jj] = hi;
-                ul[jj] = static_cast<_Float16>(fmaf(-1.0f, static_cast<float>(hi), u));
+                const float u1 = dot3(Mat<M>::g(j, 0), gi[jj + 1][0], Mat<M>::g(j, 1), gi[jj + 1][1],
+                                      Mat<M>::g(j, 2), gi[jj + 1][2]);
+                const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(u0, u1);
+                const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(u0 - static_cast<float>(h[0]), u1 - static_cast<float>(h[1]));
+                uh[jj] = h[0];
+                uh[jj + 1] = h[1];
+                ul[jj] = l[0];
+                ul[jj + 1] = l[1];
             }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
