@@ -31,11 +31,14 @@ constexpr int kWave = 64;
 constexpr float kSplitDown = 0.0625f;
 constexpr float kSplitUp = 16.0f;
 
-__device__ __forceinline__ void split2(float x, _Float16 &hi, _Float16 &lo) {
-    const float s = x * kSplitDown;
+// The two parts of s, a number already scaled by 2^-4 (with whatever other
+// power of two a caller folds into the same factor).
+__device__ __forceinline__ void split_scaled(float s, _Float16 &hi, _Float16 &lo) {
     hi = static_cast<_Float16>(s);
     lo = static_cast<_Float16>(s - static_cast<float>(hi));
 }
+
+__device__ __forceinline__ void split2(float x, _Float16 &hi, _Float16 &lo) { split_scaled(x * kSplitDown, hi, lo); }
 
 // ------------------------------------------------------------------ scalar math
 

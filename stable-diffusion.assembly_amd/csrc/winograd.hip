@@ -126,10 +126,11 @@ __device__ __forceinline__ float abs_max4(float4v v) {
 }
 
 // One workgroup per channel: blocks [0, IC) input channel c's greatest |x|
-// over every image, four independent float4 loads in flight per thread where
-// the rows are contiguous, and its exponent e[c] (zero channels: the least,
-// so that they scale to zero); blocks [IC, IC + OC) output channel o's
-// greatest FP16 weight, four loads of eight in flight per thread, and a[o].
+// over every image, eight independent float4 loads in flight per thread
+// (across the images) where the rows are contiguous, and its exponent e[c]
+// (zero channels: the least, so that they scale to zero); blocks
+// [IC, IC + OC) output channel o's greatest FP16 weight, four loads of eight
+// in flight per thread, and a[o].
 template <int M>
 __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__restrict__ e,
                                                      int32_t *__restrict__ amax) {
@@ -139,22 +140,36 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
     if (w < a.ic) {
         const int64_t plane = a.ih * a.iw;
-        for (int64_t n = 0; n < a.n; ++n) {
-            const float *p = a.x + n * a.xnb3 + w * a.xnb2;
-            if (a.xnb1 == a.iw && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-                const float4v *q = reinterpret_cast<const float4v *>(p);
-                const int64_t quads = plane / 4;
-                int64_t i = tid;
-                for (; i + 768 < quads; i += 1024) {
-                    const float4v v0 = q[i], v1 = q[i + 256], v2 = q[i + 512], v3 = q[i + 768];
-                    m0 = fmaxf(m0, abs_max4(v0));
-                    m1 = fmaxf(m1, abs_max4(v1));
-                    m2 = fmaxf(m2, abs_max4(v2));
-                    m3 = fmaxf(m3, abs_max4(v3));
+        const float *p0 = a.x + w * a.xnb2;
+        const bool vec = a.xnb1 == a.iw && plane % 4 == 0 && a.xnb3 % 4 == 0 &&
+                         (reinterpret_cast<uintptr_t>(p0) & 15) == 0 && a.n * (plane / 4) < (int64_t{1} << 32);
+        if (vec) {
+            // The channel's planes as one run of n * plane / 4 quads, the
+            // image of quad i being i / quads.
+            const uint32_t quads = static_cast<uint32_t>(plane / 4);
+            const uint32_t total = static_cast<uint32_t>(a.n) * quads;
+            for (uint32_t base = tid; base < total; base += 256 * 8) {
+                float4v v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t i = base + 256 * u;
+                    v[u] = float4v{};
+                    if (i < total) {
+                        const uint32_t n = i / quads;
+                        v[u] = reinterpret_cast<const float4v *>(p0 + n * a.xnb3)[i - n * quads];
+                    }
                 }
-                for (; i < quads; i += 256) m0 = fmaxf(m0, abs_max4(q[i]));
-                for (int64_t j = quads * 4 + tid; j < plane; j += 256) m1 = fmaxf(m1, fabsf(p[j]));
-            } else {
+#pragma unroll
+                for (int u = 0; u < 8; u += 4) {
+                    m0 = fmaxf(m0, abs_max4(v[u]));
+                    m1 = fmaxf(m1, abs_max4(v[u + 1]));
+                    m2 = fmaxf(m2, abs_max4(v[u + 2]));
+                    m3 = fmaxf(m3, abs_max4(v[u + 3]));
+                }
+            }
+        } else {
+            for (int64_t n = 0; n < a.n; ++n) {
+                const float *p = p0 + n * a.xnb3;
                 for (int64_t i = tid; i < plane; i += 256) {
                     const int64_t y = i / a.iw;
                     m0 = fmaxf(m0, fabsf(p[y * a.xnb1 + (i - y * a.iw)]));
@@ -269,10 +284,15 @@ __device__ __forceinline__ void transform_g(const float (&g)[3][3], float (&u)[M
 // from IC to kp.
 constexpr int kWeightOc = 4, kWeightIc = 64;
 
-// LDS of a block of weights_split: the 4 floats of the reduction, then the
-// staged parts.
+// The points of one pass of the transforms' staging in LDS: half of them.
 template <int M>
-constexpr int kWeightLds = 16 + 2 * Mat<M>::A * Mat<M>::A * kWeightOc * kWeightIc * 2;
+constexpr int kHalfPoints = Mat<M>::A * Mat<M>::A / 2;
+static_assert(Mat<2>::A % 2 == 0 && Mat<4>::A % 2 == 0, "the points split into two halves");
+
+// LDS of a block of weights_split: the 4 floats of the reduction, then the
+// staged parts of half of the points.
+template <int M>
+constexpr int kWeightLds = 16 + 2 * kHalfPoints<M> * kWeightOc * kWeightIc * 2;
 
 // Block (bx, by) of weights_split, its LDS at `lds`.
 template <int M>
@@ -281,7 +301,7 @@ __device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__
                                                     _Float16 *__restrict__ u, int32_t *__restrict__ shift, int64_t bx,
                                                     int64_t by, char *lds) {
     constexpr int A = Mat<M>::A;
-    constexpr int kRows = 2 * A * A;
+    constexpr int H = kHalfPoints<M>;
     float *scratch = reinterpret_cast<float *>(lds);
     auto stage = reinterpret_cast<_Float16(*)[kWeightOc][kWeightIc]>(lds + 16);
     const int tid = threadIdx.x;
@@ -304,32 +324,36 @@ __device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__
     const int E = static_cast<int>(block_max(static_cast<float>(emax), scratch));
     if (o < oc && by == 0 && cl == 0) shift[o] = E - ao;
     float t[A][A] = {};
-    int s = 0;
+    float f = 0.0f;
     if (live) {
         transform_g<M>(g, t);
-        s = ao + ec - E;
+        f = ldexpf(kSplitDown, ao + ec - E);
     }
-#pragma unroll
-    for (int i = 0; i < A; ++i)
-#pragma unroll
-        for (int j = 0; j < A; ++j) {
-            _Float16 hi, lo;
-            split2(ldexpf(t[i][j], s), hi, lo);
-            stage[2 * (i * A + j)][ol][cl] = hi;
-            stage[2 * (i * A + j) + 1][ol][cl] = lo;
-        }
-    __syncthreads();
-    // kRows x kWeightOc rows of `width` halves, 8 at a time.
+    // Half of the points at a time: kRows / 2 x kWeightOc rows of `width`
+    // halves, 8 at a time.
     const int width = static_cast<int>(kp - c0 < kWeightIc ? kp - c0 : kWeightIc);
     const int per_row = width / 8;
-    for (int q = tid; q < kRows * kWeightOc * per_row; q += 256) {
-        const int row = q / per_row;
-        const int k = (q - row * per_row) * 8;
-        const int r = row / kWeightOc, oo = row % kWeightOc;
-        if (o0 + oo >= oc) continue;
-        const int64_t c = c0 + k;
-        *reinterpret_cast<half8 *>(u + r * oc * kp + (c >> 5) * oc * 32 + (o0 + oo) * 32 + (c & 31)) =
-            *reinterpret_cast<const half8 *>(&stage[r][oo][k]);
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) __syncthreads();  // the first half read out
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const int pt = pass * H + h;
+            _Float16 hi, lo;
+            split_scaled(t[pt / A][pt % A] * f, hi, lo);
+            stage[2 * h][ol][cl] = hi;
+            stage[2 * h + 1][ol][cl] = lo;
+        }
+        __syncthreads();
+        for (int q = tid; q < 2 * H * kWeightOc * per_row; q += 256) {
+            const int row = q / per_row;
+            const int k = (q - row * per_row) * 8;
+            const int r = 2 * H * pass + row / kWeightOc, oo = row % kWeightOc;
+            if (o0 + oo >= oc) continue;
+            const int64_t cc = c0 + k;
+            *reinterpret_cast<half8 *>(u + r * oc * kp + (cc >> 5) * oc * 32 + (o0 + oo) * 32 + (cc & 31)) =
+                *reinterpret_cast<const half8 *>(&stage[row / kWeightOc][oo][k]);
+        }
     }
 }
 
@@ -393,15 +417,29 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
     const int64_t y0 = static_cast<int64_t>(ty) * M - a.p1;
     const int64_t x0 = static_cast<int64_t>(tx) * M - a.p0;
     const float *plane = a.x + static_cast<int64_t>(n) * a.xnb3 + static_cast<int64_t>(c) * a.xnb2;
+    // Every load unconditional, from the nearest point inside the image, and
+    // the points outside then cleared by masks of all ones or zeros.  The
+    // masks pass through an empty asm so that the compiler sees no select of
+    // a load, which it would turn back into a branch around each load.
+    int64_t xc[A];
+    int mask_col[A];
+#pragma unroll
+    for (int j = 0; j < A; ++j) {
+        const int64_t xx = x0 + j;
+        mask_col[j] = xx >= 0 && xx < a.iw ? -1 : 0;
+        asm("" : "+v"(mask_col[j]));
+        xc[j] = xx < 0 ? 0 : (xx < a.iw ? xx : a.iw - 1);
+    }
     float d[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i) {
         const int64_t yy = y0 + i;
-        const bool row_in = yy >= 0 && yy < a.ih;
+        int mask_row = yy >= 0 && yy < a.ih ? -1 : 0;
+        asm("" : "+v"(mask_row));
+        const float *row = plane + (yy < 0 ? 0 : (yy < a.ih ? yy : a.ih - 1)) * a.xnb1;
 #pragma unroll
         for (int j = 0; j < A; ++j) {
-            const int64_t xx = x0 + j;
-            d[i][j] = (row_in && xx >= 0 && xx < a.iw) ? plane[yy * a.xnb1 + xx] : 0.0f;
+            d[i][j] = __builtin_bit_cast(float, __builtin_bit_cast(int, row[xc[j]]) & (mask_row & mask_col[j]));
         }
     }
     float bd[A][A];
@@ -422,22 +460,25 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
 // to kp.  A block takes 8 consecutive tiles by
 // 32 channels, one (tile, channel) a thread, consecutive threads consecutive
 // tiles (so that the reads of a channel are rows of the image); the results
-// are staged in LDS as [xi][part][tile][channel] and written out as rows of
-// 32 channels.
+// are staged in LDS as [xi][part][tile][channel], half of the points at a
+// time (so that more blocks fit a CU), and written out as rows of 32
+// channels.
 constexpr int kInTiles = 8, kInChannels = 32;
 
-// LDS of a block of inputs_split: the staged parts of V, [xi][part][tile]
-// [channel], rows of a tile 40 halves apart (16-byte aligned).
+// LDS of a block of inputs_split: the staged parts of half of the points,
+// [xi][part][tile][channel], rows of a tile 40 halves apart (16-byte aligned).
 template <int M>
-constexpr int kInputLds = 2 * Mat<M>::A * Mat<M>::A * kInTiles * (kInChannels + 8) * 2;
+constexpr int kInputLds = 2 * kHalfPoints<M> * kInTiles * (kInChannels + 8) * 2;
 
 // Block (bx, by) of inputs_split, its LDS at `lds`: V * 2^-e_c split into
-// its two FP16 parts (split2, the form the products take), written as
+// its two FP16 parts (split2, the form the products take; the channel's
+// 2^-e_c and the split's 2^-4 one factor), written as
 // v[xi][part][c / 32][tile][c % 32].
 template <int M>
 __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_t kp, const int32_t *__restrict__ e,
                                                    _Float16 *__restrict__ v, int64_t bx, int64_t by, char *lds) {
     constexpr int A = Mat<M>::A;
+    constexpr int H = kHalfPoints<M>;
     auto stage = reinterpret_cast<_Float16(*)[kInTiles][kInChannels + 8]>(lds);
     const int tid = threadIdx.x;
     const int64_t t0 = bx * kInTiles;
@@ -445,32 +486,33 @@ __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_
     const int tl = tid % kInTiles, cl = tid / kInTiles;
     const int64_t tile = t0 + tl, c = c0 + cl;
     float x[A][A] = {};
+    float f = 0.0f;
     if (c < a.ic && tile < a.tiles) {
         transform_d<M>(a, static_cast<uint32_t>(tile), static_cast<uint32_t>(c), x);
-        const int s = -e[c];
-#pragma unroll
-        for (int r = 0; r < A; ++r)
-#pragma unroll
-            for (int q = 0; q < A; ++q) x[r][q] = ldexpf(x[r][q], s);
+        f = ldexpf(kSplitDown, -e[c]);
     }
 #pragma unroll
-    for (int r = 0; r < A; ++r)
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) __syncthreads();  // the first half read out
 #pragma unroll
-        for (int q = 0; q < A; ++q) {
+        for (int h = 0; h < H; ++h) {
+            const int pt = pass * H + h;
             _Float16 hi, lo;
-            split2(x[r][q], hi, lo);
-            stage[2 * (r * A + q)][tl][cl] = hi;
-            stage[2 * (r * A + q) + 1][tl][cl] = lo;
+            split_scaled(x[pt / A][pt % A] * f, hi, lo);
+            stage[2 * h][tl][cl] = hi;
+            stage[2 * h + 1][tl][cl] = lo;
         }
-    __syncthreads();
-    // 2 A * A * kInTiles rows of 32 halves, 8 at a time.
-    for (int q = tid; q < 2 * A * A * kInTiles * (kInChannels / 8); q += 256) {
-        const int row = q / (kInChannels / 8);
-        const int k = (q % (kInChannels / 8)) * 8;
-        const int xp = row / kInTiles, t = row % kInTiles;
-        if (t0 + t >= a.tiles) continue;
-        *reinterpret_cast<half8 *>(v + xp * a.tiles * kp + c0 * a.tiles + (t0 + t) * kInChannels + k) =
-            *reinterpret_cast<const half8 *>(&stage[xp][t][k]);
+        __syncthreads();
+        // 2 H * kInTiles rows of 32 halves, 8 at a time.
+        for (int q = tid; q < 2 * H * kInTiles * (kInChannels / 8); q += 256) {
+            const int row = q / (kInChannels / 8);
+            const int k = (q % (kInChannels / 8)) * 8;
+            const int xl = row / kInTiles, t = row % kInTiles;
+            if (t0 + t >= a.tiles) continue;
+            const int xp = 2 * H * pass + xl;
+            *reinterpret_cast<half8 *>(v + xp * a.tiles * kp + c0 * a.tiles + (t0 + t) * kInChannels + k) =
+                *reinterpret_cast<const half8 *>(&stage[xl][t][k]);
+        }
     }
 }
 
@@ -491,7 +533,9 @@ __global__ __launch_bounds__(256) void inputs_split_kernel(WinogradArgs a, int64
         for (int64_t o = threadIdx.x; o < a.oc; o += 256) shift[o] = E - amax[o];
         __syncthreads();
     }
-    inputs_split_block<M>(a, kp, e, v, blockIdx.x, blockIdx.y, lds);
+    // Neighbouring tiles on one XCD, as in the transforms' launch.
+    const uint32_t b = xcd_swizzle(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x * gridDim.y);
+    inputs_split_block<M>(a, kp, e, v, b % gridDim.x, b / gridDim.x, lds);
 }
 
 // The weights' and the inputs' transforms of a call without kept weights in
@@ -508,8 +552,11 @@ __global__ __launch_bounds__(256) void transforms_kernel(WinogradArgs a, int64_t
                                                          int64_t wgx, int64_t wblocks, int64_t igx) {
     __shared__ __attribute__((aligned(16))) char lds[kTransformLds<M>];
     // The two kinds alternate while both last, so that every CU gets some of
-    // each; the rest of the longer kind follows.
-    const int64_t b = blockIdx.x;
+    // each; the rest of the longer kind follows.  The blocks an XCD takes
+    // (every 8th of the launch) are consecutive ones of this order, so that
+    // each XCD gets both kinds and the inputs' blocks of one XCD are
+    // neighbouring tiles, whose overlapping rows its own L2 then holds.
+    const int64_t b = xcd_swizzle(blockIdx.x, gridDim.x);
     const int64_t iblocks = gridDim.x - wblocks;
     const int64_t both = wblocks < iblocks ? wblocks : iblocks;
     bool weights;
