@@ -45,8 +45,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only-main", action="store_true")
     p.add_argument("--workload", default="", help="run one workload alone (cfg1 cfg2 cfg2_kept cfg3a cfg3a_kept "
-                                                  "cfg3b cfg4_self cfg4_cross cfg5 unet unet_kept copy), for a "
-                                                  "profiler")
+                                                  "cfg3b cfg4_self cfg4_cross cfg5 unet unet_kept copy "
+                                                  "vendor_products vendor_4096), for a profiler")
     p.add_argument("--no-unet", action="store_true", help="leave out the UNet step")
     p.add_argument("--no-vae", action="store_true", help="leave out the VAE decoder's operations")
     return p.parse_args()
@@ -249,6 +249,27 @@ def copy_workload(dev, mib=256):
     return run, 0.0
 
 
+def vendor_workload(dev, batch, m, n, k, seed):
+    """torch.bmm (the vendor's hipBLASLt / rocBLAS) in FP16 on contiguous
+    operands, for comparison only, never a path of the library: the vendor's
+    time for the same MFMA work as one of this library's kernels
+    (vendor_products: configs[1]'s products, 36 points x 3 split products of
+    320 x 512 x 320, as one batch of 108), or for a large square product that
+    shows the MFMA rate the vendor reaches where K is long (vendor_4096)."""
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    a = torch.randn(batch, m, k, device=dev, dtype=torch.float16, generator=gen)
+    b = torch.randn(batch, k, n, device=dev, dtype=torch.float16, generator=gen)
+    out = torch.empty(batch, m, n, device=dev, dtype=torch.float16)
+
+    def run():
+        torch.bmm(a, b, out=out)
+
+    run.keep = (a, b, out)
+    return run, 2.0 * batch * m * n * k
+
+
 def unet_workload(dev, seed=7, keep=False):
     """The synthetic SD1.5 UNet step (unet_step.py) at 512x512, batch 2,
     captured in a HIP graph; with `keep`, Winograd's transformed weights kept
@@ -312,6 +333,10 @@ def make_workload(dev, name):
         return attention_workload(dev, 2, 8, 4096, 77, 40, seed=5)
     if name == "copy":
         return copy_workload(dev)
+    if name == "vendor_products":
+        return vendor_workload(dev, 108, 320, 512, 320, seed=11)
+    if name == "vendor_4096":
+        return vendor_workload(dev, 1, 4096, 4096, 4096, seed=12)
     if name == "cfg5":
         graph = sdxl_block_workload(dev)
         return graph.run, graph.flops
