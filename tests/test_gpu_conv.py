@@ -247,3 +247,37 @@ def test_winograd_graph_replays(gpu, c):
         sdhip.conv2d(k_d, x_d, other, params)
         torch.cuda.synchronize()
         assert np.array_equal(other.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [
+    (40, 36, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2),   # Winograd F(4x4), transforms of the large path
+    (15, 9, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2),    # small images, F(2x2)
+    (16, 16, 72, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1),   # small images, F(4x4)
+    (33, 33, 24, 30, 3, 3, 2, 2, 1, 1, 1, 1, 1),   # direct by columns
+    (32, 32, 64, 40, 1, 1, 1, 1, 0, 0, 1, 1, 2),   # 1x1
+], ids=lambda c: "x".join(map(str, c)))
+def test_conv2d_strided_input(gpu, c):
+    """The input as a view into a larger tensor: rows, planes and images
+    further apart than their extents, and a start that is no multiple of 16
+    bytes -- ggml's nb[1..3] of a view (the predicate takes any multiple of 4
+    bytes, conv2d.cc:320-331)."""
+    w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
+    r = rng(sum(c) + 11)
+    kh16, k32 = weights_f16(r, (oc, ic, kh, kw))
+    big = uniform(r, (n, ic + 3, h_ + 2, w_ + 5), 1.0)
+    x = np.ascontiguousarray(big[:, 1:ic + 1, 1:h_ + 1, 2:w_ + 2])
+    big_d = dev(big, gpu)
+    x_d = big_d[:, 1:ic + 1, 1:h_ + 1, 2:w_ + 2]
+    assert not x_d.is_contiguous()
+    oh, ow = out_size(h_, kh, s1, p1, d1), out_size(w_, kw, s0, p0, d0)
+    k_d = dev(kh16, gpu)
+    y_d = unwritten((n, oc, oh, ow), gpu)
+    params = sdhip.conv_params(s0, s1, p0, p1, d0, d1)
+    path = sdhip.conv2d_path(k_d, x_d, y_d, params)
+    sdhip.conv2d(k_d, x_d, y_d, params)
+    torch.cuda.synchronize()
+    exact, mag = orc.exact_conv2d(x, k32, s0, s1, p0, p1, d0, d1)
+    err = orc.metric(y_d.cpu().numpy(), exact, mag)
+    print(f"strided input {c} path {path}: {err:.3g}")
+    assert err <= BOUND
