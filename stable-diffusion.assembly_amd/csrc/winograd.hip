@@ -1201,6 +1201,9 @@ __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(Winograd
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // The last step's copy into LDS (of kernels no step reads) done before
+    // the workgroup's LDS can be given to another.
+    wait_loads<0>();
     // Lane holds the sums of channels o0 + 4 kg + r, tile 16 t + lr; both
     // operands were scaled by 2^-4 in their splits.
     const int64_t oplane = a.oc * TP;
