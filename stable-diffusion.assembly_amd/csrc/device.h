@@ -208,18 +208,6 @@ __device__ __forceinline__ void wait_loads() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-// A barrier of the workgroup for LDS alone: every wave's LDS reads and writes
-// before it are done before any wave's after it, while global loads and
-// stores stay in flight across it (__syncthreads waits for all of them,
-// which would drain loads issued ahead for later steps).  Data that a
-// global_load_lds brings into LDS is the caller's to wait for (wait_loads)
-// before it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // One 16-byte piece a lane of a 1 KB copy from global memory into LDS; the
 // LDS address is the wave's (lane l's piece lands 16 l bytes past it).
 __device__ __forceinline__ void copy_lds(const void *src, char *lds) {

@@ -335,7 +335,7 @@ __device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__
     const int per_row = width / 8;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
-        if (pass == 1) lds_barrier();  // the first half read out
+        if (pass == 1) __syncthreads();  // the first half read out
 #pragma unroll
         for (int h = 0; h < H; ++h) {
             const int pt = pass * H + h;
@@ -344,7 +344,7 @@ __device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__
             stage[2 * h][ol][cl] = hi;
             stage[2 * h + 1][ol][cl] = lo;
         }
-        lds_barrier();
+        __syncthreads();
         for (int q = tid; q < 2 * H * kWeightOc * per_row; q += 256) {
             const int row = q / per_row;
             const int k = (q - row * per_row) * 8;
@@ -405,56 +405,43 @@ __global__ __launch_bounds__(256) void weights_scaled_kernel(const _Float16 *__r
 
 // ------------------------------------------------------------------ 2. inputs
 
-// The alpha x alpha inputs of a tile as loaded: every load unconditional,
-// from the nearest point inside the image, with masks of all ones or zeros
-// that clear the points outside when the tile is transformed (so that the
-// loads of one tile can be in flight while another is transformed).  The
-// masks pass through an empty asm so that the compiler sees no select of a
-// load, which it would turn back into a branch around each load.
+// (B^T d B) of the alpha x alpha inputs of a tile, zeros outside the image:
+// B^T d (a row r of B^T takes its combination of the rows of d), then each of
+// those times B.
 template <int M>
-struct InputTile {
-    float d[Mat<M>::A][Mat<M>::A];
-    int mask_row[Mat<M>::A], mask_col[Mat<M>::A];
-};
-
-template <int M>
-__device__ __forceinline__ void load_tile(const WinogradArgs &a, uint32_t tile, uint32_t c, InputTile<M> &t) {
+__device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile, uint32_t c,
+                                            float (&v)[Mat<M>::A][Mat<M>::A]) {
     constexpr int A = Mat<M>::A;
     uint32_t tx, ty, n;
     split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     const int64_t y0 = static_cast<int64_t>(ty) * M - a.p1;
     const int64_t x0 = static_cast<int64_t>(tx) * M - a.p0;
     const float *plane = a.x + static_cast<int64_t>(n) * a.xnb3 + static_cast<int64_t>(c) * a.xnb2;
+    // Every load unconditional, from the nearest point inside the image, and
+    // the points outside then cleared by masks of all ones or zeros.  The
+    // masks pass through an empty asm so that the compiler sees no select of
+    // a load, which it would turn back into a branch around each load.
     int64_t xc[A];
+    int mask_col[A];
 #pragma unroll
     for (int j = 0; j < A; ++j) {
         const int64_t xx = x0 + j;
-        t.mask_col[j] = xx >= 0 && xx < a.iw ? -1 : 0;
-        asm("" : "+v"(t.mask_col[j]));
+        mask_col[j] = xx >= 0 && xx < a.iw ? -1 : 0;
+        asm("" : "+v"(mask_col[j]));
         xc[j] = xx < 0 ? 0 : (xx < a.iw ? xx : a.iw - 1);
     }
+    float d[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i) {
         const int64_t yy = y0 + i;
-        t.mask_row[i] = yy >= 0 && yy < a.ih ? -1 : 0;
-        asm("" : "+v"(t.mask_row[i]));
+        int mask_row = yy >= 0 && yy < a.ih ? -1 : 0;
+        asm("" : "+v"(mask_row));
         const float *row = plane + (yy < 0 ? 0 : (yy < a.ih ? yy : a.ih - 1)) * a.xnb1;
 #pragma unroll
-        for (int j = 0; j < A; ++j) t.d[i][j] = row[xc[j]];
+        for (int j = 0; j < A; ++j) {
+            d[i][j] = __builtin_bit_cast(float, __builtin_bit_cast(int, row[xc[j]]) & (mask_row & mask_col[j]));
+        }
     }
-}
-
-// (B^T d B) of a loaded tile, zeros outside the image: B^T d (a row r of B^T
-// takes its combination of the rows of d), then each of those times B.
-template <int M>
-__device__ __forceinline__ void transform_tile(const InputTile<M> &t, float (&v)[Mat<M>::A][Mat<M>::A]) {
-    constexpr int A = Mat<M>::A;
-    float d[A][A];
-#pragma unroll
-    for (int i = 0; i < A; ++i)
-#pragma unroll
-        for (int j = 0; j < A; ++j)
-            d[i][j] = __builtin_bit_cast(float, __builtin_bit_cast(int, t.d[i][j]) & (t.mask_row[i] & t.mask_col[j]));
     float bd[A][A];
 #pragma unroll
     for (int r = 0; r < A; ++r)
@@ -466,14 +453,6 @@ __device__ __forceinline__ void transform_tile(const InputTile<M> &t, float (&v)
 #pragma unroll
         for (int s = 0; s < A; ++s)
             v[r][s] = dot_n<A>([&](int j) { return Mat<M>::bt(s, j); }, [&](int j) { return bd[r][j]; });
-}
-
-template <int M>
-__device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile, uint32_t c,
-                                            float (&v)[Mat<M>::A][Mat<M>::A]) {
-    InputTile<M> t;
-    load_tile<M>(a, tile, c, t);
-    transform_tile<M>(t, v);
 }
 
 // V[xi][tile][ic] * 2^-e_c split into two FP16 parts, in blocks of 32
@@ -491,16 +470,10 @@ constexpr int kInTiles = 8, kInChannels = 32;
 template <int M>
 constexpr int kInputLds = 2 * kHalfPoints<M> * kInTiles * (kInChannels + 8) * 2;
 
-// Tile groups a block of inputs_split takes, one after another, the inputs
-// of each loaded before the first is transformed and written (one: two
-// measured slower, 29 us against 20 at configs[1], for the registers).
-constexpr int kInItems = 1;
-
 // Block (bx, by) of inputs_split, its LDS at `lds`: V * 2^-e_c split into
 // its two FP16 parts (split2, the form the products take; the channel's
 // 2^-e_c and the split's 2^-4 one factor), written as
-// v[xi][part][c / 32][tile][c % 32], for the tile groups kInItems bx ..
-// kInItems bx + kInItems - 1.
+// v[xi][part][c / 32][tile][c % 32].
 template <int M>
 __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_t kp, const int32_t *__restrict__ e,
                                                    _Float16 *__restrict__ v, int64_t bx, int64_t by, char *lds) {
@@ -508,49 +481,37 @@ __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_
     constexpr int H = kHalfPoints<M>;
     auto stage = reinterpret_cast<_Float16(*)[kInTiles][kInChannels + 8]>(lds);
     const int tid = threadIdx.x;
+    const int64_t t0 = bx * kInTiles;
     const int64_t c0 = by * kInChannels;
     const int tl = tid % kInTiles, cl = tid / kInTiles;
-    const int64_t c = c0 + cl;
-    // The channel's exponent first: loads complete in order, and the first
-    // group must not wait for the second's.
-    const int ec = c < a.ic ? e[c] : 0;
-    InputTile<M> in[kInItems];
-    bool live[kInItems];
-#pragma unroll
-    for (int it = 0; it < kInItems; ++it) {
-        const int64_t tile = (kInItems * bx + it) * kInTiles + tl;
-        live[it] = c < a.ic && tile < a.tiles;
-        if (live[it]) load_tile<M>(a, static_cast<uint32_t>(tile), static_cast<uint32_t>(c), in[it]);
+    const int64_t tile = t0 + tl, c = c0 + cl;
+    float x[A][A] = {};
+    float f = 0.0f;
+    if (c < a.ic && tile < a.tiles) {
+        transform_d<M>(a, static_cast<uint32_t>(tile), static_cast<uint32_t>(c), x);
+        f = ldexpf(kSplitDown, -e[c]);
     }
-    const float f = c < a.ic ? ldexpf(kSplitDown, -ec) : 0.0f;
 #pragma unroll
-    for (int it = 0; it < kInItems; ++it) {
-        const int64_t t0 = (kInItems * bx + it) * kInTiles;
-        if (t0 >= a.tiles) break;  // the same for the whole block
-        float x[A][A] = {};
-        if (live[it]) transform_tile<M>(in[it], x);
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) __syncthreads();  // the first half read out
 #pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
-            if (it > 0 || pass == 1) lds_barrier();  // the staging read out
-#pragma unroll
-            for (int h = 0; h < H; ++h) {
-                const int pt = pass * H + h;
-                _Float16 hi, lo;
-                split_scaled(x[pt / A][pt % A] * f, hi, lo);
-                stage[2 * h][tl][cl] = hi;
-                stage[2 * h + 1][tl][cl] = lo;
-            }
-            lds_barrier();
-            // 2 H * kInTiles rows of 32 halves, 8 at a time.
-            for (int q = tid; q < 2 * H * kInTiles * (kInChannels / 8); q += 256) {
-                const int row = q / (kInChannels / 8);
-                const int k = (q % (kInChannels / 8)) * 8;
-                const int xl = row / kInTiles, t = row % kInTiles;
-                if (t0 + t >= a.tiles) continue;
-                const int xp = 2 * H * pass + xl;
-                *reinterpret_cast<half8 *>(v + xp * a.tiles * kp + c0 * a.tiles + (t0 + t) * kInChannels + k) =
-                    *reinterpret_cast<const half8 *>(&stage[xl][t][k]);
-            }
+        for (int h = 0; h < H; ++h) {
+            const int pt = pass * H + h;
+            _Float16 hi, lo;
+            split_scaled(x[pt / A][pt % A] * f, hi, lo);
+            stage[2 * h][tl][cl] = hi;
+            stage[2 * h + 1][tl][cl] = lo;
+        }
+        __syncthreads();
+        // 2 H * kInTiles rows of 32 halves, 8 at a time.
+        for (int q = tid; q < 2 * H * kInTiles * (kInChannels / 8); q += 256) {
+            const int row = q / (kInChannels / 8);
+            const int k = (q % (kInChannels / 8)) * 8;
+            const int xl = row / kInTiles, t = row % kInTiles;
+            if (t0 + t >= a.tiles) continue;
+            const int xp = 2 * H * pass + xl;
+            *reinterpret_cast<half8 *>(v + xp * a.tiles * kp + c0 * a.tiles + (t0 + t) * kInChannels + k) =
+                *reinterpret_cast<const half8 *>(&stage[xl][t][k]);
         }
     }
 }
@@ -1132,18 +1093,12 @@ __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(Winograd
         // before, whose stage the next step's kernels now overwrite.  The
         // exponents and V are waited for where they are used.
         wait_loads<2 + 2 * NT * A>();
-        // The barrier alone: the fences of __syncthreads (or of an LDS
-        // fence, which covers the copies into LDS) would wait for every load
-        // in flight, V's and the exponents' of the next step among them.
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __syncthreads();
         int4v q[9];
         const char *gl = gbuf[stage] + (lr * kRowPieces + 9 * kg) * 16;
 #pragma unroll
         for (int k = 0; k < 9; ++k) q[k] = *reinterpret_cast<const int4v *>(gl + 16 * k);
-        // Every step copies (the last one its own kernels again, into the
-        // stage no step reads), so that every path into the loop's top has
-        // the same copies and loads in flight and the waits stay exact.
-        copy_g(next, stage ^ 1);
+        if (c0 + 32 < c_end) copy_g(c0 + 32, stage ^ 1);
         const int64_t c = c0 + 8 * kg;
         const bool c_in = c < a.ic;
         // Row `row` of G g of each kernel, times 2^(a_os + e_c - E) and the
@@ -1201,9 +1156,6 @@ __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(Winograd
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    // The last step's copy into LDS (of kernels no step reads) done before
-    // the workgroup's LDS can be given to another.
-    wait_loads<0>();
     // Lane holds the sums of channels o0 + 4 kg + r, tile 16 t + lr; both
     // operands were scaled by 2^-4 in their splits.
     const int64_t oplane = a.oc * TP;
@@ -1382,7 +1334,7 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         // Both transforms in one launch.
         KernelScope scope(names[5].c_str(), stream);
         const int64_t wgx = ceil_div(a.oc, kWeightOc), wblocks = wgx * ceil_div(l.kp, kWeightIc);
-        const int64_t igx = ceil_div(a.tiles, kInTiles * kInItems), iblocks = igx * (l.kp / kInChannels);
+        const int64_t igx = ceil_div(a.tiles, kInTiles), iblocks = igx * (l.kp / kInChannels);
         hipLaunchKernelGGL((transforms_kernel<M>), dim3(static_cast<uint32_t>(wblocks + iblocks)), dim3(256), 0,
                            stream, a, l.kp, e, a_oc, uh, shift, vh, wgx, wblocks, igx);
     } else if (!ready) {
@@ -1395,8 +1347,7 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     }
     if (kept != nullptr) {
         KernelScope scope(names[2].c_str(), stream);
-        hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles * kInItems), l.kp / kInChannels),
-                           dim3(256), 0,
+        hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
                            stream, a, l.kp, e, vh, a_kept, f, shift);
     }
     {
