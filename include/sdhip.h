@@ -82,12 +82,25 @@ const char *sdhip_last_error(void);
 
 /* The tuning that changes what is computed, in the reference's SDASM_TUNE
  * syntax "name=value,..." (sources/kernels.h:91-135, parsed by cpu.cc:121-212):
- * bits, input_bits, group, weight_group, quantize, winograd,
- * winograd_positions, winograd4_positions, winograd_small_tiles, fuse,
- * attention_keys; and this library's own: winograd_fp32, winograd_splits,
- * gemm_stages, gemm_tiles, attention_generic, attention_fp32 (forms to
- * compare, same results within the bounds).  Returns SDHIP_ERROR naming the
- * first unknown name.  "" resets the defaults. */
+ * every name of the reference's Tuning is taken, with its default.  Those
+ * that change what is computed: bits (2..8; 16, the reference's products of
+ * 16-bit numbers, is refused), input_bits, group, weight_group, quantize
+ * (with bits: 1 linear layers, 4 attention; 2, the convolutions, makes
+ * CONV_2D not taken -- quantized convolutions are not a form of this
+ * library), winograd, winograd_positions, winograd4_positions,
+ * winograd_small_tiles, attention_keys, fuse and fuse_residual (0: the
+ * planner fuses no chain, or no residual connection, and an entry point
+ * handed one computes it in a pass of its own after the operation, as ggml's
+ * nodes would), todo and todo_tokens (sdhip_token_downsampling) and
+ * store_forget (0 keeps every store entry, for the store's canary test).  The
+ * names that size the reference's CPU blocks or choose among its CPU forms
+ * (conv_kc, mul_mat_mc, amx_*, wide, prefetch, guided, half_format, ...) are
+ * taken and have no effect here.  The reference's names take any int, as its
+ * parser does, and are clamped where it clamps them (quant.cc:59-67).  This
+ * library's own: winograd_fp32, winograd_splits, gemm_stages, gemm_tiles,
+ * attention_generic, attention_fp32 (forms to compare, same results within
+ * the bounds), each taking only its documented values.  Returns SDHIP_ERROR
+ * naming the first unknown name or refused value.  "" resets the defaults. */
 sdhip_status sdhip_set_tuning(const char *text);
 /* The value of one tuning field, or -1 if it has no such name. */
 int sdhip_get_tuning(const char *name);
@@ -218,6 +231,88 @@ sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int 
 int sdhip_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y);
 sdhip_status sdhip_norm(const sdhip_tensor *x, const sdhip_tensor *y, float eps, const sdhip_epilogue *chain,
                         void *stream);
+
+/* ---------------------------------------------------------------- the graph */
+
+/* A node of a ggml graph, as the planner reads it: what ggml_tensor holds of
+ * it, without ggml's types.  `op` is ggml's operation by this enumeration
+ * (GGML_OP_NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE -- the empty ones,
+ * ggml_op_is_empty -- and the rest the planner looks at; any other operation
+ * is SDHIP_OP_OTHER), `unary` ggml_get_unary_op of a UNARY node, `flags`
+ * GGML_TENSOR_FLAG_COMPUTE and GGML_TENSOR_FLAG_OUTPUT as these bits,
+ * `op_params` ggml's op_params words, `tensor` the node's own type, ne, nb
+ * and data, `src` and `view_src` the nodes ggml points at (NULL where none). */
+enum {
+    SDHIP_OP_NONE = 0,
+    SDHIP_OP_VIEW,
+    SDHIP_OP_RESHAPE,
+    SDHIP_OP_PERMUTE,
+    SDHIP_OP_TRANSPOSE,
+    SDHIP_OP_ADD,
+    SDHIP_OP_MUL,
+    SDHIP_OP_CONT,
+    SDHIP_OP_UNARY,
+    SDHIP_OP_MUL_MAT,
+    SDHIP_OP_CONV_2D,
+    SDHIP_OP_FLASH_ATTN_EXT,
+    SDHIP_OP_GROUP_NORM,
+    SDHIP_OP_NORM,
+    SDHIP_OP_OTHER
+};
+enum { SDHIP_UNARY_OTHER = 0, SDHIP_UNARY_SILU = 1, SDHIP_UNARY_GELU = 2 };
+enum { SDHIP_FLAG_COMPUTE = 1, SDHIP_FLAG_OUTPUT = 2 };
+#define SDHIP_MAX_SRC 10
+#define SDHIP_MAX_OP_PARAMS 16
+
+typedef struct sdhip_node {
+    int32_t op;
+    int32_t unary;
+    int32_t flags;
+    int32_t op_params[SDHIP_MAX_OP_PARAMS];
+    sdhip_tensor tensor;
+    const struct sdhip_node *src[SDHIP_MAX_SRC];
+    const struct sdhip_node *view_src;
+} sdhip_node;
+
+/* What the library does with node `index` of a graph: `taken`, the operation
+ * it computes it as (SDHIP_OP_MUL_MAT, CONV_2D, FLASH_ATTN_EXT, GROUP_NORM,
+ * NORM), or SDHIP_OP_NONE; `count`, the nodes that computation stands for
+ * (1 + the chain's and the gated GELU's nodes, the views between included);
+ * `chain`, the nodes after it computed along with it (its redirect pointing
+ * at a node's tensor); `gated_out`, GEGLU's output node when the gated GELU
+ * is fused, else NULL.  The decisions of hooks.cc:100-147 -- match_chain,
+ * redirect_apart and match_gated_gelu (fusion.cc:136-394), under the tuning's
+ * fuse and fuse_residual -- made over sdhip_node.  SDHIP_UNSUPPORTED where the
+ * node is not taken. */
+typedef struct sdhip_node_plan {
+    int32_t taken;
+    int32_t count;
+    sdhip_epilogue chain;
+    const sdhip_node *gated_out;
+} sdhip_node_plan;
+
+sdhip_status sdhip_plan_nodes(const sdhip_node *const *nodes, int n_nodes, int index, sdhip_node_plan *plan);
+
+/* Computes node `index` of the graph with the nodes its plan fuses, on the
+ * device, and returns how many nodes that was; 0 when the node is not taken
+ * (the caller computes it), -1 on an error (sdhip_last_error).  Replaces
+ * sdasm_compute_nodes (sdasm.h:41-51, hooks.cc:100-164): as there, the memory
+ * the node (and a redirect or gated output) writes is forgotten by the store
+ * first, taken or not.  `work` is the caller's buffer, of at least
+ * sdhip_node_work_size bytes. */
+int sdhip_compute_nodes(const sdhip_node *const *nodes, int n_nodes, int index, void *work, size_t work_size,
+                        void *stream);
+
+/* Sets *size to the work buffer node needs and returns 1, or returns 0 when
+ * the node is not taken.  Replaces sdasm_work_size (sdasm.h:53-56,
+ * hooks.cc:174-196). */
+int sdhip_node_work_size(const sdhip_node *node, size_t *size);
+
+/* ToDo's step for a grid of width x height tokens: the tuning's todo where it
+ * is 2 or more and the grid has todo_tokens tokens or more, else 1.  Replaces
+ * sdasm_token_downsampling (sdasm.h:61-67, hooks.cc:166-172), which
+ * stable-diffusion.cpp calls to thin its self-attention's keys and values. */
+int sdhip_token_downsampling(int64_t width, int64_t height);
 
 #ifdef __cplusplus
 }

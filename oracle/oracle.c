@@ -49,6 +49,14 @@ float oracle_gelu(float x) {
     return x / (1.0f + oracle_exponential(-1.5957691216057308f * y));
 }
 
+void oracle_exponential_array(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_exponential(x[i]);
+}
+
+void oracle_gelu_array(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_gelu(x[i]);
+}
+
 void oracle_gated_gelu_array(const float *x, const float *gate, float *out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = x[i] * oracle_gelu(gate[i]);
 }

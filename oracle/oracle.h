@@ -36,6 +36,9 @@ float oracle_silu(float x);
 float oracle_gelu(float x);
 /* SiLU of n numbers in place. */
 void oracle_silu_array(float *x, int64_t n);
+/* exponential() and GELU of n numbers, into y. */
+void oracle_exponential_array(const float *x, float *y, int64_t n);
+void oracle_gelu_array(const float *x, float *y, int64_t n);
 /* out = x * GELU(gate) of n numbers (fusion.cc:290-310). */
 void oracle_gated_gelu_array(const float *x, const float *gate, float *out, int64_t n);
 

@@ -6,7 +6,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -48,30 +50,97 @@ Tuning &tuning() {
 
 namespace {
 
+// A tuning name, its field, and the values it takes.  The reference's own
+// names take any integer, as its parser does (cpu.cc:180-212), and clamp or
+// read them as it does (quant.cc:53-67, winograd.cc:1204-1206): kAny.  This
+// library's own names take only the values they are documented with.
+enum Range { kAny, kFlag, kStages, kTiles, kNonNegative, kBits };
+
 struct Field {
     const char *name;
     int Tuning::*member;
+    Range range;
 };
 
 const Field kFields[] = {
-    {"bits", &Tuning::bits},
-    {"input_bits", &Tuning::input_bits},
-    {"group", &Tuning::group},
-    {"weight_group", &Tuning::weight_group},
-    {"quantize", &Tuning::quantize},
-    {"winograd", &Tuning::winograd},
-    {"winograd_positions", &Tuning::winograd_positions},
-    {"winograd4_positions", &Tuning::winograd4_positions},
-    {"winograd_small_tiles", &Tuning::winograd_small_tiles},
-    {"winograd_splits", &Tuning::winograd_splits},
-    {"fuse", &Tuning::fuse},
-    {"winograd_fp32", &Tuning::winograd_fp32},
-    {"gemm_stages", &Tuning::gemm_stages},
-    {"gemm_tiles", &Tuning::gemm_tiles},
-    {"attention_generic", &Tuning::attention_generic},
-    {"attention_fp32", &Tuning::attention_fp32},
-    {"attention_keys", &Tuning::attention_keys},
+    {"bits", &Tuning::bits, kBits},
+    {"input_bits", &Tuning::input_bits, kAny},
+    {"group", &Tuning::group, kAny},
+    {"weight_group", &Tuning::weight_group, kAny},
+    {"quantize", &Tuning::quantize, kAny},
+    {"winograd", &Tuning::winograd, kAny},
+    {"winograd_positions", &Tuning::winograd_positions, kAny},
+    {"winograd4_positions", &Tuning::winograd4_positions, kAny},
+    {"winograd_small_tiles", &Tuning::winograd_small_tiles, kAny},
+    {"fuse", &Tuning::fuse, kAny},
+    {"fuse_residual", &Tuning::fuse_residual, kAny},
+    {"todo", &Tuning::todo, kAny},
+    {"todo_tokens", &Tuning::todo_tokens, kAny},
+    {"attention_keys", &Tuning::attention_keys, kAny},
+    {"store_forget", &Tuning::store_forget, kAny},
+    // The reference's CPU blocking and form names: taken, no effect here.
+    {"conv_kc", &Tuning::conv_kc, kAny},
+    {"conv_mc", &Tuning::conv_mc, kAny},
+    {"conv_nc", &Tuning::conv_nc, kAny},
+    {"conv_rows_outer", &Tuning::conv_rows_outer, kAny},
+    {"conv_shared_columns", &Tuning::conv_shared_columns, kAny},
+    {"conv_columns_bytes", &Tuning::conv_columns_bytes, kAny},
+    {"mul_mat_kc", &Tuning::mul_mat_kc, kAny},
+    {"mul_mat_mc", &Tuning::mul_mat_mc, kAny},
+    {"mul_mat_shared_rows", &Tuning::mul_mat_shared_rows, kAny},
+    {"amx_kc", &Tuning::amx_kc, kAny},
+    {"amx_mc", &Tuning::amx_mc, kAny},
+    {"amx_attention", &Tuning::amx_attention, kAny},
+    {"amx_queries", &Tuning::amx_queries, kAny},
+    {"amx_fp16", &Tuning::amx_fp16, kAny},
+    {"attention_queries", &Tuning::attention_queries, kAny},
+    {"attention_sum_keys", &Tuning::attention_sum_keys, kAny},
+    {"attention_sum_dims", &Tuning::attention_sum_dims, kAny},
+    {"winograd_kc", &Tuning::winograd_kc, kAny},
+    {"winograd_mc", &Tuning::winograd_mc, kAny},
+    {"winograd_tiles", &Tuning::winograd_tiles, kAny},
+    {"winograd_small_mc", &Tuning::winograd_small_mc, kAny},
+    {"winograd_small_kc", &Tuning::winograd_small_kc, kAny},
+    {"prefetch", &Tuning::prefetch, kAny},
+    {"wide", &Tuning::wide, kAny},
+    {"bf16", &Tuning::bf16, kAny},
+    {"guided", &Tuning::guided, kAny},
+    {"half_format", &Tuning::half_format, kAny},
+    // This library's own.
+    {"winograd_splits", &Tuning::winograd_splits, kNonNegative},
+    {"winograd_fp32", &Tuning::winograd_fp32, kFlag},
+    {"gemm_stages", &Tuning::gemm_stages, kStages},
+    {"gemm_tiles", &Tuning::gemm_tiles, kTiles},
+    {"attention_generic", &Tuning::attention_generic, kFlag},
+    {"attention_fp32", &Tuning::attention_fp32, kFlag},
 };
+
+// Whether `v` is a value `r` takes; else the values it does, for the error.
+bool in_range(Range r, long v, const char *&takes) {
+    switch (r) {
+    case kAny:
+        takes = "an int";
+        return v >= INT32_MIN && v <= INT32_MAX;
+    case kFlag:
+        takes = "0 or 1";
+        return v == 0 || v == 1;
+    case kStages:
+        takes = "2 or 4";
+        return v == 2 || v == 4;
+    case kTiles:
+        takes = "0, 11, 21 or 22";
+        return v == 0 || v == 11 || v == 21 || v == 22;
+    case kNonNegative:
+        takes = "0 or more";
+        return v >= 0 && v <= INT32_MAX;
+    case kBits:
+        // 16, the reference's products of 16-bit numbers (gemm.h:226-237), is
+        // a form of its vector units that this library does not have.
+        takes = "an int other than 16 (products of 16-bit numbers are not a form of this library)";
+        return v >= INT32_MIN && v <= INT32_MAX && v != 16;
+    }
+    return false;
+}
 
 }  // namespace
 
@@ -215,6 +284,10 @@ sdhip_status sdhip_set_tuning(const char *text) {
             bool known = false;
             for (const Field &f : kFields) {
                 if (name == f.name) {
+                    const char *takes = "";
+                    if (!in_range(f.range, v, takes)) {
+                        return fail(SDHIP_ERROR, "tuning %s=%ld: %s takes %s", name.c_str(), v, name.c_str(), takes);
+                    }
                     t.*(f.member) = static_cast<int>(v);
                     known = true;
                 }
@@ -236,7 +309,18 @@ int sdhip_get_tuning(const char *name) {
     return -1;
 }
 
-void sdhip_forget(const void *begin, size_t size) { store_forget(begin, size); }
+void sdhip_forget(const void *begin, size_t size) {
+    // store_forget=0 keeps every entry: the store's canary test (store.cc:241-266).
+    if (tuning().store_forget != 0) store_forget(begin, size);
+}
+
+int sdhip_token_downsampling(int64_t width, int64_t height) {
+    // hooks.cc:166-172: every todo-th row and column of a grid of todo_tokens
+    // tokens or more; 1 (none) otherwise.
+    const Tuning &t = tuning();
+    if (t.todo < 2 || width <= 0 || height <= 0 || width * height < t.todo_tokens) return 1;
+    return t.todo;
+}
 
 void sdhip_store_arena(void *arena, size_t bytes) { store_arena(arena, bytes); }
 

@@ -25,7 +25,19 @@ struct Tuning {
     // This library's own: the splits of the input channels of the small
     // images' Winograd products, or 0 to choose by the size.
     int winograd_splits = 0;
-    int fuse = 1;                    // chains fused: 1; the caller computes them apart: 0
+    // The chains after operations: 1 fused into them; 0 apart -- the planner
+    // (graph.cpp) matches none, and an entry point handed one applies it in a
+    // pass of its own after the operation, as ggml's nodes would one by one.
+    int fuse = 1;
+    // The residual connections that end chains (fusion.h:64-80): 1 fused as a
+    // redirect; 0 apart -- the planner matches none, and an entry point handed
+    // one writes its own output and adds the residual in a pass of its own.
+    int fuse_residual = 1;
+    // ToDo (token downsampling, sdasm.h:61-67): attention of an image's tokens
+    // with keys and values from every todo-th row and column of the grid, for
+    // grids of todo_tokens tokens or more; 0 or 1 none.
+    int todo = 0;
+    int todo_tokens = 2048;
     // This library's own: Winograd's products on the single-precision MFMA
     // (1) instead of split FP16 parts (0), for comparison; results agree
     // within the same bound.
@@ -47,6 +59,19 @@ struct Tuning {
     // The keys of a stretch of attention's second product (kernels.h:107):
     // with bits, it sets where the exponentials switch to std::exp.
     int attention_keys = 256;
+    // The reference's names that size its CPU blocks and choose among its CPU
+    // forms (kernels.h:92-120, 124-125, 129): taken so that SDASM_TUNE
+    // strings carry over, held for sdhip_get_tuning, and without effect on
+    // what this library computes or how.
+    int conv_kc = 256, conv_mc = 480, conv_nc = 128, conv_rows_outer = 0, conv_shared_columns = 1024,
+        conv_columns_bytes = 4 << 20, mul_mat_kc = 256, mul_mat_mc = 96, mul_mat_shared_rows = 1024, amx_kc = 256,
+        amx_mc = 128, amx_attention = 0, amx_queries = 64, amx_fp16 = 1, attention_queries = 32,
+        attention_sum_keys = 32, attention_sum_dims = 40, winograd_kc = 256, winograd_mc = 512, winograd_tiles = 64,
+        winograd_small_mc = 48, winograd_small_kc = 128, prefetch = 1, wide = 1, bf16 = 0, guided = 1,
+        half_format = 0;
+    // The store forgets what sdhip_forget names: 1; 0 keeps every entry, only
+    // for the store's canary test (kernels.h:126).
+    int store_forget = 1;
 };
 
 Tuning &tuning();
@@ -65,6 +90,29 @@ int64_t nelements(const sdhip_tensor *t);
 
 sdhip_status device_chain(const sdhip_epilogue *e, const int64_t ne[4], DevChain &c);
 sdhip_status output_of(const sdhip_tensor *y, const sdhip_epilogue *e, float *&out, int32_t &from_redirect);
+
+// How an operation computes the chain it is handed (chain.hip): `fused`, the
+// steps it applies to its tile, into `out` (begun from what out holds if
+// from_redirect); and, with Tuning::fuse = 0 or (for a redirect)
+// fuse_residual = 0, a pass `after` the operation over its own output
+// (apart_in) into apart_out -- the steps it did not apply and, from a
+// redirect, the residual's addition.  With a redirect and no from_redirect,
+// the chain's last step is the residual's addition (fusion.cc:262-271).
+struct ChainRun {
+    DevChain fused;
+    float *out = nullptr;
+    int32_t from_redirect = 0;
+    bool apart = false;
+    DevChain after;
+    const float *apart_in = nullptr;
+    float *apart_out = nullptr;
+    int64_t ne[4] = {0, 0, 0, 0};
+};
+sdhip_status chain_plan(const sdhip_tensor *y, const sdhip_epilogue *e, ChainRun &r);
+sdhip_status chain_after(const ChainRun &r, hipStream_t stream);
+// out[m][j] = p[m][j] GELU(p[m][half + j]), rows of p ldp apart, of out ldo.
+sdhip_status gated_after(const float *p, float *out, int64_t rows, int64_t half, int64_t ldp, int64_t ldo,
+                         hipStream_t stream);
 
 // The device store of derived weights (store.cpp).  store_entry: the entry of
 // `bytes` for the form `layout`/`variant` of the tensor at `begin` (of

@@ -66,6 +66,14 @@ QAttentionArgs qargs_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhi
     return a;
 }
 
+// Whether the quantized form takes these heads and the tuning's group.
+bool quantized_form_takes(const sdhip_tensor *q, const sdhip_tensor *v) {
+    if (q->ne[0] > 256 || v->ne[0] > 256) return false;
+    int quads = tuning().group / 4;
+    quads = quads < 1 ? 1 : (quads > 256 ? 256 : quads);
+    return (4 * quads) % 16 == 0 && 4 * quads <= 256;
+}
+
 // The launch's description of the operands (ggml's ne and nb, in elements).
 AttentionArgs args_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v, const sdhip_tensor *y,
                       float scale) {
@@ -113,11 +121,17 @@ int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, cons
     const bool shapes = q->ne[0] == k->ne[0] && k->ne[1] == v->ne[1] && k->ne[2] == v->ne[2] && k->ne[2] > 0 &&
                         q->ne[2] % k->ne[2] == 0 && q->ne[3] == k->ne[3] && q->ne[3] == v->ne[3] && k->ne[1] >= 1 &&
                         y->ne[0] == v->ne[0] && y->ne[1] == q->ne[2] && y->ne[2] == q->ne[1] && y->ne[3] == q->ne[3];
-    return max_bias == 0.0f && softcap == 0.0f && holds_f32(q) && kv_type(k) && kv_type(v) && holds_f32(y) &&
-           contiguous(y) && shapes && q->ne[0] <= kAttentionMaxDims && v->ne[0] <= kAttentionMaxDims &&
-           q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 && q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 &&
-           k->nb[2] % k->nb[0] == 0 && k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 &&
-           v->nb[2] % v->nb[0] == 0 && v->nb[3] % v->nb[0] == 0;
+    const bool taken = max_bias == 0.0f && softcap == 0.0f && holds_f32(q) && kv_type(k) && kv_type(v) &&
+                       holds_f32(y) && contiguous(y) && shapes && q->ne[0] <= kAttentionMaxDims &&
+                       v->ne[0] <= kAttentionMaxDims && q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 &&
+                       q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 && k->nb[2] % k->nb[0] == 0 &&
+                       k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 && v->nb[2] % v->nb[0] == 0 &&
+                       v->nb[3] % v->nb[0] == 0;
+    if (!taken) return 0;
+    // In the bits mode the quantized form takes heads of up to 256
+    // dimensions and groups of keys that are a multiple of 16 up to 256; the
+    // rest is left to the caller, as not taken.
+    return !quantized_attention(k) || quantized_form_takes(q, v);
 }
 
 size_t sdhip_attention_work_size(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,

@@ -44,8 +44,18 @@ int64_t out_size(int64_t in, int64_t k, int32_t s, int32_t p, int32_t d) {
     return (in + 2 * p - d * (k - 1) - 1) / s + 1;
 }
 
+// Whether bits asks for the convolutions' products quantized (quantized(
+// Quantized_op::convolution), quant.cc:53-56): a form this library does not
+// have, so such convolutions are not taken -- the caller's own form computes
+// them, as ggml computes what the reference does not take.
+bool conv_quantized() {
+    const Tuning &t = tuning();
+    return t.bits >= 2 && t.bits <= 8 && (t.quantize & 2) != 0;
+}
+
 bool direct_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
     if (kernel == nullptr || input == nullptr || y == nullptr || op == nullptr) return false;
+    if (conv_quantized()) return false;
     // FP16 kernels only: single-precision ones are left to the caller.
     const bool weights = holds_f16(kernel) && contiguous(kernel);
     if (!(weights && holds_f32(input) && holds_f32(y) && contiguous(y) && kernel->ne[2] == input->ne[2] &&
@@ -184,37 +194,36 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
     if (path < 0) {
         return fail(SDHIP_UNSUPPORTED, "conv2d: operands not taken");
     }
-    DevChain dc;
-    sdhip_status s = device_chain(chain, y->ne, dc);
-    if (s != SDHIP_OK) return s;
-    float *out = nullptr;
-    int32_t from_redirect = 0;
-    s = output_of(y, chain, out, from_redirect);
+    ChainRun run;
+    sdhip_status s = chain_plan(y, chain, run);
     if (s != SDHIP_OK) return s;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (path == 2 || path == 4) {
         WinogradArgs a = winograd_args(kernel, input, y, op_params, path);
-        a.y = out;
-        a.from_redirect = from_redirect;
-        a.chain = dc;
+        a.y = run.out;
+        a.from_redirect = run.from_redirect;
+        a.chain = run.fused;
         const size_t need = winograd_work_size(a);
         if (work == nullptr || work_size < need) {
             return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
         }
-        return winograd(a, work, st);
+        s = winograd(a, work, st);
+        return s == SDHIP_OK ? chain_after(run, st) : s;
     }
     ConvArgs c = conv_args(kernel, input, y, op_params);
-    c.y = out;
-    c.from_redirect = from_redirect;
-    c.chain = dc;
+    c.y = run.out;
+    c.from_redirect = run.from_redirect;
+    c.chain = run.fused;
     if (conv_columns_taken(c)) {
         const size_t need = conv_columns_work_size(c);
         if (work == nullptr || work_size < need) {
             return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
         }
-        return launched(launch_conv_columns(c, work, gemm_shape(), st), "conv2d by columns");
+        s = launched(launch_conv_columns(c, work, gemm_shape(), st), "conv2d by columns");
+    } else {
+        s = launched(launch_conv_direct(c, gemm_shape(), st), "conv2d direct");
     }
-    return launched(launch_conv_direct(c, gemm_shape(), st), "conv2d direct");
+    return s == SDHIP_OK ? chain_after(run, st) : s;
 }
 
 }  // extern "C"

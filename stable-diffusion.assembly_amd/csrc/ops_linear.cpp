@@ -89,26 +89,29 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
         return fail(SDHIP_UNSUPPORTED, "mul_mat: operands not taken");
     }
     MulMatArgs a = args_of(w, x, y);
-    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    ChainRun run;
+    sdhip_status s = chain_plan(y, chain, run);
     if (s != SDHIP_OK) return s;
-    s = output_of(y, chain, a.y, a.from_redirect);
-    if (s != SDHIP_OK) return s;
+    a.chain = run.fused;
+    a.y = run.out;
+    a.from_redirect = run.from_redirect;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (mul_mat_quantized(x)) {
         const size_t need = quantized_linear_work_size(a.K, a.N, a.M);
         if (work == nullptr || work_size < need) {
             return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
         }
-        return quantized_linear(a, false, work, st);
-    }
-    if (mul_mat_split_taken(a)) {
+        s = quantized_linear(a, false, work, st);
+    } else if (mul_mat_split_taken(a)) {
         const size_t need = mul_mat_split_work_size(a);
         if (work == nullptr || work_size < need) {
             return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
         }
-        return launched(launch_mul_mat_split(a, work, gemm_shape(), st), "mul_mat split along K");
+        s = launched(launch_mul_mat_split(a, work, gemm_shape(), st), "mul_mat split along K");
+    } else {
+        s = launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
     }
-    return launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
+    return s == SDHIP_OK ? chain_after(run, st) : s;
 }
 
 int sdhip_mul_mat_gated_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
@@ -136,6 +139,15 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
     }
     if (chain != nullptr && chain->redirect != nullptr) {
         return fail(SDHIP_UNSUPPORTED, "mul_mat_gated: a chain with a residual redirect is not gated");
+    }
+    if (tuning().fuse == 0) {
+        // The gated GELU apart, as ggml's nodes compute it when nothing is
+        // fused: the product and its chain into y, then out from y's halves.
+        sdhip_status s = sdhip_mul_mat(w, x, y, chain, work, work_size, stream);
+        if (s != SDHIP_OK) return s;
+        return gated_after(static_cast<const float *>(y->data), static_cast<float *>(out->data),
+                           x->ne[1] * x->ne[2] * x->ne[3], y->ne[0] / 2, y->nb[1] / 4, out->nb[1] / 4,
+                           static_cast<hipStream_t>(stream));
     }
     MulMatArgs a = args_of(w, x, y);
     sdhip_status s = device_chain(chain, y->ne, a.chain);

@@ -31,8 +31,10 @@ sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int 
         return fail(SDHIP_UNSUPPORTED, "group_norm: no residual redirect after a normalisation");
     }
     GroupNormArgs a{};
-    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    ChainRun run;
+    sdhip_status s = chain_plan(y, chain, run);
     if (s != SDHIP_OK) return s;
+    a.chain = run.fused;
     a.x = static_cast<const float *>(x->data);
     a.y = static_cast<float *>(y->data);
     a.ne0 = x->ne[0];
@@ -56,7 +58,8 @@ sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int 
     a.chunk = shape.chunk;
     a.slices = shape.slices;
     a.partials = static_cast<double *>(work);
-    return launched(launch_group_norm(a, static_cast<hipStream_t>(stream)), "group_norm");
+    s = launched(launch_group_norm(a, static_cast<hipStream_t>(stream)), "group_norm");
+    return s == SDHIP_OK ? chain_after(run, static_cast<hipStream_t>(stream)) : s;
 }
 
 int sdhip_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y) {
@@ -74,8 +77,10 @@ sdhip_status sdhip_norm(const sdhip_tensor *x, const sdhip_tensor *y, float eps,
         return fail(SDHIP_UNSUPPORTED, "norm: no residual redirect after a normalisation");
     }
     NormArgs a{};
-    sdhip_status s = device_chain(chain, y->ne, a.chain);
+    ChainRun run;
+    sdhip_status s = chain_plan(y, chain, run);
     if (s != SDHIP_OK) return s;
+    a.chain = run.fused;
     a.x = static_cast<const float *>(x->data);
     a.y = static_cast<float *>(y->data);
     a.ne0 = x->ne[0];
@@ -89,7 +94,8 @@ sdhip_status sdhip_norm(const sdhip_tensor *x, const sdhip_tensor *y, float eps,
     a.ynb2 = y->nb[2] / 4;
     a.ynb3 = y->nb[3] / 4;
     a.eps = eps;
-    return launched(launch_norm(a, static_cast<hipStream_t>(stream)), "norm");
+    s = launched(launch_norm(a, static_cast<hipStream_t>(stream)), "norm");
+    return s == SDHIP_OK ? chain_after(run, static_cast<hipStream_t>(stream)) : s;
 }
 
 }  // extern "C"

@@ -445,6 +445,8 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
         KernelScope scope("quantize_weights", stream);
         hipLaunchKernelGGL(quantize_weights_kernel, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w, a.ldw, a.N,
                            a.K, q, l, wq, ws, wo, wsum);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return launched(err, "quantize_weights");
         if (kept != nullptr) store_publish(kept);
     }
     QgemmArgs p{};

@@ -101,15 +101,18 @@ void *store_entry(const void *begin, int32_t type, const int64_t ne[4], const in
     std::memcpy(k.nb, nb, sizeof(k.nb));
     k.layout = layout;
     k.variant = variant;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    const bool capturing =
+        hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
     const auto it = s.entries.find(k);
     if (it != s.entries.end()) {
+        // An entry not yet filled is filled by an eager call only: a captured
+        // call would publish it before the graph that fills it has run.
+        if (!it->second.ready && capturing) return nullptr;
         ready = it->second.ready;
         return s.arena + it->second.offset;
     }
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) {
-        return nullptr;
-    }
+    if (capturing) return nullptr;
     const size_t at = first_fit(s, bytes);
     if (at == SIZE_MAX) return nullptr;  // past the budget: the call derives into its work buffer
     s.blocks.emplace(at, bytes);

@@ -43,6 +43,34 @@ class Epilogue(ctypes.Structure):
     ]
 
 
+MAX_SRC = 10
+MAX_OP_PARAMS = 16
+
+
+class Node(ctypes.Structure):
+    """sdhip_node: a node of a ggml graph as the planner reads it."""
+
+
+Node._fields_ = [
+    ("op", ctypes.c_int32),
+    ("unary", ctypes.c_int32),
+    ("flags", ctypes.c_int32),
+    ("op_params", ctypes.c_int32 * MAX_OP_PARAMS),
+    ("tensor", Tensor),
+    ("src", ctypes.POINTER(Node) * MAX_SRC),
+    ("view_src", ctypes.POINTER(Node)),
+]
+
+
+class NodePlan(ctypes.Structure):
+    _fields_ = [
+        ("taken", ctypes.c_int32),
+        ("count", ctypes.c_int32),
+        ("chain", Epilogue),
+        ("gated_out", ctypes.POINTER(Node)),
+    ]
+
+
 _T = ctypes.POINTER(Tensor)
 _E = ctypes.POINTER(Epilogue)
 _P = ctypes.c_void_p
@@ -81,6 +109,12 @@ SIGNATURES = [
     ("sdhip_group_norm", ctypes.c_int, [_T, _T, ctypes.c_int, ctypes.c_float, _E, _P, _SZ, _P]),
     ("sdhip_norm_supported", ctypes.c_int, [_T, _T]),
     ("sdhip_norm", ctypes.c_int, [_T, _T, ctypes.c_float, _E, _P]),
+    ("sdhip_plan_nodes", ctypes.c_int,
+     [ctypes.POINTER(ctypes.POINTER(Node)), ctypes.c_int, ctypes.c_int, ctypes.POINTER(NodePlan)]),
+    ("sdhip_compute_nodes", ctypes.c_int,
+     [ctypes.POINTER(ctypes.POINTER(Node)), ctypes.c_int, ctypes.c_int, _P, _SZ, _P]),
+    ("sdhip_node_work_size", ctypes.c_int, [ctypes.POINTER(Node), ctypes.POINTER(_SZ)]),
+    ("sdhip_token_downsampling", ctypes.c_int, [ctypes.c_int64, ctypes.c_int64]),
 ]
 
 _lib = None

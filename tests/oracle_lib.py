@@ -38,6 +38,9 @@ def lib():
         L.oracle_gelu.restype = _F
         L.oracle_gelu.argtypes = [_F]
         L.oracle_silu_array.argtypes = [_f, _L]
+        L.oracle_exponential_array.argtypes = [_f, _f, _L]
+        L.oracle_gelu_array.argtypes = [_f, _f, _L]
+        L.oracle_port_mul_mat.argtypes = [_f, _f, ctypes.c_void_p, _L, _L, _L, _f, _I]
         L.oracle_gated_gelu_array.argtypes = [_f, _f, _f, _L]
         L.oracle_exact_mul_mat.argtypes = [_f, _L, _f, _L, _L, _L, _L, _d, _d]
         L.oracle_exact_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L, _d, _d]
@@ -55,6 +58,63 @@ def lib():
         L.oracle_quantized_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _L, _I, _I, _L, _f]
         _lib = L
     return _lib
+
+
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref_scalar_math.so")
+_ref = None
+
+
+def ref_lib():
+    """The reference's own sources/scalar_math.h, compiled unmodified by
+    oracle/ref.mk into oracle/_ref; None where it was not built (the
+    reference checkout is absent)."""
+    global _ref
+    if _ref is None and os.path.exists(REF_SO):
+        L = ctypes.CDLL(REF_SO)
+        for name in ("ref_exponential", "ref_silu", "ref_gelu"):
+            getattr(L, name).restype = _F
+            getattr(L, name).argtypes = [_F]
+        for name in ("ref_exponential_array", "ref_silu_array", "ref_gelu_array"):
+            getattr(L, name).argtypes = [_f, _f, _L]
+        _ref = L
+    return _ref
+
+
+def ref_array(name, x):
+    """The reference's exponential / silu / gelu of each number of x."""
+    x = c32(x)
+    out = np.empty_like(x)
+    getattr(ref_lib(), f"ref_{name}_array")(x, out, x.size)
+    return out
+
+
+def exponential(x):
+    x = c32(x)
+    out = np.empty_like(x)
+    lib().oracle_exponential_array(x, out, x.size)
+    return out
+
+
+def gelu(x):
+    x = c32(x)
+    out = np.empty_like(x)
+    lib().oracle_gelu_array(x, out, x.size)
+    return out
+
+
+def port_mul_mat(w, x, bias=None, threads=1):
+    """port.c's packed single-precision GEMM (the CPU baseline of MUL_MAT):
+    w [N, K], x [M, K] -> y [M, N] = x w^T (+ bias)."""
+    w, x = c32(w), c32(x)
+    N, K = w.shape
+    M = x.shape[0]
+    y = np.empty((M, N), np.float32)
+    bp = None
+    if bias is not None:
+        bias = c32(bias)
+        bp = bias.ctypes.data_as(ctypes.c_void_p)
+    lib().oracle_port_mul_mat(w, x, bp, M, N, K, y, threads)
+    return y
 
 
 def c32(a):

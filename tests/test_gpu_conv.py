@@ -250,18 +250,20 @@ def test_winograd_graph_replays(gpu, c):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("c", [
-    (40, 36, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2),   # Winograd F(4x4), transforms of the large path
-    (15, 9, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2),    # small images, F(2x2)
-    (16, 16, 72, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1),   # small images, F(4x4)
-    (33, 33, 24, 30, 3, 3, 2, 2, 1, 1, 1, 1, 1),   # direct by columns
-    (32, 32, 64, 40, 1, 1, 1, 1, 0, 0, 1, 1, 2),   # 1x1
-], ids=lambda c: "x".join(map(str, c)))
-def test_conv2d_strided_input(gpu, c):
+@pytest.mark.parametrize("c,want_path,small_path", [
+    ((40, 36, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 2), 4, False),  # Winograd F(4x4), transforms of the large path
+    ((15, 9, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), 2, False),   # F(2x2), 80 tiles: the large path
+    ((8, 8, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), 2, True),     # small images, F(2x2): 32 tiles
+    ((16, 16, 72, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1), 4, True),   # small images, F(4x4)
+    ((33, 33, 24, 30, 3, 3, 2, 2, 1, 1, 1, 1, 1), 0, False),  # direct by columns
+    ((32, 32, 64, 40, 1, 1, 1, 1, 0, 0, 1, 1, 2), 0, False),  # 1x1
+], ids=lambda c: "x".join(map(str, c)) if isinstance(c, tuple) else str(c))
+def test_conv2d_strided_input(gpu, c, want_path, small_path):
     """The input as a view into a larger tensor: rows, planes and images
     further apart than their extents, and a start that is no multiple of 16
     bytes -- ggml's nb[1..3] of a view (the predicate takes any multiple of 4
-    bytes, conv2d.cc:320-331)."""
+    bytes, conv2d.cc:320-331).  The path and, for Winograd, whether the small
+    images' kernels ran (no transforms launch) are checked from the profile."""
     w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
     r = rng(sum(c) + 11)
     kh16, k32 = weights_f16(r, (oc, ic, kh, kw))
@@ -275,8 +277,21 @@ def test_conv2d_strided_input(gpu, c):
     y_d = unwritten((n, oc, oh, ow), gpu)
     params = sdhip.conv_params(s0, s1, p0, p1, d0, d1)
     path = sdhip.conv2d_path(k_d, x_d, y_d, params)
-    sdhip.conv2d(k_d, x_d, y_d, params)
-    torch.cuda.synchronize()
+    assert path == want_path
+    sdhip.profile_reset()
+    sdhip.profile_enable(True)
+    try:
+        sdhip.conv2d(k_d, x_d, y_d, params)
+        torch.cuda.synchronize()
+        ran = sdhip.profile_collect()
+    finally:
+        sdhip.profile_enable(False)
+        sdhip.profile_reset()
+    if path in (2, 4):
+        tag = f"winograd{path}"
+        assert f"{tag}.products" in ran
+        large = f"{tag}.transforms" in ran or f"{tag}.weights" in ran
+        assert large != small_path, sorted(ran)
     exact, mag = orc.exact_conv2d(x, k32, s0, s1, p0, p1, d0, d1)
     err = orc.metric(y_d.cpu().numpy(), exact, mag)
     print(f"strided input {c} path {path}: {err:.3g}")

@@ -137,3 +137,52 @@ def test_quantized_gated(gpu, K, half, M, tuning):
     print(f"quantized gated {K}->2x{half} x {M} [{tuning}]: error {err:.3g}, bit-exact: {same}")
     assert same
     assert err <= bound(levels, wmax)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("from_redirect", [False, True])
+def test_sdxl_ff_out_with_residual(gpu, from_redirect):
+    """configs[4]'s FF-out product at full size: 5120 -> 1280 over 988 x 2
+    tokens, bits=8 with a scale per whole row of weights (weight_group=0),
+    its bias, and the block's residual connection ending the chain -- as a
+    redirect with the residual's addition as its last step, or begun from the
+    residual already in the output's memory (fusion.h:64-80).  Bit for bit
+    with the oracle at a sample of rows (each row's quantization and sums
+    depend on that row alone), and every row within the reference's bound."""
+    K, N, M, B = 5120, 1280, 988, 2
+    r = rng(5120)
+    wh, w32 = weights_f16(r, (N, K), 0.02 * 1.7)
+    x = uniform(r, (B, M, K), 1.0)
+    b = uniform(r, (N,), 0.01)
+    res = uniform(r, (B, M, N), 1.0)
+    w_d, x_d, b_d, res_d = dev(wh, gpu), dev(x, gpu), dev(b, gpu), dev(res, gpu)
+    y = unwritten((B, M, N), gpu)
+    if from_redirect:
+        out = res_d.clone()
+        chain = sdhip.epilogue([("add", b_d)], redirect=out, from_redirect=True)
+    else:
+        out = unwritten((B, M, N), gpu)
+        chain = sdhip.epilogue([("add", b_d), ("add", res_d)], redirect=out)
+    sdhip.set_tuning("bits=8,weight_group=0")
+    try:
+        sdhip.mul_mat(w_d, x_d, y, chain)
+        torch.cuda.synchronize()
+    finally:
+        sdhip.set_tuning("")
+    got = out.cpu().numpy().reshape(B * M, N)
+    assert torch.isnan(y).all(), "the product's own tensor is not written under a redirect"
+    xs = x.reshape(B * M, K)
+    rows = np.unique(np.concatenate([np.arange(0, 8), rng(7).integers(0, B * M, 56), [B * M - 1]]))
+    rs = res.reshape(B * M, N)[rows]
+    if from_redirect:
+        want = orc.quantized_mul_mat(w32, xs[rows], 64, 255, 127, 0, init=rs)[0]
+        want = (want + b).astype(np.float32)
+    else:
+        want = orc.quantized_mul_mat(w32, xs[rows], 64, 255, 127, 0)[0]
+        want = ((want + b).astype(np.float32) + rs).astype(np.float32)
+    same = np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
+    print(f"FF-out 5120->1280 x {B * M} (from_redirect={from_redirect}): {rows.size} rows bit-exact: {same}")
+    assert same, f"{np.sum(got[rows] != want)} of {want.size} differ"
+    exact, mag = orc.exact_mul_mat(w32, xs[rows])
+    add = b.astype(np.float64) + rs
+    assert orc.metric(got[rows], exact + add, mag + np.abs(add)) <= bound(255, 127)

@@ -54,6 +54,35 @@ def test_tuning_parses_like_sdasm_tune():
         assert sdhip.get_tuning(name) == value
 
 
+def test_tuning_takes_every_reference_name_and_checks_its_own():
+    """Every name of the reference's Tuning (kernels.h:91-135) is taken with
+    its default, so that SDASM_TUNE strings carry over; this library's own
+    names take only their documented values; bits=16 is refused."""
+    ref = {"conv_kc": 256, "conv_mc": 480, "conv_nc": 128, "conv_rows_outer": 0, "conv_shared_columns": 1024,
+           "conv_columns_bytes": 4 << 20, "mul_mat_kc": 256, "mul_mat_mc": 96, "mul_mat_shared_rows": 1024,
+           "amx_kc": 256, "amx_mc": 128, "amx_attention": 0, "amx_queries": 64, "amx_fp16": 1,
+           "attention_queries": 32, "attention_keys": 256, "attention_sum_keys": 32, "attention_sum_dims": 40,
+           "winograd": 2, "winograd_positions": 1024, "winograd4_positions": 256, "winograd_kc": 256,
+           "winograd_mc": 512, "winograd_tiles": 64, "winograd_small_tiles": 256, "winograd_small_mc": 48,
+           "winograd_small_kc": 128, "prefetch": 1, "wide": 1, "bf16": 0, "fuse": 1, "fuse_residual": 1,
+           "guided": 1, "store_forget": 1, "bits": 0, "input_bits": 8, "group": 64, "weight_group": 1,
+           "quantize": 7, "half_format": 0, "todo": 0, "todo_tokens": 2048}
+    sdhip.set_tuning("")
+    for name, value in ref.items():
+        assert sdhip.get_tuning(name) == value, name
+    try:
+        sdhip.set_tuning("conv_kc=128,amx_fp16=0,fuse_residual=0,todo=2,todo_tokens=100,group=1000,bits=3")
+        assert sdhip.get_tuning("conv_kc") == 128 and sdhip.get_tuning("todo_tokens") == 100
+        for bad in ("gemm_stages=3", "gemm_tiles=12", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
+                    "winograd_splits=-2", "bits=16", "fuse=99999999999"):
+            with pytest.raises(sdhip.SdhipError):
+                sdhip.set_tuning(bad)
+        for good in ("gemm_stages=4", "gemm_tiles=21", "winograd_fp32=1", "winograd_splits=3", "bits=8"):
+            sdhip.set_tuning(good)
+    finally:
+        sdhip.set_tuning("")
+
+
 FAKE = 1 << 20  # a data pointer the predicates never dereference
 
 

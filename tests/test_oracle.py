@@ -33,6 +33,39 @@ def test_exponential_against_exp():
     assert L.oracle_exponential(0.0) == 1.0
 
 
+def scalar_sweep():
+    """A dense sweep of single-precision arguments: every 61st bit pattern of
+    [0, 88.73] with both signs, the clamp edges and their neighbours, points
+    past them, and the integers and half-integers of the range."""
+    top = np.float32(88.73).view(np.uint32)
+    pos = np.arange(0, int(top) + 1, 61, dtype=np.uint32).view(np.float32)
+    edges = np.float32([-87.3, 88.73, -87.29999, 88.72999, -87.30001, 88.73001, -88.0, 89.0, -100.0, 100.0,
+                        -1e30, 1e30, 0.0, -0.0, 1e-38, -1e-38, 1e-45, -1e-45])
+    near = np.concatenate([np.nextafter(edges, np.float32(np.inf)), np.nextafter(edges, np.float32(-np.inf))])
+    grid = np.arange(-180, 181, dtype=np.float32) * np.float32(0.5)
+    return np.concatenate([pos, -pos, edges, near, grid]).astype(np.float32)
+
+
+@pytest.mark.skipif(orc.ref_lib() is None, reason="oracle/_ref not built: the reference checkout is absent")
+@pytest.mark.parametrize("name", ["exponential", "silu", "gelu"])
+def test_scalar_math_bit_identical_to_the_reference(name):
+    """oracle.c's exponential, SiLU and GELU against the reference's own
+    sources/scalar_math.h compiled unmodified (oracle/ref.mk): the same bits
+    at every argument of a dense sweep, the clamp edges included.  A changed
+    low-order digit of a Cephes coefficient, a dropped reduction step or a
+    wrong clamp shows here even where it stays within an ulp of exp."""
+    xs = scalar_sweep()
+    if name == "silu":
+        got = orc.silu(xs)
+    elif name == "gelu":
+        got = orc.gelu(xs)
+    else:
+        got = orc.exponential(xs)
+    want = orc.ref_array(name, xs)
+    bad = got.view(np.uint32) != want.view(np.uint32)
+    assert not bad.any(), f"{bad.sum()} of {xs.size} differ, first at x = {xs[bad][:5]}"
+
+
 def test_silu_and_gelu_closed_forms():
     L = orc.lib()
     for x in np.linspace(-10, 10, 401, dtype=np.float32):
@@ -230,6 +263,51 @@ def test_input_quantization_invariants(levels):
         assert np.all(np.abs(recon - x) <= 0.5 * s * (1 + 1e-5) + 1e-7)
 
 
+@pytest.mark.parametrize("levels", [255, 127])
+def test_input_quantization_rounds_ties_to_even(levels):
+    """quant.cc:282-315 rounds x / s with rint, to the nearest and ties to
+    even.  Inputs from 0 up to levels / 128 give the scale 1/128 exactly (a
+    power of two) and the zero point 0, so that x = (k + 1/2) / 128 makes
+    x inv = k + 1/2 exactly: each such input must land on the even one of k
+    and k + 1 -- rounding half away from zero (roundf) lands on k + 1 half of
+    the time, truncation on k."""
+    step = np.float32(1.0 / 128)
+    k = np.arange(0, 62, dtype=np.float32)
+    x = np.concatenate([np.float32([0.0, levels / 128.0]), (k + np.float32(0.5)) * step]).astype(np.float32)
+    q, s, o = orc.quantize_input_row(x, 64, levels)
+    assert s == step and o == 0.0 and q[0] == 0 and q[1] == levels
+    want = 2 * np.floor((k + 0.5) / 2 + 0.25).astype(np.int64)  # the even neighbour of k + 1/2
+    assert np.array_equal(q[2:2 + k.size].astype(np.int64), want)
+    # With a zero point: the range [-z/128, (levels - z)/128] puts z at
+    # rint(z) = z, and the ties stay ties after adding it.
+    z = 37
+    xz = np.concatenate([np.float32([-z / 128.0, (levels - z) / 128.0]),
+                         (np.arange(-30, 30, dtype=np.float32) + np.float32(0.5)) * step]).astype(np.float32)
+    qz, sz, oz = orc.quantize_input_row(xz, 64, levels)
+    assert sz == step and qz[0] == 0 and qz[1] == levels
+    t = np.arange(-30, 30) + 0.5
+    assert np.array_equal(qz[2:62].astype(np.int64) - z, 2 * np.floor(t / 2 + 0.25).astype(np.int64))
+
+
+def test_weight_quantization_rounds_ties_to_even():
+    """quant.cc:186-243 rounds w / s with rint.  A group whose greatest
+    magnitude is 127/64 has the scale 1/64 exactly, so that w = (k + 1/2) / 64
+    makes w inv = k + 1/2: ties to even, both signs."""
+    k = np.arange(-60, 60, dtype=np.float32)
+    w = np.zeros((1, 128), np.float32)
+    w[0, 0] = 127.0 / 64
+    w[0, 1:1 + 60] = (k[:60] + np.float32(0.5)) / 64
+    w[0, 64] = -127.0 / 64
+    w[0, 65:125] = (k[60:] + np.float32(0.5)) / 64
+    q, sc, of, su = orc.quantize_weights(w, 64, 127, 1)
+    assert sc[0, 0] == np.float32(1.0 / 64) and sc[0, 1] == np.float32(1.0 / 64)
+    t = k + 0.5
+    want = 2 * np.floor(t / 2 + 0.25).astype(np.int64)
+    got = np.concatenate([q[0, 1:61], q[0, 65:125]]).astype(np.int64)
+    assert np.array_equal(got, want)
+    assert q[0, 0] == 127 and q[0, 64] == -127
+
+
 @pytest.mark.parametrize("weight_groups", [1, 0])
 def test_weight_quantization_invariants(weight_groups):
     """quant.cc:186-243: |q| <= wmax, the greatest magnitude of the group (or
@@ -275,6 +353,24 @@ def test_quantized_product_against_its_own_integers_and_float64():
     init = uniform(r, (M, N), 1.0)
     y2 = orc.quantized_mul_mat(w, x, init=init)[0]
     assert np.allclose(y2, y + init, atol=1e-5)
+
+
+def test_port_mul_mat_within_the_reference_bound():
+    """port.c's single-precision GEMM (the CPU baseline of MUL_MAT) against
+    float64: the reference's 2e-5 bound with its bias, at a ragged shape and
+    at threads 1 and 3 alike; a transposed operand or a dropped bias fails."""
+    r = rng(21)
+    N, K, M = 37, 150, 43
+    w = uniform(r, (N, K), 0.25).astype(np.float16).astype(np.float32)
+    x = uniform(r, (M, K), 1.0)
+    b = uniform(r, (N,), 1.0)
+    exact, mag = orc.exact_mul_mat(w, x)
+    y1 = orc.port_mul_mat(w, x, b, threads=1)
+    y3 = orc.port_mul_mat(w, x, b, threads=3)
+    assert orc.metric(y1, exact + b, mag + np.abs(b)) <= 2e-5
+    assert np.array_equal(y1, y3)
+    y0 = orc.port_mul_mat(w, x, None, threads=2)
+    assert orc.metric(y0, exact, mag) <= 2e-5
 
 
 # ------------------------------------------------------------------ quantized attention
