@@ -32,7 +32,10 @@ def exact_split(x):
     s = x * np.float32(0.0625)
     hi = s.astype(np.float16).astype(np.float32)
     lo = (s - hi).astype(np.float16).astype(np.float32)
-    ok = (hi.astype(np.float64) + lo.astype(np.float64) == s.astype(np.float64))
+    # The parts give back x itself (not a flushed x 2^-4), and x is no -0:
+    # the product's sum of +0 and -0 terms is +0 whatever x's sign.
+    ok = (hi.astype(np.float64) + lo.astype(np.float64)) * 16.0 == x.astype(np.float64)
+    ok &= ~((x == 0) & np.signbit(x))
     ok &= (lo == 0) | (np.abs(lo) >= 2.0 ** -14)
     ok &= (hi == 0) | (np.abs(hi) >= 2.0 ** -14)
     return x[ok]
