@@ -226,6 +226,19 @@ size_t sdhip_group_norm_work_size(const sdhip_tensor *x, const sdhip_tensor *y, 
 sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
                               const sdhip_epilogue *chain, void *work, size_t work_size, void *stream);
 
+/* sdhip_group_norm without a work buffer, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): no counterpart in the reference, whose GROUP_NORM
+ * takes no work buffer (sdasm_work_size reports none for it, hooks.cc:188-191).
+ * The partial sums go to a static scratch of 1 MiB in the library's device
+ * code, one copy per GPU, held until the process ends: shapes whose sums need
+ * more (sdhip_group_norm_work_size > 1 MiB) are SDHIP_ERROR.  Allocates
+ * nothing, on the current device; the scratch keeps the last call's sums and
+ * every call on one GPU shares it, so calls that overlap on one GPU (two
+ * streams, or two threads) race.  Results are those of sdhip_group_norm. */
+sdhip_status sdhip_group_norm_static(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
+                                     const sdhip_epilogue *chain, void *stream);
+
 /* GGML_OP_NORM over ne[0] (norm.cc:148-175), then the chain.  Replaces
  * norm_supported / norm_compute (ops.h:62-63). */
 int sdhip_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y);

@@ -15,6 +15,7 @@
 
 #include "host.h"
 #include "kernels.h"
+#include "norm.h"
 
 namespace sdhip {
 
@@ -254,7 +255,9 @@ sdhip_status sdhip_init(int device) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         return fail(SDHIP_ERROR, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
     }
-    return SDHIP_OK;
+    // The address of the static scratch on this device (sdhip_group_norm_static).
+    double *scratch_ptr = nullptr;
+    return static_scratch(device, scratch_ptr);
 }
 
 const char *sdhip_last_error(void) { return g_error.c_str(); }

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/sdhip.h"
 #include "device.h"
 
 namespace sdhip {
@@ -38,6 +39,11 @@ struct NormArgs {
 };
 
 hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream);
+
+// The static scratch of sdhip_group_norm_static (norm.hip): its bytes, and
+// its address on `device`, which must be current (looked up once per device).
+constexpr size_t kStaticScratchBytes = size_t(1) << 20;
+sdhip_status static_scratch(int device, double *&ptr);
 hipError_t launch_norm(const NormArgs &a, hipStream_t stream);
 
 }  // namespace sdhip

@@ -6,6 +6,8 @@
 // (x - mean) * scale and then the chain (norm.cc:44-175).  Only the order of
 // the double-precision sums differs from the reference's eight lanes.
 
+#include <mutex>
+
 #include "host.h"
 #include "norm.h"
 #include "profile.h"
@@ -48,14 +50,14 @@ __device__ __forceinline__ GroupView group_view(const GroupNormArgs &a) {
     return v;
 }
 
-__device__ __forceinline__ double block_sum(double v, double *scratch) {
+__device__ __forceinline__ double block_sum(double v, double *lds_sums) {
     v = wave_sum(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) lds_sums[threadIdx.x >> 6] = v;
     __syncthreads();
     double s = 0.0;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s += scratch[w];
+    for (int w = 0; w < kThreads / 64; ++w) s += lds_sums[w];
     return s;
 }
 
@@ -77,7 +79,7 @@ __device__ __forceinline__ double term(float x, float mean) {
 
 template <int PASS>
 __global__ __launch_bounds__(kThreads) void group_sums_kernel(GroupNormArgs a) {
-    __shared__ double scratch[kThreads / 64];
+    __shared__ double lds_sums[kThreads / 64];
     __shared__ float shared_mean;
     const GroupView g = group_view(a);
     const int tid = threadIdx.x;
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void group_sums_kernel(GroupNormArgs a) {
     } else {
         for (int64_t e = g.e0 + tid; e < g.e1; e += kThreads) s0 += term<PASS>(x[e], mean);
     }
-    const double sum = block_sum((s0 + s1) + (s2 + s3), scratch);
+    const double sum = block_sum((s0 + s1) + (s2 + s3), lds_sums);
     if (tid == 0) a.partials[(PASS * a.ne3 * a.groups + g.item) * a.slices + g.slice] = sum;
 }
 
@@ -211,19 +213,19 @@ constexpr int kResidentThreads = 1024;
 constexpr int kResidentQuads = 4;  // float4 a thread
 constexpr int64_t kResident = int64_t(kResidentThreads) * 4 * kResidentQuads;
 
-__device__ __forceinline__ double block_sum_wide(double v, double *scratch) {
+__device__ __forceinline__ double block_sum_wide(double v, double *lds_sums) {
     v = wave_sum(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) lds_sums[threadIdx.x >> 6] = v;
     __syncthreads();
     double s = 0.0;
 #pragma unroll
-    for (int w = 0; w < kResidentThreads / 64; ++w) s += scratch[w];
+    for (int w = 0; w < kResidentThreads / 64; ++w) s += lds_sums[w];
     return s;
 }
 
 __global__ __launch_bounds__(kResidentThreads) void group_norm_resident_kernel(GroupNormArgs a) {
-    __shared__ double scratch[kResidentThreads / 64];
+    __shared__ double lds_sums[kResidentThreads / 64];
     const int tid = threadIdx.x;
     const int64_t item = blockIdx.x;
     const int64_t i3 = item / a.groups;
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(kResidentThreads) void group_norm_resident_kernel(G
              (static_cast<double>(v[u][2]) + static_cast<double>(v[u][3]));
     }
     const double n = static_cast<double>(count);
-    const float mean = static_cast<float>(block_sum_wide(s, scratch) / n);
+    const float mean = static_cast<float>(block_sum_wide(s, lds_sums) / n);
     double t = 0.0;
 #pragma unroll
     for (int u = 0; u < kResidentQuads; ++u) {
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(kResidentThreads) void group_norm_resident_kernel(G
             t += static_cast<double>(__fmul_rn(d, d));
         }
     }
-    const float variance = static_cast<float>(block_sum_wide(t, scratch) / n);
+    const float variance = static_cast<float>(block_sum_wide(t, lds_sums) / n);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
     float4v *y4 = reinterpret_cast<float4v *>(a.y + i3 * a.ynb3 + c0 * a.ynb2);
 #pragma unroll
@@ -405,6 +407,48 @@ hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream) {
     KernelScope scope("group_norm.apply", stream);
     hipLaunchKernelGGL(group_apply_kernel, grid, dim3(kThreads), 0, stream, a);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ the entry point that allocates nothing
+
+// The partial sums of sdhip_group_norm_static: a file-scope array of the
+// device code, one copy on each GPU the library runs on, held until the
+// process ends.  Host code never names it as a device address: its address
+// on each device comes from hipGetSymbolAddress, once per device, with that
+// device current (static_scratch below), and only that address goes to the
+// kernels.  The sums are written before they are read, so nothing needs
+// clearing; every call on one GPU shares it, so calls that overlap on one
+// GPU race.
+static __device__ __align__(256) double scratch[kStaticScratchBytes / sizeof(double)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+double *g_scratch[kMaxDevices] = {};
+
+}  // namespace
+
+sdhip_status static_scratch(int device, double *&ptr) {
+    ptr = nullptr;
+    if (device < 0 || device >= kMaxDevices) {
+        return fail(SDHIP_ERROR, "device %d: at most %d devices hold the static scratch", device, kMaxDevices);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch[device] == nullptr) {
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess || current != device) {
+            return fail(SDHIP_ERROR, "static scratch of device %d looked up with device %d current", device, current);
+        }
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            return fail(SDHIP_ERROR, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+        }
+        g_scratch[device] = static_cast<double *>(p);
+    }
+    ptr = g_scratch[device];
+    return SDHIP_OK;
 }
 
 hipError_t launch_norm(const NormArgs &a, hipStream_t stream) {

@@ -62,6 +62,24 @@ sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int 
     return s == SDHIP_OK ? chain_after(run, static_cast<hipStream_t>(stream)) : s;
 }
 
+sdhip_status sdhip_group_norm_static(const sdhip_tensor *x, const sdhip_tensor *y, int groups, float eps,
+                                     const sdhip_epilogue *chain, void *stream) {
+    if (!sdhip_group_norm_supported(x, y, groups)) {
+        return fail(SDHIP_UNSUPPORTED, "group_norm_static: operands not taken");
+    }
+    const GroupNormShape shape = group_norm_shape(x->ne[0], x->ne[1], x->ne[2], x->ne[3], groups);
+    if (shape.work > kStaticScratchBytes) {
+        return fail(SDHIP_ERROR, "group_norm_static: %zu bytes of partial sums, the static scratch holds %zu",
+                    shape.work, kStaticScratchBytes);
+    }
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess) return fail(SDHIP_ERROR, "group_norm_static: no current device");
+    double *ptr = nullptr;
+    const sdhip_status s = static_scratch(device, ptr);
+    if (s != SDHIP_OK) return s;
+    return sdhip_group_norm(x, y, groups, eps, chain, ptr, kStaticScratchBytes, stream);
+}
+
 int sdhip_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y) {
     if (x == nullptr || y == nullptr) return 0;
     return holds_f32(x) && holds_f32(y) && same_shape(x, y) && x->nb[1] % 4 == 0 && x->nb[2] % 4 == 0 &&

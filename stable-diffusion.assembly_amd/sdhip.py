@@ -107,6 +107,7 @@ SIGNATURES = [
     ("sdhip_group_norm_supported", ctypes.c_int, [_T, _T, ctypes.c_int]),
     ("sdhip_group_norm_work_size", _SZ, [_T, _T, ctypes.c_int]),
     ("sdhip_group_norm", ctypes.c_int, [_T, _T, ctypes.c_int, ctypes.c_float, _E, _P, _SZ, _P]),
+    ("sdhip_group_norm_static", ctypes.c_int, [_T, _T, ctypes.c_int, ctypes.c_float, _E, _P]),
     ("sdhip_norm_supported", ctypes.c_int, [_T, _T]),
     ("sdhip_norm", ctypes.c_int, [_T, _T, ctypes.c_float, _E, _P]),
     ("sdhip_plan_nodes", ctypes.c_int,
@@ -286,6 +287,12 @@ def group_norm(x, y, groups, eps, chain=None, work=None):
     check(lib.sdhip_group_norm(dx, dy, groups, eps, ctypes.byref(chain) if chain else None, ptr, size,
                                stream_handle()), "group_norm")
     return buf
+
+
+def group_norm_static(x, y, groups, eps, chain=None):
+    """sdhip_group_norm_static: no work buffer, the library's static scratch."""
+    check(load().sdhip_group_norm_static(desc(x), desc(y), groups, eps, ctypes.byref(chain) if chain else None,
+                                         stream_handle()), "group_norm_static")
 
 
 def norm(x, y, eps, chain=None):
