@@ -208,6 +208,12 @@ __device__ __forceinline__ void wait_loads() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
+// The workgroup's barrier alone, with no wait for the loads in flight (which
+// __syncthreads drains): what a wave must have in LDS before it, it waits for
+// itself (wait_loads).  The memory clobber keeps the compiler from moving
+// loads or stores across it.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
 // One 16-byte piece a lane of a 1 KB copy from global memory into LDS; the
 // LDS address is the wave's (lane l's piece lands 16 l bytes past it).
 __device__ __forceinline__ void copy_lds(const void *src, char *lds) {

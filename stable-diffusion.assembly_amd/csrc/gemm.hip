@@ -445,12 +445,15 @@ constexpr int lds_halves() {
 // the block's 128 rows of W are 64 features of the first half and the same 64
 // of the second (the gate), each wave's two column tiles a pair, and the
 // block writes out[m * ldo + j] = P[m][j] GELU(P[m][half + j]).
-template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS>
+template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS, int WP = 1>
 __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
+    // WP: the weights' planes, 1 (FP16 weights) or 2 (single-precision ones
+    // split, w_plane apart): then three MFMAs a product, x and W both split.
+    constexpr int MODE = WP == 2 ? kSplitBoth : kSplitA;
     static_assert(!GATED || TN == 2, "the gated form pairs two column tiles");
-    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, kSplitA>()];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, MODE>()];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -483,13 +486,15 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
     F32Rows<BM, VECX, FULL> xa[NS];
-    F16Rows<BN, VECW, FULL> wb[NS];
+    F16Rows<BN, VECW, FULL, WP> wb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         xa[s].init(p.x, p.ldx, x_row, p.K, tid);
-        wb[s].init(p.w, p.ldw, w_row, p.K, tid);
+        wb[s].init(p.w, p.ldw, w_row, p.K, tid, p.w_plane);
     }
-    main_loop<TM, TN, kSplitA, NS>(acc, xa, wb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
+    main_loop<TM, TN, MODE, NS>(acc, xa, wb, lds, (p.K + kBK - 1) / kBK, tid, lane, wr, wc);
+    // The product's factor: x's split took 2^-4, and split weights 2^s of their row.
+    const auto up = [&](int64_t feature) -> float { return WP == 2 ? kSplitUp * p.w_scale[feature] : kSplitUp; };
 
     // The epilogue: rows m of the tile, column (feature) lane % 32; a tile's
     // 16 values of the lane at a time, their loads before their stores.  A
@@ -527,10 +532,11 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
             const int64_t f = n0 + 32 * wc + col;
             const int64_t fc = f < p.half ? f : p.half - 1;
             float xv[16], gv[16];
+            const float fx = up(fc), fg = up(p.half + fc);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                xv[e] = acc[i][0][e] * kSplitUp;
-                gv[e] = acc[i][1][e] * kSplitUp;
+                xv[e] = acc[i][0][e] * fx;
+                gv[e] = acc[i][1][e] * fg;
             }
             apply_chain_tile(
                 p.chain, xv, full, [&](int s) { return fc * p.chain.steps[s].nb[0] + first(s); }, stride,
@@ -552,8 +558,9 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
                 const int64_t n = n0 + wc * 32 * TN + 32 * j + col;
                 const int64_t nc = n < p.N ? n : p.N - 1;
                 float v[16];
+                const float f = up(nc);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * f;
                 float *out = p.y + mbase * p.ldy + nc;
                 if (p.from_redirect) {
                     float r[16];
@@ -654,11 +661,13 @@ __global__ __launch_bounds__(256) void mul_mat_sum_kernel(MulMatArgs p, const fl
 
 // y[n][oc][pos] = sum_k W[oc][k] columns[k][pos], the chain applied; W rows
 // K-contiguous FP16 (the kernel as ggml holds it, [OC][IC][KH][KW]).
-template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS, bool K3 = false>
+template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS, bool K3 = false, int WP = 1>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     constexpr int BM = 64 * TM;  // output channels
     constexpr int BN = 64 * TN;  // positions
-    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, kSplitB>()];
+    // WP as mul_mat_kernel's: split single-precision kernels in two planes.
+    constexpr int MODE = WP == 2 ? kSplitBoth : kSplitB;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, MODE>()];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -679,14 +688,14 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    F16Rows<BM, VECW, FULL> wa[NS];
+    F16Rows<BM, VECW, FULL, WP> wa[NS];
     Columns<BN, POINTWISE, FULL, K3> xb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        wa[s].init(c.w, c.K, w_row, c.K, tid);
+        wa[s].init(c.w, c.ldw, w_row, c.K, tid, c.w_plane);
         xb[s].init(c, p0, tid);
     }
-    main_loop<TM, TN, kSplitB, NS>(acc, wa, xb, lds, (c.K + kBK - 1) / kBK, tid, lane, wr, wc);
+    main_loop<TM, TN, MODE, NS>(acc, wa, xb, lds, (c.K + kBK - 1) / kBK, tid, lane, wr, wc);
 
     // The epilogue: output channels oc down the tile, position lane % 32 across;
     // a tile wholly inside OC addresses its channels as a stride from its first.
@@ -716,8 +725,13 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
                 return oc < c.oc ? oc : c.oc - 1;
             };
             float v[16];
+            if (WP == 2) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * (kSplitUp * c.w_scale[chan(e)]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e] * kSplitUp;
+            }
             float *out = c.y + at + obase * c.ynb2;
             if (c.from_redirect) {
                 float r[16];
@@ -786,12 +800,13 @@ __global__ __launch_bounds__(256) void columns_kernel(ConvArgs c, float *__restr
 // part[s][oc][p] = 16 sum over split s's k of W[oc][k] cols[p][k]: blocks of
 // 64 output channels by 64 positions, the splits of split_len (a multiple of
 // the K-step) one after the other in the grid.
-template <int NS>
+template <int NS, int WP = 1>
 __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const float *__restrict__ cols,
                                                            int64_t split_len, int64_t p_blocks,
                                                            float *__restrict__ part) {
     constexpr int BM = 64, BN = 64;
-    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<1, 1, kSplitB>()];
+    constexpr int MODE = WP == 2 ? kSplitBoth : kSplitB;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<1, 1, MODE>()];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -810,16 +825,16 @@ __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const flo
 
     float16v acc[1][1];
     acc[0][0] = float16v{};
-    F16Rows<BM, true, true> wa[NS];
+    F16Rows<BM, true, true, WP> wa[NS];
     F32Rows<BN, true, true> xb[NS];
     const auto w_row = [&](int r) -> int64_t { return oc0 + r < c.oc ? oc0 + r : -1; };
     const auto p_row = [&](int r) -> int64_t { return p0 + r < c.P ? p0 + r : -1; };
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
-        wa[q].init(c.w + k_begin, c.K, w_row, k_len, tid);
+        wa[q].init(c.w + k_begin, c.ldw, w_row, k_len, tid, c.w_plane);
         xb[q].init(cols + k_begin, c.K, p_row, k_len, tid);
     }
-    main_loop<1, 1, kSplitB, NS>(acc, wa, xb, lds, k_len / kBK, tid, lane, wr, wc);
+    main_loop<1, 1, MODE, NS>(acc, wa, xb, lds, k_len / kBK, tid, lane, wr, wc);
 
     // The columns were scaled by 2^-4 in their split.
     const int64_t pos = p0 + wc * 32 + (lane & 31);
@@ -829,7 +844,7 @@ __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const flo
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int64_t oc = obase + tile_row(e);
-        if (oc < c.oc) out[oc * c.P] = acc[0][0][e] * kSplitUp;
+        if (oc < c.oc) out[oc * c.P] = acc[0][0][e] * (WP == 2 ? kSplitUp * c.w_scale[oc] : kSplitUp);
     }
 }
 
@@ -934,6 +949,22 @@ __global__ __launch_bounds__(256) void split_batched_kernel(SplitBatchedArgs p) 
 // ------------------------------------------------------------------ launchers
 
 template <int TM, int TN, bool GATED>
+hipError_t launch_mul_mat_w32(const MulMatArgs &a, dim3 grid, hipStream_t stream) {
+    // Split weights: rows 32-aligned and zero past K, so their loads are
+    // always whole vectors; x's decide FULL.
+    const bool vx = a.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+    const dim3 block(256);
+    if (vx && a.K % kBK == 0) {
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 2>), grid, block, 0, stream, a);
+    } else if (vx) {
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 2>), grid, block, 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, true, false, 2, 2>), grid, block, 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+template <int TM, int TN, bool GATED>
 hipError_t launch_mul_mat_t(const MulMatArgs &p, int stages, hipStream_t stream) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
@@ -946,6 +977,7 @@ hipError_t launch_mul_mat_t(const MulMatArgs &p, int stages, hipStream_t stream)
     const bool full = vx && vw && p.K % kBK == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(GATED ? "mul_mat_gated" : "mul_mat", stream);
+    if (p.w_scale != nullptr) return launch_mul_mat_w32<TM, TN, GATED>(a, grid, stream);
     if (full && stages == 4) {
         hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 4>), grid, block, 0, stream, a);
     } else if (full) {
@@ -969,10 +1001,21 @@ hipError_t launch_conv_t(const ConvArgs &c, int stages, hipStream_t stream) {
     ConvArgs a = c;
     a.oc_blocks = (c.oc + BM - 1) / BM;
     const int64_t blocks = ((c.P + BN - 1) / BN) * a.oc_blocks;
-    const bool vw = c.K % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0;
+    const bool vw = c.ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0;
     const bool full = POINTWISE && vw && c.K % kBK == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(POINTWISE ? "conv_direct_pointwise" : "conv_direct", stream);
+    if (c.w_scale != nullptr) {
+        // Split kernels: whole vectors always (rows 32-aligned, zeros past K).
+        if (full) {
+            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 2>), grid, block, 0,
+                               stream, a);
+        } else {
+            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 2>), grid, block, 0,
+                               stream, a);
+        }
+        return hipGetLastError();
+    }
     if (full && stages == 4) {
         hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 4>), grid, block, 0, stream, a);
     } else if (full) {
@@ -1072,6 +1115,7 @@ MulMatSplitPlan mul_mat_split_plan(const MulMatArgs &p) {
 }  // namespace
 
 bool mul_mat_split_taken(const MulMatArgs &p) {
+    if (p.w_scale != nullptr) return false;  // split weights go in one pass
     const bool aligned = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0 && p.ldw % 8 == 0 &&
                          (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
     return aligned && p.K % kBK == 0 && mul_mat_split_plan(p).splits > 1;
@@ -1128,7 +1172,8 @@ ColumnsPlan columns_plan(const ConvArgs &c) {
 
 bool conv_columns_taken(const ConvArgs &c) {
     const bool pointwise = c.kw == 1 && c.kh == 1 && c.s0 == 1 && c.s1 == 1 && c.p0 == 0 && c.p1 == 0;
-    return !pointwise && c.K % kBK == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0 &&
+    const bool w_aligned = c.w_split || (c.ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0);
+    return !pointwise && c.K % kBK == 0 && w_aligned &&
            c.P * c.K <= (int64_t{1} << 28) && c.P < (int64_t{1} << 31);
 }
 
@@ -1152,7 +1197,10 @@ hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipSt
         ConvArgs a = c;
         a.oc_blocks = (c.oc + 63) / 64;
         const dim3 grid(static_cast<uint32_t>(l.blocks * l.splits));
-        if (g.stages == 4) {
+        if (c.w_scale != nullptr) {
+            hipLaunchKernelGGL((conv_columns_kernel<2, 2>), grid, dim3(256), 0, stream, a, cols, l.split_len,
+                               l.p_blocks, part);
+        } else if (g.stages == 4) {
             hipLaunchKernelGGL((conv_columns_kernel<4>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
                                part);
         } else {
@@ -1163,6 +1211,52 @@ hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipSt
     KernelScope scope("conv_direct.sum", stream);
     hipLaunchKernelGGL(conv_sum_kernel, dim3(static_cast<uint32_t>((c.oc * c.P + 255) / 256)), dim3(256), 0, stream, c,
                        part, l.splits);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ single-precision weights
+
+namespace {
+
+// One block per row: the row's greatest |w|, its exponent, then the row split.
+__global__ __launch_bounds__(256) void split_weights_kernel(const float *__restrict__ w, int64_t ld, int64_t k,
+                                                            int64_t kw, int64_t rows, _Float16 *__restrict__ hi,
+                                                            _Float16 *__restrict__ lo, float *__restrict__ scale) {
+    __shared__ float lds_max[4];
+    const int64_t row = blockIdx.x;
+    const float *src = w + row * ld;
+    float m = 0.0f;
+    for (int64_t i = threadIdx.x; i < k; i += 256) m = fmaxf(m, fabsf(src[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((threadIdx.x & 63) == 0) lds_max[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(lds_max[0], lds_max[1]), fmaxf(lds_max[2], lds_max[3]));
+    int e = 0;
+    if (m > 0.0f) frexpf(m, &e);  // m < 2^e
+    const int s = m > 0.0f ? 15 - e : 0;  // m 2^s in [2^14, 2^15)
+    if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, -s);
+    for (int64_t i = threadIdx.x; i < kw; i += 256) {
+        _Float16 h, l;
+        split_scaled(i < k ? ldexpf(src[i], s) : 0.0f, h, l);
+        hi[row * kw + i] = h;
+        lo[row * kw + i] = l;
+    }
+}
+
+}  // namespace
+
+size_t split_weights_bytes(int64_t rows, int64_t k) {
+    const size_t planes = static_cast<size_t>(2 * rows * split_weights_ld(k) * 2 + 255) / 256 * 256;
+    return planes + static_cast<size_t>(rows * 4 + 255) / 256 * 256;
+}
+
+hipError_t launch_split_weights(const float *w, int64_t ld, int64_t rows, int64_t k, void *out, hipStream_t stream) {
+    const int64_t kw = split_weights_ld(k);
+    _Float16 *hi = static_cast<_Float16 *>(out);
+    KernelScope scope("split_weights", stream);
+    hipLaunchKernelGGL(split_weights_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, w, ld, k, kw,
+                       rows, hi, hi + rows * kw, const_cast<float *>(split_weights_scale(out, rows, k)));
     return hipGetLastError();
 }
 

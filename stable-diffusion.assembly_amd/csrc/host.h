@@ -46,8 +46,12 @@ struct Tuning {
     // MFMAs, 2 or 4.
     int gemm_stages = 2;
     // This library's own: a product's block of 64 TM x 64 TN as TM TN (11,
-    // 21, 22), or 0 to choose by the size.
+    // 12, 21, 22), or 0 to choose by the size.
     int gemm_tiles = 0;
+    // This library's own: Winograd's products by the core staged through
+    // registers (1) or by the one whose copies into LDS global_load_lds
+    // makes (2), for comparison: the same bits, measured no faster.
+    int gemm_core = 1;
     // This library's own: attention by its generic form (1) even where the
     // fast one takes the operands (0), for comparison; results agree within
     // the same bound.

@@ -16,6 +16,16 @@ struct MulMatArgs {
     int64_t ldx;
     const _Float16 *w;
     int64_t ldw;
+    // Single-precision weights, split (split_weights): w the hi plane, the lo
+    // plane w_plane halves after it, rows ldw (a multiple of 32) apart, zeros
+    // past K; row n scaled by 1 / w_scale[n], a power of two, which the
+    // epilogue undoes.  Null w_scale: FP16 weights as they are.
+    int64_t w_plane;
+    const float *w_scale;
+    // The single-precision weights as the caller holds them (rows ldw32
+    // floats apart), for the bits mode's quantizer; null for FP16 weights.
+    const float *w32;
+    int64_t ldw32;
     float *y;  // the output, or the redirect, or the gated output
     int64_t ldy;
     int64_t M, N, K;
@@ -38,12 +48,35 @@ struct GemmShape {
 hipError_t launch_mul_mat(const MulMatArgs &p, GemmShape g, hipStream_t stream);
 hipError_t launch_mul_mat_gated(const MulMatArgs &p, GemmShape g, hipStream_t stream);
 
+// Single-precision weights [rows][k] (rows ld apart) split into two FP16
+// planes for the products (gemm.hip): each row scaled by 2^s, s bringing its
+// greatest |w| into [2^14, 2^15) (0 for a row of zeros), hi = fp16(w 2^s),
+// lo = fp16(w 2^s - hi), rows kw (K rounded up to 32) halves apart and zeros
+// past K, lo kw * rows halves after hi; scale[row] = 2^-s.  22 bits of each
+// weight, as the activations' split keeps 22 of theirs.
+size_t split_weights_bytes(int64_t rows, int64_t k);
+hipError_t launch_split_weights(const float *w, int64_t ld, int64_t rows, int64_t k, void *out, hipStream_t stream);
+// Where launch_split_weights puts the planes and the scales in `out`.
+inline int64_t split_weights_ld(int64_t k) { return (k + 31) / 32 * 32; }
+inline const _Float16 *split_weights_hi(const void *out) { return static_cast<const _Float16 *>(out); }
+inline const float *split_weights_scale(const void *out, int64_t rows, int64_t k) {
+    const size_t planes = static_cast<size_t>(2 * rows * split_weights_ld(k) * 2 + 255) / 256 * 256;
+    return reinterpret_cast<const float *>(static_cast<const char *>(out) + planes);
+}
+
 // The direct convolution: y[n][oc][oy][ox] = sum over (ic, kh, kw).
 struct ConvArgs {
     const float *x;  // [N][IC][IH][IW], strides xnb1..3
     int64_t xnb1, xnb2, xnb3;
     int64_t iw, ih, ic, n;
-    const _Float16 *w;  // [OC][IC * KH * KW], contiguous
+    const _Float16 *w;  // [OC][IC * KH * KW], rows ldw apart
+    int64_t ldw;
+    // Single-precision kernels, split as MulMatArgs's weights (w_split: the
+    // call splits them, into rows ldw = K rounded up to 32 apart); null
+    // w_scale: FP16 kernels as they are.
+    int32_t w_split;
+    int64_t w_plane;
+    const float *w_scale;
     int64_t kw, kh, oc;
     float *y;  // [N][OC][OH][OW], strides ynb1..3
     int64_t ynb1, ynb2, ynb3;
@@ -99,5 +132,12 @@ struct SplitBatchedArgs {
 };
 
 hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream);
+
+// The same products with the copies into LDS made by global_load_lds
+// (gemm2.hip): both operands as two FP16 planes (a, not a32), K a multiple of
+// 32, every plane and batch 16-byte aligned.  `tiles` as GemmShape's (11, 12,
+// 21, 22 for blocks of 64 WM x 64 WN), or 0 to choose by the size.
+bool split_batched2_takes(const SplitBatchedArgs &p);
+hipError_t launch_split_batched2(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream);
 
 }  // namespace sdhip

@@ -56,8 +56,8 @@ bool conv_quantized() {
 bool direct_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
     if (kernel == nullptr || input == nullptr || y == nullptr || op == nullptr) return false;
     if (conv_quantized()) return false;
-    // FP16 kernels only: single-precision ones are left to the caller.
-    const bool weights = holds_f16(kernel) && contiguous(kernel);
+    // FP16 or single-precision kernels (conv2d.cc:320-331).
+    const bool weights = (holds_f16(kernel) || holds_f32(kernel)) && contiguous(kernel);
     if (!(weights && holds_f32(input) && holds_f32(y) && contiguous(y) && kernel->ne[2] == input->ne[2] &&
           op[0] > 0 && op[1] > 0 && op[4] > 0 && op[5] > 0 && op[2] >= 0 && op[3] >= 0)) {
         return false;
@@ -82,15 +82,15 @@ bool winograd_taken(const sdhip_tensor *kernel, const sdhip_tensor *input, const
 }
 
 // F(4x4, 3x3) for FP16 kernels and images of winograd4_positions outputs and
-// more (winograd.cc:1204-1206).
-bool four(const Geometry &g) {
-    return tuning().winograd == 2 && g.ow * g.oh >= tuning().winograd4_positions;
+// more (winograd.cc:1204-1206); single-precision kernels take F(2x2).
+bool four(const Geometry &g, const sdhip_tensor *kernel) {
+    return tuning().winograd == 2 && kernel->type == SDHIP_TYPE_F16 && g.ow * g.oh >= tuning().winograd4_positions;
 }
 
 int path_of(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
     if (!direct_supported(kernel, input, y, op)) return -1;
     if (winograd_taken(kernel, input, y, op)) {
-        return four(geometry(kernel, input, y, op)) ? 4 : 2;
+        return four(geometry(kernel, input, y, op), kernel) ? 4 : 2;
     }
     return 0;
 }
@@ -106,7 +106,7 @@ ConvArgs conv_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const 
     c.ih = input->ne[1];
     c.ic = input->ne[2];
     c.n = input->ne[3];
-    c.w = static_cast<const _Float16 *>(kernel->data);
+    c.w = kernel->type == SDHIP_TYPE_F16 ? static_cast<const _Float16 *>(kernel->data) : nullptr;
     c.kw = kernel->ne[0];
     c.kh = kernel->ne[1];
     c.oc = kernel->ne[3];
@@ -123,10 +123,18 @@ ConvArgs conv_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const 
     c.d0 = op[4];
     c.d1 = op[5];
     c.K = c.ic * c.kh * c.kw;
+    c.ldw = c.K;
     c.taps = c.kh * c.kw;
     c.plane = c.oh * c.ow;
     c.P = c.n * c.plane;
     return c;
+}
+
+// A convolution of single-precision kernels, which the call splits into two
+// FP16 planes of rows 32-aligned (split_weights) before the products.
+void mark_split(ConvArgs &c) {
+    c.w_split = 1;
+    c.ldw = split_weights_ld(c.K);
 }
 
 WinogradArgs winograd_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
@@ -141,7 +149,8 @@ WinogradArgs winograd_args(const sdhip_tensor *kernel, const sdhip_tensor *input
     a.ih = input->ne[1];
     a.ic = input->ne[2];
     a.n = input->ne[3];
-    a.w = static_cast<const _Float16 *>(kernel->data);
+    a.w = kernel->type == SDHIP_TYPE_F16 ? static_cast<const _Float16 *>(kernel->data) : nullptr;
+    a.w32 = kernel->type == SDHIP_TYPE_F32 ? static_cast<const float *>(kernel->data) : nullptr;
     a.oc = kernel->ne[3];
     a.ow = y->ne[0];
     a.oh = y->ne[1];
@@ -181,8 +190,12 @@ size_t sdhip_conv2d_work_size(const sdhip_tensor *kernel, const sdhip_tensor *in
         return winograd_work_size(winograd_args(kernel, input, y, op_params, path));
     }
     if (path == 0) {
-        const ConvArgs c = conv_args(kernel, input, y, op_params);
-        if (conv_columns_taken(c)) return conv_columns_work_size(c);
+        ConvArgs c = conv_args(kernel, input, y, op_params);
+        // Single-precision kernels: split into two FP16 planes at every call,
+        // after the columns' work (the split's rows are 32-aligned).
+        const size_t split = kernel->type == SDHIP_TYPE_F32 ? split_weights_bytes(c.oc, c.K) : 0;
+        if (split > 0) mark_split(c);
+        return (conv_columns_taken(c) ? round_up(conv_columns_work_size(c), 256) : 0) + split;
     }
     return 0;
 }
@@ -214,6 +227,21 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
     c.y = run.out;
     c.from_redirect = run.from_redirect;
     c.chain = run.fused;
+    if (kernel->type == SDHIP_TYPE_F32) {
+        mark_split(c);
+        const size_t cols = conv_columns_taken(c) ? round_up(conv_columns_work_size(c), 256) : 0;
+        const size_t need = cols + split_weights_bytes(c.oc, c.K);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        void *split = static_cast<char *>(work) + cols;
+        s = launched(launch_split_weights(static_cast<const float *>(kernel->data), c.K, c.oc, c.K, split, st),
+                     "conv2d split kernels");
+        if (s != SDHIP_OK) return s;
+        c.w = split_weights_hi(split);
+        c.w_scale = split_weights_scale(split, c.oc, c.K);
+        c.w_plane = c.oc * c.ldw;
+    }
     if (conv_columns_taken(c)) {
         const size_t need = conv_columns_work_size(c);
         if (work == nullptr || work_size < need) {

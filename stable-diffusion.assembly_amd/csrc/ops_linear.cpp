@@ -33,8 +33,13 @@ MulMatArgs args_of(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_ten
     MulMatArgs a{};
     a.x = static_cast<const float *>(x->data);
     a.ldx = x->nb[1] / 4;
-    a.w = static_cast<const _Float16 *>(w->data);
-    a.ldw = w->nb[1] / 2;
+    if (w->type == SDHIP_TYPE_F32) {
+        a.w32 = static_cast<const float *>(w->data);
+        a.ldw32 = w->nb[1] / 4;
+    } else {
+        a.w = static_cast<const _Float16 *>(w->data);
+        a.ldw = w->nb[1] / 2;
+    }
     a.K = w->ne[0];
     a.N = w->ne[1];
     a.M = x->ne[1] * x->ne[2] * x->ne[3];
@@ -62,12 +67,11 @@ extern "C" {
 
 int sdhip_mul_mat_supported(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y) {
     if (w == nullptr || x == nullptr || y == nullptr) return 0;
-    // The weights are one matrix of FP16, the other operand and the result
-    // contiguous single precision, the products large enough to pay for the
-    // launch (mul_mat.cc:181-194).  Single-precision weights are not taken:
-    // the caller computes them (not taken, as ggml computes what the
-    // reference does not take).
-    const bool weights = holds_f16(w) && w->ne[2] == 1 && w->ne[3] == 1;
+    // The weights are one matrix of FP16 or single precision, the other
+    // operand and the result contiguous single precision, the products large
+    // enough to pay for the launch (mul_mat.cc:181-194).
+    const bool weights = (holds_f16(w) || holds_f32(w)) && w->ne[2] == 1 && w->ne[3] == 1 &&
+                         w->nb[1] % w->nb[0] == 0 && w->nb[1] >= w->nb[0] * w->ne[0];
     const bool shapes = x->ne[0] == w->ne[0] && y->ne[0] == w->ne[1] && y->ne[1] == x->ne[1] &&
                         y->ne[2] == x->ne[2] && y->ne[3] == x->ne[3];
     return weights && shapes && holds_f32(x) && contiguous(x) && holds_f32(y) && contiguous(y) &&
@@ -80,8 +84,30 @@ size_t sdhip_mul_mat_work_size(const sdhip_tensor *w, const sdhip_tensor *x, con
         return quantized_linear_work_size(w->ne[0], w->ne[1], x->ne[1] * x->ne[2] * x->ne[3]);
     }
     const MulMatArgs a = args_of(w, x, y);
+    // Single-precision weights: split into two FP16 planes at every call.
+    if (a.w32 != nullptr) return split_weights_bytes(a.N, a.K);
     return mul_mat_split_taken(a) ? mul_mat_split_work_size(a) : 0;
 }
+
+namespace sdhip {
+
+// Single-precision weights split into the work buffer (split_weights), and
+// the product's description pointed at the planes.
+sdhip_status split_into(MulMatArgs &a, void *work, size_t work_size, hipStream_t st, const char *what) {
+    const size_t need = split_weights_bytes(a.N, a.K);
+    if (work == nullptr || work_size < need) {
+        return fail(SDHIP_ERROR, "%s: work buffer of %zu bytes, %zu needed", what, work_size, need);
+    }
+    const sdhip_status s = launched(launch_split_weights(a.w32, a.ldw32, a.N, a.K, work, st), "split weights");
+    if (s != SDHIP_OK) return s;
+    a.w = split_weights_hi(work);
+    a.ldw = split_weights_ld(a.K);
+    a.w_plane = a.N * a.ldw;
+    a.w_scale = split_weights_scale(work, a.N, a.K);
+    return SDHIP_OK;
+}
+
+}  // namespace sdhip
 
 sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y,
                            const sdhip_epilogue *chain, void *work, size_t work_size, void *stream) {
@@ -102,6 +128,9 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
             return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
         }
         s = quantized_linear(a, false, work, st);
+    } else if (a.w32 != nullptr) {
+        s = split_into(a, work, work_size, st, "mul_mat");
+        if (s == SDHIP_OK) s = launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
     } else if (mul_mat_split_taken(a)) {
         const size_t need = mul_mat_split_work_size(a);
         if (work == nullptr || work_size < need) {
@@ -169,6 +198,10 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
             return fail(SDHIP_ERROR, "mul_mat_gated: work buffer of %zu bytes, %zu needed", work_size, need);
         }
         return quantized_linear(a, true, work, st);
+    }
+    if (a.w32 != nullptr) {
+        const sdhip_status s = split_into(a, work, work_size, st, "mul_mat_gated");
+        if (s != SDHIP_OK) return s;
     }
     return launched(launch_mul_mat_gated(a, gemm_shape(), st), "mul_mat_gated");
 }

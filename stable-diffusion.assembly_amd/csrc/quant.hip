@@ -146,14 +146,17 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(const float *__res
 // One wave per column (a row of W): the whole row's greatest magnitude when
 // the weights have one scale a row, then group by group the scale, the
 // bytes and their sum.
-__global__ __launch_bounds__(256) void quantize_weights_kernel(const _Float16 *__restrict__ w, int64_t ldw, int64_t N,
+// W: the weights' type, FP16 or single precision (quantize_weights_f16 and
+// _f32, quant.cc:366-380: the same quantizer of their widened values).
+template <class W>
+__global__ __launch_bounds__(256) void quantize_weights_kernel(const W *__restrict__ w, int64_t ldw, int64_t N,
                                                                int64_t K, Quant q, Layout l, int8_t *__restrict__ wq,
                                                                float *__restrict__ ws, float *__restrict__ wo,
                                                                int32_t *__restrict__ wsum) {
     const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
     const int lane = threadIdx.x & 63;
-    const _Float16 *row = w + n * ldw;
+    const W *row = w + n * ldw;
     float row_max = 0.0f;
     if (!q.weight_groups) {
         for (int64_t e = lane; e < K; e += 64) row_max = fmaxf(row_max, fabsf(static_cast<float>(row[e])));
@@ -424,12 +427,16 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     // into the work buffer at every call.
     const size_t wbytes = l.total - l.wq;
     const int64_t ne[4] = {a.K, a.N, 1, 1};
-    const int64_t nb[4] = {2, 2 * a.ldw, 2 * a.ldw * a.N, 2 * a.ldw * a.N};
+    const int64_t esize = a.w32 != nullptr ? 4 : 2;
+    const int64_t ld = a.w32 != nullptr ? a.ldw32 : a.ldw;
+    const int64_t nb[4] = {esize, esize * ld, esize * ld * a.N, esize * ld * a.N};
+    const void *wsrc = a.w32 != nullptr ? static_cast<const void *>(a.w32) : static_cast<const void *>(a.w);
     const uint64_t variant = static_cast<uint64_t>(q.group) | static_cast<uint64_t>(q.wmax) << 16 |
                              static_cast<uint64_t>(q.weight_groups) << 24;
     bool ready = false;
-    char *kept = static_cast<char *>(store_entry(a.w, SDHIP_TYPE_F16, ne, nb, kStoreQuantizedLinear, variant,
-                                                 static_cast<size_t>(2 * (a.ldw * (a.N - 1) + a.K)), wbytes, stream,
+    char *kept = static_cast<char *>(store_entry(wsrc, a.w32 != nullptr ? SDHIP_TYPE_F32 : SDHIP_TYPE_F16, ne, nb,
+                                                 kStoreQuantizedLinear, variant,
+                                                 static_cast<size_t>(esize * (ld * (a.N - 1) + a.K)), wbytes, stream,
                                                  ready));
     char *wbase = kept != nullptr ? kept : base + l.wq;  // the weights' parts, at their offsets from l.wq
     int8_t *wq = reinterpret_cast<int8_t *>(wbase);
@@ -443,8 +450,13 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     }
     if (!ready) {
         KernelScope scope("quantize_weights", stream);
-        hipLaunchKernelGGL(quantize_weights_kernel, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w, a.ldw, a.N,
-                           a.K, q, l, wq, ws, wo, wsum);
+        if (a.w32 != nullptr) {
+            hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w32,
+                               a.ldw32, a.N, a.K, q, l, wq, ws, wo, wsum);
+        } else {
+            hipLaunchKernelGGL(quantize_weights_kernel<_Float16>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w,
+                               a.ldw, a.N, a.K, q, l, wq, ws, wo, wsum);
+        }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return launched(err, "quantize_weights");
         if (kept != nullptr) store_publish(kept);

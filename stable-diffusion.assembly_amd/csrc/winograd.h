@@ -16,7 +16,8 @@ struct WinogradArgs {
     const float *x;
     int64_t xnb1, xnb2, xnb3;
     int64_t iw, ih, ic, n;
-    const _Float16 *w;  // [OC][IC][3][3]
+    const _Float16 *w;    // [OC][IC][3][3] in FP16, or null
+    const float *w32;     // the same in single precision, or null (F(2x2) only, winograd.cc:1204-1206)
     int64_t oc;
     float *y;
     int64_t ynb1, ynb2, ynb3;

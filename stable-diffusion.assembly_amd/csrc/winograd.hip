@@ -181,8 +181,12 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
     } else {
         const int64_t o = w - a.ic;
         const int64_t count = a.ic * 9;
-        const _Float16 *p = a.w + o * count;
-        if (count % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+        const _Float16 *p = a.w != nullptr ? a.w + o * count : nullptr;
+        if (a.w32 != nullptr) {
+            // Single-precision kernels.
+            const float *q = a.w32 + o * count;
+            for (int64_t i = tid; i < count; i += 256) m0 = fmaxf(m0, fabsf(q[i]));
+        } else if (count % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
             const half8 *q = reinterpret_cast<const half8 *>(p);
             const int64_t octs = count / 8;
             int64_t i = tid;
@@ -211,7 +215,8 @@ __global__ __launch_bounds__(256) void scales_kernel(WinogradArgs a, int32_t *__
 
 // ------------------------------------------------------------------ 1. weights
 
-__device__ __forceinline__ void load_g(const _Float16 *w, float (&g)[3][3]) {
+template <class W>
+__device__ __forceinline__ void load_g(const W *w, float (&g)[3][3]) {
 #pragma unroll
     for (int i = 0; i < 9; ++i) g[i / 3][i % 3] = static_cast<float>(w[i]);
 }
@@ -295,8 +300,8 @@ template <int M>
 constexpr int kWeightLds = 16 + 2 * kHalfPoints<M> * kWeightOc * kWeightIc * 2;
 
 // Block (bx, by) of weights_split, its LDS at `lds`.
-template <int M>
-__device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__ w, int64_t oc, int64_t ic, int64_t kp,
+template <int M, class W>
+__device__ __forceinline__ void weights_split_block(const W *__restrict__ w, int64_t oc, int64_t ic, int64_t kp,
                                                     const int32_t *__restrict__ e, const int32_t *__restrict__ amax,
                                                     _Float16 *__restrict__ u, int32_t *__restrict__ shift, int64_t bx,
                                                     int64_t by, char *lds) {
@@ -358,8 +363,8 @@ __device__ __forceinline__ void weights_split_block(const _Float16 *__restrict__
 }
 
 // Unscaled U[xi][oc][ic], one thread per (oc, ic), for the single-precision products.
-template <int M>
-__global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict__ w, float *__restrict__ u, int64_t oc,
+template <int M, class W>
+__global__ __launch_bounds__(256) void weights_kernel(const W *__restrict__ w, float *__restrict__ u, int64_t oc,
                                                       int64_t ic) {
     constexpr int A = Mat<M>::A;
     const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -377,8 +382,8 @@ __global__ __launch_bounds__(256) void weights_kernel(const _Float16 *__restrict
 // U[xi][oc][kp] * 2^a_o in single precision, zeros from IC to kp, one thread
 // per (oc, channel): the transformed weights as the store keeps them, the
 // inputs' scales 2^(e_c - E) applied by the products as they read them.
-template <int M>
-__global__ __launch_bounds__(256) void weights_scaled_kernel(const _Float16 *__restrict__ w, int64_t oc, int64_t ic,
+template <int M, class W>
+__global__ __launch_bounds__(256) void weights_scaled_kernel(const W *__restrict__ w, int64_t oc, int64_t ic,
                                                              int64_t kp, const int32_t *__restrict__ amax,
                                                              float *__restrict__ u) {
     constexpr int A = Mat<M>::A;
@@ -569,7 +574,11 @@ __global__ __launch_bounds__(256) void transforms_kernel(WinogradArgs a, int64_t
         q = b - both;
     }
     if (weights) {
-        weights_split_block<M>(a.w, a.oc, a.ic, kp, e, amax, u, shift, q % wgx, q / wgx, lds);
+        if (a.w32 != nullptr) {
+            weights_split_block<M>(a.w32, a.oc, a.ic, kp, e, amax, u, shift, q % wgx, q / wgx, lds);
+        } else {
+            weights_split_block<M>(a.w, a.oc, a.ic, kp, e, amax, u, shift, q % wgx, q / wgx, lds);
+        }
     } else {
         inputs_split_block<M>(a, kp, e, v, q % igx, q / igx, lds);
     }
@@ -1185,7 +1194,7 @@ struct WorkLayout {
 // (few tiles in all, winograd.cc:194-196) of at most 32 tiles, FP16 kernels
 // whose rows of eight channels are 16-byte aligned; not with winograd_fp32.
 bool small_path(const WinogradArgs &a) {
-    return !tuning().winograd_fp32 && a.tiles <= kSmallTilesMax &&
+    return !tuning().winograd_fp32 && a.w32 == nullptr && a.tiles <= kSmallTilesMax &&
            a.n * ((a.ow + 1) / 2) * ((a.oh + 1) / 2) <= tuning().winograd_small_tiles && a.ic % 8 == 0 &&
            (reinterpret_cast<uintptr_t>(a.w) & 15) == 0;
 }
@@ -1256,8 +1265,13 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         const int64_t n_in = a.tiles * a.ic;
         {
             KernelScope scope(names[1].c_str(), stream);
-            hipLaunchKernelGGL((weights_kernel<M>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0, stream, a.w, u,
-                               a.oc, a.ic);
+            if (a.w32 != nullptr) {
+                hipLaunchKernelGGL((weights_kernel<M, float>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0, stream,
+                                   a.w32, u, a.oc, a.ic);
+            } else {
+                hipLaunchKernelGGL((weights_kernel<M, _Float16>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0,
+                                   stream, a.w, u, a.oc, a.ic);
+            }
         }
         {
             KernelScope scope(names[2].c_str(), stream);
@@ -1311,13 +1325,15 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     // default, store.h:26-34), U 2^(a_o + e_c - E) is made at every call
     // already split into two FP16 planes, which the products read as they are.
     const int64_t wne[4] = {3, 3, a.ic, a.oc};
-    const int64_t wnb[4] = {2, 6, 18, 18 * a.ic};
+    const int64_t wsize = a.w32 != nullptr ? 4 : 2;
+    const int64_t wnb[4] = {wsize, 3 * wsize, 9 * wsize, 9 * wsize * a.ic};
+    const void *wdata = a.w32 != nullptr ? static_cast<const void *>(a.w32) : static_cast<const void *>(a.w);
     const size_t a_bytes = static_cast<size_t>(round_up(a.oc * 4, 256));
     const size_t u_bytes = static_cast<size_t>(A * A * a.oc * l.kp * 4);
     bool ready = false;
-    char *kept = static_cast<char *>(store_entry(a.w, SDHIP_TYPE_F16, wne, wnb, kStoreWinograd, M,
-                                                 static_cast<size_t>(a.oc * a.ic * 18), a_bytes + u_bytes, stream,
-                                                 ready));
+    char *kept = static_cast<char *>(store_entry(wdata, a.w32 != nullptr ? SDHIP_TYPE_F32 : SDHIP_TYPE_F16, wne, wnb,
+                                                 kStoreWinograd, M, static_cast<size_t>(a.oc * a.ic * 9 * wsize),
+                                                 a_bytes + u_bytes, stream, ready));
     int32_t *a_kept = kept != nullptr ? reinterpret_cast<int32_t *>(kept) : a_oc;
     float *u_kept = kept != nullptr ? reinterpret_cast<float *>(kept + a_bytes) : nullptr;
     float *f = kept != nullptr ? reinterpret_cast<float *>(base + l.f) : nullptr;
@@ -1339,8 +1355,14 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
                            stream, a, l.kp, e, a_oc, uh, shift, vh, wgx, wblocks, igx);
     } else if (!ready) {
         KernelScope scope(names[1].c_str(), stream);
-        hipLaunchKernelGGL((weights_scaled_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256))),
-                           dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp, a_kept, u_kept);
+        const dim3 grid(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256)));
+        if (a.w32 != nullptr) {
+            hipLaunchKernelGGL((weights_scaled_kernel<M, float>), grid, dim3(256), 0, stream, a.w32, a.oc, a.ic, l.kp,
+                               a_kept, u_kept);
+        } else {
+            hipLaunchKernelGGL((weights_scaled_kernel<M, _Float16>), grid, dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp,
+                               a_kept, u_kept);
+        }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return launched(err, "winograd weights");
         store_publish(kept);
@@ -1371,7 +1393,9 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         p.N = a.tiles;
         p.K = l.kp;
         p.batches = A * A;
-        const hipError_t err = launch_split_batched(p, gemm_shape(), stream);
+        const hipError_t err = tuning().gemm_core == 2 && split_batched2_takes(p)
+                                   ? launch_split_batched2(p, tuning().gemm_tiles, tuning().gemm_stages, stream)
+                                   : launch_split_batched(p, gemm_shape(), stream);
         if (err != hipSuccess) return launched(err, "winograd products");
     }
     KernelScope scope(names[4].c_str(), stream);

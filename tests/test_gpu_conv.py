@@ -36,10 +36,15 @@ def out_size(i, k, s, p, d):
     return (i + 2 * p - d * (k - 1) - 1) // s + 1
 
 
-def conv_case(gpu, c, seed, chain_steps=(), redirect=None, from_redirect=False, tuning=""):
+def conv_case(gpu, c, seed, chain_steps=(), redirect=None, from_redirect=False, tuning="", f32=False):
     w_, h_, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n = c
     r = rng(seed)
     kh16, k32 = weights_f16(r, (oc, ic, kh, kw))
+    if f32:
+        # Single-precision kernels, not FP16 numbers (the reference's
+        # GGML_TYPE_F32 cases): FP16 ones plus a part below FP16's step.
+        k32 = (k32 + uniform(r, k32.shape, 2.0 ** -14)).astype(np.float32)
+        kh16 = k32
     x = uniform(r, (n, ic, h_, w_), 1.0)
     oh, ow = out_size(h_, kh, s1, p1, d1), out_size(w_, kw, s0, p0, d0)
     k_d, x_d = dev(kh16, gpu), dev(x, gpu)
@@ -63,6 +68,36 @@ def test_conv2d(gpu, c, tuning):
     exact, mag = orc.exact_conv2d(x, k32, *p)
     err = orc.metric(y.cpu().numpy(), exact, mag)
     print(f"conv {c} path {path} [{tuning}]: {err:.3g}")
+    assert err <= BOUND
+
+
+# The reference's single-precision kernels (ops_test.cc:809-810, 817) and a
+# large 3x3 one: F(2x2) where FP16 kernels would take F(4x4)
+# (winograd.cc:1204-1206), directly where not Winograd.
+F32_CASES = [
+    ((17, 13, 5, 7, 3, 3, 1, 1, 1, 1, 1, 1, 3), 2),
+    ((40, 9, 7, 13, 5, 3, 1, 2, 2, 0, 2, 1, 1), 0),
+    ((96, 16, 32, 17, 3, 3, 1, 1, 1, 1, 1, 1, 1), 2),
+    ((64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), 2),
+    ((32, 32, 64, 40, 1, 1, 1, 1, 0, 0, 1, 1, 2), 0),
+    ((33, 33, 24, 30, 3, 3, 2, 2, 1, 1, 1, 1, 1), 0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c,want_path", F32_CASES, ids=lambda c: "x".join(map(str, c)) if isinstance(c, tuple) else str(c))
+@pytest.mark.parametrize("tuning", ["", "winograd=0", "winograd_fp32=1"])
+def test_conv2d_single_precision_kernels(gpu, c, want_path, tuning):
+    r = rng(sum(c) + 3)
+    b = uniform(r, (1, c[3], 1, 1), 1.0)
+    b_d = dev(b, gpu)
+    x, k32, y, path, p = conv_case(gpu, c, seed=sum(c) + 1, chain_steps=[("add", b_d)], tuning=tuning, f32=True)
+    if tuning == "":
+        assert path == want_path
+    exact, mag = orc.exact_conv2d(x, k32, *p)
+    exact = exact + b.astype(np.float64)
+    err = orc.metric(y.cpu().numpy(), exact, mag + np.abs(b))
+    print(f"conv single-precision kernels {c} path {path} [{tuning}]: {err:.3g}")
     assert err <= BOUND
 
 

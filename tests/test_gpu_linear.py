@@ -139,12 +139,56 @@ def test_gated(gpu, K, half, M, B):
     assert torch.isnan(y_d).all(), "the product itself is never written"
 
 
+F32_CASES = [  # K, N, M, batch: the reference's single-precision cases (ops_test.cc:829, 831) and SD1.5's
+    (77, 100, 23, 1),
+    (40, 2560, 96, 1),
+    (320, 320, 512, 2),
+    (1280, 320, 300, 1),
+]
+
+
+def weights_f32(r, shape, scale=0.25):
+    """Single-precision weights: no FP16 rounding (the reference's
+    GGML_TYPE_F32 weights, mul_mat.cc:190)."""
+    return uniform(r, shape, scale)
+
+
 @pytest.mark.gpu
-def test_single_precision_weights_not_taken(gpu):
-    """Weights of single precision are left to the caller (not taken)."""
-    w = torch.zeros((17, 32), dtype=torch.float32, device=gpu)
-    x = torch.zeros((40, 32), dtype=torch.float32, device=gpu)
-    y = torch.zeros((40, 17), dtype=torch.float32, device=gpu)
-    with pytest.raises(sdhip.SdhipError) as e:
-        sdhip.mul_mat(w, x, y)
-    assert e.value.status == sdhip.UNSUPPORTED
+@pytest.mark.parametrize("K,N,M,B", F32_CASES)
+def test_mul_mat_single_precision_weights(gpu, K, N, M, B):
+    """Single-precision weights, taken as the reference takes them
+    (mul_mat.cc:181-194): split into two FP16 planes with a power-of-two
+    scale per row, three MFMAs a product; the bias fused.  Rows of very
+    different magnitudes (2^-20 .. 2^12) check the per-row scale."""
+    r = rng(K + 3 * N)
+    w = weights_f32(r, (N, K))
+    w *= (2.0 ** r.integers(-20, 13, size=(N, 1))).astype(np.float32)
+    x = uniform(r, (B, M, K), 1.0)
+    b = uniform(r, (N,), 1.0)
+    w_d, x_d, b_d = dev(w, gpu), dev(x, gpu), dev(b, gpu)
+    assert sdhip.load().sdhip_mul_mat_supported(sdhip.desc(w_d), sdhip.desc(x_d), sdhip.desc(unwritten((B, M, N), gpu)))
+    y = unwritten((B, M, N), gpu)
+    sdhip.mul_mat(w_d, x_d, y, sdhip.epilogue([("add", b_d)]))
+    torch.cuda.synchronize()
+    exact, mag = orc.exact_mul_mat(w, x.reshape(B * M, K))
+    err = orc.metric(y.cpu().numpy().reshape(B * M, N), exact + b, mag + np.abs(b))
+    print(f"mul_mat single-precision weights {K}->{N} x {M}x{B}: {err:.3g}")
+    assert err <= BOUND_SPLIT
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,half,M", [(320, 1280, 200), (40, 100, 37)])
+def test_gated_single_precision_weights(gpu, K, half, M):
+    r = rng(K + half + 1)
+    w = weights_f32(r, (2 * half, K))
+    x = uniform(r, (M, K), 1.0)
+    bias = uniform(r, (2 * half,), 1.0)
+    w_d, x_d, b_d = dev(w, gpu), dev(x, gpu), dev(bias, gpu)
+    y_d = unwritten((M, 2 * half), gpu)
+    out = unwritten((M, half), gpu)
+    sdhip.mul_mat_gated(w_d, x_d, y_d, out, sdhip.epilogue([("add", b_d)]))
+    torch.cuda.synchronize()
+    exact, mag = orc.exact_gated(w, x, bias)
+    err = orc.metric(out.cpu().numpy(), exact, mag)
+    print(f"gated single-precision weights {K}->2x{half} x {M}: {err:.3g}")
+    assert err <= BOUND_SPLIT

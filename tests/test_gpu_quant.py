@@ -186,3 +186,30 @@ def test_sdxl_ff_out_with_residual(gpu, from_redirect):
     exact, mag = orc.exact_mul_mat(w32, xs[rows])
     add = b.astype(np.float64) + rs
     assert orc.metric(got[rows], exact + add, mag + np.abs(add)) <= bound(255, 127)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,N,M", [(77, 100, 300), (40, 2560, 296)])  # ops_test.cc:878, 880
+@pytest.mark.parametrize("tuning", ["bits=8", "bits=8,weight_group=0", "bits=7"])
+def test_quantized_single_precision_weights(gpu, K, N, M, tuning):
+    """The bits mode with single-precision weights: quantize_weights_f32
+    (quant.cc:373-380), the same quantizer of the weights as they are; bit
+    for bit with the oracle's restatement."""
+    group, levels, wmax, wg = quant_params(tuning)
+    r = rng(K + N + M + 5)
+    w = uniform(r, (N, K), 0.25)
+    x = uniform(r, (M, K), 1.0)
+    b = uniform(r, (N,), 1.0)
+    w_d, x_d, b_d = dev(w, gpu), dev(x, gpu), dev(b, gpu)
+    y = unwritten((M, N), gpu)
+    sdhip.set_tuning(tuning)
+    try:
+        sdhip.mul_mat(w_d, x_d, y, sdhip.epilogue([("add", b_d)]))
+        torch.cuda.synchronize()
+    finally:
+        sdhip.set_tuning("")
+    got = y.cpu().numpy()
+    want = (orc.quantized_mul_mat(w, x, group, levels, wmax, wg)[0] + b).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    exact, mag = orc.exact_mul_mat(w, x)
+    assert orc.metric(got, exact + b, mag + np.abs(b)) <= bound(levels, wmax)

@@ -73,11 +73,11 @@ def test_tuning_takes_every_reference_name_and_checks_its_own():
     try:
         sdhip.set_tuning("conv_kc=128,amx_fp16=0,fuse_residual=0,todo=2,todo_tokens=100,group=1000,bits=3")
         assert sdhip.get_tuning("conv_kc") == 128 and sdhip.get_tuning("todo_tokens") == 100
-        for bad in ("gemm_stages=3", "gemm_tiles=12", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
+        for bad in ("gemm_stages=3", "gemm_tiles=13", "gemm_core=3", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
                     "winograd_splits=-2", "bits=16", "fuse=99999999999"):
             with pytest.raises(sdhip.SdhipError):
                 sdhip.set_tuning(bad)
-        for good in ("gemm_stages=4", "gemm_tiles=21", "winograd_fp32=1", "winograd_splits=3", "bits=8"):
+        for good in ("gemm_stages=4", "gemm_tiles=21", "gemm_tiles=12", "gemm_core=1", "winograd_fp32=1", "winograd_splits=3", "bits=8"):
             sdhip.set_tuning(good)
     finally:
         sdhip.set_tuning("")
@@ -107,8 +107,8 @@ def test_mul_mat_predicate():
     # Fewer than 16 rows, or K under 16, are left to the caller (mul_mat.cc:192-193).
     assert not lib.sdhip_mul_mat_supported(w, tensor(F32, (15, 320)), tensor(F32, (15, 320)))
     assert not lib.sdhip_mul_mat_supported(tensor(F16, (8, 8)), tensor(F32, (40, 8)), tensor(F32, (40, 8)))
-    # Single-precision weights are not taken by this form.
-    assert not lib.sdhip_mul_mat_supported(tensor(F32, (320, 320)), x, y)
+    # Single-precision weights are taken, as the reference takes them (mul_mat.cc:190).
+    assert lib.sdhip_mul_mat_supported(tensor(F32, (320, 320)), x, y)
     try:
         sdhip.set_tuning("bits=8")
         assert lib.sdhip_mul_mat_work_size(w, x, y) > 0
@@ -192,3 +192,24 @@ def test_bench_refuses_several_gpus():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_single_precision_weights_taken():
+    """MUL_MAT and CONV_2D take single-precision weights as the reference
+    does (mul_mat.cc:190; conv2d.cc:325-326); a 3x3 kernel of single
+    precision takes F(2x2) where an FP16 one takes F(4x4)
+    (winograd.cc:1204-1206).  Descriptors only: nothing is computed."""
+    lib = sdhip.load()
+    w = tensor(sdhip.TYPE_F32, (17, 32))
+    x = tensor(sdhip.TYPE_F32, (40, 32))
+    y = tensor(sdhip.TYPE_F32, (40, 17))
+    assert lib.sdhip_mul_mat_supported(w, x, y) == 1
+    assert lib.sdhip_mul_mat_work_size(w, x, y) > 0  # the split weights
+    k32 = tensor(sdhip.TYPE_F32, (320, 320, 3, 3))
+    k16 = tensor(sdhip.TYPE_F16, (320, 320, 3, 3))
+    img = tensor(sdhip.TYPE_F32, (2, 320, 64, 64))
+    out = tensor(sdhip.TYPE_F32, (2, 320, 64, 64))
+    params = sdhip.conv_params(1, 1, 1, 1, 1, 1)
+    assert lib.sdhip_conv2d_supported(k32, img, out, params) == 1
+    assert lib.sdhip_conv2d_path(k16, img, out, params) == 4
+    assert lib.sdhip_conv2d_path(k32, img, out, params) == 2
