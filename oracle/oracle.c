@@ -390,6 +390,30 @@ void oracle_quantize_weights(const float *w, int64_t ld, int64_t rows, int64_t k
     }
 }
 
+/* qgemm (quant.cc:113-164): y[m][n] = init (or 0), then per group g in order
+ * t = fma(sa sb, S, t); t = fma(-oa, ob, t), S the exact integer sum of the
+ * group's products; operands [rows][groups * group], scales and offsets
+ * [rows][groups]. */
+void oracle_qgemm(const uint8_t *xq, const float *xs, const float *xo, const int8_t *wq, const float *ws,
+                  const float *wo, int64_t M, int64_t N, int64_t groups, int64_t group, const float *init, float *y) {
+    const int64_t kp = groups * group;
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float t = init ? init[m * N + n] : 0.0f;
+            for (int64_t g = 0; g < groups; ++g) {
+                int32_t s = 0;
+                const uint8_t *a = xq + m * kp + g * group;
+                const int8_t *b = wq + n * kp + g * group;
+                for (int64_t e = 0; e < group; ++e) s += (int32_t)a[e] * (int32_t)b[e];
+                const float ab = xs[m * groups + g] * ws[n * groups + g];
+                t = fmaf(ab, (float)s, t);
+                t = fmaf(-xo[m * groups + g], wo[n * groups + g], t);
+            }
+            y[m * N + n] = t;
+        }
+    }
+}
+
 void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t N, int64_t K, int64_t group,
                               int input_levels, int weight_max, int weight_groups, const float *init, float *y,
                               uint8_t *xq, float *xscale, float *xoffset, int8_t *wq, float *wscale, float *woffset,
@@ -411,21 +435,7 @@ void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t
         }
     }
     oracle_quantize_weights(w, K, N, K, group, weight_max, weight_groups, qw, sb, ob, qs);
-    for (int64_t m = 0; m < M; ++m) {
-        for (int64_t n = 0; n < N; ++n) {
-            float t = init ? init[m * N + n] : 0.0f;
-            for (int64_t g = 0; g < groups; ++g) {
-                int32_t s = 0;
-                const uint8_t *a = qx + m * kp + g * group;
-                const int8_t *b = qw + n * kp + g * group;
-                for (int64_t e = 0; e < group; ++e) s += (int32_t)a[e] * (int32_t)b[e];
-                const float ab = sa[m * groups + g] * sb[n * groups + g];
-                t = fmaf(ab, (float)s, t);
-                t = fmaf(-oa[m * groups + g], ob[n * groups + g], t);
-            }
-            y[m * N + n] = t;
-        }
-    }
+    oracle_qgemm(qx, sa, oa, qw, sb, ob, M, N, groups, group, init, y);
     if (!xq) free(qx);
     if (!xscale) free(sa);
     if (!xoffset) free(oa);
@@ -517,4 +527,177 @@ void oracle_quantized_attention(const float *q, const float *k, const float *v, 
     }
     free(kq); free(ks); free(ko); free(ksum); free(vt); free(vq); free(vs); free(vo); free(vsum);
     free(krow); free(scores); free(qq); free(eq); free(t);
+}
+
+/* ------------------------------------------------------------------ bits mode: convolutions */
+
+/* The columns of a direct convolution (conv2d.cc:228-316): position p = (n,
+ * oy, ox), k = ic KH KW + kh KW + kw, zeros outside the image. */
+static float column_at(const float *x, int64_t ic, int64_t ih, int64_t iw, int64_t kh, int64_t kw, int s0, int s1, int p0,
+                       int p1, int d0, int d1, int64_t oh, int64_t ow, int64_t p, int64_t k) {
+    const int64_t n = p / (oh * ow), r = p % (oh * ow), oy = r / ow, ox = r % ow;
+    const int64_t c = k / (kh * kw), t = k % (kh * kw), y = oy * s1 - p1 + (t / kw) * d1, xx = ox * s0 - p0 + (t % kw) * d0;
+    return (y >= 0 && y < ih && xx >= 0 && xx < iw) ? x[((n * ic + c) * ih + y) * iw + xx] : 0.0f;
+}
+
+void oracle_quantized_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
+                             int64_t kh, int64_t kw, int s0, int s1, int p0, int p1, int d0, int d1, int64_t oh,
+                             int64_t ow, int64_t group, int input_levels, int weight_max, int weight_groups,
+                             const float *init, float *y) {
+    const int64_t K = ic * kh * kw, P = n * oh * ow;
+    float *cols = (float *)malloc((size_t)(P * K) * sizeof(float));
+    float *t = (float *)malloc((size_t)(P * oc) * sizeof(float));
+    float *it = init ? (float *)malloc((size_t)(P * oc) * sizeof(float)) : NULL;
+    for (int64_t p = 0; p < P; ++p)
+        for (int64_t k = 0; k < K; ++k)
+            cols[p * K + k] = column_at(x, ic, ih, iw, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, p, k);
+    for (int64_t p = 0; p < P; ++p) {
+        const int64_t b = p / (oh * ow), r = p % (oh * ow);
+        for (int64_t o = 0; o < oc; ++o) {
+            if (it) it[p * oc + o] = init[(b * oc + o) * oh * ow + r];
+        }
+    }
+    oracle_quantized_mul_mat(w, cols, P, oc, K, group, input_levels, weight_max, weight_groups, it, t, NULL, NULL,
+                             NULL, NULL, NULL, NULL, NULL);
+    for (int64_t p = 0; p < P; ++p) {
+        const int64_t b = p / (oh * ow), r = p % (oh * ow);
+        for (int64_t o = 0; o < oc; ++o) y[(b * oc + o) * oh * ow + r] = t[p * oc + o];
+    }
+    free(cols);
+    free(t);
+    free(it);
+}
+
+/* Row i of F(2x2)'s B^T of four numbers (winograd.cc:321-332). */
+static float bt2(int i, float d0, float d1, float d2, float d3) {
+    switch (i) {
+    case 0: return d0 - d2;
+    case 1: return d1 + d2;
+    case 2: return d2 - d1;
+    default: return d1 - d3;
+    }
+}
+
+/* F(2x2, 3x3) with quantized products (winograd.cc:1826-2103): V = B^T d B
+ * as transform_inputs_small computes it (each row of d by bt(s), then the
+ * rows by bt(r), winograd.cc:631-672), U = G g G^T as transform_weights does
+ * (G g a column at a time, then (G g) G^T a row at a time, each sum of three
+ * left to right and halved after, winograd.cc:681-729); for each of the 16
+ * points, the tiles' V quantized per (tile, group of input channels) and the
+ * output channels' U per (channel, group), or per stretch of `stretch` input
+ * channels with weight_groups = 0 (the scale of the stretch's greatest, as the
+ * weights of a stretch are quantized at a time, winograd.cc:1917-1930); the
+ * quantized products M per point (qgemm); then Y = A^T M A as
+ * transform_outputs sums it (winograd.cc:509-623), added to y where
+ * from_redirect.  x [n][ic][ih][iw], w [oc][ic][3][3]; y [n][oc][oh][ow]. */
+void oracle_quantized_winograd2(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w,
+                                int64_t oc, int p0, int p1, int64_t oh, int64_t ow, int64_t group, int input_levels,
+                                int weight_max, int weight_groups, int64_t stretch, int from_redirect, float *y) {
+    const int64_t tw = (ow + 1) / 2, th = (oh + 1) / 2, tiles = n * tw * th;
+    const int64_t groups = (ic + group - 1) / group, kp = groups * group;
+    float *v = (float *)malloc((size_t)(16 * tiles * ic) * sizeof(float));
+    float *u = (float *)malloc((size_t)(16 * oc * ic) * sizeof(float));
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t ty = 0; ty < th; ++ty)
+            for (int64_t tx = 0; tx < tw; ++tx)
+                for (int64_t c = 0; c < ic; ++c) {
+                    const int64_t tile = (b * th + ty) * tw + tx;
+                    float d[4][4];
+                    for (int i = 0; i < 4; ++i)
+                        for (int j = 0; j < 4; ++j) {
+                            const int64_t yy = 2 * ty - p1 + i, xx = 2 * tx - p0 + j;
+                            d[i][j] = (yy >= 0 && yy < ih && xx >= 0 && xx < iw) ? x[((b * ic + c) * ih + yy) * iw + xx]
+                                                                                   : 0.0f;
+                        }
+                    for (int s4 = 0; s4 < 4; ++s4) {
+                        float row[4];
+                        for (int i = 0; i < 4; ++i) row[i] = bt2(s4, d[i][0], d[i][1], d[i][2], d[i][3]);
+                        for (int r = 0; r < 4; ++r)
+                            v[((int64_t)(r * 4 + s4) * tiles + tile) * ic + c] = bt2(r, row[0], row[1], row[2], row[3]);
+                    }
+                }
+    for (int64_t o = 0; o < oc; ++o)
+        for (int64_t c = 0; c < ic; ++c) {
+            const float *g = w + (o * ic + c) * 9;
+            float t[4][3];
+            for (int j = 0; j < 3; ++j) {
+                const float g0 = g[0 * 3 + j], g1 = g[1 * 3 + j], g2 = g[2 * 3 + j];
+                t[0][j] = g0;
+                t[1][j] = 0.5f * (g0 + g1 + g2);
+                t[2][j] = 0.5f * (g0 - g1 + g2);
+                t[3][j] = g2;
+            }
+            for (int i = 0; i < 4; ++i) {
+                const float a = t[i][0], bb = t[i][1], dd = t[i][2];
+                u[((int64_t)(i * 4 + 0) * oc + o) * ic + c] = a;
+                u[((int64_t)(i * 4 + 1) * oc + o) * ic + c] = 0.5f * (a + bb + dd);
+                u[((int64_t)(i * 4 + 2) * oc + o) * ic + c] = 0.5f * (a - bb + dd);
+                u[((int64_t)(i * 4 + 3) * oc + o) * ic + c] = dd;
+            }
+        }
+    uint8_t *xq = (uint8_t *)malloc((size_t)(tiles * kp));
+    float *xs = (float *)malloc((size_t)(tiles * groups) * sizeof(float));
+    float *xo = (float *)malloc((size_t)(tiles * groups) * sizeof(float));
+    int8_t *wq = (int8_t *)malloc((size_t)(oc * kp));
+    float *ws = (float *)malloc((size_t)(oc * groups) * sizeof(float));
+    float *wo = (float *)malloc((size_t)(oc * groups) * sizeof(float));
+    int32_t *wsum = (int32_t *)malloc((size_t)(oc * groups) * sizeof(int32_t));
+    const int64_t sg = stretch / group;  /* groups of a stretch */
+    int8_t *tq = (int8_t *)malloc((size_t)(oc * sg * group));
+    float *ts = (float *)malloc((size_t)(oc * sg) * sizeof(float));
+    float *to = (float *)malloc((size_t)(oc * sg) * sizeof(float));
+    int32_t *tsum = (int32_t *)malloc((size_t)(oc * sg) * sizeof(int32_t));
+    float *m = (float *)malloc((size_t)(16 * tiles * oc) * sizeof(float));
+    for (int xi = 0; xi < 16; ++xi) {
+        const float *vx = v + (int64_t)xi * tiles * ic;
+        const float *ux = u + (int64_t)xi * oc * ic;
+        for (int64_t t = 0; t < tiles; ++t)
+            for (int64_t g = 0; g < groups; ++g) {
+                const int64_t cnt = ic - g * group < group ? ic - g * group : group;
+                oracle_quantize_input_row(vx + t * ic + g * group, cnt, group, input_levels, xq + t * kp + g * group,
+                                          &xs[t * groups + g], &xo[t * groups + g]);
+            }
+        if (weight_groups) {
+            oracle_quantize_weights(ux, ic, oc, ic, group, weight_max, 1, wq, ws, wo, wsum);
+        } else {
+            for (int64_t k0 = 0; k0 < ic; k0 += stretch) {
+                const int64_t kc = ic - k0 < stretch ? ic - k0 : stretch;
+                const int64_t kg = (kc + group - 1) / group;
+                oracle_quantize_weights(ux + k0, ic, oc, kc, group, weight_max, 0, tq, ts, to, tsum);
+                for (int64_t o = 0; o < oc; ++o) {
+                    memcpy(wq + o * kp + k0, tq + o * kg * group, (size_t)(kg * group));
+                    for (int64_t g = 0; g < kg; ++g) {
+                        ws[o * groups + k0 / group + g] = ts[o * kg + g];
+                        wo[o * groups + k0 / group + g] = to[o * kg + g];
+                        wsum[o * groups + k0 / group + g] = tsum[o * kg + g];
+                    }
+                }
+            }
+        }
+        oracle_qgemm(xq, xs, xo, wq, ws, wo, tiles, oc, groups, group, NULL, m + (int64_t)xi * tiles * oc);
+    }
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t o = 0; o < oc; ++o)
+            for (int64_t ty = 0; ty < th; ++ty)
+                for (int64_t tx = 0; tx < tw; ++tx) {
+                    const int64_t tile = (b * th + ty) * tw + tx;
+                    float vv[16];
+                    for (int xi = 0; xi < 16; ++xi) vv[xi] = m[((int64_t)xi * tiles + tile) * oc + o];
+                    float a0[4], a1[4];
+                    for (int j = 0; j < 4; ++j) {
+                        a0[j] = vv[0 * 4 + j] + vv[1 * 4 + j] + vv[2 * 4 + j];
+                        a1[j] = vv[1 * 4 + j] - vv[2 * 4 + j] - vv[3 * 4 + j];
+                    }
+                    const float out[2][2] = {{a0[0] + a0[1] + a0[2], a0[1] - a0[2] - a0[3]},
+                                             {a1[0] + a1[1] + a1[2], a1[1] - a1[2] - a1[3]}};
+                    for (int i = 0; i < 2; ++i)
+                        for (int j = 0; j < 2; ++j) {
+                            const int64_t yy = 2 * ty + i, xx = 2 * tx + j;
+                            if (yy >= oh || xx >= ow) continue;
+                            float *p = y + ((b * oc + o) * oh + yy) * ow + xx;
+                            *p = from_redirect ? *p + out[i][j] : out[i][j];
+                        }
+                }
+    free(v); free(u); free(xq); free(xs); free(xo); free(wq); free(ws); free(wo); free(wsum);
+    free(tq); free(ts); free(to); free(tsum); free(m);
 }

@@ -114,6 +114,34 @@ void oracle_quantized_mul_mat(const float *w, const float *x, int64_t M, int64_t
                               uint8_t *xq, float *xscale, float *xoffset, int8_t *wq, float *wscale, float *woffset,
                               int32_t *wsums);
 
+/* The quantized product of operands already quantized (quant.cc:113-164):
+ * y[m*N + n] = init (or 0) + per group g in order t = fma(xs*ws, S, t);
+ * t = fma(-xo, wo, t); operands [rows][groups*group]. */
+void oracle_qgemm(const uint8_t *xq, const float *xs, const float *xo, const int8_t *wq, const float *ws,
+                  const float *wo, int64_t M, int64_t N, int64_t groups, int64_t group, const float *init, float *y);
+
+/* The quantized direct convolution (conv2d.cc:338-483): the columns of each
+ * output position (k = ic KH KW + kh KW + kw, zeros outside the image)
+ * quantized as the linear layers' inputs per (position, group), the kernels
+ * as their weights per (output channel, group) or per whole row, the
+ * products summed as qgemm, begun from init (the residual's own layout,
+ * [n][oc][oh][ow], with from_redirect) or 0.  x [n][ic][ih][iw], w
+ * [oc][ic][kh][kw]; y [n][oc][oh][ow]. */
+void oracle_quantized_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
+                             int64_t kh, int64_t kw, int s0, int s1, int p0, int p1, int d0, int d1, int64_t oh,
+                             int64_t ow, int64_t group, int input_levels, int weight_max, int weight_groups,
+                             const float *init, float *y);
+
+/* Winograd F(2x2, 3x3) with quantized products (winograd.cc:1826-2103), the
+ * form every Winograd convolution takes in the bits mode: the reference's
+ * transforms in its order of single-precision operations, the points'
+ * operands quantized per (tile, group) and per (output channel, group) -- or
+ * per stretch of `stretch` input channels with weight_groups = 0 -- their
+ * products as qgemm, the outputs' transform, added to y with from_redirect. */
+void oracle_quantized_winograd2(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w,
+                                int64_t oc, int p0, int p1, int64_t oh, int64_t ow, int64_t group, int input_levels,
+                                int weight_max, int weight_groups, int64_t stretch, int from_redirect, float *y);
+
 /* Self-attention with quantized products (attention.cc:612-824): keys
  * signed, one group over the head's d dimensions (group 4 ceil(d / 4)),
  * queries unsigned with a zero point likewise, the softmax scale folded into

@@ -77,6 +77,7 @@ struct ConvArgs {
     int32_t w_split;
     int64_t w_plane;
     const float *w_scale;
+    const float *w32;  // the kernel in single precision, for the bits mode's quantizer; null for FP16
     int64_t kw, kh, oc;
     float *y;  // [N][OC][OH][OW], strides ynb1..3
     int64_t ynb1, ynb2, ynb3;

@@ -7,6 +7,7 @@
 
 #include "host.h"
 #include "kernels.h"
+#include "quant.h"
 #include "winograd.h"
 
 namespace sdhip {
@@ -45,9 +46,9 @@ int64_t out_size(int64_t in, int64_t k, int32_t s, int32_t p, int32_t d) {
 }
 
 // Whether bits asks for the convolutions' products quantized (quantized(
-// Quantized_op::convolution), quant.cc:53-56): a form this library does not
-// have, so such convolutions are not taken -- the caller's own form computes
-// them, as ggml computes what the reference does not take.
+// Quantized_op::convolution), quant.cc:53-56): then the convolutions Winograd
+// takes are F(2x2) with quantized products (winograd.cc:2230-2244) and the
+// others direct ones with quantized products (conv2d.cc:338-483).
 bool conv_quantized() {
     const Tuning &t = tuning();
     return t.bits >= 2 && t.bits <= 8 && (t.quantize & 2) != 0;
@@ -55,7 +56,6 @@ bool conv_quantized() {
 
 bool direct_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
     if (kernel == nullptr || input == nullptr || y == nullptr || op == nullptr) return false;
-    if (conv_quantized()) return false;
     // FP16 or single-precision kernels (conv2d.cc:320-331).
     const bool weights = (holds_f16(kernel) || holds_f32(kernel)) && contiguous(kernel);
     if (!(weights && holds_f32(input) && holds_f32(y) && contiguous(y) && kernel->ne[2] == input->ne[2] &&
@@ -90,7 +90,8 @@ bool four(const Geometry &g, const sdhip_tensor *kernel) {
 int path_of(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y, const int32_t *op) {
     if (!direct_supported(kernel, input, y, op)) return -1;
     if (winograd_taken(kernel, input, y, op)) {
-        return four(geometry(kernel, input, y, op), kernel) ? 4 : 2;
+        // The bits mode's Winograd is F(2x2) (winograd.cc:2236-2244 before four()).
+        return !conv_quantized() && four(geometry(kernel, input, y, op), kernel) ? 4 : 2;
     }
     return 0;
 }
@@ -107,6 +108,7 @@ ConvArgs conv_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const 
     c.ic = input->ne[2];
     c.n = input->ne[3];
     c.w = kernel->type == SDHIP_TYPE_F16 ? static_cast<const _Float16 *>(kernel->data) : nullptr;
+    c.w32 = kernel->type == SDHIP_TYPE_F32 ? static_cast<const float *>(kernel->data) : nullptr;
     c.kw = kernel->ne[0];
     c.kh = kernel->ne[1];
     c.oc = kernel->ne[3];
@@ -186,6 +188,9 @@ int sdhip_conv2d_path(const sdhip_tensor *kernel, const sdhip_tensor *input, con
 size_t sdhip_conv2d_work_size(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
                               const int32_t op_params[6]) {
     const int path = path_of(kernel, input, y, op_params);
+    if (path >= 0 && conv_quantized()) {
+        return quantized_conv_work_size(conv_args(kernel, input, y, op_params), path == 2);
+    }
     if (path == 2 || path == 4) {
         return winograd_work_size(winograd_args(kernel, input, y, op_params, path));
     }
@@ -211,6 +216,18 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
     sdhip_status s = chain_plan(y, chain, run);
     if (s != SDHIP_OK) return s;
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (conv_quantized()) {
+        ConvArgs c = conv_args(kernel, input, y, op_params);
+        c.y = run.out;
+        c.from_redirect = run.from_redirect;
+        c.chain = run.fused;
+        const size_t need = quantized_conv_work_size(c, path == 2);
+        if (work == nullptr || work_size < need) {
+            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
+        }
+        s = quantized_conv(c, path == 2, work, st);
+        return s == SDHIP_OK ? chain_after(run, st) : s;
+    }
     if (path == 2 || path == 4) {
         WinogradArgs a = winograd_args(kernel, input, y, op_params, path);
         a.y = run.out;

@@ -22,4 +22,11 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
 
 bool mul_mat_quantized(const sdhip_tensor *x);
 
+// CONV_2D in the bits mode (quantize & 2): the direct convolution's products
+// quantized (conv2d.cc:338-483), or, for the convolutions Winograd takes,
+// F(2x2, 3x3) with quantized products (winograd.cc:1826-2103).  `c` as the
+// direct convolution's (the kernel FP16 in w, or single precision in w32).
+size_t quantized_conv_work_size(const ConvArgs &c, bool winograd);
+sdhip_status quantized_conv(const ConvArgs &c, bool winograd, void *work, hipStream_t stream);
+
 }  // namespace sdhip

@@ -99,11 +99,20 @@ __device__ __forceinline__ float clampf(float v, float lo, float hi) { return v 
 
 // ------------------------------------------------------------------ inputs
 
+// The rows of the inputs: x[m][k], rows ldx apart.
+struct RowsSrc {
+    const float *x;
+    int64_t ldx;
+    __device__ float operator()(int64_t m, int64_t k) const { return x[m * ldx + k]; }
+};
+
 // One wave per (row, group): the group's least and greatest (with 0), its
-// scale and zero point, and its bytes, stored as q - 128.
-__global__ __launch_bounds__(256) void quantize_inputs_kernel(const float *__restrict__ x, int64_t ldx, int64_t M,
-                                                              int64_t K, Quant q, Layout l, int8_t *__restrict__ xq,
-                                                              float *__restrict__ xs, float *__restrict__ xo) {
+// scale and zero point, and its bytes, stored as q - 128.  Src gives the
+// inputs' numbers: rows of x, or a convolution's columns.
+template <class Src>
+__global__ __launch_bounds__(256) void quantize_inputs_kernel(Src src, int64_t M, int64_t K, Quant q, Layout l,
+                                                              int8_t *__restrict__ xq, float *__restrict__ xs,
+                                                              float *__restrict__ xo) {
     const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (item >= M * l.groups) return;
     const int lane = threadIdx.x & 63;
@@ -111,11 +120,12 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(const float *__res
     const int64_t g = item - m * l.groups;
     const int64_t k0 = g * q.group;
     const int64_t n = K - k0 < q.group ? K - k0 : q.group;
-    const float *row = x + m * ldx + k0;
+    const auto row = [&](int64_t e) { return src(m, k0 + e); };
     float lo = 0.0f, hi = 0.0f;
     for (int64_t e = lane; e < n; e += 64) {
-        lo = fminf(lo, row[e]);
-        hi = fmaxf(hi, row[e]);
+        const float v = row(e);
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
     }
     lo = wave_min(lo);
     hi = wave_max(hi);
@@ -127,7 +137,7 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(const float *__res
     for (int64_t e = lane; e < l.slot; e += 64) {
         float v = 0.0f;
         if (e < n) {
-            v = clampf(__fadd_rn(rintf(__fmul_rn(row[e], inverse)), zero), 0.0f, levels);
+            v = clampf(__fadd_rn(rintf(__fmul_rn(row(e), inverse)), zero), 0.0f, levels);
         } else if (e < q.group) {
             v = zero;  // the group's tail stands for zeros
         } else {
@@ -148,24 +158,36 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(const float *__res
 // bytes and their sum.
 // W: the weights' type, FP16 or single precision (quantize_weights_f16 and
 // _f32, quant.cc:366-380: the same quantizer of their widened values).
+// `stretch`, with one scale a row (weight_groups = 0): the stretches of k
+// the row is quantized in, a multiple of the group, their scale the
+// stretch's greatest (Winograd's weights, quantized a stretch of input
+// channels at a time, winograd.cc:1917-1930); 0 for the whole row.
 template <class W>
 __global__ __launch_bounds__(256) void quantize_weights_kernel(const W *__restrict__ w, int64_t ldw, int64_t N,
                                                                int64_t K, Quant q, Layout l, int8_t *__restrict__ wq,
                                                                float *__restrict__ ws, float *__restrict__ wo,
-                                                               int32_t *__restrict__ wsum) {
+                                                               int32_t *__restrict__ wsum, int64_t stretch) {
     const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
     const int lane = threadIdx.x & 63;
     const W *row = w + n * ldw;
     float row_max = 0.0f;
-    if (!q.weight_groups) {
-        for (int64_t e = lane; e < K; e += 64) row_max = fmaxf(row_max, fabsf(static_cast<float>(row[e])));
-        row_max = wave_max(row_max);
-    }
+    int64_t stretch_of = -1;  // the stretch row_max is of
     const float wmax = static_cast<float>(q.wmax);
     for (int64_t g = 0; g < l.groups; ++g) {
         const int64_t k0 = g * q.group;
         const int64_t cnt = K - k0 < q.group ? K - k0 : q.group;
+        if (!q.weight_groups) {
+            const int64_t st = stretch > 0 ? k0 / stretch : 0;
+            if (st != stretch_of) {
+                const int64_t s0 = stretch > 0 ? st * stretch : 0;
+                const int64_t s1 = stretch > 0 && s0 + stretch < K ? s0 + stretch : K;
+                float mm = 0.0f;
+                for (int64_t e = s0 + lane; e < s1; e += 64) mm = fmaxf(mm, fabsf(static_cast<float>(row[e])));
+                row_max = wave_max(mm);
+                stretch_of = st;
+            }
+        }
         float m = row_max;
         if (q.weight_groups) {
             float mm = 0.0f;
@@ -409,7 +431,325 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ convolutions
+
+// The columns of a direct convolution (conv2d.cc:228-316): position m = (n,
+// oy, ox), k = ic KH KW + kh KW + kw, zeros outside the image.
+struct ColumnsSrc {
+    ConvArgs c;
+    __device__ float operator()(int64_t m, int64_t k) const {
+        uint32_t ox, oy, n;
+        split_index(static_cast<uint32_t>(m), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
+        const int64_t ic = k / c.taps, t = k - ic * c.taps;
+        const int64_t kh = t / c.kw, kw = t - kh * c.kw;
+        const int64_t iy = static_cast<int64_t>(oy) * c.s1 - c.p1 + kh * c.d1;
+        const int64_t ix = static_cast<int64_t>(ox) * c.s0 - c.p0 + kw * c.d0;
+        if (iy < 0 || iy >= c.ih || ix < 0 || ix >= c.iw) return 0.0f;
+        return c.x[static_cast<int64_t>(n) * c.xnb3 + ic * c.xnb2 + iy * c.xnb1 + ix];
+    }
+};
+
+// t[p][oc] = y at (position p, channel oc): the residual the quantized sums
+// begin from (conv2d.cc:466-468, accumulate with from_redirect).
+__global__ __launch_bounds__(256) void conv_gather_kernel(ConvArgs c, float *__restrict__ t) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= c.P * c.oc) return;
+    const int64_t p = i / c.oc, oc = i - p * c.oc;
+    uint32_t ox, oy, n;
+    split_index(static_cast<uint32_t>(p), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
+    t[i] = c.y[static_cast<int64_t>(n) * c.ynb3 + oc * c.ynb2 + static_cast<int64_t>(oy) * c.ynb1 + ox];
+}
+
+// y at (p, oc) = the chain of t[p][oc] over the positions of channel oc
+// (apply_chain_positions, conv2d.cc:472-474).
+__global__ __launch_bounds__(256) void conv_scatter_kernel(ConvArgs c, const float *__restrict__ t) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= c.P * c.oc) return;
+    const int64_t oc = i / c.P, p = i - oc * c.P;  // consecutive threads: consecutive positions
+    uint32_t ox, oy, n;
+    split_index(static_cast<uint32_t>(p), static_cast<uint32_t>(c.ow), static_cast<uint32_t>(c.oh), ox, oy, n);
+    float v[1] = {t[p * c.oc + oc]};
+    const int64_t in_image = static_cast<int64_t>(oy) * c.ow + ox;
+    apply_chain_block<1>(c.chain, v, [&](int s, int) -> int64_t {
+        const DevStep &st = c.chain.steps[s];
+        const int64_t xy =
+            st.flat01 ? in_image * st.nb[0] : static_cast<int64_t>(ox) * st.nb[0] + static_cast<int64_t>(oy) * st.nb[1];
+        return xy + static_cast<int64_t>(n) * st.nb[3] + oc * st.nb[2];
+    });
+    c.y[static_cast<int64_t>(n) * c.ynb3 + oc * c.ynb2 + static_cast<int64_t>(oy) * c.ynb1 + ox] = v[0];
+}
+
+// Row i of F(2x2)'s B^T of four numbers (winograd.cc:321-332).
+__device__ __forceinline__ float bt2(int i, float d0, float d1, float d2, float d3) {
+    return i == 0 ? __fsub_rn(d0, d2) : i == 1 ? __fadd_rn(d1, d2) : i == 2 ? __fsub_rn(d2, d1) : __fsub_rn(d1, d3);
+}
+
+// The transformed inputs of F(2x2) in single precision, as the reference's
+// transform_inputs_small computes them (each row of d by bt(s), then the rows
+// by bt(r), winograd.cc:631-672): v[xi][tile][ic], a thread per (tile,
+// channel).
+__global__ __launch_bounds__(256) void wq_inputs_kernel(ConvArgs c, int64_t tw, int64_t th, int64_t tiles,
+                                                        float *__restrict__ v) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= tiles * c.ic) return;
+    const int64_t tile = i / c.ic, ic = i - tile * c.ic;
+    const int64_t per = tw * th;
+    const int64_t n = tile / per, r = tile - n * per, ty = r / tw, tx = r - ty * tw;
+    const float *plane = c.x + n * c.xnb3 + ic * c.xnb2;
+    float d[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int64_t y = 2 * ty - c.p1 + a, x = 2 * tx - c.p0 + b;
+            d[a][b] = (y >= 0 && y < c.ih && x >= 0 && x < c.iw) ? plane[y * c.xnb1 + x] : 0.0f;
+        }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+        float row[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) row[a] = bt2(s4, d[a][0], d[a][1], d[a][2], d[a][3]);
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) v[((r4 * 4 + s4) * tiles + tile) * c.ic + ic] = bt2(r4, row[0], row[1], row[2], row[3]);
+    }
+}
+
+// The transformed kernels of F(2x2) in single precision, as the reference's
+// transform_weights computes them (G g a column at a time, then (G g) G^T a
+// row at a time, each sum of three left to right and halved after,
+// winograd.cc:681-729): u[xi][oc][ic], a thread per (oc, channel).
+template <class W>
+__global__ __launch_bounds__(256) void wq_weights_kernel(const W *__restrict__ w, int64_t oc, int64_t ic,
+                                                         float *__restrict__ u) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= oc * ic) return;
+    const W *g = w + i * 9;
+    float t[4][3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const float g0 = static_cast<float>(g[j]), g1 = static_cast<float>(g[3 + j]), g2 = static_cast<float>(g[6 + j]);
+        t[0][j] = g0;
+        t[1][j] = __fmul_rn(0.5f, __fadd_rn(__fadd_rn(g0, g1), g2));
+        t[2][j] = __fmul_rn(0.5f, __fadd_rn(__fsub_rn(g0, g1), g2));
+        t[3][j] = g2;
+    }
+    const int64_t plane = oc * ic;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float a = t[r][0], b = t[r][1], d = t[r][2];
+        u[(r * 4 + 0) * plane + i] = a;
+        u[(r * 4 + 1) * plane + i] = __fmul_rn(0.5f, __fadd_rn(__fadd_rn(a, b), d));
+        u[(r * 4 + 2) * plane + i] = __fmul_rn(0.5f, __fadd_rn(__fsub_rn(a, b), d));
+        u[(r * 4 + 3) * plane + i] = d;
+    }
+}
+
+// Y = A^T M A of F(2x2) as the reference's transform_outputs sums it (rows 0
+// and 1 of A^T M, then their columns, left to right, winograd.cc:509-623),
+// added to y with from_redirect, then the chain over the positions; m
+// [xi][tile][oc], a thread per (oc, tile).
+__global__ __launch_bounds__(256) void wq_outputs_kernel(ConvArgs c, int64_t tw, int64_t th, int64_t tiles,
+                                                         const float *__restrict__ m) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= tiles * c.oc) return;
+    const int64_t tile = i / c.oc, oc = i - tile * c.oc;
+    const int64_t per = tw * th;
+    const int64_t n = tile / per, r = tile - n * per, ty = r / tw, tx = r - ty * tw;
+    float v[16];
+#pragma unroll
+    for (int xi = 0; xi < 16; ++xi) v[xi] = m[(xi * tiles + tile) * c.oc + oc];
+    float a0[4], a1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        a0[j] = __fadd_rn(__fadd_rn(v[j], v[4 + j]), v[8 + j]);
+        a1[j] = __fsub_rn(__fsub_rn(v[4 + j], v[8 + j]), v[12 + j]);
+    }
+    const float out[2][2] = {{__fadd_rn(__fadd_rn(a0[0], a0[1]), a0[2]), __fsub_rn(__fsub_rn(a0[1], a0[2]), a0[3])},
+                             {__fadd_rn(__fadd_rn(a1[0], a1[1]), a1[2]), __fsub_rn(__fsub_rn(a1[1], a1[2]), a1[3])}};
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int64_t oy = 2 * ty + a, ox = 2 * tx + b;
+            if (oy >= c.oh || ox >= c.ow) continue;
+            float *p = c.y + n * c.ynb3 + oc * c.ynb2 + oy * c.ynb1 + ox;
+            float val[1] = {c.from_redirect ? __fadd_rn(*p, out[a][b]) : out[a][b]};
+            const int64_t in_image = oy * c.ow + ox;
+            apply_chain_block<1>(c.chain, val, [&](int s, int) -> int64_t {
+                const DevStep &st = c.chain.steps[s];
+                const int64_t xy = st.flat01 ? in_image * st.nb[0] : ox * st.nb[0] + oy * st.nb[1];
+                return xy + n * st.nb[3] + oc * st.nb[2];
+            });
+            *p = val[0];
+        }
+}
+
+// The quantized product of rows [m0, m0 + rows) of the inputs' layout by
+// rows [n0, n0 + cols) of the weights' (qgemm), into t (rows ldt apart),
+// begun from t where from_redirect; no chain.
+hipError_t launch_qgemm_part(const Layout &l, int8_t *xq, float *xs, float *xo, int8_t *wq, float *ws, float *wo,
+                             int32_t *wsum, int64_t m0, int64_t rows, int64_t n0, int64_t cols, float *t, int64_t ldt,
+                             int32_t from_redirect, hipStream_t stream) {
+    QgemmArgs p{};
+    p.xq = xq + m0 * l.kp;
+    p.xs = xs + m0 * l.groups;
+    p.xo = xo + m0 * l.groups;
+    p.wq = wq + n0 * l.kp;
+    p.ws = ws + n0 * l.groups;
+    p.wo = wo + n0 * l.groups;
+    p.wsum = wsum + n0 * l.groups;
+    p.y = t;
+    p.ldy = ldt;
+    p.M = rows;
+    p.N = cols;
+    p.ne1 = rows;
+    p.ne2 = 1;
+    p.groups = l.groups;
+    p.slot = l.slot;
+    p.kp = l.kp;
+    p.from_redirect = from_redirect;
+    p.col_blocks = ceil_div(cols, kQB);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(rows, kQB) * p.col_blocks));
+    hipLaunchKernelGGL(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// ------------------------------------------------------------------ convolutions: host
+
+namespace {
+
+struct QconvLayout {
+    Layout q;       // the quantized operands
+    size_t t;       // direct: t[P][OC]; Winograd: M[16][tiles][OC]
+    size_t v, u;    // Winograd: V[16][tiles][IC], U[16][OC][IC] in single precision
+    size_t total;
+};
+
+QconvLayout qconv_layout(const ConvArgs &c, bool winograd, int64_t tiles, const Quant &q) {
+    QconvLayout l{};
+    size_t at = 0;
+    const auto take = [&](size_t bytes) {
+        const size_t here = at;
+        at += static_cast<size_t>(round_up(static_cast<int64_t>(bytes), 256));
+        return here;
+    };
+    if (winograd) {
+        l.q = layout_of(c.ic, 16 * c.oc, 16 * tiles, q);
+        const size_t qbase = take(l.q.total);
+        (void)qbase;  // the quantized operands first, at 0
+        l.t = take(static_cast<size_t>(16 * tiles * c.oc) * 4);
+        l.v = take(static_cast<size_t>(16 * tiles * c.ic) * 4);
+        l.u = take(static_cast<size_t>(16 * c.oc * c.ic) * 4);
+    } else {
+        l.q = layout_of(c.K, c.oc, c.P, q);
+        take(l.q.total);
+        l.t = take(static_cast<size_t>(c.P * c.oc) * 4);
+    }
+    l.total = at;
+    return l;
+}
+
+int64_t qtiles(const ConvArgs &c) { return c.n * ceil_div(c.ow, 2) * ceil_div(c.oh, 2); }
+
+// The stretch of input channels whose transformed weights are quantized at
+// a time (winograd.cc:1859-1866 with plan and plan_small, 236-266): the
+// blocks of input channels of the reference's single-precision plan, in
+// groups; weight_group = 0 gives each stretch a scale of its own.
+int64_t winograd_stretch(const ConvArgs &c, const Quant &q) {
+    const Tuning &t = tuning();
+    const bool small = c.n * ceil_div(c.ow, 2) * ceil_div(c.oh, 2) <= t.winograd_small_tiles;
+    const int64_t want = small ? (t.winograd_small_kc > 8 ? t.winograd_small_kc : 8) : t.winograd_kc;
+    const int64_t kc = c.ic < want ? c.ic : want;
+    const int64_t stretch = kc / q.group * q.group;
+    return stretch > q.group ? stretch : q.group;
+}
+
+}  // namespace
+
+size_t quantized_conv_work_size(const ConvArgs &c, bool winograd) {
+    return qconv_layout(c, winograd, qtiles(c), quant_of(tuning())).total;
+}
+
+sdhip_status quantized_conv(const ConvArgs &c, bool winograd, void *work, hipStream_t stream) {
+    const Quant q = quant_of(tuning());
+    const int64_t tiles = qtiles(c);
+    const QconvLayout L = qconv_layout(c, winograd, tiles, q);
+    const Layout &l = L.q;
+    char *base = static_cast<char *>(work);
+    int8_t *xq = reinterpret_cast<int8_t *>(base + l.xq);
+    float *xs = reinterpret_cast<float *>(base + l.xs);
+    float *xo = reinterpret_cast<float *>(base + l.xo);
+    int8_t *wq = reinterpret_cast<int8_t *>(base + l.wq);
+    float *ws = reinterpret_cast<float *>(base + l.ws);
+    float *wo = reinterpret_cast<float *>(base + l.wo);
+    int32_t *wsum = reinterpret_cast<int32_t *>(base + l.wsum);
+    float *t = reinterpret_cast<float *>(base + L.t);
+    const auto grid = [](int64_t n) { return dim3(static_cast<uint32_t>(ceil_div(n, 256))); };
+    if (!winograd) {
+        // conv2d.cc:338-483: the columns quantized per (position, group), the
+        // kernels per (output channel, group) or per whole row; the sums in
+        // t[p][oc], begun from the residual where from_redirect; then the
+        // chain into y.
+        {
+            KernelScope scope("qconv.quantize", stream);
+            hipLaunchKernelGGL(quantize_inputs_kernel<ColumnsSrc>, dim3(ceil_div(c.P * l.groups, 4)), dim3(256), 0,
+                               stream, ColumnsSrc{c}, c.P, c.K, q, l, xq, xs, xo);
+            if (c.w32 != nullptr) {
+                hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(c.oc, 4)), dim3(256), 0, stream, c.w32,
+                                   c.K, c.oc, c.K, q, l, wq, ws, wo, wsum, int64_t{0});
+            } else {
+                hipLaunchKernelGGL(quantize_weights_kernel<_Float16>, dim3(ceil_div(c.oc, 4)), dim3(256), 0, stream,
+                                   c.w, c.K, c.oc, c.K, q, l, wq, ws, wo, wsum, int64_t{0});
+            }
+            if (c.from_redirect) hipLaunchKernelGGL(conv_gather_kernel, grid(c.P * c.oc), dim3(256), 0, stream, c, t);
+        }
+        {
+            KernelScope scope("qconv.products", stream);
+            const hipError_t e = launch_qgemm_part(l, xq, xs, xo, wq, ws, wo, wsum, 0, c.P, 0, c.oc, t, c.oc,
+                                                   c.from_redirect, stream);
+            if (e != hipSuccess) return launched(e, "quantized conv2d products");
+        }
+        KernelScope scope("qconv.outputs", stream);
+        hipLaunchKernelGGL(conv_scatter_kernel, grid(c.P * c.oc), dim3(256), 0, stream, c, t);
+        return launched(hipGetLastError(), "quantized conv2d");
+    }
+    // winograd.cc:1826-2103: F(2x2) whatever F(4x4) would take; the points'
+    // operands quantized per (tile, group) and (output channel, group or
+    // stretch); sixteen quantized products; the outputs' transform and chain.
+    const int64_t tw = ceil_div(c.ow, 2), th = ceil_div(c.oh, 2);
+    float *v = reinterpret_cast<float *>(base + L.v);
+    float *u = reinterpret_cast<float *>(base + L.u);
+    {
+        KernelScope scope("qwinograd2.transforms", stream);
+        hipLaunchKernelGGL(wq_inputs_kernel, grid(tiles * c.ic), dim3(256), 0, stream, c, tw, th, tiles, v);
+        if (c.w32 != nullptr) {
+            hipLaunchKernelGGL(wq_weights_kernel<float>, grid(c.oc * c.ic), dim3(256), 0, stream, c.w32, c.oc, c.ic, u);
+        } else {
+            hipLaunchKernelGGL(wq_weights_kernel<_Float16>, grid(c.oc * c.ic), dim3(256), 0, stream, c.w, c.oc, c.ic,
+                               u);
+        }
+    }
+    {
+        KernelScope scope("qwinograd2.quantize", stream);
+        hipLaunchKernelGGL(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(16 * tiles * l.groups, 4)), dim3(256), 0,
+                           stream, RowsSrc{v, c.ic}, 16 * tiles, c.ic, q, l, xq, xs, xo);
+        hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(16 * c.oc, 4)), dim3(256), 0, stream, u, c.ic,
+                           16 * c.oc, c.ic, q, l, wq, ws, wo, wsum, winograd_stretch(c, q));
+    }
+    {
+        KernelScope scope("qwinograd2.products", stream);
+        for (int xi = 0; xi < 16; ++xi) {
+            const hipError_t e = launch_qgemm_part(l, xq, xs, xo, wq, ws, wo, wsum, xi * tiles, tiles, xi * c.oc, c.oc,
+                                                   t + xi * tiles * c.oc, c.oc, 0, stream);
+            if (e != hipSuccess) return launched(e, "quantized winograd products");
+        }
+    }
+    KernelScope scope("qwinograd2.outputs", stream);
+    hipLaunchKernelGGL(wq_outputs_kernel, grid(tiles * c.oc), dim3(256), 0, stream, c, tw, th, tiles, t);
+    return launched(hipGetLastError(), "quantized winograd");
+}
 
 size_t quantized_linear_work_size(int64_t K, int64_t N, int64_t M) {
     return layout_of(K, N, M, quant_of(tuning())).total;
@@ -445,17 +785,17 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     int32_t *wsum = reinterpret_cast<int32_t *>(wbase + (l.wsum - l.wq));
     {
         KernelScope scope("quantize_inputs", stream);
-        hipLaunchKernelGGL(quantize_inputs_kernel, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream, a.x,
-                           a.ldx, a.M, a.K, q, l, xq, xs, xo);
+        hipLaunchKernelGGL(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream,
+                           RowsSrc{a.x, a.ldx}, a.M, a.K, q, l, xq, xs, xo);
     }
     if (!ready) {
         KernelScope scope("quantize_weights", stream);
         if (a.w32 != nullptr) {
             hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w32,
-                               a.ldw32, a.N, a.K, q, l, wq, ws, wo, wsum);
+                               a.ldw32, a.N, a.K, q, l, wq, ws, wo, wsum, int64_t{0});
         } else {
             hipLaunchKernelGGL(quantize_weights_kernel<_Float16>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w,
-                               a.ldw, a.N, a.K, q, l, wq, ws, wo, wsum);
+                               a.ldw, a.N, a.K, q, l, wq, ws, wo, wsum, int64_t{0});
         }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return launched(err, "quantize_weights");

@@ -55,6 +55,9 @@ def lib():
         L.oracle_quantize_weights.argtypes = [_f, _L, _L, _L, _L, _I, _I, _s8, _f, _f, _i32]
         L.oracle_quantized_mul_mat.argtypes = [_f, _f, _L, _L, _L, _L, _I, _I, _I, ctypes.c_void_p, _f,
                                                _u8, _f, _f, _s8, _f, _f, _i32]
+        L.oracle_quantized_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L, _L,
+                                              _I, _I, _I, ctypes.c_void_p, _f]
+        L.oracle_quantized_winograd2.argtypes = [_f, _L, _L, _L, _L, _f, _L, _I, _I, _L, _L, _L, _I, _I, _I, _L, _I, _f]
         L.oracle_quantized_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _L, _I, _I, _L, _f]
         _lib = L
     return _lib
@@ -286,4 +289,37 @@ def quantized_attention(q, k, v, scale, group=64, input_levels=255, weight_max=1
     y = np.zeros((b, lq, h, dv), np.float32)
     lib().oracle_quantized_attention(q, k, v, d, dv, lq, lk, h, hk, b, scale, group, input_levels, weight_max,
                                      key_block, y)
+    return y
+
+
+def quantized_conv2d(x, w, s0, s1, p0, p1, d0, d1, group=64, levels=255, wmax=127, weight_groups=1, init=None):
+    """The reference's bits-mode direct convolution (conv2d.cc:338-483), bit
+    for bit: x [n, ic, ih, iw], w [oc, ic, kh, kw] -> y [n, oc, oh, ow],
+    begun from init (the residual) if given."""
+    x, w = c32(x), c32(w)
+    n, ic, ih, iw = x.shape
+    oc, _, kh, kw = w.shape
+    oh = (ih + 2 * p1 - d1 * (kh - 1) - 1) // s1 + 1
+    ow = (iw + 2 * p0 - d0 * (kw - 1) - 1) // s0 + 1
+    y = np.zeros((n, oc, oh, ow), np.float32)
+    ip = None
+    if init is not None:
+        init = c32(init)
+        ip = init.ctypes.data_as(ctypes.c_void_p)
+    lib().oracle_quantized_conv2d(x, n, ic, ih, iw, w, oc, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, group, levels, wmax,
+                                  weight_groups, ip, y)
+    return y
+
+
+def quantized_winograd2(x, w, p0, p1, group=64, levels=255, wmax=127, weight_groups=1, stretch=64, init=None):
+    """The reference's bits-mode Winograd F(2x2) (winograd.cc:1826-2103), bit
+    for bit: x [n, ic, ih, iw], w [oc, ic, 3, 3] -> y [n, oc, oh, ow], added to
+    init (the residual, from_redirect) if given."""
+    x, w = c32(x), c32(w)
+    n, ic, ih, iw = x.shape
+    oc = w.shape[0]
+    oh, ow = ih + 2 * p1 - 2, iw + 2 * p0 - 2
+    y = np.zeros((n, oc, oh, ow), np.float32) if init is None else np.array(c32(init), copy=True)
+    lib().oracle_quantized_winograd2(x, n, ic, ih, iw, w, oc, p0, p1, oh, ow, group, levels, wmax, weight_groups,
+                                     stretch, 0 if init is None else 1, y)
     return y

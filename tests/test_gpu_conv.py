@@ -331,3 +331,17 @@ def test_conv2d_strided_input(gpu, c, want_path, small_path):
     err = orc.metric(y_d.cpu().numpy(), exact, mag)
     print(f"strided input {c} path {path}: {err:.3g}")
     assert err <= BOUND
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [(64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), (65, 33, 24, 20, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+                               (96, 16, 32, 17, 3, 3, 1, 1, 1, 1, 1, 1, 1)], ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("tiles", [0, 11, 12, 21, 22])
+def test_winograd_products_cores_agree(gpu, c, tiles):
+    """Winograd's products by the core whose copies into LDS global_load_lds
+    makes (gemm_core=2) give the bits of the register-staged core, at every
+    block shape."""
+    _, _, y1, path, _ = conv_case(gpu, c, seed=sum(c), tuning="gemm_core=1")
+    _, _, y2, _, _ = conv_case(gpu, c, seed=sum(c), tuning=f"gemm_core=2,gemm_tiles={tiles}")
+    assert path in (2, 4)
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))

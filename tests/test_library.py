@@ -213,3 +213,25 @@ def test_single_precision_weights_taken():
     assert lib.sdhip_conv2d_supported(k32, img, out, params) == 1
     assert lib.sdhip_conv2d_path(k16, img, out, params) == 4
     assert lib.sdhip_conv2d_path(k32, img, out, params) == 2
+
+
+def test_quantized_convolutions_taken():
+    """In the bits mode (quantize & 2) convolutions are taken: those Winograd
+    takes as F(2x2) with quantized products, even where single precision
+    takes F(4x4) (winograd.cc:2230-2244); the others directly
+    (conv2d.cc:338-483); each with a work buffer for its quantized operands."""
+    lib = sdhip.load()
+    k16 = tensor(F16, (320, 320, 3, 3))
+    img = tensor(F32, (2, 320, 64, 64))
+    out = tensor(F32, (2, 320, 64, 64))
+    params = sdhip.conv_params(1, 1, 1, 1, 1, 1)
+    assert lib.sdhip_conv2d_path(k16, img, out, params) == 4
+    try:
+        sdhip.set_tuning("bits=8")
+        assert lib.sdhip_conv2d_supported(k16, img, out, params) == 1
+        assert lib.sdhip_conv2d_path(k16, img, out, params) == 2
+        assert lib.sdhip_conv2d_work_size(k16, img, out, params) > 0
+        sdhip.set_tuning("bits=8,quantize=5")  # not the convolutions: single precision again
+        assert lib.sdhip_conv2d_path(k16, img, out, params) == 4
+    finally:
+        sdhip.set_tuning("")
