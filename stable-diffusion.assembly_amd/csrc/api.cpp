@@ -139,10 +139,8 @@ bool in_range(Range r, long v, const char *&takes) {
         takes = "0 or more";
         return v >= 0 && v <= INT32_MAX;
     case kBits:
-        // 16, the reference's products of 16-bit numbers (gemm.h:226-237), is
-        // a form of its vector units that this library does not have.
-        takes = "an int other than 16 (products of 16-bit numbers are not a form of this library)";
-        return v >= INT32_MIN && v <= INT32_MAX && v != 16;
+        takes = "an int";
+        return v >= INT32_MIN && v <= INT32_MAX;
     }
     return false;
 }

@@ -44,10 +44,12 @@ constexpr int kBK = 32;
 constexpr int kLdk = kBK + 8;  // halves per LDS row: 80 bytes, 16-byte aligned, skewed across banks
 
 // Which operands are single precision, split into two FP16 planes.
-enum Split { kSplitA = 0, kSplitB = 1, kSplitBoth = 2 };
+// kSplitNone: the products of 16 bits (bits=16): the single-precision
+// operand rounded to FP16, its first part alone, one MFMA a product.
+enum Split { kSplitA = 0, kSplitB = 1, kSplitBoth = 2, kSplitNone = 3 };
 
-constexpr int planes_a(int mode) { return mode == kSplitB ? 1 : 2; }
-constexpr int planes_b(int mode) { return mode == kSplitA ? 1 : 2; }
+constexpr int planes_a(int mode) { return mode == kSplitB || mode == kSplitNone ? 1 : 2; }
+constexpr int planes_b(int mode) { return mode == kSplitA || mode == kSplitNone ? 1 : 2; }
 
 // ------------------------------------------------------------------ MFMA core
 
@@ -65,22 +67,22 @@ __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float1
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             a[i] = *reinterpret_cast<const half8 *>(a_hi + (32 * i + r) * kLdk + ks + kh);
-            if (MODE != kSplitB) al[i] = *reinterpret_cast<const half8 *>(a_lo + (32 * i + r) * kLdk + ks + kh);
+            if (planes_a(MODE) == 2) al[i] = *reinterpret_cast<const half8 *>(a_lo + (32 * i + r) * kLdk + ks + kh);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             b[j] = *reinterpret_cast<const half8 *>(b_hi + (32 * j + r) * kLdk + ks + kh);
-            if (MODE != kSplitA) bl[j] = *reinterpret_cast<const half8 *>(b_lo + (32 * j + r) * kLdk + ks + kh);
+            if (planes_b(MODE) == 2) bl[j] = *reinterpret_cast<const half8 *>(b_lo + (32 * j + r) * kLdk + ks + kh);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-                if (MODE != kSplitB) {
+                if (planes_a(MODE) == 2) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
                 }
-                if (MODE != kSplitA) {
+                if (planes_b(MODE) == 2) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
                 }
             }
@@ -100,7 +102,7 @@ __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float1
 // the end read the block's first row instead, whose products are never
 // stored -- the loads then have no conditions, and so no branches that would
 // wait on the loads before them.
-template <int BR, bool VEC, bool FULL>
+template <int BR, bool VEC, bool FULL, bool LO = true>
 struct F32Rows {
     static constexpr int kQuads = BR * kBK / 4 / 256;  // float4 per thread
     static_assert(kQuads >= 1, "tile too small for 256 threads");
@@ -158,7 +160,8 @@ struct F32Rows {
             split2(v[i].z, a, b); h[2] = a; l[2] = b;
             split2(v[i].w, a, b); h[3] = a; l[3] = b;
             *reinterpret_cast<half4 *>(hi + r * kLdk + kq) = h;
-            *reinterpret_cast<half4 *>(lo + r * kLdk + kq) = l;
+            // !LO: the first parts alone (the products of 16 bits).
+            if (LO) *reinterpret_cast<half4 *>(lo + r * kLdk + kq) = l;
         }
     }
 };
@@ -274,7 +277,7 @@ struct F16Rows {
 // positions, which are consecutive in a row of the image at stride 1.  FULL
 // (1x1 kernels, K = IC a multiple of BK): positions past the last read the
 // block's first, never stored, and the loads have no conditions.
-template <int BN, bool POINTWISE, bool FULL, bool K3 = false>
+template <int BN, bool POINTWISE, bool FULL, bool K3 = false, bool LO = true>
 struct Columns {
     static constexpr int kLoads = BN * kBK / 4 / 256;
     static_assert(!FULL || POINTWISE, "FULL columns are those of 1x1 kernels");
@@ -367,7 +370,7 @@ struct Columns {
                 l[e] = b;
             }
             *reinterpret_cast<half4 *>(hi + pl * kLdk + kq) = h;
-            *reinterpret_cast<half4 *>(lo + pl * kLdk + kq) = l;
+            if (LO) *reinterpret_cast<half4 *>(lo + pl * kLdk + kq) = l;
         }
     }
 };
@@ -445,13 +448,15 @@ constexpr int lds_halves() {
 // the block's 128 rows of W are 64 features of the first half and the same 64
 // of the second (the gate), each wave's two column tiles a pair, and the
 // block writes out[m * ldo + j] = P[m][j] GELU(P[m][half + j]).
-template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS, int WP = 1>
+template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS, int WP = 1, bool HALF = false>
 __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
     // WP: the weights' planes, 1 (FP16 weights) or 2 (single-precision ones
     // split, w_plane apart): then three MFMAs a product, x and W both split.
-    constexpr int MODE = WP == 2 ? kSplitBoth : kSplitA;
+    // HALF: the products of 16 bits, x rounded to FP16, one MFMA a product.
+    static_assert(!HALF || WP == 1, "products of 16 bits take FP16 weights");
+    constexpr int MODE = HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitA;
     static_assert(!GATED || TN == 2, "the gated form pairs two column tiles");
     __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, MODE>()];
 
@@ -485,7 +490,7 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    F32Rows<BM, VECX, FULL> xa[NS];
+    F32Rows<BM, VECX, FULL, !HALF> xa[NS];
     F16Rows<BN, VECW, FULL, WP> wb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -661,12 +666,15 @@ __global__ __launch_bounds__(256) void mul_mat_sum_kernel(MulMatArgs p, const fl
 
 // y[n][oc][pos] = sum_k W[oc][k] columns[k][pos], the chain applied; W rows
 // K-contiguous FP16 (the kernel as ggml holds it, [OC][IC][KH][KW]).
-template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS, bool K3 = false, int WP = 1>
+template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS, bool K3 = false, int WP = 1,
+          bool HALF = false>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     constexpr int BM = 64 * TM;  // output channels
     constexpr int BN = 64 * TN;  // positions
-    // WP as mul_mat_kernel's: split single-precision kernels in two planes.
-    constexpr int MODE = WP == 2 ? kSplitBoth : kSplitB;
+    // WP as mul_mat_kernel's: split single-precision kernels in two planes;
+    // HALF, the products of 16 bits: the columns rounded to FP16.
+    static_assert(!HALF || WP == 1, "products of 16 bits take FP16 kernels");
+    constexpr int MODE = HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitB;
     __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, MODE>()];
 
     const int tid = threadIdx.x;
@@ -689,7 +697,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
     F16Rows<BM, VECW, FULL, WP> wa[NS];
-    Columns<BN, POINTWISE, FULL, K3> xb[NS];
+    Columns<BN, POINTWISE, FULL, K3, !HALF> xb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         wa[s].init(c.w, c.ldw, w_row, c.K, tid, c.w_plane);
@@ -800,12 +808,12 @@ __global__ __launch_bounds__(256) void columns_kernel(ConvArgs c, float *__restr
 // part[s][oc][p] = 16 sum over split s's k of W[oc][k] cols[p][k]: blocks of
 // 64 output channels by 64 positions, the splits of split_len (a multiple of
 // the K-step) one after the other in the grid.
-template <int NS, int WP = 1>
+template <int NS, int WP = 1, bool HALF = false>
 __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const float *__restrict__ cols,
                                                            int64_t split_len, int64_t p_blocks,
                                                            float *__restrict__ part) {
     constexpr int BM = 64, BN = 64;
-    constexpr int MODE = WP == 2 ? kSplitBoth : kSplitB;
+    constexpr int MODE = HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitB;
     __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<1, 1, MODE>()];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -826,7 +834,7 @@ __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const flo
     float16v acc[1][1];
     acc[0][0] = float16v{};
     F16Rows<BM, true, true, WP> wa[NS];
-    F32Rows<BN, true, true> xb[NS];
+    F32Rows<BN, true, true, !HALF> xb[NS];
     const auto w_row = [&](int r) -> int64_t { return oc0 + r < c.oc ? oc0 + r : -1; };
     const auto p_row = [&](int r) -> int64_t { return p0 + r < c.P ? p0 + r : -1; };
 #pragma unroll
@@ -978,6 +986,18 @@ hipError_t launch_mul_mat_t(const MulMatArgs &p, int stages, hipStream_t stream)
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(GATED ? "mul_mat_gated" : "mul_mat", stream);
     if (p.w_scale != nullptr) return launch_mul_mat_w32<TM, TN, GATED>(a, grid, stream);
+    if (p.half16) {
+        // The products of 16 bits.
+        if (full) {
+            hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 1, true>), grid, block, 0, stream, a);
+        } else if (vx && vw) {
+            hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 1, true>), grid, block, 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, false, false, 2, 1, true>), grid, block, 0, stream,
+                               a);
+        }
+        return hipGetLastError();
+    }
     if (full && stages == 4) {
         hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 4>), grid, block, 0, stream, a);
     } else if (full) {
@@ -1005,6 +1025,20 @@ hipError_t launch_conv_t(const ConvArgs &c, int stages, hipStream_t stream) {
     const bool full = POINTWISE && vw && c.K % kBK == 0;
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(POINTWISE ? "conv_direct_pointwise" : "conv_direct", stream);
+    if (c.half16) {
+        // The products of 16 bits.
+        if (full) {
+            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 1, true>), grid, block,
+                               0, stream, a);
+        } else if (vw) {
+            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 1, true>), grid, block, 0,
+                               stream, a);
+        } else {
+            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2, false, 1, true>), grid, block, 0,
+                               stream, a);
+        }
+        return hipGetLastError();
+    }
     if (c.w_scale != nullptr) {
         // Split kernels: whole vectors always (rows 32-aligned, zeros past K).
         if (full) {
@@ -1115,7 +1149,7 @@ MulMatSplitPlan mul_mat_split_plan(const MulMatArgs &p) {
 }  // namespace
 
 bool mul_mat_split_taken(const MulMatArgs &p) {
-    if (p.w_scale != nullptr) return false;  // split weights go in one pass
+    if (p.w_scale != nullptr || p.half16) return false;  // split weights and 16-bit products go in one pass
     const bool aligned = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0 && p.ldw % 8 == 0 &&
                          (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
     return aligned && p.K % kBK == 0 && mul_mat_split_plan(p).splits > 1;
@@ -1199,6 +1233,9 @@ hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipSt
         const dim3 grid(static_cast<uint32_t>(l.blocks * l.splits));
         if (c.w_scale != nullptr) {
             hipLaunchKernelGGL((conv_columns_kernel<2, 2>), grid, dim3(256), 0, stream, a, cols, l.split_len,
+                               l.p_blocks, part);
+        } else if (c.half16) {
+            hipLaunchKernelGGL((conv_columns_kernel<2, 1, true>), grid, dim3(256), 0, stream, a, cols, l.split_len,
                                l.p_blocks, part);
         } else if (g.stages == 4) {
             hipLaunchKernelGGL((conv_columns_kernel<4>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,

@@ -13,7 +13,12 @@ namespace sdhip {
 // The fields of the reference's Tuning that change what is computed
 // (sources/kernels.h:91-135), with its defaults.
 struct Tuning {
-    int bits = 0;                    // 0 single precision; 2..8 quantized products (quant.h)
+    // 0 single precision; 2..8 quantized products (quant.h); 16 products of
+    // 16 bits: MUL_MAT and direct convolutions of FP16 weights by their other
+    // operand rounded to FP16, one product each, summed in single precision
+    // (the reference's FP16 format of gemm.h:226-237); Winograd and attention
+    // stay single precision, as on the reference's vector units.
+    int bits = 0;
     int input_bits = 8;              // the inputs' bits, unsigned with a zero point
     int group = 64;                  // numbers of k sharing a scale, a multiple of 4
     int weight_group = 1;            // the weights' scale per group: 1; per whole row of k: 0

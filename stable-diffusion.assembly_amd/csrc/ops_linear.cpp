@@ -46,6 +46,9 @@ MulMatArgs args_of(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_ten
     a.ne1 = y->ne[1];
     a.ne2 = y->ne[2];
     a.ldy = y->nb[1] / 4;
+    // The products of 16 bits: FP16 weights by x rounded to FP16
+    // (split_form's first parts alone, cpu.cc:336-366).
+    a.half16 = tuning().bits == 16 && w->type == SDHIP_TYPE_F16 ? 1 : 0;
     return a;
 }
 

@@ -57,7 +57,7 @@ def test_tuning_parses_like_sdasm_tune():
 def test_tuning_takes_every_reference_name_and_checks_its_own():
     """Every name of the reference's Tuning (kernels.h:91-135) is taken with
     its default, so that SDASM_TUNE strings carry over; this library's own
-    names take only their documented values; bits=16 is refused."""
+    names take only their documented values."""
     ref = {"conv_kc": 256, "conv_mc": 480, "conv_nc": 128, "conv_rows_outer": 0, "conv_shared_columns": 1024,
            "conv_columns_bytes": 4 << 20, "mul_mat_kc": 256, "mul_mat_mc": 96, "mul_mat_shared_rows": 1024,
            "amx_kc": 256, "amx_mc": 128, "amx_attention": 0, "amx_queries": 64, "amx_fp16": 1,
@@ -74,10 +74,11 @@ def test_tuning_takes_every_reference_name_and_checks_its_own():
         sdhip.set_tuning("conv_kc=128,amx_fp16=0,fuse_residual=0,todo=2,todo_tokens=100,group=1000,bits=3")
         assert sdhip.get_tuning("conv_kc") == 128 and sdhip.get_tuning("todo_tokens") == 100
         for bad in ("gemm_stages=3", "gemm_tiles=13", "gemm_core=3", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
-                    "winograd_splits=-2", "bits=16", "fuse=99999999999"):
+                    "winograd_splits=-2", "fuse=99999999999"):
             with pytest.raises(sdhip.SdhipError):
                 sdhip.set_tuning(bad)
-        for good in ("gemm_stages=4", "gemm_tiles=21", "gemm_tiles=12", "gemm_core=1", "winograd_fp32=1", "winograd_splits=3", "bits=8"):
+        for good in ("gemm_stages=4", "gemm_tiles=21", "gemm_tiles=12", "gemm_core=1", "winograd_fp32=1", "winograd_splits=3", "bits=8",
+                     "bits=16"):
             sdhip.set_tuning(good)
     finally:
         sdhip.set_tuning("")
