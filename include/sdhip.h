@@ -83,11 +83,12 @@ const char *sdhip_last_error(void);
 /* The tuning that changes what is computed, in the reference's SDASM_TUNE
  * syntax "name=value,..." (sources/kernels.h:91-135, parsed by cpu.cc:121-212):
  * every name of the reference's Tuning is taken, with its default.  Those
- * that change what is computed: bits (2..8; 16, the reference's products of
- * 16-bit numbers, is refused), input_bits, group, weight_group, quantize
- * (with bits: 1 linear layers, 4 attention; 2, the convolutions, makes
- * CONV_2D not taken -- quantized convolutions are not a form of this
- * library), winograd, winograd_positions, winograd4_positions,
+ * that change what is computed: bits (2..8, the quantized products; 16, the
+ * reference's products of 16-bit numbers: MUL_MAT, the gated GELU and direct
+ * convolutions of FP16 weights take the other operand rounded to FP16),
+ * input_bits, group, weight_group, quantize (with bits 2..8: 1 linear layers,
+ * 2 convolutions -- direct, or F(2x2,3x3) for those Winograd takes -- 4
+ * attention), winograd, winograd_positions, winograd4_positions,
  * winograd_small_tiles, attention_keys, fuse and fuse_residual (0: the
  * planner fuses no chain, or no residual connection, and an entry point
  * handed one computes it in a pass of its own after the operation, as ggml's
@@ -98,8 +99,8 @@ const char *sdhip_last_error(void);
  * taken and have no effect here.  The reference's names take any int, as its
  * parser does, and are clamped where it clamps them (quant.cc:59-67).  This
  * library's own: winograd_fp32, winograd_splits, gemm_stages, gemm_tiles,
- * attention_generic, attention_fp32 (forms to compare, same results within
- * the bounds), each taking only its documented values.  Returns SDHIP_ERROR
+ * gemm_core, attention_generic, attention_fp32 (forms to compare, same
+ * results within the bounds), each taking only its documented values.  Returns SDHIP_ERROR
  * naming the first unknown name or refused value.  "" resets the defaults. */
 sdhip_status sdhip_set_tuning(const char *text);
 /* The value of one tuning field, or -1 if it has no such name. */
@@ -142,8 +143,11 @@ int sdhip_profile_entry(int i, const char **name, double *total_ms, int64_t *lau
 
 /* GGML_OP_MUL_MAT of one weight matrix w (F16/F32, ne = [K, N, 1, 1]) by
  * x (F32 contiguous, ne = [K, M1, M2, M3]) into y (F32 contiguous,
- * ne = [N, M1, M2, M3]): y[n, m] = sum_k w[k, n] x[k, m].  The work buffer:
- * in the bits mode the quantized operands; otherwise, for a product of few
+ * ne = [N, M1, M2, M3]): y[n, m] = sum_k w[k, n] x[k, m].  Single-precision
+ * weights are taken as the reference takes them (mul_mat.cc:187-194): split
+ * into two FP16 planes with a power-of-two scale per row, products of both
+ * parts.  The work buffer: in the bits mode the quantized operands; for
+ * single-precision weights their planes; otherwise, for a product of few
  * output blocks and long K (split along K), the splits' partial sums; 0
  * else.  A buffer short of sdhip_mul_mat_work_size is SDHIP_ERROR.
  * Replaces mul_mat_supported / mul_mat_work_size / mul_mat_compute
@@ -172,10 +176,13 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
  * The library takes it by Winograd F(4x4,3x3) / F(2x2,3x3) where the
  * reference would (winograd_supported, four, small; winograd.cc:194-196,
  * 1204-1206, 2107-2123) and directly otherwise (conv2d_supported,
- * conv2d.cc:320-331).  The work buffer: Winograd's exponents, transformed
- * operands and products; for a direct convolution of a kernel other than
- * 1x1 with IC KH KW a multiple of 32, its columns and the partial sums of
- * its splits of K; 0 else.  A buffer short of sdhip_conv2d_work_size is
+ * conv2d.cc:320-331); in the bits mode with quantize & 2, the direct
+ * convolution's products quantized (conv2d.cc:338-483) or F(2x2,3x3) with
+ * quantized products (winograd.cc:1826-2103).  The work buffer: Winograd's
+ * exponents, transformed operands and products; for a direct convolution of
+ * a kernel other than 1x1 with IC KH KW a multiple of 32, its columns and
+ * the partial sums of its splits of K; single-precision kernels' FP16
+ * planes; the quantized columns and products; 0 else.  A buffer short of sdhip_conv2d_work_size is
  * SDHIP_ERROR.  Replaces conv2d_* and winograd_* of ops.h:26-38. */
 int sdhip_conv2d_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
                            const int32_t op_params[6]);

@@ -1063,9 +1063,9 @@ hipError_t launch_split(AttentionArgs a, void *work, hipStream_t stream) {
     const int64_t nk = ceil_div(a.lk, SH::kKeys);
     {
         KernelScope scope("attention.tiles", stream);
-        hipLaunchKernelGGL((attention_tiles_kernel<D, SH::kKeys>),
-                           dim3(static_cast<uint32_t>(nk), static_cast<uint32_t>(a.b * a.hk)), dim3(256), 0, stream,
-                           a, static_cast<_Float16 *>(work));
+        SDHIP_LAUNCH((attention_tiles_kernel<D, SH::kKeys>),
+                     dim3(static_cast<uint32_t>(nk), static_cast<uint32_t>(a.b * a.hk)), dim3(256), 0, stream,
+                     a, static_cast<_Float16 *>(work));
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
@@ -1077,8 +1077,8 @@ hipError_t launch_split(AttentionArgs a, void *work, hipStream_t stream) {
     if (attr != hipSuccess) return attr;
     dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
     KernelScope scope("attention", stream);
-    hipLaunchKernelGGL((attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe>), grid, block, lds, stream, a,
-                       static_cast<const char *>(work));
+    SDHIP_LAUNCH((attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe>), grid, block, lds, stream, a,
+                 static_cast<const char *>(work));
     return hipGetLastError();
 }
 
@@ -1089,7 +1089,7 @@ hipError_t launch_fast(AttentionArgs a, hipStream_t stream) {
     const size_t lds = sizeof(float) * 2 * F::kBuffer;
     dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
     KernelScope scope("attention", stream);
-    hipLaunchKernelGGL((attention_fast_kernel<D, QT, KB>), grid, block, lds, stream, a);
+    SDHIP_LAUNCH((attention_fast_kernel<D, QT, KB>), grid, block, lds, stream, a);
     return hipGetLastError();
 }
 
@@ -1157,7 +1157,7 @@ hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(kernel, grid, block, lds, stream, a, w.splits, w.key_len, part);
+        SDHIP_LAUNCH(kernel, grid, block, lds, stream, a, w.splits, w.key_len, part);
         return hipGetLastError();
     };
     hipError_t e;
@@ -1171,8 +1171,8 @@ hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
         e = launch(attention_wide_kernel<NDV, false, false>);
     }
     if (e != hipSuccess || w.splits == 1) return e;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lq, 4))),
-                       dim3(256), 0, stream, a, w.splits, part);
+    SDHIP_LAUNCH(attention_combine_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lq, 4))),
+                 dim3(256), 0, stream, a, w.splits, part);
     return hipGetLastError();
 }
 
@@ -1182,13 +1182,13 @@ hipError_t launch_ndv(AttentionArgs a, hipStream_t stream) {
     const size_t lds = sizeof(float) * (kQueries * a.ldq + kKeys * a.ldk + kKeys * a.ldv);
     dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
     if (a.khalf && a.vhalf) {
-        hipLaunchKernelGGL((attention_kernel<NDV, true, true>), grid, block, lds, stream, a);
+        SDHIP_LAUNCH((attention_kernel<NDV, true, true>), grid, block, lds, stream, a);
     } else if (a.khalf) {
-        hipLaunchKernelGGL((attention_kernel<NDV, true, false>), grid, block, lds, stream, a);
+        SDHIP_LAUNCH((attention_kernel<NDV, true, false>), grid, block, lds, stream, a);
     } else if (a.vhalf) {
-        hipLaunchKernelGGL((attention_kernel<NDV, false, true>), grid, block, lds, stream, a);
+        SDHIP_LAUNCH((attention_kernel<NDV, false, true>), grid, block, lds, stream, a);
     } else {
-        hipLaunchKernelGGL((attention_kernel<NDV, false, false>), grid, block, lds, stream, a);
+        SDHIP_LAUNCH((attention_kernel<NDV, false, false>), grid, block, lds, stream, a);
     }
     return hipGetLastError();
 }

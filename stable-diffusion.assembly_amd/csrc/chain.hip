@@ -116,9 +116,9 @@ sdhip_status chain_after(const ChainRun &r, hipStream_t stream) {
     const int64_t n = r.ne[0] * r.ne[1] * r.ne[2] * r.ne[3];
     if (n == 0) return SDHIP_OK;
     KernelScope prof("chain.apart", stream);
-    hipLaunchKernelGGL(chain_apart_kernel, dim3(grid_of(n)), dim3(256), 0, stream, r.apart_in, r.apart_out, n,
-                       static_cast<uint32_t>(r.ne[0]), static_cast<uint32_t>(r.ne[1]), static_cast<uint32_t>(r.ne[2]),
-                       r.after);
+    SDHIP_LAUNCH(chain_apart_kernel, dim3(grid_of(n)), dim3(256), 0, stream, r.apart_in, r.apart_out, n,
+                 static_cast<uint32_t>(r.ne[0]), static_cast<uint32_t>(r.ne[1]), static_cast<uint32_t>(r.ne[2]),
+                 r.after);
     return launched(hipGetLastError(), "chain apart");
 }
 
@@ -126,8 +126,8 @@ sdhip_status gated_after(const float *p, float *out, int64_t rows, int64_t half,
                          hipStream_t stream) {
     if (rows * half == 0) return SDHIP_OK;
     KernelScope prof("gated.apart", stream);
-    hipLaunchKernelGGL(gated_apart_kernel, dim3(grid_of(rows * half)), dim3(256), 0, stream, p, out, rows, half, ldp,
-                       ldo);
+    SDHIP_LAUNCH(gated_apart_kernel, dim3(grid_of(rows * half)), dim3(256), 0, stream, p, out, rows, half, ldp,
+                 ldo);
     return launched(hipGetLastError(), "gated GELU apart");
 }
 

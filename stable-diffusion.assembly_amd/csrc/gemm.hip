@@ -963,11 +963,11 @@ hipError_t launch_mul_mat_w32(const MulMatArgs &a, dim3 grid, hipStream_t stream
     const bool vx = a.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
     const dim3 block(256);
     if (vx && a.K % kBK == 0) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 2>), grid, block, 0, stream, a);
     } else if (vx) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 2>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, true, false, 2, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, false, true, false, 2, 2>), grid, block, 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -989,27 +989,27 @@ hipError_t launch_mul_mat_t(const MulMatArgs &p, int stages, hipStream_t stream)
     if (p.half16) {
         // The products of 16 bits.
         if (full) {
-            hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 1, true>), grid, block, 0, stream, a);
+            SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 1, true>), grid, block, 0, stream, a);
         } else if (vx && vw) {
-            hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 1, true>), grid, block, 0, stream, a);
+            SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 1, true>), grid, block, 0, stream, a);
         } else {
-            hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, false, false, 2, 1, true>), grid, block, 0, stream,
-                               a);
+            SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, false, false, false, 2, 1, true>), grid, block, 0, stream,
+                         a);
         }
         return hipGetLastError();
     }
     if (full && stages == 4) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 4>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, true, 4>), grid, block, 0, stream, a);
     } else if (full) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, true, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, true, 2>), grid, block, 0, stream, a);
     } else if (vx && vw) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, true, false, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, false, 2>), grid, block, 0, stream, a);
     } else if (vx) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, true, false, false, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, false, false, 2>), grid, block, 0, stream, a);
     } else if (vw) {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, true, false, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, false, true, false, 2>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((mul_mat_kernel<TM, TN, GATED, false, false, false, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, false, false, false, 2>), grid, block, 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -1028,38 +1028,38 @@ hipError_t launch_conv_t(const ConvArgs &c, int stages, hipStream_t stream) {
     if (c.half16) {
         // The products of 16 bits.
         if (full) {
-            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 1, true>), grid, block,
-                               0, stream, a);
+            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 1, true>), grid, block,
+                         0, stream, a);
         } else if (vw) {
-            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 1, true>), grid, block, 0,
-                               stream, a);
+            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 1, true>), grid, block, 0,
+                         stream, a);
         } else {
-            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2, false, 1, true>), grid, block, 0,
-                               stream, a);
+            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2, false, 1, true>), grid, block, 0,
+                         stream, a);
         }
         return hipGetLastError();
     }
     if (c.w_scale != nullptr) {
         // Split kernels: whole vectors always (rows 32-aligned, zeros past K).
         if (full) {
-            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 2>), grid, block, 0,
-                               stream, a);
+            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 2>), grid, block, 0,
+                         stream, a);
         } else {
-            hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 2>), grid, block, 0,
-                               stream, a);
+            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 2>), grid, block, 0,
+                         stream, a);
         }
         return hipGetLastError();
     }
     if (full && stages == 4) {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 4>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 4>), grid, block, 0, stream, a);
     } else if (full) {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2>), grid, block, 0, stream, a);
     } else if (vw && !POINTWISE && c.kh == 3 && c.kw == 3) {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, false, true, false, 2, true>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((conv_direct_kernel<TM, TN, false, true, false, 2, true>), grid, block, 0, stream, a);
     } else if (vw) {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2>), grid, block, 0, stream, a);
+        SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2>), grid, block, 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -1071,14 +1071,14 @@ hipError_t launch_split_t(SplitBatchedArgs p, int stages, hipStream_t stream) {
     dim3 grid(static_cast<uint32_t>(p.batches * p.m_blocks * p.n_blocks)), block(256);
     if (p.a32 != nullptr) {
         if (stages == 4) {
-            hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 4, true>), grid, block, 0, stream, p);
+            SDHIP_LAUNCH((split_batched_kernel<TM, TN, true, 4, true>), grid, block, 0, stream, p);
         } else {
-            hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 2, true>), grid, block, 0, stream, p);
+            SDHIP_LAUNCH((split_batched_kernel<TM, TN, true, 2, true>), grid, block, 0, stream, p);
         }
     } else if (stages == 4) {
-        hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 4>), grid, block, 0, stream, p);
+        SDHIP_LAUNCH((split_batched_kernel<TM, TN, true, 4>), grid, block, 0, stream, p);
     } else {
-        hipLaunchKernelGGL((split_batched_kernel<TM, TN, true, 2>), grid, block, 0, stream, p);
+        SDHIP_LAUNCH((split_batched_kernel<TM, TN, true, 2>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -1168,14 +1168,14 @@ hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hi
         KernelScope scope("mul_mat", stream);
         const dim3 grid(static_cast<uint32_t>(l.blocks * l.splits));
         if (g.stages == 4) {
-            hipLaunchKernelGGL((mul_mat_split_kernel<4>), grid, dim3(256), 0, stream, a, l.split_len, part);
+            SDHIP_LAUNCH((mul_mat_split_kernel<4>), grid, dim3(256), 0, stream, a, l.split_len, part);
         } else {
-            hipLaunchKernelGGL((mul_mat_split_kernel<2>), grid, dim3(256), 0, stream, a, l.split_len, part);
+            SDHIP_LAUNCH((mul_mat_split_kernel<2>), grid, dim3(256), 0, stream, a, l.split_len, part);
         }
     }
     KernelScope scope("mul_mat.sum", stream);
-    hipLaunchKernelGGL(mul_mat_sum_kernel, dim3(static_cast<uint32_t>((p.M * p.N + 255) / 256)), dim3(256), 0, stream,
-                       a, part, l.splits);
+    SDHIP_LAUNCH(mul_mat_sum_kernel, dim3(static_cast<uint32_t>((p.M * p.N + 255) / 256)), dim3(256), 0, stream,
+                 a, part, l.splits);
     return hipGetLastError();
 }
 
@@ -1221,9 +1221,9 @@ hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipSt
         KernelScope scope("conv_direct.columns", stream);
         const dim3 grid(static_cast<uint32_t>((c.P * (c.K / 4) + 255) / 256));
         if (c.kh == 3 && c.kw == 3) {
-            hipLaunchKernelGGL((columns_kernel<true>), grid, dim3(256), 0, stream, c, cols);
+            SDHIP_LAUNCH((columns_kernel<true>), grid, dim3(256), 0, stream, c, cols);
         } else {
-            hipLaunchKernelGGL((columns_kernel<false>), grid, dim3(256), 0, stream, c, cols);
+            SDHIP_LAUNCH((columns_kernel<false>), grid, dim3(256), 0, stream, c, cols);
         }
     }
     {
@@ -1232,22 +1232,22 @@ hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipSt
         a.oc_blocks = (c.oc + 63) / 64;
         const dim3 grid(static_cast<uint32_t>(l.blocks * l.splits));
         if (c.w_scale != nullptr) {
-            hipLaunchKernelGGL((conv_columns_kernel<2, 2>), grid, dim3(256), 0, stream, a, cols, l.split_len,
-                               l.p_blocks, part);
+            SDHIP_LAUNCH((conv_columns_kernel<2, 2>), grid, dim3(256), 0, stream, a, cols, l.split_len,
+                         l.p_blocks, part);
         } else if (c.half16) {
-            hipLaunchKernelGGL((conv_columns_kernel<2, 1, true>), grid, dim3(256), 0, stream, a, cols, l.split_len,
-                               l.p_blocks, part);
+            SDHIP_LAUNCH((conv_columns_kernel<2, 1, true>), grid, dim3(256), 0, stream, a, cols, l.split_len,
+                         l.p_blocks, part);
         } else if (g.stages == 4) {
-            hipLaunchKernelGGL((conv_columns_kernel<4>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
-                               part);
+            SDHIP_LAUNCH((conv_columns_kernel<4>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
+                         part);
         } else {
-            hipLaunchKernelGGL((conv_columns_kernel<2>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
-                               part);
+            SDHIP_LAUNCH((conv_columns_kernel<2>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,
+                         part);
         }
     }
     KernelScope scope("conv_direct.sum", stream);
-    hipLaunchKernelGGL(conv_sum_kernel, dim3(static_cast<uint32_t>((c.oc * c.P + 255) / 256)), dim3(256), 0, stream, c,
-                       part, l.splits);
+    SDHIP_LAUNCH(conv_sum_kernel, dim3(static_cast<uint32_t>((c.oc * c.P + 255) / 256)), dim3(256), 0, stream, c,
+                 part, l.splits);
     return hipGetLastError();
 }
 
@@ -1292,8 +1292,8 @@ hipError_t launch_split_weights(const float *w, int64_t ld, int64_t rows, int64_
     const int64_t kw = split_weights_ld(k);
     _Float16 *hi = static_cast<_Float16 *>(out);
     KernelScope scope("split_weights", stream);
-    hipLaunchKernelGGL(split_weights_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, w, ld, k, kw,
-                       rows, hi, hi + rows * kw, const_cast<float *>(split_weights_scale(out, rows, k)));
+    SDHIP_LAUNCH(split_weights_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, w, ld, k, kw,
+                 rows, hi, hi + rows * kw, const_cast<float *>(split_weights_scale(out, rows, k)));
     return hipGetLastError();
 }
 

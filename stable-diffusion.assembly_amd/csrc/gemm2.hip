@@ -172,7 +172,7 @@ hipError_t launch2(SplitBatchedArgs p, hipStream_t stream) {
     p.m_blocks = (p.M + 64 * WM - 1) / (64 * WM);
     p.n_blocks = (p.N + 64 * WN - 1) / (64 * WN);
     const dim3 grid(static_cast<uint32_t>(p.batches * p.m_blocks * p.n_blocks));
-    hipLaunchKernelGGL((split_batched2_kernel<WM, WN, NS>), grid, dim3(256), 0, stream, p);
+    SDHIP_LAUNCH((split_batched2_kernel<WM, WN, NS>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

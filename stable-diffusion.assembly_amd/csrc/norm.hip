@@ -391,21 +391,21 @@ hipError_t launch_group_norm(const GroupNormArgs &a, hipStream_t stream) {
                           (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.xnb3 % 4 == 0 && a.ynb3 % 4 == 0;
     if (resident) {
         KernelScope scope("group_norm", stream);
-        hipLaunchKernelGGL(group_norm_resident_kernel, dim3(static_cast<uint32_t>(a.ne3 * a.groups)),
-                           dim3(kResidentThreads), 0, stream, a);
+        SDHIP_LAUNCH(group_norm_resident_kernel, dim3(static_cast<uint32_t>(a.ne3 * a.groups)),
+                     dim3(kResidentThreads), 0, stream, a);
         return hipGetLastError();
     }
     const dim3 grid(static_cast<uint32_t>(a.ne3 * a.groups * a.slices));
     {
         KernelScope scope("group_norm.sums", stream);
-        hipLaunchKernelGGL(group_sums_kernel<0>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH(group_sums_kernel<0>, grid, dim3(kThreads), 0, stream, a);
     }
     {
         KernelScope scope("group_norm.squares", stream);
-        hipLaunchKernelGGL(group_sums_kernel<1>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH(group_sums_kernel<1>, grid, dim3(kThreads), 0, stream, a);
     }
     KernelScope scope("group_norm.apply", stream);
-    hipLaunchKernelGGL(group_apply_kernel, grid, dim3(kThreads), 0, stream, a);
+    SDHIP_LAUNCH(group_apply_kernel, grid, dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -455,13 +455,13 @@ hipError_t launch_norm(const NormArgs &a, hipStream_t stream) {
     KernelScope scope("norm", stream);
     const dim3 grid(static_cast<uint32_t>(ceil_div(a.rows, kThreads / 64)));
     if (a.ne0 <= 64 * 8) {
-        hipLaunchKernelGGL(norm_resident_kernel<8>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH(norm_resident_kernel<8>, grid, dim3(kThreads), 0, stream, a);
     } else if (a.ne0 <= 64 * 16) {
-        hipLaunchKernelGGL(norm_resident_kernel<16>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH(norm_resident_kernel<16>, grid, dim3(kThreads), 0, stream, a);
     } else if (a.ne0 <= 64 * 32) {
-        hipLaunchKernelGGL(norm_resident_kernel<32>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH(norm_resident_kernel<32>, grid, dim3(kThreads), 0, stream, a);
     } else {
-        hipLaunchKernelGGL(norm_kernel, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH(norm_kernel, grid, dim3(kThreads), 0, stream, a);
     }
     return hipGetLastError();
 }

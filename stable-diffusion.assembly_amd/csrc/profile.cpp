@@ -1,8 +1,9 @@
-// The profile of the library's kernels: with sdhip_profile_enable(1), every
-// launch is bracketed by two HIP events recorded on the launch's own stream,
-// and sdhip_profile_collect() adds their elapsed times up per kernel name.
-// The reference's profile (profile.cc, sdasm_profile_*) times each node and
-// each phase of it on the CPU; here the phases are the kernels.
+// The profile of the library's kernels: with sdhip_profile_enable(1), the
+// kernels of every KernelScope stamp two HIP events from their own dispatch
+// packets (profile.h), and sdhip_profile_collect() adds the elapsed times up
+// per scope name.  The reference's profile (profile.cc, sdasm_profile_*)
+// times each node and each phase of it on the CPU; here the phases are the
+// kernels.
 
 #include <hip/hip_runtime.h>
 
@@ -56,21 +57,42 @@ hipEvent_t take_event(Profile &p) {
 
 bool profiling() { return profile().enabled; }
 
-KernelScope::KernelScope(const char *name, hipStream_t stream) : name_(name), stream_(stream) {
+namespace {
+thread_local ScopeEvents *innermost = nullptr;
+}
+
+ScopeEvents *active_scope() { return innermost; }
+
+KernelScope::KernelScope(const char *name, hipStream_t) : name_(name) {
     Profile &p = profile();
     if (!p.enabled) return;
-    std::lock_guard<std::mutex> g(p.lock);
-    start_ = take_event(p);
-    stop_ = take_event(p);
-    if (start_ == nullptr || stop_ == nullptr || hipEventRecord(start_, stream_) != hipSuccess) start_ = nullptr;
+    {
+        std::lock_guard<std::mutex> g(p.lock);
+        events_.start = take_event(p);
+        events_.stop = take_event(p);
+    }
+    if (events_.start == nullptr || events_.stop == nullptr) {
+        std::lock_guard<std::mutex> g(p.lock);
+        if (events_.start != nullptr) p.spare.push_back(events_.start);
+        if (events_.stop != nullptr) p.spare.push_back(events_.stop);
+        return;
+    }
+    outer_ = innermost;
+    innermost = &events_;
+    open_ = true;
 }
 
 KernelScope::~KernelScope() {
-    if (start_ == nullptr) return;
+    if (!open_) return;
+    innermost = outer_;
     Profile &p = profile();
-    if (hipEventRecord(stop_, stream_) != hipSuccess) return;
     std::lock_guard<std::mutex> g(p.lock);
-    p.pending.push_back({name_, start_, stop_});
+    if (events_.launches > 0) {
+        p.pending.push_back({name_, events_.start, events_.stop});
+    } else {
+        p.spare.push_back(events_.start);
+        p.spare.push_back(events_.stop);
+    }
 }
 
 }  // namespace sdhip

@@ -383,11 +383,11 @@ template <int SUBS, int NDV>
 hipError_t launch_qa_gt(const QAttentionArgs &a, hipStream_t stream, dim3 grid) {
     const int gt = static_cast<int>(a.group / 16);
     if (gt <= 4) {
-        hipLaunchKernelGGL((qa_attention_kernel<SUBS, NDV, 4>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 4>), grid, dim3(256), 0, stream, a);
     } else if (gt <= 8) {
-        hipLaunchKernelGGL((qa_attention_kernel<SUBS, NDV, 8>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 8>), grid, dim3(256), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((qa_attention_kernel<SUBS, NDV, 16>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 16>), grid, dim3(256), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -463,19 +463,19 @@ hipError_t launch_quantized_attention(QAttentionArgs a, void *work, hipStream_t 
     a.qo = reinterpret_cast<float *>(base + l.qo);
     {
         KernelScope scope("qattention.keys", stream);
-        hipLaunchKernelGGL(qa_keys_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.lkp, 4))), dim3(256), 0,
-                           stream, a);
+        SDHIP_LAUNCH(qa_keys_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.lkp, 4))), dim3(256), 0,
+                     stream, a);
     }
     {
         KernelScope scope("qattention.values", stream);
-        hipLaunchKernelGGL(qa_values_kernel,
-                           dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.groups * a.dvp, 4))), dim3(256), 0,
-                           stream, a);
+        SDHIP_LAUNCH(qa_values_kernel,
+                     dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.groups * a.dvp, 4))), dim3(256), 0,
+                     stream, a);
     }
     {
         KernelScope scope("qattention.queries", stream);
-        hipLaunchKernelGGL(qa_queries_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lqp, 4))), dim3(256),
-                           0, stream, a);
+        SDHIP_LAUNCH(qa_queries_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lqp, 4))), dim3(256),
+                     0, stream, a);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

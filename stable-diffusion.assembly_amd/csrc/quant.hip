@@ -610,7 +610,7 @@ hipError_t launch_qgemm_part(const Layout &l, int8_t *xq, float *xs, float *xo, 
     p.from_redirect = from_redirect;
     p.col_blocks = ceil_div(cols, kQB);
     const dim3 grid(static_cast<uint32_t>(ceil_div(rows, kQB) * p.col_blocks));
-    hipLaunchKernelGGL(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
+    SDHIP_LAUNCH(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -694,16 +694,16 @@ sdhip_status quantized_conv(const ConvArgs &c, bool winograd, void *work, hipStr
         // chain into y.
         {
             KernelScope scope("qconv.quantize", stream);
-            hipLaunchKernelGGL(quantize_inputs_kernel<ColumnsSrc>, dim3(ceil_div(c.P * l.groups, 4)), dim3(256), 0,
-                               stream, ColumnsSrc{c}, c.P, c.K, q, l, xq, xs, xo);
+            SDHIP_LAUNCH(quantize_inputs_kernel<ColumnsSrc>, dim3(ceil_div(c.P * l.groups, 4)), dim3(256), 0,
+                         stream, ColumnsSrc{c}, c.P, c.K, q, l, xq, xs, xo);
             if (c.w32 != nullptr) {
-                hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(c.oc, 4)), dim3(256), 0, stream, c.w32,
-                                   c.K, c.oc, c.K, q, l, wq, ws, wo, wsum, int64_t{0});
+                SDHIP_LAUNCH(quantize_weights_kernel<float>, dim3(ceil_div(c.oc, 4)), dim3(256), 0, stream, c.w32,
+                             c.K, c.oc, c.K, q, l, wq, ws, wo, wsum, int64_t{0});
             } else {
-                hipLaunchKernelGGL(quantize_weights_kernel<_Float16>, dim3(ceil_div(c.oc, 4)), dim3(256), 0, stream,
-                                   c.w, c.K, c.oc, c.K, q, l, wq, ws, wo, wsum, int64_t{0});
+                SDHIP_LAUNCH(quantize_weights_kernel<_Float16>, dim3(ceil_div(c.oc, 4)), dim3(256), 0, stream,
+                             c.w, c.K, c.oc, c.K, q, l, wq, ws, wo, wsum, int64_t{0});
             }
-            if (c.from_redirect) hipLaunchKernelGGL(conv_gather_kernel, grid(c.P * c.oc), dim3(256), 0, stream, c, t);
+            if (c.from_redirect) SDHIP_LAUNCH(conv_gather_kernel, grid(c.P * c.oc), dim3(256), 0, stream, c, t);
         }
         {
             KernelScope scope("qconv.products", stream);
@@ -712,7 +712,7 @@ sdhip_status quantized_conv(const ConvArgs &c, bool winograd, void *work, hipStr
             if (e != hipSuccess) return launched(e, "quantized conv2d products");
         }
         KernelScope scope("qconv.outputs", stream);
-        hipLaunchKernelGGL(conv_scatter_kernel, grid(c.P * c.oc), dim3(256), 0, stream, c, t);
+        SDHIP_LAUNCH(conv_scatter_kernel, grid(c.P * c.oc), dim3(256), 0, stream, c, t);
         return launched(hipGetLastError(), "quantized conv2d");
     }
     // winograd.cc:1826-2103: F(2x2) whatever F(4x4) would take; the points'
@@ -723,20 +723,20 @@ sdhip_status quantized_conv(const ConvArgs &c, bool winograd, void *work, hipStr
     float *u = reinterpret_cast<float *>(base + L.u);
     {
         KernelScope scope("qwinograd2.transforms", stream);
-        hipLaunchKernelGGL(wq_inputs_kernel, grid(tiles * c.ic), dim3(256), 0, stream, c, tw, th, tiles, v);
+        SDHIP_LAUNCH(wq_inputs_kernel, grid(tiles * c.ic), dim3(256), 0, stream, c, tw, th, tiles, v);
         if (c.w32 != nullptr) {
-            hipLaunchKernelGGL(wq_weights_kernel<float>, grid(c.oc * c.ic), dim3(256), 0, stream, c.w32, c.oc, c.ic, u);
+            SDHIP_LAUNCH(wq_weights_kernel<float>, grid(c.oc * c.ic), dim3(256), 0, stream, c.w32, c.oc, c.ic, u);
         } else {
-            hipLaunchKernelGGL(wq_weights_kernel<_Float16>, grid(c.oc * c.ic), dim3(256), 0, stream, c.w, c.oc, c.ic,
-                               u);
+            SDHIP_LAUNCH(wq_weights_kernel<_Float16>, grid(c.oc * c.ic), dim3(256), 0, stream, c.w, c.oc, c.ic,
+                         u);
         }
     }
     {
         KernelScope scope("qwinograd2.quantize", stream);
-        hipLaunchKernelGGL(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(16 * tiles * l.groups, 4)), dim3(256), 0,
-                           stream, RowsSrc{v, c.ic}, 16 * tiles, c.ic, q, l, xq, xs, xo);
-        hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(16 * c.oc, 4)), dim3(256), 0, stream, u, c.ic,
-                           16 * c.oc, c.ic, q, l, wq, ws, wo, wsum, winograd_stretch(c, q));
+        SDHIP_LAUNCH(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(16 * tiles * l.groups, 4)), dim3(256), 0,
+                     stream, RowsSrc{v, c.ic}, 16 * tiles, c.ic, q, l, xq, xs, xo);
+        SDHIP_LAUNCH(quantize_weights_kernel<float>, dim3(ceil_div(16 * c.oc, 4)), dim3(256), 0, stream, u, c.ic,
+                     16 * c.oc, c.ic, q, l, wq, ws, wo, wsum, winograd_stretch(c, q));
     }
     {
         KernelScope scope("qwinograd2.products", stream);
@@ -747,7 +747,7 @@ sdhip_status quantized_conv(const ConvArgs &c, bool winograd, void *work, hipStr
         }
     }
     KernelScope scope("qwinograd2.outputs", stream);
-    hipLaunchKernelGGL(wq_outputs_kernel, grid(tiles * c.oc), dim3(256), 0, stream, c, tw, th, tiles, t);
+    SDHIP_LAUNCH(wq_outputs_kernel, grid(tiles * c.oc), dim3(256), 0, stream, c, tw, th, tiles, t);
     return launched(hipGetLastError(), "quantized winograd");
 }
 
@@ -785,17 +785,17 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     int32_t *wsum = reinterpret_cast<int32_t *>(wbase + (l.wsum - l.wq));
     {
         KernelScope scope("quantize_inputs", stream);
-        hipLaunchKernelGGL(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream,
-                           RowsSrc{a.x, a.ldx}, a.M, a.K, q, l, xq, xs, xo);
+        SDHIP_LAUNCH(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream,
+                     RowsSrc{a.x, a.ldx}, a.M, a.K, q, l, xq, xs, xo);
     }
     if (!ready) {
         KernelScope scope("quantize_weights", stream);
         if (a.w32 != nullptr) {
-            hipLaunchKernelGGL(quantize_weights_kernel<float>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w32,
-                               a.ldw32, a.N, a.K, q, l, wq, ws, wo, wsum, int64_t{0});
+            SDHIP_LAUNCH(quantize_weights_kernel<float>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w32,
+                         a.ldw32, a.N, a.K, q, l, wq, ws, wo, wsum, int64_t{0});
         } else {
-            hipLaunchKernelGGL(quantize_weights_kernel<_Float16>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w,
-                               a.ldw, a.N, a.K, q, l, wq, ws, wo, wsum, int64_t{0});
+            SDHIP_LAUNCH(quantize_weights_kernel<_Float16>, dim3(ceil_div(a.N, 4)), dim3(256), 0, stream, a.w,
+                         a.ldw, a.N, a.K, q, l, wq, ws, wo, wsum, int64_t{0});
         }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return launched(err, "quantize_weights");
@@ -826,9 +826,9 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     const dim3 grid(static_cast<uint32_t>(ceil_div(a.M, kQB) * p.col_blocks));
     KernelScope scope(gated ? "qgemm_gated" : "qgemm", stream);
     if (gated) {
-        hipLaunchKernelGGL(qgemm_kernel<true>, grid, dim3(256), 0, stream, p);
+        SDHIP_LAUNCH(qgemm_kernel<true>, grid, dim3(256), 0, stream, p);
     } else {
-        hipLaunchKernelGGL(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
+        SDHIP_LAUNCH(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
     }
     return launched(hipGetLastError(), gated ? "quantized mul_mat_gated" : "quantized mul_mat");
 }

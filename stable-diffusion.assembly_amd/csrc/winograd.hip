@@ -741,8 +741,8 @@ __global__ __launch_bounds__(256) void batched_gemm_f32(const float *__restrict_
 // shift[s][oc]; they are added in the order of s.
 template <int M, bool PAIRS = false>
 __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const float *__restrict__ prod,
-                                                      const int32_t *__restrict__ shift, int64_t splits = 1,
-                                                      int64_t ld = 0) {
+                                                      const int32_t *__restrict__ shift, int64_t splits,
+                                                      int64_t ld) {
     constexpr int A = Mat<M>::A;
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
     if (t >= static_cast<uint32_t>(a.tiles * a.oc)) return;
@@ -1266,39 +1266,39 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         {
             KernelScope scope(names[1].c_str(), stream);
             if (a.w32 != nullptr) {
-                hipLaunchKernelGGL((weights_kernel<M, float>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0, stream,
-                                   a.w32, u, a.oc, a.ic);
+                SDHIP_LAUNCH((weights_kernel<M, float>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0, stream,
+                             a.w32, u, a.oc, a.ic);
             } else {
-                hipLaunchKernelGGL((weights_kernel<M, _Float16>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0,
-                                   stream, a.w, u, a.oc, a.ic);
+                SDHIP_LAUNCH((weights_kernel<M, _Float16>), dim3(ceil_div(a.oc * a.ic, 256)), dim3(256), 0,
+                             stream, a.w, u, a.oc, a.ic);
             }
         }
         {
             KernelScope scope(names[2].c_str(), stream);
-            hipLaunchKernelGGL((inputs_kernel<M>), dim3(ceil_div(n_in, 256)), dim3(256), 0, stream, a, v);
+            SDHIP_LAUNCH((inputs_kernel<M>), dim3(ceil_div(n_in, 256)), dim3(256), 0, stream, a, v);
         }
         {
             KernelScope scope(names[3].c_str(), stream);
             const int64_t mb = ceil_div(a.oc, kGBM), nb = ceil_div(a.tiles, kGBN);
-            hipLaunchKernelGGL(batched_gemm_f32, dim3(A * A * mb * nb), dim3(256), 0, stream, u, v, m, a.oc, a.tiles,
-                               a.ic, mb, nb);
+            SDHIP_LAUNCH(batched_gemm_f32, dim3(A * A * mb * nb), dim3(256), 0, stream, u, v, m, a.oc, a.tiles,
+                         a.ic, mb, nb);
         }
         KernelScope scope(names[4].c_str(), stream);
-        hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
-                           nullptr);
+        SDHIP_LAUNCH((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
+                     nullptr, int64_t{1}, int64_t{0});
         return launched(hipGetLastError(), "winograd");
     }
     if (l.small) {
         {
             KernelScope scope(names[0].c_str(), stream);  // the inputs' exponents only
-            hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(a.ic)), dim3(256), 0, stream, a, e,
-                               a_oc);
+            SDHIP_LAUNCH((scales_kernel<M>), dim3(static_cast<uint32_t>(a.ic)), dim3(256), 0, stream, a, e,
+                         a_oc);
         }
         _Float16 *vh = reinterpret_cast<_Float16 *>(v);
         {
             KernelScope scope(names[2].c_str(), stream);
-            hipLaunchKernelGGL((inputs_small_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(l.tp * l.kp, 256))),
-                               dim3(256), 0, stream, a, l.kp, l.tp, e, vh);
+            SDHIP_LAUNCH((inputs_small_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(l.tp * l.kp, 256))),
+                         dim3(256), 0, stream, a, l.kp, l.tp, e, vh);
         }
         {
             KernelScope scope(names[3].c_str(), stream);
@@ -1306,16 +1306,16 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
             const dim3 grid(static_cast<uint32_t>(oc_blocks * l.splits));
             const dim3 block(64 * A);
             if (l.tp <= 16) {
-                hipLaunchKernelGGL((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.split_len,
-                                   oc_blocks, e, vh, m, shift);
+                SDHIP_LAUNCH((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.split_len,
+                             oc_blocks, e, vh, m, shift);
             } else {
-                hipLaunchKernelGGL((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.split_len,
-                                   oc_blocks, e, vh, m, shift);
+                SDHIP_LAUNCH((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.split_len,
+                             oc_blocks, e, vh, m, shift);
             }
         }
         KernelScope scope(names[4].c_str(), stream);
-        hipLaunchKernelGGL((outputs_kernel<M, true>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
-                           shift, l.splits, l.tp);
+        SDHIP_LAUNCH((outputs_kernel<M, true>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m,
+                     shift, l.splits, l.tp);
         return launched(hipGetLastError(), "winograd (small images)");
     }
     // The transformed weights U 2^a_o and their exponents a_o, kept in the
@@ -1341,8 +1341,8 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         // The inputs' exponents, and the weights' unless kept.
         KernelScope scope(names[0].c_str(), stream);
         const int64_t waves = ready ? a.ic : a.ic + a.oc;
-        hipLaunchKernelGGL((scales_kernel<M>), dim3(static_cast<uint32_t>(waves)), dim3(256), 0, stream, a, e,
-                           a_kept);
+        SDHIP_LAUNCH((scales_kernel<M>), dim3(static_cast<uint32_t>(waves)), dim3(256), 0, stream, a, e,
+                     a_kept);
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
     _Float16 *vh = reinterpret_cast<_Float16 *>(v);
@@ -1351,17 +1351,17 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         KernelScope scope(names[5].c_str(), stream);
         const int64_t wgx = ceil_div(a.oc, kWeightOc), wblocks = wgx * ceil_div(l.kp, kWeightIc);
         const int64_t igx = ceil_div(a.tiles, kInTiles), iblocks = igx * (l.kp / kInChannels);
-        hipLaunchKernelGGL((transforms_kernel<M>), dim3(static_cast<uint32_t>(wblocks + iblocks)), dim3(256), 0,
-                           stream, a, l.kp, e, a_oc, uh, shift, vh, wgx, wblocks, igx);
+        SDHIP_LAUNCH((transforms_kernel<M>), dim3(static_cast<uint32_t>(wblocks + iblocks)), dim3(256), 0,
+                     stream, a, l.kp, e, a_oc, uh, shift, vh, wgx, wblocks, igx);
     } else if (!ready) {
         KernelScope scope(names[1].c_str(), stream);
         const dim3 grid(static_cast<uint32_t>(ceil_div(a.oc * l.kp, 256)));
         if (a.w32 != nullptr) {
-            hipLaunchKernelGGL((weights_scaled_kernel<M, float>), grid, dim3(256), 0, stream, a.w32, a.oc, a.ic, l.kp,
-                               a_kept, u_kept);
+            SDHIP_LAUNCH((weights_scaled_kernel<M, float>), grid, dim3(256), 0, stream, a.w32, a.oc, a.ic, l.kp,
+                         a_kept, u_kept);
         } else {
-            hipLaunchKernelGGL((weights_scaled_kernel<M, _Float16>), grid, dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp,
-                               a_kept, u_kept);
+            SDHIP_LAUNCH((weights_scaled_kernel<M, _Float16>), grid, dim3(256), 0, stream, a.w, a.oc, a.ic, l.kp,
+                         a_kept, u_kept);
         }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return launched(err, "winograd weights");
@@ -1369,8 +1369,8 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
     }
     if (kept != nullptr) {
         KernelScope scope(names[2].c_str(), stream);
-        hipLaunchKernelGGL((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
-                           stream, a, l.kp, e, vh, a_kept, f, shift);
+        SDHIP_LAUNCH((inputs_split_kernel<M>), dim3(ceil_div(a.tiles, kInTiles), l.kp / kInChannels), dim3(256), 0,
+                     stream, a, l.kp, e, vh, a_kept, f, shift);
     }
     {
         KernelScope scope(names[3].c_str(), stream);
@@ -1399,7 +1399,8 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         if (err != hipSuccess) return launched(err, "winograd products");
     }
     KernelScope scope(names[4].c_str(), stream);
-    hipLaunchKernelGGL((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, shift);
+    SDHIP_LAUNCH((outputs_kernel<M>), dim3(ceil_div(a.tiles * a.oc, 256)), dim3(256), 0, stream, a, m, shift,
+                 int64_t{1}, int64_t{0});
     return launched(hipGetLastError(), "winograd");
 }
 
