@@ -7,11 +7,20 @@ configuration BASELINE.json's metric is quoted on, configs[1] -- the SD1.5
 ResNet 3x3 convolution [2, 320, 64, 64] -> 320 by Winograd F(4x4, 3x3) with
 its bias and residual add fused -- with inputs resident in HBM.  `value` is
 TFLOP/s counted in direct-convolution FLOPs (2 * N * OC * OH * OW * IC * 9),
-as the metric asks.  The other configurations are timed the same way and
-reported under "configs"; the roofline object is that of the workload's
-dominant kernel, timed with HIP events on its own stream; cpu_baseline is the
-oracle's single-precision restatement of the same F(4x4) algorithm on this
-host's cores (oracle/port.c).
+as the metric asks.
+
+Every configuration of BASELINE.json is timed the same way and reported under
+"configs": warm (the mean over `steps` calls after `warmup`) and cold (caches
+flushed before each call), its kernels' times, and the roofline of its
+dominant kernel(s) -- the algorithmic FLOPs or bytes one call gives them over
+their time, measured by the library's kernel profile (HIP events stamped by
+the kernels' own dispatch packets on their stream), against MI355X's peak.
+The top-level roofline is configs[1]'s.  The SD1.5 UNet step follows (a HIP
+graph), then the VAE decoder's operations, then cpu_baseline: every
+configuration and the UNet step on the host's cores by oracle/port.c (this
+repository's AVX-512 restatement of the reference's CPU algorithms), on all
+the cores the run may use and on one thread, with the host named and its
+measured FMA peak.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -23,12 +32,15 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "stable-diffusion.assembly_amd"))
 
 METRIC = "TFLOP/s per op (direct-conv-equiv) + SD1.5 UNet step ms, 1 MI355X"
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, dense
 PEAK_FP16_MFMA = 2500.0
+PEAK_INT8_MFMA = 5000.0  # TOPS, dense
 PEAK_HBM = 8000.0  # GB/s
 
 
@@ -339,45 +351,343 @@ def make_workload(dev, name):
         return vendor_workload(dev, 1, 4096, 4096, 4096, seed=12)
     if name == "cfg5":
         graph = sdxl_block_workload(dev)
-        return graph.run, graph.flops
+
+        def run():
+            graph.run()
+
+        run.eager, run.keep = graph.eager, graph
+        return run, graph.flops
     if name in ("unet", "unet_kept"):
         step = unet_workload(dev, keep=name.endswith("kept"))
         return step.run, step.flops
     raise SystemExit(f"unknown workload {name}")
 
 
-def cpu_baseline(seconds):
-    """The oracle's F(4x4) restatement on this host's cores, on the full
-    configs[1] convolution, repeated for about `seconds`; the best rate."""
-    import numpy as np
+# ---------------------------------------------------------------- the host CPU baseline
 
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import oracle_lib as orc
 
-    lib = orc.lib()
-    f = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
-    L, I = ctypes.c_int64, ctypes.c_int
-    lib.oracle_port_winograd4.argtypes = [f, L, L, L, L, f, L, I, I, f, f, f, I]
-    n, ic, h, w, oc = 2, 320, 64, 64, 320
-    r = np.random.default_rng(1)
-    x = r.standard_normal((n, ic, h, w)).astype(np.float32)
-    k = (0.02 * r.standard_normal((oc, ic, 3, 3))).astype(np.float16).astype(np.float32)
-    bias = (0.01 * r.standard_normal(oc)).astype(np.float32)
-    res = r.standard_normal((n, oc, h, w)).astype(np.float32)
-    y = np.empty((n, oc, h, w), np.float32)
-    cores = min(16, os.cpu_count() or 1)
-    flops = 2.0 * n * oc * h * w * ic * 9
-    best, runs, t_end = None, 0, time.time() + seconds
-    while time.time() < t_end or runs < 2:
+def host_threads():
+    """The host cores this run may use: its affinity, at most 16 (a GPU box
+    gives one GPU's job 16 cores, whatever os.cpu_count() reports)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def host_info():
+    """The host CPU as lscpu names it (model, sockets, cores), /proc/cpuinfo
+    where lscpu is missing."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        out = ""
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "CPU(s)": "cpus", "CPU max MHz": "max_mhz",
+            "Flags": "flags"}
+    for line in out.splitlines():
+        key, _, val = line.partition(":")
+        if key.strip() in keys:
+            info[keys[key.strip()]] = val.strip()
+    if "model" not in info and os.path.exists("/proc/cpuinfo"):
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["model"] = line.partition(":")[2].strip()
+                break
+    flags = info.pop("flags", "").split()
+    info["isa"] = [f for f in ("avx2", "fma", "avx512f", "avx512_vnni", "avx512_bf16", "amx_int8") if f in flags]
+    return info
+
+
+def best_seconds(fn, budget, least=2):
+    """The fastest of repeated runs of fn after one uncounted run, repeated
+    for about `budget` seconds and at least `least` times
+    (tools/bench.cc:427-451)."""
+    fn()
+    best, runs, end = None, 0, time.perf_counter() + budget
+    while runs < least or time.perf_counter() < end:
         t = time.perf_counter()
-        lib.oracle_port_winograd4(x, n, ic, h, w, k, oc, 1, 1, bias, res, y, cores)
+        fn()
         dt = time.perf_counter() - t
+        best = dt if best is None else min(best, dt)
         runs += 1
-        if runs > 1:  # the first run is not counted (tools/bench.cc:427-451)
-            best = dt if best is None else min(best, dt)
-    return {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"the whole configs[1] convolution (F(4x4), bias + residual) in single precision, "
-                      f"best of {runs - 1} runs after one uncounted, {cores} OpenMP threads"}
+    return best, runs
+
+
+def _orc():
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib
+
+    return oracle_lib
+
+
+def cpu_ops(threads, bits=0, weight_groups=1):
+    """The UNet's and the SDXL block's nodes on the host's cores by
+    oracle/port.c's restatements (the cpu_baseline leg): convolutions by the
+    path the library would take (F(4x4), F(2x2) or direct, by
+    sdhip_conv2d_path's host-side rule), MUL_MAT, the GEGLU product,
+    attention, GROUP_NORM and NORM; the nodes the reference leaves to ggml by
+    torch on the CPU, as HipOps leaves them to torch.  With bits=8, the linear
+    layers quantized (weights quantized and packed once, kept, as the
+    reference keeps its quantized layouts; inputs per call)."""
+    import unet_step
+
+    class CpuOps(unet_step.Ops):
+        def __init__(self, threads, bits=0, weight_groups=1):
+            import sdhip
+
+            self.orc = _orc()
+            self.threads = threads
+            self.bits = bits
+            self.weight_groups = weight_groups
+            self.lib = sdhip.load()  # sdhip_conv2d_path only: host code, no device call
+            self.widened = {}
+            self.quantized = {}
+            self.reset()
+
+        def _w32(self, w):
+            key = (w.data_ptr(), tuple(w.shape))
+            got = self.widened.get(key)
+            if got is None:
+                got = self.widened[key] = w.float().contiguous().numpy()
+            return got
+
+        @staticmethod
+        def _np(t):
+            return t.detach().contiguous().numpy()
+
+        def conv(self, x, w, bias, stride=1, pad=None, add=()):
+            import torch
+
+            import sdhip
+
+            oc, ic, kh, kw = w.shape
+            pad = kh // 2 if pad is None else pad
+            n, _, h, wd = x.shape
+            oh, ow = (h + 2 * pad - kh) // stride + 1, (wd + 2 * pad - kw) // stride + 1
+            y = torch.empty((n, oc, oh, ow))
+            x = x.contiguous()
+            params = sdhip.conv_params(stride, stride, pad, pad, 1, 1)
+            path = self.lib.sdhip_conv2d_path(sdhip.desc(w), sdhip.desc(x), sdhip.desc(y), params)
+            full = [a for a in add if tuple(a.shape) == (n, oc, oh, ow)]
+            res = self._np(full[0]) if full else None
+            rest = [a for a in add if not (full and a is full[0])]
+            b = self._np(bias)
+            if path in (2, 4):
+                self.orc.port_winograd(self._np(x), self._w32(w), pad, b, res, four=path == 4, threads=self.threads,
+                                       out=y.numpy())
+            else:
+                self.orc.port_conv2d(self._np(x), self._w32(w), stride, pad, b, res, threads=self.threads, out=y.numpy())
+            for a in rest:
+                y += a
+            self.count_conv(x, w, y)
+            return y
+
+        def group_norm(self, x, groups, eps, gamma, beta, silu):
+            import torch
+
+            return torch.from_numpy(self.orc.port_group_norm(self._np(x), groups, eps, self._np(gamma), self._np(beta),
+                                                             silu, self.threads))
+
+        def layer_norm(self, x, eps, gamma, beta):
+            import torch
+
+            return torch.from_numpy(self.orc.port_norm(self._np(x), eps, self._np(gamma), self._np(beta), self.threads))
+
+        def _product(self, x2, w, bias, gated=False):
+            n, k = w.shape
+            if self.bits:
+                key = (w.data_ptr(), tuple(w.shape))
+                packed = self.quantized.get(key)
+                if packed is None:
+                    wq, ws, wo, _ = self.orc.quantize_weights(self._w32(w), 64, 127, self.weight_groups)
+                    packed = self.quantized[key] = self.orc.port_pack_qweights(wq, ws, wo, 64)
+                return self.orc.port_quantized_linear(x2, packed, n, 64, 255, bias, gated=gated, threads=self.threads)
+            y = self.orc.port_mul_mat(self._w32(w), x2, bias, threads=self.threads)
+            return (y, self.orc.port_gated(y, self.threads)) if gated else y
+
+        def linear(self, x, w, bias=None, add=()):
+            import torch
+
+            n, k = w.shape
+            m = x.numel() // k
+            self.count_linear(x, w)
+            if m < 16:  # ggml's node, as HipOps leaves it to torch
+                y = x.reshape(-1, k) @ torch.from_numpy(self._w32(w)).t()
+                if bias is not None:
+                    y = y + bias
+            else:
+                y = torch.from_numpy(self._product(self._np(x.reshape(-1, k)), w,
+                                                   None if bias is None else self._np(bias)))
+            for a in add:
+                y = y + a.reshape(y.shape)
+            return y.reshape(*x.shape[:-1], n)
+
+        def geglu(self, x, w, bias):
+            import torch
+
+            n, k = w.shape
+            self.count_linear(x, w)
+            _, out = self._product(self._np(x.reshape(-1, k)), w, self._np(bias), gated=True)
+            return torch.from_numpy(np.ascontiguousarray(out)).reshape(*x.shape[:-1], n // 2)
+
+        def attention(self, q, k, v, heads):
+            import torch
+
+            b, lq, c = q.shape
+            d = c // heads
+            self.count_attention(q, k, heads)
+            y = self.orc.port_attention(self._np(q).reshape(b, lq, heads, d), self._np(k).reshape(b, -1, heads, d),
+                                        self._np(v).reshape(b, -1, heads, d), 1.0 / d ** 0.5, threads=self.threads)
+            return torch.from_numpy(y).reshape(b, lq, c)
+
+    return CpuOps(threads, bits, weight_groups)
+
+
+def sdxl_block_ops(tokens=988, batch=2, c=1280):
+    """configs[4]'s operations: its products (2 M N K: Q, K, V and the output
+    projection C x C, the GEGLU C -> 8C, the FF out 4C -> C) and its attention
+    (4 L^2 C a batch)."""
+    m = tokens * batch
+    return 2.0 * m * c * (4 * c + 8 * c + 4 * c) + 4.0 * batch * tokens * tokens * c
+
+
+def cpu_configs():
+    """Per configuration: (make(threads) -> fn, work, unit, fp32): the
+    configuration's operation on the host, on synthetic inputs of its shapes
+    (weights FP16 ~N(0,0.02) widened once; the bits mode's quantized once)."""
+    orc = _orc()
+    r = np.random.default_rng(1)
+
+    def randn(*shape, std=1.0, mean=0.0):
+        return (mean + std * r.standard_normal(shape)).astype(np.float32)
+
+    def weights(*shape):
+        return randn(*shape, std=0.02).astype(np.float16).astype(np.float32)
+
+    out = {}
+    x1, w1, b1 = randn(8192, 320), weights(320, 320), randn(320, std=0.01)
+    out["cfg1_linear"] = (lambda t: (lambda: orc.port_mul_mat(w1, x1, b1, t)), 2.0 * 8192 * 320 * 320, "TFLOP/s", True)
+    x2, w2, b2, r2 = randn(2, 320, 64, 64), weights(320, 320, 3, 3), randn(320, std=0.01), randn(2, 320, 64, 64)
+    y2 = np.empty_like(x2)
+    out["cfg2_winograd4"] = (lambda t: (lambda: orc.port_winograd(x2, w2, 1, b2, r2, True, t, out=y2)),
+                             2.0 * 2 * 320 * 64 * 64 * 320 * 9, "TFLOP/s", True)
+    x3, w3, b3 = randn(2, 1280, 8, 8), weights(1280, 1280, 3, 3), randn(1280, std=0.01)
+    g3, be3 = randn(1280, std=0.1, mean=1.0), randn(1280, std=0.1)
+
+    def cfg3a(t):
+        def run():
+            y = orc.port_winograd(x3, w3, 1, b3, None, False, t)
+            orc.port_group_norm(y, 32, 1e-5, g3, be3, True, t)
+        return run
+
+    out["cfg3a_winograd2_gn_silu"] = (cfg3a, 2.0 * 2 * 1280 * 64 * 1280 * 9, "TFLOP/s", True)
+    x4, w4 = randn(2, 640, 32, 32), weights(1280, 640, 1, 1)
+
+    def cfg3b(t):
+        def run():
+            y = orc.port_conv2d(x4, w4, 1, 0, b3, None, t)
+            orc.port_group_norm(y, 32, 1e-5, g3, be3, True, t)
+        return run
+
+    out["cfg3b_pointwise_gn_silu"] = (cfg3b, 2.0 * 2 * 1280 * 1024 * 640, "TFLOP/s", True)
+    q5 = randn(2, 4096, 8, 40)
+    k5, v5 = randn(2, 4096, 8, 40), randn(2, 4096, 8, 40)
+    kc, vc = randn(2, 77, 8, 40), randn(2, 77, 8, 40)
+    s5 = 1.0 / 40 ** 0.5
+    out["cfg4_self_attention"] = (lambda t: (lambda: orc.port_attention(q5, k5, v5, s5, t)),
+                                  4.0 * 2 * 8 * 4096 * 4096 * 40, "TFLOP/s", True)
+    out["cfg4_cross_attention"] = (lambda t: (lambda: orc.port_attention(q5, kc, vc, s5, t)),
+                                   4.0 * 2 * 8 * 4096 * 77 * 40, "TFLOP/s", True)
+
+    def cfg5(t):
+        import torch
+
+        import unet_step
+
+        block = unet_step.SdxlBlock(torch.device("cpu"), seed=9)
+        x = torch.from_numpy(randn(2, 988, 1280))
+        ops = cpu_ops(t, bits=8, weight_groups=0)
+        torch.set_num_threads(t)
+        return lambda: block.forward(ops, x)
+
+    out["cfg5_sdxl_block_bits8"] = (cfg5, None, "TOPS", False)
+    return out
+
+
+def cpu_unet_step(threads, seconds):
+    """The SD1.5 UNet step (the GPU's synthetic model and inputs, random
+    weights from the CPU's generator) on the host through CpuOps: ms of the
+    fastest of the timed steps after one uncounted."""
+    import torch
+
+    import unet_step
+
+    torch.set_num_threads(threads)
+    model = unet_step.Model(unet_step.Config(), torch.device("cpu"), seed=7)
+    x, t, ctx = model.inputs(seed=8, device="cpu")
+    ops = cpu_ops(threads)
+
+    def step():
+        ops.reset()
+        return model.forward(ops, x, t, ctx)
+
+    best, runs = best_seconds(step, seconds, least=1)
+    return {"ms": round(best * 1e3, 1), "tflops": round(ops.flops / best / 1e12, 3), "threads": threads,
+            "runs": runs, "gflop": round(ops.flops / 1e9, 1)}
+
+
+def cpu_baseline(seconds):
+    """The host CPU beside the GPU: each configuration's operation by
+    oracle/port.c on all the cores this run may use and on one thread, as a
+    rate and as a fraction of the host's measured FMA peak at that thread
+    count; the UNet step on all cores; the host named (lscpu).  `value` is
+    configs[1] on all cores."""
+    import torch
+
+    orc = _orc()
+    if not orc.port_available():
+        return {"value": None, "unit": "TFLOP/s", "cores": 0, "kind": "port",
+                "sample": "not run: the host lacks AVX-512 with VNNI, which oracle/port.c is built for"}
+    threads = host_threads()
+    torch_threads = torch.get_num_threads()
+    peaks = {1: orc.port_fma_peak(1, 0.3), threads: orc.port_fma_peak(threads, 0.3)}
+    per = max(0.3, seconds / 16)
+    table = {}
+    for name, (make, work, unit, fp32) in cpu_configs().items():
+        row = {}
+        for t in (threads, 1):
+            fn = make(t)
+            best, runs = best_seconds(fn, per)
+            amount = work if work is not None else sdxl_block_ops()
+            entry = {"ms": round(best * 1e3, 3), unit.split("/")[0].lower(): round(amount / best / 1e12, 4),
+                     "runs": runs}
+            if fp32:
+                entry["fma_peak_frac"] = round(amount / best / 1e9 / peaks[t], 3)
+            row[f"threads_{t}"] = entry
+            log(f"cpu {name} {t} threads: {best * 1e3:.2f} ms ({runs} runs)")
+        table[name] = row
+    unet = cpu_unet_step(threads, max(1.0, seconds / 4))
+    log(f"cpu unet step {threads} threads: {unet['ms']} ms")
+    torch.set_num_threads(torch_threads)
+    head = table["cfg2_winograd4"][f"threads_{threads}"]
+    return {"value": head["tflop"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"the whole configs[1] convolution (F(4x4), bias + residual) in single precision, the fastest "
+                      f"of {head['runs']} runs after one uncounted, {threads} OpenMP threads (AVX-512); every "
+                      f"configuration likewise on {threads} threads and on one under 'configs', the UNet step "
+                      f"under 'unet_step'",
+            "host": host_info(), "threads": threads,
+            "fma_peak_gflops": {f"threads_{t}": round(v, 1) for t, v in peaks.items()},
+            "configs": table, "unet_step": unet,
+            "note": "oracle/port.c: this repository's AVX-512 restatement of the reference's CPU algorithms "
+                    "(packed GEMM, Winograd with transforms per block, blocked attention, VNNI W8A8); the "
+                    "reference's own x86 kernels need ggml and C++26 and are not built here.  cfg5 on the CPU: "
+                    "the block with its linear layers quantized (weights per row, kept) and attention in single "
+                    "precision (the bits mode's quantized attention is not restated in the port)"}
 
 
 # The VAE decoder's operations of the reference's bench (tools/bench.cc:146-153):
@@ -442,6 +752,102 @@ def unet_step_line(dev, args):
                                        "other hardware, context only"}}
 
 
+# Per configuration: its workload, its work (direct-convolution FLOPs for the
+# convolutions; int8 operations for configs[4]) and the roofline of its
+# dominant kernel -- the kernel(s) named, the algorithmic amount one call of
+# the configuration gives them (FLOPs, or the ideal HBM bytes where HBM
+# bounds them), the bound and MI355X's published peak.  The amounts are
+# those of the configurations' table of work units, restated:
+#   cfg1  Y = X W^T + b, X 2x4096x320 f32, W 320x320 f16: X 10.49 MB + W 0.20 +
+#         b + Y 10.49 = 21.18 MB (AI 79: HBM-bound at the split-FP16 rate)
+#   cfg2  the 36 products of 320x320 by 512 tiles: 3.775 GFLOP (the F(4x4)
+#         direct-equivalent 15.10 GFLOP for the op)
+#   cfg3a F(2x2) of 8x8 maps: the products kernel reads the FP16 weights,
+#         1280x1280x9x2 = 29.49 MB (it makes U in registers)
+#   cfg3b 1x1 conv 2x640x1024 -> 1280: 3.355 GFLOP
+#   cfg4  self: 4 b h L^2 d = 42.95 GFLOP; cross (77 keys): Q 10.49 MB + K, V
+#         0.39 MB + Y 10.49 MB = 21.37 MB (HBM)
+#   cfg5  the quantized products of the block: 103.6 G int8 operations
+CONFIGS = {
+    "cfg1_linear": dict(workload="cfg1", unit="TFLOP/s", kernels=("mul_mat",), bound="hbm", amount=21.18e6,
+                        peak=PEAK_HBM),
+    "cfg2_winograd4": dict(workload="cfg2", unit="TFLOP/s", kernels=("winograd4.products",), bound="mfma",
+                           amount=2.0 * 36 * 320 * 320 * 512, peak=PEAK_FP16_MFMA, split=3),
+    "cfg3a_winograd2_gn_silu": dict(workload="cfg3a", unit="TFLOP/s", kernels=("winograd2.products",), bound="hbm",
+                                    amount=1280 * 1280 * 9 * 2.0, peak=PEAK_HBM),
+    "cfg3b_pointwise_gn_silu": dict(workload="cfg3b", unit="TFLOP/s", kernels=("conv_direct_pointwise",),
+                                    bound="mfma", amount=2.0 * 2 * 1280 * 1024 * 640, peak=PEAK_FP16_MFMA, split=2),
+    "cfg4_self_attention": dict(workload="cfg4_self", unit="TFLOP/s", kernels=("attention",), bound="mfma",
+                                amount=4.0 * 2 * 8 * 4096 * 4096 * 40, peak=PEAK_FP16_MFMA, split=3),
+    "cfg4_cross_attention": dict(workload="cfg4_cross", unit="TFLOP/s", kernels=("attention",), bound="hbm",
+                                 amount=21.37e6, peak=PEAK_HBM),
+    "cfg5_sdxl_block_bits8": dict(workload="cfg5", unit="TOPS", kernels=("qgemm", "qgemm_gated"), bound="mfma",
+                                  amount=2.0 * 1976 * 1280 * 16 * 1280, peak=PEAK_INT8_MFMA),
+}
+
+
+def roofline(spec, kt, op_ms, work):
+    """The roofline object of a configuration's dominant kernel(s): achieved
+    = the algorithmic amount / their time per call (the library's kernel
+    profile: HIP events stamped by the kernels' own dispatch packets, on their
+    stream), against MI355X's published peak; the op's own rate beside it."""
+    ms = sum(kt[k][0] * kt[k][1] for k in spec["kernels"] if k in kt)
+    if ms <= 0:
+        return None
+    hbm = spec["bound"] == "hbm"
+    achieved = spec["amount"] / ms / (1e6 if hbm else 1e9)  # GB/s or TFLOP/s
+    out = {"kernel": "+".join(spec["kernels"]), "bound": spec["bound"], "achieved": round(achieved, 2),
+           "peak": spec["peak"], "unit": "GB/s" if hbm else ("TOPS" if spec["unit"] == "TOPS" else "TFLOP/s"),
+           "frac": round(achieved / spec["peak"], 4), "kernel_us": round(ms * 1e3, 2),
+           "amount": spec["amount"], "traffic": profiled_traffic(spec["workload"], spec["kernels"][0])}
+    if spec.get("split"):
+        # Split-FP16: each product takes `split` FP16 MFMA products.
+        out["effective_peak"] = round(spec["peak"] / spec["split"], 1)
+        out["frac_of_effective"] = round(achieved * spec["split"] / spec["peak"], 4)
+    rate = work / op_ms / 1e9
+    out["op_rate"] = round(rate, 2)
+    out["op_rate_vs_mfma_peak"] = round(rate / (PEAK_INT8_MFMA if spec["unit"] == "TOPS" else PEAK_FP16_MFMA), 4)
+    return out
+
+
+def cold_ms(fn, calls=10):
+    """ms of one call with the caches cold: before each call 1 GiB is written
+    (past the 4 MB L2 of each XCD and the 256 MB MALL); the median over
+    `calls`, HIP events around the call alone."""
+    import torch
+
+    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    times = []
+    for i in range(calls):
+        flush.fill_(float(i))
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        stop.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(stop))
+    del flush
+    times.sort()
+    return times[len(times) // 2]
+
+
+def measure_config(dev, name, args):
+    """A configuration timed warm (the mean of `steps` calls after `warmup`),
+    cold (cold_ms), its kernels and its roofline."""
+    spec = CONFIGS[name]
+    run, work = make_workload(dev, spec["workload"])
+    ms = timed(run, args.steps, args.warmup)
+    kt = kernel_times(getattr(run, "eager", run), min(args.steps, 20))
+    entry = {"ms": round(ms, 5), spec["unit"].split("/")[0].lower(): round(work / ms / 1e9, 2),
+             "cold_ms": round(cold_ms(run), 5),
+             "kernels_us": {k: round(v[0] * v[1] * 1e3, 2) for k, v in sorted(kt.items(), key=lambda kv: -kv[1][0] * kv[1][1])},
+             "roofline": roofline(spec, kt, ms, work)}
+    log(f"{name}: {ms * 1e3:.1f} us warm, {entry['cold_ms'] * 1e3:.1f} us cold, "
+        f"{work / ms / 1e9:.1f} {spec['unit']}; roofline {entry['roofline']}")
+    return entry, ms, work, kt
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -465,77 +871,39 @@ def main():
         return
 
     # The headline: configs[1], F(4x4) with bias and residual fused.
-    run, flops, path = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2)
+    _, _, path = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2)
     assert path == 4, f"configs[1] takes path {path}, not F(4x4)"
-    ms = timed(run, args.steps, args.warmup)
-    value = flops / ms / 1e9
-    log(f"cfg2 F(4x4) 64x64x320: {ms * 1e3:.1f} us, {value:.1f} TFLOP/s direct-eq")
-    kt = kernel_times(run, args.steps)
-    dominant = max(kt, key=lambda n: kt[n][0] * kt[n][1])
-    dom_ms = kt[dominant][0]
-    # The products: 36 GEMMs of OC x IC x tiles, 2 FLOP per multiply-add,
-    # each product taken as three FP16 MFMA products of its split parts, so
-    # the instruction's peak is the FP16 one and a third of it the ceiling.
-    tiles = 2 * 16 * 16
-    alg = 2.0 * 36 * 320 * 320 * tiles
+    head, ms, work, kt = measure_config(dev, "cfg2_winograd4", args)
+    value = work / ms / 1e9
     fp32 = sdhip.get_tuning("winograd_fp32") == 1
-    peak = PEAK_FP32_MFMA if fp32 else PEAK_FP16_MFMA
-    roof = {"kernel": dominant, "bound": "mfma", "achieved": round(alg / dom_ms / 1e9, 2), "peak": peak,
-            "unit": "TFLOP/s", "frac": round(alg / dom_ms / 1e9 / peak, 4),
-            "traffic": profiled_traffic("cfg2", dominant),
-            "mfma": "v_mfma_f32_16x16x4_f32" if fp32 else "v_mfma_f32_32x32x16_f16, 3 per product (split FP16)",
-            "effective_peak": peak if fp32 else round(PEAK_FP16_MFMA / 3, 1),
-            "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kt.items()}}
-    log(f"kernels: {roof['kernels_us']}")
-
-    configs = {"cfg2_winograd4": {"ms": round(ms, 5), "tflops": round(value, 2)}}
+    roof = dict(head["roofline"])
+    roof["mfma"] = "v_mfma_f32_16x16x4_f32" if fp32 else "v_mfma_f32_32x32x16_f16, 3 per product (split FP16)"
+    roof["kernels_us"] = {k: round(v[0] * 1e3, 2) for k, v in kt.items()}
+    roof["direct_eq_vs_fp16_peak"] = round(value / PEAK_FP16_MFMA, 4)
+    configs = {"cfg2_winograd4": head}
     # Beside it, the transformed weights kept from call to call, as the
     # reference's store keeps them when given a budget (none by default).
     run_k, _, _ = conv_workload(dev, 2, 320, 64, 64, 320, 3, 1, seed=2, keep=True)
     ms_k = timed(run_k, args.steps, args.warmup)
-    configs["cfg2_winograd4"]["weights_kept"] = {"ms": round(ms_k, 5), "tflops": round(flops / ms_k / 1e9, 2)}
+    head["weights_kept"] = {"ms": round(ms_k, 5), "tflop": round(work / ms_k / 1e9, 2)}
     log(f"cfg2 weights kept: {ms_k * 1e3:.1f} us")
+    del run_k
     no_store()
     if not args.only_main:
-        run1, f1 = linear_workload(dev, 320, 320, 4096, 2, seed=1)
-        m1 = timed(run1, args.steps, args.warmup)
-        configs["cfg1_linear"] = {"ms": round(m1, 5), "tflops": round(f1 / m1 / 1e9, 2),
-                                  "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kernel_times(run1, 10).items()}}
-        log(f"cfg1 linear: {m1 * 1e3:.1f} us")
-        run3a, f3a, p3a = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True,
-                                        seed=3)
-        m3a = timed(run3a, args.steps, args.warmup)
-        configs["cfg3a_winograd2_gn_silu"] = {"ms": round(m3a, 5), "tflops": round(f3a / m3a / 1e9, 2), "path": p3a,
-                                              "kernels_us": {k: round(v[0] * 1e3, 2)
-                                                             for k, v in kernel_times(run3a, 10).items()}}
-        log(f"cfg3a F(2x2)+GN+SiLU: {m3a * 1e3:.1f} us")
-        run3k, _, _ = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False, groupnorm=True, seed=3,
-                                    keep=True)
-        m3k = timed(run3k, args.steps, args.warmup)
-        configs["cfg3a_winograd2_gn_silu"]["weights_kept"] = {"ms": round(m3k, 5), "tflops": round(f3a / m3k / 1e9, 2)}
-        log(f"cfg3a weights kept: {m3k * 1e3:.1f} us")
-        no_store()
-        run3b, f3b, p3b = conv_workload(dev, 2, 640, 32, 32, 1280, 1, 0, bias=True, residual=False, groupnorm=True,
-                                        seed=4)
-        m3b = timed(run3b, args.steps, args.warmup)
-        configs["cfg3b_pointwise_gn_silu"] = {"ms": round(m3b, 5), "tflops": round(f3b / m3b / 1e9, 2),
-                                              "path": p3b,
-                                              "kernels_us": {k: round(v[0] * 1e3, 2)
-                                                             for k, v in kernel_times(run3b, 10).items()}}
-        log(f"cfg3b 1x1+GN+SiLU: {m3b * 1e3:.1f} us")
-        g5 = sdxl_block_workload(dev)
-        m5 = timed(g5.run, args.steps, args.warmup)
-        configs["cfg5_sdxl_block_bits8"] = {
-            "ms": round(m5, 5), "tops": round(g5.flops / m5 / 1e9, 2), "gop": round(g5.flops / 1e9, 2),
-            "tuning": "bits=8,weight_group=0", "store": "quantized weights kept (the reference's default)",
-            "kernels_us": {k: round(v[0] * v[1] * 1e3, 2) for k, v in kernel_times(g5.eager, 5).items()}}
-        log(f"cfg5 SDXL block bits=8: {m5 * 1e3:.1f} us, {g5.flops / m5 / 1e9:.1f} TOPS")
-        for name, lk in (("cfg4_self_attention", 4096), ("cfg4_cross_attention", 77)):
-            run4, f4 = attention_workload(dev, 2, 8, 4096, lk, 40, seed=5)
-            m4 = timed(run4, args.steps, args.warmup)
-            configs[name] = {"ms": round(m4, 5), "tflops": round(f4 / m4 / 1e9, 2),
-                             "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in kernel_times(run4, 5).items()}}
-            log(f"{name}: {m4 * 1e3:.1f} us, {f4 / m4 / 1e9:.1f} TFLOP/s")
+        for name in CONFIGS:
+            if name == "cfg2_winograd4":
+                continue
+            configs[name] = measure_config(dev, name, args)[0]
+            if name == "cfg3a_winograd2_gn_silu":
+                run3k, f3a, _ = conv_workload(dev, 2, 1280, 8, 8, 1280, 3, 1, bias=True, residual=False,
+                                              groupnorm=True, seed=3, keep=True)
+                m3k = timed(run3k, args.steps, args.warmup)
+                configs[name]["weights_kept"] = {"ms": round(m3k, 5), "tflop": round(f3a / m3k / 1e9, 2)}
+                del run3k
+                no_store()
+        configs["cfg5_sdxl_block_bits8"].update(
+            {"gop": round(sdxl_block_ops() / 1e9, 2), "tuning": "bits=8,weight_group=0",
+             "store": "quantized weights kept (the reference's default)"})
 
     line = {
         "metric": METRIC,
@@ -563,6 +931,11 @@ def main():
     if not args.no_cpu:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if not args.no_unet:
+            host = line["cpu_baseline"].get("unet_step")
+            if host:
+                line["unet_step"]["host_cpu"] = host
+                line["unet_step"]["vs_host_cpu"] = round(host["ms"] / line["unet_step"]["ms"], 1)
     print(json.dumps(line), flush=True)
 
 

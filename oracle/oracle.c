@@ -701,3 +701,12 @@ void oracle_quantized_winograd2(const float *x, int64_t n, int64_t ic, int64_t i
     free(v); free(u); free(xq); free(xs); free(xo); free(wq); free(ws); free(wo); free(wsum);
     free(tq); free(ts); free(to); free(tsum); free(m);
 }
+
+/* Whether this host runs port.c's code, which is built for AVX-512 F, BW, DQ,
+ * VL and VNNI; this file is not, so the check itself runs anywhere. */
+int oracle_port_available(void) {
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+           __builtin_cpu_supports("avx512dq") && __builtin_cpu_supports("avx512vl") &&
+           __builtin_cpu_supports("avx512vnni");
+}

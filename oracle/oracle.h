@@ -24,6 +24,7 @@
 #ifndef SDHIP_ORACLE_H
 #define SDHIP_ORACLE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -156,16 +157,57 @@ void oracle_quantized_attention(const float *q, const float *k, const float *v, 
                                 int64_t lk, int64_t h, int64_t hk, int64_t b, float scale, int64_t group,
                                 int input_levels, int weight_max, int64_t key_block, float *y);
 
-/* ---- CPU-baseline restatements (port.c), threads OpenMP threads */
+/* ---- CPU-baseline restatements (port.c), threads OpenMP threads; built
+ * for AVX-512 with VNNI: call oracle_port_available() first. */
+
+/* 1 if this host runs port.c's code (AVX-512 F/BW/DQ/VL and VNNI). */
+int oracle_port_available(void);
 
 /* Winograd F(4x4, 3x3) of winograd.cc:1548-1613 with bias and residual:
  * x [n][ic][ih][iw], w [oc][ic][3][3] widened, y [n][oc][oh][ow]. */
 void oracle_port_winograd4(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
                            int p0, int p1, const float *bias, const float *residual, float *y, int threads);
+/* Winograd F(2x2, 3x3), the same arguments. */
+void oracle_port_winograd2(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
+                           int p0, int p1, const float *bias, const float *residual, float *y, int threads);
+/* CONV_2D directly: x [n][ic][ih][iw], w [oc][ic][kh][kw], strides s0 (x),
+ * s1 (y), pads p0, p1; bias [oc] and residual (as y) may be NULL. */
+void oracle_port_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
+                        int64_t kh, int64_t kw, int s0, int s1, int p0, int p1, const float *bias,
+                        const float *residual, float *y, int threads);
 
 /* MUL_MAT in single precision: y[m][n] = sum_k x[m][k] w[n][k] (+ bias[n]). */
 void oracle_port_mul_mat(const float *w, const float *x, const float *bias, int64_t M, int64_t N, int64_t K, float *y,
                          int threads);
+
+/* GROUP_NORM with gamma, beta (NULL: 1, 0) and SiLU; x, y [n][c][hw]. */
+void oracle_port_group_norm(const float *x, float *y, int64_t n, int64_t c, int64_t hw, int groups, float eps,
+                            const float *gamma, const float *beta, int silu, int threads);
+/* NORM over rows of len, with gamma, beta. */
+void oracle_port_norm(const float *x, float *y, int64_t rows, int64_t len, float eps, const float *gamma,
+                      const float *beta, int threads);
+
+/* FLASH_ATTN_EXT in single precision: q [b][lq][h][d], k [b][lk][h][d],
+ * v [b][lk][h][dv], y [b][lq][h][dv]. */
+void oracle_port_attention(const float *q, const float *k, const float *v, int64_t b, int64_t lq, int64_t lk,
+                           int64_t h, int64_t d, int64_t dv, float scale, float *y, int threads);
+
+/* The bits mode's MUL_MAT: weights quantized by oracle_quantize_weights and
+ * packed once (oracle_port_qweights_bytes of memory), inputs quantized per
+ * call; y [M][N] (+ bias); with `gated`, out [M][N / 2] = y[:, :N/2]
+ * GELU(y[:, N/2:]).  Per group in the order of oracle_qgemm, so that y is
+ * oracle_qgemm's bits (plus the bias). */
+size_t oracle_port_qweights_bytes(int64_t N, int64_t groups, int64_t group);
+void oracle_port_pack_qweights(const int8_t *wq, const float *ws, const float *wo, int64_t N, int64_t groups,
+                               int64_t group, void *packed);
+void oracle_port_quantized_linear(const float *x, int64_t M, int64_t K, const void *packed, int64_t N, int64_t group,
+                                  int levels, const float *bias, float *y, int gated, float *out, int threads);
+
+/* out [M][N / 2] = y[:, :N/2] GELU(y[:, N/2:]), the GEGLU of a product. */
+void oracle_port_gated(const float *y, int64_t M, int64_t N, float *out, int threads);
+
+/* The host's single-precision FMA rate on `threads` threads, GFLOP/s. */
+double oracle_port_fma_peak(int threads, double seconds);
 
 #ifdef __cplusplus
 }

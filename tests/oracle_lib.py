@@ -41,6 +41,21 @@ def lib():
         L.oracle_exponential_array.argtypes = [_f, _f, _L]
         L.oracle_gelu_array.argtypes = [_f, _f, _L]
         L.oracle_port_mul_mat.argtypes = [_f, _f, ctypes.c_void_p, _L, _L, _L, _f, _I]
+        L.oracle_port_available.restype = _I
+        _v = ctypes.c_void_p
+        for name in ("oracle_port_winograd4", "oracle_port_winograd2"):
+            getattr(L, name).argtypes = [_f, _L, _L, _L, _L, _f, _L, _I, _I, _v, _v, _f, _I]
+        L.oracle_port_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _v, _v, _f, _I]
+        L.oracle_port_group_norm.argtypes = [_f, _f, _L, _L, _L, _I, _F, _v, _v, _I, _I]
+        L.oracle_port_norm.argtypes = [_f, _f, _L, _L, _F, _v, _v, _I]
+        L.oracle_port_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _F, _f, _I]
+        L.oracle_port_qweights_bytes.restype = ctypes.c_size_t
+        L.oracle_port_qweights_bytes.argtypes = [_L, _L, _L]
+        L.oracle_port_pack_qweights.argtypes = [_s8, _f, _f, _L, _L, _L, _u8]
+        L.oracle_port_quantized_linear.argtypes = [_f, _L, _L, _u8, _L, _L, _I, _v, _f, _I, _v, _I]
+        L.oracle_port_gated.argtypes = [_f, _L, _L, _f, _I]
+        L.oracle_port_fma_peak.restype = ctypes.c_double
+        L.oracle_port_fma_peak.argtypes = [_I, ctypes.c_double]
         L.oracle_gated_gelu_array.argtypes = [_f, _f, _f, _L]
         L.oracle_exact_mul_mat.argtypes = [_f, _L, _f, _L, _L, _L, _L, _d, _d]
         L.oracle_exact_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L, _d, _d]
@@ -122,6 +137,111 @@ def port_mul_mat(w, x, bias=None, threads=1):
 
 def c32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _opt(a):
+    """A float32 array's pointer, or NULL for None (kept alive by the caller)."""
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def port_available():
+    """Whether this host runs port.c (AVX-512 with VNNI)."""
+    return bool(lib().oracle_port_available())
+
+
+def port_winograd(x, w, pad, bias=None, residual=None, four=True, threads=1, out=None):
+    """port.c's Winograd F(4x4, 3x3) (four) or F(2x2, 3x3): x [n, ic, h, w],
+    w [oc, ic, 3, 3] -> y [n, oc, oh, ow] (+ bias [oc], + residual)."""
+    x, w = c32(x), c32(w)
+    n, ic, h, wd = x.shape
+    oc = w.shape[0]
+    bias = None if bias is None else c32(bias)
+    residual = None if residual is None else c32(residual)
+    y = out if out is not None else np.empty((n, oc, h + 2 * pad - 2, wd + 2 * pad - 2), np.float32)
+    fn = lib().oracle_port_winograd4 if four else lib().oracle_port_winograd2
+    fn(x, n, ic, h, wd, w, oc, pad, pad, _opt(bias), _opt(residual), y, threads)
+    return y
+
+
+def port_conv2d(x, w, stride=1, pad=0, bias=None, residual=None, threads=1, out=None):
+    """port.c's direct convolution: x [n, ic, h, w], w [oc, ic, kh, kw]."""
+    x, w = c32(x), c32(w)
+    n, ic, h, wd = x.shape
+    oc, _, kh, kw = w.shape
+    oh, ow = (h + 2 * pad - kh) // stride + 1, (wd + 2 * pad - kw) // stride + 1
+    bias = None if bias is None else c32(bias)
+    residual = None if residual is None else c32(residual)
+    y = out if out is not None else np.empty((n, oc, oh, ow), np.float32)
+    lib().oracle_port_conv2d(x, n, ic, h, wd, w, oc, kh, kw, stride, stride, pad, pad, _opt(bias), _opt(residual), y,
+                             threads)
+    return y
+
+
+def port_group_norm(x, groups, eps, gamma=None, beta=None, silu=False, threads=1):
+    x = c32(x)
+    gamma = None if gamma is None else c32(gamma)
+    beta = None if beta is None else c32(beta)
+    y = np.empty_like(x)
+    n, c = x.shape[:2]
+    lib().oracle_port_group_norm(x, y, n, c, x[0, 0].size, groups, eps, _opt(gamma), _opt(beta), int(silu), threads)
+    return y
+
+
+def port_norm(x, eps, gamma=None, beta=None, threads=1):
+    x = c32(x)
+    gamma = None if gamma is None else c32(gamma)
+    beta = None if beta is None else c32(beta)
+    y = np.empty_like(x)
+    lib().oracle_port_norm(x, y, x.size // x.shape[-1], x.shape[-1], eps, _opt(gamma), _opt(beta), threads)
+    return y
+
+
+def port_attention(q, k, v, scale, threads=1):
+    """port.c's attention: q [b, lq, h, d], k [b, lk, h, d], v [b, lk, h, dv]
+    -> y [b, lq, h, dv]."""
+    q, k, v = c32(q), c32(k), c32(v)
+    b, lq, h, d = q.shape
+    lk, dv = k.shape[1], v.shape[3]
+    y = np.empty((b, lq, h, dv), np.float32)
+    lib().oracle_port_attention(q, k, v, b, lq, lk, h, d, dv, scale, y, threads)
+    return y
+
+
+def port_pack_qweights(wq, ws, wo, group):
+    """The quantized weights (quantize_weights' q, scale, offset) packed for
+    port_quantized_linear."""
+    n, kp = wq.shape
+    groups = kp // group
+    packed = np.zeros(lib().oracle_port_qweights_bytes(n, groups, group), np.uint8)
+    lib().oracle_port_pack_qweights(np.ascontiguousarray(wq), c32(ws), c32(wo), n, groups, group, packed)
+    return packed
+
+
+def port_quantized_linear(x, packed, n, group=64, levels=255, bias=None, gated=False, threads=1):
+    """port.c's bits-mode MUL_MAT: x [M, K] -> y [M, n] (+ bias); with gated,
+    (y, y[:, :n/2] GELU(y[:, n/2:]))."""
+    x = c32(x)
+    m, k = x.shape
+    bias = None if bias is None else c32(bias)
+    y = np.empty((m, n), np.float32)
+    out = np.empty((m, n // 2), np.float32) if gated else None
+    lib().oracle_port_quantized_linear(x, m, k, packed, n, group, levels, _opt(bias), y, int(gated), _opt(out),
+                                       threads)
+    return (y, out) if gated else y
+
+
+def port_gated(y, threads=1):
+    """port.c's GEGLU of a product y [M, N]: y[:, :N/2] GELU(y[:, N/2:])."""
+    y = c32(y)
+    m, n = y.shape
+    out = np.empty((m, n // 2), np.float32)
+    lib().oracle_port_gated(y, m, n, out, threads)
+    return out
+
+
+def port_fma_peak(threads, seconds=0.3):
+    """The host's single-precision FMA rate on `threads` threads, GFLOP/s."""
+    return lib().oracle_port_fma_peak(threads, seconds)
 
 
 def metric(y, exact, mag):

@@ -174,24 +174,6 @@ def test_winograd_matrices_compute_the_convolution():
         assert np.allclose(y, want, atol=1e-13)
 
 
-def test_port_winograd4_within_the_reference_bound():
-    """oracle/port.c's F(4x4) (the CPU baseline) against float64: within the
-    reference's published 5-11e-7 class, and the 2e-5 bound."""
-    import ctypes
-
-    L = orc.lib()
-    f = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
-    I64, I = ctypes.c_int64, ctypes.c_int
-    L.oracle_port_winograd4.argtypes = [f, I64, I64, I64, I64, f, I64, I, I, ctypes.c_void_p, ctypes.c_void_p, f, I]
-    r = rng(8)
-    n, ic, h, w, oc = 2, 13, 18, 22, 11
-    x = uniform(r, (n, ic, h, w), 1.0)
-    k = uniform(r, (oc, ic, 3, 3), 0.25).astype(np.float16).astype(np.float32)
-    y = np.zeros((n, oc, h, w), np.float32)
-    L.oracle_port_winograd4(x, n, ic, h, w, k, oc, 1, 1, None, None, y, 2)
-    exact, mag = orc.exact_conv2d(x, k, 1, 1, 1, 1, 1, 1)
-    assert orc.metric(y, exact, mag) <= 2e-6
-
 # ------------------------------------------------------------------ norms
 
 
@@ -353,24 +335,6 @@ def test_quantized_product_against_its_own_integers_and_float64():
     init = uniform(r, (M, N), 1.0)
     y2 = orc.quantized_mul_mat(w, x, init=init)[0]
     assert np.allclose(y2, y + init, atol=1e-5)
-
-
-def test_port_mul_mat_within_the_reference_bound():
-    """port.c's single-precision GEMM (the CPU baseline of MUL_MAT) against
-    float64: the reference's 2e-5 bound with its bias, at a ragged shape and
-    at threads 1 and 3 alike; a transposed operand or a dropped bias fails."""
-    r = rng(21)
-    N, K, M = 37, 150, 43
-    w = uniform(r, (N, K), 0.25).astype(np.float16).astype(np.float32)
-    x = uniform(r, (M, K), 1.0)
-    b = uniform(r, (N,), 1.0)
-    exact, mag = orc.exact_mul_mat(w, x)
-    y1 = orc.port_mul_mat(w, x, b, threads=1)
-    y3 = orc.port_mul_mat(w, x, b, threads=3)
-    assert orc.metric(y1, exact + b, mag + np.abs(b)) <= 2e-5
-    assert np.array_equal(y1, y3)
-    y0 = orc.port_mul_mat(w, x, None, threads=2)
-    assert orc.metric(y0, exact, mag) <= 2e-5
 
 
 # ------------------------------------------------------------------ quantized attention
