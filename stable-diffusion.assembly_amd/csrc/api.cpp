@@ -55,7 +55,7 @@ namespace {
 // names take any integer, as its parser does (cpu.cc:180-212), and clamp or
 // read them as it does (quant.cc:53-67, winograd.cc:1204-1206): kAny.  This
 // library's own names take only the values they are documented with.
-enum Range { kAny, kFlag, kStages, kTiles, kNonNegative, kBits, kCore };
+enum Range { kAny, kFlag, kStages, kTiles, kNonNegative, kBits, kCore, kFlag2 };
 
 struct Field {
     const char *name;
@@ -113,6 +113,7 @@ const Field kFields[] = {
     {"gemm_stages", &Tuning::gemm_stages, kStages},
     {"gemm_tiles", &Tuning::gemm_tiles, kTiles},
     {"gemm_core", &Tuning::gemm_core, kCore},
+    {"qgemm_core", &Tuning::qgemm_core, kFlag2},
     {"attention_generic", &Tuning::attention_generic, kFlag},
     {"attention_fp32", &Tuning::attention_fp32, kFlag},
 };
@@ -130,9 +131,12 @@ bool in_range(Range r, long v, const char *&takes) {
         takes = "2 or 4";
         return v == 2 || v == 4;
     case kTiles:
-        takes = "0, 11, 12, 21 or 22";
-        return v == 0 || v == 11 || v == 12 || v == 21 || v == 22;
+        takes = "0, 11, 12, 21, 22 (the LDS cores' blocks) or 42, 44, 52, 55 (gemm_core=3's wave tiles)";
+        return v == 0 || v == 11 || v == 12 || v == 21 || v == 22 || v == 42 || v == 44 || v == 52 || v == 55;
     case kCore:
+        takes = "1, 2 or 3";
+        return v == 1 || v == 2 || v == 3;
+    case kFlag2:
         takes = "1 or 2";
         return v == 1 || v == 2;
     case kNonNegative:

@@ -15,6 +15,7 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef int int4v __attribute__((ext_vector_type(4)));
+typedef int int16v __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 
@@ -213,6 +214,14 @@ __device__ __forceinline__ void wait_loads() {
 // itself (wait_loads).  The memory clobber keeps the compiler from moving
 // loads or stores across it.
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// The wave's own LDS accesses done (lgkmcnt(0), nothing else waited for),
+// then the workgroup's barrier: what __syncthreads gives the LDS without its
+// wait for every global load in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    barrier_only();
+}
 
 // One 16-byte piece a lane of a 1 KB copy from global memory into LDS; the
 // LDS address is the wave's (lane l's piece lands 16 l bytes past it).

@@ -420,7 +420,7 @@ __device__ __forceinline__ void main_loop(float16v (&acc)[TM][TN], LA (&la)[NS],
 #pragma unroll
     for (int q = 0; q < NS; ++q) load(q, at(q));
     store(0, 0);
-    __syncthreads();
+    lds_barrier();
     load(0, at(NS));
     // At the top of each pass: buffer 0 holds step s, stages 1 .. NS - 1 steps
     // s + 1 .. s + NS - 1, stage 0 step s + NS on its way.  One exit, at the
@@ -430,7 +430,7 @@ __device__ __forceinline__ void main_loop(float16v (&acc)[TM][TN], LA (&la)[NS],
         for (int q = 0; q < NS; ++q) {
             if (s + q < steps) compute(q & 1);
             store((q + 1) % NS, (q + 1) & 1);
-            __syncthreads();
+            lds_barrier();
             load((q + 1) % NS, at(s + q + 1 + NS));
         }
     }

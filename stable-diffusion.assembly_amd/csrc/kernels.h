@@ -144,5 +144,8 @@ hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStrea
 // 21, 22 for blocks of 64 WM x 64 WN), or 0 to choose by the size.
 bool split_batched2_takes(const SplitBatchedArgs &p);
 hipError_t launch_split_batched2(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream);
+// The same products with no LDS (gemm3.hip): each wave's operands loaded
+// straight into its registers; the same operands as split_batched2_takes.
+hipError_t launch_split_batched3(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream);
 
 }  // namespace sdhip

@@ -20,9 +20,11 @@
 // so that the result is the reference's C++ result, bit for bit, when the
 // sum starts from the same number (0, or the residual with from_redirect).
 //
-// Layout in the work buffer: each group of k padded to a slot of 64 bytes
-// (the MFMA's k), inputs [M][groups][slot] and weights [N][groups][slot],
-// then the scales, offsets and (weights) integer sums [rows][groups].
+// Layout in the work buffer: each group of k padded to a slot (a multiple
+// of 64 bytes, the MFMA's k), cut into steps of 64 bytes; the bytes held
+// step-major, inputs [step][M][64] and weights [step][N][64], so that one
+// step of 32 consecutive rows is 2 KB in a row; then the scales, offsets
+// and (weights) integer sums, group-major, [groups][rows].
 
 #include "host.h"
 #include "profile.h"
@@ -54,6 +56,7 @@ Quant quant_of(const Tuning &t) {
 
 struct Layout {
     int64_t groups, slot, kp;  // groups of k, bytes a group takes, bytes a row takes
+    int64_t m, n;              // rows of the inputs and of the weights
     size_t xq, xs, xo, wq, ws, wo, wsum, total;
 };
 
@@ -62,6 +65,8 @@ Layout layout_of(int64_t K, int64_t N, int64_t M, const Quant &q) {
     l.groups = ceil_div(K, q.group);
     l.slot = round_up(q.group, 64);
     l.kp = l.groups * l.slot;
+    l.m = M;
+    l.n = N;
     size_t at = 0;
     const auto take = [&](size_t bytes) {
         const size_t here = at;
@@ -133,7 +138,8 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(Src src, int64_t M
     const float s = __fdiv_rn(__fsub_rn(hi, lo), levels);
     const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
     const float zero = rintf(__fmul_rn(-lo, inverse));
-    int8_t *dst = xq + m * l.kp + g * l.slot;
+    // Slot byte e: step g (slot / 64) + e / 64, byte e % 64.
+    int8_t *dst = xq + (g * (l.slot / 64) * l.m + m) * 64;
     for (int64_t e = lane; e < l.slot; e += 64) {
         float v = 0.0f;
         if (e < n) {
@@ -143,11 +149,51 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(Src src, int64_t M
         } else {
             v = 128.0f;  // the slot's padding: 0 after the shift, times a weight of 0
         }
-        dst[e] = static_cast<int8_t>(static_cast<int>(v) - 128);
+        dst[(e >> 6) * l.m * 64 + (e & 63)] = static_cast<int8_t>(static_cast<int>(v) - 128);
     }
     if (lane == 0) {
-        xs[m * l.groups + g] = s;
-        xo[m * l.groups + g] = __fmul_rn(s, zero);
+        xs[g * l.m + m] = s;
+        xo[g * l.m + m] = __fmul_rn(s, zero);
+    }
+}
+
+// The same quantizer for groups of 64 that fill their slots (K a multiple of
+// 64, rows of x 16-byte aligned): 16 lanes a (row, group), each lane 4
+// consecutive numbers (one 16-byte load), the least and greatest reduced
+// over the 16 lanes, and the lane's 4 bytes written as one word -- a wave
+// takes 4 groups, where the general kernel takes one, with no loop.  The
+// same IEEE operations in the same order: the same bytes, scales and
+// offsets.
+__global__ __launch_bounds__(256) void quantize_inputs64_kernel(const float *__restrict__ x, int64_t ldx, int64_t M,
+                                                                int64_t groups, float levels,
+                                                                int8_t *__restrict__ xq, float *__restrict__ xs,
+                                                                float *__restrict__ xo) {
+    const int64_t seg = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+    if (seg >= M * groups) return;
+    const int j = threadIdx.x & 15;
+    const int64_t m = seg / groups;
+    const int64_t g = seg - m * groups;
+    const float4v v = *reinterpret_cast<const float4v *>(x + m * ldx + 64 * g + 4 * j);
+    float lo = fminf(fminf(fminf(0.0f, v[0]), fminf(v[1], v[2])), v[3]);
+    float hi = fmaxf(fmaxf(fmaxf(0.0f, v[0]), fmaxf(v[1], v[2])), v[3]);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, off, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+    }
+    const float s = __fdiv_rn(__fsub_rn(hi, lo), levels);
+    const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+    const float zero = rintf(__fmul_rn(-lo, inverse));
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float q = clampf(__fadd_rn(rintf(__fmul_rn(v[e], inverse)), zero), 0.0f, levels);
+        word |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int>(q) - 128)) << (8 * e);
+    }
+    *reinterpret_cast<uint32_t *>(xq + (g * M + m) * 64 + 4 * j) = word;
+    if (j == 0) {
+        xs[g * M + m] = s;
+        xo[g * M + m] = __fmul_rn(s, zero);
     }
 }
 
@@ -196,21 +242,21 @@ __global__ __launch_bounds__(256) void quantize_weights_kernel(const W *__restri
         }
         const float s = __fdiv_rn(m, wmax);
         const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
-        int8_t *dst = wq + n * l.kp + g * l.slot;
+        int8_t *dst = wq + (g * (l.slot / 64) * l.n + n) * 64;
         int sum = 0;
         for (int64_t e = lane; e < l.slot; e += 64) {
             int v = 0;
             if (e < cnt) {
                 v = static_cast<int>(clampf(rintf(__fmul_rn(static_cast<float>(row[k0 + e]), inverse)), -wmax, wmax));
             }
-            dst[e] = static_cast<int8_t>(v);
+            dst[(e >> 6) * l.n * 64 + (e & 63)] = static_cast<int8_t>(v);
             sum += v;
         }
         sum = wave_isum(sum);
         if (lane == 0) {
-            ws[n * l.groups + g] = s;
-            wo[n * l.groups + g] = __fmul_rn(s, static_cast<float>(sum));
-            wsum[n * l.groups + g] = sum;
+            ws[g * l.n + n] = s;
+            wo[g * l.n + n] = __fmul_rn(s, static_cast<float>(sum));
+            wsum[g * l.n + n] = sum;
         }
     }
 }
@@ -235,6 +281,7 @@ struct QgemmArgs {
     int64_t M, N, half;
     int64_t ne1, ne2;
     int64_t groups, slot, kp;
+    int64_t xrows, wrows;  // rows of the layouts: the step and group strides (x 64 bytes, x 1)
     int64_t col_blocks;
     int32_t from_redirect;
     DevChain chain;
@@ -277,18 +324,18 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
     float rsa = 0.f, roa = 0.f, rsb = 0.f, rob = 0.f;
     int32_t rqs = 0;
     const auto load = [&](int64_t g, int64_t sub) {
-        const int64_t off = g * p.slot + sub * 64 + lq;
-        ra = arow >= 0 ? *reinterpret_cast<const int4v *>(p.xq + arow * p.kp + off) : int4v{};
-        rb = brow >= 0 ? *reinterpret_cast<const int4v *>(p.wq + brow * p.kp + off) : int4v{};
+        const int64_t step = g * (p.slot / 64) + sub;
+        ra = arow >= 0 ? *reinterpret_cast<const int4v *>(p.xq + (step * p.xrows + arow) * 64 + lq) : int4v{};
+        rb = brow >= 0 ? *reinterpret_cast<const int4v *>(p.wq + (step * p.wrows + brow) * 64 + lq) : int4v{};
         if (tid < kQB) {
             const int64_t r = m0 + tid;
-            rsa = r < p.M ? p.xs[r * p.groups + g] : 0.0f;
-            roa = r < p.M ? p.xo[r * p.groups + g] : 0.0f;
+            rsa = r < p.M ? p.xs[g * p.xrows + r] : 0.0f;
+            roa = r < p.M ? p.xo[g * p.xrows + r] : 0.0f;
         } else if (tid < 2 * kQB) {
             const int64_t c = w_row(tid - kQB);
-            rsb = c >= 0 ? p.ws[c * p.groups + g] : 0.0f;
-            rob = c >= 0 ? p.wo[c * p.groups + g] : 0.0f;
-            rqs = c >= 0 ? p.wsum[c * p.groups + g] : 0;
+            rsb = c >= 0 ? p.ws[g * p.wrows + c] : 0.0f;
+            rob = c >= 0 ? p.wo[g * p.wrows + c] : 0.0f;
+            rqs = c >= 0 ? p.wsum[g * p.wrows + c] : 0;
         }
     };
     const auto store = [&](int buf) {
@@ -429,6 +476,307 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
             }
         }
     }
+}
+
+// The same products by wider tiles (64 x 64 a wave) on v_mfma_i32_32x32x32_i8,
+// fed by a deep ring of LDS stages.
+//
+// Per group a wave's MFMAs are few and its dequantisation long -- five VALU
+// operations an output, the reference's fma order fixed by bit-exactness --
+// and a K-step (one 64-byte step of a group's slot) is a few hundred cycles,
+// well under the memory's latency: the loads of a step are issued S - 1
+// steps ahead, each straight into LDS by global_load_lds (no register
+// staging, so that S can be 8), with the wave's own wait for its copies and
+// a bare s_barrier the only synchronisation.
+//
+// A workgroup of 4 waves (2 x 2) covers 128 rows of x (tokens) by 128 rows
+// of W (features; GATED: 64 features and their 64 gates, each wave's two
+// column tiles a pair).  A stage holds the step's 128 rows of bytes of each
+// operand (the layouts are step-major, so each is 8 KB in a row), the row
+// scales and offsets of its group and the column scales, offsets and sums.
+// The 16-byte piece p of a row r lands at p ^ s(r), s(r) = ((r >> 1) ^
+// (r >> 2)) & 3 (the copies pick which global piece each lane brings), so
+// that the 32 rows a fragment read takes spread over the banks.  Lane l of
+// a wave takes 32 bytes of its row at byte 32 (l / 32) of the step's 64, the
+// first 16 to the first MFMA and the rest to the second: A and B take the
+// same order of k, and integer sums do not depend on it.
+constexpr int kQRows = 128;                      // rows of each operand a block
+constexpr int kQStageA = kQRows * 64;            // bytes of a step's rows
+constexpr int kQScales = kQRows * 4;             // bytes of one row of scales
+constexpr int kQStage = 2 * kQStageA + 5 * kQScales;  // A, B, sa, oa, sb, ob, qs
+constexpr int kQUnits16 = 2 * kQStageA / 1024;   // 1 KB copies (16 bytes a lane)
+constexpr int kQUnits4 = 5 * kQScales / 256;     // 256-byte copies (4 bytes a lane)
+constexpr int kQCopies = kQUnits16 / 4 + (kQUnits4 + 3) / 4;  // a wave's copies a step
+
+__device__ __forceinline__ int qswizzle(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+
+template <bool GATED, int S>
+__global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
+    static_assert(kQUnits16 % 4 == 0, "1 KB copies shared evenly");
+    __shared__ __attribute__((aligned(1024))) char lds[S * kQStage];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave >> 1, wc = wave & 1;
+    const int r32 = lane & 31, h = lane >> 5;
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t mb = b / p.col_blocks;
+    const int64_t nb = b % p.col_blocks;
+    const int64_t m0 = mb * kQRows;
+    const int64_t n0 = nb * (GATED ? kQRows / 2 : kQRows);
+    // The W row of block row r (clamped): GATED, rows 0..63 features n0 +
+    // r and rows 64..127 their gates.
+    const auto w_row = [&](int r) -> int64_t {
+        if (GATED) {
+            const int64_t f = n0 + (r & 63);
+            return (r >> 6) * p.half + (f < p.half ? f : p.half - 1);
+        }
+        return n0 + r < p.N ? n0 + r : p.N - 1;
+    };
+    const auto x_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : p.M - 1; };
+
+    // This wave's copies a step: 1 KB units wave + 4 q (A's rows for units
+    // 0..7, B's for 8..15, 16 rows each), then 256-byte units 16 + wave +
+    // 4 q of the scales (sa, oa, sb, ob, qs: two units each); waves past the
+    // last unit repeat it.  Per copy: the lane's source at step 0, its
+    // stride a step (bytes of the row layout) or a group (scales), and the
+    // stage offset of the unit.
+    constexpr int C16 = kQUnits16 / 4, C4 = (kQUnits4 + 3) / 4;
+    const int8_t *src16[C16];
+    int dst16[C16];
+#pragma unroll
+    for (int q = 0; q < C16; ++q) {
+        const int u = wave + 4 * q;
+        const int op = u / (kQUnits16 / 2);  // 0: A, 1: B
+        const int row = 16 * (u % (kQUnits16 / 2)) + (lane >> 2);
+        const int piece = (lane & 3) ^ qswizzle(row);
+        src16[q] = op == 0 ? p.xq + x_row(row) * 64 + 16 * piece : p.wq + w_row(row) * 64 + 16 * piece;
+        dst16[q] = op * kQStageA + 16 * (u % (kQUnits16 / 2)) * 64;
+    }
+    const char *src4[C4];
+    int dst4[C4], kind4[C4];
+#pragma unroll
+    for (int q = 0; q < C4; ++q) {
+        int u = wave + 4 * q;
+        u = u < kQUnits4 ? u : kQUnits4 - 1;
+        const int which = u / 2;  // sa, oa, sb, ob, qs
+        const int row = 64 * (u % 2) + lane;
+        kind4[q] = which;
+        const char *base = which == 0   ? reinterpret_cast<const char *>(p.xs + x_row(row))
+                           : which == 1 ? reinterpret_cast<const char *>(p.xo + x_row(row))
+                           : which == 2 ? reinterpret_cast<const char *>(p.ws + w_row(row))
+                           : which == 3 ? reinterpret_cast<const char *>(p.wo + w_row(row))
+                                        : reinterpret_cast<const char *>(p.wsum + w_row(row));
+        src4[q] = base;
+        dst4[q] = 2 * kQStageA + which * kQScales + 256 * (u % 2);
+    }
+    const int64_t subs = p.slot / 64;
+    const int64_t steps = p.groups * subs;
+    const int64_t last = steps - 1;
+    const auto copy_step = [&](int64_t s, int stage) {
+        const int64_t k = s < last ? s : last;
+        const int64_t g = k / subs;
+        char *base = lds + stage * kQStage;
+#pragma unroll
+        for (int q = 0; q < C16; ++q) {
+            const int64_t stride = (wave + 4 * q) < kQUnits16 / 2 ? p.xrows * 64 : p.wrows * 64;
+            __builtin_amdgcn_global_load_lds(src16[q] + k * stride, (__attribute__((address_space(3))) void *)(base + dst16[q]),
+                                             16, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < C4; ++q) {
+            const int64_t stride = kind4[q] < 2 ? p.xrows * 4 : p.wrows * 4;
+            __builtin_amdgcn_global_load_lds(src4[q] + g * stride, (__attribute__((address_space(3))) void *)(base + dst4[q]),
+                                             4, 0, 0);
+        }
+    };
+
+    // The outputs: tile (i, j) of the wave, lane column r32, rows
+    // 8 (e / 4) + 4 h + e % 4.
+    float t[2][2][16];
+    const auto out_row = [&](int i, int e) -> int64_t { return m0 + wr * 64 + 32 * i + 4 * h + tile_row(e); };
+    const auto out_col = [&](int j) -> int64_t { return n0 + 64 * wc + 32 * j + r32; };
+    if (!GATED && p.from_redirect) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t n = out_col(j);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int64_t m = out_row(i, e);
+                    t[i][j][e] = (m < p.M && n < p.N) ? p.y[m * p.ldy + n] : 0.0f;
+                }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) t[i][j][e] = 0.0f;
+    }
+
+    // Fragment reads: A tile i at block row wr 64 + 32 i + r32, B tile j at
+    // block row (GATED: j 64 + wc 32 + r32; else wc 64 + 32 j + r32), the two
+    // 16-byte pieces 2 h and 2 h + 1 at their swizzled places.
+    int aread[2][2], bread[2][2], brow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = wr * 64 + 32 * i + r32;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) aread[i][q] = row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = GATED ? 64 * j + 32 * wc + r32 : 64 * wc + 32 * j + r32;
+        brow[j] = row;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) bread[j][q] = kQStageA + row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
+    }
+
+    int16v acc[2][2];
+    const auto compute = [&](int stage, int64_t sub) {
+        const char *base = lds + stage * kQStage;
+        int4v a[2][2], bv[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) a[i][q] = *reinterpret_cast<const int4v *>(base + aread[i][q]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) bv[j][q] = *reinterpret_cast<const int4v *>(base + bread[j][q]);
+        // A group's first step starts its sums from zero (a branch uniform
+        // over the workgroup).
+        if (sub == 0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][0], bv[j][0], int16v{}, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][0], bv[j][0], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][1], bv[j][1], acc[i][j], 0, 0, 0);
+        if (sub != subs - 1) return;
+        // The group's sums into the outputs, as quant.cc:150-155 does:
+        // t = fma(sa sb, S, t); t = fma(-oa, ob, t).
+        const float *sa = reinterpret_cast<const float *>(base + 2 * kQStageA);
+        const float *oa = sa + kQRows;
+        const float *sb = oa + kQRows;
+        const float *ob = sb + kQRows;
+        const int32_t *qs = reinterpret_cast<const int32_t *>(ob + kQRows);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float cs = sb[brow[j]], nco = -ob[brow[j]];
+            const int32_t shift = 128 * qs[brow[j]];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4) {
+                    const int row = wr * 64 + 32 * i + 4 * h + 8 * e4;
+                    const float4v sa4 = *reinterpret_cast<const float4v *>(sa + row);
+                    const float4v oa4 = *reinterpret_cast<const float4v *>(oa + row);
+#pragma unroll
+                    for (int e1 = 0; e1 < 4; ++e1) {
+                        const int e = 4 * e4 + e1;
+                        const float ab = __fmul_rn(sa4[e1], cs);
+                        const float sum = static_cast<float>(acc[i][j][e] + shift);
+                        const float v = __builtin_fmaf(ab, sum, t[i][j][e]);
+                        t[i][j][e] = __builtin_fmaf(oa4[e1], nco, v);
+                    }
+                }
+        }
+    };
+
+    // The residual's loads done before any copy is in flight, so that the
+    // compiler need not wait for the copies to know t is there.
+    wait_loads<0>();
+#pragma unroll
+    for (int q = 0; q < S - 1; ++q) copy_step(q, q);
+    for (int64_t s = 0; s < steps; ++s) {
+        // This wave's copies of step s are in (those of the S - 2 steps after
+        // it may still be in flight), and every wave's, past the barrier --
+        // which also means every wave is done with the stage the next copies
+        // overwrite, read at step s - 1.
+        wait_loads<(S - 2) * kQCopies>();
+        barrier_only();
+        copy_step(s + S - 1, static_cast<int>((s + S - 1) % S));
+        compute(static_cast<int>(s % S), s % subs);
+    }
+    // No copy may still be landing in LDS when the workgroup ends.
+    wait_loads<0>();
+
+    // The chain, then the stores (or the gated GELU of the pair).
+    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
+    const auto row_off = [&](const DevStep &st, int64_t m) -> int64_t {
+        if (st.flat123) return m * st.nb[1];
+        uint32_t i1, i2, i3;
+        split_index(static_cast<uint32_t>(m), ne1, ne2, i1, i2, i3);
+        return i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const auto row = [&](int e) -> int64_t {
+            const int64_t m = out_row(i, e);
+            return m < p.M ? m : p.M - 1;
+        };
+        if (GATED) {
+            const int64_t f = n0 + 32 * wc + r32;
+            const int64_t fc = f < p.half ? f : p.half - 1;
+            apply_chain_block(p.chain, t[i][0], [&](int s, int e) {
+                return fc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+            });
+            apply_chain_block(p.chain, t[i][1], [&](int s, int e) {
+                return (p.half + fc) * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+            });
+            if (f >= p.half) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int64_t m = out_row(i, e);
+                if (m < p.M) p.y[m * p.ldy + f] = t[i][0][e] * gelu(t[i][1][e]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t n = out_col(j);
+                const int64_t nc = n < p.N ? n : p.N - 1;
+                apply_chain_block(p.chain, t[i][j], [&](int s, int e) {
+                    return nc * p.chain.steps[s].nb[0] + row_off(p.chain.steps[s], row(e));
+                });
+                if (n >= p.N) continue;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int64_t m = out_row(i, e);
+                    if (m < p.M) p.y[m * p.ldy + n] = t[i][j][e];
+                }
+            }
+        }
+    }
+}
+
+constexpr int kQStages = 8;
+static_assert(kQStages * kQStage <= 160 * 1024, "the ring fits the CU's LDS");
+static_assert((kQStages - 2) * kQCopies < 64, "vmcnt");
+
+template <bool GATED>
+hipError_t launch_qgemm2(QgemmArgs p, hipStream_t stream) {
+    const int64_t cols = GATED ? p.half : p.N;
+    p.col_blocks = ceil_div(cols, GATED ? kQRows / 2 : kQRows);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.M, kQRows) * p.col_blocks));
+    SDHIP_LAUNCH((qgemm3_kernel<GATED, kQStages>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ convolutions
@@ -591,13 +939,15 @@ hipError_t launch_qgemm_part(const Layout &l, int8_t *xq, float *xs, float *xo, 
                              int32_t *wsum, int64_t m0, int64_t rows, int64_t n0, int64_t cols, float *t, int64_t ldt,
                              int32_t from_redirect, hipStream_t stream) {
     QgemmArgs p{};
-    p.xq = xq + m0 * l.kp;
-    p.xs = xs + m0 * l.groups;
-    p.xo = xo + m0 * l.groups;
-    p.wq = wq + n0 * l.kp;
-    p.ws = ws + n0 * l.groups;
-    p.wo = wo + n0 * l.groups;
-    p.wsum = wsum + n0 * l.groups;
+    p.xq = xq + m0 * 64;
+    p.xs = xs + m0;
+    p.xo = xo + m0;
+    p.wq = wq + n0 * 64;
+    p.ws = ws + n0;
+    p.wo = wo + n0;
+    p.wsum = wsum + n0;
+    p.xrows = l.m;
+    p.wrows = l.n;
     p.y = t;
     p.ldy = ldt;
     p.M = rows;
@@ -608,10 +958,13 @@ hipError_t launch_qgemm_part(const Layout &l, int8_t *xq, float *xs, float *xo, 
     p.slot = l.slot;
     p.kp = l.kp;
     p.from_redirect = from_redirect;
-    p.col_blocks = ceil_div(cols, kQB);
-    const dim3 grid(static_cast<uint32_t>(ceil_div(rows, kQB) * p.col_blocks));
-    SDHIP_LAUNCH(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
-    return hipGetLastError();
+    if (tuning().qgemm_core == 1) {
+        p.col_blocks = ceil_div(cols, kQB);
+        const dim3 grid(static_cast<uint32_t>(ceil_div(rows, kQB) * p.col_blocks));
+        SDHIP_LAUNCH(qgemm_kernel<false>, grid, dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    return launch_qgemm2<false>(p, stream);
 }
 
 }  // namespace
@@ -785,8 +1138,15 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     int32_t *wsum = reinterpret_cast<int32_t *>(wbase + (l.wsum - l.wq));
     {
         KernelScope scope("quantize_inputs", stream);
-        SDHIP_LAUNCH(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream,
-                     RowsSrc{a.x, a.ldx}, a.M, a.K, q, l, xq, xs, xo);
+        const bool fast = q.group == 64 && l.slot == 64 && a.K % 64 == 0 && a.ldx % 4 == 0 &&
+                          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
+        if (fast) {
+            SDHIP_LAUNCH(quantize_inputs64_kernel, dim3(ceil_div(a.M * l.groups, 16)), dim3(256), 0, stream, a.x,
+                         a.ldx, a.M, l.groups, static_cast<float>(q.levels), xq, xs, xo);
+        } else {
+            SDHIP_LAUNCH(quantize_inputs_kernel<RowsSrc>, dim3(ceil_div(a.M * l.groups, 4)), dim3(256), 0, stream,
+                         RowsSrc{a.x, a.ldx}, a.M, a.K, q, l, xq, xs, xo);
+        }
     }
     if (!ready) {
         KernelScope scope("quantize_weights", stream);
@@ -819,12 +1179,18 @@ sdhip_status quantized_linear(const MulMatArgs &a, bool gated, void *work, hipSt
     p.groups = l.groups;
     p.slot = l.slot;
     p.kp = l.kp;
+    p.xrows = l.m;
+    p.wrows = l.n;
     p.from_redirect = a.from_redirect;
     p.chain = a.chain;
+    KernelScope scope(gated ? "qgemm_gated" : "qgemm", stream);
+    if (tuning().qgemm_core != 1) {
+        const hipError_t err = gated ? launch_qgemm2<true>(p, stream) : launch_qgemm2<false>(p, stream);
+        return launched(err, gated ? "quantized mul_mat_gated" : "quantized mul_mat");
+    }
     const int64_t cols = gated ? a.half : a.N;
     p.col_blocks = ceil_div(cols, gated ? kQB / 2 : kQB);
     const dim3 grid(static_cast<uint32_t>(ceil_div(a.M, kQB) * p.col_blocks));
-    KernelScope scope(gated ? "qgemm_gated" : "qgemm", stream);
     if (gated) {
         SDHIP_LAUNCH(qgemm_kernel<true>, grid, dim3(256), 0, stream, p);
     } else {

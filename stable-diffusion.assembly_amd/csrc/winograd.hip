@@ -1393,8 +1393,11 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         p.N = a.tiles;
         p.K = l.kp;
         p.batches = A * A;
-        const hipError_t err = tuning().gemm_core == 2 && split_batched2_takes(p)
+        const int core = tuning().gemm_core;
+        const hipError_t err = core == 2 && split_batched2_takes(p)
                                    ? launch_split_batched2(p, tuning().gemm_tiles, tuning().gemm_stages, stream)
+                               : core == 3 && split_batched2_takes(p)
+                                   ? launch_split_batched3(p, tuning().gemm_tiles, tuning().gemm_stages, stream)
                                    : launch_split_batched(p, gemm_shape(), stream);
         if (err != hipSuccess) return launched(err, "winograd products");
     }

@@ -345,3 +345,24 @@ def test_winograd_products_cores_agree(gpu, c, tiles):
     _, _, y2, _, _ = conv_case(gpu, c, seed=sum(c), tuning=f"gemm_core=2,gemm_tiles={tiles}")
     assert path in (2, 4)
     assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [(64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), (65, 33, 24, 20, 3, 3, 1, 1, 1, 1, 1, 1, 2),
+                               (96, 16, 32, 17, 3, 3, 1, 1, 1, 1, 1, 1, 1), (40, 40, 96, 160, 3, 3, 1, 1, 1, 1, 1, 1, 2)],
+                         ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("tuning", ["gemm_core=3", "gemm_core=3,gemm_tiles=55", "gemm_core=3,gemm_tiles=44",
+                                    "gemm_core=3,gemm_tiles=52", "gemm_core=3,gemm_tiles=42",
+                                    "gemm_core=3,gemm_tiles=22", "gemm_core=3,gemm_tiles=21",
+                                    "gemm_core=3,gemm_stages=4", "gemm_core=3,gemm_tiles=55,gemm_stages=4"])
+def test_winograd_products_without_lds(gpu, c, tuning):
+    """Winograd's products by wide wave tiles of the 16 x 16 x 32 MFMA
+    (gemm_core=3): each product's k summed in another order than the 32 x 32
+    cores', so held to the bound against float64 rather than to their bits;
+    ragged rows (OC, tiles) at every wave shape and both ring depths."""
+    x, k32, y, path, p = conv_case(gpu, c, seed=sum(c), tuning=tuning)
+    assert path in (2, 4)
+    exact, mag = orc.exact_conv2d(x, k32, *p)
+    err = orc.metric(y.cpu().numpy(), exact, mag)
+    print(f"conv {c} path {path} [{tuning}]: {err:.3g}")
+    assert err <= BOUND

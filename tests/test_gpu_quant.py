@@ -213,3 +213,41 @@ def test_quantized_single_precision_weights(gpu, K, N, M, tuning):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     exact, mag = orc.exact_mul_mat(w, x)
     assert orc.metric(got, exact + b, mag + np.abs(b)) <= bound(levels, wmax)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,N,M,B", [(320, 320, 512, 2), (77, 100, 300, 1), (300, 17, 131, 3), (1280, 1280, 988, 2),
+                                     (5120, 1280, 300, 1)])
+@pytest.mark.parametrize("tuning", ["bits=8", "bits=8,weight_group=0", "bits=8,group=128", "bits=8,group=32",
+                                    "bits=7,input_bits=7"])
+def test_quantized_cores_agree(gpu, K, N, M, B, tuning):
+    """The products by 128 x 128 blocks through a ring of LDS stages
+    (qgemm_core=2) give the bits of the 64 x 64 kernel: the integer sums are
+    exact whatever the order of k, and the dequantisation is the same
+    sequence of operations."""
+    w32, x, b, y1 = run_quantized(gpu, K, N, M, B, tuning, seed=K + N)
+    _, _, _, y2 = run_quantized(gpu, K, N, M, B, tuning + ",qgemm_core=2", seed=K + N)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,half,M", [(320, 1280, 400), (96, 2000, 300), (1280, 5120, 300)])
+def test_quantized_gated_cores_agree(gpu, K, half, M):
+    """The gated GELU after the quantized products, both kernels, bit for bit."""
+    r = rng(K + half)
+    wh, _ = weights_f16(r, (2 * half, K))
+    x = uniform(r, (M, K), 1.0)
+    b = uniform(r, (2 * half,), 1.0)
+    w_d, x_d, b_d = dev(wh, gpu), dev(x, gpu), dev(b, gpu)
+    outs = []
+    for core in (1, 2):
+        y = unwritten((M, 2 * half), gpu)
+        out = unwritten((M, half), gpu)
+        sdhip.set_tuning(f"bits=8,qgemm_core={core}")
+        try:
+            sdhip.mul_mat_gated(w_d, x_d, y, out, sdhip.epilogue([("add", b_d)]))
+            torch.cuda.synchronize()
+        finally:
+            sdhip.set_tuning("")
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))

@@ -73,7 +73,7 @@ def test_tuning_takes_every_reference_name_and_checks_its_own():
     try:
         sdhip.set_tuning("conv_kc=128,amx_fp16=0,fuse_residual=0,todo=2,todo_tokens=100,group=1000,bits=3")
         assert sdhip.get_tuning("conv_kc") == 128 and sdhip.get_tuning("todo_tokens") == 100
-        for bad in ("gemm_stages=3", "gemm_tiles=13", "gemm_core=3", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
+        for bad in ("gemm_stages=3", "gemm_tiles=13", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
                     "winograd_splits=-2", "fuse=99999999999"):
             with pytest.raises(sdhip.SdhipError):
                 sdhip.set_tuning(bad)
