@@ -229,6 +229,11 @@ __device__ __forceinline__ void copy_lds(const void *src, char *lds) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
 
+// The same with 4 bytes a lane: a copy of 256 bytes.
+__device__ __forceinline__ void copy_lds4(const void *src, char *lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
+}
+
 // ------------------------------------------------------------------ grid
 
 // The 8 XCDs of an MI355X each take every 8th workgroup of a launch, and each

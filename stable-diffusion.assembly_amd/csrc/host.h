@@ -57,7 +57,7 @@ struct Tuning {
     // registers (1) or by the one whose copies into LDS global_load_lds
     // makes (2), for comparison: the same bits, measured no faster.
     int gemm_core = 1;
-    int qgemm_core = 1;
+    int qgemm_core = 2;
     // This library's own: attention by its generic form (1) even where the
     // fast one takes the operands (0), for comparison; results agree within
     // the same bound.

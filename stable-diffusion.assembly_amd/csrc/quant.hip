@@ -478,21 +478,23 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
     }
 }
 
-// The same products by wider tiles (64 x 64 a wave) on v_mfma_i32_32x32x32_i8,
-// fed by a deep ring of LDS stages.
+// The same products by wider tiles on v_mfma_i32_32x32x32_i8, fed by a ring
+// of LDS stages.
 //
 // Per group a wave's MFMAs are few and its dequantisation long -- five VALU
-// operations an output, the reference's fma order fixed by bit-exactness --
-// and a K-step (one 64-byte step of a group's slot) is a few hundred cycles,
-// well under the memory's latency: the loads of a step are issued S - 1
-// steps ahead, each straight into LDS by global_load_lds (no register
-// staging, so that S can be 8), with the wave's own wait for its copies and
-// a bare s_barrier the only synchronisation.
+// operations an output (the sums kept in VGPRs, no AGPR reads), the
+// reference's fma order fixed by bit-exactness -- so the VALU bounds the
+// kernel, and what matters is that every SIMD has work and that a wave's
+// VALU overlaps another's MFMAs and loads: two workgroups a CU (at most 256
+// registers a lane, 4 stages of LDS a workgroup).  The loads of a step are
+// issued S - 1 steps ahead, straight into LDS by global_load_lds (no
+// register staging), with the wave's own wait for its copies and a bare
+// s_barrier the only synchronisation.
 //
-// A workgroup of 4 waves (2 x 2) covers 128 rows of x (tokens) by 128 rows
+// A workgroup of 4 waves (2 x 2) covers 64 TM rows of x (tokens) by 128 rows
 // of W (features; GATED: 64 features and their 64 gates, each wave's two
-// column tiles a pair).  A stage holds the step's 128 rows of bytes of each
-// operand (the layouts are step-major, so each is 8 KB in a row), the row
+// column tiles a pair).  A stage holds the step's rows of bytes of each
+// operand (the layouts are step-major, so each is contiguous), the row
 // scales and offsets of its group and the column scales, offsets and sums.
 // The 16-byte piece p of a row r lands at p ^ s(r), s(r) = ((r >> 1) ^
 // (r >> 2)) & 3 (the copies pick which global piece each lane brings), so
@@ -500,20 +502,34 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
 // a wave takes 32 bytes of its row at byte 32 (l / 32) of the step's 64, the
 // first 16 to the first MFMA and the rest to the second: A and B take the
 // same order of k, and integer sums do not depend on it.
-constexpr int kQRows = 128;                      // rows of each operand a block
-constexpr int kQStageA = kQRows * 64;            // bytes of a step's rows
-constexpr int kQScales = kQRows * 4;             // bytes of one row of scales
-constexpr int kQStage = 2 * kQStageA + 5 * kQScales;  // A, B, sa, oa, sb, ob, qs
-constexpr int kQUnits16 = 2 * kQStageA / 1024;   // 1 KB copies (16 bytes a lane)
-constexpr int kQUnits4 = 5 * kQScales / 256;     // 256-byte copies (4 bytes a lane)
-constexpr int kQCopies = kQUnits16 / 4 + (kQUnits4 + 3) / 4;  // a wave's copies a step
+constexpr int kQWRows = 128;  // rows of W a workgroup
+
+template <int TM>
+struct QStage {
+    static constexpr int kXRows = 64 * TM;
+    static constexpr int kA = kXRows * 64;       // bytes of x a step
+    static constexpr int kB = kQWRows * 64;      // bytes of W a step
+    static constexpr int kSa = kA + kB;          // offsets of the scales
+    static constexpr int kOa = kSa + kXRows * 4;
+    static constexpr int kSb = kOa + kXRows * 4;
+    static constexpr int kOb = kSb + kQWRows * 4;
+    static constexpr int kQs = kOb + kQWRows * 4;
+    static constexpr int kBytes = kQs + kQWRows * 4;
+    static constexpr int kUnits16 = (kA + kB) / 1024;                 // 1 KB copies
+    static constexpr int kUnits4 = (2 * kXRows + 3 * kQWRows) / 64;    // 256-byte copies
+    static constexpr int kC16 = kUnits16 / 4;                         // a wave's, a step
+    static constexpr int kC4 = (kUnits4 + 3) / 4;
+    static constexpr int kCopies = kC16 + kC4;
+    static_assert(kUnits16 % 4 == 0, "1 KB copies shared evenly");
+};
 
 __device__ __forceinline__ int qswizzle(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
-template <bool GATED, int S>
+template <bool GATED, int TM, int S>
 __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
-    static_assert(kQUnits16 % 4 == 0, "1 KB copies shared evenly");
-    __shared__ __attribute__((aligned(1024))) char lds[S * kQStage];
+    using L = QStage<TM>;
+    constexpr int BM = L::kXRows;
+    __shared__ __attribute__((aligned(1024))) char lds[S * L::kBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -524,8 +540,8 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
     const int64_t mb = b / p.col_blocks;
     const int64_t nb = b % p.col_blocks;
-    const int64_t m0 = mb * kQRows;
-    const int64_t n0 = nb * (GATED ? kQRows / 2 : kQRows);
+    const int64_t m0 = mb * BM;
+    const int64_t n0 = nb * (GATED ? kQWRows / 2 : kQWRows);
     // The W row of block row r (clamped): GATED, rows 0..63 features n0 +
     // r and rows 64..127 their gates.
     const auto w_row = [&](int r) -> int64_t {
@@ -537,73 +553,90 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     };
     const auto x_row = [&](int r) -> int64_t { return m0 + r < p.M ? m0 + r : p.M - 1; };
 
-    // This wave's copies a step: 1 KB units wave + 4 q (A's rows for units
-    // 0..7, B's for 8..15, 16 rows each), then 256-byte units 16 + wave +
-    // 4 q of the scales (sa, oa, sb, ob, qs: two units each); waves past the
-    // last unit repeat it.  Per copy: the lane's source at step 0, its
-    // stride a step (bytes of the row layout) or a group (scales), and the
-    // stage offset of the unit.
-    constexpr int C16 = kQUnits16 / 4, C4 = (kQUnits4 + 3) / 4;
+    // This wave's copies a step: 1 KB units wave + 4 q (x's rows first, 16
+    // rows a unit, then W's), then 256-byte units wave + 4 q of the scales
+    // (sa, oa: TM units each, sb, ob, qs: two each, 64 rows a unit); waves
+    // past the last unit repeat it.  Per copy: the lane's source, advanced a
+    // step (bytes) or a group (scales) at a time, and the unit's place in a
+    // stage.
+    constexpr int C16 = L::kC16, C4 = L::kC4;
     const int8_t *src16[C16];
     int dst16[C16];
+    bool x16[C16];
 #pragma unroll
     for (int q = 0; q < C16; ++q) {
         const int u = wave + 4 * q;
-        const int op = u / (kQUnits16 / 2);  // 0: A, 1: B
-        const int row = 16 * (u % (kQUnits16 / 2)) + (lane >> 2);
+        const bool isx = u < L::kA / 1024;
+        const int ub = isx ? u : u - L::kA / 1024;
+        const int row = 16 * ub + (lane >> 2);
         const int piece = (lane & 3) ^ qswizzle(row);
-        src16[q] = op == 0 ? p.xq + x_row(row) * 64 + 16 * piece : p.wq + w_row(row) * 64 + 16 * piece;
-        dst16[q] = op * kQStageA + 16 * (u % (kQUnits16 / 2)) * 64;
+        x16[q] = isx;
+        src16[q] = isx ? p.xq + x_row(row) * 64 + 16 * piece : p.wq + w_row(row) * 64 + 16 * piece;
+        dst16[q] = (isx ? 0 : L::kA) + 16 * ub * 64;
     }
     const char *src4[C4];
-    int dst4[C4], kind4[C4];
+    int dst4[C4];
+    bool x4[C4];
 #pragma unroll
     for (int q = 0; q < C4; ++q) {
         int u = wave + 4 * q;
-        u = u < kQUnits4 ? u : kQUnits4 - 1;
-        const int which = u / 2;  // sa, oa, sb, ob, qs
-        const int row = 64 * (u % 2) + lane;
-        kind4[q] = which;
-        const char *base = which == 0   ? reinterpret_cast<const char *>(p.xs + x_row(row))
-                           : which == 1 ? reinterpret_cast<const char *>(p.xo + x_row(row))
-                           : which == 2 ? reinterpret_cast<const char *>(p.ws + w_row(row))
-                           : which == 3 ? reinterpret_cast<const char *>(p.wo + w_row(row))
-                                        : reinterpret_cast<const char *>(p.wsum + w_row(row));
-        src4[q] = base;
-        dst4[q] = 2 * kQStageA + which * kQScales + 256 * (u % 2);
-    }
-    const int64_t subs = p.slot / 64;
-    const int64_t steps = p.groups * subs;
-    const int64_t last = steps - 1;
-    const auto copy_step = [&](int64_t s, int stage) {
-        const int64_t k = s < last ? s : last;
-        const int64_t g = k / subs;
-        char *base = lds + stage * kQStage;
-#pragma unroll
-        for (int q = 0; q < C16; ++q) {
-            const int64_t stride = (wave + 4 * q) < kQUnits16 / 2 ? p.xrows * 64 : p.wrows * 64;
-            __builtin_amdgcn_global_load_lds(src16[q] + k * stride, (__attribute__((address_space(3))) void *)(base + dst16[q]),
-                                             16, 0, 0);
+        u = u < L::kUnits4 ? u : L::kUnits4 - 1;
+        // Units [0, TM): sa; [TM, 2 TM): oa; then sb, ob, qs two each.
+        const char *base;
+        int off;
+        if (u < 2 * TM) {
+            const int v = u % TM, row = 64 * v + lane;
+            base = reinterpret_cast<const char *>((u < TM ? p.xs : p.xo) + x_row(row));
+            off = (u < TM ? L::kSa : L::kOa) + 256 * v;
+            x4[q] = true;
+        } else {
+            const int w = (u - 2 * TM) / 2, v = (u - 2 * TM) % 2, row = 64 * v + lane;
+            base = w == 0   ? reinterpret_cast<const char *>(p.ws + w_row(row))
+                   : w == 1 ? reinterpret_cast<const char *>(p.wo + w_row(row))
+                            : reinterpret_cast<const char *>(p.wsum + w_row(row));
+            off = (w == 0 ? L::kSb : w == 1 ? L::kOb : L::kQs) + 256 * v;
+            x4[q] = false;
         }
+        src4[q] = base;
+        dst4[q] = off;
+    }
+    const int subs = static_cast<int>(p.slot / 64);
+    const int steps = static_cast<int>(p.groups) * subs;
+    // The copies' sources advance a step at a time (the bytes) or a group at
+    // a time (the scales), and stop at the last step, which the copies past
+    // it repeat; counters, not divisions, track the step and group.
+    const int64_t xstep = p.xrows * 64, wstep = p.wrows * 64;
+    const int64_t xgroup = p.xrows * 4, wgroup = p.wrows * 4;
+    int copied = 0, copy_sub = 0;  // the step the next copies bring, and its place in its group
+    const auto copy_step = [&](int stage) {
+        char *base = lds + stage * L::kBytes;
 #pragma unroll
-        for (int q = 0; q < C4; ++q) {
-            const int64_t stride = kind4[q] < 2 ? p.xrows * 4 : p.wrows * 4;
-            __builtin_amdgcn_global_load_lds(src4[q] + g * stride, (__attribute__((address_space(3))) void *)(base + dst4[q]),
-                                             4, 0, 0);
+        for (int q = 0; q < C16; ++q) copy_lds(src16[q], base + dst16[q]);
+#pragma unroll
+        for (int q = 0; q < C4; ++q) copy_lds4(src4[q], base + dst4[q]);
+        if (copied + 1 < steps) {
+            ++copied;
+#pragma unroll
+            for (int q = 0; q < C16; ++q) src16[q] += x16[q] ? xstep : wstep;
+            if (++copy_sub == subs) {
+                copy_sub = 0;
+#pragma unroll
+                for (int q = 0; q < C4; ++q) src4[q] += x4[q] ? xgroup : wgroup;
+            }
         }
     };
 
     // The outputs: tile (i, j) of the wave, lane column r32, rows
     // 8 (e / 4) + 4 h + e % 4.
-    float t[2][2][16];
-    const auto out_row = [&](int i, int e) -> int64_t { return m0 + wr * 64 + 32 * i + 4 * h + tile_row(e); };
+    float t[TM][2][16];
+    const auto out_row = [&](int i, int e) -> int64_t { return m0 + wr * 32 * TM + 32 * i + 4 * h + tile_row(e); };
     const auto out_col = [&](int j) -> int64_t { return n0 + 64 * wc + 32 * j + r32; };
     if (!GATED && p.from_redirect) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int64_t n = out_col(j);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int64_t m = out_row(i, e);
@@ -612,20 +645,20 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) t[i][j][e] = 0.0f;
     }
 
-    // Fragment reads: A tile i at block row wr 64 + 32 i + r32, B tile j at
-    // block row (GATED: j 64 + wc 32 + r32; else wc 64 + 32 j + r32), the two
-    // 16-byte pieces 2 h and 2 h + 1 at their swizzled places.
-    int aread[2][2], bread[2][2], brow[2];
+    // Fragment reads: A tile i at block row wr 32 TM + 32 i + r32, B tile j
+    // at block row (GATED: j 64 + wc 32 + r32; else wc 64 + 32 j + r32), the
+    // two 16-byte pieces 2 h and 2 h + 1 at their swizzled places.
+    int aread[TM][2], bread[2][2], brow[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = wr * 64 + 32 * i + r32;
+    for (int i = 0; i < TM; ++i) {
+        const int row = wr * 32 * TM + 32 * i + r32;
 #pragma unroll
         for (int q = 0; q < 2; ++q) aread[i][q] = row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
     }
@@ -634,15 +667,15 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
         const int row = GATED ? 64 * j + 32 * wc + r32 : 64 * wc + 32 * j + r32;
         brow[j] = row;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) bread[j][q] = kQStageA + row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
+        for (int q = 0; q < 2; ++q) bread[j][q] = L::kA + row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
     }
 
-    int16v acc[2][2];
-    const auto compute = [&](int stage, int64_t sub) {
-        const char *base = lds + stage * kQStage;
-        int4v a[2][2], bv[2][2];
+    int16v acc[TM][2];
+    const auto compute = [&](int stage, int sub) {
+        const char *base = lds + stage * L::kBytes;
+        int4v a[TM][2], bv[2][2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int q = 0; q < 2; ++q) a[i][q] = *reinterpret_cast<const int4v *>(base + aread[i][q]);
 #pragma unroll
@@ -653,39 +686,39 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
         // over the workgroup).
         if (sub == 0) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][0], bv[j][0], int16v{}, 0, 0, 0);
         } else {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][0], bv[j][0], acc[i][j], 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][1], bv[j][1], acc[i][j], 0, 0, 0);
         if (sub != subs - 1) return;
         // The group's sums into the outputs, as quant.cc:150-155 does:
         // t = fma(sa sb, S, t); t = fma(-oa, ob, t).
-        const float *sa = reinterpret_cast<const float *>(base + 2 * kQStageA);
-        const float *oa = sa + kQRows;
-        const float *sb = oa + kQRows;
-        const float *ob = sb + kQRows;
-        const int32_t *qs = reinterpret_cast<const int32_t *>(ob + kQRows);
+        const float *sa = reinterpret_cast<const float *>(base + L::kSa);
+        const float *oa = reinterpret_cast<const float *>(base + L::kOa);
+        const float *sb = reinterpret_cast<const float *>(base + L::kSb);
+        const float *ob = reinterpret_cast<const float *>(base + L::kOb);
+        const int32_t *qs = reinterpret_cast<const int32_t *>(base + L::kQs);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const float cs = sb[brow[j]], nco = -ob[brow[j]];
             const int32_t shift = 128 * qs[brow[j]];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int e4 = 0; e4 < 4; ++e4) {
-                    const int row = wr * 64 + 32 * i + 4 * h + 8 * e4;
+                    const int row = wr * 32 * TM + 32 * i + 4 * h + 8 * e4;
                     const float4v sa4 = *reinterpret_cast<const float4v *>(sa + row);
                     const float4v oa4 = *reinterpret_cast<const float4v *>(oa + row);
 #pragma unroll
@@ -703,17 +736,21 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     // The residual's loads done before any copy is in flight, so that the
     // compiler need not wait for the copies to know t is there.
     wait_loads<0>();
+    static_assert((S & (S - 1)) == 0, "stages a power of two");
+    constexpr int kBehind = (S - 2) * QStage<TM>::kCopies;  // a wave's copies behind a step's
 #pragma unroll
-    for (int q = 0; q < S - 1; ++q) copy_step(q, q);
-    for (int64_t s = 0; s < steps; ++s) {
+    for (int q = 0; q < S - 1; ++q) copy_step(q);
+    int sub = 0;
+    for (int s = 0; s < steps; ++s) {
         // This wave's copies of step s are in (those of the S - 2 steps after
         // it may still be in flight), and every wave's, past the barrier --
         // which also means every wave is done with the stage the next copies
         // overwrite, read at step s - 1.
-        wait_loads<(S - 2) * kQCopies>();
+        wait_loads<kBehind>();
         barrier_only();
-        copy_step(s + S - 1, static_cast<int>((s + S - 1) % S));
-        compute(static_cast<int>(s % S), s % subs);
+        copy_step((s + S - 1) & (S - 1));
+        compute(s & (S - 1), sub);
+        sub = sub + 1 == subs ? 0 : sub + 1;
     }
     // No copy may still be landing in LDS when the workgroup ends.
     wait_loads<0>();
@@ -727,7 +764,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
         return i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
     };
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TM; ++i) {
         const auto row = [&](int e) -> int64_t {
             const int64_t m = out_row(i, e);
             return m < p.M ? m : p.M - 1;
@@ -766,16 +803,24 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     }
 }
 
-constexpr int kQStages = 8;
-static_assert(kQStages * kQStage <= 160 * 1024, "the ring fits the CU's LDS");
-static_assert((kQStages - 2) * kQCopies < 64, "vmcnt");
+constexpr int kQStages = 4;
+static_assert(2 * kQStages * QStage<2>::kBytes <= 160 * 1024, "two workgroups' rings fit a CU's LDS");
+static_assert((kQStages - 2) * QStage<2>::kCopies < 64, "vmcnt");
 
+// Workgroups of 128 rows of x where the launch still gives every SIMD two
+// waves, else 64.
 template <bool GATED>
 hipError_t launch_qgemm2(QgemmArgs p, hipStream_t stream) {
     const int64_t cols = GATED ? p.half : p.N;
-    p.col_blocks = ceil_div(cols, GATED ? kQRows / 2 : kQRows);
-    const dim3 grid(static_cast<uint32_t>(ceil_div(p.M, kQRows) * p.col_blocks));
-    SDHIP_LAUNCH((qgemm3_kernel<GATED, kQStages>), grid, dim3(256), 0, stream, p);
+    p.col_blocks = ceil_div(cols, GATED ? kQWRows / 2 : kQWRows);
+    const int64_t blocks128 = ceil_div(p.M, 128) * p.col_blocks;
+    if (blocks128 >= 512) {
+        SDHIP_LAUNCH((qgemm3_kernel<GATED, 2, kQStages>), dim3(static_cast<uint32_t>(blocks128)), dim3(256), 0,
+                     stream, p);
+    } else {
+        const dim3 grid(static_cast<uint32_t>(ceil_div(p.M, 64) * p.col_blocks));
+        SDHIP_LAUNCH((qgemm3_kernel<GATED, 1, kQStages>), grid, dim3(256), 0, stream, p);
+    }
     return hipGetLastError();
 }
 

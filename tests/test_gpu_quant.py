@@ -221,11 +221,11 @@ def test_quantized_single_precision_weights(gpu, K, N, M, tuning):
 @pytest.mark.parametrize("tuning", ["bits=8", "bits=8,weight_group=0", "bits=8,group=128", "bits=8,group=32",
                                     "bits=7,input_bits=7"])
 def test_quantized_cores_agree(gpu, K, N, M, B, tuning):
-    """The products by 128 x 128 blocks through a ring of LDS stages
-    (qgemm_core=2) give the bits of the 64 x 64 kernel: the integer sums are
+    """The products through a ring of LDS stages (qgemm_core=2, the default)
+    give the bits of the 64 x 64 kernel (qgemm_core=1): the integer sums are
     exact whatever the order of k, and the dequantisation is the same
     sequence of operations."""
-    w32, x, b, y1 = run_quantized(gpu, K, N, M, B, tuning, seed=K + N)
+    w32, x, b, y1 = run_quantized(gpu, K, N, M, B, tuning + ",qgemm_core=1", seed=K + N)
     _, _, _, y2 = run_quantized(gpu, K, N, M, B, tuning + ",qgemm_core=2", seed=K + N)
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
