@@ -131,11 +131,11 @@ bool in_range(Range r, long v, const char *&takes) {
         takes = "2 or 4";
         return v == 2 || v == 4;
     case kTiles:
-        takes = "0, 11, 12, 21, 22 (the LDS cores' blocks) or 42, 44, 52, 55 (gemm_core=3's wave tiles)";
-        return v == 0 || v == 11 || v == 12 || v == 21 || v == 22 || v == 42 || v == 44 || v == 52 || v == 55;
+        takes = "0, 11, 12, 21, 22 or 41 (gemm_core=3)";
+        return v == 0 || v == 11 || v == 12 || v == 21 || v == 22 || v == 41;
     case kCore:
-        takes = "1, 2 or 3";
-        return v == 1 || v == 2 || v == 3;
+        takes = "0, 1, 2 or 3";
+        return v >= 0 && v <= 3;
     case kFlag2:
         takes = "1 or 2";
         return v == 1 || v == 2;

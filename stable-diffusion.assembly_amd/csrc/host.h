@@ -56,7 +56,7 @@ struct Tuning {
     // This library's own: Winograd's products by the core staged through
     // registers (1) or by the one whose copies into LDS global_load_lds
     // makes (2), for comparison: the same bits, measured no faster.
-    int gemm_core = 1;
+    int gemm_core = 0;
     int qgemm_core = 2;
     // This library's own: attention by its generic form (1) even where the
     // fast one takes the operands (0), for comparison; results agree within

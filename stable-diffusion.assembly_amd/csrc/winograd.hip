@@ -1393,11 +1393,22 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         p.N = a.tiles;
         p.K = l.kp;
         p.batches = A * A;
-        const int core = tuning().gemm_core;
+        // gemm_core 0 (the default) chooses by the shape: the core whose
+        // waves load their own rows of B (gemm_core=3, four stages ahead)
+        // for grids of up to twelve workgroups a CU, where it was measured
+        // faster (the UNet's and the VAE's 64x64 .. 128x128 maps), the
+        // register-staged one (1) for larger.
+        int core = tuning().gemm_core;
+        int stages = tuning().gemm_stages;
+        if (core == 0) {
+            const int64_t blocks3 = p.batches * ceil_div(p.M, 64) * ceil_div(p.N, 128);
+            core = split_batched2_takes(p) && blocks3 <= 12 * 256 ? 3 : 1;
+            if (core == 3) stages = 4;
+        }
         const hipError_t err = core == 2 && split_batched2_takes(p)
-                                   ? launch_split_batched2(p, tuning().gemm_tiles, tuning().gemm_stages, stream)
+                                   ? launch_split_batched2(p, tuning().gemm_tiles, stages, stream)
                                : core == 3 && split_batched2_takes(p)
-                                   ? launch_split_batched3(p, tuning().gemm_tiles, tuning().gemm_stages, stream)
+                                   ? launch_split_batched3(p, tuning().gemm_tiles, stages, stream)
                                    : launch_split_batched(p, gemm_shape(), stream);
         if (err != hipSuccess) return launched(err, "winograd products");
     }

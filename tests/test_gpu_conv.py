@@ -336,13 +336,16 @@ def test_conv2d_strided_input(gpu, c, want_path, small_path):
 @pytest.mark.gpu
 @pytest.mark.parametrize("c", [(64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), (65, 33, 24, 20, 3, 3, 1, 1, 1, 1, 1, 1, 2),
                                (96, 16, 32, 17, 3, 3, 1, 1, 1, 1, 1, 1, 1)], ids=lambda c: "x".join(map(str, c)))
-@pytest.mark.parametrize("tiles", [0, 11, 12, 21, 22])
-def test_winograd_products_cores_agree(gpu, c, tiles):
+@pytest.mark.parametrize("core,tiles", [(2, 0), (2, 11), (2, 12), (2, 21), (2, 22), (3, 0), (3, 22), (3, 41), (3, 12),
+                                        (0, 0)])
+def test_winograd_products_cores_agree(gpu, c, core, tiles):
     """Winograd's products by the core whose copies into LDS global_load_lds
-    makes (gemm_core=2) give the bits of the register-staged core, at every
-    block shape."""
+    makes (gemm_core=2), by the one whose waves load their own transformed
+    inputs (3) and by the default choice (0) give the bits of the
+    register-staged core, at every block shape: the same MFMAs in the same
+    order of k."""
     _, _, y1, path, _ = conv_case(gpu, c, seed=sum(c), tuning="gemm_core=1")
-    _, _, y2, _, _ = conv_case(gpu, c, seed=sum(c), tuning=f"gemm_core=2,gemm_tiles={tiles}")
+    _, _, y2, _, _ = conv_case(gpu, c, seed=sum(c), tuning=f"gemm_core={core},gemm_tiles={tiles}")
     assert path in (2, 4)
     assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
 
@@ -351,15 +354,14 @@ def test_winograd_products_cores_agree(gpu, c, tiles):
 @pytest.mark.parametrize("c", [(64, 64, 64, 48, 3, 3, 1, 1, 1, 1, 1, 1, 2), (65, 33, 24, 20, 3, 3, 1, 1, 1, 1, 1, 1, 2),
                                (96, 16, 32, 17, 3, 3, 1, 1, 1, 1, 1, 1, 1), (40, 40, 96, 160, 3, 3, 1, 1, 1, 1, 1, 1, 2)],
                          ids=lambda c: "x".join(map(str, c)))
-@pytest.mark.parametrize("tuning", ["gemm_core=3", "gemm_core=3,gemm_tiles=55", "gemm_core=3,gemm_tiles=44",
-                                    "gemm_core=3,gemm_tiles=52", "gemm_core=3,gemm_tiles=42",
-                                    "gemm_core=3,gemm_tiles=22", "gemm_core=3,gemm_tiles=21",
-                                    "gemm_core=3,gemm_stages=4", "gemm_core=3,gemm_tiles=55,gemm_stages=4"])
+@pytest.mark.parametrize("tuning", ["gemm_core=3", "gemm_core=3,gemm_tiles=22", "gemm_core=3,gemm_tiles=41",
+                                    "gemm_core=3,gemm_tiles=12", "gemm_core=3,gemm_stages=4",
+                                    "gemm_core=3,gemm_tiles=22,gemm_stages=4"])
 def test_winograd_products_without_lds(gpu, c, tuning):
-    """Winograd's products by wide wave tiles of the 16 x 16 x 32 MFMA
-    (gemm_core=3): each product's k summed in another order than the 32 x 32
-    cores', so held to the bound against float64 rather than to their bits;
-    ragged rows (OC, tiles) at every wave shape and both ring depths."""
+    """Winograd's products with the transformed weights shared through LDS
+    and each wave's transformed inputs loaded straight into its registers
+    (gemm_core=3): held to the bound against float64, with ragged rows (OC,
+    tiles) at every block shape and both prefetch depths."""
     x, k32, y, path, p = conv_case(gpu, c, seed=sum(c), tuning=tuning)
     assert path in (2, 4)
     exact, mag = orc.exact_conv2d(x, k32, *p)
