@@ -702,19 +702,13 @@ __device__ __forceinline__ int key_of_column(int c) {
     return (c & ~15) + 8 * (s >> 2) + 4 * g + (s & 3);
 }
 
-// The tiles of the keys and values of every (image, head of the keys), one
-// workgroup a tile: grid (tiles, b hk).
+// The keys of tile kt of (image bi, key head kh) split into their two parts,
+// [KB][kLdk] twice, into `rec` (the work buffer's record or an LDS buffer),
+// by the workgroup's threads: a thread a key's four dimensions, float4 loads.
 template <int D, int KB>
-__global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _Float16 *__restrict__ tiles) {
+__device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, int64_t kh, int64_t kt, _Float16 *rec) {
     using S = Split<D, KB>;
-    const int64_t kt = blockIdx.x;
-    const int64_t bh = blockIdx.y;
-    const int64_t bi = bh / a.hk, kh = bh - bi * a.hk;
-    const int64_t nk = gridDim.x;
-    _Float16 *rec = tiles + (bh * nk + kt) * (S::kRecord / 2);
     const float *kg = static_cast<const float *>(a.k) + bi * a.knb3 + kh * a.knb2;
-    const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
-    // The keys: a thread a key's four dimensions, float4 loads.
     for (int idx = threadIdx.x; idx < KB * (S::kLdk / 4); idx += 256) {
         const int j = idx / (S::kLdk / 4);
         const int c4 = idx - j * (S::kLdk / 4);
@@ -732,6 +726,46 @@ __global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _
         *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = h;
         *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
     }
+}
+
+// The values of tile kt split and transposed, [kDvp][kLdv] twice after the
+// keys' planes of `rec`, a thread four columns (four keys, in the order of
+// key_of_column) of a dimension; `vt(j, dim)` gives value dim of key j of the
+// tile (zero past lk).
+template <int D, int KB, class V>
+__device__ __forceinline__ void split_values(V vt, _Float16 *rec) {
+    using S = Split<D, KB>;
+    _Float16 *vh = rec + 2 * S::kPlaneK;
+    for (int idx = threadIdx.x; idx < S::kDvp * (S::kLdv / 4); idx += 256) {
+        const int dim = idx / (S::kLdv / 4);
+        const int c4 = idx - dim * (S::kLdv / 4);
+        half4a h, l;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = 4 * c4 + u;
+            const float x = c < KB && dim < D ? vt(key_of_column(c), dim) : 0.0f;
+            _Float16 hh, ll;
+            split_part(x * kSplitDown, hh, ll);
+            h[u] = hh;
+            l[u] = ll;
+        }
+        *reinterpret_cast<half4a *>(vh + dim * S::kLdv + 4 * c4) = h;
+        *reinterpret_cast<half4a *>(vh + S::kPlaneV + dim * S::kLdv + 4 * c4) = l;
+    }
+}
+
+// The tiles of the keys and values of every (image, head of the keys), one
+// workgroup a tile: grid (tiles, b hk).
+template <int D, int KB>
+__global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _Float16 *__restrict__ tiles) {
+    using S = Split<D, KB>;
+    const int64_t kt = blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    const int64_t bi = bh / a.hk, kh = bh - bi * a.hk;
+    const int64_t nk = gridDim.x;
+    _Float16 *rec = tiles + (bh * nk + kt) * (S::kRecord / 2);
+    const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
+    split_keys<D, KB>(a, bi, kh, kt, rec);
     // The values, transposed through LDS: rows read as float4, then a thread
     // four columns (four consecutive keys) of a dimension, consecutive threads
     // consecutive columns.
@@ -745,23 +779,7 @@ __global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _
         *reinterpret_cast<float4v *>(&vt[j][4 * c4]) = x;
     }
     __syncthreads();
-    _Float16 *vh = rec + 2 * S::kPlaneK;
-    for (int idx = threadIdx.x; idx < S::kDvp * (S::kLdv / 4); idx += 256) {
-        const int dim = idx / (S::kLdv / 4);
-        const int c4 = idx - dim * (S::kLdv / 4);
-        half4a h, l;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int c = 4 * c4 + u;
-            const float x = c < KB && dim < D ? vt[key_of_column(c)][dim] : 0.0f;
-            _Float16 hh, ll;
-            split_part(x * kSplitDown, hh, ll);
-            h[u] = hh;
-            l[u] = ll;
-        }
-        *reinterpret_cast<half4a *>(vh + dim * S::kLdv + 4 * c4) = h;
-        *reinterpret_cast<half4a *>(vh + S::kPlaneV + dim * S::kLdv + 4 * c4) = l;
-    }
+    split_values<D, KB>([&](int j, int dim) { return vt[j][dim]; }, rec);
 }
 
 // The online softmax of the wave's scores over KB keys, in base 2: the
@@ -821,10 +839,12 @@ __device__ __forceinline__ void split_softmax(const float16v (&sh)[KT], const fl
     l += part;
 }
 
-template <int D, int KB, int NS, int OCC, bool PIPE>
+template <int D, int KB, int NS, int OCC, bool PIPE, bool LOCAL>
 __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs a, const char *__restrict__ tiles) {
     using S = Split<D, KB>;
     static_assert(NS >= 3 && (NS - 2) * S::kPerWave < 64, "stages");
+    static_assert(S::kQueries * D * 4 <= NS * S::kRecord, "the queries' staging fits the ring");
+    static_assert(KB * (D + 4) * 4 <= S::kRecord, "a tile's values fit a buffer as they stand");
     extern __shared__ __attribute__((aligned(1024))) char sbuf[];  // NS tiles of S::kRecord bytes
 
     const int tid = threadIdx.x;
@@ -859,13 +879,31 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         }
     };
     // The wave's queries, operand B of S^T: lane (query lr, half g) holds
-    // dimensions 16 st + 8 g .. + 7 at step st.  Queries past lq read the last.
+    // dimensions 16 st + 8 g .. + 7 at step st; queries past lq read the
+    // last.  With LOCAL (a few tiles of keys, so the queries' loads weigh)
+    // the workgroup's queries go through LDS first, rows of D read as float4
+    // by consecutive threads; otherwise each lane reads its own row.
     half8 qh[S::kSteps], ql[S::kSteps];
     const float qscale = a.scale * 1.44269504088896341f;  // scale log2(e), folded into the queries
     {
-        int64_t i = q0 + lr;
-        i = i < a.lq ? i : a.lq - 1;
-        const float *qp = a.q + bi * a.qnb3 + hi * a.qnb2 + i * a.qnb1;
+        const float *qp;
+        if constexpr (LOCAL) {
+            float *qstage = reinterpret_cast<float *>(sbuf);  // [kQueries][D]
+            const int64_t qrow0 = static_cast<int64_t>(qb) * S::kQueries;
+            for (int idx = tid; idx < S::kQueries * (D / 4); idx += 256) {
+                const int r = idx / (D / 4), c4 = idx - r * (D / 4);
+                int64_t i = qrow0 + r;
+                i = i < a.lq ? i : a.lq - 1;
+                *reinterpret_cast<float4v *>(qstage + r * D + 4 * c4) =
+                    *reinterpret_cast<const float4v *>(a.q + bi * a.qnb3 + hi * a.qnb2 + i * a.qnb1 + 4 * c4);
+            }
+            __syncthreads();
+            qp = qstage + (wave * 32 + lr) * D;
+        } else {
+            int64_t i = q0 + lr;
+            i = i < a.lq ? i : a.lq - 1;
+            qp = a.q + bi * a.qnb3 + hi * a.qnb2 + i * a.qnb1;
+        }
 #pragma unroll
         for (int st = 0; st < S::kSteps; ++st)
 #pragma unroll
@@ -876,8 +914,31 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 qh[st][j] = h;
                 ql[st][j] = l;
             }
+        if constexpr (LOCAL) __syncthreads();  // every wave's queries read before the ring is filled
     }
-
+    // LOCAL (the tiles fit the ring with a buffer to spare): the workgroup
+    // splits the keys and values itself, tile t into buffer t, where the other
+    // form copies the tiles made by attention_tiles_kernel; each tile's values
+    // go first as they stand into the spare buffer, rows read as float4, and
+    // are transposed from there.
+    if constexpr (LOCAL) {
+        const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
+        float *vt = reinterpret_cast<float *>(sbuf + (NS - 1) * S::kRecord);  // [KB][D + 4]
+        for (int64_t t = 0; t < nk; ++t) {
+            _Float16 *rec = reinterpret_cast<_Float16 *>(sbuf + t * S::kRecord);
+            split_keys<D, KB>(a, bi, kh, t, rec);
+            for (int idx = tid; idx < KB * (D / 4); idx += 256) {
+                const int j = idx / (D / 4), c4 = idx - j * (D / 4);
+                const int64_t key = t * KB + j;
+                float4v x = float4v{};
+                if (key < a.lk) x = *reinterpret_cast<const float4v *>(vg + key * a.vnb1 + 4 * c4);
+                *reinterpret_cast<float4v *>(vt + j * (D + 4) + 4 * c4) = x;
+            }
+            __syncthreads();
+            split_values<D, KB>([&](int j, int dim) { return vt[j * (D + 4) + dim]; }, rec);
+            __syncthreads();
+        }
+    }
     float16v oh[S::kDvt], ol[S::kDvt];
 #pragma unroll
     for (int c = 0; c < S::kDvt; ++c) {
@@ -895,6 +956,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // NS - 1 is.
     constexpr int kAhead = PIPE ? NS - 2 : NS - 1;
     const auto sync = [&](int64_t t) {
+        if constexpr (LOCAL) return;  // every tile in LDS since the start
         // The wave's copies of tile t are done once at most kAhead - 1
         // tiles' copies are outstanding after them (none, near the end);
         // every wave's are, past the barrier, which also ends every wave's
@@ -964,9 +1026,11 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // The first kAhead tiles on their way, once the queries are in; then
     // every tile but the last (with PIPE, the next one's scores beside it),
     // and the last, masked where it is not full.
+    if constexpr (!LOCAL) {
 #pragma unroll
-    for (int st = 0; st < kAhead; ++st) {
-        if (st < nk) issue(st, st);
+        for (int st = 0; st < kAhead; ++st) {
+            if (st < nk) issue(st, st);
+        }
     }
     const auto last = [&](float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
         float p[S::kTiles][16];
@@ -1056,11 +1120,31 @@ size_t split_work(const AttentionArgs &a) {
     return static_cast<size_t>(a.b * a.hk) * static_cast<size_t>(ceil_div(a.lk, SplitShape<D>::kKeys)) * S::kRecord;
 }
 
+template <int D, bool LOCAL>
+hipError_t launch_split_t(AttentionArgs a, const void *work, hipStream_t stream) {
+    using SH = SplitShape<D>;
+    using S = Split<D, SH::kKeys>;
+    a.qblocks = ceil_div(a.lq, S::kQueries);
+    const size_t lds = static_cast<size_t>(SH::kStages) * S::kRecord;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe, LOCAL>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (attr != hipSuccess) return attr;
+    dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
+    KernelScope scope("attention", stream);
+    SDHIP_LAUNCH((attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe, LOCAL>), grid, block, lds,
+                 stream, a, static_cast<const char *>(work));
+    return hipGetLastError();
+}
+
 template <int D>
 hipError_t launch_split(AttentionArgs a, void *work, hipStream_t stream) {
     using SH = SplitShape<D>;
-    using S = Split<D, SH::kKeys>;
     const int64_t nk = ceil_div(a.lk, SH::kKeys);
+    // Keys and values that fit the ring with a buffer to spare
+    // (cross-attention's 77 at heads of up to 64): each workgroup splits them
+    // itself, with no launch before it.
+    if (nk < SH::kStages) return launch_split_t<D, true>(a, nullptr, stream);
     {
         KernelScope scope("attention.tiles", stream);
         SDHIP_LAUNCH((attention_tiles_kernel<D, SH::kKeys>),
@@ -1069,17 +1153,7 @@ hipError_t launch_split(AttentionArgs a, void *work, hipStream_t stream) {
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
-    a.qblocks = ceil_div(a.lq, S::kQueries);
-    const size_t lds = static_cast<size_t>(SH::kStages) * S::kRecord;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (attr != hipSuccess) return attr;
-    dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
-    KernelScope scope("attention", stream);
-    SDHIP_LAUNCH((attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe>), grid, block, lds, stream, a,
-                 static_cast<const char *>(work));
-    return hipGetLastError();
+    return launch_split_t<D, false>(a, work, stream);
 }
 
 template <int D, int QT, int KB>
@@ -1099,9 +1173,10 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 // of d = dv dimensions, an instantiated head size, float4-aligned rows.
 bool fast_form(const AttentionArgs &a) {
     const bool size = a.d == 32 || a.d == 40 || a.d == 64 || a.d == 80 || a.d == 96 || a.d == 128 || a.d == 160;
-    return size && a.d == a.dv && !a.khalf && !a.vhalf && aligned16(a.k) && aligned16(a.v) && aligned16(a.y) &&
-           a.knb1 % 4 == 0 && a.knb2 % 4 == 0 && a.knb3 % 4 == 0 && a.vnb1 % 4 == 0 && a.vnb2 % 4 == 0 &&
-           a.vnb3 % 4 == 0 && a.ynb1 % 4 == 0 && a.ynb2 % 4 == 0 && a.ynb3 % 4 == 0;
+    return size && a.d == a.dv && !a.khalf && !a.vhalf && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) &&
+           aligned16(a.y) && a.qnb1 % 4 == 0 && a.qnb2 % 4 == 0 && a.qnb3 % 4 == 0 && a.knb1 % 4 == 0 &&
+           a.knb2 % 4 == 0 && a.knb3 % 4 == 0 && a.vnb1 % 4 == 0 && a.vnb2 % 4 == 0 && a.vnb3 % 4 == 0 &&
+           a.ynb1 % 4 == 0 && a.ynb2 % 4 == 0 && a.ynb3 % 4 == 0;
 }
 
 // Whether the split form takes the operands: the fast form's, unless the

@@ -146,3 +146,22 @@ def test_attention_work_buffer_checked(gpu):
     sdhip.check(lib.sdhip_attention(dq, dq, dq, dy, 0.1, 0.0, 0.0, work.data_ptr(), size, sdhip.stream_handle()),
                 "attention")
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,lq,lk,h,hk,b", [(40, 300, 77, 2, 2, 2), (40, 129, 1, 1, 1, 1), (40, 130, 31, 2, 1, 1),
+                                            (40, 64, 32, 1, 1, 2), (40, 200, 33, 2, 2, 1), (64, 257, 96, 2, 1, 1),
+                                            (64, 100, 97, 2, 2, 1), (96, 70, 64, 2, 2, 1), (96, 70, 65, 2, 2, 1),
+                                            (160, 40, 77, 2, 1, 2), (32, 33, 90, 3, 3, 1), (128, 128, 64, 1, 1, 1)],
+                         ids=lambda c: str(c))
+def test_short_keys_in_the_workgroup(gpu, d, lq, lk, h, hk, b):
+    """Keys and values that fit the split form's ring with a buffer to spare
+    (up to three tiles of 32 keys for heads of 64 or fewer, two above): every
+    workgroup splits them itself, with no tiles launch before it; at the edges
+    of that (one key, 31, 32, 33, 96 and 97 of 64, 64 and 65 of 96, 77 of
+    160), ragged queries, heads sharing keys."""
+    q, k, v, y, scale = attention_case(gpu, d, lq, lk, h, hk, b, False, seed=d + lq + lk)
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    print(f"attention d={d} lq={lq} lk={lk}: {err:.3g}")
+    assert err <= BOUND
