@@ -885,7 +885,114 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // by consecutive threads; otherwise each lane reads its own row.
     half8 qh[S::kSteps], ql[S::kSteps];
     const float qscale = a.scale * 1.44269504088896341f;  // scale log2(e), folded into the queries
-    {
+    // LOCAL, where the staging fits: every load of the workgroup -- its
+    // queries, and the keys and values of every tile -- in flight at once,
+    // into registers; then the queries staged in buffers 1 .., the values as
+    // they stand in the spare buffer NS - 1, tile 0's keys split into buffer
+    // 0; past a barrier each lane's query from the staging; past another the
+    // other tiles' keys split, the padding dimensions of the keys cleared and
+    // every tile's values split and transposed from the staging.  One wait for
+    // memory where a tile at a time takes one a tile.
+    constexpr bool kBatch = LOCAL && (NS - 1) * KB * (D + 4) * 4 <= S::kRecord &&
+                            S::kQueries * D * 4 <= (NS - 2) * S::kRecord;
+    if constexpr (kBatch) {
+        constexpr int kQ4 = S::kQueries * (D / 4);  // float4s of the workgroup's queries
+        constexpr int kQPer = (kQ4 + 255) / 256;
+        constexpr int kKV4 = (NS - 1) * KB * (D / 4);  // float4s of the keys (or values) of NS - 1 tiles
+        constexpr int kKVPer = (kKV4 + 255) / 256;
+        const float *qg = a.q + bi * a.qnb3 + hi * a.qnb2;
+        const float *kg = static_cast<const float *>(a.k) + bi * a.knb3 + kh * a.knb2;
+        const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
+        const int64_t qrow0 = static_cast<int64_t>(qb) * S::kQueries;
+        float4v qv[kQPer], kv[kKVPer], vv[kKVPer];
+#pragma unroll
+        for (int i = 0; i < kQPer; ++i) {
+            const int idx = tid + 256 * i;
+            qv[i] = float4v{};
+            if (idx < kQ4) {
+                const int r = idx / (D / 4), c4 = idx - r * (D / 4);
+                const int64_t row = qrow0 + r < a.lq ? qrow0 + r : a.lq - 1;
+                qv[i] = *reinterpret_cast<const float4v *>(qg + row * a.qnb1 + 4 * c4);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kKVPer; ++i) {
+            const int idx = tid + 256 * i;
+            const int key = idx / (D / 4), c4 = idx - key * (D / 4);
+            kv[i] = float4v{};
+            vv[i] = float4v{};
+            if (idx < kKV4 && key < a.lk) {
+                kv[i] = *reinterpret_cast<const float4v *>(kg + key * a.knb1 + 4 * c4);
+                vv[i] = *reinterpret_cast<const float4v *>(vg + key * a.vnb1 + 4 * c4);
+            }
+        }
+        float *qstage = reinterpret_cast<float *>(sbuf + S::kRecord);              // [kQueries][D]
+        float *vstage = reinterpret_cast<float *>(sbuf + (NS - 1) * S::kRecord);   // [key][D + 4]
+        // Key `key`'s four dimensions 4 c4 .. split into its tile's two planes.
+        const auto put_key = [&](int key, int c4, float4v x) {
+            _Float16 *rec = reinterpret_cast<_Float16 *>(sbuf + (key / KB) * S::kRecord);
+            const int j = key % KB;
+            half4a h, l;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                _Float16 hh, ll;
+                split_part(x[r] * kSplitDown, hh, ll);
+                h[r] = hh;
+                l[r] = ll;
+            }
+            *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = h;
+            *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
+        };
+#pragma unroll
+        for (int i = 0; i < kQPer; ++i) {
+            const int idx = tid + 256 * i;
+            if (idx < kQ4) {
+                const int r = idx / (D / 4), c4 = idx - r * (D / 4);
+                *reinterpret_cast<float4v *>(qstage + r * D + 4 * c4) = qv[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kKVPer; ++i) {
+            const int idx = tid + 256 * i;
+            const int key = idx / (D / 4), c4 = idx - key * (D / 4);
+            if (idx < kKV4) {
+                *reinterpret_cast<float4v *>(vstage + key * (D + 4) + 4 * c4) = vv[i];
+                if (key < KB) put_key(key, c4, kv[i]);
+            }
+        }
+        __syncthreads();
+        const float *qp = qstage + (wave * 32 + lr) * D;
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int dim = 16 * st + 8 * g + j;
+                _Float16 h, l;
+                split_part(dim < D ? (qp[dim] * qscale) * kSplitDown : 0.0f, h, l);
+                qh[st][j] = h;
+                ql[st][j] = l;
+            }
+        __syncthreads();  // every wave's queries read before the tiles overwrite their staging
+#pragma unroll
+        for (int i = 0; i < kKVPer; ++i) {
+            const int idx = tid + 256 * i;
+            const int key = idx / (D / 4), c4 = idx - key * (D / 4);
+            if (idx < kKV4 && key >= KB && key < nk * KB) put_key(key, c4, kv[i]);
+        }
+        constexpr int kPad4 = (S::kDp - D) / 4;  // float4s of padding dimensions a key
+        if constexpr (kPad4 > 0) {
+            for (int idx = tid; idx < nk * KB * kPad4; idx += 256) {
+                const int key = idx / kPad4, c4 = D / 4 + (idx - key * kPad4);
+                put_key(key, c4, float4v{});
+            }
+        }
+        for (int64_t t = 0; t < nk; ++t) {
+            const float *vt = vstage + t * KB * (D + 4);
+            split_values<D, KB>([&](int j, int dim) { return vt[j * (D + 4) + dim]; },
+                                reinterpret_cast<_Float16 *>(sbuf + t * S::kRecord));
+        }
+        __syncthreads();
+    } else {
         const float *qp;
         if constexpr (LOCAL) {
             float *qstage = reinterpret_cast<float *>(sbuf);  // [kQueries][D]
@@ -921,7 +1028,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // form copies the tiles made by attention_tiles_kernel; each tile's values
     // go first as they stand into the spare buffer, rows read as float4, and
     // are transposed from there.
-    if constexpr (LOCAL) {
+    if constexpr (LOCAL && !kBatch) {
         const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
         float *vt = reinterpret_cast<float *>(sbuf + (NS - 1) * S::kRecord);  // [KB][D + 4]
         for (int64_t t = 0; t < nk; ++t) {
