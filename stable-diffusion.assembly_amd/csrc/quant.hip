@@ -283,6 +283,11 @@ struct QgemmArgs {
     int64_t groups, slot, kp;
     int64_t xrows, wrows;  // rows of the layouts: the step and group strides (x 64 bytes, x 1)
     int64_t col_blocks;
+    // qgemm3: the workgroups' order, along the rows of x within a column
+    // block (row_blocks of them) where that reads less, else along the
+    // column blocks within a row block.
+    int64_t row_blocks;
+    int32_t by_columns;
     int32_t from_redirect;
     DevChain chain;
 };
@@ -537,9 +542,13 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     const int wr = wave >> 1, wc = wave & 1;
     const int r32 = lane & 31, h = lane >> 5;
 
+    // An XCD takes consecutive workgroups of this order (xcd_swizzle), which
+    // share the operand the order holds fixed in its L2.
     const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int64_t mb = b / p.col_blocks;
-    const int64_t nb = b % p.col_blocks;
+    const uint32_t major = p.by_columns ? static_cast<uint32_t>(p.row_blocks) : static_cast<uint32_t>(p.col_blocks);
+    const uint32_t bq = b / major, br = b - bq * major;
+    const int64_t mb = p.by_columns ? br : bq;
+    const int64_t nb = p.by_columns ? bq : br;
     const int64_t m0 = mb * BM;
     const int64_t n0 = nb * (GATED ? kQWRows / 2 : kQWRows);
     // The W row of block row r (clamped): GATED, rows 0..63 features n0 +
@@ -809,16 +818,24 @@ static_assert((kQStages - 2) * QStage<2>::kCopies < 64, "vmcnt");
 
 // Workgroups of 128 rows of x where the launch still gives every SIMD two
 // waves, else 64.
+// The workgroups go along the rows of x within a column block of W where x
+// is the smaller operand (the gated FF-in's 1976 x 1280 bytes of x against
+// 10240 x 1280 of W): each XCD then reads W's column blocks once and holds
+// all of x in its L2, where the other order reads all of W once per pass of
+// an XCD's workgroups over a row block.
 template <bool GATED>
 hipError_t launch_qgemm2(QgemmArgs p, hipStream_t stream) {
     const int64_t cols = GATED ? p.half : p.N;
     p.col_blocks = ceil_div(cols, GATED ? kQWRows / 2 : kQWRows);
+    p.by_columns = p.M < (GATED ? 2 * p.half : p.N) ? 1 : 0;
     const int64_t blocks128 = ceil_div(p.M, 128) * p.col_blocks;
     if (blocks128 >= 512) {
+        p.row_blocks = ceil_div(p.M, 128);
         SDHIP_LAUNCH((qgemm3_kernel<GATED, 2, kQStages>), dim3(static_cast<uint32_t>(blocks128)), dim3(256), 0,
                      stream, p);
     } else {
-        const dim3 grid(static_cast<uint32_t>(ceil_div(p.M, 64) * p.col_blocks));
+        p.row_blocks = ceil_div(p.M, 64);
+        const dim3 grid(static_cast<uint32_t>(p.row_blocks * p.col_blocks));
         SDHIP_LAUNCH((qgemm3_kernel<GATED, 1, kQStages>), grid, dim3(256), 0, stream, p);
     }
     return hipGetLastError();
