@@ -179,6 +179,25 @@ bool same_layout(const sdhip_tensor *a, const sdhip_tensor *b) {
 
 int64_t nelements(const sdhip_tensor *t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }
 
+size_t tensor_span(const sdhip_tensor *t) {
+    size_t n = t->type == SDHIP_TYPE_F16 ? 2 : 4;
+    for (int k = 0; k < 4; ++k) {
+        if (t->ne[k] <= 0) return 0;
+        if (t->nb[k] < 0) return SIZE_MAX;
+        const uint64_t reach = static_cast<uint64_t>(t->ne[k] - 1) * static_cast<uint64_t>(t->nb[k]);
+        if (reach > SIZE_MAX - n) return SIZE_MAX;
+        n += static_cast<size_t>(reach);
+    }
+    return n;
+}
+
+bool spans_overlap(const void *a, size_t an, const void *b, size_t bn) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    const uintptr_t ea = an > UINTPTR_MAX - pa ? UINTPTR_MAX : pa + an;
+    const uintptr_t eb = bn > UINTPTR_MAX - pb ? UINTPTR_MAX : pb + bn;
+    return pa < eb && pb < ea;
+}
+
 // The chain for an output of extents `ne`: each operand F32, nb[0] = 4, and
 // of the output's extent or 1 along each dimension (the broadcast ggml's ADD
 // and MUL take, fusion.cc:174-186).

@@ -18,25 +18,12 @@ namespace sdhip {
 
 namespace {
 
-// ggml_nbytes of a tensor of one-element blocks: the bytes from its first
-// element to one past its last.
-size_t tensor_bytes(const sdhip_tensor &t) {
-    size_t n = t.type == SDHIP_TYPE_F16 ? 2 : 4;
-    for (int k = 0; k < 4; ++k) {
-        if (t.ne[k] <= 0) return 0;
-        n += static_cast<size_t>((t.ne[k] - 1) * t.nb[k]);
-    }
-    return n;
-}
-
 // Whether the bytes of two tensors share any (memory.cc:42-55): addresses
 // compared, never read.
 bool overlap(const sdhip_tensor &a, const sdhip_tensor &b) {
-    const size_t an = tensor_bytes(a), bn = tensor_bytes(b);
+    const size_t an = tensor_span(&a), bn = tensor_span(&b);
     if (a.data == nullptr || b.data == nullptr || an == 0 || bn == 0) return false;
-    const char *pa = static_cast<const char *>(a.data);
-    const char *pb = static_cast<const char *>(b.data);
-    return pa < pb + bn && pb < pa + an;
+    return spans_overlap(a.data, an, b.data, bn);
 }
 
 // holds<float> (memory.h:196-209): single precision, aligned, whole strides.
@@ -267,7 +254,7 @@ bool redirect_apart(const sdhip_node *node, const Chain &c) {
 bool columns_of(const sdhip_node *view, const sdhip_node *whole, int64_t begin, int64_t width) {
     const sdhip_tensor &v = view->tensor, &w = whole->tensor;
     if (!holds_float(v) || !holds_float(w) || v.ne[0] != width || v.nb[0] != 4 || begin > w.ne[0] ||
-        static_cast<const char *>(v.data) != static_cast<const char *>(w.data) + begin * w.nb[0]) {
+        reinterpret_cast<uintptr_t>(v.data) != address_past(w.data, begin * w.nb[0])) {
         return false;
     }
     for (int k = 1; k < 4; ++k) {
@@ -426,7 +413,7 @@ int sdhip_compute_nodes(const sdhip_node *const *nodes, int n_nodes, int index, 
     const sdhip_node *node = nodes[index];
     // What the node writes was derived from nothing that is kept, or is not
     // to be kept any more, whoever computes it (hooks.cc:104-108).
-    if (node->tensor.data != nullptr) sdhip_forget(node->tensor.data, tensor_bytes(node->tensor));
+    if (node->tensor.data != nullptr) sdhip_forget(node->tensor.data, tensor_span(&node->tensor));
     sdhip_node_plan p;
     const sdhip_status planned = sdhip_plan_nodes(nodes, n_nodes, index, &p);
     if (planned == SDHIP_UNSUPPORTED) return 0;
@@ -434,7 +421,7 @@ int sdhip_compute_nodes(const sdhip_node *const *nodes, int n_nodes, int index, 
     // And what a fused node writes in place of the node's own (hooks.cc:110-121).
     const sdhip_tensor *written[] = {p.chain.redirect, p.gated_out != nullptr ? &p.gated_out->tensor : nullptr};
     for (const sdhip_tensor *t : written) {
-        if (t != nullptr && t->data != nullptr) sdhip_forget(t->data, tensor_bytes(*t));
+        if (t != nullptr && t->data != nullptr) sdhip_forget(t->data, tensor_span(t));
     }
     const sdhip_tensor *y = &node->tensor;
     const sdhip_epilogue *chain = p.chain.count > 0 || p.chain.redirect != nullptr ? &p.chain : nullptr;

@@ -97,6 +97,18 @@ bool contiguous(const sdhip_tensor *t);
 bool same_shape(const sdhip_tensor *a, const sdhip_tensor *b);
 bool same_layout(const sdhip_tensor *a, const sdhip_tensor *b);
 int64_t nelements(const sdhip_tensor *t);
+// The bytes from a tensor's first element to one past its last (ggml_nbytes
+// of one-element blocks); 0 for an empty tensor, SIZE_MAX where a stride is
+// negative (its reach is not bounded here, so it is taken to reach anything).
+size_t tensor_span(const sdhip_tensor *t);
+// Whether the bytes [a, a + an) and [b, b + bn) share any: the addresses
+// compared as integers, the ends saturating, nothing read.
+bool spans_overlap(const void *a, size_t an, const void *b, size_t bn);
+// The address `bytes` past p as an integer (no pointer arithmetic on what
+// may be a null or foreign pointer).
+inline uintptr_t address_past(const void *p, int64_t bytes) {
+    return reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(bytes);
+}
 
 sdhip_status device_chain(const sdhip_epilogue *e, const int64_t ne[4], DevChain &c);
 sdhip_status output_of(const sdhip_tensor *y, const sdhip_epilogue *e, float *&out, int32_t &from_redirect);

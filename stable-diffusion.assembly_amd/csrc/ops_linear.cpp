@@ -13,21 +13,9 @@ namespace sdhip {
 
 namespace {
 
-bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
-    const char *pa = static_cast<const char *>(a);
-    const char *pb = static_cast<const char *>(b);
-    return pa < pb + bn && pb < pa + an;
-}
+bool overlaps(const void *a, size_t an, const void *b, size_t bn) { return spans_overlap(a, an, b, bn); }
 
-size_t nbytes(const sdhip_tensor *t) {
-    // The span of memory a tensor of these strides reaches (ggml_nbytes).
-    size_t n = t->type == SDHIP_TYPE_F16 ? 2 : 4;
-    for (int k = 0; k < 4; ++k) {
-        if (t->ne[k] <= 0) return 0;
-        n += static_cast<size_t>((t->ne[k] - 1) * t->nb[k]);
-    }
-    return n;
-}
+size_t nbytes(const sdhip_tensor *t) { return tensor_span(t); }
 
 MulMatArgs args_of(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_tensor *y) {
     MulMatArgs a{};

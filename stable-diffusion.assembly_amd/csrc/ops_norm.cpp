@@ -13,6 +13,9 @@ extern "C" {
 int sdhip_group_norm_supported(const sdhip_tensor *x, const sdhip_tensor *y, int groups) {
     if (x == nullptr || y == nullptr) return 0;
     if (!(holds_f32(x) && holds_f32(y) && contiguous(x) && contiguous(y) && same_shape(x, y) && groups > 0)) return 0;
+    // Empty tensors are the caller's (nothing to compute; the split of the
+    // groups into slices takes at least one image and number).
+    if (nelements(x) <= 0) return 0;
     // A group's numbers are indexed in 32 bits.
     return ceil_div(x->ne[2], groups) * x->ne[0] * x->ne[1] < (int64_t(1) << 31);
 }

@@ -80,11 +80,7 @@ size_t first_fit(const State &s, size_t bytes) {
     return at + bytes <= s.size ? at : SIZE_MAX;
 }
 
-bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
-    const char *pa = static_cast<const char *>(a);
-    const char *pb = static_cast<const char *>(b);
-    return pa < pb + bn && pb < pa + an;
-}
+bool overlaps(const void *a, size_t an, const void *b, size_t bn) { return spans_overlap(a, an, b, bn); }
 
 }  // namespace
 
