@@ -364,6 +364,161 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
         }
 }
 
+// Heads of up to 512 dimensions (more than 384) with single-precision keys
+// and values (the VAE's middle block, 512): the wide form's products, softmax and sums, in the same
+// order -- bit for bit its output -- with each wave's 16 queries held in
+// registers for the whole split (lane (lr, lg) holds dimensions 4 j + lg of
+// query lr: operand B of step j) and a block's 32 keys and their values
+// staged whole in LDS, rows of DP + 4 and 16 NDV + 4 floats (64 banks for
+// both reads), float4 copies: two barriers a block of keys, where the wide
+// form restages its queries with every chunk of every block.
+template <int DP, int NDV>
+__global__ __launch_bounds__(256, 1) void attention_wide2_kernel(AttentionArgs a, int64_t splits, int64_t key_len,
+                                                                  WidePartial part) {
+    constexpr int kLdk = DP + 4, kLdv = 16 * NDV + 4;
+    constexpr int NQ = DP / 4;
+    extern __shared__ float lds[];
+    float *ks = lds;                // [32][kLdk]
+    float *vs = ks + kKeys * kLdk;  // [32][kLdv]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t qb = b % static_cast<uint32_t>(a.qblocks);
+    const uint32_t rest = b / static_cast<uint32_t>(a.qblocks);
+    const int64_t sp = rest % splits;
+    const uint32_t bh = static_cast<uint32_t>(rest / splits);
+    const int64_t k_begin = sp * key_len;
+    const int64_t k_end = k_begin + key_len < a.lk ? k_begin + key_len : a.lk;
+    const int64_t hi = bh % a.h;
+    const int64_t bi = bh / a.h;
+    const int64_t kh = hi / (a.h / a.hk);
+    const int64_t q0 = static_cast<int64_t>(qb) * kQueries;
+    const float *kg = static_cast<const float *>(a.k) + bi * a.knb3 + kh * a.knb2;
+    const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
+
+    float qr[NQ];
+    {
+        const int64_t i = q0 + wave * 16 + lr;
+        const float *qp = a.q + bi * a.qnb3 + hi * a.qnb2 + (i < a.lq ? i : 0) * a.qnb1;
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+            const int e = 4 * j + lg;
+            qr[j] = (e < a.d && i < a.lq) ? qp[e] : 0.0f;
+        }
+    }
+    float4v o[NDV];
+#pragma unroll
+    for (int t = 0; t < NDV; ++t) o[t] = float4v{};
+    float m = -INFINITY;
+    double l = 0.0;
+
+    for (int64_t k0 = k_begin; k0 < k_end; k0 += kKeys) {
+        __syncthreads();  // the last block's keys and values are read
+        // A row's float4s past d (dv) and the rows past k_end are zeros.
+        for (int idx = tid; idx < kKeys * (DP / 4); idx += 256) {
+            const int j = idx / (DP / 4), e = 4 * (idx - j * (DP / 4));
+            const int64_t key = k0 + j;
+            float4v x = float4v{};
+            if (e < a.d && key < k_end) x = *reinterpret_cast<const float4v *>(kg + key * a.knb1 + e);
+            *reinterpret_cast<float4v *>(ks + j * kLdk + e) = x;
+        }
+        for (int idx = tid; idx < kKeys * 4 * NDV; idx += 256) {
+            const int j = idx / (4 * NDV), e = 4 * (idx - j * (4 * NDV));
+            const int64_t key = k0 + j;
+            float4v x = float4v{};
+            if (e < a.dv && key < k_end) x = *reinterpret_cast<const float4v *>(vg + key * a.vnb1 + e);
+            *reinterpret_cast<float4v *>(vs + j * kLdv + e) = x;
+        }
+        __syncthreads();
+
+        // S^T = K Q^T for two tiles of 16 keys: the lane's scores of its
+        // query lr, keys 16 t + 4 lg + r; dimensions in order, four a step.
+        float4v s[2] = {float4v{}, float4v{}};
+#pragma unroll
+        for (int j = 0; j < NQ; ++j)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float kv = ks[(16 * t + lr) * kLdk + 4 * j + lg];
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv, qr[j], s[t], 0, 0, 0);
+            }
+
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t key = k0 + 16 * t + 4 * lg + r;
+                const float x = key < k_end ? s[t][r] * a.scale : -INFINITY;
+                s[t][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float alpha = m == -INFINITY ? 0.0f : cephes_exp(m - mnew);
+        m = mnew;
+        double psum = 0.0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = s[t][r] == -INFINITY ? 0.0f : cephes_exp(s[t][r] - mnew);
+                s[t][r] = p;
+                psum += static_cast<double>(p);
+            }
+        l = l * static_cast<double>(alpha) + psum;
+#pragma unroll
+        for (int t = 0; t < NDV; ++t) o[t] *= alpha;
+
+        // O^T += V^T P^T: k index 4 lg + r of each tile of 16 keys.
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float *vrow = vs + (16 * t + 4 * lg + r) * kLdv + lr;
+#pragma unroll
+                for (int c = 0; c < NDV; ++c) {
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * c], s[t][r], o[c], 0, 0, 0);
+                }
+            }
+    }
+
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int64_t i = q0 + wave * 16 + lr;
+    if (i >= a.lq) return;
+    if (part.o != nullptr) {
+        const int64_t at = (static_cast<int64_t>(bh) * splits + sp) * a.lq + i;
+        if (lg == 0) {
+            part.m[at] = m;
+            part.l[at] = l;
+        }
+        float *po = part.o + at * a.dv;
+#pragma unroll
+        for (int c = 0; c < NDV; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int e = 16 * c + 4 * lg + r;
+                if (e < a.dv) po[e] = o[c][r];
+            }
+        return;
+    }
+    const float reciprocal = static_cast<float>(1.0 / l);
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
+#pragma unroll
+    for (int c = 0; c < NDV; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = 16 * c + 4 * lg + r;
+            if (e < a.dv) out[e] = o[c][r] * reciprocal;
+        }
+}
+
 // The splits of the keys of a query merged: each split's sum and output
 // rescaled by exp(its maximum - the greatest), as the single pass rescales
 // its running ones, the sum in double, the output times the reciprocal of
@@ -1343,7 +1498,21 @@ hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
         return hipGetLastError();
     };
     hipError_t e;
-    if (a.khalf && a.vhalf) {
+    // Single-precision keys and values of heads of 388 .. 512 dimensions (a
+    // multiple of 4, rows float4-aligned): the queries held in registers,
+    // the dimensions past d zeros that add nothing to the sums.
+    const bool rows4 = a.knb1 % 4 == 0 && a.vnb1 % 4 == 0 && a.knb2 % 4 == 0 && a.vnb2 % 4 == 0 &&
+                       a.knb3 % 4 == 0 && a.vnb3 % 4 == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
+    if (!a.khalf && !a.vhalf && a.dp > 384 && a.dp <= 512 && a.d % 4 == 0 && a.dv % 4 == 0 && rows4 && NDV == 32 &&
+        tuning().attention_generic == 0) {
+        const size_t lds2 = sizeof(float) * (kKeys * (512 + 4) + kKeys * (16 * NDV + 4));
+        hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(attention_wide2_kernel<512, NDV>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));
+        if (e2 != hipSuccess) return e2;
+        SDHIP_LAUNCH((attention_wide2_kernel<512, NDV>), grid, block, lds2, stream, a, w.splits, w.key_len, part);
+        e = hipGetLastError();
+    } else if (a.khalf && a.vhalf) {
         e = launch(attention_wide_kernel<NDV, true, true>);
     } else if (a.khalf) {
         e = launch(attention_wide_kernel<NDV, true, false>);

@@ -86,6 +86,26 @@ def test_attention_vae_decoder(gpu):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("c", [(512, 100, 70, 1, 1, 1), (512, 300, 1000, 2, 1, 1), (500, 65, 33, 2, 2, 1),
+                               (512, 64, 4096, 1, 1, 1)], ids=lambda c: "x".join(map(str, c)))
+def test_wide_heads_in_registers_agree(gpu, c):
+    """Heads of 512 dimensions (500 rounded up to them) with single-precision
+    keys and values: the form that holds each wave's queries in registers
+    gives the wide form's bits (attention_generic=1 takes the latter) -- the
+    same products, softmax and sums in the same order -- one split or
+    several, heads sharing keys, ragged queries and keys."""
+    d, lq, lk, h, hk, b = c
+    _, _, _, y1, _ = attention_case(gpu, d, lq, lk, h, hk, b, False, seed=d + lq)
+    sdhip.set_tuning("attention_generic=1")
+    try:
+        _, _, _, y2, _ = attention_case(gpu, d, lq, lk, h, hk, b, False, seed=d + lq)
+    finally:
+        sdhip.set_tuning("")
+    assert np.isfinite(y1).all()
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,lk", [("cfg4 self", 4096), ("cfg4 cross", 77)])
 def test_attention_bench_shapes(gpu, name, lk):
     """cfg4: Q [2, 8, 4096, 40] ~N(0,1) against 4096 or 77 keys; a sample of
