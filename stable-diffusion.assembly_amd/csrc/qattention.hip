@@ -253,9 +253,15 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     const int32_t *ksum = a.ksum + head_k * a.lkp;
 
     // First pass: the greatest score of each query over the keys.
+    // Tiles wholly of keys take no test per key.
     float top = -INFINITY;
+    const int64_t whole = a.lk / 16;
     for (int64_t kt = 0; kt < a.lkp / 16; ++kt) {
         const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, kt, lr, lg);
+        if (kt < whole) {
+            top = fmaxf(fmaxf(top, fmaxf(sc[0], sc[1])), fmaxf(sc[2], sc[3]));
+            continue;
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (16 * kt + 4 * lg + r < a.lk) top = fmaxf(top, sc[r]);
@@ -281,6 +287,23 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
         // The group's exponentials: tile kt of the group, keys 16 kt + 4 lg + r.
         float e[GT][4];
         float lo = 0.0f, hi = 0.0f;
+        // A group of GT whole tiles of keys, none of them past tail_from,
+        // takes no test per key: Cephes' exponential for each.
+        const int64_t g_end = (g + 1) * a.group;
+        if (a.group == 16 * GT && g_end <= a.lk && g_end <= a.tail_from) {
+#pragma unroll
+            for (int kt = 0; kt < GT; ++kt) {
+                const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, g * GT + kt, lr, lg);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = cephes_exp(__fsub_rn(sc[r], top));
+                    total += static_cast<double>(x);
+                    lo = fminf(lo, x);
+                    hi = fmaxf(hi, x);
+                    e[kt][r] = x;
+                }
+            }
+        } else {
 #pragma unroll
         for (int kt = 0; kt < GT; ++kt) {
             const int64_t j0 = g * a.group + 16 * kt;  // the tile's first key
@@ -304,6 +327,7 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
                 e[kt][r] = x;
             }
         }
+        }
         lo = fminf(lo, __shfl_xor(lo, 16, 64));
         lo = fminf(lo, __shfl_xor(lo, 32, 64));
         hi = fmaxf(hi, __shfl_xor(hi, 16, 64));
@@ -321,6 +345,8 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
 #pragma unroll
         for (int chunk = 0; chunk < (GT + 3) / 4; ++chunk) {
             if (64 * chunk >= a.slot) continue;
+            // The bytes q - 128 of the quantized exponentials (q an integer
+            // in [0, 255]): q packed as an unsigned byte, its top bit flipped.
             int4v bv;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
@@ -330,10 +356,9 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
                     const int kt = 4 * chunk + w;
                     float q = 0.0f;
                     if (kt < GT) q = qa_clamp(__fadd_rn(rintf(__fmul_rn(e[kt][r], inverse)), zero), 0.0f, levels);
-                    const uint32_t byte = static_cast<uint32_t>(static_cast<int>(q) - 128) & 0xffu;
-                    word |= byte << (8 * r);
+                    word = __builtin_amdgcn_cvt_pk_u8_f32(q, r, word);
                 }
-                bv[w] = static_cast<int>(word);
+                bv[w] = static_cast<int>(word ^ 0x80808080u);
             }
             // Tiles of the group past its keys: positions with no key, whose
             // values' bytes are 0; the -128 there multiplies them.
