@@ -43,103 +43,169 @@ namespace {
 
 __device__ __forceinline__ float qa_clamp(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-__device__ __forceinline__ float qa_wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-__device__ __forceinline__ float qa_wave_min(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-__device__ __forceinline__ int qa_wave_sum(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 __device__ __forceinline__ float load_num(const void *p, int64_t at, bool half) {
     if (half) return static_cast<float>(static_cast<const _Float16 *>(p)[at]);
     return static_cast<const float *>(p)[at];
 }
 
-// ------------------------------------------------------------------ keys
+// ------------------------------------------------------------------ operands
 
-// One wave per (image, key head, key): the key's bytes over its sd slot (zeros
-// past d), its scale, offset and integer sum.  Keys from lk to lkp: zeros.
-__global__ __launch_bounds__(256) void qa_keys_kernel(QAttentionArgs a) {
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+// The three quantizers run as one launch: first the values' blocks, then the
+// keys', then the queries'.  A key or a query takes 16 lanes, each lane 4
+// consecutive numbers of every 64 of the slot (sd <= 64 kQaSteps), held in
+// registers between the group's maximum and its quantization; the maxima and
+// the integer sums are exact whatever the order of their reductions.
+constexpr int kQaLanes = 16;
+constexpr int kQaSteps = 4;  // the most 64-byte steps of a slot (sd <= 256)
+constexpr int kQaItems = 256 / kQaLanes;
+
+__device__ __forceinline__ float qa_lanes_max(float v) {
+#pragma unroll
+    for (int off = kQaLanes / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float qa_lanes_min(float v) {
+#pragma unroll
+    for (int off = kQaLanes / 2; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ int qa_lanes_sum(int v) {
+#pragma unroll
+    for (int off = kQaLanes / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Numbers e .. e + 3 of the row at element `base` of p, zeros from `limit`:
+// one 16-byte load where the four are single precision, inside the row and
+// 16-byte aligned.
+__device__ __forceinline__ void qa_load4(const void *p, int64_t base, int64_t e, int64_t limit, bool half,
+                                         float (&x)[4]) {
+    const float *f = half ? nullptr : static_cast<const float *>(p) + base + e;
+    if (!half && e + 4 <= limit && (reinterpret_cast<uintptr_t>(f) & 15) == 0) {
+        const float4v v = *reinterpret_cast<const float4v *>(f);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = v[r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = e + r < limit ? load_num(p, base + e + r, half) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ uint32_t qa_byte(int q, int r) { return static_cast<uint32_t>(q & 0xff) << (8 * r); }
+
+// Keys: 16 a block, each over its sd slot (zeros past d), its scale, offset
+// and integer sum.  Keys from lk to lkp: zeros.
+__device__ __forceinline__ void qa_keys_block(const QAttentionArgs &a, int64_t blk) {
+    const int64_t item = blk * kQaItems + (threadIdx.x / kQaLanes);
     if (item >= a.b * a.hk * a.lkp) return;
-    const int lane = threadIdx.x & 63;
+    const int l = threadIdx.x % kQaLanes;
     const int64_t j = item % a.lkp;
     const int64_t head = item / a.lkp;  // bi * hk + kh
     const int64_t bi = head / a.hk, kh = head % a.hk;
     const bool valid = j < a.lk;
     const int64_t base = bi * a.knb3 + kh * a.knb2 + (valid ? j : 0) * a.knb1;
+    const int64_t limit = valid ? a.d : 0;
+    const int steps = static_cast<int>(a.sd / 64);
+    float x[kQaSteps][4] = {};
     float m = 0.0f;
-    for (int64_t e = lane; e < a.d; e += 64) m = fmaxf(m, valid ? fabsf(load_num(a.k, base + e, a.khalf)) : 0.0f);
-    m = qa_wave_max(m);
+#pragma unroll
+    for (int st = 0; st < kQaSteps; ++st) {
+        if (st < steps) {
+            qa_load4(a.k, base, 64 * st + 4 * l, limit, a.khalf, x[st]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(x[st][r]));
+        }
+    }
+    m = qa_lanes_max(m);
     const float wmax = static_cast<float>(a.wmax);
     const float s = __fdiv_rn(m, wmax);
     const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
     int sum = 0;
     int8_t *dst = a.kq + item * a.sd;
-    for (int64_t e = lane; e < a.sd; e += 64) {
-        int q = 0;
-        if (valid && e < a.d) {
-            q = static_cast<int>(qa_clamp(rintf(__fmul_rn(load_num(a.k, base + e, a.khalf), inverse)), -wmax, wmax));
+#pragma unroll
+    for (int st = 0; st < kQaSteps; ++st) {
+        if (st < steps) {
+            const int64_t e = 64 * st + 4 * l;
+            uint32_t word = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int q = 0;
+                if (e + r < limit) q = static_cast<int>(qa_clamp(rintf(__fmul_rn(x[st][r], inverse)), -wmax, wmax));
+                word |= qa_byte(q, r);
+                sum += q;
+            }
+            *reinterpret_cast<uint32_t *>(dst + e) = word;
         }
-        dst[e] = static_cast<int8_t>(q);
-        sum += q;
     }
-    sum = qa_wave_sum(sum);
-    if (lane == 0) {
+    sum = qa_lanes_sum(sum);
+    if (l == 0) {
         a.ks[item] = s;
         a.ko[item] = __fmul_rn(s, static_cast<float>(sum));
         a.ksum[item] = sum;
     }
 }
 
-// ------------------------------------------------------------------ values
+// Values: a block per (image, key head, group of keys, 64 dimensions), per
+// (dimension, group) the group's bytes in the order of operand A (below), its
+// scale, offset and integer sum, stored [head][group][dvp].  Keys past lk and
+// dimensions past dv: zeros.  A wave takes 16 dimensions, a lane one of them
+// and every fourth run of 4 consecutive keys of the slot: key w = 64 chunk +
+// 16 kt + 4 kg + r sits at position p = 64 chunk + 16 kg + 4 kt + r, so that a
+// run's 4 bytes are one word.
+constexpr int kQaRuns = 256 / 16;  // the most runs a lane takes (slot <= 256)
 
-// One wave per (image, key head, group of keys, dimension): the group's bytes
-// in the order of operand A (above), its scale, offset and integer sum,
-// stored [head][group][dvp].  Keys past lk and dimensions past dv: zeros.
-__global__ __launch_bounds__(256) void qa_values_kernel(QAttentionArgs a) {
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (item >= a.b * a.hk * a.groups * a.dvp) return;
-    const int lane = threadIdx.x & 63;
-    const int64_t c = item % a.dvp;
-    const int64_t rest = item / a.dvp;
+__device__ __forceinline__ void qa_values_block(const QAttentionArgs &a, int64_t blk) {
+    const int64_t chunks = (a.dvp + 63) / 64;
+    const int64_t cc = blk % chunks;
+    const int64_t rest = blk / chunks;
     const int64_t g = rest % a.groups;
     const int64_t head = rest / a.groups;
     const int64_t bi = head / a.hk, kh = head % a.hk;
-    const int64_t base = bi * a.vnb3 + kh * a.vnb2 + c;
-    // Position p of the slot holds key w of the group (or nothing).
-    const auto key_of = [&](int64_t p) -> int64_t {
-        const int64_t chunk = p >> 6, kg = (p >> 4) & 3, kt = (p >> 2) & 3, r = p & 3;
-        return 64 * chunk + 16 * kt + 4 * kg + r;
-    };
-    const auto value_at = [&](int64_t w) -> float {
-        const int64_t key = g * a.group + w;
-        return (w < a.group && key < a.lk && c < a.dv) ? load_num(a.v, base + key * a.vnb1, a.vhalf) : 0.0f;
-    };
+    const int lane = threadIdx.x & 63;
+    const int64_t c = cc * 64 + (threadIdx.x >> 6) * 16 + (lane & 15);
+    const int rg = lane >> 4;  // runs rg, rg + 4, ...
+    const int runs = static_cast<int>(a.slot / 16);
+    const bool dim = c < a.dv;
+    const int64_t base = bi * a.vnb3 + kh * a.vnb2 + (dim ? c : 0);
+    float x[kQaRuns][4] = {};
     float m = 0.0f;
-    for (int64_t p = lane; p < a.slot; p += 64) m = fmaxf(m, fabsf(value_at(key_of(p))));
-    m = qa_wave_max(m);
+#pragma unroll
+    for (int i = 0; i < kQaRuns; ++i) {
+        if (i < runs) {
+            const int64_t w0 = 4 * (rg + 4 * i);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t key = g * a.group + w0 + r;
+                if (dim && w0 + r < a.group && key < a.lk) x[i][r] = load_num(a.v, base + key * a.vnb1, a.vhalf);
+                m = fmaxf(m, fabsf(x[i][r]));
+            }
+        }
+    }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
     const float wmax = static_cast<float>(a.wmax);
     const float s = __fdiv_rn(m, wmax);
     const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
     int sum = 0;
     int8_t *dst = a.vq + ((head * a.dvp + c) * a.groups + g) * a.slot;
-    for (int64_t p = lane; p < a.slot; p += 64) {
-        const int q = static_cast<int>(qa_clamp(rintf(__fmul_rn(value_at(key_of(p)), inverse)), -wmax, wmax));
-        dst[p] = static_cast<int8_t>(q);
-        sum += q;
+#pragma unroll
+    for (int i = 0; i < kQaRuns; ++i) {
+        if (i < runs) {
+            const int64_t w0 = 4 * (rg + 4 * i);
+            uint32_t word = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int q = static_cast<int>(qa_clamp(rintf(__fmul_rn(x[i][r], inverse)), -wmax, wmax));
+                word |= qa_byte(q, r);
+                sum += q;
+            }
+            const int64_t p = (w0 & ~63) + 16 * ((w0 >> 2) & 3) + 4 * ((w0 >> 4) & 3);
+            if (c < a.dvp) *reinterpret_cast<uint32_t *>(dst + p) = word;
+        }
     }
-    sum = qa_wave_sum(sum);
-    if (lane == 0) {
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (rg == 0 && c < a.dvp) {
         const int64_t at = (head * a.groups + g) * a.dvp + c;
         a.vs[at] = s;
         a.vo[at] = __fmul_rn(s, static_cast<float>(sum));
@@ -147,53 +213,86 @@ __global__ __launch_bounds__(256) void qa_values_kernel(QAttentionArgs a) {
     }
 }
 
-// ------------------------------------------------------------------ queries
-
-// One wave per (image, head, query): the query's bytes as q - 128 over its sd
-// slot (the group's tail past d its zero point, the slot past the group 0:
-// the keys' bytes there are 0), its scale and offset times the softmax's
-// scale.  Queries from lq to lqp: zeros.
-__global__ __launch_bounds__(256) void qa_queries_kernel(QAttentionArgs a) {
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+// Queries: 16 a block, each over its sd slot as q - 128 (the group's tail past
+// d its zero point, the slot past the group 0: the keys' bytes there are 0),
+// its scale and offset times the softmax's scale.  Queries from lq to lqp:
+// zeros.
+__device__ __forceinline__ void qa_queries_block(const QAttentionArgs &a, int64_t blk) {
+    const int64_t item = blk * kQaItems + (threadIdx.x / kQaLanes);
     if (item >= a.b * a.h * a.lqp) return;
-    const int lane = threadIdx.x & 63;
+    const int l = threadIdx.x % kQaLanes;
     const int64_t i = item % a.lqp;
     const int64_t head = item / a.lqp;  // bi * h + hh
     const int64_t bi = head / a.h, hh = head % a.h;
     const bool valid = i < a.lq;
-    const float *row = a.q + bi * a.qnb3 + hh * a.qnb2 + (valid ? i : 0) * a.qnb1;
+    const int64_t base = bi * a.qnb3 + hh * a.qnb2 + (valid ? i : 0) * a.qnb1;
+    const int64_t limit = valid ? a.d : 0;
+    const int steps = static_cast<int>(a.sd / 64);
+    float x[kQaSteps][4] = {};
     float lo = 0.0f, hi = 0.0f;
-    for (int64_t e = lane; e < a.d; e += 64) {
-        const float x = valid ? row[e] : 0.0f;
-        lo = fminf(lo, x);
-        hi = fmaxf(hi, x);
+#pragma unroll
+    for (int st = 0; st < kQaSteps; ++st) {
+        if (st < steps) {
+            qa_load4(a.q, base, 64 * st + 4 * l, limit, false, x[st]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                lo = fminf(lo, x[st][r]);
+                hi = fmaxf(hi, x[st][r]);
+            }
+        }
     }
-    lo = qa_wave_min(lo);
-    hi = qa_wave_max(hi);
+    lo = qa_lanes_min(lo);
+    hi = qa_lanes_max(hi);
     const float levels = static_cast<float>(a.levels);
     const float s = __fdiv_rn(__fsub_rn(hi, lo), levels);
     const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
     const float zero = rintf(__fmul_rn(-lo, inverse));
     int8_t *dst = a.qq + item * a.sd;
-    for (int64_t e = lane; e < a.sd; e += 64) {
-        float q = 128.0f;
-        if (e < a.d) {
-            q = qa_clamp(__fadd_rn(rintf(__fmul_rn(valid ? row[e] : 0.0f, inverse)), zero), 0.0f, levels);
-        } else if (e < a.gd) {
-            q = zero;
+#pragma unroll
+    for (int st = 0; st < kQaSteps; ++st) {
+        if (st < steps) {
+            const int64_t e = 64 * st + 4 * l;
+            uint32_t word = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float q = 128.0f;
+                if (e + r < a.d) {
+                    q = qa_clamp(__fadd_rn(rintf(__fmul_rn(x[st][r], inverse)), zero), 0.0f, levels);
+                } else if (e + r < a.gd) {
+                    q = zero;
+                }
+                word |= qa_byte(static_cast<int>(q) - 128, r);
+            }
+            *reinterpret_cast<uint32_t *>(dst + e) = word;
         }
-        dst[e] = static_cast<int8_t>(static_cast<int>(q) - 128);
     }
-    if (lane == 0) {
+    if (l == 0) {
         a.qs[item] = __fmul_rn(s, a.scale);
         a.qo[item] = __fmul_rn(__fmul_rn(s, zero), a.scale);
     }
 }
 
-// ------------------------------------------------------------------ attention
+struct QaOperandBlocks {
+    int64_t values, keys, queries;
+};
 
-// The most 16-byte steps of the scores' k (sd <= 256).
-constexpr int kQaSteps = 4;
+QaOperandBlocks qa_operand_blocks(const QAttentionArgs &a) {
+    return {a.b * a.hk * a.groups * ceil_div(a.dvp, 64), ceil_div(a.b * a.hk * a.lkp, kQaItems),
+            ceil_div(a.b * a.h * a.lqp, kQaItems)};
+}
+
+__global__ __launch_bounds__(256) void qa_operands_kernel(QAttentionArgs a, QaOperandBlocks n) {
+    const int64_t blk = blockIdx.x;
+    if (blk < n.values) {
+        qa_values_block(a, blk);
+    } else if (blk < n.values + n.keys) {
+        qa_keys_block(a, blk - n.values);
+    } else {
+        qa_queries_block(a, blk - n.values - n.keys);
+    }
+}
+
+// ------------------------------------------------------------------ attention
 
 // The scores of key tile kt (keys 16 kt + 4 lg + r) for the lane's query:
 // the integer products over the sd bytes, restored, and scaled back.
@@ -487,20 +586,10 @@ hipError_t launch_quantized_attention(QAttentionArgs a, void *work, hipStream_t 
     a.qs = reinterpret_cast<float *>(base + l.qs);
     a.qo = reinterpret_cast<float *>(base + l.qo);
     {
-        KernelScope scope("qattention.keys", stream);
-        SDHIP_LAUNCH(qa_keys_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.lkp, 4))), dim3(256), 0,
-                     stream, a);
-    }
-    {
-        KernelScope scope("qattention.values", stream);
-        SDHIP_LAUNCH(qa_values_kernel,
-                     dim3(static_cast<uint32_t>(ceil_div(a.b * a.hk * a.groups * a.dvp, 4))), dim3(256), 0,
-                     stream, a);
-    }
-    {
-        KernelScope scope("qattention.queries", stream);
-        SDHIP_LAUNCH(qa_queries_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lqp, 4))), dim3(256),
-                     0, stream, a);
+        KernelScope scope("qattention.operands", stream);
+        const QaOperandBlocks n = qa_operand_blocks(a);
+        SDHIP_LAUNCH(qa_operands_kernel, dim3(static_cast<uint32_t>(n.values + n.keys + n.queries)), dim3(256), 0,
+                     stream, a, n);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
