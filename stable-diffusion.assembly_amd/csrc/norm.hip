@@ -325,6 +325,115 @@ __global__ __launch_bounds__(kThreads) void norm_resident_kernel(NormArgs a) {
     }
 }
 
+// NORM of rows of ne0 <= 256 Q, a multiple of 4, rows 16-byte aligned: one
+// wave per row, Q float4 a lane (lane + 64 u), x read once; the same
+// statistics as norm_kernel (sums in double, whose order moves no float
+// result).  A chain step whose operand runs along the row with stride 1 and
+// 16-byte aligned rows loads it a float4 at a time.
+template <int Q>
+__global__ __launch_bounds__(kThreads) void norm_rows4_kernel(NormArgs a) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= a.rows) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t i1 = row % a.ne1;
+    const int64_t i2 = (row / a.ne1) % a.ne2;
+    const int64_t i3 = row / (a.ne1 * a.ne2);
+    const float4v *x = reinterpret_cast<const float4v *>(a.x + i1 * a.xnb1 + i2 * a.xnb2 + i3 * a.xnb3);
+    float4v *y = reinterpret_cast<float4v *>(a.y + i1 * a.ynb1 + i2 * a.ynb2 + i3 * a.ynb3);
+    const int n4 = static_cast<int>(a.ne0 / 4);
+    float v[Q][4];
+#pragma unroll
+    for (int u = 0; u < Q; ++u) {
+        const int j = lane + 64 * u;
+        const float4v q4 = x[j < n4 ? j : n4 - 1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[u][k] = q4[k];
+    }
+    // Step st_i's operand where it lies along the row (the first two steps'
+    // loaded with x's, before the statistics wait for it).
+    const auto operand = [&](int st_i, float (&o)[Q][4]) {
+        const DevStep &st = a.chain.steps[st_i];
+        const float *base = st.operand + i1 * st.nb[1] + i2 * st.nb[2] + i3 * st.nb[3];
+        const bool vec = st.nb[0] == 1 && (reinterpret_cast<uintptr_t>(base) & 15) == 0;
+#pragma unroll
+        for (int u = 0; u < Q; ++u) {
+            const int j = lane + 64 * u;
+            const int64_t e = 4 * static_cast<int64_t>(j < n4 ? j : n4 - 1);
+            if (vec) {
+                const float4v o4 = *reinterpret_cast<const float4v *>(base + e);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[u][k] = o4[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[u][k] = base[(e + k) * st.nb[0]];
+            }
+        }
+    };
+    constexpr int kEarly = 2;
+    float early[kEarly][Q][4];
+#pragma unroll
+    for (int st_i = 0; st_i < kEarly; ++st_i)
+        if (st_i < a.chain.count && a.chain.steps[st_i].kind != 2) operand(st_i, early[st_i]);
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < Q; ++u)
+        if (lane + 64 * u < n4)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) s += static_cast<double>(v[u][k]);
+    const float mean = static_cast<float>(wave_sum(s) / static_cast<double>(a.ne0));
+    double q = 0.0;
+#pragma unroll
+    for (int u = 0; u < Q; ++u) {
+        if (lane + 64 * u >= n4) continue;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float d = v[u][k] - mean;
+            q += static_cast<double>(__fmul_rn(d, d));
+        }
+    }
+    const float variance = static_cast<float>(wave_sum(q) / static_cast<double>(a.ne0));
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
+#pragma unroll
+    for (int u = 0; u < Q; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[u][k] = __fmul_rn(v[u][k] - mean, scale);
+#pragma unroll 1
+    for (int st_i = 0; st_i < a.chain.count; ++st_i) {
+        const DevStep &st = a.chain.steps[st_i];
+        if (st.kind == 2) {
+#pragma unroll
+            for (int u = 0; u < Q; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[u][k] = silu(v[u][k]);
+            continue;
+        }
+        float o[Q][4];
+        if (st_i == 0) {
+#pragma unroll
+            for (int u = 0; u < Q; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[u][k] = early[0][u][k];
+        } else if (st_i == 1) {
+#pragma unroll
+            for (int u = 0; u < Q; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[u][k] = early[1][u][k];
+        } else {
+            operand(st_i, o);
+        }
+#pragma unroll
+        for (int u = 0; u < Q; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                v[u][k] = st.kind == 0 ? __fadd_rn(v[u][k], o[u][k]) : __fmul_rn(v[u][k], o[u][k]);
+    }
+#pragma unroll
+    for (int u = 0; u < Q; ++u) {
+        const int j = lane + 64 * u;
+        if (j < n4) y[j] = float4v{v[u][0], v[u][1], v[u][2], v[u][3]};
+    }
+}
+
 // One wave per row of ne0.
 __global__ __launch_bounds__(kThreads) void norm_kernel(NormArgs a) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
@@ -454,7 +563,19 @@ sdhip_status static_scratch(int device, double *&ptr) {
 hipError_t launch_norm(const NormArgs &a, hipStream_t stream) {
     KernelScope scope("norm", stream);
     const dim3 grid(static_cast<uint32_t>(ceil_div(a.rows, kThreads / 64)));
-    if (a.ne0 <= 64 * 8) {
+    const bool rows4 = a.ne0 >= 4 && a.ne0 % 4 == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.xnb1 % 4 == 0 && a.xnb2 % 4 == 0 &&
+                       a.xnb3 % 4 == 0 && a.ynb1 % 4 == 0 && a.ynb2 % 4 == 0 && a.ynb3 % 4 == 0;
+    const int64_t quads = ceil_div(a.ne0, 256);
+    if (rows4 && quads <= 2) {
+        SDHIP_LAUNCH(norm_rows4_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+    } else if (rows4 && quads <= 3) {
+        SDHIP_LAUNCH(norm_rows4_kernel<3>, grid, dim3(kThreads), 0, stream, a);
+    } else if (rows4 && quads <= 5) {
+        SDHIP_LAUNCH(norm_rows4_kernel<5>, grid, dim3(kThreads), 0, stream, a);
+    } else if (rows4 && quads <= 8) {
+        SDHIP_LAUNCH(norm_rows4_kernel<8>, grid, dim3(kThreads), 0, stream, a);
+    } else if (a.ne0 <= 64 * 8) {
         SDHIP_LAUNCH(norm_resident_kernel<8>, grid, dim3(kThreads), 0, stream, a);
     } else if (a.ne0 <= 64 * 16) {
         SDHIP_LAUNCH(norm_resident_kernel<16>, grid, dim3(kThreads), 0, stream, a);

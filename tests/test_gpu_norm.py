@@ -90,3 +90,34 @@ def test_norm(gpu, shape):
     diff = np.abs(got - want).max() / np.abs(want).max()
     print(f"norm {shape}: {diff:.3g} of the largest")
     assert diff <= CLOSE
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,view", [((2, 50, 4), False), ((1, 7, 2048), False), ((1, 9, 2052), False),
+                                        ((2, 300, 640), True), ((3, 33, 1280), True), ((2, 64, 320), False)],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_norm_rows_and_operands(gpu, shape, view):
+    """NORM over rows of 4 .. 2048 numbers a float4 at a time (2052: the
+    general form), the input a view whose rows lie further apart where
+    `view`; the chain a per-column scale, a residual of the output's shape
+    starting one number past a 16-byte boundary (read a number at a time), a
+    per-row scale (broadcast along the row) and the SiLU."""
+    r = rng(sum(shape) + view)
+    n = shape[-1]
+    full = uniform(r, shape[:-1] + (n + 8,), 3.0)
+    x = np.ascontiguousarray(full[..., :n])
+    gamma = normal(r, (n,), 1.0, 0.1)
+    res_full = uniform(r, shape[:-1] + (n + 4,), 1.0)
+    res = np.ascontiguousarray(res_full[..., 1:n + 1])
+    per_row = normal(r, shape[:-1] + (1,), 1.0, 0.5)
+    x_d = dev(full, gpu)[..., :n] if view else dev(x, gpu)
+    g_d, pr_d = dev(gamma, gpu), dev(per_row, gpu)
+    r_d = dev(res_full, gpu)[..., 1:n + 1]
+    y = unwritten(shape, gpu)
+    sdhip.norm(x_d, y, 1e-5, sdhip.epilogue([("mul", g_d), ("add", r_d), ("mul", pr_d), ("silu", None)]))
+    torch.cuda.synchronize()
+    want = orc.silu((orc.norm(x, 1e-5) * gamma + res) * per_row)
+    got = y.cpu().numpy()
+    diff = np.abs(got - want).max() / np.abs(want).max()
+    print(f"norm {shape} view={view}: {diff:.3g} of the largest")
+    assert diff <= CLOSE
