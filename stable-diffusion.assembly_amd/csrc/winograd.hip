@@ -929,10 +929,55 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
 //   outputs:  the splits added in their order (outputs_kernel).
 constexpr int kSmallTilesMax = 32;
 
+typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+
+// The blocks from `iblocks` on take the weights' exponents instead, a wave
+// per (split, output channel): a_os = kTop - the exponent above the split's
+// greatest |weight| of channel o times the weight transform's gain (0 for a
+// channel of zeros), read as the 16-byte pieces of its 9 split_len
+// consecutive FP16 numbers, whose magnitudes compare as their bits, two to
+// a register.
+template <int M>
+__device__ __forceinline__ void weights_split_max(const WinogradArgs &a, int64_t split_len, int64_t item,
+                                                  int32_t *__restrict__ ao) {
+    const int lane = threadIdx.x & 63;
+    const int64_t sp = item / a.oc, o = item - sp * a.oc;
+    const int64_t c_begin = sp * split_len;
+    const int64_t c_end = c_begin + split_len < a.ic ? c_begin + split_len : a.ic;
+    ushort2v big = {0, 0};
+    if (c_begin < c_end) {
+        // (o ic + c_begin) is a multiple of 8: the run starts 16-byte aligned
+        // and is whole pieces of 8 numbers.
+        const int4v *run = reinterpret_cast<const int4v *>(a.w + (o * a.ic + c_begin) * 9);
+        const int64_t pieces = (c_end - c_begin) * 9 / 8;
+        for (int64_t q = lane; q < pieces; q += 64) {
+            const int4v w = run[q];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                big = __builtin_elementwise_max(big, __builtin_bit_cast(ushort2v, w[k] & 0x7fff7fff));
+        }
+    }
+    int bits = big.x > big.y ? big.x : big.y;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) bits = max(bits, __shfl_xor(bits, off, 64));
+    if (lane == 0) {
+        const float wm = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(bits)));
+        ao[item] = wm > 0.0f ? kTop - exponent_above(wm * Mat<M>::kWeightGain) : 0;
+    }
+}
+
 template <int M>
 __global__ __launch_bounds__(256) void inputs_small_kernel(WinogradArgs a, int64_t kp, int64_t tp,
-                                                           const int32_t *__restrict__ e, _Float16 *__restrict__ v) {
+                                                           const int32_t *__restrict__ e, _Float16 *__restrict__ v,
+                                                           int64_t iblocks, int64_t split_len, int64_t splits,
+                                                           int32_t *__restrict__ ao) {
     constexpr int A = Mat<M>::A;
+    if (blockIdx.x >= iblocks) {
+        const int64_t item = (static_cast<int64_t>(blockIdx.x) - iblocks) * 4 + (threadIdx.x >> 6);
+        if (item < splits * a.oc) weights_split_max<M>(a, split_len, item, ao);
+        return;
+    }
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= tp * kp) return;
     const int64_t tile = idx / kp, c = idx - tile * kp;
@@ -961,18 +1006,15 @@ __global__ __launch_bounds__(256) void inputs_small_kernel(WinogradArgs a, int64
         }
 }
 
-typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
-typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
-
 template <int M, int NT>
 __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(WinogradArgs a, int64_t kp, int64_t split_len,
                                                                         int64_t oc_blocks, const int32_t *__restrict__ e,
                                                                         const _Float16 *__restrict__ v,
                                                                         float *__restrict__ prod,
-                                                                        int32_t *__restrict__ shift) {
+                                                                        int32_t *__restrict__ shift,
+                                                                        const int32_t *__restrict__ ao_split) {
     constexpr int A = Mat<M>::A;
     constexpr int TP = 16 * NT;  // tiles, padded
-    __shared__ float greatest[A][16];
     const int lane = threadIdx.x & 63;
     const int row = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, kg = lane >> 4;
@@ -995,43 +1037,8 @@ __global__ __launch_bounds__(64 * Mat<M>::A) void products_small_kernel(Winograd
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) emax = max(emax, __shfl_xor(emax, off, 64));
 
-    // Kernels (og, c .. c + 7): 144 consecutive bytes.  Past IC, the last
-    // eight instead, finite numbers that meet V's zeros there.
-    const auto load_g = [&](int64_t c, int4v(&q)[9]) {
-        const int64_t cc = c < a.ic ? c : a.ic - 8;
-        const int4v *p = reinterpret_cast<const int4v *>(a.w + (og * a.ic + cc) * 9);
-#pragma unroll
-        for (int k = 0; k < 9; ++k) q[k] = p[k];
-    };
-
-    // The split's greatest |weight| of channel o: FP16 magnitudes compare as
-    // their bits, two to a register.
-    {
-        ushort2v big = {0, 0};
-        for (int64_t c0 = c_begin + 32 * row; c0 < c_end; c0 += 32 * A) {
-            const int64_t c = c0 + 8 * kg;
-            if (o_in && c < a.ic) {
-                int4v q[9];
-                load_g(c, q);
-#pragma unroll
-                for (int k = 0; k < 9; ++k)
-#pragma unroll
-                    for (int w = 0; w < 4; ++w)
-                        big = __builtin_elementwise_max(big, __builtin_bit_cast(ushort2v, q[k][w] & 0x7fff7fff));
-            }
-        }
-        int bits = big.x > big.y ? big.x : big.y;
-        bits = max(bits, __shfl_xor(bits, 16, 64));
-        bits = max(bits, __shfl_xor(bits, 32, 64));
-        if (kg == 0) {
-            greatest[row][lr] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(bits)));
-        }
-    }
-    __syncthreads();
-    float wm = 0.0f;
-#pragma unroll
-    for (int r = 0; r < A; ++r) wm = fmaxf(wm, greatest[r][lr]);
-    const int ao = wm > 0.0f ? kTop - exponent_above(wm * Mat<M>::kWeightGain) : 0;
+    // The split's exponent of channel o (taken with the inputs' transform).
+    const int ao = ao_split[sp * a.oc + og];
     if (row == 0 && kg == 0 && o_in) shift[sp * a.oc + o] = emax - ao;
 
     // The kernels of a step, 16 output channels by 32 input channels, copied
@@ -1223,7 +1230,7 @@ WorkLayout work_layout(const WinogradArgs &a) {
         l.split_len = round_up(ceil_div(l.kp, sp), 32);
         l.splits = ceil_div(l.kp, l.split_len);
         l.e = take(a.ic * 4);
-        l.a = take(a.oc * 4);
+        l.a = take(l.splits * a.oc * 4);
         l.shift = take(l.splits * a.oc * 4);
         l.u = at;
         l.v = take(alpha2 * 2 * l.tp * l.kp * 2);
@@ -1296,9 +1303,13 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
         }
         _Float16 *vh = reinterpret_cast<_Float16 *>(v);
         {
+            // The inputs' transform, and beside it each split's exponents of
+            // the weights into a_oc ([split][oc]).
             KernelScope scope(names[2].c_str(), stream);
-            SDHIP_LAUNCH((inputs_small_kernel<M>), dim3(static_cast<uint32_t>(ceil_div(l.tp * l.kp, 256))),
-                         dim3(256), 0, stream, a, l.kp, l.tp, e, vh);
+            const int64_t iblocks = ceil_div(l.tp * l.kp, 256);
+            const int64_t wblocks = ceil_div(l.splits * a.oc, 4);
+            SDHIP_LAUNCH((inputs_small_kernel<M>), dim3(static_cast<uint32_t>(iblocks + wblocks)), dim3(256), 0,
+                         stream, a, l.kp, l.tp, e, vh, iblocks, l.split_len, l.splits, a_oc);
         }
         {
             KernelScope scope(names[3].c_str(), stream);
@@ -1307,10 +1318,10 @@ sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
             const dim3 block(64 * A);
             if (l.tp <= 16) {
                 SDHIP_LAUNCH((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.split_len,
-                             oc_blocks, e, vh, m, shift);
+                             oc_blocks, e, vh, m, shift, a_oc);
             } else {
                 SDHIP_LAUNCH((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.split_len,
-                             oc_blocks, e, vh, m, shift);
+                             oc_blocks, e, vh, m, shift, a_oc);
             }
         }
         KernelScope scope(names[4].c_str(), stream);
