@@ -913,11 +913,12 @@ __global__ __launch_bounds__(256) void outputs_kernel(WinogradArgs a, const floa
 // FP16 kernels, straight into the MFMA's operands.
 //
 //   inputs:   V[xi][part][c / 32][tile][c % 32] * 2^-e_c as two FP16 planes,
-//             tiles padded to tp (16 or 32) with zeros;
+//             tiles padded to tp (16 or 32) with zeros; beside it, in the
+//             same launch, each split's exponent a_os of every output
+//             channel from its greatest weight (a wave a pair);
 //   products: a block of A waves per (16 output channels, split of the input
 //             channels), wave i taking row i of U, so that each kernel is read
-//             once (and once more, from the caches, for the split's greatest
-//             weight, the waves taking its steps in turn).  A step is 32 input
+//             once.  A step is 32 input
 //             channels, eight a lane: the lane makes row i of G g of each of
 //             its kernels, scaled by 2^(a_os + e_c - E) -- a_os from the
 //             split's greatest weight of the output channel, as a_o from the
