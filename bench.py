@@ -761,7 +761,13 @@ def unet_step_line(dev, args):
 #   cfg1  Y = X W^T + b, X 2x4096x320 f32, W 320x320 f16: X 10.49 MB + W 0.20 +
 #         b + Y 10.49 = 21.18 MB (AI 79: HBM-bound at the split-FP16 rate)
 #   cfg2  the 36 products of 320x320 by 512 tiles: 3.775 GFLOP (the F(4x4)
-#         direct-equivalent 15.10 GFLOP for the op)
+#         direct-equivalent 15.10 GFLOP for the op) over U and V read once as
+#         two FP16 planes (36 x 2 x 2 x (320 + 512) x 320 = 38.34 MB) and M
+#         written once in single precision (36 x 4 x 320 x 512 = 23.59 MB):
+#         AI 61 flop/B, below the ridge of the three-MFMA split (833 TF / 8
+#         TB/s = 104) and of the raw FP16 peak (312) -- HBM bounds it at this
+#         K, so the roofline takes the bytes; the MFMA view is reported beside
+#         them
 #   cfg3a F(2x2) of 8x8 maps: the products kernel reads the FP16 weights,
 #         1280x1280x9x2 = 29.49 MB (it makes U in registers)
 #   cfg3b 1x1 conv 2x640x1024 -> 1280: 3.355 GFLOP
@@ -771,8 +777,9 @@ def unet_step_line(dev, args):
 CONFIGS = {
     "cfg1_linear": dict(workload="cfg1", unit="TFLOP/s", kernels=("mul_mat",), bound="hbm", amount=21.18e6,
                         peak=PEAK_HBM),
-    "cfg2_winograd4": dict(workload="cfg2", unit="TFLOP/s", kernels=("winograd4.products",), bound="mfma",
-                           amount=2.0 * 36 * 320 * 320 * 512, peak=PEAK_FP16_MFMA, split=3),
+    "cfg2_winograd4": dict(workload="cfg2", unit="TFLOP/s", kernels=("winograd4.products",), bound="hbm",
+                           amount=36 * 2 * 2 * (320 + 512) * 320 + 36 * 4 * 320 * 512.0, peak=PEAK_HBM,
+                           flops=2.0 * 36 * 320 * 320 * 512, split=3),
     "cfg3a_winograd2_gn_silu": dict(workload="cfg3a", unit="TFLOP/s", kernels=("winograd2.products",), bound="hbm",
                                     amount=1280 * 1280 * 9 * 2.0, peak=PEAK_HBM),
     "cfg3b_pointwise_gn_silu": dict(workload="cfg3b", unit="TFLOP/s", kernels=("conv_direct_pointwise",),
@@ -800,7 +807,17 @@ def roofline(spec, kt, op_ms, work):
            "peak": spec["peak"], "unit": "GB/s" if hbm else ("TOPS" if spec["unit"] == "TOPS" else "TFLOP/s"),
            "frac": round(achieved / spec["peak"], 4), "kernel_us": round(ms * 1e3, 2),
            "amount": spec["amount"], "traffic": profiled_traffic(spec["workload"], spec["kernels"][0])}
-    if spec.get("split"):
+    if hbm and spec.get("flops"):
+        # The same kernel against the MFMA peak: its arithmetic intensity
+        # (algorithmic flops / bytes) below the ridge is why HBM bounds it.
+        tflops = spec["flops"] / ms / 1e9
+        out["mfma_view"] = {"achieved": round(tflops, 2), "peak": PEAK_FP16_MFMA, "unit": "TFLOP/s",
+                            "frac": round(tflops / PEAK_FP16_MFMA, 4),
+                            "effective_peak": round(PEAK_FP16_MFMA / spec["split"], 1),
+                            "frac_of_effective": round(tflops * spec["split"] / PEAK_FP16_MFMA, 4),
+                            "ai_flop_per_byte": round(spec["flops"] / spec["amount"], 1),
+                            "ridge_effective": round(PEAK_FP16_MFMA / spec["split"] / (PEAK_HBM / 1e3), 1)}
+    elif spec.get("split"):
         # Split-FP16: each product takes `split` FP16 MFMA products.
         out["effective_peak"] = round(spec["peak"] / spec["split"], 1)
         out["frac_of_effective"] = round(achieved * spec["split"] / spec["peak"], 4)
