@@ -496,9 +496,9 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
 // register staging), with the wave's own wait for its copies and a bare
 // s_barrier the only synchronisation.
 //
-// A workgroup of 4 waves (2 x 2) covers 64 TM rows of x (tokens) by 128 rows
-// of W (features; GATED: 64 features and their 64 gates, each wave's two
-// column tiles a pair).  A stage holds the step's rows of bytes of each
+// A workgroup of 4 waves (2 x 2) covers 64 TM rows of x (tokens) by 64 TJ rows
+// of W (features; GATED, TJ = 2: 64 features and their 64 gates, each wave's
+// two column tiles a pair).  A stage holds the step's rows of bytes of each
 // operand (the layouts are step-major, so each is contiguous), the row
 // scales and offsets of its group and the column scales, offsets and sums.
 // The 16-byte piece p of a row r lands at p ^ s(r), s(r) = ((r >> 1) ^
@@ -507,21 +507,20 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs p) {
 // a wave takes 32 bytes of its row at byte 32 (l / 32) of the step's 64, the
 // first 16 to the first MFMA and the rest to the second: A and B take the
 // same order of k, and integer sums do not depend on it.
-constexpr int kQWRows = 128;  // rows of W a workgroup
-
-template <int TM>
+template <int TM, int TJ>
 struct QStage {
     static constexpr int kXRows = 64 * TM;
+    static constexpr int kWRows = 64 * TJ;      // rows of W a workgroup
     static constexpr int kA = kXRows * 64;       // bytes of x a step
-    static constexpr int kB = kQWRows * 64;      // bytes of W a step
+    static constexpr int kB = kWRows * 64;       // bytes of W a step
     static constexpr int kSa = kA + kB;          // offsets of the scales
     static constexpr int kOa = kSa + kXRows * 4;
     static constexpr int kSb = kOa + kXRows * 4;
-    static constexpr int kOb = kSb + kQWRows * 4;
-    static constexpr int kQs = kOb + kQWRows * 4;
-    static constexpr int kBytes = kQs + kQWRows * 4;
+    static constexpr int kOb = kSb + kWRows * 4;
+    static constexpr int kQs = kOb + kWRows * 4;
+    static constexpr int kBytes = kQs + kWRows * 4;
     static constexpr int kUnits16 = (kA + kB) / 1024;                 // 1 KB copies
-    static constexpr int kUnits4 = (2 * kXRows + 3 * kQWRows) / 64;    // 256-byte copies
+    static constexpr int kUnits4 = (2 * kXRows + 3 * kWRows) / 64;     // 256-byte copies
     static constexpr int kC16 = kUnits16 / 4;                         // a wave's, a step
     static constexpr int kC4 = (kUnits4 + 3) / 4;
     static constexpr int kCopies = kC16 + kC4;
@@ -530,9 +529,10 @@ struct QStage {
 
 __device__ __forceinline__ int qswizzle(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
-template <bool GATED, int TM, int S>
+template <bool GATED, int TM, int S, int TJ>
 __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
-    using L = QStage<TM>;
+    static_assert(!GATED || TJ == 2, "the gated products pair two column tiles");
+    using L = QStage<TM, TJ>;
     constexpr int BM = L::kXRows;
     __shared__ __attribute__((aligned(1024))) char lds[S * L::kBytes];
 
@@ -550,7 +550,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     const int64_t mb = p.by_columns ? br : bq;
     const int64_t nb = p.by_columns ? bq : br;
     const int64_t m0 = mb * BM;
-    const int64_t n0 = nb * (GATED ? kQWRows / 2 : kQWRows);
+    const int64_t n0 = nb * (GATED ? 64 : L::kWRows);
     // The W row of block row r (clamped): GATED, rows 0..63 features n0 +
     // r and rows 64..127 their gates.
     const auto w_row = [&](int r) -> int64_t {
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
 
     // This wave's copies a step: 1 KB units wave + 4 q (x's rows first, 16
     // rows a unit, then W's), then 256-byte units wave + 4 q of the scales
-    // (sa, oa: TM units each, sb, ob, qs: two each, 64 rows a unit); waves
+    // (sa, oa: TM units each, sb, ob, qs: TJ each, 64 rows a unit); waves
     // past the last unit repeat it.  Per copy: the lane's source, advanced a
     // step (bytes) or a group (scales) at a time, and the unit's place in a
     // stage.
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     for (int q = 0; q < C4; ++q) {
         int u = wave + 4 * q;
         u = u < L::kUnits4 ? u : L::kUnits4 - 1;
-        // Units [0, TM): sa; [TM, 2 TM): oa; then sb, ob, qs two each.
+        // Units [0, TM): sa; [TM, 2 TM): oa; then sb, ob, qs TJ each.
         const char *base;
         int off;
         if (u < 2 * TM) {
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
             off = (u < TM ? L::kSa : L::kOa) + 256 * v;
             x4[q] = true;
         } else {
-            const int w = (u - 2 * TM) / 2, v = (u - 2 * TM) % 2, row = 64 * v + lane;
+            const int w = (u - 2 * TM) / TJ, v = (u - 2 * TM) % TJ, row = 64 * v + lane;
             base = w == 0   ? reinterpret_cast<const char *>(p.ws + w_row(row))
                    : w == 1 ? reinterpret_cast<const char *>(p.wo + w_row(row))
                             : reinterpret_cast<const char *>(p.wsum + w_row(row));
@@ -637,12 +637,12 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
 
     // The outputs: tile (i, j) of the wave, lane column r32, rows
     // 8 (e / 4) + 4 h + e % 4.
-    float t[TM][2][16];
+    float t[TM][TJ][16];
     const auto out_row = [&](int i, int e) -> int64_t { return m0 + wr * 32 * TM + 32 * i + 4 * h + tile_row(e); };
-    const auto out_col = [&](int j) -> int64_t { return n0 + 64 * wc + 32 * j + r32; };
+    const auto out_col = [&](int j) -> int64_t { return n0 + 32 * TJ * wc + 32 * j + r32; };
     if (!GATED && p.from_redirect) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             const int64_t n = out_col(j);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -656,15 +656,15 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TJ; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) t[i][j][e] = 0.0f;
     }
 
     // Fragment reads: A tile i at block row wr 32 TM + 32 i + r32, B tile j
-    // at block row (GATED: j 64 + wc 32 + r32; else wc 64 + 32 j + r32), the
-    // two 16-byte pieces 2 h and 2 h + 1 at their swizzled places.
-    int aread[TM][2], bread[2][2], brow[2];
+    // at block row (GATED: j 64 + wc 32 + r32; else wc 32 TJ + 32 j + r32),
+    // the two 16-byte pieces 2 h and 2 h + 1 at their swizzled places.
+    int aread[TM][2], bread[TJ][2], brow[TJ];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int row = wr * 32 * TM + 32 * i + r32;
@@ -672,23 +672,23 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
         for (int q = 0; q < 2; ++q) aread[i][q] = row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = GATED ? 64 * j + 32 * wc + r32 : 64 * wc + 32 * j + r32;
+    for (int j = 0; j < TJ; ++j) {
+        const int row = GATED ? 64 * j + 32 * wc + r32 : 32 * TJ * wc + 32 * j + r32;
         brow[j] = row;
 #pragma unroll
         for (int q = 0; q < 2; ++q) bread[j][q] = L::kA + row * 64 + (((2 * h + q) ^ qswizzle(row)) << 4);
     }
 
-    int16v acc[TM][2];
+    int16v acc[TM][TJ];
     const auto compute = [&](int stage, int sub) {
         const char *base = lds + stage * L::kBytes;
-        int4v a[TM][2], bv[2][2];
+        int4v a[TM][2], bv[TJ][2];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int q = 0; q < 2; ++q) a[i][q] = *reinterpret_cast<const int4v *>(base + aread[i][q]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int q = 0; q < 2; ++q) bv[j][q] = *reinterpret_cast<const int4v *>(base + bread[j][q]);
         // A group's first step starts its sums from zero (a branch uniform
@@ -697,19 +697,19 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][0], bv[j][0], int16v{}, 0, 0, 0);
         } else {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][0], bv[j][0], acc[i][j], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][1], bv[j][1], acc[i][j], 0, 0, 0);
         if (sub != subs - 1) return;
         // The group's sums into the outputs, as quant.cc:150-155 does:
@@ -720,7 +720,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
         const float *ob = reinterpret_cast<const float *>(base + L::kOb);
         const int32_t *qs = reinterpret_cast<const int32_t *>(base + L::kQs);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             const float cs = sb[brow[j]], nco = -ob[brow[j]];
             const int32_t shift = 128 * qs[brow[j]];
 #pragma unroll
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
     // compiler need not wait for the copies to know t is there.
     wait_loads<0>();
     static_assert((S & (S - 1)) == 0, "stages a power of two");
-    constexpr int kBehind = (S - 2) * QStage<TM>::kCopies;  // a wave's copies behind a step's
+    constexpr int kBehind = (S - 2) * L::kCopies;  // a wave's copies behind a step's
 #pragma unroll
     for (int q = 0; q < S - 1; ++q) copy_step(q);
     int sub = 0;
@@ -795,7 +795,7 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < TJ; ++j) {
                 const int64_t n = out_col(j);
                 const int64_t nc = n < p.N ? n : p.N - 1;
                 apply_chain_block(p.chain, t[i][j], [&](int s, int e) {
@@ -813,11 +813,12 @@ __global__ __launch_bounds__(256) void qgemm3_kernel(QgemmArgs p) {
 }
 
 constexpr int kQStages = 4;
-static_assert(2 * kQStages * QStage<2>::kBytes <= 160 * 1024, "two workgroups' rings fit a CU's LDS");
-static_assert((kQStages - 2) * QStage<2>::kCopies < 64, "vmcnt");
+static_assert(2 * kQStages * QStage<2, 2>::kBytes <= 160 * 1024, "two workgroups' rings fit a CU's LDS");
+static_assert((kQStages - 2) * QStage<2, 2>::kCopies < 64, "vmcnt");
 
-// Workgroups of 128 rows of x where the launch still gives every SIMD two
-// waves, else 64.
+// Workgroups of 128 rows of x by 128 of W where the launch still gives every
+// SIMD two waves, else 64 by 128, else (not gated) 64 by 64: the block's
+// products and sums are the same whatever its shape.
 // The workgroups go along the rows of x within a column block of W where x
 // is the smaller operand (the gated FF-in's 1976 x 1280 bytes of x against
 // 10240 x 1280 of W): each XCD then reads W's column blocks once and holds
@@ -826,17 +827,23 @@ static_assert((kQStages - 2) * QStage<2>::kCopies < 64, "vmcnt");
 template <bool GATED>
 hipError_t launch_qgemm2(QgemmArgs p, hipStream_t stream) {
     const int64_t cols = GATED ? p.half : p.N;
-    p.col_blocks = ceil_div(cols, GATED ? kQWRows / 2 : kQWRows);
     p.by_columns = p.M < (GATED ? 2 * p.half : p.N) ? 1 : 0;
-    const int64_t blocks128 = ceil_div(p.M, 128) * p.col_blocks;
-    if (blocks128 >= 512) {
+    const int64_t cols128 = ceil_div(cols, GATED ? 64 : 128);
+    if (ceil_div(p.M, 128) * cols128 >= 512) {
+        p.col_blocks = cols128;
         p.row_blocks = ceil_div(p.M, 128);
-        SDHIP_LAUNCH((qgemm3_kernel<GATED, 2, kQStages>), dim3(static_cast<uint32_t>(blocks128)), dim3(256), 0,
-                     stream, p);
-    } else {
+        SDHIP_LAUNCH((qgemm3_kernel<GATED, 2, kQStages, 2>), dim3(static_cast<uint32_t>(p.row_blocks * p.col_blocks)),
+                     dim3(256), 0, stream, p);
+    } else if (GATED || ceil_div(p.M, 64) * cols128 >= 512) {
+        p.col_blocks = cols128;
         p.row_blocks = ceil_div(p.M, 64);
-        const dim3 grid(static_cast<uint32_t>(p.row_blocks * p.col_blocks));
-        SDHIP_LAUNCH((qgemm3_kernel<GATED, 1, kQStages>), grid, dim3(256), 0, stream, p);
+        SDHIP_LAUNCH((qgemm3_kernel<GATED, 1, kQStages, 2>), dim3(static_cast<uint32_t>(p.row_blocks * p.col_blocks)),
+                     dim3(256), 0, stream, p);
+    } else {
+        p.col_blocks = ceil_div(cols, 64);
+        p.row_blocks = ceil_div(p.M, 64);
+        SDHIP_LAUNCH((qgemm3_kernel<false, 1, kQStages, 1>), dim3(static_cast<uint32_t>(p.row_blocks * p.col_blocks)),
+                     dim3(256), 0, stream, p);
     }
     return hipGetLastError();
 }
