@@ -120,6 +120,10 @@ __global__ __launch_bounds__(kThreads) void group_sums_kernel(GroupNormArgs a) {
 // The output of the block's slice, (x - mean) * scale and the chain, four
 // consecutive numbers of a thread at a time where the planes allow (the four
 // then share their channel); all loads of a step before its stores.
+// The most channels a slice's operands of one number a channel are held
+// for in LDS.
+constexpr int kApplyChannels = 256;
+
 __global__ __launch_bounds__(kThreads) void group_apply_kernel(GroupNormArgs a) {
     __shared__ float shared[2];
     const GroupView g = group_view(a);
@@ -151,6 +155,56 @@ __global__ __launch_bounds__(kThreads) void group_apply_kernel(GroupNormArgs a) 
     };
     const bool quads = plane % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    // Operands of one number a channel, for the channels of the slice (few
+    // enough): loaded once into LDS, and the slice's quads four a thread at a
+    // time, all four loads issued before any is used -- no global load waits
+    // on another inside the loop.
+    __shared__ float chan_ops[kMaxSteps][kApplyChannels];
+    const int64_t c_first = g.e0 / plane;
+    const int64_t nch = g.e1 > g.e0 ? (g.e1 - 1) / plane - c_first + 1 : 0;
+    if (quads && per_channel && nch <= kApplyChannels) {
+        for (int s = 0; s < a.chain.count; ++s) {
+            const DevStep &st = a.chain.steps[s];
+            if (st.kind == 2) continue;
+            for (int64_t ch = tid; ch < nch; ch += kThreads) chan_ops[s][ch] = st.operand[offset(st, c_first + ch, 0)];
+        }
+        __syncthreads();
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        float4 *y4 = reinterpret_cast<float4 *>(y);
+        const int64_t q_end = g.e1 / 4;
+        constexpr int kBatch = 4;
+        for (int64_t q0 = g.e0 / 4 + tid; q0 < q_end; q0 += kBatch * kThreads) {
+            float4 q[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int64_t i = q0 + u * kThreads;
+                q[u] = x4[i < q_end ? i : q0];
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int64_t i = q0 + u * kThreads;
+                if (i >= q_end) continue;
+                const int64_t ch = static_cast<int64_t>(static_cast<uint32_t>(4 * i) / static_cast<uint32_t>(plane)) -
+                                   c_first;
+                float v[4] = {__fmul_rn(q[u].x - mean, scale), __fmul_rn(q[u].y - mean, scale),
+                              __fmul_rn(q[u].z - mean, scale), __fmul_rn(q[u].w - mean, scale)};
+#pragma unroll 1
+                for (int s = 0; s < a.chain.count; ++s) {
+                    const int kind = a.chain.steps[s].kind;
+                    if (kind == 2) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) v[k] = silu(v[k]);
+                        continue;
+                    }
+                    const float b = chan_ops[s][ch];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) v[k] = kind == 0 ? __fadd_rn(v[k], b) : __fmul_rn(v[k], b);
+                }
+                y4[i] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        return;
+    }
     if (quads) {
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
         float4 *y4 = reinterpret_cast<float4 *>(y);
