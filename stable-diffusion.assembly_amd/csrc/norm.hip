@@ -117,13 +117,13 @@ __global__ __launch_bounds__(kThreads) void group_sums_kernel(GroupNormArgs a) {
     if (tid == 0) a.partials[(PASS * a.ne3 * a.groups + g.item) * a.slices + g.slice] = sum;
 }
 
-// The output of the block's slice, (x - mean) * scale and the chain, four
-// consecutive numbers of a thread at a time where the planes allow (the four
-// then share their channel); all loads of a step before its stores.
 // The most channels a slice's operands of one number a channel are held
 // for in LDS.
 constexpr int kApplyChannels = 256;
 
+// The output of the block's slice, (x - mean) * scale and the chain, four
+// consecutive numbers of a thread at a time where the planes allow (the four
+// then share their channel); all loads of a step before its stores.
 __global__ __launch_bounds__(kThreads) void group_apply_kernel(GroupNormArgs a) {
     __shared__ float shared[2];
     const GroupView g = group_view(a);
