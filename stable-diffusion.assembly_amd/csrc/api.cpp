@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstdarg>
 #include <cstdint>
@@ -196,6 +197,18 @@ bool spans_overlap(const void *a, size_t an, const void *b, size_t bn) {
     const uintptr_t ea = an > UINTPTR_MAX - pa ? UINTPTR_MAX : pa + an;
     const uintptr_t eb = bn > UINTPTR_MAX - pb ? UINTPTR_MAX : pb + bn;
     return pa < eb && pb < ea;
+}
+
+int compute_units() {
+    constexpr int kDevices = 64;
+    static std::atomic<int> known[kDevices] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kDevices) return 256;
+    int n = known[device].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
+    known[device].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 // The chain for an output of extents `ne`: each operand F32, nb[0] = 4, and

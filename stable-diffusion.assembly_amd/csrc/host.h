@@ -104,6 +104,9 @@ size_t tensor_span(const sdhip_tensor *t);
 // Whether the bytes [a, a + an) and [b, b + bn) share any: the addresses
 // compared as integers, the ends saturating, nothing read.
 bool spans_overlap(const void *a, size_t an, const void *b, size_t bn);
+// The compute units of the current device (looked up once a device; 256,
+// MI355X's, where the runtime cannot say).
+int compute_units();
 // The address `bytes` past p as an integer (no pointer arithmetic on what
 // may be a null or foreign pointer).
 inline uintptr_t address_past(const void *p, int64_t bytes) {
