@@ -994,8 +994,17 @@ __device__ __forceinline__ void split_softmax(const float16v (&sh)[KT], const fl
     l += part;
 }
 
+// Partial results of the split form's key splits: per (b h, split, query)
+// the running maximum, the sum and the unnormalised output.
+struct KeyPartial {
+    float *m;   // [b h][split][lq]
+    double *l;  // [b h][split][lq]
+    float *o;   // [b h][split][lq][dv], 16-byte aligned
+};
+
 template <int D, int KB, int NS, int OCC, bool PIPE, bool LOCAL>
-__global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs a, const char *__restrict__ tiles) {
+__global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs a, const char *__restrict__ tiles,
+                                                                   int64_t splits, int64_t per, KeyPartial part) {
     using S = Split<D, KB>;
     static_assert(NS >= 3 && (NS - 2) * S::kPerWave < 64, "stages");
     static_assert(S::kQueries * D * 4 <= NS * S::kRecord, "the queries' staging fits the ring");
@@ -1008,15 +1017,22 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     const int lr = lane & 31;  // the lane's query, or its row of operand A
     const int g = lane >> 5;   // the lane's half of the wave
 
+    // With key splits (splits > 1) the workgroup takes tiles [t0, t0 +
+    // per) of the head's nk_all and writes partial results for
+    // split_combine_kernel; nk is then its own count of tiles.
     const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint32_t qb = b % static_cast<uint32_t>(a.qblocks);
-    const uint32_t bh = b / static_cast<uint32_t>(a.qblocks);
+    const uint32_t rest = b / static_cast<uint32_t>(a.qblocks);
+    const int64_t sp = static_cast<int64_t>(rest % static_cast<uint32_t>(splits));
+    const uint32_t bh = rest / static_cast<uint32_t>(splits);
     const int64_t hi = bh % a.h;
     const int64_t bi = bh / a.h;
     const int64_t kh = hi / (a.h / a.hk);
     const int64_t q0 = static_cast<int64_t>(qb) * S::kQueries + wave * 32;
-    const int64_t nk = (a.lk + KB - 1) / KB;
-    const char *head = tiles + (bi * a.hk + kh) * nk * S::kRecord;
+    const int64_t nk_all = (a.lk + KB - 1) / KB;
+    const int64_t t0 = sp * per;
+    const int64_t nk = t0 + per < nk_all ? per : nk_all - t0;
+    const char *head = tiles + ((bi * a.hk + kh) * nk_all + t0) * S::kRecord;
 
     // Tile `t` into LDS buffer `stage`: the wave's kPerWave copies of 1 KB
     // (those past the tile's last repeat it).
@@ -1296,7 +1312,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     }
     const auto last = [&](float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
         float p[S::kTiles][16];
-        const int valid = static_cast<int>(a.lk - (nk - 1) * KB);
+        const int valid = t0 + nk == nk_all ? static_cast<int>(a.lk - (nk_all - 1) * KB) : KB;
         if (valid < KB) {
             split_softmax<true, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, valid, g);
         } else {
@@ -1346,9 +1362,32 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // 4 g + e % 4][lr], and the values' 2^-4 comes back with the reciprocal.
     double sum = l;
     sum += __shfl_xor(sum, 32, 64);
-    const float reciprocal = static_cast<float>(1.0 / sum);
     const int64_t i = q0 + lr;
     if (i >= a.lq) return;
+    if (splits > 1) {
+        // The split's maximum (the same on the query's two lanes), sum and
+        // unnormalised output.
+        const int64_t at = (static_cast<int64_t>(bh) * splits + sp) * a.lq + i;
+        if (g == 0) {
+            part.m[at] = m;
+            part.l[at] = sum;
+        }
+        float *o = part.o + at * a.dv;
+#pragma unroll
+        for (int dt = 0; dt < S::kDvt; ++dt)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int dim = 32 * dt + 8 * e4 + 4 * g;
+                if (dim < D) {
+                    float4v r;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) r[u] = (oh[dt][4 * e4 + u] + ol[dt][4 * e4 + u] * kPartDown) * 16.0f;
+                    *reinterpret_cast<float4v *>(o + dim) = r;
+                }
+            }
+        return;
+    }
+    const float reciprocal = static_cast<float>(1.0 / sum);
     float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
 #pragma unroll
     for (int dt = 0; dt < S::kDvt; ++dt)
@@ -1366,6 +1405,37 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         }
 }
 
+// The key splits of the split form merged, query by query: each split's sum
+// and output rescaled by 2^(256 (its maximum - the greatest)), as
+// split_softmax rescales its running ones, the sum in double, the output
+// times the reciprocal of the sum rounded to single precision.  A wave per
+// query.
+__global__ __launch_bounds__(256) void split_combine_kernel(AttentionArgs a, int64_t splits, KeyPartial part) {
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // (b h) lq + i
+    const int lane = threadIdx.x & 63;
+    if (item >= a.b * a.h * a.lq) return;
+    const int64_t bh = item / a.lq, i = item - bh * a.lq;
+    const int64_t hi = bh % a.h, bi = bh / a.h;
+    const int64_t first = bh * splits * a.lq + i;  // split 0 of the query
+    float mx = -INFINITY;
+    for (int64_t sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part.m[first + sp * a.lq]);
+    double l = 0.0;
+    for (int64_t sp = 0; sp < splits; ++sp) {
+        const float w = __builtin_amdgcn_exp2f((part.m[first + sp * a.lq] - mx) * 256.0f);
+        l += part.l[first + sp * a.lq] * static_cast<double>(w);
+    }
+    const float reciprocal = static_cast<float>(1.0 / l);
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
+    for (int64_t e = lane; e < a.dv; e += 64) {
+        float acc = 0.0f;
+        for (int64_t sp = 0; sp < splits; ++sp) {
+            const float w = __builtin_amdgcn_exp2f((part.m[first + sp * a.lq] - mx) * 256.0f);
+            acc = fmaf(part.o[(first + sp * a.lq) * a.dv + e], w, acc);
+        }
+        out[e] = acc * reciprocal;
+    }
+}
+
 // The split form's shape for head size D: its tiles' keys, the stages of its
 // ring, the workgroups a CU holds at least.
 template <int D>
@@ -1376,14 +1446,59 @@ struct SplitShape {
     static constexpr bool kPipe = D <= 64;  // registers for two sets of scores
 };
 
+// Splits of the keys where the split form's workgroups would leave CUs idle
+// (the UNet's 32 x 32 and 16 x 16 maps): as many, of two tiles or more, as
+// fill one round of one workgroup a CU; the tiles a split takes.
+struct KeySplits {
+    int64_t splits, per;
+};
+
 template <int D>
-size_t split_work(const AttentionArgs &a) {
+KeySplits key_splits(const AttentionArgs &a) {
+    using SH = SplitShape<D>;
+    using S = Split<D, SH::kKeys>;
+    const int64_t nk = ceil_div(a.lk, SH::kKeys);
+    const int64_t blocks = ceil_div(a.lq, S::kQueries) * a.h * a.b;
+    int64_t sp = 1;
+    if (nk >= SH::kStages && blocks > 0 && blocks < compute_units()) {  // the tiles' launch (not LOCAL)
+        sp = compute_units() / blocks;
+        sp = sp < nk / 2 ? sp : nk / 2;
+        sp = sp < 1 ? 1 : sp;
+    }
+    const int64_t per = ceil_div(nk, sp);
+    return {ceil_div(nk, per), per};
+}
+
+// The partial results' layout in the work buffer from `at` on, and its bytes.
+struct KeyPartialLayout {
+    size_t l, m, o, bytes;
+};
+
+inline KeyPartialLayout key_partial_layout(const AttentionArgs &a, int64_t splits) {
+    const size_t n = static_cast<size_t>(a.b * a.h * splits * a.lq);
+    KeyPartialLayout k{};
+    k.l = 0;
+    k.m = n * 8;
+    k.o = static_cast<size_t>(round_up(static_cast<int64_t>(n * 12), 256));
+    k.bytes = k.o + n * static_cast<size_t>(a.dv) * 4;
+    return k;
+}
+
+template <int D>
+size_t split_tiles_bytes(const AttentionArgs &a) {
     using S = Split<D, SplitShape<D>::kKeys>;
     return static_cast<size_t>(a.b * a.hk) * static_cast<size_t>(ceil_div(a.lk, SplitShape<D>::kKeys)) * S::kRecord;
 }
 
+template <int D>
+size_t split_work(const AttentionArgs &a) {
+    const KeySplits ks = key_splits<D>(a);
+    const size_t tiles = split_tiles_bytes<D>(a);
+    return ks.splits > 1 ? tiles + key_partial_layout(a, ks.splits).bytes : tiles;
+}
+
 template <int D, bool LOCAL>
-hipError_t launch_split_t(AttentionArgs a, const void *work, hipStream_t stream) {
+hipError_t launch_split_t(AttentionArgs a, void *work, hipStream_t stream) {
     using SH = SplitShape<D>;
     using S = Split<D, SH::kKeys>;
     a.qblocks = ceil_div(a.lq, S::kQueries);
@@ -1392,10 +1507,24 @@ hipError_t launch_split_t(AttentionArgs a, const void *work, hipStream_t stream)
         reinterpret_cast<const void *>(&attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe, LOCAL>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (attr != hipSuccess) return attr;
-    dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b)), block(256);
+    const int64_t nk = ceil_div(a.lk, SH::kKeys);
+    const KeySplits ks = LOCAL ? KeySplits{1, nk} : key_splits<D>(a);
+    KeyPartial part{};
+    if (ks.splits > 1) {
+        char *base = static_cast<char *>(work) + split_tiles_bytes<D>(a);
+        const KeyPartialLayout k = key_partial_layout(a, ks.splits);
+        part.l = reinterpret_cast<double *>(base + k.l);
+        part.m = reinterpret_cast<float *>(base + k.m);
+        part.o = reinterpret_cast<float *>(base + k.o);
+    }
+    dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b * ks.splits)), block(256);
     KernelScope scope("attention", stream);
     SDHIP_LAUNCH((attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe, LOCAL>), grid, block, lds,
-                 stream, a, static_cast<const char *>(work));
+                 stream, a, static_cast<const char *>(work), ks.splits, ks.per, part);
+    if (ks.splits > 1) {
+        SDHIP_LAUNCH(split_combine_kernel, dim3(static_cast<uint32_t>(ceil_div(a.b * a.h * a.lq, 4))), block, 0,
+                     stream, a, ks.splits, part);
+    }
     return hipGetLastError();
 }
 

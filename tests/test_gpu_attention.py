@@ -185,3 +185,21 @@ def test_short_keys_in_the_workgroup(gpu, d, lq, lk, h, hk, b):
     err = orc.metric(y, exact, mag)
     print(f"attention d={d} lq={lq} lk={lk}: {err:.3g}")
     assert err <= BOUND
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [(80, 1024, 1024, 8, 8, 2), (160, 256, 256, 8, 8, 2), (80, 1000, 999, 8, 4, 1),
+                               (160, 130, 96, 2, 2, 1)], ids=lambda c: "x".join(map(str, c)))
+def test_attention_key_splits(gpu, c):
+    """Workgroups too few to fill the chip (the UNet's 32 x 32 and 16 x 16
+    self-attention, a ragged case with heads sharing keys, three tiles of
+    keys): the keys split across workgroups, each writing its running
+    maximum, sum and output, merged by split_combine_kernel -- held to the
+    bound against float64."""
+    d, lq, lk, h, hk, b = c
+    q, k, v, y, scale = attention_case(gpu, d, lq, lk, h, hk, b, False, seed=d + lq + lk)
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    print(f"attention key splits {c}: {err:.3g}")
+    assert np.isfinite(y).all()
+    assert err <= BOUND
