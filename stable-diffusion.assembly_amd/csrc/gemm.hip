@@ -1210,7 +1210,12 @@ ColumnsPlan columns_plan(const ConvArgs &c) {
 bool conv_columns_taken(const ConvArgs &c) {
     const bool pointwise = c.kw == 1 && c.kh == 1 && c.s0 == 1 && c.s1 == 1 && c.p0 == 0 && c.p1 == 0;
     const bool w_aligned = c.w_split || (c.ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) % 16) == 0);
-    return !pointwise && c.K % kBK == 0 && w_aligned &&
+    // 1x1 kernels too where their direct blocks would leave most CUs idle
+    // and K is long (the UNet's 16 x 16 and 8 x 8 levels): the split along K
+    // fills the chip, the columns then being x transposed.
+    const int64_t direct_blocks = ((c.oc + 63) / 64) * ((c.P + 63) / 64);
+    const bool split_pays = direct_blocks < 256 && c.K / kBK >= 16;
+    return (!pointwise || split_pays) && c.K % kBK == 0 && w_aligned &&
            c.P * c.K <= (int64_t{1} << 28) && c.P < (int64_t{1} << 31);
 }
 

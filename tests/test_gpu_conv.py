@@ -29,6 +29,8 @@ CASES = [
     (17, 13, 5, 7, 3, 3, 1, 1, 1, 1, 1, 1, 3),
     (32, 32, 64, 64, 3, 3, 2, 2, 1, 1, 1, 1, 2),   # the UNet's downsampling, fewer channels
     (20, 20, 16, 8, 3, 3, 1, 1, 2, 2, 2, 2, 1),    # 3x3 dilated: direct
+    (16, 16, 1280, 640, 1, 1, 1, 1, 0, 0, 1, 1, 2),  # 1x1 of few blocks and long K: split along K by columns
+    (8, 8, 2560, 1280, 1, 1, 1, 1, 0, 0, 1, 1, 1),   # the same at the UNet's 8 x 8, one image
 ]
 
 
