@@ -1134,15 +1134,16 @@ struct MulMatSplitPlan {
 };
 
 // Splits of K for about 512 blocks where the output has fewer than 256 of
-// 64 x 64, each of 32 K-steps or more (shorter ones cost more in partial sums
-// than their blocks gain: measured at 512 x 1280 x 1280, two splits of 20
-// steps 19.7 us against 17.3 in one pass); one where that leaves no room.
+// 64 x 64, each of 8 K-steps or more (measured at 512 x 1280 x 1280, the
+// UNet's deepest level: two splits of 20 steps 19.7 us against 17.3 in one
+// pass, while four of 10 took the UNet step 11.67 -> 11.61 ms); one where
+// that leaves no room.
 MulMatSplitPlan mul_mat_split_plan(const MulMatArgs &p) {
     MulMatSplitPlan l{};
     l.blocks = ((p.M + 63) / 64) * ((p.N + 63) / 64);
     const int64_t steps = p.K / kBK;
     int64_t sp = l.blocks < 256 ? (512 + l.blocks - 1) / l.blocks : 1;
-    const int64_t most = steps / 32 > 1 ? steps / 32 : 1;
+    const int64_t most = steps / 8 > 1 ? steps / 8 : 1;
     sp = sp < most ? sp : most;
     l.split_len = (steps + sp - 1) / sp * kBK;
     l.splits = steps > 0 ? (p.K + l.split_len - 1) / l.split_len : 1;

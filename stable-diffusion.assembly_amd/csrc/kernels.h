@@ -99,7 +99,7 @@ struct ConvArgs {
 hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream);
 
 // MUL_MAT split along K (gemm.hip): taken for products of fewer than 256
-// output blocks of 64 x 64 whose K (a multiple of 32) gives two splits of 32
+// output blocks of 64 x 64 whose K (a multiple of 32) gives two splits of 8
 // K-steps or more, x and W rows 16-byte aligned; its work buffer holds the
 // splits' partial sums.
 bool mul_mat_split_taken(const MulMatArgs &p);
