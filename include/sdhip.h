@@ -181,8 +181,9 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
  * convolution's products quantized (conv2d.cc:338-483) or F(2x2,3x3) with
  * quantized products (winograd.cc:1826-2103).  The work buffer: Winograd's
  * exponents, transformed operands and products; for a direct convolution of
- * a kernel other than 1x1 with IC KH KW a multiple of 32, its columns and
- * the partial sums of its splits of K; single-precision kernels' FP16
+ * a kernel other than 1x1 with IC KH KW a multiple of 32 (and of a 1x1 one
+ * whose output has few blocks and whose K is long), its columns and the
+ * partial sums of its splits of K; single-precision kernels' FP16
  * planes; the quantized columns and products; 0 else.  A buffer short of sdhip_conv2d_work_size is
  * SDHIP_ERROR.  Replaces conv2d_* and winograd_* of ops.h:26-38. */
 int sdhip_conv2d_supported(const sdhip_tensor *kernel, const sdhip_tensor *input, const sdhip_tensor *y,
@@ -207,9 +208,11 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
  * in the bits mode: wider ones return SDHIP_UNSUPPORTED there).  The work
  * buffer: in the bits mode the quantized operands; otherwise, for
  * single-precision keys and values of the head sizes 32, 40, 64, 80, 96, 128
- * and 160, the keys and values split into FP16 parts, tile by tile; for heads
- * of more than 256 dimensions whose keys are split across blocks, each
- * split's maximum, sum and output; 0 for the other forms.  A buffer short of
+ * and 160, the keys and values split into FP16 parts, tile by tile, and,
+ * where the queries alone leave the device's CUs idle and the keys are split
+ * across blocks, each split's maximum, sum and output; the same for heads of
+ * more than 256 dimensions whose keys are split across blocks; 0 for the
+ * other forms.  A buffer short of
  * sdhip_attention_work_size is SDHIP_ERROR.  Replaces attention_supported /
  * attention_work_size / attention_compute (ops.h:51-56). */
 int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
