@@ -540,24 +540,39 @@ static float column_at(const float *x, int64_t ic, int64_t ih, int64_t iw, int64
     return (y >= 0 && y < ih && xx >= 0 && xx < iw) ? x[((n * ic + c) * ih + y) * iw + xx] : 0.0f;
 }
 
+/* A mistake planted on purpose, for the tests that show the quantized
+ * convolutions' checks can see one (0: none): 1, the direct convolution's
+ * columns and kernels enumerated tap-major (k = (kh KW + kw) IC + ic) instead
+ * of conv2d.cc:255-258's order -- the same sum, other groups; 2, Winograd's
+ * weights quantized over every input channel at once instead of per stretch;
+ * 3, per stretch of one group. */
+int oracle_plant = 0;
+
+void oracle_set_plant(int mode) { oracle_plant = mode; }
+
 void oracle_quantized_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, int64_t iw, const float *w, int64_t oc,
                              int64_t kh, int64_t kw, int s0, int s1, int p0, int p1, int d0, int d1, int64_t oh,
                              int64_t ow, int64_t group, int input_levels, int weight_max, int weight_groups,
                              const float *init, float *y) {
-    const int64_t K = ic * kh * kw, P = n * oh * ow;
+    const int64_t K = ic * kh * kw, P = n * oh * ow, taps = kh * kw;
     float *cols = (float *)malloc((size_t)(P * K) * sizeof(float));
     float *t = (float *)malloc((size_t)(P * oc) * sizeof(float));
     float *it = init ? (float *)malloc((size_t)(P * oc) * sizeof(float)) : NULL;
-    for (int64_t p = 0; p < P; ++p)
-        for (int64_t k = 0; k < K; ++k)
-            cols[p * K + k] = column_at(x, ic, ih, iw, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, p, k);
+    float *wk = (float *)malloc((size_t)(oc * K) * sizeof(float));
+    /* Column k of the reference's order at place `at` of this one. */
+    for (int64_t k = 0; k < K; ++k) {
+        const int64_t at = oracle_plant == 1 ? (k % taps) * ic + k / taps : k;
+        for (int64_t p = 0; p < P; ++p)
+            cols[p * K + at] = column_at(x, ic, ih, iw, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, p, k);
+        for (int64_t o = 0; o < oc; ++o) wk[o * K + at] = w[o * K + k];
+    }
     for (int64_t p = 0; p < P; ++p) {
         const int64_t b = p / (oh * ow), r = p % (oh * ow);
         for (int64_t o = 0; o < oc; ++o) {
             if (it) it[p * oc + o] = init[(b * oc + o) * oh * ow + r];
         }
     }
-    oracle_quantized_mul_mat(w, cols, P, oc, K, group, input_levels, weight_max, weight_groups, it, t, NULL, NULL,
+    oracle_quantized_mul_mat(wk, cols, P, oc, K, group, input_levels, weight_max, weight_groups, it, t, NULL, NULL,
                              NULL, NULL, NULL, NULL, NULL);
     for (int64_t p = 0; p < P; ++p) {
         const int64_t b = p / (oh * ow), r = p % (oh * ow);
@@ -566,6 +581,7 @@ void oracle_quantized_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, 
     free(cols);
     free(t);
     free(it);
+    free(wk);
 }
 
 /* Row i of F(2x2)'s B^T of four numbers (winograd.cc:321-332). */
@@ -642,6 +658,8 @@ void oracle_quantized_winograd2(const float *x, int64_t n, int64_t ic, int64_t i
     float *ws = (float *)malloc((size_t)(oc * groups) * sizeof(float));
     float *wo = (float *)malloc((size_t)(oc * groups) * sizeof(float));
     int32_t *wsum = (int32_t *)malloc((size_t)(oc * groups) * sizeof(int32_t));
+    if (oracle_plant == 2) stretch = (ic + group - 1) / group * group;
+    if (oracle_plant == 3) stretch = group;
     const int64_t sg = stretch / group;  /* groups of a stretch */
     int8_t *tq = (int8_t *)malloc((size_t)(oc * sg * group));
     float *ts = (float *)malloc((size_t)(oc * sg) * sizeof(float));

@@ -133,6 +133,12 @@ void oracle_quantized_conv2d(const float *x, int64_t n, int64_t ic, int64_t ih, 
                              int64_t ow, int64_t group, int input_levels, int weight_max, int weight_groups,
                              const float *init, float *y);
 
+/* A mistake planted in the two quantized convolutions below, for tests that
+ * show their checks see one: 0 none, 1 the direct convolution's columns and
+ * kernels in tap-major order, 2 Winograd's weights per every input channel
+ * instead of per stretch, 3 per stretch of one group. */
+void oracle_set_plant(int mode);
+
 /* Winograd F(2x2, 3x3) with quantized products (winograd.cc:1826-2103), the
  * form every Winograd convolution takes in the bits mode: the reference's
  * transforms in its order of single-precision operations, the points'

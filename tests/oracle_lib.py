@@ -73,6 +73,7 @@ def lib():
         L.oracle_quantized_conv2d.argtypes = [_f, _L, _L, _L, _L, _f, _L, _L, _L, _I, _I, _I, _I, _I, _I, _L, _L, _L,
                                               _I, _I, _I, ctypes.c_void_p, _f]
         L.oracle_quantized_winograd2.argtypes = [_f, _L, _L, _L, _L, _f, _L, _I, _I, _L, _L, _L, _I, _I, _I, _L, _I, _f]
+        L.oracle_set_plant.argtypes = [_I]
         L.oracle_quantized_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _L, _I, _I, _L, _f]
         _lib = L
     return _lib
@@ -429,6 +430,22 @@ def quantized_conv2d(x, w, s0, s1, p0, p1, d0, d1, group=64, levels=255, wmax=12
     lib().oracle_quantized_conv2d(x, n, ic, ih, iw, w, oc, kh, kw, s0, s1, p0, p1, d0, d1, oh, ow, group, levels, wmax,
                                   weight_groups, ip, y)
     return y
+
+
+class planted:
+    """A mistake planted in the oracle's quantized convolutions for the length
+    of a `with` block (oracle_set_plant: 1 tap-major columns, 2 Winograd's
+    weights over every input channel, 3 over stretches of one group), so that
+    a test can show its check sees it."""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        lib().oracle_set_plant(self.mode)
+
+    def __exit__(self, *exc):
+        lib().oracle_set_plant(0)
 
 
 def quantized_winograd2(x, w, p0, p1, group=64, levels=255, wmax=127, weight_groups=1, stretch=64, init=None):

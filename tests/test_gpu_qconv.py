@@ -14,7 +14,7 @@ import torch
 
 import oracle_lib as orc
 import sdhip
-from helpers import dev, rng, uniform, unwritten, weights_f16
+from helpers import anchored, dev, rng, two_valued, uniform, unwritten, weights_f16, winograd_exact_operands
 from test_gpu_quant import bound, quant_params
 
 # w, h, ic, oc, kw, kh, s0, s1, p0, p1, d0, d1, n, single-precision kernel
@@ -117,10 +117,12 @@ def test_quantized_conv2d_from_redirect(gpu, c):
 
 
 def test_quantized_winograd_oracle_against_float64():
-    """The oracle's restatement of the bits-mode F(2x2) (winograd.cc:1826-2103)
-    within the quantized bound of float64 and not single-precision-close (a
-    transposed point, a dropped transform row or a misplaced group would be
-    far off); and its direct form's the same.  CPU only."""
+    """The oracle's restatements of the bits-mode F(2x2) (winograd.cc:1826-2103)
+    and direct form on ordinary operands: within the reference's bound for
+    quantized forms of float64, and quantized (not single-precision-close).
+    This bound does not see where the groups and stretches lie (groups of 32
+    in place of 64 would pass it); test_oracle.py's exact constructions do.
+    CPU only."""
     r = rng(3)
     x = uniform(r, (2, 24, 10, 12), 1.0)
     w = uniform(r, (16, 24, 3, 3), 0.25)
@@ -130,3 +132,54 @@ def test_quantized_winograd_oracle_against_float64():
     for y in (yw, yd):
         err = orc.metric(y, exact, mag)
         assert 1e-5 < err <= bound(255, 127), err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tuning", ["bits=8,weight_group=0", "bits=8", "bits=8,group=32", "bits=8,group=128"])
+@pytest.mark.parametrize("form", ["winograd_small", "winograd_large", "direct3", "direct1"])
+def test_quantized_conv2d_exact_operands(gpu, form, tuning):
+    """The device on operands that quantize exactly where the reference puts
+    its groups and stretches (tests/helpers.py: anchored kernels, two-valued
+    or per-group-scaled inputs): bit for bit with the oracle, and float64's
+    result to single-precision rounding -- the device's groups, stretches and
+    column order are the reference's, not merely the oracle's."""
+    group, levels, wmax, wg = quant_params(tuning)
+    r = rng(len(tuning) + len(form))
+    if form.startswith("winograd"):
+        n, h, w = (1, 8, 10) if form == "winograd_small" else (2, 24, 24)
+        ic, oc, kk = 320, 24, 3
+        stretch = stretch_of(tuning, ic, n, h, w)
+        spans = ([(s, min(s + stretch, ic)) for s in range(0, ic, stretch)] if wg == 0
+                 else [(g, min(g + group, ic)) for g in range(0, ic, group)])
+        x, k32 = winograd_exact_operands(r, (n, ic, h, w), oc, group, spans)
+    else:
+        kk = 3 if form == "direct3" else 1
+        n, h, w, oc = 2, 9, 11, 24
+        ic = 29 if kk == 3 else 150
+        K = ic * kk * kk
+        spans = [(0, K)] if wg == 0 else [(g, min(g + group, K)) for g in range(0, K, group)]
+        k32 = anchored(r, oc, K, spans).reshape(oc, ic, kk, kk)
+        x = two_valued(r, (n, ic, h, w))
+    pad = kk // 2
+    st = 2 if form == "direct3" else 1  # a stride of 2: the bits mode takes every 3x3 of stride 1 by F(2x2)
+    p = (st, st, pad, pad, 1, 1)
+    oh, ow = out_size(h, kk, st, pad, 1), out_size(w, kk, st, pad, 1)
+    k_d, x_d = dev(k32.astype(np.float16), gpu), dev(x, gpu)
+    y_d = unwritten((n, oc, oh, ow), gpu)
+    params = sdhip.conv_params(*p)
+    sdhip.set_tuning(tuning)
+    try:
+        path = sdhip.conv2d_path(k_d, x_d, y_d, params)
+        sdhip.conv2d(k_d, x_d, y_d, params, sdhip.epilogue([]))
+        torch.cuda.synchronize()
+    finally:
+        sdhip.set_tuning("")
+    assert path == (2 if form.startswith("winograd") else 0)
+    got = y_d.cpu().numpy()
+    want = (orc.quantized_winograd2(x, k32, pad, pad, group, levels, wmax, wg, stretch_of(tuning, ic, n, oh, ow))
+            if path == 2 else orc.quantized_conv2d(x, k32, *p, group, levels, wmax, wg))
+    exact, mag = orc.exact_conv2d(x, k32, *p)
+    err = orc.metric(got, exact, mag)
+    print(f"exact operands {form} [{tuning}] path {path}: error {err:.3g}")
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert err <= 1e-6

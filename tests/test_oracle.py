@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle_lib as orc
-from helpers import rng, uniform
+from helpers import anchored, rng, two_valued, uniform, winograd_exact_operands
 
 # ------------------------------------------------------------------ scalar math
 
@@ -389,3 +389,105 @@ def test_quantized_attention_groups_exactly():
     mean = v.astype(np.float64).mean(axis=1)  # [b, h, d]
     want = np.broadcast_to(mean[:, None], y.shape)
     assert np.max(np.abs(y - want) / np.abs(v).max()) < 1e-6
+
+
+# ------------------------------------------------------------------ quantized convolutions, exactly
+
+
+EXACT_BAR = 1e-6   # single-precision roundings of the dequantised sums only
+OFF_BAR = 1e-4     # a grouping mistake misquantizes a fraction of the weights by up to half a step
+
+
+@pytest.mark.parametrize("kernel", [3, 1])
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("weight_groups", [1, 0])
+def test_quantized_conv2d_groups_exactly(kernel, group, weight_groups):
+    """The bits-mode direct convolution (conv2d.cc:338-483) on operands that
+    quantize exactly where the reference puts its groups: the kernels'
+    groups of `group` consecutive k = ic KH KW + kh KW + kw (conv2d.cc:255-258)
+    of an output channel, or its whole row with weight_group=0 (quant.cc:
+    186-243), each an integer multiple of its own power of two with one +-127
+    of it.  The result is then float64's to single-precision rounding; the
+    same operands under the columns in another order (planted: tap-major), or
+    under groups of half or twice the length, are off by a step of a byte."""
+    r = rng(1000 * kernel + group + weight_groups)
+    n, ic, h, w, oc = 2, 29 if kernel == 3 else 150, 9, 11, 6
+    K = ic * kernel * kernel
+    spans = [(0, K)] if weight_groups == 0 else [(g, min(g + group, K)) for g in range(0, K, group)]
+    wts = anchored(r, oc, K, spans).reshape(oc, ic, kernel, kernel)
+    assert np.array_equal(wts.astype(np.float16).astype(np.float32), wts)
+    x = two_valued(r, (n, ic, h, w))
+    pad = kernel // 2
+    p = (1, 1, pad, pad, 1, 1)
+    exact, mag = orc.exact_conv2d(x, wts, *p)
+
+    def err(**kw):
+        return orc.metric(orc.quantized_conv2d(x, wts, *p, group=kw.pop("g", group), weight_groups=kw.pop(
+            "wg", weight_groups)), exact, mag)
+
+    assert err() <= EXACT_BAR
+    if kernel == 3 and weight_groups == 1:
+        # With one scale per whole row the order of k is not observable.
+        with orc.planted(1):
+            assert err() > OFF_BAR
+    if weight_groups == 1:
+        assert err(g=group // 2) > OFF_BAR
+        assert err(g=group * 2) > OFF_BAR
+    else:
+        assert err(wg=1) > OFF_BAR   # per group where the reference takes the whole row
+
+
+def stretch_for(group, ic, small):
+    """The stretch of input channels over which the bits mode quantizes
+    Winograd's weights at a time: max(group, kc rounded down to the group),
+    kc = min(ic, max(8, winograd_small_kc = 128)) for small images and
+    min(ic, winograd_kc = 256) for large (winograd.cc:238-255, 1859-1866)."""
+    kc = min(ic, 128) if small else min(ic, 256)
+    return max(group, kc // group * group)
+
+
+@pytest.mark.parametrize("size", ["small", "large"])
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("weight_groups", [0, 1])
+def test_quantized_winograd2_groups_exactly(size, group, weight_groups):
+    """The bits-mode F(2x2) (winograd.cc:1826-2103) on operands whose
+    transforms quantize exactly where the reference puts its scales:
+    * inputs d_c = k_c 2^(b_g) D, D one small-integer image for every
+      channel, k_c in [0, 255] with one 255 in each group g of input
+      channels, b_g the group's: each (tile, group, point) of V = B^T d B is
+      k_c 2^(b_g) times one integer, exact at the group's scale and zero point;
+    * kernels, per output channel and stretch of input channels
+      (weight_group=0) or group (1), 4 k 2^e with |k| <= 14 except one anchor
+      channel of +-127 2^e at the four corners, whose G g G^T is +-127 2^e at
+      all sixteen points (G (1, 0, 1)^T = (1, 1, 1, 1)^T): every point's
+      greatest |U| is 127 2^e, the others multiples of 2^e below it.
+    IC = 320 is above the stretch, so that the weights' scale changes between
+    stretches.  The result is float64's to single-precision rounding; the
+    weights over every input channel at once, or over stretches of one group
+    (both planted), or groups of another length, are off by a step."""
+    r = rng(7 * group + weight_groups + (0 if size == "small" else 1))
+    n, h, w = (1, 8, 10) if size == "small" else (2, 24, 24)
+    ic, oc = 320, 5
+    tiles = n * ((h + 1) // 2) * ((w + 1) // 2)
+    assert (tiles <= 256) == (size == "small")  # winograd_small_tiles (winograd.cc:194-196)
+    stretch = stretch_for(group, ic, size == "small")
+    assert stretch < ic
+    spans = ([(s, min(s + stretch, ic)) for s in range(0, ic, stretch)] if weight_groups == 0
+             else [(g, min(g + group, ic)) for g in range(0, ic, group)])
+    x, wts = winograd_exact_operands(r, (n, ic, h, w), oc, group, spans)
+    exact, mag = orc.exact_conv2d(x, wts, 1, 1, 1, 1, 1, 1)
+
+    def err(g=group, wg=weight_groups, st=stretch):
+        return orc.metric(orc.quantized_winograd2(x, wts, 1, 1, g, weight_groups=wg, stretch=st), exact, mag)
+
+    assert err() <= EXACT_BAR
+    if weight_groups == 0:
+        with orc.planted(2):
+            assert err() > OFF_BAR
+        if stretch > group:
+            with orc.planted(3):
+                assert err() > OFF_BAR
+    else:
+        assert err(g=group // 2, st=stretch_for(group // 2, ic, size == "small")) > OFF_BAR
+        if group * 2 <= 128:
+            assert err(g=group * 2, st=stretch_for(group * 2, ic, size == "small")) > OFF_BAR
