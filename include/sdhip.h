@@ -12,7 +12,10 @@
  * buffer (as ggml hands its wdata, sized by sdasm_work_size) and a HIP stream.
  *
  * Nothing here allocates device memory: the caller owns every tensor and the
- * work buffer, as ggml owns them for the reference (sdasm.h:51-54).
+ * work buffer, as ggml owns them for the reference (sdasm.h:51-54).  A work
+ * buffer must be 16-byte aligned (the kernels move 16-byte vectors through
+ * it; hipMalloc's are 256-byte aligned): a call that needs one and is handed
+ * a misaligned, missing or short one returns SDHIP_ERROR.
  *
  * Errors.  SDHIP_UNSUPPORTED is the reference's "not taken" (false / 0 from
  * sdasm_compute_nodes, hooks.cc:29-55): the caller computes the node itself.
@@ -93,10 +96,14 @@ const char *sdhip_last_error(void);
  * planner fuses no chain, or no residual connection, and an entry point
  * handed one computes it in a pass of its own after the operation, as ggml's
  * nodes would), todo and todo_tokens (sdhip_token_downsampling) and
- * store_forget (0 keeps every store entry, for the store's canary test).  The
- * names that size the reference's CPU blocks or choose among its CPU forms
- * (conv_kc, mul_mat_mc, amx_*, wide, prefetch, guided, half_format, ...) are
- * taken and have no effect here.  The reference's names take any int, as its
+ * store_forget (0 keeps every store entry, for the store's canary test).  Two
+ * names of the reference's CPU blocking also change results, and act here as
+ * there: winograd_kc and winograd_small_kc set the stretch of input channels
+ * over which the bits mode quantizes Winograd's transformed weights at a time
+ * (winograd.cc:238-255, 1859-1866).  The other names that size the
+ * reference's CPU blocks or choose among its CPU forms (conv_kc, mul_mat_mc,
+ * amx_*, wide, prefetch, guided, ...) are taken and have no effect here;
+ * half_format (bits=16's FP16 or bfloat16 products) is described with bits.  The reference's names take any int, as its
  * parser does, and are clamped where it clamps them (quant.cc:59-67).  This
  * library's own: winograd_fp32, winograd_splits, gemm_stages, gemm_tiles,
  * gemm_core, qgemm_core, attention_generic, attention_fp32 (forms to
@@ -228,7 +235,7 @@ sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const
 /* GGML_OP_GROUP_NORM (norm.cc:100-140): x, y F32 contiguous of one shape,
  * `groups` groups of ceil(ne2 / groups) channels over ne[2], per image ne[3];
  * then the chain (scale, shift, SiLU).  Replaces group_norm_supported /
- * group_norm_compute (ops.h:58-61).  The work buffer (8-byte aligned) holds
+ * group_norm_compute (ops.h:58-61).  The work buffer holds
  * the partial sums of the group's slices: the bytes sdasm_work_size would
  * report for the node (sdasm.h:51-54), where the reference's own form needs
  * none. */

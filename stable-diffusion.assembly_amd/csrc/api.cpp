@@ -36,6 +36,17 @@ sdhip_status fail(sdhip_status s, const char *fmt, ...) {
     return s;
 }
 
+sdhip_status check_work(const char *what, const void *work, size_t work_size, size_t need) {
+    if (need == 0) return SDHIP_OK;
+    if (work == nullptr || work_size < need) {
+        return fail(SDHIP_ERROR, "%s: work buffer of %zu bytes, %zu needed", what, work_size, need);
+    }
+    if ((reinterpret_cast<uintptr_t>(work) & 15) != 0) {
+        return fail(SDHIP_ERROR, "%s: work buffer not 16-byte aligned", what);
+    }
+    return SDHIP_OK;
+}
+
 sdhip_status launched(hipError_t e, const char *what) {
     if (e != hipSuccess) {
         return fail(SDHIP_ERROR, "%s: %s", what, hipGetErrorString(e));

@@ -163,8 +163,9 @@ Chain match_chain(const sdhip_node *const *nodes, int n_nodes, int index, bool s
         const sdhip_node *a = node->src[0];
         const sdhip_node *b = node->src[1];
         if (a == nullptr || b == nullptr) break;
-        // Through src0, the tensor ggml's in-place operations change; the
-        // other operand added or multiplied.
+        // An in-place ADD or MUL updates its first source, so the step is
+        // ours only if that source is the head's memory, unchanged in shape;
+        // the second source is the step's operand.
         const sdhip_tensor &bt = b->tensor;
         if (a->tensor.data != ht.data || !shape_of(a->tensor, ht) || overlap(bt, ht) || !holds_float(bt) ||
             bt.nb[0] != 4) {
@@ -177,8 +178,9 @@ Chain match_chain(const sdhip_node *const *nodes, int n_nodes, int index, bool s
             nb[k] = bt.ne[k] == 1 ? 0 : bt.nb[k] / 4;
         }
         if (positions) {
-            // An image's positions run on across its rows: the operand one
-            // number for them all, or in rows as the output.
+            // The convolution's epilogue walks an image's positions as one
+            // flat run, so within a channel the operand must either be a
+            // single number or laid out row by row exactly like the output.
             const bool broadcast = nb[0] == 0 && nb[1] == 0;
             const bool rows = nb[0] == 1 && nb[1] == ht.ne[0];
             fits = fits && (broadcast || rows);
@@ -187,8 +189,9 @@ Chain match_chain(const sdhip_node *const *nodes, int n_nodes, int index, bool s
         add_step(c, node->op == SDHIP_OP_ADD ? SDHIP_STEP_ADD : SDHIP_STEP_MUL, b);
         c.last_node = j;
     }
-    // The residual connection: an addition, not in place, of the chain's
-    // tensor and another of its shape and layout, into a third; views between.
+    // A skip connection after the chain: skipping view-only nodes, the next
+    // node may add the head's tensor to a same-shaped, same-strided tensor
+    // and write the sum somewhere else.  That sum can be written directly.
     for (; redirect && j < n_nodes && empty_op(nodes[j]->op); ++j) {
     }
     if (!redirect || j >= n_nodes || c.e.count >= SDHIP_MAX_STEPS) return c;
@@ -207,20 +210,24 @@ Chain match_chain(const sdhip_node *const *nodes, int n_nodes, int index, bool s
                               : b != nullptr && b->tensor.data == ht.data && alike(b) ? a
                                                                                       : nullptr;
     if (!alike(other) || overlap(other->tensor, ht)) return c;
-    // Nothing after reads the operation's tensor or the chain's, and none is
-    // an output of the graph.
+    // Writing the sum directly means the head's own tensor, and every chain
+    // node living in its memory, is never written.  That is only allowed if
+    // none of them is a graph output and no later node reads one of them.
+    // Too many of them to track: no redirect.
     const sdhip_node *unwritten[kMaxUnwritten];
     int count = 0;
-    for (int i = index; i <= c.last_node && count < kMaxUnwritten; ++i) {
+    for (int i = index; i <= c.last_node; ++i) {
         const sdhip_node *t = nodes[i];
         if (t->tensor.data != ht.data) continue;
-        if (graph_output(t)) return c;
+        if (graph_output(t) || count == kMaxUnwritten) return c;
         unwritten[count++] = t;
     }
     if (read_after(nodes, n_nodes, j + 1, unwritten, count)) return c;
     if (other->tensor.data == node->tensor.data) {
-        // The sum in the other operand's memory: begun from it, which only
-        // additions before may be reordered with.
+        // The skip tensor is the destination itself, so the epilogue starts
+        // its sum from the value already there.  That moves the skip term to
+        // the front of the sum, which is only the same sum in the reference's
+        // rounding order when every earlier step is an addition.
         for (int s = 0; s < c.e.count; ++s) {
             if (c.e.steps[s].kind != SDHIP_STEP_ADD) return c;
         }
@@ -249,8 +256,8 @@ bool redirect_apart(const sdhip_node *node, const Chain &c) {
     return true;
 }
 
-// fusion.cc:333-345: a view of `whole` that is its columns [begin, begin +
-// width), every row of it as the whole has them.
+// fusion.cc:333-345: whether `view` selects exactly the columns [begin,
+// begin + width) of `whole`, keeping each of its rows and their strides.
 bool columns_of(const sdhip_node *view, const sdhip_node *whole, int64_t begin, int64_t width) {
     const sdhip_tensor &v = view->tensor, &w = whole->tensor;
     if (!holds_float(v) || !holds_float(w) || v.ne[0] != width || v.nb[0] != 4 || begin > w.ne[0] ||
@@ -292,10 +299,13 @@ Gated match_gated_gelu(const sdhip_node *const *nodes, int n_nodes, int index, c
         mul->tensor.type != SDHIP_TYPE_F32 || !dense(mul->tensor) || !shape_of(mul->tensor, x->tensor)) {
         return r;
     }
-    // Nothing after reads what is not written, and none is a graph output.
+    // The fused form writes only the MUL's output, so the product, its chain
+    // and the four nodes of the pattern are never written: none may be a
+    // graph output or be read later.  Too many of them to track: no match.
+    if (c.last_node - index + 1 > kMaxUnwritten) return r;
     const sdhip_node *unwritten[kMaxUnwritten + 4];
     int count = 0;
-    for (int i = index; i <= c.last_node && count < kMaxUnwritten; ++i) unwritten[count++] = nodes[i];
+    for (int i = index; i <= c.last_node; ++i) unwritten[count++] = nodes[i];
     for (const sdhip_node *t : {v0, v1, cont, gelu}) unwritten[count++] = t;
     for (int i = 0; i < count; ++i) {
         if (graph_output(unwritten[i])) return r;

@@ -89,6 +89,10 @@ Tuning &tuning();
 inline GemmShape gemm_shape() { return GemmShape{tuning().gemm_stages, tuning().gemm_tiles}; }
 
 sdhip_status fail(sdhip_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// The caller's work buffer of a call that needs `need` bytes of it (none: any
+// buffer, or none): present, at least that large, and 16-byte aligned, as the
+// kernels move 16-byte vectors through it.  SDHIP_ERROR naming `what` else.
+sdhip_status check_work(const char *what, const void *work, size_t work_size, size_t need);
 sdhip_status launched(hipError_t e, const char *what);
 
 bool holds_f32(const sdhip_tensor *t);

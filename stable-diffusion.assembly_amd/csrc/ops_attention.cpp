@@ -158,18 +158,14 @@ sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const
                                            "is taken)", static_cast<long long>(qa.group));
         }
         const size_t need = qattention_layout(qa).total;
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "attention: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("attention", work, work_size, need); ws != SDHIP_OK) return ws;
         if (qa.lq == 0 || qa.h == 0 || qa.b == 0) return SDHIP_OK;
         return launched(launch_quantized_attention(qa, work, static_cast<hipStream_t>(stream)),
                         "quantized attention");
     }
     const AttentionArgs a = args_of(q, k, v, y, scale);
     const size_t need = attention_work_bytes(a);
-    if (need > 0 && (work == nullptr || work_size < need)) {
-        return fail(SDHIP_ERROR, "attention: work buffer of %zu bytes, %zu needed", work_size, need);
-    }
+    if (const sdhip_status ws = check_work("attention", work, work_size, need); ws != SDHIP_OK) return ws;
     return launched(launch_attention(a, work, static_cast<hipStream_t>(stream)), "attention");
 }
 

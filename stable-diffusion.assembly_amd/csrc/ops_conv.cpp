@@ -225,9 +225,7 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
         c.from_redirect = run.from_redirect;
         c.chain = run.fused;
         const size_t need = quantized_conv_work_size(c, path == 2);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("conv2d", work, work_size, need); ws != SDHIP_OK) return ws;
         s = quantized_conv(c, path == 2, work, st);
         return s == SDHIP_OK ? chain_after(run, st) : s;
     }
@@ -237,9 +235,7 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
         a.from_redirect = run.from_redirect;
         a.chain = run.fused;
         const size_t need = winograd_work_size(a);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("conv2d", work, work_size, need); ws != SDHIP_OK) return ws;
         s = winograd(a, work, st);
         return s == SDHIP_OK ? chain_after(run, st) : s;
     }
@@ -251,9 +247,7 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
         mark_split(c);
         const size_t cols = conv_columns_taken(c) ? round_up(conv_columns_work_size(c), 256) : 0;
         const size_t need = cols + split_weights_bytes(c.oc, c.K);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("conv2d", work, work_size, need); ws != SDHIP_OK) return ws;
         void *split = static_cast<char *>(work) + cols;
         s = launched(launch_split_weights(static_cast<const float *>(kernel->data), c.K, c.oc, c.K, split, st),
                      "conv2d split kernels");
@@ -264,9 +258,7 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
     }
     if (conv_columns_taken(c)) {
         const size_t need = conv_columns_work_size(c);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "conv2d: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("conv2d", work, work_size, need); ws != SDHIP_OK) return ws;
         s = launched(launch_conv_columns(c, work, gemm_shape(), st), "conv2d by columns");
     } else {
         s = launched(launch_conv_direct(c, gemm_shape(), st), "conv2d direct");

@@ -86,9 +86,7 @@ namespace sdhip {
 // the product's description pointed at the planes.
 sdhip_status split_into(MulMatArgs &a, void *work, size_t work_size, hipStream_t st, const char *what) {
     const size_t need = split_weights_bytes(a.N, a.K);
-    if (work == nullptr || work_size < need) {
-        return fail(SDHIP_ERROR, "%s: work buffer of %zu bytes, %zu needed", what, work_size, need);
-    }
+    if (const sdhip_status ws = check_work(what, work, work_size, need); ws != SDHIP_OK) return ws;
     const sdhip_status s = launched(launch_split_weights(a.w32, a.ldw32, a.N, a.K, work, st), "split weights");
     if (s != SDHIP_OK) return s;
     a.w = split_weights_hi(work);
@@ -115,18 +113,14 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (mul_mat_quantized(x)) {
         const size_t need = quantized_linear_work_size(a.K, a.N, a.M);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("mul_mat", work, work_size, need); ws != SDHIP_OK) return ws;
         s = quantized_linear(a, false, work, st);
     } else if (a.w32 != nullptr) {
         s = split_into(a, work, work_size, st, "mul_mat");
         if (s == SDHIP_OK) s = launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
     } else if (mul_mat_split_taken(a)) {
         const size_t need = mul_mat_split_work_size(a);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "mul_mat: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("mul_mat", work, work_size, need); ws != SDHIP_OK) return ws;
         s = launched(launch_mul_mat_split(a, work, gemm_shape(), st), "mul_mat split along K");
     } else {
         s = launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
@@ -185,9 +179,7 @@ sdhip_status sdhip_mul_mat_gated(const sdhip_tensor *w, const sdhip_tensor *x, c
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (mul_mat_quantized(x)) {
         const size_t need = quantized_linear_work_size(a.K, a.N, a.M);
-        if (work == nullptr || work_size < need) {
-            return fail(SDHIP_ERROR, "mul_mat_gated: work buffer of %zu bytes, %zu needed", work_size, need);
-        }
+        if (const sdhip_status ws = check_work("mul_mat_gated", work, work_size, need); ws != SDHIP_OK) return ws;
         return quantized_linear(a, true, work, st);
     }
     if (a.w32 != nullptr) {

@@ -52,12 +52,7 @@ sdhip_status sdhip_group_norm(const sdhip_tensor *x, const sdhip_tensor *y, int 
     a.per_group = ceil_div(a.ne2, groups);
     a.eps = eps;
     const GroupNormShape shape = group_norm_shape(a.ne0, a.ne1, a.ne2, a.ne3, groups);
-    if (work == nullptr || work_size < shape.work) {
-        return fail(SDHIP_ERROR, "group_norm: work buffer of %zu bytes, %zu needed", work_size, shape.work);
-    }
-    if ((reinterpret_cast<uintptr_t>(work) & 7) != 0) {
-        return fail(SDHIP_ERROR, "group_norm: work buffer not 8-byte aligned");
-    }
+    if (const sdhip_status ws = check_work("group_norm", work, work_size, shape.work); ws != SDHIP_OK) return ws;
     a.chunk = shape.chunk;
     a.slices = shape.slices;
     a.partials = static_cast<double *>(work);

@@ -89,13 +89,18 @@ def test_mul_mat_residual(gpu, from_redirect):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("K,M,B", [
+    (4096, 150, 2),  # 20 blocks of 64 x 64: 16 splits of 8 K-steps (256), all alike
+    (2336, 150, 1),  # 12 blocks, 73 K-steps: 8 splits of 9 steps and a last one of a single step
+])
 @pytest.mark.parametrize("from_redirect", [False, True])
-def test_mul_mat_split_chain(gpu, from_redirect):
-    """A product of few output blocks and long K, split along K: the splits'
-    sums added with bias, a per-token scale and a residual (or begun from the
-    residual), the epilogue of the single pass."""
-    K, N, M, B = 4096, 200, 150, 2  # 20 blocks of 64 x 64: four splits of 1024
-    r = rng(13)
+def test_mul_mat_split_chain(gpu, from_redirect, K, M, B):
+    """A product of few output blocks and long K, split along K (about 512
+    blocks, each split 8 K-steps of 32 or more, the last one what is left):
+    the splits' sums added with bias, a per-token scale and a residual (or
+    begun from the residual), the epilogue of the single pass."""
+    N = 200
+    r = rng(13 + K)
     bias = dev(uniform(r, (N,), 1.0), gpu)
     scale = dev(uniform(r, (B, M, 1), 1.0), gpu)
     res = uniform(r, (B, M, N), 1.0)

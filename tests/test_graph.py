@@ -207,6 +207,35 @@ def test_gated_gelu(lib):
     assert not p.gated_out and p.count == 2
 
 
+@pytest.mark.parametrize("views", [1, 3])
+def test_gated_gelu_with_views_in_the_chain(lib, views):
+    """The GEGLU pattern after a chain whose steps are separated by views
+    (RESHAPE nodes of the same memory): with one view a step the product,
+    its 6 steps and their views are 13 nodes and the pattern is fused; with
+    three a step they are 25, more than the planner tracks as never written,
+    and it declines the gated form rather than check only some of them (the
+    chain itself is still fused)."""
+    g = gl.Graph("cpu")
+    w = g.leaf(f16((2 * 64, 32)))
+    x = g.leaf(f32((2, 20, 32)))
+    y = g.mul_mat(w, x)
+    p_ = y
+    for i in range(6):
+        for _ in range(views):
+            p_ = g.reshape(p_, (2, 20, 2 * 64))
+        p_ = g.add_inplace(p_, g.leaf(f32((2 * 64,))))
+    xv = g.view_columns(p_, 0, 64)
+    gate = g.gelu_inplace(g.cont(g.view_columns(p_, 64, 64)))
+    out = g.mul(xv, gate)
+    order, status, p, steps = planned(lib, (g, out), y)
+    assert steps == ["add"] * 6
+    chain_nodes = 1 + 6 * (views + 1)
+    if views == 1:
+        assert p.gated_out and p.count == chain_nodes + 5
+    else:
+        assert not p.gated_out and p.count == chain_nodes
+
+
 def test_redirect_refused_when_the_head_is_read_after(lib):
     g = gl.Graph("cpu")
     y, yb = conv_bias(g)

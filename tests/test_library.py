@@ -236,3 +236,29 @@ def test_quantized_convolutions_taken():
         assert lib.sdhip_conv2d_path(k16, img, out, params) == 4
     finally:
         sdhip.set_tuning("")
+
+
+def test_misaligned_work_buffer_refused():
+    """Every entry point that takes a work buffer refuses one that is not
+    16-byte aligned (its kernels move 16-byte vectors and doubles through it),
+    before anything is launched: SDHIP_ERROR and a message that says so."""
+    lib = sdhip.load()
+    big = 1 << 40
+    odd = FAKE + 8  # 8-byte aligned, not 16
+    calls = []
+    q = tensor(F32, (2, 8, 4096, 40))
+    calls.append(lambda: lib.sdhip_attention(q, q, q, tensor(F32, (2, 4096, 8, 40)), 0.158, 0.0, 0.0,
+                                             odd, big, None))
+    kern, x, y = tensor(F16, (320, 320, 3, 3)), tensor(F32, (2, 320, 64, 64)), tensor(F32, (2, 320, 64, 64))
+    calls.append(lambda: lib.sdhip_conv2d(kern, x, y, sdhip.conv_params(1, 1, 1, 1, 1, 1), None, odd, big, None))
+    g = tensor(F32, (2, 1280, 32, 32))
+    calls.append(lambda: lib.sdhip_group_norm(g, g, 32, 1e-5, None, odd, big, None))
+    w, xm = tensor(F16, (320, 320)), tensor(F32, (2, 4096, 320))
+    for call, tuning in zip(calls + [lambda: lib.sdhip_mul_mat(w, xm, xm, None, odd, big, None)],
+                            ["", "", "", "bits=8"]):
+        sdhip.set_tuning(tuning)
+        try:
+            assert call() == sdhip.ERROR
+            assert b"16-byte aligned" in lib.sdhip_last_error()
+        finally:
+            sdhip.set_tuning("")

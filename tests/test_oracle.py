@@ -53,8 +53,12 @@ def test_scalar_math_bit_identical_to_the_reference(name):
     sources/scalar_math.h compiled unmodified (oracle/ref.mk): the same bits
     at every argument of a dense sweep, the clamp edges included.  A changed
     low-order digit of a Cephes coefficient, a dropped reduction step or a
-    wrong clamp shows here even where it stays within an ulp of exp."""
-    xs = scalar_sweep()
+    wrong clamp shows here even where it stays within an ulp of exp.  The
+    sweep includes every finite FP16 number times 16, the arguments
+    test_gpu_scalar_math.py adds for the device."""
+    with np.errstate(invalid="ignore", over="ignore"):
+        halves = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32) * 16
+    xs = np.concatenate([scalar_sweep(), halves[np.isfinite(halves)]])
     if name == "silu":
         got = orc.silu(xs)
     elif name == "gelu":
