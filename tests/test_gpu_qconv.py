@@ -146,7 +146,7 @@ def test_quantized_conv2d_exact_operands(gpu, form, tuning):
     group, levels, wmax, wg = quant_params(tuning)
     r = rng(len(tuning) + len(form))
     if form.startswith("winograd"):
-        n, h, w = (1, 8, 10) if form == "winograd_small" else (2, 24, 24)
+        n, h, w = (1, 8, 10) if form == "winograd_small" else (2, 40, 40)
         ic, oc, kk = 320, 24, 3
         stretch = stretch_of(tuning, ic, n, h, w)
         spans = ([(s, min(s + stretch, ic)) for s in range(0, ic, stretch)] if wg == 0

@@ -470,7 +470,7 @@ def test_quantized_winograd2_groups_exactly(size, group, weight_groups):
     weights over every input channel at once, or over stretches of one group
     (both planted), or groups of another length, are off by a step."""
     r = rng(7 * group + weight_groups + (0 if size == "small" else 1))
-    n, h, w = (1, 8, 10) if size == "small" else (2, 24, 24)
+    n, h, w = (1, 8, 10) if size == "small" else (2, 40, 40)  # 1600 positions an image: Winograd, not small
     ic, oc = 320, 5
     tiles = n * ((h + 1) // 2) * ((w + 1) // 2)
     assert (tiles <= 256) == (size == "small")  # winograd_small_tiles (winograd.cc:194-196)
