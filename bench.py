@@ -541,8 +541,14 @@ def cpu_ops(threads, bits=0, weight_groups=1):
             b, lq, c = q.shape
             d = c // heads
             self.count_attention(q, k, heads)
-            y = self.orc.port_attention(self._np(q).reshape(b, lq, heads, d), self._np(k).reshape(b, -1, heads, d),
-                                        self._np(v).reshape(b, -1, heads, d), 1.0 / d ** 0.5, threads=self.threads)
+            qn, kn, vn = (self._np(t).reshape(b, -1, heads, d) for t in (q, k, v))
+            if self.bits and kn.shape[1] >= 256:
+                # The bits mode's attention where the reference quantizes it
+                # (attention.cc:622-624): group 64, stretches of 256 keys.
+                y = self.orc.port_quantized_attention(qn, kn, vn, 1.0 / d ** 0.5, 64, 255, 127, 256,
+                                                      threads=self.threads)
+            else:
+                y = self.orc.port_attention(qn, kn, vn, 1.0 / d ** 0.5, threads=self.threads)
             return torch.from_numpy(y).reshape(b, lq, c)
 
     return CpuOps(threads, bits, weight_groups)
@@ -686,8 +692,8 @@ def cpu_baseline(seconds):
             "note": "oracle/port.c: this repository's AVX-512 restatement of the reference's CPU algorithms "
                     "(packed GEMM, Winograd with transforms per block, blocked attention, VNNI W8A8); the "
                     "reference's own x86 kernels need ggml and C++26 and are not built here.  cfg5 on the CPU: "
-                    "the block with its linear layers quantized (weights per row, kept) and attention in single "
-                    "precision (the bits mode's quantized attention is not restated in the port)"}
+                    "the block in the bits mode, as on the GPU -- its linear layers quantized (weights per row, "
+                    "kept) and its self-attention quantized (VNNI, attention.cc:612-824)"}
 
 
 # The VAE decoder's operations of the reference's bench (tools/bench.cc:146-153):
@@ -760,14 +766,15 @@ def unet_step_line(dev, args):
 # those of the configurations' table of work units, restated:
 #   cfg1  Y = X W^T + b, X 2x4096x320 f32, W 320x320 f16: X 10.49 MB + W 0.20 +
 #         b + Y 10.49 = 21.18 MB (AI 79: HBM-bound at the split-FP16 rate)
-#   cfg2  the 36 products of 320x320 by 512 tiles: 3.775 GFLOP (the F(4x4)
-#         direct-equivalent 15.10 GFLOP for the op) over U and V read once as
-#         two FP16 planes (36 x 2 x 2 x (320 + 512) x 320 = 38.34 MB) and M
-#         written once in single precision (36 x 4 x 320 x 512 = 23.59 MB):
-#         AI 61 flop/B, below the ridge of the three-MFMA split (833 TF / 8
-#         TB/s = 104) and of the raw FP16 peak (312) -- HBM bounds it at this
-#         K, so the roofline takes the bytes; the MFMA view is reported beside
-#         them
+#   cfg2  the 36 products of 320x320 by 512 tiles: 2 x 36 x 320 x 320 x 512
+#         = 3.775 GFLOP a call on the FP16 MFMA, three MFMAs a product, against
+#         the raw 2.5 PF (and the split's 833 TF effective); the op's
+#         direct-equivalent 15.10 GFLOP against the target of 1.5 x 2.5 PF.
+#         Beside it, the products' bytes (U and V read once as two FP16
+#         planes, 36 x 2 x 2 x (320 + 512) x 320 = 38.34 MB; M written once,
+#         36 x 4 x 320 x 512 = 23.59 MB) against 8 TB/s, and the whole op's
+#         counter bytes against its own algorithmic 33.3 MB (input 10.49 MB,
+#         FP16 weights 1.84, bias, residual 10.49, output 10.49)
 #   cfg3a F(2x2) of 8x8 maps: the products kernel reads the FP16 weights,
 #         1280x1280x9x2 = 29.49 MB (it makes U in registers)
 #   cfg3b 1x1 conv 2x640x1024 -> 1280: 3.355 GFLOP
@@ -777,9 +784,10 @@ def unet_step_line(dev, args):
 CONFIGS = {
     "cfg1_linear": dict(workload="cfg1", unit="TFLOP/s", kernels=("mul_mat",), bound="hbm", amount=21.18e6,
                         peak=PEAK_HBM),
-    "cfg2_winograd4": dict(workload="cfg2", unit="TFLOP/s", kernels=("winograd4.products",), bound="hbm",
-                           amount=36 * 2 * 2 * (320 + 512) * 320 + 36 * 4 * 320 * 512.0, peak=PEAK_HBM,
-                           flops=2.0 * 36 * 320 * 320 * 512, split=3),
+    "cfg2_winograd4": dict(workload="cfg2", unit="TFLOP/s", kernels=("winograd4.products",), bound="mfma",
+                           amount=2.0 * 36 * 320 * 320 * 512, peak=PEAK_FP16_MFMA, split=3,
+                           hbm_bytes=36 * 2 * 2 * (320 + 512) * 320 + 36 * 4 * 320 * 512.0,
+                           op_bytes=(3 * 2 * 320 * 64 * 64 + 320) * 4 + 320 * 320 * 9 * 2.0, op_target=1.5),
     "cfg3a_winograd2_gn_silu": dict(workload="cfg3a", unit="TFLOP/s", kernels=("winograd2.products",), bound="hbm",
                                     amount=1280 * 1280 * 9 * 2.0, peak=PEAK_HBM),
     "cfg3b_pointwise_gn_silu": dict(workload="cfg3b", unit="TFLOP/s", kernels=("conv_direct_pointwise",),
@@ -807,23 +815,29 @@ def roofline(spec, kt, op_ms, work):
            "peak": spec["peak"], "unit": "GB/s" if hbm else ("TOPS" if spec["unit"] == "TOPS" else "TFLOP/s"),
            "frac": round(achieved / spec["peak"], 4), "kernel_us": round(ms * 1e3, 2),
            "amount": spec["amount"], "traffic": profiled_traffic(spec["workload"], spec["kernels"][0])}
-    if hbm and spec.get("flops"):
-        # The same kernel against the MFMA peak: its arithmetic intensity
-        # (algorithmic flops / bytes) below the ridge is why HBM bounds it.
-        tflops = spec["flops"] / ms / 1e9
-        out["mfma_view"] = {"achieved": round(tflops, 2), "peak": PEAK_FP16_MFMA, "unit": "TFLOP/s",
-                            "frac": round(tflops / PEAK_FP16_MFMA, 4),
-                            "effective_peak": round(PEAK_FP16_MFMA / spec["split"], 1),
-                            "frac_of_effective": round(tflops * spec["split"] / PEAK_FP16_MFMA, 4),
-                            "ai_flop_per_byte": round(spec["flops"] / spec["amount"], 1),
-                            "ridge_effective": round(PEAK_FP16_MFMA / spec["split"] / (PEAK_HBM / 1e3), 1)}
-    elif spec.get("split"):
+    if spec.get("split"):
         # Split-FP16: each product takes `split` FP16 MFMA products.
         out["effective_peak"] = round(spec["peak"] / spec["split"], 1)
         out["frac_of_effective"] = round(achieved * spec["split"] / spec["peak"], 4)
+    if spec.get("hbm_bytes"):
+        # The same kernel's algorithmic bytes against HBM's peak.
+        gbs = spec["hbm_bytes"] / ms / 1e6
+        out["hbm_view"] = {"achieved": round(gbs, 1), "peak": PEAK_HBM, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM, 4), "amount": spec["hbm_bytes"]}
     rate = work / op_ms / 1e9
+    peak = PEAK_INT8_MFMA if spec["unit"] == "TOPS" else PEAK_FP16_MFMA
     out["op_rate"] = round(rate, 2)
-    out["op_rate_vs_mfma_peak"] = round(rate / (PEAK_INT8_MFMA if spec["unit"] == "TOPS" else PEAK_FP16_MFMA), 4)
+    out["op_rate_vs_mfma_peak"] = round(rate / peak, 4)
+    if spec.get("op_target"):
+        # The north star's target for Winograd: op_target x the FP16 peak in
+        # direct-convolution FLOPs.
+        out["op_target"] = {"rate": spec["op_target"] * peak, "frac": round(rate / (spec["op_target"] * peak), 4)}
+    if spec.get("op_bytes"):
+        # Every kernel of the op, counter bytes per call, against the op's
+        # algorithmic bytes (inputs and outputs once each).
+        op_traffic = profiled_traffic(spec["workload"], "op")
+        out["op_bytes"] = {"algorithmic": spec["op_bytes"], "traffic": op_traffic,
+                           "ratio": round(op_traffic / spec["op_bytes"], 2) if op_traffic else None}
     return out
 
 

@@ -213,6 +213,12 @@ void oracle_port_quantized_linear(const float *x, int64_t M, int64_t K, const vo
 void oracle_port_gated(const float *y, int64_t M, int64_t N, float *out, int threads);
 
 /* The host's single-precision FMA rate on `threads` threads, GFLOP/s. */
+/* The bits mode's self-attention (attention.cc:612-824) on AVX512-VNNI: the
+ * oracle's algorithm, 16 keys or dimensions a vector (its exponentials by the
+ * port's own polynomial, not bit for bit). */
+void oracle_port_quantized_attention(const float *q, const float *k, const float *v, int64_t b, int64_t lq,
+                                     int64_t lk, int64_t h, int64_t hk, int64_t d, int64_t dv, float scale,
+                                     int64_t group, int levels, int wmax, int64_t key_block, float *y, int threads);
 double oracle_port_fma_peak(int threads, double seconds);
 
 #ifdef __cplusplus

@@ -50,8 +50,8 @@ static void *alloc64(size_t bytes) {
  * touch of fresh pages -- the reference's pool keeps its buffers likewise.
  * The contents are not kept: each call writes what it reads. */
 static void *kept(int slot, size_t bytes) {
-    static void *buffers[4];
-    static size_t sizes[4];
+    static void *buffers[8];
+    static size_t sizes[8];
     if (sizes[slot] < bytes) {
         free(buffers[slot]);
         buffers[slot] = alloc64(bytes);
@@ -894,6 +894,39 @@ static void quantize_group(const float *x, int64_t cnt, int64_t group, int level
     *offset = s * zero;
 }
 
+/* quantize_group 16 numbers a vector: the least and greatest with 0 between
+ * them, the scale and its inverse, each byte rint(x inverse) + zero clamped
+ * to [0, levels] (round to nearest even, as nearbyintf), the tail the zero
+ * point. */
+static void quantize16(const float *x, int64_t cnt, int64_t group, int levels, uint8_t *dst, float *scale,
+                       float *offset) {
+    __m512 lo = _mm512_setzero_ps(), hi = _mm512_setzero_ps();
+    for (int64_t e = 0; e < cnt; e += 16) {
+        const __mmask16 live = cnt - e >= 16 ? (__mmask16)0xffff : (__mmask16)((1u << (cnt - e)) - 1u);
+        const __m512 v = _mm512_maskz_loadu_ps(live, x + e);
+        lo = _mm512_min_ps(lo, v);
+        hi = _mm512_max_ps(hi, v);
+    }
+    const float least = _mm512_reduce_min_ps(lo), greatest = _mm512_reduce_max_ps(hi);
+    const float s = (greatest - least) / (float)levels;
+    const float inverse = s > 0.0f ? 1.0f / s : 0.0f;
+    const float zero = nearbyintf(-least * inverse);
+    const __m512 inv = _mm512_set1_ps(inverse), z = _mm512_set1_ps(zero), top = _mm512_set1_ps((float)levels);
+    for (int64_t e = 0; e < group; e += 16) {
+        const __mmask16 live = cnt - e >= 16 ? (__mmask16)0xffff
+                               : cnt > e     ? (__mmask16)((1u << (cnt - e)) - 1u)
+                                             : (__mmask16)0;
+        const __m512 v = _mm512_maskz_loadu_ps(live, x + e);
+        __m512 qv = _mm512_add_ps(_mm512_roundscale_ps(_mm512_mul_ps(v, inv), _MM_FROUND_TO_NEAREST_INT), z);
+        qv = _mm512_min_ps(_mm512_max_ps(qv, _mm512_setzero_ps()), top);
+        qv = _mm512_mask_mov_ps(z, live, qv);
+        const __mmask16 keep = group - e >= 16 ? (__mmask16)0xffff : (__mmask16)((1u << (group - e)) - 1u);
+        _mm_mask_storeu_epi8(dst + e, keep, _mm512_cvtusepi32_epi8(_mm512_cvtps_epu32(qv)));
+    }
+    *scale = s;
+    *offset = s * zero;
+}
+
 /* One QR x QN tile of the quantized product: per group the exact integer sum
  * S (AVX512-VNNI, unsigned inputs by signed weights), then t = fma(sa sb, S,
  * t), t = fma(-oa, ob, t) in the order of quant.cc:113-164. */
@@ -977,6 +1010,197 @@ void oracle_port_quantized_linear(const float *x, int64_t M, int64_t K, const vo
             for (int64_t n = 0; n < N; ++n) row[n] += bias[n];
     }
     if (gated) oracle_port_gated(y, M, N, out, threads);
+}
+
+/* The bits mode's self-attention (attention.cc:612-824) on AVX512-VNNI, in
+ * the reference's algorithm: per (image, key head) the keys quantized signed,
+ * one group over the head's dimensions, packed [key tile of 16][gd / 4][16][4];
+ * the values signed per (dimension, group of `group` keys), packed per group
+ * [dim panel of 16][group / 4][16][4]; per query its bytes unsigned with a
+ * zero point over the dimensions, the softmax's scale folded into its scale
+ * and offset (754-764); its scores, the integer sums of 16 keys a vector
+ * (vpdpbusd), scaled back as quant.cc:150-155 does; their maximum; then per
+ * stretch of key_block keys the exponentials (the polynomial of exp16 for the
+ * stretch's multiples of 8 keys, expf for the rest), summed in double, and per
+ * group of keys quantized unsigned with a zero point, their product with the
+ * values 16 dimensions a vector, dequantised in the reference's order; the
+ * output times float(1 / sum).  q [b][lq][h][d], k [b][lk][hk][d],
+ * v [b][lk][hk][dv], y [b][lq][h][dv]. */
+void oracle_port_quantized_attention(const float *q, const float *k, const float *v, int64_t b, int64_t lq,
+                                     int64_t lk, int64_t h, int64_t hk, int64_t d, int64_t dv, float scale,
+                                     int64_t group, int levels, int wmax, int64_t key_block, float *y, int threads) {
+    const int64_t gd = cdiv(d, 4) * 4, lkt = cdiv(lk, 16), groups = cdiv(lk, group), dvt = cdiv(dv, 16);
+    const int64_t heads = b * hk;
+    const size_t kbytes = (size_t)(lkt * gd * 16), vbytes = (size_t)(groups * dvt * group * 16);
+    int8_t *kq = (int8_t *)kept(0, (size_t)heads * kbytes);
+    float *ks = (float *)kept(1, (size_t)(heads * lkt * 16) * sizeof(float));
+    float *ko = (float *)kept(2, (size_t)(heads * lkt * 16) * sizeof(float));
+    int8_t *vq = (int8_t *)kept(3, (size_t)heads * vbytes);
+    float *vs = (float *)kept(4, (size_t)(heads * groups * dvt * 16) * sizeof(float));
+    float *vo = (float *)kept(5, (size_t)(heads * groups * dvt * 16) * sizeof(float));
+    const float wm = (float)wmax;
+    /* The keys and the values of each head, quantized and packed. */
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+    for (int64_t item = 0; item < heads * (lkt + groups * dvt); ++item) {
+        const int64_t head = item / (lkt + groups * dvt), u = item % (lkt + groups * dvt);
+        const int64_t bi = head / hk, kh = head % hk;
+        if (u < lkt) {
+            for (int64_t jj = 0; jj < 16; ++jj) {
+                const int64_t j = u * 16 + jj;
+                const float *row = k + ((bi * lk + (j < lk ? j : 0)) * hk + kh) * d;
+                float m = 0.0f;
+                if (j < lk)
+                    for (int64_t e = 0; e < d; ++e) m = fmaxf(m, fabsf(row[e]));
+                const float sc = m / wm, inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+                int32_t sum = 0;
+                for (int64_t e = 0; e < gd; ++e) {
+                    float qv = j < lk && e < d ? nearbyintf(row[e] * inv) : 0.0f;
+                    qv = qv < -wm ? -wm : qv > wm ? wm : qv;
+                    kq[(size_t)head * kbytes + ((u * (gd / 4) + e / 4) * 16 + jj) * 4 + e % 4] = (int8_t)qv;
+                    sum += (int32_t)qv;
+                }
+                ks[head * lkt * 16 + j] = sc;
+                ko[head * lkt * 16 + j] = sc * (float)sum;
+            }
+        } else {
+            const int64_t g = (u - lkt) / dvt, pnl = (u - lkt) % dvt;
+            for (int64_t cc = 0; cc < 16; ++cc) {
+                const int64_t c = pnl * 16 + cc;
+                float m = 0.0f;
+                for (int64_t w = 0; w < group && c < dv; ++w) {
+                    const int64_t j = g * group + w;
+                    if (j < lk) m = fmaxf(m, fabsf(v[((bi * lk + j) * hk + kh) * dv + c]));
+                }
+                const float sc = m / wm, inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+                int32_t sum = 0;
+                int8_t *dst = vq + (size_t)head * vbytes + (size_t)((g * dvt + pnl) * group * 16);
+                for (int64_t w = 0; w < group; ++w) {
+                    const int64_t j = g * group + w;
+                    float qv = c < dv && j < lk ? nearbyintf(v[((bi * lk + j) * hk + kh) * dv + c] * inv) : 0.0f;
+                    qv = qv < -wm ? -wm : qv > wm ? wm : qv;
+                    dst[((w / 4) * 16 + cc) * 4 + w % 4] = (int8_t)qv;
+                    sum += (int32_t)qv;
+                }
+                vs[((head * groups + g) * dvt + pnl) * 16 + cc] = sc;
+                vo[((head * groups + g) * dvt + pnl) * 16 + cc] = sc * (float)sum;
+            }
+        }
+    }
+    enum { AQ = 4 };  /* queries a thread takes at once: each key and value load serves all of them */
+    const int64_t qblocks = cdiv(lq, AQ);
+#pragma omp parallel num_threads(threads)
+    {
+        float *sc = (float *)kept_local(0, (size_t)(AQ * lkt * 16) * sizeof(float));
+        uint8_t *qq = (uint8_t *)kept_local(1, (size_t)(AQ * gd));
+        uint8_t *eq = (uint8_t *)kept_local(2, (size_t)(AQ * group));
+        float *t = (float *)kept_local(3, (size_t)(AQ * dvt * 16) * sizeof(float));
+#pragma omp for schedule(dynamic, 2)
+        for (int64_t item = 0; item < b * h * qblocks; ++item) {
+            const int64_t i0 = (item % qblocks) * AQ, bh = item / qblocks, bi = bh / h, hh = bh % h;
+            const int64_t rows = min64(AQ, lq - i0);
+            const int64_t head = bi * hk + hh / (h / hk);
+            float qs[AQ], qo[AQ], mx[AQ];
+            double total[AQ];
+            for (int r = 0; r < AQ; ++r) {
+                const int64_t i = i0 + (r < rows ? r : 0);
+                quantize16(q + ((bi * lq + i) * h + hh) * d, d, gd, levels, qq + r * gd, &qs[r], &qo[r]);
+                qs[r] *= scale;
+                qo[r] *= scale;
+            }
+            /* The scores, 16 keys a vector, AQ queries a key load. */
+            const int8_t *kh_q = kq + (size_t)head * kbytes;
+            __m512 top[AQ];
+            for (int r = 0; r < AQ; ++r) top[r] = _mm512_set1_ps(-INFINITY);
+            for (int64_t u = 0; u < lkt; ++u) {
+                __m512i acc[AQ];
+                for (int r = 0; r < AQ; ++r) acc[r] = _mm512_setzero_si512();
+                for (int64_t e4 = 0; e4 < gd / 4; ++e4) {
+                    const __m512i kv = _mm512_loadu_si512((const void *)(kh_q + (u * (gd / 4) + e4) * 64));
+                    for (int r = 0; r < AQ; ++r) {
+                        int32_t four;
+                        memcpy(&four, qq + r * gd + 4 * e4, 4);
+                        acc[r] = _mm512_dpbusd_epi32(acc[r], _mm512_set1_epi32(four), kv);
+                    }
+                }
+                const __m512 s4 = _mm512_loadu_ps(ks + head * lkt * 16 + u * 16);
+                const __m512 o4 = _mm512_sub_ps(_mm512_setzero_ps(), _mm512_loadu_ps(ko + head * lkt * 16 + u * 16));
+                const __mmask16 live = lk - u * 16 >= 16 ? (__mmask16)0xffff : (__mmask16)((1u << (lk - u * 16)) - 1u);
+                for (int r = 0; r < AQ; ++r) {
+                    __m512 x = _mm512_fmadd_ps(_mm512_mul_ps(s4, _mm512_set1_ps(qs[r])), _mm512_cvtepi32_ps(acc[r]),
+                                               _mm512_setzero_ps());
+                    x = _mm512_fmadd_ps(o4, _mm512_set1_ps(qo[r]), x);
+                    _mm512_storeu_ps(sc + r * lkt * 16 + u * 16, x);
+                    top[r] = _mm512_mask_max_ps(top[r], live, top[r], x);
+                }
+            }
+            for (int r = 0; r < AQ; ++r) {
+                mx[r] = _mm512_reduce_max_ps(top[r]);
+                total[r] = 0.0;
+            }
+            for (int64_t c = 0; c < AQ * dvt * 16; ++c) t[c] = 0.0f;
+            for (int64_t j0 = 0; j0 < lk; j0 += key_block) {
+                const int64_t j1 = min64(j0 + key_block, lk), whole = j0 + (j1 - j0) / 8 * 8;
+                for (int r = 0; r < AQ; ++r) {
+                    float *row = sc + r * lkt * 16;
+                    __m512d sum0 = _mm512_setzero_pd(), sum1 = _mm512_setzero_pd();
+                    int64_t j = j0;
+                    for (; j < whole; j += 16) {
+                        /* the polynomial for the stretch's multiples of 8 keys */
+                        const __mmask16 live = whole - j >= 16 ? (__mmask16)0xffff
+                                                               : (__mmask16)((1u << (whole - j)) - 1u);
+                        v16 z = (v16)_mm512_maskz_loadu_ps(live, row + j);
+                        z = (v16)_mm512_maskz_mov_ps(live, (__m512)exp16(z - mx[r]));
+                        _mm512_mask_storeu_ps(row + j, live, (__m512)z);
+                        sum0 = _mm512_add_pd(sum0, _mm512_cvtps_pd(_mm512_castps512_ps256((__m512)z)));
+                        sum1 = _mm512_add_pd(sum1, _mm512_cvtps_pd(_mm256_castpd_ps(
+                                                       _mm512_extractf64x4_pd(_mm512_castps_pd((__m512)z), 1))));
+                    }
+                    double tail = 0.0;
+                    for (j = whole; j < j1; ++j) {
+                        row[j] = expf(row[j] - mx[r]);
+                        tail += (double)row[j];
+                    }
+                    total[r] += _mm512_reduce_add_pd(_mm512_add_pd(sum0, sum1)) + tail;
+                }
+                for (int64_t g0 = j0; g0 < j1; g0 += group) {
+                    float es[AQ], eo[AQ];
+                    for (int r = 0; r < AQ; ++r)
+                        quantize16(sc + r * lkt * 16 + g0, min64(group, j1 - g0), group, levels, eq + r * group, &es[r],
+                                   &eo[r]);
+                    const int64_t g = g0 / group;
+                    const int8_t *vg = vq + (size_t)head * vbytes + (size_t)(g * dvt * group * 16);
+                    for (int64_t pnl = 0; pnl < dvt; ++pnl) {
+                        __m512i acc[AQ];
+                        for (int r = 0; r < AQ; ++r) acc[r] = _mm512_setzero_si512();
+                        const int8_t *vp = vg + pnl * group * 16;
+                        for (int64_t w4 = 0; w4 < group / 4; ++w4) {
+                            const __m512i vv = _mm512_loadu_si512((const void *)(vp + w4 * 64));
+                            for (int r = 0; r < AQ; ++r) {
+                                int32_t four;
+                                memcpy(&four, eq + r * group + 4 * w4, 4);
+                                acc[r] = _mm512_dpbusd_epi32(acc[r], _mm512_set1_epi32(four), vv);
+                            }
+                        }
+                        const __m512 vs4 = _mm512_loadu_ps(vs + ((head * groups + g) * dvt + pnl) * 16);
+                        const __m512 vo4 =
+                            _mm512_sub_ps(_mm512_setzero_ps(), _mm512_loadu_ps(vo + ((head * groups + g) * dvt + pnl) * 16));
+                        for (int r = 0; r < AQ; ++r) {
+                            float *tr = t + (r * dvt + pnl) * 16;
+                            __m512 tt = _mm512_loadu_ps(tr);
+                            tt = _mm512_fmadd_ps(_mm512_mul_ps(vs4, _mm512_set1_ps(es[r])), _mm512_cvtepi32_ps(acc[r]), tt);
+                            tt = _mm512_fmadd_ps(vo4, _mm512_set1_ps(eo[r]), tt);
+                            _mm512_storeu_ps(tr, tt);
+                        }
+                    }
+                }
+            }
+            for (int64_t r = 0; r < rows; ++r) {
+                const float inv = (float)(1.0 / total[r]);
+                float *dst = y + ((bi * lq + i0 + r) * h + hh) * dv;
+                for (int64_t c = 0; c < dv; ++c) dst[c] = t[r * dvt * 16 + c] * inv;
+            }
+        }
+    }
 }
 
 /* The GEGLU after a product (fusion.cc:347-394): out[m][j] = y[m][j]

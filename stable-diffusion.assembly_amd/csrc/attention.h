@@ -46,7 +46,7 @@ struct QAttentionArgs {
     int32_t levels, wmax;
     int64_t group, key_block;
     // Set by qattention_layout.
-    int64_t gd, sd, lkp, lqp, groups, slot, dvp, tail_from, qblocks;
+    int64_t gd, sd, lkp, lqp, groups, slot, dvp, dvc, tail_from, qblocks;
     int8_t *kq, *vq, *qq;
     float *ks, *ko, *vs, *vo, *qs, *qo;
     int32_t *ksum, *vsum;

@@ -66,13 +66,6 @@ QAttentionArgs qargs_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhi
     return a;
 }
 
-// Whether the quantized form takes these heads and the tuning's group.
-bool quantized_form_takes(const sdhip_tensor *q, const sdhip_tensor *v) {
-    if (q->ne[0] > 256 || v->ne[0] > 256) return false;
-    int quads = tuning().group / 4;
-    quads = quads < 1 ? 1 : (quads > 256 ? 256 : quads);
-    return (4 * quads) % 16 == 0 && 4 * quads <= 256;
-}
 
 // The launch's description of the operands (ggml's ne and nb, in elements).
 AttentionArgs args_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v, const sdhip_tensor *y,
@@ -127,11 +120,10 @@ int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, cons
                        q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 && k->nb[2] % k->nb[0] == 0 &&
                        k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 && v->nb[2] % v->nb[0] == 0 &&
                        v->nb[3] % v->nb[0] == 0;
-    if (!taken) return 0;
-    // In the bits mode the quantized form takes heads of up to 256
-    // dimensions and groups of keys that are a multiple of 16 up to 256; the
-    // rest is left to the caller, as not taken.
-    return !quantized_attention(k) || quantized_form_takes(q, v);
+    // In the bits mode the quantized form takes the same heads (up to
+    // kAttentionMaxDims dimensions) and every group quant() gives (a multiple
+    // of 4 from 4 to 1024 keys).
+    return taken ? 1 : 0;
 }
 
 size_t sdhip_attention_work_size(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_tensor *v,
@@ -150,13 +142,6 @@ sdhip_status sdhip_attention(const sdhip_tensor *q, const sdhip_tensor *k, const
     }
     if (quantized_attention(k)) {
         QAttentionArgs qa = qargs_of(q, k, v, y, scale);
-        if (q->ne[0] > 256 || v->ne[0] > 256) {
-            return fail(SDHIP_UNSUPPORTED, "attention: quantized heads of more than 256 dimensions are not taken");
-        }
-        if (qa.group % 16 != 0 || qa.group > 256) {
-            return fail(SDHIP_UNSUPPORTED, "attention: quantized groups of %lld keys (a multiple of 16 up to 256 "
-                                           "is taken)", static_cast<long long>(qa.group));
-        }
         const size_t need = qattention_layout(qa).total;
         if (const sdhip_status ws = check_work("attention", work, work_size, need); ws != SDHIP_OK) return ws;
         if (qa.lq == 0 || qa.h == 0 || qa.b == 0) return SDHIP_OK;

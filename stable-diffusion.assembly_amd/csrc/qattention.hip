@@ -56,7 +56,7 @@ __device__ __forceinline__ float load_num(const void *p, int64_t at, bool half) 
 // registers between the group's maximum and its quantization; the maxima and
 // the integer sums are exact whatever the order of their reductions.
 constexpr int kQaLanes = 16;
-constexpr int kQaSteps = 4;  // the most 64-byte steps of a slot (sd <= 256)
+constexpr int kQaSteps = 8;  // the most 64-byte steps of a slot (sd <= 512)
 constexpr int kQaItems = 256 / kQaLanes;
 
 __device__ __forceinline__ float qa_lanes_max(float v) {
@@ -151,8 +151,71 @@ __device__ __forceinline__ void qa_keys_block(const QAttentionArgs &a, int64_t b
 // dimensions past dv: zeros.  A wave takes 16 dimensions, a lane one of them
 // and every fourth run of 4 consecutive keys of the slot: key w = 64 chunk +
 // 16 kt + 4 kg + r sits at position p = 64 chunk + 16 kg + 4 kt + r, so that a
-// run's 4 bytes are one word.
-constexpr int kQaRuns = 256 / 16;  // the most runs a lane takes (slot <= 256)
+// run's 4 bytes are one word.  Slots of up to 256 keys are held in registers
+// between the group's maximum and its quantization; longer ones (groups of up
+// to 1024 keys) are read twice.
+constexpr int kQaRuns = 256 / 16;  // the most runs a lane holds (slot <= 256)
+
+__device__ __forceinline__ int64_t qa_value_position(int64_t w0) {
+    return (w0 & ~63) + 16 * ((w0 >> 2) & 3) + 4 * ((w0 >> 4) & 3);
+}
+
+__device__ __forceinline__ void qa_values_block_long(const QAttentionArgs &a, int64_t blk) {
+    const int64_t chunks = (a.dvp + 63) / 64;
+    const int64_t cc = blk % chunks;
+    const int64_t rest = blk / chunks;
+    const int64_t g = rest % a.groups;
+    const int64_t head = rest / a.groups;
+    const int64_t bi = head / a.hk, kh = head % a.hk;
+    const int lane = threadIdx.x & 63;
+    const int64_t c = cc * 64 + (threadIdx.x >> 6) * 16 + (lane & 15);
+    const int rg = lane >> 4;
+    const int runs = static_cast<int>(a.slot / 16);
+    const bool dim = c < a.dv;
+    const int64_t base = bi * a.vnb3 + kh * a.vnb2 + (dim ? c : 0);
+    const auto load_run = [&](int i, float (&x)[4]) {
+        const int64_t w0 = 4 * (rg + 4 * i);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t key = g * a.group + w0 + r;
+            x[r] = dim && w0 + r < a.group && key < a.lk ? load_num(a.v, base + key * a.vnb1, a.vhalf) : 0.0f;
+        }
+    };
+    float m = 0.0f;
+    for (int i = 0; i < runs; ++i) {
+        float x[4];
+        load_run(i, x);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(x[r]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const float wmax = static_cast<float>(a.wmax);
+    const float s = __fdiv_rn(m, wmax);
+    const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
+    int sum = 0;
+    int8_t *dst = a.vq + ((head * a.dvp + c) * a.groups + g) * a.slot;
+    for (int i = 0; i < runs; ++i) {
+        float x[4];
+        load_run(i, x);
+        uint32_t word = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int q = static_cast<int>(qa_clamp(rintf(__fmul_rn(x[r], inverse)), -wmax, wmax));
+            word |= qa_byte(q, r);
+            sum += q;
+        }
+        if (c < a.dvp) *reinterpret_cast<uint32_t *>(dst + qa_value_position(4 * (rg + 4 * i))) = word;
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (rg == 0 && c < a.dvp) {
+        const int64_t at = (head * a.groups + g) * a.dvp + c;
+        a.vs[at] = s;
+        a.vo[at] = __fmul_rn(s, static_cast<float>(sum));
+        a.vsum[at] = sum;
+    }
+}
 
 __device__ __forceinline__ void qa_values_block(const QAttentionArgs &a, int64_t blk) {
     const int64_t chunks = (a.dvp + 63) / 64;
@@ -199,8 +262,7 @@ __device__ __forceinline__ void qa_values_block(const QAttentionArgs &a, int64_t
                 word |= qa_byte(q, r);
                 sum += q;
             }
-            const int64_t p = (w0 & ~63) + 16 * ((w0 >> 2) & 3) + 4 * ((w0 >> 4) & 3);
-            if (c < a.dvp) *reinterpret_cast<uint32_t *>(dst + p) = word;
+            if (c < a.dvp) *reinterpret_cast<uint32_t *>(dst + qa_value_position(w0)) = word;
         }
     }
     sum += __shfl_xor(sum, 16, 64);
@@ -284,7 +346,11 @@ QaOperandBlocks qa_operand_blocks(const QAttentionArgs &a) {
 __global__ __launch_bounds__(256) void qa_operands_kernel(QAttentionArgs a, QaOperandBlocks n) {
     const int64_t blk = blockIdx.x;
     if (blk < n.values) {
-        qa_values_block(a, blk);
+        if (a.slot <= 16 * kQaRuns) {
+            qa_values_block(a, blk);
+        } else {
+            qa_values_block_long(a, blk);
+        }
     } else if (blk < n.values + n.keys) {
         qa_keys_block(a, blk - n.values);
     } else {
@@ -294,20 +360,21 @@ __global__ __launch_bounds__(256) void qa_operands_kernel(QAttentionArgs a, QaOp
 
 // ------------------------------------------------------------------ attention
 
-// The scores of key tile kt (keys 16 kt + 4 lg + r) for the lane's query:
-// the integer products over the sd bytes, restored, and scaled back.
+// The scores of the 16 keys j0 .. j0 + 15 (j0 a multiple of 4; the lane's
+// are j0 + 4 lg + r) for the lane's query: the integer products over the sd
+// bytes, restored, and scaled back.
 template <int SUBS>
 __device__ __forceinline__ float4v qa_scores(const QAttentionArgs &a, const int8_t *kq, const float *ks,
-                                             const float *ko, const int32_t *ksum, const int4v (&qb)[kQaSteps],
-                                             float qs, float qo, int64_t kt, int lr, int lg) {
+                                             const float *ko, const int32_t *ksum, const int4v (&qb)[SUBS],
+                                             float qs, float qo, int64_t j0, int lr, int lg) {
     int4v acc = int4v{};
-    const int8_t *krow = kq + (16 * kt + lr) * a.sd + 16 * lg;
+    const int8_t *krow = kq + (j0 + lr) * a.sd + 16 * lg;
 #pragma unroll
     for (int sub = 0; sub < SUBS; ++sub) {
         const int4v av = *reinterpret_cast<const int4v *>(krow + 64 * sub);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qb[sub], acc, 0, 0, 0);
     }
-    const int64_t j = 16 * kt + 4 * lg;
+    const int64_t j = j0 + 4 * lg;
     const float4v s4 = *reinterpret_cast<const float4v *>(ks + j);
     const float4v o4 = *reinterpret_cast<const float4v *>(ko + j);
     const int4v n4 = *reinterpret_cast<const int4v *>(ksum + j);
@@ -321,17 +388,27 @@ __device__ __forceinline__ float4v qa_scores(const QAttentionArgs &a, const int8
     return out;
 }
 
-template <int SUBS, int NDV, int GT>
+// A workgroup per (64 queries, head, image, chunk of up to 256 dimensions of
+// the values); NDV the most tiles of 16 dimensions of a chunk the instance
+// takes.  A group of keys is taken a part of 16 GT keys at a time (GT tiles
+// of 16): groups of up to 16 GT keys in one part, their exponentials held in
+// registers from their quantization's statistics to their product; longer
+// groups (16 GT = 256) in parts computed twice, once for the group's
+// statistics and sum, once for the product.
+template <int SUBS, int NDV, int GT, bool LONG>
 __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int lr = lane & 15;
     const int lg = lane >> 4;
+    constexpr int64_t kPart = 16 * GT;
 
     const uint32_t blk = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint32_t qb_ = blk % static_cast<uint32_t>(a.qblocks);
-    const uint32_t bh = blk / static_cast<uint32_t>(a.qblocks);
+    const uint32_t rest = blk / static_cast<uint32_t>(a.qblocks);
+    const uint32_t bh = rest % static_cast<uint32_t>(a.h * a.b);
+    const int64_t c0 = static_cast<int64_t>(rest / static_cast<uint32_t>(a.h * a.b)) * a.dvc;  // the chunk's first dimension
     const int64_t hh = bh % a.h;
     const int64_t bi = bh / a.h;
     const int64_t kh = hh / (a.h / a.hk);
@@ -340,10 +417,10 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     const int64_t qrow = (bi * a.h + hh) * a.lqp + i0 + lr;        // the lane's query, in qq / qs / qo
 
     // Operand B of the scores: the lane's query, bytes 64 sub + 16 lg.
-    int4v qbv[kQaSteps];
+    int4v qbv[SUBS];
 #pragma unroll
-    for (int sub = 0; sub < kQaSteps; ++sub)
-        qbv[sub] = sub < SUBS ? *reinterpret_cast<const int4v *>(a.qq + qrow * a.sd + 64 * sub + 16 * lg) : int4v{};
+    for (int sub = 0; sub < SUBS; ++sub)
+        qbv[sub] = *reinterpret_cast<const int4v *>(a.qq + qrow * a.sd + 64 * sub + 16 * lg);
     const float qs = a.qs[qrow], qo = a.qo[qrow];
 
     const int8_t *kq = a.kq + head_k * a.lkp * a.sd;
@@ -355,8 +432,9 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     // Tiles wholly of keys take no test per key.
     float top = -INFINITY;
     const int64_t whole = a.lk / 16;
-    for (int64_t kt = 0; kt < a.lkp / 16; ++kt) {
-        const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, kt, lr, lg);
+    const int64_t tiles = (a.lk + 15) / 16;
+    for (int64_t kt = 0; kt < tiles; ++kt) {
+        const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, 16 * kt, lr, lg);
         if (kt < whole) {
             top = fmaxf(fmaxf(top, fmaxf(sc[0], sc[1])), fmaxf(sc[2], sc[3]));
             continue;
@@ -368,9 +446,9 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     top = fmaxf(top, __shfl_xor(top, 16, 64));
     top = fmaxf(top, __shfl_xor(top, 32, 64));
 
-    // Second pass, group by group.  NDV is the most tiles of 16 dimensions
-    // the instance takes; ndv those the values have.
-    const int ndv = static_cast<int>(a.dvp / 16);
+    // Second pass, group by group, over the chunk's ndv tiles of dimensions.
+    const int64_t left = (a.dvp - c0) / 16;
+    const int ndv = static_cast<int>(left < NDV ? left : NDV);
     float t[NDV][4];
 #pragma unroll
     for (int c = 0; c < NDV; ++c)
@@ -378,55 +456,55 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
         for (int r = 0; r < 4; ++r) t[c][r] = 0.0f;
     double total = 0.0;
     const float levels = static_cast<float>(a.levels);
-    const int8_t *vq = a.vq + head_k * a.dvp * a.groups * a.slot;
-    const float *vs = a.vs + head_k * a.groups * a.dvp;
-    const float *vo = a.vo + head_k * a.groups * a.dvp;
-    const int32_t *vsum = a.vsum + head_k * a.groups * a.dvp;
+    const int8_t *vq = a.vq + (head_k * a.dvp + c0) * a.groups * a.slot;
+    const float *vs = a.vs + head_k * a.groups * a.dvp + c0;
+    const float *vo = a.vo + head_k * a.groups * a.dvp + c0;
+    const int32_t *vsum = a.vsum + head_k * a.groups * a.dvp + c0;
+    const int parts = LONG ? static_cast<int>((a.group + kPart - 1) / kPart) : 1;
     for (int64_t g = 0; g < a.groups; ++g) {
-        // The group's exponentials: tile kt of the group, keys 16 kt + 4 lg + r.
+        const int64_t gbase = g * a.group;
+        // The exponentials of part p of the group: tile kt, keys gbase + p
+        // kPart + 16 kt + 4 lg + r, zero past the group and past lk; with
+        // `stats` their sum, least and greatest taken too.
         float e[GT][4];
         float lo = 0.0f, hi = 0.0f;
-        // A group of GT whole tiles of keys, none of them past tail_from,
-        // takes no test per key: Cephes' exponential for each.
-        const int64_t g_end = (g + 1) * a.group;
-        if (a.group == 16 * GT && g_end <= a.lk && g_end <= a.tail_from) {
+        const auto exps = [&](int p, bool stats) {
+            const int64_t rel0 = p * kPart;
+            const int64_t end = gbase + rel0 + kPart;
+            const bool plain = a.group % 16 == 0 && rel0 + kPart <= a.group && end <= a.lk && end <= a.tail_from;
 #pragma unroll
             for (int kt = 0; kt < GT; ++kt) {
-                const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, g * GT + kt, lr, lg);
+                const int64_t rel = rel0 + 16 * kt;  // the tile's first key, in the group
+                if (!plain && (rel >= a.group || gbase + rel >= a.lk)) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) e[kt][r] = 0.0f;
+                    continue;
+                }
+                const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, gbase + rel, lr, lg);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float x = cephes_exp(__fsub_rn(sc[r], top));
-                    total += static_cast<double>(x);
-                    lo = fminf(lo, x);
-                    hi = fmaxf(hi, x);
+                    const int64_t jr = rel + 4 * lg + r;
+                    const int64_t j = gbase + jr;
+                    const bool key = plain || (jr < a.group && j < a.lk);
+                    float x = 0.0f;
+                    if (plain) {
+                        // Whole tiles of keys, none past tail_from: Cephes'
+                        // exponential for each, no test per key.
+                        x = cephes_exp(__fsub_rn(sc[r], top));
+                    } else if (key) {
+                        const float arg = __fsub_rn(sc[r], top);
+                        x = j < a.tail_from ? cephes_exp(arg) : static_cast<float>(exp(static_cast<double>(arg)));
+                    }
+                    if (stats && key) {
+                        total += static_cast<double>(x);
+                        lo = fminf(lo, x);
+                        hi = fmaxf(hi, x);
+                    }
                     e[kt][r] = x;
                 }
             }
-        } else {
-#pragma unroll
-        for (int kt = 0; kt < GT; ++kt) {
-            const int64_t j0 = g * a.group + 16 * kt;  // the tile's first key
-            if (16 * kt >= a.group || j0 >= a.lk) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) e[kt][r] = 0.0f;
-                continue;
-            }
-            const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, j0 / 16, lr, lg);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t j = j0 + 4 * lg + r;
-                float x = 0.0f;
-                if (j < a.lk) {
-                    const float arg = __fsub_rn(sc[r], top);
-                    x = j < a.tail_from ? cephes_exp(arg) : static_cast<float>(exp(static_cast<double>(arg)));
-                    total += static_cast<double>(x);
-                    lo = fminf(lo, x);
-                    hi = fmaxf(hi, x);
-                }
-                e[kt][r] = x;
-            }
-        }
-        }
+        };
+        for (int p = 0; p < parts; ++p) exps(p, true);
         lo = fminf(lo, __shfl_xor(lo, 16, 64));
         lo = fminf(lo, __shfl_xor(lo, 32, 64));
         hi = fmaxf(hi, __shfl_xor(hi, 16, 64));
@@ -441,35 +519,40 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
         int4v acc[NDV];
 #pragma unroll
         for (int c = 0; c < NDV; ++c) acc[c] = int4v{};
+        for (int p = 0; p < parts; ++p) {
+            if (LONG) exps(p, false);  // a long group's part again: the same exponentials
 #pragma unroll
-        for (int chunk = 0; chunk < (GT + 3) / 4; ++chunk) {
-            if (64 * chunk >= a.slot) continue;
-            // The bytes q - 128 of the quantized exponentials (q an integer
-            // in [0, 255]): q packed as an unsigned byte, its top bit flipped.
-            int4v bv;
+            for (int chunk = 0; chunk < (GT + 3) / 4; ++chunk) {
+                const int64_t pos = p * kPart + 64 * chunk;  // the chunk's first position in the slot
+                if (pos >= a.slot) continue;
+                // The bytes q - 128 of the quantized exponentials (q an
+                // integer in [0, 255]): q packed as an unsigned byte, its top
+                // bit flipped.
+                int4v bv;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t word = 0;
+                for (int w = 0; w < 4; ++w) {
+                    uint32_t word = 0;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kt = 4 * chunk + w;
-                    float q = 0.0f;
-                    if (kt < GT) q = qa_clamp(__fadd_rn(rintf(__fmul_rn(e[kt][r], inverse)), zero), 0.0f, levels);
-                    word = __builtin_amdgcn_cvt_pk_u8_f32(q, r, word);
+                    for (int r = 0; r < 4; ++r) {
+                        const int kt = 4 * chunk + w;
+                        float q = 0.0f;
+                        if (kt < GT) q = qa_clamp(__fadd_rn(rintf(__fmul_rn(e[kt][r], inverse)), zero), 0.0f, levels);
+                        word = __builtin_amdgcn_cvt_pk_u8_f32(q, r, word);
+                    }
+                    bv[w] = static_cast<int>(word ^ 0x80808080u);
                 }
-                bv[w] = static_cast<int>(word ^ 0x80808080u);
-            }
-            // Tiles of the group past its keys: positions with no key, whose
-            // values' bytes are 0; the -128 there multiplies them.
+                // Positions of the slot past the group's keys hold value
+                // bytes of 0, which the exponentials' bytes there multiply.
 #pragma unroll
-            for (int c = 0; c < NDV; ++c) {
-                if (c >= ndv) continue;
-                const int4v av = *reinterpret_cast<const int4v *>(
-                    vq + ((16 * c + lr) * a.groups + g) * a.slot + 64 * chunk + 16 * lg);
-                acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[c], 0, 0, 0);
+                for (int c = 0; c < NDV; ++c) {
+                    if (c >= ndv) continue;
+                    const int4v av =
+                        *reinterpret_cast<const int4v *>(vq + ((16 * c + lr) * a.groups + g) * a.slot + pos + 16 * lg);
+                    acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[c], 0, 0, 0);
+                }
             }
         }
-        // Scaled back into the output, dimensions 16 c + 4 lg + r.
+        // Scaled back into the output, dimensions c0 + 16 c + 4 lg + r.
 #pragma unroll
         for (int c = 0; c < NDV; ++c) {
             if (c >= ndv) continue;
@@ -491,58 +574,66 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     const float reciprocal = static_cast<float>(1.0 / total);
     const int64_t i = i0 + lr;
     if (i >= a.lq) return;
-    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hh * a.ynb1;
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hh * a.ynb1 + c0;
 #pragma unroll
     for (int c = 0; c < NDV; ++c) {
         if (c >= ndv) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t dim = 16 * c + 4 * lg + r;
-            if (dim < a.dv) out[dim] = __fmul_rn(t[c][r], reciprocal);
+            if (c0 + dim < a.dv) out[dim] = __fmul_rn(t[c][r], reciprocal);
         }
     }
 }
 
 template <int SUBS, int NDV>
 hipError_t launch_qa_gt(const QAttentionArgs &a, hipStream_t stream, dim3 grid) {
-    const int gt = static_cast<int>(a.group / 16);
+    const int64_t gt = (a.group + 15) / 16;
     if (gt <= 4) {
-        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 4>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 4, false>), grid, dim3(256), 0, stream, a);
     } else if (gt <= 8) {
-        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 8>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 8, false>), grid, dim3(256), 0, stream, a);
+    } else if (gt <= 16) {
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 16, false>), grid, dim3(256), 0, stream, a);
     } else {
-        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 16>), grid, dim3(256), 0, stream, a);
+        // Groups of more than 256 keys, in parts of 256.
+        SDHIP_LAUNCH((qa_attention_kernel<SUBS, NDV, 16, true>), grid, dim3(256), 0, stream, a);
     }
     return hipGetLastError();
 }
 
 template <int SUBS>
 hipError_t launch_qa_ndv(const QAttentionArgs &a, hipStream_t stream, dim3 grid) {
-    switch (a.dvp / 16) {
-    case 1: return launch_qa_gt<SUBS, 1>(a, stream, grid);
-    case 2: return launch_qa_gt<SUBS, 2>(a, stream, grid);
-    case 3: return launch_qa_gt<SUBS, 3>(a, stream, grid);
-    case 4: return launch_qa_gt<SUBS, 4>(a, stream, grid);
-    case 5: return launch_qa_gt<SUBS, 5>(a, stream, grid);
-    case 6:
-    case 7:
-    case 8: return launch_qa_gt<SUBS, 8>(a, stream, grid);
-    case 9:
-    case 10: return launch_qa_gt<SUBS, 10>(a, stream, grid);
-    default: return launch_qa_gt<SUBS, 16>(a, stream, grid);
-    }
+    // Instances of 2, 4, 8 and 16 tiles of dimensions (a chunk's tiles past
+    // its own are skipped).  With parts of 256 keys the instance of 8 spills
+    // its registers where that of 16 does not (the compiler's resource
+    // usage): it takes those.
+    const int64_t tiles = a.dvc / 16;
+    if (tiles <= 2) return launch_qa_gt<SUBS, 2>(a, stream, grid);
+    if (tiles <= 4) return launch_qa_gt<SUBS, 4>(a, stream, grid);
+    if (tiles <= 8 && a.group <= 128) return launch_qa_gt<SUBS, 8>(a, stream, grid);
+    return launch_qa_gt<SUBS, 16>(a, stream, grid);
 }
 
 }  // namespace
 
 QAttentionLayout qattention_layout(QAttentionArgs &a) {
     a.gd = round_up(a.d, 4);
+    // Slots of 1, 2, 4 or 8 steps of 64 bytes (the kernels' instances); the
+    // bytes past gd are 0 in the keys and the queries.
     a.sd = round_up(a.gd, 64);
-    a.lkp = round_up(a.lk, 16);
-    a.lqp = round_up(a.lq, 64);
+    if (a.sd == 192) a.sd = 256;
+    if (a.sd > 256) a.sd = 512;
     a.groups = ceil_div(a.lk, a.group);
+    // The keys' rows: a tile of 16 starting at any key of the last group (a
+    // multiple of 4) stays inside them.
+    a.lkp = round_up(a.groups * a.group + 15, 16);
+    a.lqp = round_up(a.lq, 64);
     a.slot = round_up(a.group, 64);
     a.dvp = round_up(a.dv, 16);
+    // The values' dimensions a workgroup takes: all of them up to 256, else
+    // chunks of 256.
+    a.dvc = a.dvp <= 256 ? a.dvp : 256;
     // Stretches of key_block keys (attention.cc:663-664); the keys past the
     // last multiple of 8 of the last one take std::exp (attention.cc:288-301).
     const int64_t last = (a.lk - 1) / a.key_block * a.key_block;
@@ -594,12 +685,12 @@ hipError_t launch_quantized_attention(QAttentionArgs a, void *work, hipStream_t 
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     KernelScope scope("qattention", stream);
-    const dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b));
+    const dim3 grid(static_cast<uint32_t>(a.qblocks * a.h * a.b * ceil_div(a.dvp, a.dvc)));
     switch (a.sd / 64) {
     case 1: return launch_qa_ndv<1>(a, stream, grid);
     case 2: return launch_qa_ndv<2>(a, stream, grid);
-    case 3: return launch_qa_ndv<3>(a, stream, grid);
-    default: return launch_qa_ndv<4>(a, stream, grid);
+    case 4: return launch_qa_ndv<4>(a, stream, grid);
+    default: return launch_qa_ndv<8>(a, stream, grid);
     }
 }
 

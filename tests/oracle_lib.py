@@ -49,6 +49,8 @@ def lib():
         L.oracle_port_group_norm.argtypes = [_f, _f, _L, _L, _L, _I, _F, _v, _v, _I, _I]
         L.oracle_port_norm.argtypes = [_f, _f, _L, _L, _F, _v, _v, _I]
         L.oracle_port_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _F, _f, _I]
+        L.oracle_port_quantized_attention.argtypes = [_f, _f, _f, _L, _L, _L, _L, _L, _L, _L, _F, _L, _I, _I, _L,
+                                                      _f, _I]
         L.oracle_port_qweights_bytes.restype = ctypes.c_size_t
         L.oracle_port_qweights_bytes.argtypes = [_L, _L, _L]
         L.oracle_port_pack_qweights.argtypes = [_s8, _f, _f, _L, _L, _L, _u8]
@@ -205,6 +207,19 @@ def port_attention(q, k, v, scale, threads=1):
     lk, dv = k.shape[1], v.shape[3]
     y = np.empty((b, lq, h, dv), np.float32)
     lib().oracle_port_attention(q, k, v, b, lq, lk, h, d, dv, scale, y, threads)
+    return y
+
+
+def port_quantized_attention(q, k, v, scale, group=64, levels=255, wmax=127, key_block=256, threads=1):
+    """port.c's bits-mode self-attention (attention.cc:612-824): q [b, lq, h,
+    d], k [b, lk, hk, d], v [b, lk, hk, dv] -> y [b, lq, h, dv]; key_block the
+    exponentials' stretch, a multiple of the group."""
+    q, k, v = c32(q), c32(k), c32(v)
+    b, lq, h, d = q.shape
+    lk, hk, dv = k.shape[1], k.shape[2], v.shape[3]
+    y = np.empty((b, lq, h, dv), np.float32)
+    lib().oracle_port_quantized_attention(q, k, v, b, lq, lk, h, hk, d, dv, scale, group, levels, wmax, key_block, y,
+                                          threads)
     return y
 
 

@@ -86,10 +86,37 @@ def test_cross_attention_stays_single_precision(gpu):
     assert orc.metric(y, exact, mag) <= 1e-6
 
 
+WIDE_AND_GROUPS = [  # case, tuning: heads to 512 dimensions and any group of keys quant() gives
+    ((512, 64, 4096, 1, 1, 1, False), "bits=8"),              # the VAE's mid-block head (64 of its 4096 queries)
+    ((512, 40, 1000, 1, 1, 1, False), "bits=8,group=20"),
+    ((320, 50, 600, 2, 1, 1, True), "bits=8,group=300"),     # a group longer than 256 keys, FP16, GQA
+    ((100, 70, 2100, 2, 2, 1, False), "bits=8,group=1024"),  # the longest group, 2100 keys in 3 groups
+    ((100, 70, 700, 2, 2, 1, False), "bits=8,group=200"),
+    ((40, 300, 4096, 2, 2, 2, False), "bits=8,group=20"),
+    ((40, 100, 1000, 2, 2, 1, False), "bits=8,group=4"),
+    ((13, 37, 290, 4, 2, 3, False), "bits=8,group=36"),
+]
+
+
 @pytest.mark.gpu
-def test_quantized_groups_not_taken(gpu):
-    """Groups of keys that are no multiple of 16 are left to the caller."""
-    c = (40, 20, 300, 1, 1, 1, False)
-    with pytest.raises(sdhip.SdhipError) as e:
-        run(gpu, c, "bits=8,group=20", seed=1)
-    assert e.value.status == sdhip.UNSUPPORTED
+@pytest.mark.parametrize("c,tuning", WIDE_AND_GROUPS, ids=lambda x: "x".join(map(str, x)) if isinstance(x, tuple)
+                         else x)
+def test_quantized_attention_wide_heads_and_any_group(gpu, c, tuning):
+    """Heads of up to 512 dimensions (the keys' and queries' slots of up to 8
+    steps of 64 bytes, the values' dimensions in chunks of 256 a workgroup)
+    and groups of keys that are any multiple of 4 up to 1024 (quant.cc:59-67;
+    attention.cc:612-664): tiles of 16 keys beginning at any multiple of 4,
+    groups past 256 keys in parts.  Within 1e-5 of the oracle and the
+    reference's bound of float64, as the other cases."""
+    group, levels, wmax, _ = quant_params(tuning)
+    q, k, v, y, scale = run(gpu, c, tuning, seed=sum(c[:3]) + group)
+    want = orc.quantized_attention(q, k, v, scale, group, levels, wmax, key_block(tuning, group))
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    apart = orc.metric(y, want, mag)
+    err = orc.metric(y, exact, mag)
+    same = np.mean(y.view(np.uint32) == want.view(np.uint32))
+    print(f"quantized attention {c} [{tuning}]: {apart:.3g} from the oracle ({same:.4%} bit-identical), "
+          f"error {err:.3g} (bound {bound(levels, wmax):.3g})")
+    assert np.isfinite(y).all()
+    assert apart <= APART
+    assert err <= bound(levels, wmax)

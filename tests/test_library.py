@@ -165,6 +165,22 @@ def test_attention_and_norm_predicates():
     assert lib.sdhip_norm_supported(tensor(F32, (2, 988, 1280)), tensor(F32, (2, 988, 1280)))
 
 
+def test_quantized_attention_takes_wide_heads_and_any_group():
+    """In the bits mode the quantized form takes what attention_supported
+    takes (attention.cc:828-845): heads of up to 512 dimensions and every
+    group quant() gives, a multiple of 4 up to 1024 (quant.cc:59-67)."""
+    lib = sdhip.load()
+    vae = tensor(F32, (1, 1, 4096, 512))
+    y = tensor(F32, (1, 4096, 1, 512))
+    for tuning in ("bits=8", "bits=8,group=20", "bits=8,group=4", "bits=8,group=1024", "bits=8,group=3000"):
+        sdhip.set_tuning(tuning)
+        try:
+            assert lib.sdhip_attention_supported(vae, vae, vae, y, 0.0, 0.0), tuning
+            assert lib.sdhip_attention_work_size(vae, vae, vae, y) > 0, tuning
+        finally:
+            sdhip.set_tuning("")
+
+
 def test_attention_work_size():
     """The split form takes the keys and values split into tiles of 32 keys in
     the work buffer: per (image, head) and tile, the keys' two FP16 parts of

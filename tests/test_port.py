@@ -80,6 +80,23 @@ def test_attention(lq, lk, h, d, dv):
     assert np.array_equal(y1, y2)
 
 
+@pytest.mark.parametrize("lq,lk,h,hk,d,group", [(60, 988, 2, 2, 64, 64), (33, 300, 4, 2, 40, 32), (20, 700, 1, 1, 80, 128)])
+def test_quantized_attention(lq, lk, h, hk, d, group):
+    """The bits-mode attention of the CPU baseline: the oracle's algorithm
+    (its exponentials by the port's own polynomial, so a quantized byte may
+    differ by one step), within the reference's bound for quantized forms of
+    float64 and close to the oracle."""
+    r = rng(lk + d)
+    q, k, v = uniform(r, (2, lq, h, d), 1.0), uniform(r, (2, lk, hk, d), 1.0), uniform(r, (2, lk, hk, d), 1.0)
+    scale = float(1.0 / np.sqrt(d))
+    kb = max(group, 256 // group * group)
+    got = orc.port_quantized_attention(q, k, v, scale, group, key_block=kb, threads=4)
+    want = orc.quantized_attention(q, k, v, scale, group, key_block=kb)
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    assert orc.metric(got, exact, mag) <= 1e-2 * (2.0 / 255 + 1.0 / 127) / (2.0 / 255 + 1.0 / 127)
+    assert orc.metric(got, want, mag) <= 1e-3
+
+
 @pytest.mark.parametrize("silu", [False, True])
 def test_group_norm(silu):
     r = rng(5)
