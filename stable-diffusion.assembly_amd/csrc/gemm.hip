@@ -587,6 +587,263 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ MUL_MAT by panels
+
+// MUL_MAT where the output holds many panels of 64 tokens by 160 features (the
+// UNet's 64 x 64 level, configs[0]): a workgroup of 2 x 2 waves, each wave 32
+// tokens by 80 features as 2 x 5 tiles of v_mfma_f32_16x16x32_f16 with W as
+// operand A (features) and x as operand B (tokens, split), so that a lane
+// holds 4 consecutive features of one token and stores them as one float4.
+// K goes in chunks of 64 through two LDS buffers: each chunk of x (64 tokens
+// by 64, single precision, rows of 256 bytes) and of W (160 features by 64
+// halves, rows of 128 bytes) loaded by whole rows -- every load a full
+// 128-byte line -- into registers one chunk ahead, x split into its FP16
+// parts once for the workgroup, both written to LDS with each row's 16-byte
+// piece p at p ^ ((row >> 1) & 7), so that the 16 rows a fragment read
+// takes fall in 16 distinct groups of banks.  Rows past M and features past
+// N read the last row and are not stored.
+constexpr int kPanelTokens = 64, kPanelFeatures = 160, kPanelK = 64;
+
+__device__ __forceinline__ int panel_swizzle(int row) { return (row >> 1) & 7; }
+
+template <bool GENERIC>
+__global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
+    constexpr int BM = kPanelTokens, BN = kPanelFeatures, KC = kPanelK;
+    constexpr int TMW = 2, TNW = 5;                 // tiles of 16 a wave
+    constexpr int XQ = BM * (KC / 4) / 256;         // float4 of x a thread a chunk
+    constexpr int WQ = BN * (KC / 8) / 256;         // half8 of W a thread a chunk
+    static_assert(BM * (KC / 4) % 256 == 0 && BN * (KC / 8) % 256 == 0, "whole pieces a thread");
+    __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BM * KC];  // [buffer][hi, lo][token][k]
+    __shared__ __attribute__((aligned(16))) _Float16 lw[2][BN * KC];     // [buffer][feature][k]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave >> 1, wc = wave & 1;
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t m0 = static_cast<int64_t>(b / p.col_blocks) * BM;
+    const int64_t n0 = static_cast<int64_t>(b % p.col_blocks) * BN;
+    const int64_t chunks = p.K / KC;
+    const float *xs[XQ];
+    int xoff[XQ];
+#pragma unroll
+    for (int u = 0; u < XQ; ++u) {
+        const int idx = tid + 256 * u, r = idx >> 4, q = idx & 15;
+        const int64_t m = m0 + r < p.M ? m0 + r : p.M - 1;
+        xs[u] = p.x + m * p.ldx + 4 * q;
+        xoff[u] = r * KC + ((((q >> 1) ^ panel_swizzle(r)) << 3) | ((q & 1) << 2));
+    }
+    const _Float16 *ws[WQ];
+    int woff[WQ];
+#pragma unroll
+    for (int u = 0; u < WQ; ++u) {
+        const int idx = tid + 256 * u, r = idx >> 3, q = idx & 7;
+        const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
+        ws[u] = p.w + n * p.ldw + 8 * q;
+        woff[u] = r * KC + ((q ^ panel_swizzle(r)) << 3);
+    }
+    float4v xr[XQ];
+    half8 wg[WQ];
+    const auto load = [&](int64_t c) {
+#pragma unroll
+        for (int u = 0; u < XQ; ++u) xr[u] = *reinterpret_cast<const float4v *>(xs[u] + KC * c);
+#pragma unroll
+        for (int u = 0; u < WQ; ++u) wg[u] = *reinterpret_cast<const half8 *>(ws[u] + KC * c);
+    };
+    const auto store = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < XQ; ++u) {
+            half4 h, l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                _Float16 a, c;
+                split2(xr[u][e], a, c);
+                h[e] = a;
+                l[e] = c;
+            }
+            *reinterpret_cast<half4 *>(&lx[buf][0][xoff[u]]) = h;
+            *reinterpret_cast<half4 *>(&lx[buf][1][xoff[u]]) = l;
+        }
+#pragma unroll
+        for (int u = 0; u < WQ; ++u) *reinterpret_cast<half8 *>(&lw[buf][woff[u]]) = wg[u];
+    };
+    const int col = lane & 15, kq = lane >> 4;
+    float4v acc[TNW][TMW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j)
+#pragma unroll
+        for (int i = 0; i < TMW; ++i) acc[j][i] = float4v{};
+    load(0);
+    store(0);
+    lds_barrier();
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int buf = static_cast<int>(c & 1);
+        if (c + 1 < chunks) load(c + 1);
+#pragma unroll
+        for (int h = 0; h < KC / 32; ++h) {
+            half8 a[TNW], bh[TMW], bl[TMW];
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) {
+                const int r = wc * 16 * TNW + 16 * j + col;
+                a[j] = *reinterpret_cast<const half8 *>(&lw[buf][r * KC + (((4 * h + kq) ^ panel_swizzle(r)) << 3)]);
+            }
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) {
+                const int r = wr * 16 * TMW + 16 * i + col;
+                const int o = r * KC + (((4 * h + kq) ^ panel_swizzle(r)) << 3);
+                bh[i] = *reinterpret_cast<const half8 *>(&lx[buf][0][o]);
+                bl[i] = *reinterpret_cast<const half8 *>(&lx[buf][1][o]);
+            }
+            // Every tile's high parts, then every tile's low parts: no MFMA
+            // waits on the one just before it.
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bh[i], acc[j][i], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bl[i], acc[j][i], 0, 0, 0);
+        }
+        if (c + 1 < chunks) store(buf ^ 1);
+        lds_barrier();
+    }
+
+    // The epilogue: the lane's 2 tokens m and, per tile, 4 features n .. n +
+    // 3.  The chain a step at a time over all 10 tiles, every load of a step
+    // issued before any is used.  !GENERIC (the host's choice, panel_chain_fast):
+    // N whole panels, the output's rows and every operand contiguous along the
+    // features and 16-byte aligned at every row, or one number a token -- each
+    // read as float4 or once; GENERIC: any operand, element by element where
+    // it is neither.
+    const uint32_t ne1 = static_cast<uint32_t>(p.ne1), ne2 = static_cast<uint32_t>(p.ne2);
+    const bool whole = !GENERIC || n0 + BN <= p.N;
+    const bool vy = !GENERIC || (whole && p.ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0);
+    int64_t mc[TMW];
+    uint32_t i1[TMW], i2[TMW], i3[TMW];
+#pragma unroll
+    for (int i = 0; i < TMW; ++i) {
+        const int64_t m = m0 + wr * 16 * TMW + 16 * i + col;
+        mc[i] = m < p.M ? m : p.M - 1;
+        split_index(static_cast<uint32_t>(mc[i]), ne1, ne2, i1[i], i2[i], i3[i]);
+    }
+    int64_t nf[TNW];  // the tile's first feature (clamped: never past N - 4 where whole)
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) nf[j] = n0 + wc * 16 * TNW + 16 * j + 4 * kq;
+    float v[TMW][TNW][4];
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+#pragma unroll
+        for (int j = 0; j < TNW; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][j][e] = acc[j][i][e] * kSplitUp;
+    // Element e of tile (i, j) of a tensor of the output's rows ld apart.
+    const auto at = [&](int i, int j, int e) -> int64_t {
+        const int64_t n = nf[j] + e;
+        return mc[i] * p.ldy + (n < p.N ? n : p.N - 1);
+    };
+    if (p.from_redirect) {
+        float r[TMW][TNW][4];
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) {
+                if (vy) {
+                    const float4v q = *reinterpret_cast<const float4v *>(p.y + mc[i] * p.ldy + nf[j]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[i][j][e] = q[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[i][j][e] = p.y[at(i, j, e)];
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][j][e] = __fadd_rn(r[i][j][e], v[i][j][e]);
+    }
+#pragma unroll 1
+    for (int s = 0; s < p.chain.count; ++s) {
+        const DevStep &st = p.chain.steps[s];
+        if (st.kind == kSilu) {
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[i][j][e] = silu(v[i][j][e]);
+            continue;
+        }
+        const float *base[TMW];
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+            base[i] = st.operand + (st.flat123 ? mc[i] * st.nb[1] : i1[i] * st.nb[1] + i2[i] * st.nb[2] + i3[i] * st.nb[3]);
+        const bool rows16 = st.flat123 ? st.nb[1] % 4 == 0 : st.nb[1] % 4 == 0 && st.nb[2] % 4 == 0 && st.nb[3] % 4 == 0;
+        const bool vec = !GENERIC || (whole && st.nb[0] == 1 && rows16 && (reinterpret_cast<uintptr_t>(st.operand) & 15) == 0);
+        float o[TMW][TNW][4];
+        if (st.nb[0] == 0) {
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) {
+                const float bv = *base[i];
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[i][j][e] = bv;
+            }
+        } else if (vec) {
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j) {
+                    const float4v q = *reinterpret_cast<const float4v *>(base[i] + nf[j]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[i][j][e] = q[e];
+                }
+        } else if (GENERIC) {
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int64_t n = nf[j] + e;
+                        o[i][j][e] = base[i][(n < p.N ? n : p.N - 1) * st.nb[0]];
+                    }
+        }
+        if (st.kind == kAdd) {
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[i][j][e] = __fadd_rn(v[i][j][e], o[i][j][e]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[i][j][e] = __fmul_rn(v[i][j][e], o[i][j][e]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TMW; ++i) {
+        if (m0 + wr * 16 * TMW + 16 * i + col >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) {
+            if (vy) {
+                *reinterpret_cast<float4v *>(p.y + mc[i] * p.ldy + nf[j]) =
+                    float4v{v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (nf[j] + e < p.N) p.y[mc[i] * p.ldy + nf[j] + e] = v[i][j][e];
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ MUL_MAT split along K
 
 // Products of few output blocks and long K (the UNet's deepest level, 512
@@ -1161,6 +1418,49 @@ bool mul_mat_split_taken(const MulMatArgs &p) {
 
 size_t mul_mat_split_work_size(const MulMatArgs &p) {
     return static_cast<size_t>(mul_mat_split_plan(p).splits * p.M * p.N * 4);
+}
+
+bool mul_mat_panels_taken(const MulMatArgs &p, bool enabled) {
+    if (!enabled || p.w_scale != nullptr || p.half16) return false;
+    const bool aligned = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0 && p.ldw % 8 == 0 &&
+                         (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
+    // Enough panels for one a CU (measured: 256 and more, the 64 x 64 level's
+    // products; fewer take the 64 x 64 core and its split along K).
+    const int64_t panels = ((p.M + kPanelTokens - 1) / kPanelTokens) *
+                           ((p.N + kPanelFeatures - 1) / kPanelFeatures);
+    return aligned && p.K % kPanelK == 0 && panels >= 256;
+}
+
+namespace {
+
+// Whether the panels' fast epilogue takes this output and chain: N whole
+// panels, the output's rows and each operand either contiguous along the
+// features with rows 16-byte aligned, or one number a token.
+bool panel_chain_fast(const MulMatArgs &p) {
+    const auto aligned = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    if (p.N % kPanelFeatures != 0 || p.ldy % 4 != 0 || !aligned(p.y)) return false;
+    for (int s = 0; s < p.chain.count; ++s) {
+        const DevStep &st = p.chain.steps[s];
+        if (st.kind == kSilu || st.nb[0] == 0) continue;
+        const bool rows16 = st.flat123 ? st.nb[1] % 4 == 0 : st.nb[1] % 4 == 0 && st.nb[2] % 4 == 0 && st.nb[3] % 4 == 0;
+        if (st.nb[0] != 1 || !rows16 || !aligned(st.operand)) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+hipError_t launch_mul_mat_panels(const MulMatArgs &p, hipStream_t stream) {
+    MulMatArgs a = p;
+    a.col_blocks = (p.N + kPanelFeatures - 1) / kPanelFeatures;
+    const int64_t blocks = ((p.M + kPanelTokens - 1) / kPanelTokens) * a.col_blocks;
+    KernelScope scope("mul_mat", stream);
+    if (panel_chain_fast(a)) {
+        SDHIP_LAUNCH(mul_mat_panel_kernel<false>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, a);
+    } else {
+        SDHIP_LAUNCH(mul_mat_panel_kernel<true>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, a);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hipStream_t stream) {

@@ -58,6 +58,10 @@ struct Tuning {
     // makes (2), for comparison: the same bits, measured no faster.
     int gemm_core = 0;
     int qgemm_core = 2;
+    // This library's own: MUL_MAT of many output panels by the panel core (1)
+    // or by the 64 x 64 core everywhere (0), for comparison; results agree
+    // within the same bound.
+    int mul_mat_panels = 1;
     // This library's own: attention by its generic form (1) even where the
     // fast one takes the operands (0), for comparison; results agree within
     // the same bound.

@@ -49,6 +49,11 @@ struct GemmShape {
 };
 
 hipError_t launch_mul_mat(const MulMatArgs &p, GemmShape g, hipStream_t stream);
+// MUL_MAT by panels of 64 tokens by 160 features (FP16 weights, K a multiple
+// of 64, rows 16-byte aligned), where the output holds enough of them and
+// `enabled` (the mul_mat_panels tuning).
+bool mul_mat_panels_taken(const MulMatArgs &p, bool enabled);
+hipError_t launch_mul_mat_panels(const MulMatArgs &p, hipStream_t stream);
 hipError_t launch_mul_mat_gated(const MulMatArgs &p, GemmShape g, hipStream_t stream);
 
 // Single-precision weights [rows][k] (rows ld apart) split into two FP16

@@ -197,3 +197,58 @@ def test_gated_single_precision_weights(gpu, K, half, M):
     err = orc.metric(out.cpu().numpy(), exact, mag)
     print(f"gated single-precision weights {K}->2x{half} x {M}: {err:.3g}")
     assert err <= BOUND_SPLIT
+
+
+PANEL_CASES = [  # K, N, M, B: outputs of 256 panels of 64 tokens by 160 features and more
+    (320, 320, 4096, 2),   # whole panels: the fast epilogue
+    (640, 480, 4050, 2),   # ragged M (8100 tokens): rows past M read the last one
+    (384, 400, 8192, 1),   # ragged N: features past N, the general epilogue
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,N,M,B", PANEL_CASES)
+@pytest.mark.parametrize("form", ["bias_scale_residual", "from_redirect", "misaligned"])
+def test_mul_mat_panels(gpu, K, N, M, B, form):
+    """The panel core (mul_mat_panels, outputs of many panels) through both of
+    its epilogues: a bias, a per-token scale and a residual (contiguous, or
+    one number a token: the fast epilogue where N is whole panels); the sum
+    begun from the residual in the output's memory; an operand whose rows are
+    not 16-byte aligned (the general epilogue).  Against float64,
+    and within the same bound of the 64 x 64 core (mul_mat_panels=0)."""
+    r = rng(K + N + M)
+    bias = uniform(r, (N,), 1.0)
+    scale = uniform(r, (B, M, 1), 1.0)
+    res = uniform(r, (B, M, N), 1.0)
+    bias_d, scale_d, res_d = dev(bias, gpu), dev(scale, gpu), dev(res, gpu)
+    outs = []
+    for tuning in ("", "mul_mat_panels=0"):
+        sdhip.set_tuning(tuning)
+        try:
+            if form == "bias_scale_residual":
+                y, exact, mag = run_mul_mat(gpu, K, N, M, B, 3, [("add", bias_d), ("mul", scale_d), ("add", res_d)])
+                b, s = bias.astype(np.float64), scale.astype(np.float64)
+                want, m2 = (exact + b) * s + res, (mag + np.abs(b)) * np.abs(s) + np.abs(res)
+                got = y.cpu().numpy()
+            elif form == "from_redirect":
+                out = res_d.clone()
+                y, exact, mag = run_mul_mat(gpu, K, N, M, B, 3, [("add", bias_d)], redirect=out, from_redirect=True)
+                b = bias.astype(np.float64)
+                want, m2 = res + exact + b, np.abs(res) + mag + np.abs(b)
+                got = out.cpu().numpy()
+            else:
+                # The residual as a view one float into rows of N + 1: rows
+                # not 16-byte aligned, the general epilogue.
+                wide = np.zeros((B, M, N + 1), np.float32)
+                wide[..., 1:] = res
+                rv = dev(wide, gpu)[..., 1:]
+                y, exact, mag = run_mul_mat(gpu, K, N, M, B, 3, [("add", rv)])
+                want, m2 = exact + res, mag + np.abs(res)
+                got = y.cpu().numpy()
+        finally:
+            sdhip.set_tuning("")
+        err = orc.metric(got, want, m2)
+        print(f"panels {K}->{N} x {M}x{B} [{form}] {tuning or 'panels'}: {err:.3g}")
+        assert err <= BOUND_SPLIT
+        outs.append(got)
+    assert orc.metric(outs[0], outs[1], m2) <= BOUND_SPLIT
