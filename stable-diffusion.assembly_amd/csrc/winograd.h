@@ -26,6 +26,10 @@ struct WinogradArgs {
     int64_t tw, th, tiles;  // tiles across, down, of all images
     int32_t from_redirect;
     DevChain chain;
+    // Set by the launcher: the bytes of x from its first element past its
+    // last where F(4x4)'s inputs can be read by rows of whole quads (see
+    // winograd.hip), else 0.
+    uint32_t xbytes;
 };
 
 size_t winograd_work_size(const WinogradArgs &a);

@@ -335,9 +335,9 @@ __device__ __forceinline__ void weights_split_block(const W *__restrict__ w, int
         f = ldexpf(kSplitDown, ao + ec - E);
     }
     // Half of the points at a time: kRows / 2 x kWeightOc rows of `width`
-    // halves, 8 at a time.
+    // halves (64, or 32 in the last block of channels), 8 at a time.
     const int width = static_cast<int>(kp - c0 < kWeightIc ? kp - c0 : kWeightIc);
-    const int per_row = width / 8;
+    constexpr int kPerRow = kWeightIc / 8;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
         if (pass == 1) __syncthreads();  // the first half read out
@@ -350,11 +350,11 @@ __device__ __forceinline__ void weights_split_block(const W *__restrict__ w, int
             stage[2 * h + 1][ol][cl] = lo;
         }
         __syncthreads();
-        for (int q = tid; q < 2 * H * kWeightOc * per_row; q += 256) {
-            const int row = q / per_row;
-            const int k = (q - row * per_row) * 8;
+        for (int q = tid; q < 2 * H * kWeightOc * kPerRow; q += 256) {
+            const int row = q / kPerRow;
+            const int k = (q % kPerRow) * 8;
             const int r = 2 * H * pass + row / kWeightOc, oo = row % kWeightOc;
-            if (o0 + oo >= oc) continue;
+            if (k >= width || o0 + oo >= oc) continue;
             const int64_t cc = c0 + k;
             *reinterpret_cast<half8 *>(u + r * oc * kp + (cc >> 5) * oc * 32 + (o0 + oo) * 32 + (cc & 31)) =
                 *reinterpret_cast<const half8 *>(&stage[row / kWeightOc][oo][k]);
@@ -410,22 +410,18 @@ __global__ __launch_bounds__(256) void weights_scaled_kernel(const W *__restrict
 
 // ------------------------------------------------------------------ 2. inputs
 
-// (B^T d B) of the alpha x alpha inputs of a tile, zeros outside the image:
-// B^T d (a row r of B^T takes its combination of the rows of d), then each of
-// those times B.
+// The alpha x alpha inputs d of a tile, zeros outside the image, one load a
+// point.  Every load unconditional, from the nearest point inside the image,
+// and the points outside then cleared by masks of all ones or zeros.  The
+// masks pass through an empty asm so that the compiler sees no select of a
+// load, which it would turn back into a branch around each load.
 template <int M>
-__device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile, uint32_t c,
-                                            float (&v)[Mat<M>::A][Mat<M>::A]) {
+__device__ __forceinline__ void load_d(const WinogradArgs &a, uint32_t tx, uint32_t ty, uint32_t n, uint32_t c,
+                                       float (&d)[Mat<M>::A][Mat<M>::A]) {
     constexpr int A = Mat<M>::A;
-    uint32_t tx, ty, n;
-    split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
     const int64_t y0 = static_cast<int64_t>(ty) * M - a.p1;
     const int64_t x0 = static_cast<int64_t>(tx) * M - a.p0;
     const float *plane = a.x + static_cast<int64_t>(n) * a.xnb3 + static_cast<int64_t>(c) * a.xnb2;
-    // Every load unconditional, from the nearest point inside the image, and
-    // the points outside then cleared by masks of all ones or zeros.  The
-    // masks pass through an empty asm so that the compiler sees no select of
-    // a load, which it would turn back into a branch around each load.
     int64_t xc[A];
     int mask_col[A];
 #pragma unroll
@@ -435,7 +431,6 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
         asm("" : "+v"(mask_col[j]));
         xc[j] = xx < 0 ? 0 : (xx < a.iw ? xx : a.iw - 1);
     }
-    float d[A][A];
 #pragma unroll
     for (int i = 0; i < A; ++i) {
         const int64_t yy = y0 + i;
@@ -447,17 +442,97 @@ __device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile
             d[i][j] = __builtin_bit_cast(float, __builtin_bit_cast(int, row[xc[j]]) & (mask_row & mask_col[j]));
         }
     }
-    float bd[A][A];
+}
+
+// The same for F(4x4) where a.xbytes is set: the image's rows are runs of a
+// multiple of 4 floats, 16-byte aligned, the padding on the left is 1 and the
+// tiles end inside each row, so that a tile's columns 4 tx - 1 .. 4 tx + 4 are
+// one 16-byte load of the middle four and one 4-byte load on each side, all
+// at one row offset.  The loads go through a buffer resource over x's
+// a.xbytes bytes, whose range check returns zeros: a point outside the image
+// (a row above or below it, the column left of the first tile or right of
+// the last) is read at an offset past the end instead of being masked.
+__device__ __forceinline__ void load_d_quads(const WinogradArgs &a, uint32_t tx, uint32_t ty, uint32_t n, uint32_t c,
+                                             float (&d)[6][6]) {
+    constexpr uint32_t kPast = 0x80000000u;  // a.xbytes is below 2^31
+    const __amdgpu_buffer_rsrc_t x =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.x), 0, static_cast<int>(a.xbytes), 0x00020000);
+    const uint32_t col = 4 * tx;
+    const uint32_t plane = n * static_cast<uint32_t>(a.xnb3) + c * static_cast<uint32_t>(a.xnb2) + col;
+    const bool left = col > 0, right = col + 4 < static_cast<uint32_t>(a.iw);
+    const int y0 = static_cast<int>(ty) * 4 - a.p1;
 #pragma unroll
-    for (int r = 0; r < A; ++r)
+    for (int i = 0; i < 6; ++i) {
+        const int yy = y0 + i;
+        const bool inside = yy >= 0 && yy < static_cast<int>(a.ih);
+        const uint32_t off = (plane + static_cast<uint32_t>(yy) * static_cast<uint32_t>(a.xnb1)) * 4;
+        const uint32_t mid = inside ? off : kPast;
+        const float4v q = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(x, mid, 0, 0));
+        d[i][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x, inside && left ? off - 4 : kPast, 0, 0));
+        d[i][1] = q[0];
+        d[i][2] = q[1];
+        d[i][3] = q[2];
+        d[i][4] = q[3];
+        d[i][5] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x, inside && right ? off + 16 : kPast, 0, 0));
+    }
+}
+
+// One row or column of B^T d B: y = B^T t over six points.  F(4x4)'s B^T
+// (points 0, 1, -1, 2, -1/2, infinity) by its shared terms, 17 operations
+// where the rows' 26 nonzero coefficients would take 26:
+//   y0 = (t0 + t4) - 2 t2 + 1.5 (t1 - t3)     y3 = (t4 - t2) - 0.5 (t1 - t3)
+//   y1 = (t4 - t1) - 2.5 t2 - 0.5 t3          y4 = (t4 - t2) + 2 (t1 - t3)
+//   y2 = (t4 + t1) + 0.5 t2 - 2.5 t3          y5 = (t1 + t5) - 2 t3 + 1.5 (t2 - t4)
+__device__ __forceinline__ void bt4(float t0, float t1, float t2, float t3, float t4, float t5, float &y0,
+                                    float &y1, float &y2, float &y3, float &y4, float &y5) {
+    const float p = t1 - t3, q = t4 - t2;
+    y0 = fmaf(1.5f, p, fmaf(-2.0f, t2, t0 + t4));
+    y1 = fmaf(-0.5f, t3, fmaf(-2.5f, t2, t4 - t1));
+    y2 = fmaf(-2.5f, t3, fmaf(0.5f, t2, t4 + t1));
+    y3 = fmaf(-0.5f, p, q);
+    y4 = fmaf(2.0f, p, q);
+    y5 = fmaf(1.5f, t2 - t4, fmaf(-2.0f, t3, t1 + t5));
+}
+
+// (B^T d B) of the alpha x alpha inputs of a tile, zeros outside the image:
+// B^T d (a row r of B^T takes its combination of the rows of d), then each of
+// those times B.
+template <int M>
+__device__ __forceinline__ void transform_d(const WinogradArgs &a, uint32_t tile, uint32_t c,
+                                            float (&v)[Mat<M>::A][Mat<M>::A]) {
+    constexpr int A = Mat<M>::A;
+    uint32_t tx, ty, n;
+    split_index(tile, static_cast<uint32_t>(a.tw), static_cast<uint32_t>(a.th), tx, ty, n);
+    float d[A][A];
+    if constexpr (M == 4) {
+        if (a.xbytes != 0) {
+            load_d_quads(a, tx, ty, n, c, d);
+        } else {
+            load_d<M>(a, tx, ty, n, c, d);
+        }
+        float bd[6][6];
 #pragma unroll
-        for (int j = 0; j < A; ++j)
-            bd[r][j] = dot_n<A>([&](int i) { return Mat<M>::bt(r, i); }, [&](int i) { return d[i][j]; });
+        for (int j = 0; j < 6; ++j)
+            bt4(d[0][j], d[1][j], d[2][j], d[3][j], d[4][j], d[5][j], bd[0][j], bd[1][j], bd[2][j], bd[3][j],
+                bd[4][j], bd[5][j]);
 #pragma unroll
-    for (int r = 0; r < A; ++r)
+        for (int r = 0; r < 6; ++r)
+            bt4(bd[r][0], bd[r][1], bd[r][2], bd[r][3], bd[r][4], bd[r][5], v[r][0], v[r][1], v[r][2], v[r][3],
+                v[r][4], v[r][5]);
+    } else {
+        load_d<M>(a, tx, ty, n, c, d);
+        float bd[A][A];
 #pragma unroll
-        for (int s = 0; s < A; ++s)
-            v[r][s] = dot_n<A>([&](int j) { return Mat<M>::bt(s, j); }, [&](int j) { return bd[r][j]; });
+        for (int r = 0; r < A; ++r)
+#pragma unroll
+            for (int j = 0; j < A; ++j)
+                bd[r][j] = dot_n<A>([&](int i) { return Mat<M>::bt(r, i); }, [&](int i) { return d[i][j]; });
+#pragma unroll
+        for (int r = 0; r < A; ++r)
+#pragma unroll
+            for (int s = 0; s < A; ++s)
+                v[r][s] = dot_n<A>([&](int j) { return Mat<M>::bt(s, j); }, [&](int j) { return bd[r][j]; });
+    }
 }
 
 // V[xi][tile][ic] * 2^-e_c split into two FP16 parts, in blocks of 32
@@ -1255,9 +1330,21 @@ WorkLayout work_layout(const WinogradArgs &a) {
     return l;
 }
 
+// x's bytes from its first element past its last where F(4x4)'s inputs can
+// be read by rows of whole quads (load_d_quads), else 0.
+uint32_t quad_rows_bytes(const WinogradArgs &a) {
+    if (a.m != 4 || a.p0 != 1 || a.iw % 4 != 0 || a.tw * 4 > a.iw || a.xnb1 % 4 != 0 || a.xnb2 % 4 != 0 ||
+        a.xnb3 % 4 != 0 || a.xnb1 < a.iw || (reinterpret_cast<uintptr_t>(a.x) & 15) != 0)
+        return 0;
+    const int64_t floats = (a.n - 1) * a.xnb3 + (a.ic - 1) * a.xnb2 + (a.ih - 1) * a.xnb1 + a.iw;
+    return floats * 4 < (int64_t{1} << 31) - 64 ? static_cast<uint32_t>(floats * 4) : 0;
+}
+
 template <int M>
-sdhip_status run(const WinogradArgs &a, void *work, hipStream_t stream) {
+sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
     constexpr int A = Mat<M>::A;
+    WinogradArgs a = in;
+    a.xbytes = quad_rows_bytes(a);
     const char *tag = M == 4 ? "winograd4" : "winograd2";
     const WorkLayout l = work_layout(a);
     char *base = static_cast<char *>(work);
