@@ -1,8 +1,9 @@
 // Winograd's batched products, each wave's tiles on v_mfma_f32_32x32x16_f16:
 // C[b][m][n] = sum_k A[b][m][k] B[b][n][k], both operands two FP16 planes,
-// hi and lo, held in blocks of 32 of K ([k / 32][row][k % 32]: a row's 32
-// halves are 64 contiguous bytes), three MFMAs a product (a_hi b_hi +
-// a_lo b_hi + a_hi b_lo).
+// hi and lo, A held in blocks of 32 of K ([k / 32][row][k % 32]: a row's 32
+// halves are 64 contiguous bytes) and B in runs of 8 ([k / 8][row][k % 8]:
+// the 16 bytes of one run of consecutive rows are next to each other), three
+// MFMAs a product (a_hi b_hi + a_lo b_hi + a_hi b_lo).
 //
 // Shape.  A workgroup's 4 waves stand along N: wave w computes the block's
 // 32 TM rows of A (transformed weights, output channels) by its own 32 TN
@@ -10,9 +11,10 @@
 // each wave loads a quarter of a step's A into registers and writes it to
 // LDS, where all four read it; a wave's rows of B are its own, so they go
 // from memory straight into its registers in the MFMA's operand order (lane
-// l takes row l % 32 and the 16 bytes (l / 32) of each half of the row's
-// 64).  Of the 16 x 16 x 32 MFMA, a wave sustains about half the rate with
-// one wave a SIMD; of the 32 x 32 x 16, nearly all of it.
+// l takes row l % 32 and the run 2 h + l / 32 of the step's four, h the half
+// of the step: each 32 lanes read 512 contiguous bytes).  Of the 16 x 16 x
+// 32 MFMA, a wave sustains about half the rate with one wave a SIMD; of the
+// 32 x 32 x 16, nearly all of it.
 //
 // Pipeline.  Every load goes into registers S steps ahead of its MFMAs (S
 // register stages), and A's from its stage into one of two LDS buffers one
@@ -80,14 +82,15 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
         aoff[q] = plane * p.a_plane + grow * 32 + 8 * pc;
         adst[q] = plane * kPlaneA + row * kRowBytes + ((pc ^ swizzle(row)) << 4);
     }
-    // B: the lane's row of each tile j (clamped) and its 16 bytes of each
-    // half of the row.
+    // B: the lane's row of each tile j (clamped) in its run of each half of
+    // the step (runs half and 2 + half of the step's four, N rows of 8 apart).
     int64_t boff[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int64_t row = n0 + 32 * j + r32;
-        boff[j] = (row < p.N ? row : p.N - 1) * 32 + 8 * half;
+        boff[j] = (row < p.N ? row : p.N - 1) * 8 + half * p.N * 8;
     }
+    const int64_t b_half = 2 * p.N * 8;
 
     const int64_t steps = p.K / 32;
     const int64_t last = steps - 1;
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
             for (int pl = 0; pl < 2; ++pl)
 #pragma unroll
                 for (int hk = 0; hk < 2; ++hk)
-                    bv[stage][j][pl][hk] = *reinterpret_cast<const half8 *>(b + pl * p.b_plane + boff[j] + 16 * hk);
+                    bv[stage][j][pl][hk] = *reinterpret_cast<const half8 *>(b + pl * p.b_plane + boff[j] + hk * b_half);
     };
     const auto store_a = [&](int stage, int buf) {
 #pragma unroll

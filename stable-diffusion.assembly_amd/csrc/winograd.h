@@ -28,8 +28,11 @@ struct WinogradArgs {
     DevChain chain;
     // Set by the launcher: the bytes of x from its first element past its
     // last where F(4x4)'s inputs can be read by rows of whole quads (see
-    // winograd.hip), else 0.
+    // winograd.hip), else 0; and the transformed inputs' layout, in runs of
+    // 8 channels (1: [xi][part][kp / 8][tile][8], for the products whose
+    // waves load their own rows) or of 32 (0: [xi][part][kp / 32][tile][32]).
     uint32_t xbytes;
+    int32_t v_by8;
 };
 
 size_t winograd_work_size(const WinogradArgs &a);

@@ -583,6 +583,20 @@ __device__ __forceinline__ void inputs_split_block(const WinogradArgs &a, int64_
             stage[2 * h + 1][tl][cl] = lo;
         }
         __syncthreads();
+        if (a.v_by8) {
+            // Runs of 8 channels, [xp][kp / 8][tile][8]: consecutive threads
+            // consecutive tiles of one run.
+            for (int q = tid; q < 2 * H * kInTiles * (kInChannels / 8); q += 256) {
+                const int t = q % kInTiles;
+                const int run = (q / kInTiles) % (kInChannels / 8);
+                const int xl = q / (kInTiles * (kInChannels / 8));
+                if (t0 + t >= a.tiles) continue;
+                const int64_t xp = 2 * H * pass + xl;
+                *reinterpret_cast<half8 *>(v + ((xp * (kp / 8) + c0 / 8 + run) * a.tiles + t0 + t) * 8) =
+                    *reinterpret_cast<const half8 *>(&stage[xl][t][8 * run]);
+            }
+            continue;
+        }
         // 2 H * kInTiles rows of 32 halves, 8 at a time.
         for (int q = tid; q < 2 * H * kInTiles * (kInChannels / 8); q += 256) {
             const int row = q / (kInChannels / 8);
@@ -1446,6 +1460,41 @@ sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
     }
     _Float16 *uh = reinterpret_cast<_Float16 *>(u);
     _Float16 *vh = reinterpret_cast<_Float16 *>(v);
+    // The products' operands and core, chosen first: the inputs' transform
+    // writes V in the layout the core reads.
+    SplitBatchedArgs p{};
+    if (kept != nullptr) {
+        p.a32 = u_kept;
+        p.a_scale = f;
+        p.a_batch = a.oc * l.kp;
+    } else {
+        p.a = uh;
+        p.a_plane = a.oc * l.kp;
+        p.a_batch = 2 * p.a_plane;
+    }
+    p.b = vh;
+    p.b_plane = a.tiles * l.kp;
+    p.b_batch = 2 * p.b_plane;
+    p.c = m;
+    p.c_batch = a.oc * a.tiles;
+    p.M = a.oc;
+    p.N = a.tiles;
+    p.K = l.kp;
+    p.batches = A * A;
+    // gemm_core 0 (the default) chooses by the shape: the core whose waves
+    // load their own rows of B (gemm_core=3, four stages ahead) for grids of
+    // up to twelve workgroups a CU, where it was measured faster (the UNet's
+    // and the VAE's 64x64 .. 128x128 maps), the register-staged one (1) for
+    // larger.  Core 3 reads V in runs of 8 channels, so that a lane's 16
+    // bytes of a row are next to its neighbours'.
+    int core = tuning().gemm_core;
+    int stages = tuning().gemm_stages;
+    if (core == 0) {
+        const int64_t blocks3 = p.batches * ceil_div(p.M, 64) * ceil_div(p.N, 128);
+        core = split_batched2_takes(p) && blocks3 <= 12 * 256 ? 3 : 1;
+        if (core == 3) stages = 4;
+    }
+    a.v_by8 = core == 3 && split_batched2_takes(p) ? 1 : 0;
     if (kept == nullptr) {
         // Both transforms in one launch.
         KernelScope scope(names[5].c_str(), stream);
@@ -1474,37 +1523,6 @@ sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
     }
     {
         KernelScope scope(names[3].c_str(), stream);
-        SplitBatchedArgs p{};
-        if (kept != nullptr) {
-            p.a32 = u_kept;
-            p.a_scale = f;
-            p.a_batch = a.oc * l.kp;
-        } else {
-            p.a = uh;
-            p.a_plane = a.oc * l.kp;
-            p.a_batch = 2 * p.a_plane;
-        }
-        p.b = vh;
-        p.b_plane = a.tiles * l.kp;
-        p.b_batch = 2 * p.b_plane;
-        p.c = m;
-        p.c_batch = a.oc * a.tiles;
-        p.M = a.oc;
-        p.N = a.tiles;
-        p.K = l.kp;
-        p.batches = A * A;
-        // gemm_core 0 (the default) chooses by the shape: the core whose
-        // waves load their own rows of B (gemm_core=3, four stages ahead)
-        // for grids of up to twelve workgroups a CU, where it was measured
-        // faster (the UNet's and the VAE's 64x64 .. 128x128 maps), the
-        // register-staged one (1) for larger.
-        int core = tuning().gemm_core;
-        int stages = tuning().gemm_stages;
-        if (core == 0) {
-            const int64_t blocks3 = p.batches * ceil_div(p.M, 64) * ceil_div(p.N, 128);
-            core = split_batched2_takes(p) && blocks3 <= 12 * 256 ? 3 : 1;
-            if (core == 3) stages = 4;
-        }
         const hipError_t err = core == 2 && split_batched2_takes(p)
                                    ? launch_split_batched2(p, tuning().gemm_tiles, stages, stream)
                                : core == 3 && split_batched2_takes(p)
