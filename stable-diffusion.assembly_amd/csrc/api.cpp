@@ -126,6 +126,7 @@ const Field kFields[] = {
     {"gemm_tiles", &Tuning::gemm_tiles, kTiles},
     {"gemm_core", &Tuning::gemm_core, kCore},
     {"mul_mat_panels", &Tuning::mul_mat_panels, kFlag},
+    {"conv_panels", &Tuning::conv_panels, kFlag},
     {"qgemm_core", &Tuning::qgemm_core, kFlag2},
     {"attention_generic", &Tuning::attention_generic, kFlag},
     {"attention_fp32", &Tuning::attention_fp32, kFlag},

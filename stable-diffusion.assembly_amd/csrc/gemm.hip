@@ -844,6 +844,227 @@ __global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ 1x1 convolution by panels
+
+// The 1x1 convolution (stride 1, no padding) by the MUL_MAT panels' product,
+// C[oc][position] = sum_ic W[oc][ic] x[ic][position]: a workgroup's panel is
+// 64 positions of one image by 160 output channels, W operand A as MUL_MAT's
+// weights (channels), the image's columns operand B (positions, split).  A
+// chunk of 64 input channels of x comes in as rows of 64 positions (256
+// bytes), a thread 4 channels by 4 positions, transposed in registers and
+// written to LDS as [position][channel] with the panels' swizzle; the
+// outputs go back through LDS as [oc][position], so that the chain and the
+// stores take rows of 64 positions, a float4 a thread.  Channels past OC read
+// the last and are not stored.
+constexpr int kConvPanelPositions = 64, kConvPanelChannels = 160, kConvStageRow = 68, kConvPanelStages = 2;
+
+template <int NS>
+__global__ __launch_bounds__(512) void conv_panel_kernel(ConvArgs c) {
+    constexpr int BM = kConvPanelPositions, BN = kConvPanelChannels, KC = kPanelK;
+    constexpr int TNW = 5;                   // a wave's tiles of 16 channels, by one tile of 16 positions
+    constexpr int WQ = BN * (KC / 8) / 256;  // half8 of W a thread of the W waves a chunk
+    static_assert(BM * KC == 256 * 16 && BN * (KC / 8) % 256 == 0, "whole pieces a thread");
+    static_assert(BN * kConvStageRow * 4 <= (2 * 2 * BM * KC + 2 * BN * KC) * 2, "the outputs fit the operands' LDS");
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * BM * KC + 2 * BN * KC];
+    _Float16 (*lx)[2][BM * KC] = reinterpret_cast<_Float16 (*)[2][BM * KC]>(lds);  // [buffer][hi, lo][position][k]
+    _Float16 (*lw)[BN * KC] = reinterpret_cast<_Float16 (*)[BN * KC]>(lds + 2 * 2 * BM * KC);  // [buffer][oc][k]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Waves 0 .. 3 load x, 4 .. 7 W; wave w computes positions 16 (w & 3) ..
+    // by channels 80 (w >> 2) ...
+    const bool loads_x = wave < 4;
+    const int t = tid & 255;
+    const int wr = wave & 3, wc = wave >> 2;
+    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int64_t pos0 = static_cast<int64_t>(b / c.oc_blocks) * BM;
+    const int64_t oc0 = static_cast<int64_t>(b % c.oc_blocks) * BN;
+    const int64_t n = pos0 / c.plane, p0 = pos0 - n * c.plane;  // a panel lies in one image
+    const int64_t chunks = c.K / KC;
+    // x: the thread's 4 positions 4 pq .. and channels 4 kq + u, u = 0 .. 3.
+    const int pq = t & 15, kq = t >> 4;
+    const float *xs = c.x + n * c.xnb3 + static_cast<int64_t>(4 * kq) * c.xnb2 + p0 + 4 * pq;
+    int xoff[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int r = 4 * pq + e;
+        xoff[e] = r * KC + ((((kq >> 1) ^ panel_swizzle(r)) << 3) | ((kq & 1) << 2));
+    }
+    const _Float16 *ws[WQ];
+    int woff[WQ];
+#pragma unroll
+    for (int u = 0; u < WQ; ++u) {
+        const int idx = t + 256 * u, r = idx >> 3, q = idx & 7;
+        const int64_t o = oc0 + r < c.oc ? oc0 + r : c.oc - 1;
+        ws[u] = c.w + o * c.ldw + 8 * q;
+        woff[u] = r * KC + ((q ^ panel_swizzle(r)) << 3);
+    }
+    // NS register stages: at the top of chunk t, stage (t + q) % NS holds the
+    // loads of chunk t + q; chunks past the last repeat it, so that every load
+    // is unconditional.  A wave's stages hold x's or W's pieces, by its kind.
+    float4v xr[NS][4];
+    half8 wg[NS][WQ];
+    const auto load = [&](int st, int64_t ch) {
+        const int64_t k = ch < chunks ? ch : chunks - 1;
+        if (loads_x) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) xr[st][u] = *reinterpret_cast<const float4v *>(xs + (KC * k + u) * c.xnb2);
+        } else {
+#pragma unroll
+            for (int u = 0; u < WQ; ++u) wg[st][u] = *reinterpret_cast<const half8 *>(ws[u] + KC * k);
+        }
+    };
+    const auto store = [&](int st, int buf) {
+        if (loads_x) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                half4 h, l;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    _Float16 a, d;
+                    split2(xr[st][u][e], a, d);
+                    h[u] = a;
+                    l[u] = d;
+                }
+                *reinterpret_cast<half4 *>(&lx[buf][0][xoff[e]]) = h;
+                *reinterpret_cast<half4 *>(&lx[buf][1][xoff[e]]) = l;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < WQ; ++u) *reinterpret_cast<half8 *>(&lw[buf][woff[u]]) = wg[st][u];
+        }
+    };
+    const int col = lane & 15, kp = lane >> 4;
+    float4v acc[TNW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) acc[j] = float4v{};
+    const auto compute = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < KC / 32; ++h) {
+            half8 a[TNW];
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) {
+                const int r = wc * 16 * TNW + 16 * j + col;
+                a[j] = *reinterpret_cast<const half8 *>(&lw[buf][r * KC + (((4 * h + kp) ^ panel_swizzle(r)) << 3)]);
+            }
+            const int r = 16 * wr + col;
+            const int o = r * KC + (((4 * h + kp) ^ panel_swizzle(r)) << 3);
+            const half8 bh = *reinterpret_cast<const half8 *>(&lx[buf][0][o]);
+            const half8 bl = *reinterpret_cast<const half8 *>(&lx[buf][1][o]);
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bh, acc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bl, acc[j], 0, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int q = 0; q < NS; ++q) load(q, q);
+    store(0, 0);
+    lds_barrier();
+    // Passes of U chunks, U a multiple of NS and of 2, so that stages and
+    // buffers are the same at every pass: chunk t's MFMAs from buffer t % 2,
+    // chunk t + 1 into the other, the loads of chunk t + NS into the stage
+    // chunk t freed.
+    constexpr int U = NS % 2 == 0 ? NS : 2 * NS;
+    for (int64_t t0 = 0; t0 < chunks; t0 += U) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if (t0 + q < chunks) compute(q & 1);
+            store((q + 1) % NS, (q + 1) & 1);
+            load(q % NS, t0 + q + NS);
+            lds_barrier();
+        }
+    }
+
+    // The outputs into LDS, [oc][position] in rows of kConvStageRow floats
+    // (rows 4 apart fall 16 banks apart): the lane's 4 channels 4 kp .. of
+    // position col of each tile.
+    float *stage = reinterpret_cast<float *>(lds);
+#pragma unroll
+    for (int j = 0; j < TNW; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            stage[(wc * 16 * TNW + 16 * j + 4 * kp + e) * kConvStageRow + 16 * wr + col] = acc[j][e] * kSplitUp;
+    lds_barrier();
+    // A float4 of a row a thread at a time: channel r = f / 16, positions
+    // 4 (f % 16) ..; the residual in the output's memory first, then the
+    // chain a step at a time, every load of a step before any is used.
+    constexpr int RQ = BN * (BM / 4) / 512;
+    int64_t oc[RQ], pp[RQ];
+    float v[RQ][4];
+#pragma unroll
+    for (int u = 0; u < RQ; ++u) {
+        const int f = tid + 512 * u, r = f >> 4, q = f & 15;
+        oc[u] = oc0 + r < c.oc ? oc0 + r : c.oc - 1;
+        pp[u] = p0 + 4 * q;
+        const float4v t = *reinterpret_cast<const float4v *>(&stage[r * kConvStageRow + 4 * q]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = t[e];
+    }
+    float *out = c.y + n * c.ynb3;
+    if (c.from_redirect) {
+        float4v r[RQ];
+#pragma unroll
+        for (int u = 0; u < RQ; ++u) r[u] = *reinterpret_cast<const float4v *>(out + oc[u] * c.ynb2 + pp[u]);
+#pragma unroll
+        for (int u = 0; u < RQ; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[u][e] = __fadd_rn(r[u][e], v[u][e]);
+    }
+#pragma unroll 1
+    for (int s = 0; s < c.chain.count; ++s) {
+        const DevStep &st = c.chain.steps[s];
+        if (st.kind == kSilu) {
+#pragma unroll
+            for (int u = 0; u < RQ; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[u][e] = silu(v[u][e]);
+            continue;
+        }
+        const float *base = st.operand + n * st.nb[3];
+        float o[RQ][4];
+        if (st.nb[0] == 0 && st.nb[1] == 0) {
+            // One number a channel (the bias).
+#pragma unroll
+            for (int u = 0; u < RQ; ++u) {
+                const float q = base[oc[u] * st.nb[2]];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[u][e] = q;
+            }
+        } else if (st.nb[0] == 1 && st.flat01 && st.nb[2] % 4 == 0 && st.nb[3] % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(st.operand) & 15) == 0) {
+#pragma unroll
+            for (int u = 0; u < RQ; ++u) {
+                const float4v q = *reinterpret_cast<const float4v *>(base + oc[u] * st.nb[2] + pp[u]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[u][e] = q[e];
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < RQ; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t p = pp[u] + e, oy = p / c.ow, ox = p - oy * c.ow;
+                    o[u][e] = base[oc[u] * st.nb[2] + ox * st.nb[0] + oy * st.nb[1]];
+                }
+        }
+        if (st.kind == kAdd) {
+#pragma unroll
+            for (int u = 0; u < RQ; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[u][e] = __fadd_rn(v[u][e], o[u][e]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < RQ; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[u][e] = __fmul_rn(v[u][e], o[u][e]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < RQ; ++u) {
+        if (oc0 + ((tid + 512 * u) >> 4) >= c.oc) continue;
+        *reinterpret_cast<float4v *>(out + oc[u] * c.ynb2 + pp[u]) = float4v{v[u][0], v[u][1], v[u][2], v[u][3]};
+    }
+}
+
 // ------------------------------------------------------------------ MUL_MAT split along K
 
 // Products of few output blocks and long K (the UNet's deepest level, 512
@@ -1418,6 +1639,29 @@ bool mul_mat_split_taken(const MulMatArgs &p) {
 
 size_t mul_mat_split_work_size(const MulMatArgs &p) {
     return static_cast<size_t>(mul_mat_split_plan(p).splits * p.M * p.N * 4);
+}
+
+bool conv_panels_taken(const ConvArgs &c, bool enabled) {
+    const bool pointwise = c.kw == 1 && c.kh == 1 && c.s0 == 1 && c.s1 == 1 && c.p0 == 0 && c.p1 == 0;
+    if (!enabled || !pointwise || c.w_scale != nullptr || c.half16) return false;
+    // A panel's 64 positions lie in one image, in consecutive memory of x and
+    // of the output; every row 16-byte aligned.
+    const bool layout = c.plane % kConvPanelPositions == 0 && c.xnb1 == c.iw && c.ynb1 == c.ow &&
+                        c.xnb2 % 4 == 0 && c.xnb3 % 4 == 0 && c.ynb2 % 4 == 0 && c.ynb3 % 4 == 0 &&
+                        (reinterpret_cast<uintptr_t>(c.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(c.y) & 15) == 0 &&
+                        c.ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(c.w) & 15) == 0;
+    // Enough panels for one a CU, as MUL_MAT's.
+    const int64_t panels = (c.P / kConvPanelPositions) * ((c.oc + kConvPanelChannels - 1) / kConvPanelChannels);
+    return layout && c.K % kPanelK == 0 && panels >= 256;
+}
+
+hipError_t launch_conv_panels(const ConvArgs &c, hipStream_t stream) {
+    ConvArgs a = c;
+    a.oc_blocks = (c.oc + kConvPanelChannels - 1) / kConvPanelChannels;
+    const int64_t blocks = (c.P / kConvPanelPositions) * a.oc_blocks;
+    KernelScope scope("conv_direct_pointwise", stream);
+    SDHIP_LAUNCH(conv_panel_kernel<kConvPanelStages>, dim3(static_cast<uint32_t>(blocks)), dim3(512), 0, stream, a);
+    return hipGetLastError();
 }
 
 bool mul_mat_panels_taken(const MulMatArgs &p, bool enabled) {

@@ -62,6 +62,7 @@ struct Tuning {
     // or by the 64 x 64 core everywhere (0), for comparison; results agree
     // within the same bound.
     int mul_mat_panels = 1;
+    int conv_panels = 1;
     // This library's own: attention by its generic form (1) even where the
     // fast one takes the operands (0), for comparison; results agree within
     // the same bound.

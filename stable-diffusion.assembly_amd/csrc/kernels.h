@@ -102,6 +102,12 @@ struct ConvArgs {
 };
 
 hipError_t launch_conv_direct(const ConvArgs &c, GemmShape g, hipStream_t stream);
+// The 1x1 convolution by panels of 64 positions by 160 output channels
+// (FP16 kernels, IC a multiple of 64, positions of an image a multiple of 64
+// and contiguous in x and the output, rows 16-byte aligned), where the output
+// holds enough of them and `enabled` (the conv_panels tuning).
+bool conv_panels_taken(const ConvArgs &c, bool enabled);
+hipError_t launch_conv_panels(const ConvArgs &c, hipStream_t stream);
 
 // MUL_MAT split along K (gemm.hip): taken for products of fewer than 256
 // output blocks of 64 x 64 whose K (a multiple of 32) gives two splits of 8

@@ -260,6 +260,8 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
         const size_t need = conv_columns_work_size(c);
         if (const sdhip_status ws = check_work("conv2d", work, work_size, need); ws != SDHIP_OK) return ws;
         s = launched(launch_conv_columns(c, work, gemm_shape(), st), "conv2d by columns");
+    } else if (conv_panels_taken(c, tuning().conv_panels != 0)) {
+        s = launched(launch_conv_panels(c, st), "conv2d by panels");
     } else {
         s = launched(launch_conv_direct(c, gemm_shape(), st), "conv2d direct");
     }

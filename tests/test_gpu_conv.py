@@ -370,3 +370,58 @@ def test_winograd_products_without_lds(gpu, c, tuning):
     err = orc.metric(y.cpu().numpy(), exact, mag)
     print(f"conv {c} path {path} [{tuning}]: {err:.3g}")
     assert err <= BOUND
+
+
+CONV_PANEL_CASES = [  # w, h, ic, oc, n: 1x1 outputs of 256 panels of 64 positions by 160 channels and more
+    (32, 32, 640, 1280, 2),   # cfg3b's
+    (64, 64, 320, 200, 2),    # ragged OC: channels past OC read the last
+    (64, 64, 384, 320, 2),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", CONV_PANEL_CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("form", ["bias_scale_residual", "from_redirect_silu", "strided_residual"])
+def test_conv_panels(gpu, c, form):
+    """The 1x1 convolution by panels (conv_panels) through each form of its
+    chain: a bias (one number a channel), a scale per position and a residual
+    (rows of positions, a float4 at a time); the sum begun from the residual
+    in the output's memory, then SiLU; a residual whose rows are one float
+    longer than the image's (positions strided: element by element).  Against
+    float64, and within the same bound of the 64 x 64 core (conv_panels=0)."""
+    w_, h_, ic, oc, n = c
+    case = (w_, h_, ic, oc, 1, 1, 1, 1, 0, 0, 1, 1, n)
+    r = rng(ic + oc)
+    bias = uniform(r, (1, oc, 1, 1), 1.0)
+    scale = uniform(r, (1, 1, h_, w_), 1.0)
+    res = uniform(r, (n, oc, h_, w_), 1.0)
+    b_d, s_d, res_d = dev(bias, gpu), dev(scale, gpu), dev(res, gpu)
+    outs = []
+    for tuning in ("", "conv_panels=0"):
+        if form == "bias_scale_residual":
+            x, k32, y, path, p = conv_case(gpu, case, 11, [("add", b_d), ("mul", s_d), ("add", res_d)], tuning=tuning)
+            exact, mag = orc.exact_conv2d(x, k32, *p)
+            b, s = bias.astype(np.float64), scale.astype(np.float64)
+            want, m2 = (exact + b) * s + res, (mag + np.abs(b)) * np.abs(s) + np.abs(res)
+            got = y.cpu().numpy()
+        elif form == "from_redirect_silu":
+            out = res_d.clone()
+            x, k32, y, path, p = conv_case(gpu, case, 11, [("add", b_d), ("silu", None)], redirect=out,
+                                           from_redirect=True, tuning=tuning)
+            exact, mag = orc.exact_conv2d(x, k32, *p)
+            t = res + exact + bias.astype(np.float64)
+            want, m2 = t / (1.0 + np.exp(-t)), np.abs(res) + mag + np.abs(bias)
+            got = out.cpu().numpy()
+        else:
+            wide = np.zeros((n, oc, h_, w_ + 1), np.float32)
+            wide[..., :w_] = res
+            rv = dev(wide, gpu)[..., :w_]
+            x, k32, y, path, p = conv_case(gpu, case, 11, [("add", rv)], tuning=tuning)
+            exact, mag = orc.exact_conv2d(x, k32, *p)
+            want, m2 = exact + res, mag + np.abs(res)
+            got = y.cpu().numpy()
+        err = orc.metric(got, want, m2)
+        print(f"conv panels {c} [{form}] {tuning or 'panels'} path {path}: {err:.3g}")
+        assert err <= BOUND
+        outs.append(got)
+    assert orc.metric(outs[0], outs[1], m2) <= BOUND
