@@ -858,6 +858,11 @@ __global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
 // the last and are not stored.
 constexpr int kConvPanelPositions = 64, kConvPanelChannels = 160, kConvStageRow = 68, kConvPanelStages = 2;
 
+// The 16-byte piece p of x's LDS row r at p ^ conv_swizzle(r): 16 consecutive
+// rows (an MFMA operand's read) take 8 distinct swizzles among their even
+// rows and among their odd ones, and so do the rows 8 m + e of a write.
+__device__ __forceinline__ int conv_swizzle(int row) { return ((row >> 1) ^ (row >> 3)) & 7; }
+
 template <int NS>
 __global__ __launch_bounds__(512) void conv_panel_kernel(ConvArgs c) {
     constexpr int BM = kConvPanelPositions, BN = kConvPanelChannels, KC = kPanelK;
@@ -879,14 +884,17 @@ __global__ __launch_bounds__(512) void conv_panel_kernel(ConvArgs c) {
     const int64_t oc0 = static_cast<int64_t>(b % c.oc_blocks) * BN;
     const int64_t n = pos0 / c.plane, p0 = pos0 - n * c.plane;  // a panel lies in one image
     const int64_t chunks = c.K / KC;
-    // x: the thread's 4 positions 4 pq .. and channels 4 kq + u, u = 0 .. 3.
-    const int pq = t & 15, kq = t >> 4;
+    // x: the thread's 4 positions 4 pq .. and channels 4 kq + u, u = 0 .. 3,
+    // its e-th write to LDS position 4 pq + (e ^ (pq & 1)): the 32 lanes of a
+    // write then take rows of both parities, which conv_swizzle spreads over
+    // all 64 banks.
+    const int pq = t & 15, kq = t >> 4, par = pq & 1;
     const float *xs = c.x + n * c.xnb3 + static_cast<int64_t>(4 * kq) * c.xnb2 + p0 + 4 * pq;
     int xoff[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int r = 4 * pq + e;
-        xoff[e] = r * KC + ((((kq >> 1) ^ panel_swizzle(r)) << 3) | ((kq & 1) << 2));
+        const int r = 4 * pq + (e ^ par);
+        xoff[e] = r * KC + ((((kq >> 1) ^ conv_swizzle(r)) << 3) | ((kq & 1) << 2));
     }
     const _Float16 *ws[WQ];
     int woff[WQ];
@@ -920,7 +928,7 @@ __global__ __launch_bounds__(512) void conv_panel_kernel(ConvArgs c) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     _Float16 a, d;
-                    split2(xr[st][u][e], a, d);
+                    split2(par ? xr[st][u][e ^ 1] : xr[st][u][e], a, d);
                     h[u] = a;
                     l[u] = d;
                 }
@@ -946,7 +954,7 @@ __global__ __launch_bounds__(512) void conv_panel_kernel(ConvArgs c) {
                 a[j] = *reinterpret_cast<const half8 *>(&lw[buf][r * KC + (((4 * h + kp) ^ panel_swizzle(r)) << 3)]);
             }
             const int r = 16 * wr + col;
-            const int o = r * KC + (((4 * h + kp) ^ panel_swizzle(r)) << 3);
+            const int o = r * KC + (((4 * h + kp) ^ conv_swizzle(r)) << 3);
             const half8 bh = *reinterpret_cast<const half8 *>(&lx[buf][0][o]);
             const half8 bl = *reinterpret_cast<const half8 *>(&lx[buf][1][o]);
 #pragma unroll
