@@ -106,9 +106,11 @@ const char *sdhip_last_error(void);
  * half_format (bits=16's FP16 or bfloat16 products) is described with bits.  The reference's names take any int, as its
  * parser does, and are clamped where it clamps them (quant.cc:59-67).  This
  * library's own: winograd_fp32, winograd_splits, gemm_stages, gemm_tiles,
- * gemm_core, qgemm_core, attention_generic, attention_fp32 (forms to
- * compare, same results within the bounds -- qgemm_core's bit for bit),
- * each taking only its documented values.  Returns SDHIP_ERROR
+ * gemm_core, qgemm_core, mul_mat_panels and conv_panels (0: MUL_MAT and 1x1
+ * convolutions by the 64 x 64 core instead of the panel kernels),
+ * attention_generic, attention_fp32 (forms to compare, same results within
+ * the bounds -- qgemm_core's bit for bit), each taking only its documented
+ * values.  Returns SDHIP_ERROR
  * naming the first unknown name or refused value.  "" resets the defaults. */
 sdhip_status sdhip_set_tuning(const char *text);
 /* The value of one tuning field, or -1 if it has no such name. */
