@@ -106,8 +106,10 @@ const char *sdhip_last_error(void);
  * half_format (bits=16's FP16 or bfloat16 products) is described with bits.  The reference's names take any int, as its
  * parser does, and are clamped where it clamps them (quant.cc:59-67).  This
  * library's own: winograd_fp32, winograd_splits, gemm_stages, gemm_tiles,
- * gemm_core, qgemm_core, mul_mat_panels and conv_panels (0: MUL_MAT and 1x1
- * convolutions by the 64 x 64 core instead of the panel kernels),
+ * gemm_core, qgemm_core, mul_mat_panels (0: MUL_MAT by the 64 x 64 core
+ * instead of the panel kernels; 2: panels of 64 x 160 only, not 64 x 64),
+ * conv_panels (0:
+ * 1x1 convolutions by the 64 x 64 core),
  * attention_generic, attention_fp32 (forms to compare, same results within
  * the bounds -- qgemm_core's bit for bit), each taking only its documented
  * values.  Returns SDHIP_ERROR

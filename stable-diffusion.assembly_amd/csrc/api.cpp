@@ -67,7 +67,7 @@ namespace {
 // names take any integer, as its parser does (cpu.cc:180-212), and clamp or
 // read them as it does (quant.cc:53-67, winograd.cc:1204-1206): kAny.  This
 // library's own names take only the values they are documented with.
-enum Range { kAny, kFlag, kStages, kTiles, kNonNegative, kBits, kCore, kFlag2 };
+enum Range { kAny, kFlag, kStages, kTiles, kNonNegative, kBits, kCore, kFlag2, kPanels };
 
 struct Field {
     const char *name;
@@ -125,7 +125,7 @@ const Field kFields[] = {
     {"gemm_stages", &Tuning::gemm_stages, kStages},
     {"gemm_tiles", &Tuning::gemm_tiles, kTiles},
     {"gemm_core", &Tuning::gemm_core, kCore},
-    {"mul_mat_panels", &Tuning::mul_mat_panels, kFlag},
+    {"mul_mat_panels", &Tuning::mul_mat_panels, kPanels},
     {"conv_panels", &Tuning::conv_panels, kFlag},
     {"qgemm_core", &Tuning::qgemm_core, kFlag2},
     {"attention_generic", &Tuning::attention_generic, kFlag},
@@ -153,6 +153,9 @@ bool in_range(Range r, long v, const char *&takes) {
     case kFlag2:
         takes = "1 or 2";
         return v == 1 || v == 2;
+    case kPanels:
+        takes = "0, 1 or 2";
+        return v >= 0 && v <= 2;
     case kNonNegative:
         takes = "0 or more";
         return v >= 0 && v <= INT32_MAX;

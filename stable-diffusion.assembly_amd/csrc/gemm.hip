@@ -589,11 +589,14 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
 
 // ------------------------------------------------------------------ MUL_MAT by panels
 
-// MUL_MAT where the output holds many panels of 64 tokens by 160 features (the
-// UNet's 64 x 64 level, configs[0]): a workgroup of 2 x 2 waves, each wave 32
-// tokens by 80 features as 2 x 5 tiles of v_mfma_f32_16x16x32_f16 with W as
-// operand A (features) and x as operand B (tokens, split), so that a lane
-// holds 4 consecutive features of one token and stores them as one float4.
+// MUL_MAT where the output holds many panels of BM tokens by BN features: 64
+// by 160 (the UNet's 64 x 64 level, configs[0]), or 64 by 64 where those leave
+// too few (the 32 x 32 level).  A workgroup of 4
+// waves, BM / 32 along the tokens by 128 / BM along the features, each wave
+// 32 tokens by TNW tiles of 16 features as 2 x TNW tiles of
+// v_mfma_f32_16x16x32_f16 with W as operand A (features) and x as operand B
+// (tokens, split), so that a lane holds 4 consecutive features of one token
+// and stores them as one float4.
 // K goes in chunks of 64 through two LDS buffers: each chunk of x (64 tokens
 // by 64, single precision, rows of 256 bytes) and of W (160 features by 64
 // halves, rows of 128 bytes) loaded by whole rows -- every load a full
@@ -604,19 +607,29 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
 // N read the last row and are not stored.
 constexpr int kPanelTokens = 64, kPanelFeatures = 160, kPanelK = 64;
 
+// The panel shapes, by preference: the first that gives 256 panels or more.
+struct PanelShape {
+    int bm, bn;
+};
+// (Panels of 32 by 64 for the 16 x 16 level were measured slower there than
+// the 64 x 64 core split along K: the UNet step 11.52 -> 11.62 ms.)
+constexpr PanelShape kPanelShapes[] = {{64, 160}, {64, 64}};
+
 __device__ __forceinline__ int panel_swizzle(int row) { return (row >> 1) & 7; }
 
-template <bool GENERIC>
+template <bool GENERIC, int BM, int BN>
 __global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
-    constexpr int BM = kPanelTokens, BN = kPanelFeatures, KC = kPanelK;
-    constexpr int TMW = 2, TNW = 5;                 // tiles of 16 a wave
+    constexpr int KC = kPanelK;
+    constexpr int WR = BM / 32, WC = 4 / WR;        // waves along the tokens, the features
+    constexpr int TMW = 2, TNW = BN / (16 * WC);    // tiles of 16 a wave
     constexpr int XQ = BM * (KC / 4) / 256;         // float4 of x a thread a chunk
     constexpr int WQ = BN * (KC / 8) / 256;         // half8 of W a thread a chunk
     static_assert(BM * (KC / 4) % 256 == 0 && BN * (KC / 8) % 256 == 0, "whole pieces a thread");
+    static_assert(WR * WC == 4 && TNW * 16 * WC == BN, "the waves tile the panel");
     __shared__ __attribute__((aligned(16))) _Float16 lx[2][2][BM * KC];  // [buffer][hi, lo][token][k]
     __shared__ __attribute__((aligned(16))) _Float16 lw[2][BN * KC];     // [buffer][feature][k]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
+    const int wr = wave / WC, wc = wave % WC;
     const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(b / p.col_blocks) * BM;
     const int64_t n0 = static_cast<int64_t>(b % p.col_blocks) * BN;
@@ -1672,25 +1685,38 @@ hipError_t launch_conv_panels(const ConvArgs &c, hipStream_t stream) {
     return hipGetLastError();
 }
 
-bool mul_mat_panels_taken(const MulMatArgs &p, bool enabled) {
-    if (!enabled || p.w_scale != nullptr || p.half16) return false;
+namespace {
+
+// The index into kPanelShapes of the panels MUL_MAT takes, or -1: the first
+// shape whose panels are one a CU or more (fewer take the 64 x 64 core and its
+// split along K).  mode: the mul_mat_panels tuning (0 none, 1 every shape, 2
+// the first only).
+int panel_shape(const MulMatArgs &p, int mode) {
+    if (mode == 0 || p.w_scale != nullptr || p.half16) return -1;
     const bool aligned = p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) % 16) == 0 && p.ldw % 8 == 0 &&
                          (reinterpret_cast<uintptr_t>(p.w) % 16) == 0;
-    // Enough panels for one a CU (measured: 256 and more, the 64 x 64 level's
-    // products; fewer take the 64 x 64 core and its split along K).
-    const int64_t panels = ((p.M + kPanelTokens - 1) / kPanelTokens) *
-                           ((p.N + kPanelFeatures - 1) / kPanelFeatures);
-    return aligned && p.K % kPanelK == 0 && panels >= 256;
+    if (!aligned || p.K % kPanelK != 0) return -1;
+    const int shapes = mode == 1 ? 2 : 1;
+    for (int i = 0; i < shapes; ++i) {
+        const int64_t panels = ((p.M + kPanelShapes[i].bm - 1) / kPanelShapes[i].bm) *
+                               ((p.N + kPanelShapes[i].bn - 1) / kPanelShapes[i].bn);
+        if (panels >= 256) return i;
+    }
+    return -1;
 }
+
+}  // namespace
+
+bool mul_mat_panels_taken(const MulMatArgs &p, int mode) { return panel_shape(p, mode) >= 0; }
 
 namespace {
 
 // Whether the panels' fast epilogue takes this output and chain: N whole
 // panels, the output's rows and each operand either contiguous along the
 // features with rows 16-byte aligned, or one number a token.
-bool panel_chain_fast(const MulMatArgs &p) {
+bool panel_chain_fast(const MulMatArgs &p, int bn) {
     const auto aligned = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-    if (p.N % kPanelFeatures != 0 || p.ldy % 4 != 0 || !aligned(p.y)) return false;
+    if (p.N % bn != 0 || p.ldy % 4 != 0 || !aligned(p.y)) return false;
     for (int s = 0; s < p.chain.count; ++s) {
         const DevStep &st = p.chain.steps[s];
         if (st.kind == kSilu || st.nb[0] == 0) continue;
@@ -1702,17 +1728,33 @@ bool panel_chain_fast(const MulMatArgs &p) {
 
 }  // namespace
 
-hipError_t launch_mul_mat_panels(const MulMatArgs &p, hipStream_t stream) {
+namespace {
+
+template <int BM, int BN>
+hipError_t launch_panels(const MulMatArgs &p, hipStream_t stream) {
     MulMatArgs a = p;
-    a.col_blocks = (p.N + kPanelFeatures - 1) / kPanelFeatures;
-    const int64_t blocks = ((p.M + kPanelTokens - 1) / kPanelTokens) * a.col_blocks;
+    a.col_blocks = (p.N + BN - 1) / BN;
+    const dim3 grid(static_cast<uint32_t>(((p.M + BM - 1) / BM) * a.col_blocks));
     KernelScope scope("mul_mat", stream);
-    if (panel_chain_fast(a)) {
-        SDHIP_LAUNCH(mul_mat_panel_kernel<false>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, a);
+    if (panel_chain_fast(a, BN)) {
+        SDHIP_LAUNCH((mul_mat_panel_kernel<false, BM, BN>), grid, dim3(256), 0, stream, a);
     } else {
-        SDHIP_LAUNCH(mul_mat_panel_kernel<true>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_panel_kernel<true, BM, BN>), grid, dim3(256), 0, stream, a);
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_mul_mat_panels(const MulMatArgs &p, int mode, hipStream_t stream) {
+    switch (panel_shape(p, mode)) {
+    case 0:
+        return launch_panels<64, 160>(p, stream);
+    case 1:
+        return launch_panels<64, 64>(p, stream);
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hipStream_t stream) {

@@ -49,11 +49,12 @@ struct GemmShape {
 };
 
 hipError_t launch_mul_mat(const MulMatArgs &p, GemmShape g, hipStream_t stream);
-// MUL_MAT by panels of 64 tokens by 160 features (FP16 weights, K a multiple
-// of 64, rows 16-byte aligned), where the output holds enough of them and
-// `enabled` (the mul_mat_panels tuning).
-bool mul_mat_panels_taken(const MulMatArgs &p, bool enabled);
-hipError_t launch_mul_mat_panels(const MulMatArgs &p, hipStream_t stream);
+// MUL_MAT by panels of 64 tokens by 160 features, or 64 by 64 where those
+// leave too few (FP16 weights, K a multiple of 64, rows 16-byte aligned),
+// where the output holds 256 of them or more; `mode` is the mul_mat_panels
+// tuning (0 none, 1 either shape, 2 the 64 by 160 only).
+bool mul_mat_panels_taken(const MulMatArgs &p, int mode);
+hipError_t launch_mul_mat_panels(const MulMatArgs &p, int mode, hipStream_t stream);
 hipError_t launch_mul_mat_gated(const MulMatArgs &p, GemmShape g, hipStream_t stream);
 
 // Single-precision weights [rows][k] (rows ld apart) split into two FP16

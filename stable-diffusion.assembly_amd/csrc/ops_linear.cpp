@@ -118,8 +118,8 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
     } else if (a.w32 != nullptr) {
         s = split_into(a, work, work_size, st, "mul_mat");
         if (s == SDHIP_OK) s = launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
-    } else if (mul_mat_panels_taken(a, tuning().mul_mat_panels != 0)) {
-        s = launched(launch_mul_mat_panels(a, st), "mul_mat");
+    } else if (mul_mat_panels_taken(a, tuning().mul_mat_panels)) {
+        s = launched(launch_mul_mat_panels(a, tuning().mul_mat_panels, st), "mul_mat");
     } else if (mul_mat_split_taken(a)) {
         const size_t need = mul_mat_split_work_size(a);
         if (const sdhip_status ws = check_work("mul_mat", work, work_size, need); ws != SDHIP_OK) return ws;

@@ -199,10 +199,12 @@ def test_gated_single_precision_weights(gpu, K, half, M):
     assert err <= BOUND_SPLIT
 
 
-PANEL_CASES = [  # K, N, M, B: outputs of 256 panels of 64 tokens by 160 features and more
-    (320, 320, 4096, 2),   # whole panels: the fast epilogue
-    (640, 480, 4050, 2),   # ragged M (8100 tokens): rows past M read the last one
-    (384, 400, 8192, 1),   # ragged N: features past N, the general epilogue
+PANEL_CASES = [  # K, N, M, B: outputs of 256 panels and more, of 64 x 160 or 64 x 64
+    (320, 320, 4096, 2),   # 64 x 160, whole panels: the fast epilogue
+    (640, 480, 4050, 2),   # 64 x 160, ragged M (8100 tokens): rows past M read the last one
+    (384, 400, 8192, 1),   # 64 x 160, ragged N: features past N, the general epilogue
+    (640, 640, 1024, 2),   # 64 x 64 (the UNet's 32 x 32 level)
+    (2560, 600, 1000, 2),  # 64 x 64, long K, ragged M and N
 ]
 
 
