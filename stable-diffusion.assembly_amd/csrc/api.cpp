@@ -148,8 +148,8 @@ bool in_range(Range r, long v, const char *&takes) {
         takes = "0, 11, 12, 21, 22 or 41 (gemm_core=3)";
         return v == 0 || v == 11 || v == 12 || v == 21 || v == 22 || v == 41;
     case kCore:
-        takes = "0, 1, 2 or 3";
-        return v >= 0 && v <= 3;
+        takes = "0, 1 or 3";
+        return v == 0 || v == 1 || v == 3;
     case kFlag2:
         takes = "1 or 2";
         return v == 1 || v == 2;

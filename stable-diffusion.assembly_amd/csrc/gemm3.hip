@@ -197,8 +197,14 @@ hipError_t launch3(SplitBatchedArgs p, hipStream_t stream) {
 
 }  // namespace
 
+bool split_batched3_takes(const SplitBatchedArgs &p) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 &&
+                         p.a_plane % 8 == 0 && p.a_batch % 8 == 0 && p.b_plane % 8 == 0 && p.b_batch % 8 == 0;
+    return p.a32 == nullptr && aligned && p.K % 32 == 0 && p.K > 0 && p.M > 0 && p.N > 0;
+}
+
 hipError_t launch_split_batched3(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream) {
-    if (!split_batched2_takes(p)) return hipErrorInvalidValue;
+    if (!split_batched3_takes(p)) return hipErrorInvalidValue;
     const bool deep = stages == 4;
     switch (tiles) {
     case 22:

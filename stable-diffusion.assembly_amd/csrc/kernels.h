@@ -150,14 +150,11 @@ struct SplitBatchedArgs {
 
 hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream);
 
-// The same products with the copies into LDS made by global_load_lds
-// (gemm2.hip): both operands as two FP16 planes (a, not a32), K a multiple of
-// 32, every plane and batch 16-byte aligned.  `tiles` as GemmShape's (11, 12,
-// 21, 22 for blocks of 64 WM x 64 WN), or 0 to choose by the size.
-bool split_batched2_takes(const SplitBatchedArgs &p);
-hipError_t launch_split_batched2(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream);
-// The same products with no LDS (gemm3.hip): each wave's operands loaded
-// straight into its registers; the same operands as split_batched2_takes.
+// The same products by waves that load their own rows of B straight into
+// their registers (gemm3.hip): both operands as two FP16 planes (a, not a32),
+// B in runs of 8 of K, K a multiple of 32, every plane and batch 16-byte
+// aligned.  `tiles` 22, 41, 12 or 0 (64 x 128 blocks).
+bool split_batched3_takes(const SplitBatchedArgs &p);
 hipError_t launch_split_batched3(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream);
 
 }  // namespace sdhip

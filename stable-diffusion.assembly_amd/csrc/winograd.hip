@@ -1491,10 +1491,10 @@ sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
     int stages = tuning().gemm_stages;
     if (core == 0) {
         const int64_t blocks3 = p.batches * ceil_div(p.M, 64) * ceil_div(p.N, 128);
-        core = split_batched2_takes(p) && blocks3 <= 12 * 256 ? 3 : 1;
+        core = split_batched3_takes(p) && blocks3 <= 12 * 256 ? 3 : 1;
         if (core == 3) stages = 4;
     }
-    a.v_by8 = core == 3 && split_batched2_takes(p) ? 1 : 0;
+    a.v_by8 = core == 3 && split_batched3_takes(p) ? 1 : 0;
     if (kept == nullptr) {
         // Both transforms in one launch.
         KernelScope scope(names[5].c_str(), stream);
@@ -1523,9 +1523,7 @@ sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
     }
     {
         KernelScope scope(names[3].c_str(), stream);
-        const hipError_t err = core == 2 && split_batched2_takes(p)
-                                   ? launch_split_batched2(p, tuning().gemm_tiles, stages, stream)
-                               : core == 3 && split_batched2_takes(p)
+        const hipError_t err = core == 3 && split_batched3_takes(p)
                                    ? launch_split_batched3(p, tuning().gemm_tiles, stages, stream)
                                    : launch_split_batched(p, gemm_shape(), stream);
         if (err != hipSuccess) return launched(err, "winograd products");

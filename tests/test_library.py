@@ -74,11 +74,12 @@ def test_tuning_takes_every_reference_name_and_checks_its_own():
         sdhip.set_tuning("conv_kc=128,amx_fp16=0,fuse_residual=0,todo=2,todo_tokens=100,group=1000,bits=3")
         assert sdhip.get_tuning("conv_kc") == 128 and sdhip.get_tuning("todo_tokens") == 100
         for bad in ("gemm_stages=3", "gemm_tiles=13", "winograd_fp32=2", "attention_fp32=-1", "attention_generic=5",
-                    "winograd_splits=-2", "fuse=99999999999", "gemm_core=4"):
+                    "winograd_splits=-2", "fuse=99999999999", "gemm_core=4", "gemm_core=2",
+                    "mul_mat_panels=3", "conv_panels=2"):
             with pytest.raises(sdhip.SdhipError):
                 sdhip.set_tuning(bad)
         for good in ("gemm_stages=4", "gemm_tiles=21", "gemm_tiles=12", "gemm_core=1", "gemm_core=0", "gemm_core=3", "winograd_fp32=1", "winograd_splits=3", "bits=8",
-                     "bits=16"):
+                     "bits=16", "mul_mat_panels=2", "conv_panels=0"):
             sdhip.set_tuning(good)
     finally:
         sdhip.set_tuning("")
