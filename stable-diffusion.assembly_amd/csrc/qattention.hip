@@ -429,11 +429,20 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
     const int32_t *ksum = a.ksum + head_k * a.lkp;
 
     // First pass: the greatest score of each query over the keys.
-    // Tiles wholly of keys take no test per key.
+    // Tiles wholly of keys take no test per key, four at a time with every
+    // load of the four issued first.
     float top = -INFINITY;
     const int64_t whole = a.lk / 16;
     const int64_t tiles = (a.lk + 15) / 16;
-    for (int64_t kt = 0; kt < tiles; ++kt) {
+    int64_t kt0 = 0;
+    for (; kt0 + 4 <= whole; kt0 += 4) {
+        float4v sc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sc[u] = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, 16 * (kt0 + u), lr, lg);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) top = fmaxf(fmaxf(top, fmaxf(sc[u][0], sc[u][1])), fmaxf(sc[u][2], sc[u][3]));
+    }
+    for (int64_t kt = kt0; kt < tiles; ++kt) {
         const float4v sc = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, 16 * kt, lr, lg);
         if (kt < whole) {
             top = fmaxf(fmaxf(top, fmaxf(sc[0], sc[1])), fmaxf(sc[2], sc[3]));
@@ -472,10 +481,35 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
             const int64_t rel0 = p * kPart;
             const int64_t end = gbase + rel0 + kPart;
             const bool plain = a.group % 16 == 0 && rel0 + kPart <= a.group && end <= a.lk && end <= a.tail_from;
+            if (plain) {
+                // Whole tiles of keys, none past tail_from: every tile's
+                // scores (their loads issued together), then Cephes'
+                // exponential of each in one straight run, then the
+                // statistics in the order of the keys.
+                float4v sc[GT];
+#pragma unroll
+                for (int kt = 0; kt < GT; ++kt)
+                    sc[kt] = qa_scores<SUBS>(a, kq, ks, ko, ksum, qbv, qs, qo, gbase + rel0 + 16 * kt, lr, lg);
+#pragma unroll
+                for (int kt = 0; kt < GT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) e[kt][r] = cephes_exp(__fsub_rn(sc[kt][r], top));
+                if (stats) {
+#pragma unroll
+                    for (int kt = 0; kt < GT; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            total += static_cast<double>(e[kt][r]);
+                            lo = fminf(lo, e[kt][r]);
+                            hi = fmaxf(hi, e[kt][r]);
+                        }
+                }
+                return;
+            }
 #pragma unroll
             for (int kt = 0; kt < GT; ++kt) {
                 const int64_t rel = rel0 + 16 * kt;  // the tile's first key, in the group
-                if (!plain && (rel >= a.group || gbase + rel >= a.lk)) {
+                if (rel >= a.group || gbase + rel >= a.lk) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) e[kt][r] = 0.0f;
                     continue;
@@ -485,13 +519,9 @@ __global__ __launch_bounds__(256) void qa_attention_kernel(QAttentionArgs a) {
                 for (int r = 0; r < 4; ++r) {
                     const int64_t jr = rel + 4 * lg + r;
                     const int64_t j = gbase + jr;
-                    const bool key = plain || (jr < a.group && j < a.lk);
+                    const bool key = jr < a.group && j < a.lk;
                     float x = 0.0f;
-                    if (plain) {
-                        // Whole tiles of keys, none past tail_from: Cephes'
-                        // exponential for each, no test per key.
-                        x = cephes_exp(__fsub_rn(sc[r], top));
-                    } else if (key) {
+                    if (key) {
                         const float arg = __fsub_rn(sc[r], top);
                         x = j < a.tail_from ? cephes_exp(arg) : static_cast<float>(exp(static_cast<double>(arg)));
                     }
