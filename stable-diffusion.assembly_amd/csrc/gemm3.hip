@@ -26,6 +26,12 @@
 // products are never stored), steps past the last repeat it, so that the
 // compiler's counts of the loads in flight are the same on every path.
 //
+// A32: A in single precision instead (the transformed weights kept in the
+// store, [batch][row][K]), each column k times a_scale[k]: a wave loads its
+// groups of 16 rows, a lane 8 consecutive columns of one row, scales and
+// splits them on their way into LDS, as the register-staged core does
+// (bit-identical parts).
+//
 // LDS layout of a buffer: per plane, the block's 32 TM rows of 64 bytes, the
 // 16-byte piece p of row r at piece p ^ s(r), s(r) = ((r >> 1) ^ (r >> 2)) & 3,
 // so that the 32 rows a fragment read takes spread over every bank whether
@@ -43,11 +49,14 @@ constexpr int kRowBytes = 64;  // a row's 32 halves of one plane and K-step
 
 __device__ __forceinline__ int swizzle(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
-template <int TM, int TN, int S>
+template <int TM, int TN, int S, bool A32>
 __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p) {
     constexpr int kPlaneA = 32 * TM * kRowBytes;  // bytes of one plane of a step of A
     constexpr int kBuf = 2 * kPlaneA;
-    constexpr int CA = TM;                        // a wave's 1 KB pieces of A a step
+    // A wave's 1 KB pieces of A a step (A32: its groups of 16 rows, each both
+    // planes' pieces).
+    constexpr int CA = A32 ? TM / 2 : TM;
+    static_assert(!A32 || TM % 2 == 0, "A32 takes blocks of 64 rows or more");
     __shared__ __attribute__((aligned(1024))) char lds[2 * kBuf];
 
     const int tid = threadIdx.x;
@@ -65,8 +74,9 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
     const int64_t n0 = (4 * nb + wave) * 32 * TN;
 
     const _Float16 *A = p.a + batch * p.a_batch;
+    const float *A32p = p.a32 + batch * p.a_batch;
     const _Float16 *B = p.b + batch * p.b_batch;
-    const int64_t a_step = p.M * 32, b_step = p.N * 32;
+    const int64_t a_step = A32 ? 32 : p.M * 32, b_step = p.N * 32;
 
     // A: piece g = wave + 4 q of the 4 TM pieces of a step (plane g / (2 TM),
     // rows 16 (g % (2 TM)) ..), the lane's row lane / 4 and 16 bytes lane % 4
@@ -76,12 +86,13 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
 #pragma unroll
     for (int q = 0; q < CA; ++q) {
         const int g = wave + 4 * q;
-        const int plane = g / (2 * TM), u = g % (2 * TM);
+        const int plane = A32 ? 0 : g / (2 * TM), u = A32 ? g : g % (2 * TM);
         const int row = 16 * u + (lane >> 2), pc = lane & 3;
         const int64_t grow = m0 + row < p.M ? m0 + row : p.M - 1;
-        aoff[q] = plane * p.a_plane + grow * 32 + 8 * pc;
+        aoff[q] = A32 ? grow * p.K + 8 * pc : plane * p.a_plane + grow * 32 + 8 * pc;
         adst[q] = plane * kPlaneA + row * kRowBytes + ((pc ^ swizzle(row)) << 4);
     }
+    const float *fcol = p.a_scale + 8 * (lane & 3);  // A32: the lane's columns' scales
     // B: the lane's row of each tile j (clamped) in its run of each half of
     // the step (runs half and 2 + half of the step's four, N rows of 8 apart).
     int64_t boff[TN];
@@ -94,13 +105,26 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
 
     const int64_t steps = p.K / 32;
     const int64_t last = steps - 1;
-    half8 av[S][CA];
+    half8 av[S][A32 ? 1 : CA];
+    float4v aw[S][A32 ? CA : 1][2];  // A32: a lane's 8 numbers of each group
+    float4v fw[S][2];                // A32: their columns' scales
     half8 bv[S][TN][2][2];  // [stage][tile][plane][half of k]
     const auto load = [&](int stage, int64_t s) {
         const int64_t k = s < last ? s : last;
-        const _Float16 *a = A + k * a_step;
+        if constexpr (A32) {
+            const float *a = A32p + k * a_step;
 #pragma unroll
-        for (int q = 0; q < CA; ++q) av[stage][q] = *reinterpret_cast<const half8 *>(a + aoff[q]);
+            for (int q = 0; q < CA; ++q) {
+                aw[stage][q][0] = *reinterpret_cast<const float4v *>(a + aoff[q]);
+                aw[stage][q][1] = *reinterpret_cast<const float4v *>(a + aoff[q] + 4);
+            }
+            fw[stage][0] = *reinterpret_cast<const float4v *>(fcol + k * 32);
+            fw[stage][1] = *reinterpret_cast<const float4v *>(fcol + k * 32 + 4);
+        } else {
+            const _Float16 *a = A + k * a_step;
+#pragma unroll
+            for (int q = 0; q < CA; ++q) av[stage][q] = *reinterpret_cast<const half8 *>(a + aoff[q]);
+        }
         const _Float16 *b = B + k * b_step;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -111,8 +135,24 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
                     bv[stage][j][pl][hk] = *reinterpret_cast<const half8 *>(b + pl * p.b_plane + boff[j] + hk * b_half);
     };
     const auto store_a = [&](int stage, int buf) {
+        if constexpr (A32) {
 #pragma unroll
-        for (int q = 0; q < CA; ++q) *reinterpret_cast<half8 *>(lds + buf * kBuf + adst[q]) = av[stage][q];
+            for (int q = 0; q < CA; ++q) {
+                half8 h, l;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    _Float16 x, y;
+                    split2(aw[stage][q][e >> 2][e & 3] * fw[stage][e >> 2][e & 3], x, y);
+                    h[e] = x;
+                    l[e] = y;
+                }
+                *reinterpret_cast<half8 *>(lds + buf * kBuf + adst[q]) = h;
+                *reinterpret_cast<half8 *>(lds + buf * kBuf + kPlaneA + adst[q]) = l;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < CA; ++q) *reinterpret_cast<half8 *>(lds + buf * kBuf + adst[q]) = av[stage][q];
+        }
     };
 
     float16v acc[TM][TN];
@@ -191,21 +231,31 @@ hipError_t launch3(SplitBatchedArgs p, hipStream_t stream) {
     p.m_blocks = (p.M + 32 * TM - 1) / (32 * TM);
     p.n_blocks = (p.N + 128 * TN - 1) / (128 * TN);
     const dim3 grid(static_cast<uint32_t>(p.batches * p.m_blocks * p.n_blocks));
-    SDHIP_LAUNCH((split_batched3_kernel<TM, TN, S>), grid, dim3(256), 0, stream, p);
+    if constexpr (TM % 2 == 0) {
+        if (p.a32 != nullptr) {
+            SDHIP_LAUNCH((split_batched3_kernel<TM, TN, S, true>), grid, dim3(256), 0, stream, p);
+            return hipGetLastError();
+        }
+    }
+    SDHIP_LAUNCH((split_batched3_kernel<TM, TN, S, false>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
 }  // namespace
 
 bool split_batched3_takes(const SplitBatchedArgs &p) {
-    const bool aligned = (reinterpret_cast<uintptr_t>(p.a) % 16) == 0 && (reinterpret_cast<uintptr_t>(p.b) % 16) == 0 &&
-                         p.a_plane % 8 == 0 && p.a_batch % 8 == 0 && p.b_plane % 8 == 0 && p.b_batch % 8 == 0;
-    return p.a32 == nullptr && aligned && p.K % 32 == 0 && p.K > 0 && p.M > 0 && p.N > 0;
+    const auto al16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) % 16) == 0; };
+    const bool b_ok = al16(p.b) && p.b_plane % 8 == 0 && p.b_batch % 8 == 0;
+    const bool a_ok = p.a32 != nullptr ? al16(p.a32) && al16(p.a_scale) && p.a_batch % 4 == 0
+                                       : al16(p.a) && p.a_plane % 8 == 0 && p.a_batch % 8 == 0;
+    return a_ok && b_ok && p.K % 32 == 0 && p.K > 0 && p.M > 0 && p.N > 0;
 }
 
 hipError_t launch_split_batched3(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream) {
     if (!split_batched3_takes(p)) return hipErrorInvalidValue;
     const bool deep = stages == 4;
+    // A32 takes blocks of 64 rows or more: tiles=12 (32 rows) takes the default.
+    if (p.a32 != nullptr && tiles == 12) tiles = 0;
     switch (tiles) {
     case 22:
         return deep ? launch3<2, 2, 4>(p, stream) : launch3<2, 2, 3>(p, stream);

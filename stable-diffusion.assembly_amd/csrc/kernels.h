@@ -151,9 +151,10 @@ struct SplitBatchedArgs {
 hipError_t launch_split_batched(const SplitBatchedArgs &p, GemmShape g, hipStream_t stream);
 
 // The same products by waves that load their own rows of B straight into
-// their registers (gemm3.hip): both operands as two FP16 planes (a, not a32),
-// B in runs of 8 of K, K a multiple of 32, every plane and batch 16-byte
-// aligned.  `tiles` 22, 41, 12 or 0 (64 x 128 blocks).
+// their registers (gemm3.hip): B as two FP16 planes in runs of 8 of K, A as
+// two FP16 planes or in single precision (a32, split on its way into LDS), K
+// a multiple of 32, every plane and batch 16-byte aligned.  `tiles` 22, 41,
+// 12 (not with a32) or 0 (64 x 128 blocks).
 bool split_batched3_takes(const SplitBatchedArgs &p);
 hipError_t launch_split_batched3(const SplitBatchedArgs &p, int tiles, int stages, hipStream_t stream);
 
