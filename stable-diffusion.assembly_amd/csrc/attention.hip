@@ -836,7 +836,23 @@ struct Split {
     static constexpr int kCopies = kRecord / 1024;                      // 1 KB copies of a tile
     static constexpr int kPerWave = (kCopies + 3) / 4;
     static constexpr int kQueries = 128;  // a workgroup's
+    // D = 16 n + 8: the scores' last step has 8 dimensions, and the keys' low
+    // parts of those fill its other 8 (the keys' first plane holds l at
+    // columns D .. D + 7 for dimensions D - 8 .. D - 1), so that the step
+    // takes two MFMAs: h h' into the first accumulator, and (h l' + l h')
+    // into the second from a lane of the upper half holding h' of the
+    // dimension 8 below its own.
+    static constexpr bool kHalfStep = D % 16 == 8;
+    // The values' last tile of 32 dimensions holds kVLast of them; at 16 or
+    // fewer its low parts go to its own spare rows kVLast .. 2 kVLast - 1 of
+    // the first plane, and it takes two MFMAs (h + l) h' where the others
+    // take three.  With 8 more rows spare those hold ones times 2^-4, so
+    // that the MFMAs sum the exponentials beside the outputs.
+    static constexpr int kVLast = D - 32 * (kDvt - 1);
+    static constexpr bool kPackV = kVLast <= 16;
+    static constexpr bool kSumRow = kPackV && 2 * kVLast + 8 <= 32;
     static_assert(D % 8 == 0 && KB % 32 == 0, "shape");
+    static_assert(!kHalfStep || kDp == D + 8, "the keys' low parts fill the last step's padding");
     static_assert((kLdk / 8) % 2 == 1 && (kLdv / 8) % 2 == 1, "rows of an odd number of 16-byte units");
 };
 
@@ -860,6 +876,8 @@ __device__ __forceinline__ int key_of_column(int c) {
 // The keys of tile kt of (image bi, key head kh) split into their two parts,
 // [KB][kLdk] twice, into `rec` (the work buffer's record or an LDS buffer),
 // by the workgroup's threads: a thread a key's four dimensions, float4 loads.
+// With kHalfStep the first plane's columns D .. D + 7 take the low parts of
+// dimensions D - 8 .. D - 1 (the second plane's are never read).
 template <int D, int KB>
 __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, int64_t kh, int64_t kt, _Float16 *rec) {
     using S = Split<D, KB>;
@@ -867,9 +885,11 @@ __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, i
     for (int idx = threadIdx.x; idx < KB * (S::kLdk / 4); idx += 256) {
         const int j = idx / (S::kLdk / 4);
         const int c4 = idx - j * (S::kLdk / 4);
+        const bool slot = S::kHalfStep && 4 * c4 >= D && 4 * c4 < D + 8;
+        const int src = slot ? 4 * c4 - 8 : 4 * c4;
         const int64_t key = kt * KB + j;
         float4v x = float4v{};
-        if (key < a.lk && 4 * c4 < D) x = *reinterpret_cast<const float4v *>(kg + key * a.knb1 + 4 * c4);
+        if (key < a.lk && src < D) x = *reinterpret_cast<const float4v *>(kg + key * a.knb1 + src);
         half4a h, l;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -878,7 +898,7 @@ __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, i
             h[r] = hh;
             l[r] = ll;
         }
-        *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = h;
+        *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = slot ? l : h;
         *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
     }
 }
@@ -886,7 +906,9 @@ __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, i
 // The values of tile kt split and transposed, [kDvp][kLdv] twice after the
 // keys' planes of `rec`, a thread four columns (four keys, in the order of
 // key_of_column) of a dimension; `vt(j, dim)` gives value dim of key j of the
-// tile (zero past lk).
+// tile (zero past lk).  With kPackV the first plane's rows D .. D + kVLast -
+// 1 take the low parts of the last tile's dimensions, and with kSumRow its
+// next 8 rows 2^-4 at every key.
 template <int D, int KB, class V>
 __device__ __forceinline__ void split_values(V vt, _Float16 *rec) {
     using S = Split<D, KB>;
@@ -894,14 +916,17 @@ __device__ __forceinline__ void split_values(V vt, _Float16 *rec) {
     for (int idx = threadIdx.x; idx < S::kDvp * (S::kLdv / 4); idx += 256) {
         const int dim = idx / (S::kLdv / 4);
         const int c4 = idx - dim * (S::kLdv / 4);
+        const bool low = S::kPackV && dim >= D && dim < D + S::kVLast;
+        const bool ones = S::kSumRow && dim >= D + S::kVLast && dim < D + S::kVLast + 8;
+        const int src = low ? dim - S::kVLast : dim;
         half4a h, l;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int c = 4 * c4 + u;
-            const float x = c < KB && dim < D ? vt(key_of_column(c), dim) : 0.0f;
+            const float x = c < KB && src < D ? vt(key_of_column(c), src) : 0.0f;
             _Float16 hh, ll;
             split_part(x * kSplitDown, hh, ll);
-            h[u] = hh;
+            h[u] = low ? ll : ones && c < KB ? static_cast<_Float16>(kSplitDown) : hh;
             l[u] = ll;
         }
         *reinterpret_cast<half4a *>(vh + dim * S::kLdv + 4 * c4) = h;
@@ -937,22 +962,39 @@ __global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _
     split_values<D, KB>([&](int j, int dim) { return vt[j][dim]; }, rec);
 }
 
-// The online softmax of the wave's scores over KB keys, in base 2: the
-// accumulators hold the products of the keys by the queries times scale
-// log2(e), scaled by 2^-8 (the keys' and queries' 2^-4), as sh + 2^-11 sx;
-// with MASK, keys from `valid` on are masked.  The running maximum m, in that
-// scaled unit, moves only when a score passes it by more than 2^4 in
-// exponential, so that the output's accumulators are rescaled (by exp2(256
-// (old max - new max))) seldom, and only while some query's maximum moves.
-// The exponentials go to p as 2^11 exp2(256 (x - m)), below 2^15 -- the 2^11
-// so that their low FP16 parts stay normal down to exponentials of 2^-14,
-// below which they weigh less than the rounding of the sum -- and their sum
-// into l, taken 16 at a time as a tree in single precision and added in
-// double.
-template <bool MASK, int KT, int DVT>
-__device__ __forceinline__ void split_softmax(const float16v (&sh)[KT], const float16v (&sx)[KT], float (&p)[KT][16],
-                                              float &m, double &l, float16v (&oh)[DVT], float16v (&ol)[DVT],
-                                              int valid, int g) {
+// The greater of x on lanes i and i + 32 (the wave's two halves), on both:
+// v_permlane32_swap of two copies leaves one with the lower half's x on
+// every lane and the other with the upper's, with no trip through LDS.
+__device__ __forceinline__ float halves_max(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    // The elements as scalars first: this compiler takes __builtin_bit_cast of
+    // an element of a vector from the vector's first element.
+    const unsigned lower = r[0], upper = r[1];
+    return fmaxf(__builtin_bit_cast(float, lower), __builtin_bit_cast(float, upper));
+}
+
+// The online softmax of the wave's scores over KB keys, in base 2, in two
+// halves: split_max, then split_exp.  The accumulators hold the products of
+// the keys by the queries times scale log2(e), scaled by 2^-8 (the keys' and
+// queries' 2^-4), as sh + 2^-11 sx; with MASK, keys from `valid` on are
+// masked.  The running maximum m, in that scaled unit, moves only when a
+// score passes it by more than 2^4 in exponential, so that the output's
+// accumulators are rescaled (by exp2(256 (old max - new max))) seldom, and
+// only while some query's maximum moves.  The exponentials go to p as 2^11
+// exp2(256 (x - m)), below 2^15 -- the 2^11 so that their low FP16 parts stay
+// normal down to exponentials of 2^-14, below which they weigh less than the
+// rounding of the sum -- and, with SUM, their sum into l, taken 16 at a time
+// as a tree in single precision and added in double (without, the MFMAs sum
+// them from the values' rows of ones).
+//
+// split_max: the scores into p, the new maximum, the rescaling; returns the
+// exponentials' shift.  The branch comes before the exponentials, so that
+// those share a basic block with the next tile's MFMAs.
+template <bool MASK, bool SUM, int KT, int DVT>
+__device__ __forceinline__ float split_max(const float16v (&sh)[KT], const float16v (&sx)[KT], float (&p)[KT][16],
+                                           float &m, double &l, float16v (&oh)[DVT], float16v (&ol)[DVT],
+                                           int valid, int g) {
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < KT; ++t)
@@ -963,27 +1005,11 @@ __device__ __forceinline__ void split_softmax(const float16v (&sh)[KT], const fl
             p[t][e] = x;
             mx = fmaxf(mx, x);
         }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = halves_max(mx);
     const float mnew = mx > m + 4.0f / 256.0f ? mx : m;
-    const float shift = mnew * 256.0f - 11.0f;
-    double part = 0.0;
-#pragma unroll
-    for (int t = 0; t < KT; ++t) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) p[t][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][e], 256.0f, -shift));
-        float a8[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) a8[u] = p[t][2 * u] + p[t][2 * u + 1];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) a8[u] = a8[2 * u] + a8[2 * u + 1];
-        part += static_cast<double>((a8[0] + a8[1]) + (a8[2] + a8[3]));
-    }
-    // The rescaling last, so that the work above shares its basic block with
-    // whatever the caller put before this (the test of the sum, always true
-    // but for a NaN, keeps the branch below the exponentials).
-    if (__ballot(mnew != m && part >= 0.0) != 0) {
+    if (__ballot(mnew != m) != 0) {
         const float alpha = __builtin_amdgcn_exp2f((m - mnew) * 256.0f);  // 0 while m is -inf
-        l *= static_cast<double>(alpha);
+        if constexpr (SUM) l *= static_cast<double>(alpha);
 #pragma unroll
         for (int c = 0; c < DVT; ++c) {
             oh[c] *= alpha;
@@ -991,7 +1017,27 @@ __device__ __forceinline__ void split_softmax(const float16v (&sh)[KT], const fl
         }
         m = mnew;
     }
-    l += part;
+    return m * 256.0f - 11.0f;
+}
+
+// split_exp: the exponentials of the scores in p, their sum with SUM.
+template <bool SUM, int KT>
+__device__ __forceinline__ void split_exp(float (&p)[KT][16], float shift, double &l) {
+    double part = 0.0;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) p[t][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][e], 256.0f, -shift));
+        if constexpr (SUM) {
+            float a8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a8[u] = p[t][2 * u] + p[t][2 * u + 1];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a8[u] = a8[2 * u] + a8[2 * u + 1];
+            part += static_cast<double>((a8[0] + a8[1]) + (a8[2] + a8[3]));
+        }
+    }
+    if constexpr (SUM) l += part;
 }
 
 // Partial results of the split form's key splits: per (b h, split, query)
@@ -1016,6 +1062,8 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     const int wave = tid >> 6;
     const int lr = lane & 31;  // the lane's query, or its row of operand A
     const int g = lane >> 5;   // the lane's half of the wave
+    float minus_one;           // -1, in a scalar register (see values below)
+    asm("s_mov_b32 %0, -1.0" : "=s"(minus_one));
 
     // With key splits (splits > 1) the workgroup takes tiles [t0, t0 +
     // per) of the head's nk_all and writes partial results for
@@ -1056,6 +1104,22 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // by consecutive threads; otherwise each lane reads its own row.
     half8 qh[S::kSteps], ql[S::kSteps];
     const float qscale = a.scale * 1.44269504088896341f;  // scale log2(e), folded into the queries
+    // The lane's query (row qp) into its parts.  With kHalfStep the last
+    // step's upper half holds h' of the dimension 8 below its own where the
+    // others hold l', and zero where they hold h'.
+    const auto take_query = [&](const float *qp) {
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool slot = S::kHalfStep && st == S::kSteps - 1 && g == 1;
+                const int dim = 16 * st + 8 * g + j - (slot ? 8 : 0);
+                _Float16 h, l;
+                split_part(dim < D ? (qp[dim] * qscale) * kSplitDown : 0.0f, h, l);
+                qh[st][j] = slot ? static_cast<_Float16>(0.0f) : h;
+                ql[st][j] = slot ? h : l;
+            }
+    };
     // LOCAL, where the staging fits: every load of the workgroup -- its
     // queries, and the keys and values of every tile -- in flight at once,
     // into registers; then the queries staged in buffers 1 .., the values as
@@ -1113,6 +1177,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             }
             *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = h;
             *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
+            if (S::kHalfStep && 4 * c4 >= D - 8) *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4 + 8) = l;
         };
 #pragma unroll
         for (int i = 0; i < kQPer; ++i) {
@@ -1133,16 +1198,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         }
         __syncthreads();
         const float *qp = qstage + (wave * 32 + lr) * D;
-#pragma unroll
-        for (int st = 0; st < S::kSteps; ++st)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int dim = 16 * st + 8 * g + j;
-                _Float16 h, l;
-                split_part(dim < D ? (qp[dim] * qscale) * kSplitDown : 0.0f, h, l);
-                qh[st][j] = h;
-                ql[st][j] = l;
-            }
+        take_query(qp);
         __syncthreads();  // every wave's queries read before the tiles overwrite their staging
 #pragma unroll
         for (int i = 0; i < kKVPer; ++i) {
@@ -1151,7 +1207,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             if (idx < kKV4 && key >= KB && key < nk * KB) put_key(key, c4, kv[i]);
         }
         constexpr int kPad4 = (S::kDp - D) / 4;  // float4s of padding dimensions a key
-        if constexpr (kPad4 > 0) {
+        if constexpr (kPad4 > 0 && !S::kHalfStep) {  // with kHalfStep the padding holds low parts
             for (int idx = tid; idx < nk * KB * kPad4; idx += 256) {
                 const int key = idx / kPad4, c4 = D / 4 + (idx - key * kPad4);
                 put_key(key, c4, float4v{});
@@ -1182,16 +1238,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             i = i < a.lq ? i : a.lq - 1;
             qp = a.q + bi * a.qnb3 + hi * a.qnb2 + i * a.qnb1;
         }
-#pragma unroll
-        for (int st = 0; st < S::kSteps; ++st)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int dim = 16 * st + 8 * g + j;
-                _Float16 h, l;
-                split_part(dim < D ? (qp[dim] * qscale) * kSplitDown : 0.0f, h, l);
-                qh[st][j] = h;
-                ql[st][j] = l;
-            }
+        take_query(qp);
         if constexpr (LOCAL) __syncthreads();  // every wave's queries read before the ring is filled
     }
     // LOCAL (the tiles fit the ring with a buffer to spare): the workgroup
@@ -1225,6 +1272,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     }
     float m = -INFINITY;
     double l = 0.0;
+    constexpr bool kSum = !S::kSumRow;  // the sum of the exponentials by VALU work, else by the MFMAs
 
     // The ring: tile t in buffer t % NS.  With PIPE the scores of tile t + 1
     // are taken while the exponentials of tile t are (the MFMAs of the one
@@ -1261,10 +1309,12 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             for (int u = 0; u < S::kTiles; ++u) {
                 const _Float16 *kp = kbuf + (32 * u + lr) * S::kLdk + 16 * st + 8 * g;
                 const half8 ka = *reinterpret_cast<const half8 *>(kp);
-                const half8 kl = *reinterpret_cast<const half8 *>(kp + S::kPlaneK);
                 sh[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[st], sh[u], 0, 0, 0);
                 sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[st], sx[u], 0, 0, 0);
-                sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[st], sx[u], 0, 0, 0);
+                if (!S::kHalfStep || st < S::kSteps - 1) {
+                    const half8 kl = *reinterpret_cast<const half8 *>(kp + S::kPlaneK);
+                    sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[st], sx[u], 0, 0, 0);
+                }
             }
     };
     // O^T += V^T P^T of tile t, a chunk of 16 keys at a time: the lane's
@@ -1282,8 +1332,11 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 for (int j = 0; j < 8; j += 2) {
                     const float x0 = p[u][8 * c + j], x1 = p[u][8 * c + j + 1];
                     const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
-                    const auto r =
-                        __builtin_amdgcn_cvt_pkrtz(x0 - static_cast<float>(h[0]), x1 - static_cast<float>(h[1]));
+                    // x - h, each one v_fma_mix_f32 (its -1 unknown to the
+                    // compiler, which would make it a conversion and a
+                    // subtraction).
+                    const auto r = __builtin_amdgcn_cvt_pkrtz(__builtin_fmaf(static_cast<float>(h[0]), minus_one, x0),
+                                                              __builtin_fmaf(static_cast<float>(h[1]), minus_one, x1));
                     ph[j] = h[0];
                     ph[j + 1] = h[1];
                     pl[j] = r[0];
@@ -1293,10 +1346,12 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 for (int dt = 0; dt < S::kDvt; ++dt) {
                     const _Float16 *vp = vbuf + (32 * dt + lr) * S::kLdv + 32 * u + 16 * c + 8 * g;
                     const half8 va = *reinterpret_cast<const half8 *>(vp);
-                    const half8 vl = *reinterpret_cast<const half8 *>(vp + S::kPlaneV);
                     oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, oh[dt], 0, 0, 0);
                     oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, oh[dt], 0, 0, 0);
-                    ol[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, ol[dt], 0, 0, 0);
+                    if (!S::kPackV || dt < S::kDvt - 1) {  // the packed tile's low parts are rows of va
+                        const half8 vl = *reinterpret_cast<const half8 *>(vp + S::kPlaneV);
+                        ol[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, ol[dt], 0, 0, 0);
+                    }
                 }
             }
     };
@@ -1313,11 +1368,9 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     const auto last = [&](float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
         float p[S::kTiles][16];
         const int valid = t0 + nk == nk_all ? static_cast<int>(a.lk - (nk_all - 1) * KB) : KB;
-        if (valid < KB) {
-            split_softmax<true, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, valid, g);
-        } else {
-            split_softmax<false, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
-        }
+        const float shift = valid < KB ? split_max<true, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, valid, g)
+                                       : split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+        split_exp<kSum, S::kTiles>(p, shift, l);
         values(nk - 1, p);
     };
     if constexpr (PIPE) {
@@ -1326,9 +1379,10 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         const auto step = [&](int64_t it, float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles],
                               float16v (&nh)[S::kTiles], float16v (&nx)[S::kTiles]) {
             sync(it + 1);
-            scores(it + 1, nh, nx);
             float p[S::kTiles][16];
-            split_softmax<false, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+            const float shift = split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+            scores(it + 1, nh, nx);
+            split_exp<kSum, S::kTiles>(p, shift, l);
             values(it, p);
         };
         sync(0);
@@ -1350,7 +1404,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             sync(it);
             scores(it, sh, sx);
             float p[S::kTiles][16];
-            split_softmax<false, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
+            split_exp<kSum, S::kTiles>(p, split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g), l);
             values(it, p);
         }
         sync(nk - 1);
@@ -1358,10 +1412,20 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         last(sh, sx);
     }
 
-    // The query's sum over its two lanes; lane holds O^T[32 dt + 8 (e / 4) +
-    // 4 g + e % 4][lr], and the values' 2^-4 comes back with the reciprocal.
-    double sum = l;
-    sum += __shfl_xor(sum, 32, 64);
+    // The query's sum over its two lanes, or from the rows of ones (the same
+    // on both); lane holds O^T[32 dt + 8 (e / 4) + 4 g + e % 4][lr], and the
+    // values' 2^-4 comes back with the reciprocal.  The packed tile's low
+    // parts are kVLast rows, kVLast / 2 elements, below its high parts.
+    double sum;
+    if constexpr (S::kSumRow) {
+        sum = static_cast<double>(oh[S::kDvt - 1][S::kVLast]) * 16.0;
+    } else {
+        sum = l;
+        sum += __shfl_xor(sum, 32, 64);
+    }
+    const auto low = [&](int dt, int e) {
+        return S::kPackV && dt == S::kDvt - 1 ? oh[dt][e + S::kVLast / 2] : ol[dt][e];
+    };
     const int64_t i = q0 + lr;
     if (i >= a.lq) return;
     if (splits > 1) {
@@ -1381,7 +1445,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 if (dim < D) {
                     float4v r;
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) r[u] = (oh[dt][4 * e4 + u] + ol[dt][4 * e4 + u] * kPartDown) * 16.0f;
+                    for (int u = 0; u < 4; ++u) r[u] = (oh[dt][4 * e4 + u] + low(dt, 4 * e4 + u) * kPartDown) * 16.0f;
                     *reinterpret_cast<float4v *>(o + dim) = r;
                 }
             }
@@ -1398,7 +1462,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 float4v r;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    r[u] = ((oh[dt][4 * e4 + u] + ol[dt][4 * e4 + u] * kPartDown) * 16.0f) * reciprocal;
+                    r[u] = ((oh[dt][4 * e4 + u] + low(dt, 4 * e4 + u) * kPartDown) * 16.0f) * reciprocal;
                 }
                 *reinterpret_cast<float4v *>(out + dim) = r;
             }
@@ -1407,7 +1471,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
 
 // The key splits of the split form merged, query by query: each split's sum
 // and output rescaled by 2^(256 (its maximum - the greatest)), as
-// split_softmax rescales its running ones, the sum in double, the output
+// split_max rescales its running ones, the sum in double, the output
 // times the reciprocal of the sum rounded to single precision.  A wave per
 // query.
 __global__ __launch_bounds__(256) void split_combine_kernel(AttentionArgs a, int64_t splits, KeyPartial part) {
