@@ -851,6 +851,10 @@ struct Split {
     static constexpr int kVLast = D - 32 * (kDvt - 1);
     static constexpr bool kPackV = kVLast <= 16;
     static constexpr bool kSumRow = kPackV && 2 * kVLast + 8 <= 32;
+    // The operands A of a tile's MFMAs read from LDS before the softmax's
+    // maximum rather than next to the MFMAs, where the registers allow it
+    // (their 44 more keep SD1.5's heads of 40 at two waves a SIMD).
+    static constexpr bool kEarlyReads = D == 40;
     static_assert(D % 8 == 0 && KB % 32 == 0, "shape");
     static_assert(!kHalfStep || kDp == D + 8, "the keys' low parts fill the last step's padding");
     static_assert((kLdk / 8) % 2 == 1 && (kLdv / 8) % 2 == 1, "rows of an odd number of 16-byte units");
@@ -1295,9 +1299,37 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (t + kAhead < nk) issue(static_cast<int>((t + kAhead) % NS), t + kAhead);
     };
-    // S^T of tile t.
-    const auto scores = [&](int64_t t, float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
+    // The operands A of a tile's MFMAs, read from LDS ahead of them (before
+    // the softmax's maximum, so that the reads are done by the time the
+    // MFMAs issue): the keys' parts of tile t, the values' of tile t.
+    half8 kah[S::kSteps][S::kTiles], kal[S::kSteps][S::kTiles];
+    half8 vah[S::kTiles][2][S::kDvt], val[S::kTiles][2][S::kDvt];
+    const auto read_keys = [&](int64_t t) {
         const _Float16 *kbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord);
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st)
+#pragma unroll
+            for (int u = 0; u < S::kTiles; ++u) {
+                const _Float16 *kp = kbuf + (32 * u + lr) * S::kLdk + 16 * st + 8 * g;
+                kah[st][u] = *reinterpret_cast<const half8 *>(kp);
+                if (!S::kHalfStep || st < S::kSteps - 1) kal[st][u] = *reinterpret_cast<const half8 *>(kp + S::kPlaneK);
+            }
+    };
+    const auto read_values = [&](int64_t t) {
+        const _Float16 *vbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord) + 2 * S::kPlaneK;
+#pragma unroll
+        for (int u = 0; u < S::kTiles; ++u)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int dt = 0; dt < S::kDvt; ++dt) {
+                    const _Float16 *vp = vbuf + (32 * dt + lr) * S::kLdv + 32 * u + 16 * c + 8 * g;
+                    vah[u][c][dt] = *reinterpret_cast<const half8 *>(vp);
+                    if (!S::kPackV || dt < S::kDvt - 1) val[u][c][dt] = *reinterpret_cast<const half8 *>(vp + S::kPlaneV);
+                }
+    };
+    // S^T of the tile whose keys read_keys read.
+    const auto scores = [&](float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
 #pragma unroll
         for (int u = 0; u < S::kTiles; ++u) {
             sh[u] = float16v{};
@@ -1307,20 +1339,15 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         for (int st = 0; st < S::kSteps; ++st)
 #pragma unroll
             for (int u = 0; u < S::kTiles; ++u) {
-                const _Float16 *kp = kbuf + (32 * u + lr) * S::kLdk + 16 * st + 8 * g;
-                const half8 ka = *reinterpret_cast<const half8 *>(kp);
-                sh[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[st], sh[u], 0, 0, 0);
-                sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[st], sx[u], 0, 0, 0);
-                if (!S::kHalfStep || st < S::kSteps - 1) {
-                    const half8 kl = *reinterpret_cast<const half8 *>(kp + S::kPlaneK);
-                    sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[st], sx[u], 0, 0, 0);
-                }
+                sh[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kah[st][u], qh[st], sh[u], 0, 0, 0);
+                sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kah[st][u], ql[st], sx[u], 0, 0, 0);
+                if (!S::kHalfStep || st < S::kSteps - 1)
+                    sx[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kal[st][u], qh[st], sx[u], 0, 0, 0);
             }
     };
     // O^T += V^T P^T of tile t, a chunk of 16 keys at a time: the lane's
     // eight exponentials 8 c .. 8 c + 7 of a tile of 32 are its operand B.
-    const auto values = [&](int64_t t, const float (&p)[S::kTiles][16]) {
-        const _Float16 *vbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord) + 2 * S::kPlaneK;
+    const auto values = [&](const float (&p)[S::kTiles][16]) {
 #pragma unroll
         for (int u = 0; u < S::kTiles; ++u)
 #pragma unroll
@@ -1344,14 +1371,10 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 }
 #pragma unroll
                 for (int dt = 0; dt < S::kDvt; ++dt) {
-                    const _Float16 *vp = vbuf + (32 * dt + lr) * S::kLdv + 32 * u + 16 * c + 8 * g;
-                    const half8 va = *reinterpret_cast<const half8 *>(vp);
-                    oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, oh[dt], 0, 0, 0);
-                    oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, oh[dt], 0, 0, 0);
-                    if (!S::kPackV || dt < S::kDvt - 1) {  // the packed tile's low parts are rows of va
-                        const half8 vl = *reinterpret_cast<const half8 *>(vp + S::kPlaneV);
-                        ol[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, ol[dt], 0, 0, 0);
-                    }
+                    oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vah[u][c][dt], ph, oh[dt], 0, 0, 0);
+                    oh[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vah[u][c][dt], pl, oh[dt], 0, 0, 0);
+                    if (!S::kPackV || dt < S::kDvt - 1)  // the packed tile's low parts are rows of vah
+                        ol[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(val[u][c][dt], ph, ol[dt], 0, 0, 0);
                 }
             }
     };
@@ -1368,10 +1391,12 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     const auto last = [&](float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles]) {
         float p[S::kTiles][16];
         const int valid = t0 + nk == nk_all ? static_cast<int>(a.lk - (nk_all - 1) * KB) : KB;
+        if constexpr (S::kEarlyReads) read_values(nk - 1);
         const float shift = valid < KB ? split_max<true, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, valid, g)
                                        : split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
         split_exp<kSum, S::kTiles>(p, shift, l);
-        values(nk - 1, p);
+        if constexpr (!S::kEarlyReads) read_values(nk - 1);
+        values(p);
     };
     if constexpr (PIPE) {
         // Two sets of scores, a and b, taking turns (no copies between them).
@@ -1379,14 +1404,21 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         const auto step = [&](int64_t it, float16v (&sh)[S::kTiles], float16v (&sx)[S::kTiles],
                               float16v (&nh)[S::kTiles], float16v (&nx)[S::kTiles]) {
             sync(it + 1);
+            if constexpr (S::kEarlyReads) {
+                read_keys(it + 1);
+                read_values(it);
+            }
             float p[S::kTiles][16];
             const float shift = split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
-            scores(it + 1, nh, nx);
+            if constexpr (!S::kEarlyReads) read_keys(it + 1);
+            scores(nh, nx);
             split_exp<kSum, S::kTiles>(p, shift, l);
-            values(it, p);
+            if constexpr (!S::kEarlyReads) read_values(it);
+            values(p);
         };
         sync(0);
-        scores(0, sa, xa);
+        read_keys(0);
+        scores(sa, xa);
         int64_t it = 0;
         for (; it + 2 < nk; it += 2) {
             step(it, sa, xa, sb, xb);
@@ -1402,13 +1434,17 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         float16v sh[S::kTiles], sx[S::kTiles];
         for (int64_t it = 0; it + 1 < nk; ++it) {
             sync(it);
-            scores(it, sh, sx);
+            read_keys(it);
+            if constexpr (S::kEarlyReads) read_values(it);
+            scores(sh, sx);
             float p[S::kTiles][16];
             split_exp<kSum, S::kTiles>(p, split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g), l);
-            values(it, p);
+            if constexpr (!S::kEarlyReads) read_values(it);
+            values(p);
         }
         sync(nk - 1);
-        scores(nk - 1, sh, sx);
+        read_keys(nk - 1);
+        scores(sh, sx);
         last(sh, sx);
     }
 
