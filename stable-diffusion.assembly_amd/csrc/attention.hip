@@ -1092,13 +1092,18 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // scalar base and the lane's fixed 16-byte offset.
     const int swave = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;
+    // The split's tiles as a buffer resource (its nk records, below 2^31
+    // bytes: key_splits caps nk), so that each copy's address is the lane's
+    // 16 bytes and a scalar offset.
+    const __amdgpu_buffer_rsrc_t head_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char *>(head), 0, static_cast<int>(LOCAL ? 0 : nk * S::kRecord), 0x00020000);
     const auto issue = [&](int stage, int64_t t) {
-        const char *src = head + t * S::kRecord;
 #pragma unroll
         for (int i = 0; i < S::kPerWave; ++i) {
             int c = swave + 4 * i;
             c = c < S::kCopies ? c : S::kCopies - 1;
-            copy_lds(src + c * 1024 + lane16, sbuf + stage * S::kRecord + c * 1024);
+            copy_lds_buffer(head_rsrc, lane16, static_cast<uint32_t>(t * S::kRecord + c * 1024),
+                            sbuf + stage * S::kRecord + c * 1024);
         }
     };
     // The wave's queries, operand B of S^T: lane (query lr, half g) holds
@@ -1565,6 +1570,10 @@ KeySplits key_splits(const AttentionArgs &a) {
         sp = sp < nk / 2 ? sp : nk / 2;
         sp = sp < 1 ? 1 : sp;
     }
+    // A split's tiles stay below 2^31 bytes, the reach of the kernel's buffer
+    // resource.
+    const int64_t most = (INT32_MAX - 1024) / S::kRecord;
+    sp = ceil_div(nk, sp) > most ? ceil_div(nk, most) : sp;
     const int64_t per = ceil_div(nk, sp);
     return {ceil_div(nk, per), per};
 }

@@ -234,6 +234,15 @@ __device__ __forceinline__ void copy_lds4(const void *src, char *lds) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
 }
 
+// copy_lds through a buffer resource: the piece at rsrc's base + voffset +
+// soffset, the lane's constant offset in a vector register and the rest in a
+// scalar one, so that a copy takes no vector instruction for its address.
+__device__ __forceinline__ void copy_lds_buffer(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
+                                                char *lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voffset,
+                                             soffset, 0, 0);
+}
+
 // ------------------------------------------------------------------ grid
 
 // The 8 XCDs of an MI355X each take every 8th workgroup of a launch, and each
