@@ -1416,10 +1416,15 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             float p[S::kTiles][16];
             const float shift = split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g);
             if constexpr (!S::kEarlyReads) read_keys(it + 1);
+            // The wave's MFMAs and exponentials ahead of the other wave's
+            // maximum on the SIMD (s_setprio): the MFMAs then issue while
+            // the other's VALU work runs, rather than after it.
+            __builtin_amdgcn_s_setprio(1);
             scores(nh, nx);
             split_exp<kSum, S::kTiles>(p, shift, l);
             if constexpr (!S::kEarlyReads) read_values(it);
             values(p);
+            __builtin_amdgcn_s_setprio(0);
         };
         sync(0);
         read_keys(0);
@@ -1441,11 +1446,15 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             sync(it);
             read_keys(it);
             if constexpr (S::kEarlyReads) read_values(it);
+            __builtin_amdgcn_s_setprio(1);  // the MFMAs ahead of the other wave's VALU work, as above
             scores(sh, sx);
+            __builtin_amdgcn_s_setprio(0);
             float p[S::kTiles][16];
             split_exp<kSum, S::kTiles>(p, split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g), l);
             if constexpr (!S::kEarlyReads) read_values(it);
+            __builtin_amdgcn_s_setprio(1);
             values(p);
+            __builtin_amdgcn_s_setprio(0);
         }
         sync(nk - 1);
         read_keys(nk - 1);
