@@ -831,10 +831,6 @@ struct Split {
     static constexpr int kLdv = KB + 8;              // halves
     static constexpr int kPlaneK = KB * kLdk;
     static constexpr int kPlaneV = kDvp * kLdv;
-    static constexpr int kHalves = 2 * kPlaneK + 2 * kPlaneV;          // of a tile
-    static constexpr int kRecord = (2 * kHalves + 1023) / 1024 * 1024;  // bytes of a tile, whole KB
-    static constexpr int kCopies = kRecord / 1024;                      // 1 KB copies of a tile
-    static constexpr int kPerWave = (kCopies + 3) / 4;
     static constexpr int kQueries = 128;  // a workgroup's
     // D = 16 n + 8: the scores' last step has 8 dimensions, and the keys' low
     // parts of those fill its other 8 (the keys' first plane holds l at
@@ -855,8 +851,24 @@ struct Split {
     // maximum rather than next to the MFMAs, where the registers allow it
     // (their 44 more keep SD1.5's heads of 40 at two waves a SIMD).
     static constexpr bool kEarlyReads = D == 40;
+    // The record holds only what the MFMAs read: the keys' second plane the
+    // dimensions of the steps that take it (rows of kLdkl halves), the
+    // values' second plane the tiles that take it (kDvlo rows).
+    static constexpr int kLdkl = (kHalfStep ? kDp - 16 : kDp) + 8;
+    static constexpr int kDvlo = kPackV ? kDvp - 32 : kDvp;
+    static constexpr int kPlaneKl = KB * kLdkl;
+    static constexpr int kValues = kPlaneK + kPlaneKl;  // halves before the values' planes
+    static constexpr int kPlaneVl = kDvlo * kLdv;
+    static constexpr int kHalves = kValues + kPlaneV + kPlaneVl;        // of a tile
+    static constexpr int kRecord = (2 * kHalves + 1023) / 1024 * 1024;  // bytes of a tile, whole KB
+    static constexpr int kCopies = kRecord / 1024;                      // 1 KB copies of a tile
+    static constexpr int kPerWave = (kCopies + 3) / 4;
+    // The LDS buffers of the form that splits the keys and values itself
+    // (LOCAL): as large as both planes in full, for its staging.
+    static constexpr int kLocalBuffer = (4 * (kPlaneK + kPlaneV) + 1023) / 1024 * 1024;
     static_assert(D % 8 == 0 && KB % 32 == 0, "shape");
     static_assert(!kHalfStep || kDp == D + 8, "the keys' low parts fill the last step's padding");
+    static_assert((kLdkl / 8) % 2 == 1, "rows of an odd number of 16-byte units");
     static_assert((kLdk / 8) % 2 == 1 && (kLdv / 8) % 2 == 1, "rows of an odd number of 16-byte units");
 };
 
@@ -881,7 +893,7 @@ __device__ __forceinline__ int key_of_column(int c) {
 // [KB][kLdk] twice, into `rec` (the work buffer's record or an LDS buffer),
 // by the workgroup's threads: a thread a key's four dimensions, float4 loads.
 // With kHalfStep the first plane's columns D .. D + 7 take the low parts of
-// dimensions D - 8 .. D - 1 (the second plane's are never read).
+// dimensions D - 8 .. D - 1, and the second plane's rows are kLdkl long.
 template <int D, int KB>
 __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, int64_t kh, int64_t kt, _Float16 *rec) {
     using S = Split<D, KB>;
@@ -903,12 +915,12 @@ __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, i
             l[r] = ll;
         }
         *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = slot ? l : h;
-        *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
+        if (4 * c4 < S::kLdkl) *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdkl + 4 * c4) = l;
     }
 }
 
-// The values of tile kt split and transposed, [kDvp][kLdv] twice after the
-// keys' planes of `rec`, a thread four columns (four keys, in the order of
+// The values of tile kt split and transposed, [kDvp][kLdv] and [kDvlo][kLdv]
+// after the keys' planes of `rec`, a thread four columns (four keys, in the order of
 // key_of_column) of a dimension; `vt(j, dim)` gives value dim of key j of the
 // tile (zero past lk).  With kPackV the first plane's rows D .. D + kVLast -
 // 1 take the low parts of the last tile's dimensions, and with kSumRow its
@@ -916,7 +928,7 @@ __device__ __forceinline__ void split_keys(const AttentionArgs &a, int64_t bi, i
 template <int D, int KB, class V>
 __device__ __forceinline__ void split_values(V vt, _Float16 *rec) {
     using S = Split<D, KB>;
-    _Float16 *vh = rec + 2 * S::kPlaneK;
+    _Float16 *vh = rec + S::kValues;
     for (int idx = threadIdx.x; idx < S::kDvp * (S::kLdv / 4); idx += 256) {
         const int dim = idx / (S::kLdv / 4);
         const int c4 = idx - dim * (S::kLdv / 4);
@@ -934,7 +946,7 @@ __device__ __forceinline__ void split_values(V vt, _Float16 *rec) {
             l[u] = ll;
         }
         *reinterpret_cast<half4a *>(vh + dim * S::kLdv + 4 * c4) = h;
-        *reinterpret_cast<half4a *>(vh + S::kPlaneV + dim * S::kLdv + 4 * c4) = l;
+        if (dim < S::kDvlo) *reinterpret_cast<half4a *>(vh + S::kPlaneV + dim * S::kLdv + 4 * c4) = l;
     }
 }
 
@@ -1057,9 +1069,12 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                                                                    int64_t splits, int64_t per, KeyPartial part) {
     using S = Split<D, KB>;
     static_assert(NS >= 3 && (NS - 2) * S::kPerWave < 64, "stages");
-    static_assert(S::kQueries * D * 4 <= NS * S::kRecord, "the queries' staging fits the ring");
-    static_assert(KB * (D + 4) * 4 <= S::kRecord, "a tile's values fit a buffer as they stand");
-    extern __shared__ __attribute__((aligned(1024))) char sbuf[];  // NS tiles of S::kRecord bytes
+    // LDS buffers of kStride bytes: a tile's record, or with LOCAL room for
+    // the staging as well.
+    constexpr int kStride = LOCAL ? S::kLocalBuffer : S::kRecord;
+    static_assert(S::kQueries * D * 4 <= NS * kStride, "the queries' staging fits the ring");
+    static_assert(KB * (D + 4) * 4 <= kStride, "a tile's values fit a buffer as they stand");
+    extern __shared__ __attribute__((aligned(1024))) char sbuf[];  // NS buffers of kStride bytes
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1103,7 +1118,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             int c = swave + 4 * i;
             c = c < S::kCopies ? c : S::kCopies - 1;
             copy_lds_buffer(head_rsrc, lane16, static_cast<uint32_t>(t * S::kRecord + c * 1024),
-                            sbuf + stage * S::kRecord + c * 1024);
+                            sbuf + stage * kStride + c * 1024);
         }
     };
     // The wave's queries, operand B of S^T: lane (query lr, half g) holds
@@ -1137,8 +1152,8 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // other tiles' keys split, the padding dimensions of the keys cleared and
     // every tile's values split and transposed from the staging.  One wait for
     // memory where a tile at a time takes one a tile.
-    constexpr bool kBatch = LOCAL && (NS - 1) * KB * (D + 4) * 4 <= S::kRecord &&
-                            S::kQueries * D * 4 <= (NS - 2) * S::kRecord;
+    constexpr bool kBatch = LOCAL && (NS - 1) * KB * (D + 4) * 4 <= kStride &&
+                            S::kQueries * D * 4 <= (NS - 2) * kStride;
     if constexpr (kBatch) {
         constexpr int kQ4 = S::kQueries * (D / 4);  // float4s of the workgroup's queries
         constexpr int kQPer = (kQ4 + 255) / 256;
@@ -1170,11 +1185,11 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 vv[i] = *reinterpret_cast<const float4v *>(vg + key * a.vnb1 + 4 * c4);
             }
         }
-        float *qstage = reinterpret_cast<float *>(sbuf + S::kRecord);              // [kQueries][D]
-        float *vstage = reinterpret_cast<float *>(sbuf + (NS - 1) * S::kRecord);   // [key][D + 4]
+        float *qstage = reinterpret_cast<float *>(sbuf + kStride);              // [kQueries][D]
+        float *vstage = reinterpret_cast<float *>(sbuf + (NS - 1) * kStride);   // [key][D + 4]
         // Key `key`'s four dimensions 4 c4 .. split into its tile's two planes.
         const auto put_key = [&](int key, int c4, float4v x) {
-            _Float16 *rec = reinterpret_cast<_Float16 *>(sbuf + (key / KB) * S::kRecord);
+            _Float16 *rec = reinterpret_cast<_Float16 *>(sbuf + (key / KB) * kStride);
             const int j = key % KB;
             half4a h, l;
 #pragma unroll
@@ -1185,7 +1200,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
                 l[r] = ll;
             }
             *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4) = h;
-            *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdk + 4 * c4) = l;
+            if (4 * c4 < S::kLdkl) *reinterpret_cast<half4a *>(rec + S::kPlaneK + j * S::kLdkl + 4 * c4) = l;
             if (S::kHalfStep && 4 * c4 >= D - 8) *reinterpret_cast<half4a *>(rec + j * S::kLdk + 4 * c4 + 8) = l;
         };
 #pragma unroll
@@ -1225,7 +1240,7 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
         for (int64_t t = 0; t < nk; ++t) {
             const float *vt = vstage + t * KB * (D + 4);
             split_values<D, KB>([&](int j, int dim) { return vt[j * (D + 4) + dim]; },
-                                reinterpret_cast<_Float16 *>(sbuf + t * S::kRecord));
+                                reinterpret_cast<_Float16 *>(sbuf + t * kStride));
         }
         __syncthreads();
     } else {
@@ -1257,9 +1272,9 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // are transposed from there.
     if constexpr (LOCAL && !kBatch) {
         const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
-        float *vt = reinterpret_cast<float *>(sbuf + (NS - 1) * S::kRecord);  // [KB][D + 4]
+        float *vt = reinterpret_cast<float *>(sbuf + (NS - 1) * kStride);  // [KB][D + 4]
         for (int64_t t = 0; t < nk; ++t) {
-            _Float16 *rec = reinterpret_cast<_Float16 *>(sbuf + t * S::kRecord);
+            _Float16 *rec = reinterpret_cast<_Float16 *>(sbuf + t * kStride);
             split_keys<D, KB>(a, bi, kh, t, rec);
             for (int idx = tid; idx < KB * (D / 4); idx += 256) {
                 const int j = idx / (D / 4), c4 = idx - j * (D / 4);
@@ -1310,18 +1325,19 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     half8 kah[S::kSteps][S::kTiles], kal[S::kSteps][S::kTiles];
     half8 vah[S::kTiles][2][S::kDvt], val[S::kTiles][2][S::kDvt];
     const auto read_keys = [&](int64_t t) {
-        const _Float16 *kbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord);
+        const _Float16 *kbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * kStride);
 #pragma unroll
         for (int st = 0; st < S::kSteps; ++st)
 #pragma unroll
             for (int u = 0; u < S::kTiles; ++u) {
                 const _Float16 *kp = kbuf + (32 * u + lr) * S::kLdk + 16 * st + 8 * g;
                 kah[st][u] = *reinterpret_cast<const half8 *>(kp);
-                if (!S::kHalfStep || st < S::kSteps - 1) kal[st][u] = *reinterpret_cast<const half8 *>(kp + S::kPlaneK);
+                if (!S::kHalfStep || st < S::kSteps - 1)
+                    kal[st][u] = *reinterpret_cast<const half8 *>(kbuf + S::kPlaneK + (32 * u + lr) * S::kLdkl + 16 * st + 8 * g);
             }
     };
     const auto read_values = [&](int64_t t) {
-        const _Float16 *vbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * S::kRecord) + 2 * S::kPlaneK;
+        const _Float16 *vbuf = reinterpret_cast<const _Float16 *>(sbuf + (t % NS) * kStride) + S::kValues;
 #pragma unroll
         for (int u = 0; u < S::kTiles; ++u)
 #pragma unroll
@@ -1446,15 +1462,11 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
             sync(it);
             read_keys(it);
             if constexpr (S::kEarlyReads) read_values(it);
-            __builtin_amdgcn_s_setprio(1);  // the MFMAs ahead of the other wave's VALU work, as above
             scores(sh, sx);
-            __builtin_amdgcn_s_setprio(0);
             float p[S::kTiles][16];
             split_exp<kSum, S::kTiles>(p, split_max<false, kSum, S::kTiles, S::kDvt>(sh, sx, p, m, l, oh, ol, KB, g), l);
             if constexpr (!S::kEarlyReads) read_values(it);
-            __builtin_amdgcn_s_setprio(1);
             values(p);
-            __builtin_amdgcn_s_setprio(0);
         }
         sync(nk - 1);
         read_keys(nk - 1);
@@ -1620,7 +1632,7 @@ hipError_t launch_split_t(AttentionArgs a, void *work, hipStream_t stream) {
     using SH = SplitShape<D>;
     using S = Split<D, SH::kKeys>;
     a.qblocks = ceil_div(a.lq, S::kQueries);
-    const size_t lds = static_cast<size_t>(SH::kStages) * S::kRecord;
+    const size_t lds = static_cast<size_t>(SH::kStages) * (LOCAL ? S::kLocalBuffer : S::kRecord);
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&attention_split_kernel<D, SH::kKeys, SH::kStages, SH::kOcc, SH::kPipe, LOCAL>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
