@@ -166,7 +166,10 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
     int aread[2];
 #pragma unroll
     for (int hk = 0; hk < 2; ++hk) aread[hk] = r32 * kRowBytes + (((2 * hk + half) ^ swizzle(r32)) << 4);
+    // Each step's MFMAs at raised wave priority (s_setprio), ahead of the
+    // other workgroups' split and stores of A on the SIMD.
     const auto compute = [&](int stage, int buf) {
+        __builtin_amdgcn_s_setprio(1);
         const char *base = lds + buf * kBuf;
 #pragma unroll
         for (int hk = 0; hk < 2; ++hk) {
@@ -186,6 +189,7 @@ __global__ __launch_bounds__(256) void split_batched3_kernel(SplitBatchedArgs p)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl, acc[i][j], 0, 0, 0);
                 }
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
 #pragma unroll
