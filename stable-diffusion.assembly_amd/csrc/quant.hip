@@ -157,6 +157,13 @@ __global__ __launch_bounds__(256) void quantize_inputs_kernel(Src src, int64_t M
     }
 }
 
+// x from another lane of its row of 16 by a DPP move (CTRL: quad_perm 0x00
+// .. 0xFF, row_mirror 0x140, row_half_mirror 0x141); every lane reads one.
+template <int CTRL>
+__device__ __forceinline__ float row_dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
 // The same quantizer for groups of 64 that fill their slots (K a multiple of
 // 64, rows of x 16-byte aligned): 16 lanes a (row, group), each lane 4
 // consecutive numbers (one 16-byte load), the least and greatest reduced
@@ -171,16 +178,25 @@ __global__ __launch_bounds__(256) void quantize_inputs64_kernel(const float *__r
     const int64_t seg = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
     if (seg >= M * groups) return;
     const int j = threadIdx.x & 15;
-    const int64_t m = seg / groups;
-    const int64_t g = seg - m * groups;
+    // Consecutive segments along the rows, so that a wave's bytes are
+    // consecutive in xq ([group][row][64]).
+    const int64_t g = seg / M;
+    const int64_t m = seg - g * M;
     const float4v v = *reinterpret_cast<const float4v *>(x + m * ldx + 64 * g + 4 * j);
     float lo = fminf(fminf(fminf(0.0f, v[0]), fminf(v[1], v[2])), v[3]);
     float hi = fmaxf(fmaxf(fmaxf(0.0f, v[0]), fmaxf(v[1], v[2])), v[3]);
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) {
-        lo = fminf(lo, __shfl_xor(lo, off, 64));
-        hi = fmaxf(hi, __shfl_xor(hi, off, 64));
-    }
+    // Over the 16 lanes of the segment (a DPP row) by DPP moves, no trip
+    // through LDS: neighbours in the quad, the other pair of the quad, the
+    // other quad of the half row (its mirror), the other half (the row's
+    // mirror).  Least and greatest do not depend on the order.
+    lo = fminf(lo, row_dpp<0xB1>(lo));
+    hi = fmaxf(hi, row_dpp<0xB1>(hi));
+    lo = fminf(lo, row_dpp<0x4E>(lo));
+    hi = fmaxf(hi, row_dpp<0x4E>(hi));
+    lo = fminf(lo, row_dpp<0x141>(lo));
+    hi = fmaxf(hi, row_dpp<0x141>(hi));
+    lo = fminf(lo, row_dpp<0x140>(lo));
+    hi = fmaxf(hi, row_dpp<0x140>(hi));
     const float s = __fdiv_rn(__fsub_rn(hi, lo), levels);
     const float inverse = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
     const float zero = rintf(__fmul_rn(-lo, inverse));
