@@ -763,7 +763,7 @@ def unet_step_line(dev, args):
 # dominant kernel -- the kernel(s) named, the algorithmic amount one call of
 # the configuration gives them (FLOPs, or the ideal HBM bytes where HBM
 # bounds them), the bound and MI355X's published peak.  The amounts are
-# those of the configurations' table of work units, restated:
+# those of the configurations' work units, restated:
 #   cfg1  Y = X W^T + b, X 2x4096x320 f32, W 320x320 f16: X 10.49 MB + W 0.20 +
 #         b + Y 10.49 = 21.18 MB (AI 79: HBM-bound at the split-FP16 rate)
 #   cfg2  the 36 products of 320x320 by 512 tiles: 2 x 36 x 320 x 320 x 512

@@ -3,7 +3,8 @@
 // computation of both -- the decisions of sdasm_compute_nodes and
 // sdasm_work_size (hooks.cc:29-196) and of match_chain, redirect_apart and
 // match_gated_gelu (fusion.cc:100-394), made over plain node descriptors
-// (sdhip_node) that a ggml backend fills from its graph, so
+// (sdhip_node) that a ggml backend fills from its graph (an adapter that
+// mirrors each ggml_tensor into one sdhip_node a graph), so
 // that the same nodes are fused, and the same redirects taken, as the
 // reference fuses and takes them.
 
