@@ -184,16 +184,22 @@ def test_quantized_attention_takes_wide_heads_and_any_group():
 
 def test_attention_work_size():
     """The split form takes the keys and values split into tiles of 32 keys in
-    the work buffer: per (image, head) and tile, the keys' two FP16 parts of
-    32 rows of 48 + 8 halves and the values' two parts of 64 rows of 32 + 8
-    halves at head size 40 -- 17408 bytes; the other forms take none."""
+    the work buffer: per (image, head) and tile at head size 40, the keys'
+    high FP16 parts in 32 rows of 48 + 8 halves, their low parts in 32 rows
+    of 32 + 8 (the last 8 dimensions keep theirs in the high rows' padding),
+    the values' high parts in 64 rows of 32 + 8 halves and their low parts in
+    32 (the last tile's are rows of the high parts) -- 13824 bytes, 14336 in
+    whole KB; the other forms take none."""
     lib = sdhip.load()
+    halves = 32 * (48 + 8) + 32 * (32 + 8) + 64 * (32 + 8) + 32 * (32 + 8)
+    record = (2 * halves + 1023) // 1024 * 1024
+    assert record == 14336
     q = tensor(F32, (2, 8, 4096, 40))
     k = tensor(F32, (2, 8, 4096, 40))
     y = tensor(F32, (2, 4096, 8, 40))
-    assert lib.sdhip_attention_work_size(q, k, k, y) == 2 * 8 * 128 * 17408
+    assert lib.sdhip_attention_work_size(q, k, k, y) == 2 * 8 * 128 * record
     k77 = tensor(F32, (2, 8, 77, 40))
-    assert lib.sdhip_attention_work_size(q, k77, k77, y) == 2 * 8 * 3 * 17408
+    assert lib.sdhip_attention_work_size(q, k77, k77, y) == 2 * 8 * 3 * record
     try:
         sdhip.set_tuning("attention_fp32=1")
         assert lib.sdhip_attention_work_size(q, k, k, y) == 0
