@@ -124,6 +124,43 @@ def test_attention_bench_shapes(gpu, name, lk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("d", [32, 40, 64, 80, 96, 128, 160])
+def test_attention_peaked_scores(gpu, d):
+    """The split form's head sizes with queries and keys ~N(0, 9): scores of
+    tens, so that the running maximum moves by large steps and most
+    exponentials underflow; 1000 keys (the last tile ragged, the keys split
+    across workgroups), heads sharing keys.  Against float64, within the
+    bound or, where single precision itself is further off at such scores,
+    twice the error of the same attention in single precision (the scores'
+    rounding grows with their size: the bound's 1e-6 is taken at unit
+    inputs)."""
+    b, lq, lk, h, hk = 1, 150, 1000, 4, 2
+    r = rng(d)
+    q = (3.0 * r.standard_normal((b, lq, h, d))).astype(np.float32)
+    k = (3.0 * r.standard_normal((b, lk, hk, d))).astype(np.float32)
+    v = r.standard_normal((b, lk, hk, d)).astype(np.float32)
+    q_d, k_d, v_d = dev(q, gpu), dev(k, gpu), dev(v, gpu)
+    y = unwritten((b, lq, h, d), gpu)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    sdhip.attention(q_d.permute(0, 2, 1, 3), k_d.permute(0, 2, 1, 3), v_d.permute(0, 2, 1, 3), y, scale)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    # The same in single precision: scores, softmax and sums in float32.
+    qh = q.transpose(0, 2, 1, 3)
+    kh = np.repeat(k.transpose(0, 2, 1, 3), h // hk, axis=1)
+    vh = np.repeat(v.transpose(0, 2, 1, 3), h // hk, axis=1)
+    sc = np.matmul(qh, kh.transpose(0, 1, 3, 2)) * np.float32(scale)
+    pr = np.exp(sc - sc.max(axis=-1, keepdims=True))
+    single = (np.matmul(pr, vh) / pr.sum(axis=-1, keepdims=True)).transpose(0, 2, 1, 3)
+    err32 = orc.metric(single.astype(np.float32), exact, mag)
+    print(f"peaked scores d={d}: {err:.3g} (single precision {err32:.3g})")
+    assert np.isfinite(y).all()
+    assert err <= max(BOUND, 2.0 * err32)
+
+
+@pytest.mark.gpu
 def test_attention_not_taken(gpu):
     """Heads of more than 512 dimensions are left to the caller; so is a soft cap."""
     q = torch.zeros((1, 40, 1, 640), device=gpu)
