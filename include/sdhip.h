@@ -88,7 +88,10 @@ const char *sdhip_last_error(void);
  * every name of the reference's Tuning is taken, with its default.  Those
  * that change what is computed: bits (2..8, the quantized products; 16, the
  * reference's products of 16-bit numbers: MUL_MAT, the gated GELU and direct
- * convolutions of FP16 weights take the other operand rounded to FP16),
+ * convolutions of FP16 weights take the other operand rounded to FP16; with
+ * half_format=1 both operands rounded to bfloat16 instead, and attention's
+ * queries, keys, values and exponentials too, cpu.cc:319-321,
+ * attention.cc:309-323),
  * input_bits, group, weight_group, quantize (with bits 2..8: 1 linear layers,
  * 2 convolutions -- direct, or F(2x2,3x3) for those Winograd takes -- 4
  * attention), winograd, winograd_positions, winograd4_positions,
@@ -103,7 +106,8 @@ const char *sdhip_last_error(void);
  * (winograd.cc:238-255, 1859-1866).  The other names that size the
  * reference's CPU blocks or choose among its CPU forms (conv_kc, mul_mat_mc,
  * amx_*, wide, prefetch, guided, ...) are taken and have no effect here;
- * half_format (bits=16's FP16 or bfloat16 products) is described with bits.  The reference's names take any int, as its
+ * half_format (1: bits=16's bfloat16 products; any other value its FP16 form)
+ * is described with bits.  The reference's names take any int, as its
  * parser does, and are clamped where it clamps them (quant.cc:59-67).  This
  * library's own: winograd_fp32, winograd_splits, gemm_stages, gemm_tiles,
  * gemm_core, qgemm_core, mul_mat_panels (0: MUL_MAT by the 64 x 64 core

@@ -19,6 +19,10 @@ struct AttentionArgs {
     int64_t d, dv, lq, lk, h, hk, b;
     float scale;
     int32_t khalf, vhalf;
+    // The products of 16 bits in bfloat16 (bits=16, half_format=1): the
+    // queries, keys, values and exponentials rounded to bfloat16 before their
+    // products, which are summed in single precision.
+    int32_t bf16;
     // Set by the launcher.
     int32_t dp, ldq, ldk, ldv;
     int64_t qblocks;

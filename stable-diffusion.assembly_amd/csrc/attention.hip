@@ -24,6 +24,16 @@
 // exponentials is kept in double precision, as the reference keeps it
 // (attention.cc:287-301), and the output is multiplied at the end by the
 // reciprocal of the sum rounded to single precision (attention.cc:1055-1062).
+//
+// With bits=16 and half_format=1 (AttentionArgs::bf16) the generic and wide
+// forms take every head: they round the queries, keys and values, and the
+// exponentials the second product takes, to bfloat16 before their products --
+// which are exact in single precision and summed there, the products of
+// bfloat16 first parts of the reference's vector units (attention.cc:309-323,
+// 466-467).  Each query's largest score is found over all its keys before any
+// exponential, so that each is rounded from exp(s - max) of the whole row, as
+// the reference's two passes round them; the sum of the exponentials takes
+// them unrounded, as the reference's does.
 
 #include <type_traits>
 
@@ -72,7 +82,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
         const int64_t i = q0 + qi;
         float x = 0.0f;
         if (e < a.d && i < a.lq) x = a.q[bi * a.qnb3 + hi * a.qnb2 + i * a.qnb1 + e];
-        qs[qi * a.ldq + e] = x;
+        qs[qi * a.ldq + e] = bf16_operand(x, a.bf16);
     }
 
     const int64_t kbase = bi * a.knb3 + kh * a.knb2;
@@ -84,23 +94,21 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
     double l = 0.0;
     const float *qw = qs + (wave * 16 + lr) * a.ldq + lg;
 
-    for (int64_t k0 = 0; k0 < a.lk; k0 += kKeys) {
-        __syncthreads();  // the last block's keys and values are read
+    // The block of keys from k0 into LDS, zeros past d and past lk.
+    const auto stage_keys = [&](int64_t k0) {
         for (int idx = tid; idx < kKeys * a.dp; idx += 256) {
             const int j = idx / a.dp, e = idx - j * a.dp;
             const int64_t key = k0 + j;
-            ks[j * a.ldk + e] = (e < a.d && key < a.lk) ? load_kv<KHALF>(a.k, kbase + key * a.knb1 + e) : 0.0f;
+            ks[j * a.ldk + e] =
+                (e < a.d && key < a.lk) ? bf16_operand(load_kv<KHALF>(a.k, kbase + key * a.knb1 + e), a.bf16) : 0.0f;
         }
-        for (int idx = tid; idx < kKeys * 16 * NDV; idx += 256) {
-            const int j = idx / (16 * NDV), e = idx - j * (16 * NDV);
-            const int64_t key = k0 + j;
-            vs[j * a.ldv + e] = (e < a.dv && key < a.lk) ? load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e) : 0.0f;
-        }
-        __syncthreads();
-
-        // S^T = K Q^T for two tiles of 16 keys: the lane's scores of its
-        // query lr, keys 16 t + 4 lg + r.
-        float4v s[2] = {float4v{}, float4v{}};
+    };
+    // S^T = K Q^T for two tiles of 16 keys, scaled, -inf past lk: the lane's
+    // scores of its query lr, keys 16 t + 4 lg + r; and the largest of the
+    // query's over its four lanes.
+    const auto block_scores = [&](int64_t k0, float4v(&s)[2]) {
+        s[0] = float4v{};
+        s[1] = float4v{};
         for (int e = 0; e < a.dp; e += 4) {
             const float qv = qw[e];
 #pragma unroll
@@ -120,7 +128,37 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
                 mx = fmaxf(mx, x);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        return fmaxf(mx, __shfl_xor(mx, 32, 64));
+    };
+
+    // Products in bfloat16: each query's largest score over all the keys
+    // first, a pass of the first product alone, so that every exponential is
+    // exp(s - max) of the whole row rounded to bfloat16 from that, as the
+    // reference's two passes round them (attention.cc:519-545); the running
+    // rescaling below then multiplies by exp(0) = 1.
+    if (a.bf16) {
+        for (int64_t k0 = 0; k0 < a.lk; k0 += kKeys) {
+            __syncthreads();
+            stage_keys(k0);
+            __syncthreads();
+            float4v s[2];
+            m = fmaxf(m, block_scores(k0, s));
+        }
+    }
+
+    for (int64_t k0 = 0; k0 < a.lk; k0 += kKeys) {
+        __syncthreads();  // the last block's keys and values are read
+        stage_keys(k0);
+        for (int idx = tid; idx < kKeys * 16 * NDV; idx += 256) {
+            const int j = idx / (16 * NDV), e = idx - j * (16 * NDV);
+            const int64_t key = k0 + j;
+            vs[j * a.ldv + e] =
+                (e < a.dv && key < a.lk) ? bf16_operand(load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e), a.bf16) : 0.0f;
+        }
+        __syncthreads();
+
+        float4v s[2];
+        const float mx = block_scores(k0, s);
         const float mnew = fmaxf(m, mx);
         const float alpha = m == -INFINITY ? 0.0f : cephes_exp(m - mnew);
         m = mnew;
@@ -130,7 +168,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float p = s[t][r] == -INFINITY ? 0.0f : cephes_exp(s[t][r] - mnew);
-                s[t][r] = p;
+                s[t][r] = bf16_operand(p, a.bf16);  // the sum takes p as it is
                 part += static_cast<double>(p);
             }
         l = l * static_cast<double>(alpha) + part;
@@ -190,7 +228,9 @@ struct WideSplits {
 inline WideSplits wide_splits(const AttentionArgs &a) {
     const int64_t blocks = ceil_div(a.lq, kQueries) * a.h * a.b;
     int64_t sp = ceil_div(512, blocks);
-    const int64_t most = a.lk / 256 > 1 ? a.lk / 256 : 1;
+    // Products in bfloat16 take all the keys in one split: each exponential
+    // is rounded from exp(s - max) of the whole row.
+    const int64_t most = a.lk / 256 > 1 && !a.bf16 ? a.lk / 256 : 1;
     sp = sp < most ? sp : most;
     WideSplits w;
     w.key_len = round_up(ceil_div(a.lk, sp), kKeys);
@@ -254,10 +294,13 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
     double l = 0.0;
     const float *qw = qs + (wave * 16 + lr) * kWideLd + lg;
 
-    for (int64_t k0 = k_begin; k0 < k_end; k0 += kKeys) {
-        // S^T = K Q^T for two tiles of 16 keys, over the chunks of the
-        // dimensions: the lane's scores of its query lr, keys 16 t + 4 lg + r.
-        float4v s[2] = {float4v{}, float4v{}};
+    // S^T = K Q^T for two tiles of 16 keys, over the chunks of the
+    // dimensions, scaled, -inf past the split's keys: the lane's scores of its
+    // query lr, keys 16 t + 4 lg + r; and the largest of the query's over its
+    // four lanes.
+    const auto block_scores = [&](int64_t k0, float4v(&s)[2]) {
+        s[0] = float4v{};
+        s[1] = float4v{};
         for (int e0 = 0; e0 < a.dp; e0 += kWideChunk) {
             const int dc = a.dp - e0 < kWideChunk ? static_cast<int>(a.dp - e0) : kWideChunk;
             __syncthreads();  // the last chunk's queries and keys are read
@@ -266,13 +309,14 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
                 const int64_t i = q0 + qi;
                 float x = 0.0f;
                 if (e0 + e < a.d && i < a.lq) x = a.q[qbase + i * a.qnb1 + e0 + e];
-                qs[qi * kWideLd + e] = x;
+                qs[qi * kWideLd + e] = bf16_operand(x, a.bf16);
             }
             for (int idx = tid; idx < kKeys * dc; idx += 256) {
                 const int j = idx / dc, e = idx - j * dc;
                 const int64_t key = k0 + j;
-                ks[j * kWideLd + e] =
-                    (e0 + e < a.d && key < k_end) ? load_kv<KHALF>(a.k, kbase + key * a.knb1 + e0 + e) : 0.0f;
+                ks[j * kWideLd + e] = (e0 + e < a.d && key < k_end)
+                                          ? bf16_operand(load_kv<KHALF>(a.k, kbase + key * a.knb1 + e0 + e), a.bf16)
+                                          : 0.0f;
             }
             __syncthreads();
             for (int e = 0; e < dc; e += 4) {
@@ -284,14 +328,6 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
                 }
             }
         }
-        __syncthreads();  // the last block's values are read
-        for (int idx = tid; idx < kKeys * 16 * NDV; idx += 256) {
-            const int j = idx / (16 * NDV), e = idx - j * (16 * NDV);
-            const int64_t key = k0 + j;
-            vs[j * a.ldv + e] = (e < a.dv && key < k_end) ? load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e) : 0.0f;
-        }
-        __syncthreads();
-
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -303,7 +339,30 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
                 mx = fmaxf(mx, x);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        return fmaxf(mx, __shfl_xor(mx, 32, 64));
+    };
+
+    // Products in bfloat16 (one split of all the keys): each query's largest
+    // score first, as the generic form takes it.
+    if (a.bf16) {
+        for (int64_t k0 = k_begin; k0 < k_end; k0 += kKeys) {
+            float4v s[2];
+            m = fmaxf(m, block_scores(k0, s));
+        }
+    }
+
+    for (int64_t k0 = k_begin; k0 < k_end; k0 += kKeys) {
+        float4v s[2];
+        const float mx = block_scores(k0, s);
+        __syncthreads();  // the last block's values are read
+        for (int idx = tid; idx < kKeys * 16 * NDV; idx += 256) {
+            const int j = idx / (16 * NDV), e = idx - j * (16 * NDV);
+            const int64_t key = k0 + j;
+            vs[j * a.ldv + e] =
+                (e < a.dv && key < k_end) ? bf16_operand(load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e), a.bf16) : 0.0f;
+        }
+        __syncthreads();
+
         const float mnew = fmaxf(m, mx);
         const float alpha = m == -INFINITY ? 0.0f : cephes_exp(m - mnew);
         m = mnew;
@@ -313,7 +372,7 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float p = s[t][r] == -INFINITY ? 0.0f : cephes_exp(s[t][r] - mnew);
-                s[t][r] = p;
+                s[t][r] = bf16_operand(p, a.bf16);  // the sum takes p as it is
                 part += static_cast<double>(p);
             }
         l = l * static_cast<double>(alpha) + part;
@@ -1701,9 +1760,10 @@ bool fast_form(const AttentionArgs &a) {
 }
 
 // Whether the split form takes the operands: the fast form's, unless the
-// tuning asks for another.
+// tuning asks for another, or for products in bfloat16 (which the generic and
+// wide forms compute).
 bool split_form(const AttentionArgs &a) {
-    return fast_form(a) && a.lk > 0 && tuning().attention_generic == 0 && tuning().attention_fp32 == 0;
+    return fast_form(a) && a.lk > 0 && tuning().attention_generic == 0 && tuning().attention_fp32 == 0 && !a.bf16;
 }
 
 size_t split_form_work(const AttentionArgs &a) {
@@ -1764,7 +1824,7 @@ hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
                        a.knb3 % 4 == 0 && a.vnb3 % 4 == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
     if (!a.khalf && !a.vhalf && a.dp > 384 && a.dp <= 512 && a.d % 4 == 0 && a.dv % 4 == 0 && rows4 && NDV == 32 &&
-        tuning().attention_generic == 0) {
+        tuning().attention_generic == 0 && !a.bf16) {
         const size_t lds2 = sizeof(float) * (kKeys * (512 + 4) + kKeys * (16 * NDV + 4));
         hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(attention_wide2_kernel<512, NDV>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));
@@ -1823,7 +1883,7 @@ size_t attention_work_bytes(const AttentionArgs &a) {
 hipError_t launch_attention(AttentionArgs a, void *work, hipStream_t stream) {
     if (a.lq == 0 || a.h == 0 || a.b == 0) return hipSuccess;  // no output
     if (split_form(a)) return launch_split_form(a, work, stream);
-    if (fast_form(a) && tuning().attention_generic == 0) return launch_fast_form(a, stream);
+    if (fast_form(a) && tuning().attention_generic == 0 && !a.bf16) return launch_fast_form(a, stream);
     a.dp = static_cast<int>(round_up(a.d, 4));
     a.ldq = a.dp + 1;
     a.ldk = a.dp + 1;

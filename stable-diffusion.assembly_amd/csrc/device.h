@@ -41,6 +41,13 @@ __device__ __forceinline__ void split_scaled(float s, _Float16 &hi, _Float16 &lo
 
 __device__ __forceinline__ void split2(float x, _Float16 &hi, _Float16 &lo) { split_scaled(x * kSplitDown, hi, lo); }
 
+// x rounded to bfloat16, to nearest with ties to even, and widened back: the
+// product of two such numbers is exact in single precision.
+__device__ __forceinline__ float bf16_round(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+
+// x as a product of 16 bits takes it: rounded to bfloat16 where bf says so.
+__device__ __forceinline__ float bf16_operand(float x, int32_t bf) { return bf ? bf16_round(x) : x; }
+
 // ------------------------------------------------------------------ scalar math
 
 // exp(x) by Cephes' expf method, as the reference's exponential()

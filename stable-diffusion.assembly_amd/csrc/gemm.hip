@@ -46,10 +46,22 @@ constexpr int kLdk = kBK + 8;  // halves per LDS row: 80 bytes, 16-byte aligned,
 // Which operands are single precision, split into two FP16 planes.
 // kSplitNone: the products of 16 bits (bits=16): the single-precision
 // operand rounded to FP16, its first part alone, one MFMA a product.
-enum Split { kSplitA = 0, kSplitB = 1, kSplitBoth = 2, kSplitNone = 3 };
+// kBf16: the same in bfloat16 (half_format=1): both operands rounded to
+// bfloat16 (to nearest, ties to even, as vcvtne2ps2bf16 rounds them), one
+// bfloat16 MFMA a product; the LDS planes hold their bits.
+enum Split { kSplitA = 0, kSplitB = 1, kSplitBoth = 2, kSplitNone = 3, kBf16 = 4 };
 
-constexpr int planes_a(int mode) { return mode == kSplitB || mode == kSplitNone ? 1 : 2; }
-constexpr int planes_b(int mode) { return mode == kSplitA || mode == kSplitNone ? 1 : 2; }
+constexpr int planes_a(int mode) { return mode == kSplitB || mode == kSplitNone || mode == kBf16 ? 1 : 2; }
+constexpr int planes_b(int mode) { return mode == kSplitA || mode == kSplitNone || mode == kBf16 ? 1 : 2; }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// The bits of x rounded to bfloat16 (to nearest, ties to even), in a 16-bit
+// container of the LDS planes' type.
+__device__ __forceinline__ _Float16 bf16_bits(float x) {
+    const __bf16 b = static_cast<__bf16>(x);
+    return __builtin_bit_cast(_Float16, b);
+}
 
 // ------------------------------------------------------------------ MFMA core
 
@@ -78,6 +90,12 @@ __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float1
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
+                if constexpr (MODE == kBf16) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[i]),
+                                                                        __builtin_bit_cast(bf16x8, b[j]), acc[i][j],
+                                                                        0, 0, 0);
+                    continue;
+                }
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
                 if (planes_a(MODE) == 2) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
@@ -102,8 +120,10 @@ __device__ __forceinline__ void mfma_step(float16v (&acc)[TM][TN], const _Float1
 // the end read the block's first row instead, whose products are never
 // stored -- the loads then have no conditions, and so no branches that would
 // wait on the loads before them.
-template <int BR, bool VEC, bool FULL, bool LO = true>
+// BF (with !LO): the first parts in bfloat16 instead.
+template <int BR, bool VEC, bool FULL, bool LO = true, bool BF = false>
 struct F32Rows {
+    static_assert(!BF || !LO, "the bfloat16 form takes the first parts alone");
     static constexpr int kQuads = BR * kBK / 4 / 256;  // float4 per thread
     static_assert(kQuads >= 1, "tile too small for 256 threads");
     static_assert(!FULL || VEC, "FULL loads are vector loads");
@@ -154,6 +174,14 @@ struct F32Rows {
             const int r = idx / (kBK / 4);
             const int kq = (idx % (kBK / 4)) * 4;
             half4 h, l;
+            if constexpr (BF) {
+                h[0] = bf16_bits(v[i].x * kSplitDown);
+                h[1] = bf16_bits(v[i].y * kSplitDown);
+                h[2] = bf16_bits(v[i].z * kSplitDown);
+                h[3] = bf16_bits(v[i].w * kSplitDown);
+                *reinterpret_cast<half4 *>(hi + r * kLdk + kq) = h;
+                continue;
+            }
             _Float16 a, b;
             split2(v[i].x, a, b); h[0] = a; l[0] = b;
             split2(v[i].y, a, b); h[1] = a; l[1] = b;
@@ -205,8 +233,10 @@ struct ScaledF32Rows {
 // (with FULL): the rows held in blocks of one K-step, [k / 32][row][k % 32],
 // `ld` then 32 and `step` elements from one block to the next, so that a
 // step's rows are whole cache lines in a row.
-template <int BR, bool VEC, bool FULL, int PLANES = 1, bool BLOCKED = false>
+// BF: each FP16 number rounded to bfloat16 on its way into LDS.
+template <int BR, bool VEC, bool FULL, int PLANES = 1, bool BLOCKED = false, bool BF = false>
 struct F16Rows {
+    static_assert(!BF || PLANES == 1, "the bfloat16 form takes one plane");
     static constexpr int kOcts = BR * kBK / 8 / 256;  // 8 halves per load
     static_assert(kOcts >= 1, "tile too small for 256 threads");
     static_assert(!FULL || VEC, "FULL loads are vector loads");
@@ -264,6 +294,13 @@ struct F16Rows {
             const int idx = tid + 256 * i;
             const int r = idx / (kBK / 8);
             const int kq = (idx % (kBK / 8)) * 8;
+            if constexpr (BF) {
+                half8 b;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) b[e] = bf16_bits(static_cast<float>(v[0][i][e]));
+                *reinterpret_cast<half8 *>(dst + r * kLdk + kq) = b;
+                continue;
+            }
             *reinterpret_cast<half8 *>(dst + r * kLdk + kq) = v[0][i];
             if (PLANES == 2) *reinterpret_cast<half8 *>(dst_lo + r * kLdk + kq) = v[PLANES - 1][i];
         }
@@ -277,8 +314,10 @@ struct F16Rows {
 // positions, which are consecutive in a row of the image at stride 1.  FULL
 // (1x1 kernels, K = IC a multiple of BK): positions past the last read the
 // block's first, never stored, and the loads have no conditions.
-template <int BN, bool POINTWISE, bool FULL, bool K3 = false, bool LO = true>
+// BF (with !LO): the first parts in bfloat16 instead.
+template <int BN, bool POINTWISE, bool FULL, bool K3 = false, bool LO = true, bool BF = false>
 struct Columns {
+    static_assert(!BF || !LO, "the bfloat16 form takes the first parts alone");
     static constexpr int kLoads = BN * kBK / 4 / 256;
     static_assert(!FULL || POINTWISE, "FULL columns are those of 1x1 kernels");
     float v[kLoads][4];
@@ -365,7 +404,12 @@ struct Columns {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 _Float16 a, b;
-                split2(v[i][e], a, b);
+                if constexpr (BF) {
+                    a = bf16_bits(v[i][e] * kSplitDown);
+                    b = a;
+                } else {
+                    split2(v[i][e], a, b);
+                }
                 h[e] = a;
                 l[e] = b;
             }
@@ -448,15 +492,16 @@ constexpr int lds_halves() {
 // the block's 128 rows of W are 64 features of the first half and the same 64
 // of the second (the gate), each wave's two column tiles a pair, and the
 // block writes out[m * ldo + j] = P[m][j] GELU(P[m][half + j]).
-template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS, int WP = 1, bool HALF = false>
+template <int TM, int TN, bool GATED, bool VECX, bool VECW, bool FULL, int NS, int WP = 1, int HALF = 0>
 __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
     constexpr int BM = 64 * TM;
     constexpr int BN = 64 * TN;
     // WP: the weights' planes, 1 (FP16 weights) or 2 (single-precision ones
     // split, w_plane apart): then three MFMAs a product, x and W both split.
-    // HALF: the products of 16 bits, x rounded to FP16, one MFMA a product.
+    // HALF: the products of 16 bits, x rounded to FP16 (1) or both operands
+    // to bfloat16 (2), one MFMA a product.
     static_assert(!HALF || WP == 1, "products of 16 bits take FP16 weights");
-    constexpr int MODE = HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitA;
+    constexpr int MODE = HALF == 2 ? kBf16 : HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitA;
     static_assert(!GATED || TN == 2, "the gated form pairs two column tiles");
     __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, MODE>()];
 
@@ -490,8 +535,8 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    F32Rows<BM, VECX, FULL, !HALF> xa[NS];
-    F16Rows<BN, VECW, FULL, WP> wb[NS];
+    F32Rows<BM, VECX, FULL, !HALF, HALF == 2> xa[NS];
+    F16Rows<BN, VECW, FULL, WP, false, HALF == 2> wb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         xa[s].init(p.x, p.ldx, x_row, p.K, tid);
@@ -1166,14 +1211,15 @@ __global__ __launch_bounds__(256) void mul_mat_sum_kernel(MulMatArgs p, const fl
 // y[n][oc][pos] = sum_k W[oc][k] columns[k][pos], the chain applied; W rows
 // K-contiguous FP16 (the kernel as ggml holds it, [OC][IC][KH][KW]).
 template <int TM, int TN, bool POINTWISE, bool VECW, bool FULL, int NS, bool K3 = false, int WP = 1,
-          bool HALF = false>
+          int HALF = 0>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
     constexpr int BM = 64 * TM;  // output channels
     constexpr int BN = 64 * TN;  // positions
     // WP as mul_mat_kernel's: split single-precision kernels in two planes;
-    // HALF, the products of 16 bits: the columns rounded to FP16.
+    // HALF, the products of 16 bits: the columns rounded to FP16 (1), or both
+    // operands to bfloat16 (2).
     static_assert(!HALF || WP == 1, "products of 16 bits take FP16 kernels");
-    constexpr int MODE = HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitB;
+    constexpr int MODE = HALF == 2 ? kBf16 : HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitB;
     __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<TM, TN, MODE>()];
 
     const int tid = threadIdx.x;
@@ -1195,8 +1241,8 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs c) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-    F16Rows<BM, VECW, FULL, WP> wa[NS];
-    Columns<BN, POINTWISE, FULL, K3, !HALF> xb[NS];
+    F16Rows<BM, VECW, FULL, WP, false, HALF == 2> wa[NS];
+    Columns<BN, POINTWISE, FULL, K3, !HALF, HALF == 2> xb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         wa[s].init(c.w, c.ldw, w_row, c.K, tid, c.w_plane);
@@ -1307,12 +1353,12 @@ __global__ __launch_bounds__(256) void columns_kernel(ConvArgs c, float *__restr
 // part[s][oc][p] = 16 sum over split s's k of W[oc][k] cols[p][k]: blocks of
 // 64 output channels by 64 positions, the splits of split_len (a multiple of
 // the K-step) one after the other in the grid.
-template <int NS, int WP = 1, bool HALF = false>
+template <int NS, int WP = 1, int HALF = 0>
 __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const float *__restrict__ cols,
                                                            int64_t split_len, int64_t p_blocks,
                                                            float *__restrict__ part) {
     constexpr int BM = 64, BN = 64;
-    constexpr int MODE = HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitB;
+    constexpr int MODE = HALF == 2 ? kBf16 : HALF ? kSplitNone : WP == 2 ? kSplitBoth : kSplitB;
     __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<1, 1, MODE>()];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1332,8 +1378,8 @@ __global__ __launch_bounds__(256) void conv_columns_kernel(ConvArgs c, const flo
 
     float16v acc[1][1];
     acc[0][0] = float16v{};
-    F16Rows<BM, true, true, WP> wa[NS];
-    F32Rows<BN, true, true, !HALF> xb[NS];
+    F16Rows<BM, true, true, WP, false, HALF == 2> wa[NS];
+    F32Rows<BN, true, true, !HALF, HALF == 2> xb[NS];
     const auto w_row = [&](int r) -> int64_t { return oc0 + r < c.oc ? oc0 + r : -1; };
     const auto p_row = [&](int r) -> int64_t { return p0 + r < c.P ? p0 + r : -1; };
 #pragma unroll
@@ -1486,14 +1532,22 @@ hipError_t launch_mul_mat_t(const MulMatArgs &p, int stages, hipStream_t stream)
     KernelScope scope(GATED ? "mul_mat_gated" : "mul_mat", stream);
     if (p.w_scale != nullptr) return launch_mul_mat_w32<TM, TN, GATED>(a, grid, stream);
     if (p.half16) {
-        // The products of 16 bits.
-        if (full) {
-            SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 1, true>), grid, block, 0, stream, a);
-        } else if (vx && vw) {
-            SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 1, true>), grid, block, 0, stream, a);
+        // The products of 16 bits, in FP16 (half16 1) or bfloat16 (2).
+        const auto half = [&](auto form) {
+            constexpr int H = decltype(form)::value;
+            if (full) {
+                SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, true, 2, 1, H>), grid, block, 0, stream, a);
+            } else if (vx && vw) {
+                SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, true, true, false, 2, 1, H>), grid, block, 0, stream, a);
+            } else {
+                SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, false, false, false, 2, 1, H>), grid, block, 0, stream,
+                             a);
+            }
+        };
+        if (p.half16 == 2) {
+            half(std::integral_constant<int, 2>{});
         } else {
-            SDHIP_LAUNCH((mul_mat_kernel<TM, TN, GATED, false, false, false, 2, 1, true>), grid, block, 0, stream,
-                         a);
+            half(std::integral_constant<int, 1>{});
         }
         return hipGetLastError();
     }
@@ -1525,16 +1579,24 @@ hipError_t launch_conv_t(const ConvArgs &c, int stages, hipStream_t stream) {
     dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     KernelScope scope(POINTWISE ? "conv_direct_pointwise" : "conv_direct", stream);
     if (c.half16) {
-        // The products of 16 bits.
-        if (full) {
-            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 1, true>), grid, block,
-                         0, stream, a);
-        } else if (vw) {
-            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 1, true>), grid, block, 0,
-                         stream, a);
+        // The products of 16 bits, in FP16 (half16 1) or bfloat16 (2).
+        const auto half = [&](auto form) {
+            constexpr int H = decltype(form)::value;
+            if (full) {
+                SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, POINTWISE, 2, false, 1, H>), grid, block,
+                             0, stream, a);
+            } else if (vw) {
+                SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, true, false, 2, false, 1, H>), grid, block, 0,
+                             stream, a);
+            } else {
+                SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2, false, 1, H>), grid, block, 0,
+                             stream, a);
+            }
+        };
+        if (c.half16 == 2) {
+            half(std::integral_constant<int, 2>{});
         } else {
-            SDHIP_LAUNCH((conv_direct_kernel<TM, TN, POINTWISE, false, false, 2, false, 1, true>), grid, block, 0,
-                         stream, a);
+            half(std::integral_constant<int, 1>{});
         }
         return hipGetLastError();
     }
@@ -1837,8 +1899,11 @@ hipError_t launch_conv_columns(const ConvArgs &c, void *work, GemmShape g, hipSt
         if (c.w_scale != nullptr) {
             SDHIP_LAUNCH((conv_columns_kernel<2, 2>), grid, dim3(256), 0, stream, a, cols, l.split_len,
                          l.p_blocks, part);
+        } else if (c.half16 == 2) {
+            SDHIP_LAUNCH((conv_columns_kernel<2, 1, 2>), grid, dim3(256), 0, stream, a, cols, l.split_len,
+                         l.p_blocks, part);
         } else if (c.half16) {
-            SDHIP_LAUNCH((conv_columns_kernel<2, 1, true>), grid, dim3(256), 0, stream, a, cols, l.split_len,
+            SDHIP_LAUNCH((conv_columns_kernel<2, 1, 1>), grid, dim3(256), 0, stream, a, cols, l.split_len,
                          l.p_blocks, part);
         } else if (g.stages == 4) {
             SDHIP_LAUNCH((conv_columns_kernel<4>), grid, dim3(256), 0, stream, a, cols, l.split_len, l.p_blocks,

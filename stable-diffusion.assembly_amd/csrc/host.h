@@ -17,7 +17,10 @@ struct Tuning {
     // 16 bits: MUL_MAT and direct convolutions of FP16 weights by their other
     // operand rounded to FP16, one product each, summed in single precision
     // (the reference's FP16 format of gemm.h:226-237); Winograd and attention
-    // stay single precision, as on the reference's vector units.
+    // stay single precision, as on the reference's vector units.  With
+    // half_format=1 (below), the bfloat16 format: both operands of those
+    // products rounded to bfloat16, and attention's too (cpu.cc:319-321,
+    // attention.cc:309-323).
     int bits = 0;
     int input_bits = 8;              // the inputs' bits, unsigned with a zero point
     int group = 64;                  // numbers of k sharing a scale, a multiple of 4

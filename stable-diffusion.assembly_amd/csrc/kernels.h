@@ -26,8 +26,8 @@ struct MulMatArgs {
     // floats apart), for the bits mode's quantizer; null for FP16 weights.
     const float *w32;
     int64_t ldw32;
-    // The products of 16 bits (bits=16): x rounded to FP16, one MFMA a
-    // product by the FP16 weights.
+    // The products of 16 bits (bits=16): x rounded to FP16 (1), or x and
+    // the FP16 weights to bfloat16 (2), one MFMA a product.
     int32_t half16;
     float *y;  // the output, or the redirect, or the gated output
     int64_t ldy;
@@ -87,7 +87,7 @@ struct ConvArgs {
     int64_t w_plane;
     const float *w_scale;
     const float *w32;  // the kernel in single precision, for the bits mode's quantizer; null for FP16
-    int32_t half16;    // the products of 16 bits (bits=16): the columns rounded to FP16
+    int32_t half16;    // the products of 16 bits (bits=16): the columns rounded to FP16 (1) or both operands to bfloat16 (2)
     int64_t kw, kh, oc;
     float *y;  // [N][OC][OH][OW], strides ynb1..3
     int64_t ynb1, ynb2, ynb3;

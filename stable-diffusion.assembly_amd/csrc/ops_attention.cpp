@@ -97,6 +97,11 @@ AttentionArgs args_of(const sdhip_tensor *q, const sdhip_tensor *k, const sdhip_
     a.hk = k->ne[2];
     a.b = q->ne[3];
     a.scale = scale;
+    // bits=16 with half_format=1: the products of the first parts in
+    // bfloat16, as on the reference's vector units of AVX512-BF16
+    // (attention.cc:309-323, 466-467).  With the FP16 format attention stays
+    // single precision there, and here.
+    a.bf16 = tuning().bits == 16 && tuning().half_format == 1 ? 1 : 0;
     return a;
 }
 

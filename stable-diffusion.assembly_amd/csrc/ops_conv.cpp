@@ -127,8 +127,9 @@ ConvArgs conv_args(const sdhip_tensor *kernel, const sdhip_tensor *input, const 
     c.K = c.ic * c.kh * c.kw;
     c.ldw = c.K;
     // The products of 16 bits: FP16 kernels by the columns rounded to FP16
-    // (cpu.cc:336-366; Winograd's products stay single precision there).
-    c.half16 = tuning().bits == 16 && kernel->type == SDHIP_TYPE_F16 ? 1 : 0;
+    // (cpu.cc:336-366; Winograd's products stay single precision there), or
+    // with half_format=1 both rounded to bfloat16 (cpu.cc:319-321).
+    c.half16 = tuning().bits == 16 && kernel->type == SDHIP_TYPE_F16 ? (tuning().half_format == 1 ? 2 : 1) : 0;
     c.taps = c.kh * c.kw;
     c.plane = c.oh * c.ow;
     c.P = c.n * c.plane;

@@ -35,8 +35,11 @@ MulMatArgs args_of(const sdhip_tensor *w, const sdhip_tensor *x, const sdhip_ten
     a.ne2 = y->ne[2];
     a.ldy = y->nb[1] / 4;
     // The products of 16 bits: FP16 weights by x rounded to FP16
-    // (split_form's first parts alone, cpu.cc:336-366).
-    a.half16 = tuning().bits == 16 && w->type == SDHIP_TYPE_F16 ? 1 : 0;
+    // (split_form's first parts alone, cpu.cc:336-366), or with
+    // half_format=1 both rounded to bfloat16 (cpu.cc:319-321, the first parts
+    // of sdasm_amx_pack_rows and _f16); 0 and 2 take FP16, the form that
+    // fits here.
+    a.half16 = tuning().bits == 16 && w->type == SDHIP_TYPE_F16 ? (tuning().half_format == 1 ? 2 : 1) : 0;
     return a;
 }
 
