@@ -14,6 +14,8 @@ float64 products of the bfloat16 operands -- for attention, of the
 reference's two-pass softmax, whose exponentials are rounded from
 exp(s - max) of the whole row."""
 
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -294,3 +296,33 @@ def test_attention_bfloat16(gpu, c):
     assert np.isfinite(y).all()
     assert err <= K_HALF and errb <= 1e-4
     assert err16 <= 1e-6 < err / 10
+
+
+def test_rounded_bf16_pinned():
+    """The bfloat16 rounding the checks above take is torch's conversion
+    (to nearest, ties to even): on random numbers over many binades, on exact
+    ties, which go to the even neighbour, and at the largest finite floats."""
+    r = np.random.default_rng(3)
+    x = (r.standard_normal(200000) * np.exp2(r.integers(-60, 60, 200000))).astype(np.float32)
+    ties = np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, -(1 + 2.0 ** -8), 2.0 ** -130 * (1 + 2.0 ** -8)], np.float32)
+    x = np.concatenate([x, ties, np.array([3.0e38, -3.0e38, 0.0, -0.0], np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy().astype(np.float64)
+    assert np.array_equal(rounded_bf16(x), ref)
+    assert rounded_bf16(ties)[0] == 1.0 and rounded_bf16(ties)[1] == 1 + 2.0 ** -6
+
+
+def test_bf16_attention_restatement_pinned(monkeypatch):
+    """The float64 restatement of attention's bfloat16 products: with its
+    roundings taken out it is the exact attention of the oracle (heads
+    sharing keys, ragged sizes); with them, within kHalf of it and not
+    nearer than the roundings allow."""
+    r = np.random.default_rng(4)
+    q = r.uniform(-1, 1, (2, 19, 4, 24)).astype(np.float32)
+    k = r.uniform(-1, 1, (2, 33, 2, 24)).astype(np.float32)
+    v = r.uniform(-1, 1, (2, 33, 2, 24)).astype(np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(24)))
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    rounded_err = orc.metric(bf16_attention(q, k, v, scale), exact, mag)
+    assert 1e-4 < rounded_err <= K_HALF
+    monkeypatch.setattr(sys.modules[__name__], "rounded_bf16", lambda x: np.asarray(x, np.float64))
+    assert orc.metric(bf16_attention(q, k, v, scale), exact, mag) <= 1e-7
