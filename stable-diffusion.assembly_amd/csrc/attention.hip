@@ -1010,14 +1010,21 @@ __device__ __forceinline__ void split_values(V vt, _Float16 *rec) {
 }
 
 // The tiles of the keys and values of every (image, head of the keys), one
-// workgroup a tile: grid (tiles, b hk).
+// workgroup a tile of nk a head.  Block (bi nk + kt) hk + kh: the heads of one
+// tile of keys, whose rows lie side by side in memory ([b][lk][hk][d]) and
+// share its lines, are consecutive blocks of one XCD, which its L2 serves
+// together.
 template <int D, int KB>
-__global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _Float16 *__restrict__ tiles) {
+__global__ __launch_bounds__(256) void attention_tiles_kernel(AttentionArgs a, _Float16 *__restrict__ tiles,
+                                                              uint32_t nk) {
     using S = Split<D, KB>;
-    const int64_t kt = blockIdx.x;
-    const int64_t bh = blockIdx.y;
-    const int64_t bi = bh / a.hk, kh = bh - bi * a.hk;
-    const int64_t nk = gridDim.x;
+    const uint32_t blk = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t hk = static_cast<uint32_t>(a.hk);
+    const uint32_t rest = blk / hk;
+    const int64_t kh = blk - rest * hk;
+    const int64_t bi = rest / nk;
+    const int64_t kt = rest - static_cast<uint32_t>(bi) * nk;
+    const int64_t bh = bi * a.hk + kh;
     _Float16 *rec = tiles + (bh * nk + kt) * (S::kRecord / 2);
     const float *vg = static_cast<const float *>(a.v) + bi * a.vnb3 + kh * a.vnb2;
     split_keys<D, KB>(a, bi, kh, kt, rec);
@@ -1725,11 +1732,13 @@ hipError_t launch_split(AttentionArgs a, void *work, hipStream_t stream) {
     // (cross-attention's 77 at heads of up to 64): each workgroup splits them
     // itself, with no launch before it.
     if (nk < SH::kStages) return launch_split_t<D, true>(a, nullptr, stream);
+    // The tiles' grid is one dimension of 256-thread blocks: under 2^24 of
+    // them (a work buffer of 14 KB or more a tile, past 230 GB, before that).
+    if (nk * a.b * a.hk >= (int64_t{1} << 24)) return hipErrorInvalidValue;
     {
         KernelScope scope("attention.tiles", stream);
-        SDHIP_LAUNCH((attention_tiles_kernel<D, SH::kKeys>),
-                     dim3(static_cast<uint32_t>(nk), static_cast<uint32_t>(a.b * a.hk)), dim3(256), 0, stream,
-                     a, static_cast<_Float16 *>(work));
+        SDHIP_LAUNCH((attention_tiles_kernel<D, SH::kKeys>), dim3(static_cast<uint32_t>(nk * a.b * a.hk)),
+                     dim3(256), 0, stream, a, static_cast<_Float16 *>(work), static_cast<uint32_t>(nk));
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }

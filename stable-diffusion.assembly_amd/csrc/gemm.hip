@@ -649,8 +649,9 @@ __global__ __launch_bounds__(256) void mul_mat_kernel(MulMatArgs p) {
 // parts once for the workgroup, both written to LDS with each row's 16-byte
 // piece p at p ^ ((row >> 1) & 7), so that the 16 rows a fragment read
 // takes fall in 16 distinct groups of banks.  Rows past M and features past
-// N read the last row and are not stored.
-constexpr int kPanelTokens = 64, kPanelFeatures = 160, kPanelK = 64;
+// N read the last row and are not stored.  The panels are BM tokens by BN
+// features (PanelShape below), K in chunks of kPanelK.
+constexpr int kPanelK = 64;
 
 // The panel shapes, by preference: the first that gives 256 panels or more.
 struct PanelShape {
