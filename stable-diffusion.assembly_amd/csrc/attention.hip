@@ -1153,9 +1153,20 @@ __global__ __launch_bounds__(256, OCC) void attention_split_kernel(AttentionArgs
     // With key splits (splits > 1) the workgroup takes tiles [t0, t0 +
     // per) of the head's nk_all and writes partial results for
     // split_combine_kernel; nk is then its own count of tiles.
+    // Consecutive blocks of one XCD: the query blocks of a head, which read
+    // the same tiles of keys; with LOCAL (a few keys, every workgroup its own
+    // copies), the heads of a query block instead, whose rows of queries and
+    // of the output lie side by side in memory and share lines.
     const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
-    const uint32_t qb = b % static_cast<uint32_t>(a.qblocks);
-    const uint32_t rest = b / static_cast<uint32_t>(a.qblocks);
+    uint32_t qb, rest;
+    if constexpr (LOCAL) {
+        const uint32_t heads = static_cast<uint32_t>(a.b * a.h);
+        qb = b / heads;
+        rest = b - qb * heads;
+    } else {
+        qb = b % static_cast<uint32_t>(a.qblocks);
+        rest = b / static_cast<uint32_t>(a.qblocks);
+    }
     const int64_t sp = static_cast<int64_t>(rest % static_cast<uint32_t>(splits));
     const uint32_t bh = rest / static_cast<uint32_t>(splits);
     const int64_t hi = bh % a.h;
