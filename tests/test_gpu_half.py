@@ -253,6 +253,10 @@ ATTENTION_BF16 = [
     (64, 50, 100, 2, 1, 1, True, False),      # FP16 keys and values: the generic form
     (40, 100, 300, 2, 2, 1, False, True),     # the generic form on the fast form's operands
     (512, 40, 200, 1, 1, 1, False, False),    # the VAE's heads: the wide form
+    (384, 65, 130, 2, 1, 2, True, False),     # wide heads sharing FP16 keys and values
+    (320, 64, 1000, 1, 1, 1, False, False),   # wide heads over keys the single-precision form splits
+    (13, 37, 29, 4, 2, 3, False, False),      # edges: no multiple of a tile, heads sharing keys
+    (40, 1, 1, 1, 1, 1, False, False),        # one query, one key
 ]
 
 
