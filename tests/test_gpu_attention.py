@@ -187,6 +187,26 @@ def test_attention_generic_form(gpu, c):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("c", [c for c in CASES if not c[6] and c[0] in (32, 40, 64, 80, 96, 128, 160)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_attention_single_precision_form(gpu, c):
+    """The fast form's products on the single-precision MFMA
+    (attention_fp32=1): within the bound of float64, and of the default split
+    form on the same operands -- two device routes to the same attention."""
+    sdhip.set_tuning("attention_fp32=1")
+    try:
+        q, k, v, y, scale = attention_case(gpu, *c, seed=c[0] + 13)
+    finally:
+        sdhip.set_tuning("")
+    _, _, _, y_split, _ = attention_case(gpu, *c, seed=c[0] + 13)
+    exact, mag = orc.exact_attention(q, k, v, scale)
+    err = orc.metric(y, exact, mag)
+    apart = orc.metric(y, y_split.astype(np.float64), mag)
+    print(f"attention single precision {c}: {err:.3g} of exact, {apart:.3g} from the split form")
+    assert err <= BOUND and apart <= 2 * BOUND
+
+
+@pytest.mark.gpu
 def test_attention_work_buffer_checked(gpu):
     """The split form's tiles of keys and values go to the work buffer: a
     buffer short of sdhip_attention_work_size is an error, not a launch."""
