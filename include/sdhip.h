@@ -219,9 +219,11 @@ sdhip_status sdhip_conv2d(const sdhip_tensor *kernel, const sdhip_tensor *input,
  * [d, lq, h, b] F32 (any strides, nb[0] = 4), k ne = [d, lk, hk, b] and v ne =
  * [dv, lk, hk, b] F32 or F16, y ne = [dv, h, lq, b] F32 contiguous; head h
  * reads key head h / (h / hk).  scale, max_bias and softcap are op_params[0..2];
- * only max_bias = softcap = 0 is taken, heads of up to 512 dimensions, in
- * the bits mode too, with every group of keys its tuning gives (a multiple of
- * 4 from 4 to 1024, quant.cc:59-67).  The work
+ * only max_bias = softcap = 0 is taken, heads of any size (values of more
+ * than 512 dimensions in slices of 512, each computing the same scores); in
+ * the bits mode, where its quantized form applies (256 keys or more), heads
+ * of up to 512 dimensions, with every group of keys its tuning gives (a
+ * multiple of 4 from 4 to 1024, quant.cc:59-67).  The work
  * buffer: in the bits mode the quantized operands; otherwise, for
  * single-precision keys and values of the head sizes 32, 40, 64, 80, 96, 128
  * and 160, the keys and values split into FP16 parts, tile by tile, and,

@@ -28,8 +28,9 @@ struct AttentionArgs {
     int64_t qblocks;
 };
 
-// The most dimensions of a head the kernels take (queries, keys and values):
-// up to 256 in one pass, wider heads (the VAE's 512) by chunks of 128.
+// The most dimensions of a head the quantized form takes (queries, keys and
+// values).  The single-precision forms take any: up to 256 in one pass, wider
+// heads (the VAE's 512) by chunks of 128, values past 512 in slices of 512.
 constexpr int64_t kAttentionMaxDims = 512;
 
 // The bits mode of self-attention (qattention.hip): the operands, the

@@ -271,12 +271,19 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
     const int lr = lane & 15;
     const int lg = lane >> 4;
 
-    // Neighbouring blocks share a split's keys and values.
+    // Neighbouring blocks share a split's keys and values.  Values of more
+    // than 16 NDV dimensions go in slices of 16 NDV, a block each, every
+    // slice with the same scores, maxima and sums.
     const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint32_t qb = b % static_cast<uint32_t>(a.qblocks);
     const uint32_t rest = b / static_cast<uint32_t>(a.qblocks);
     const int64_t sp = rest % splits;
-    const uint32_t bh = static_cast<uint32_t>(rest / splits);
+    const uint32_t rest2 = static_cast<uint32_t>(rest / splits);
+    const uint32_t heads = static_cast<uint32_t>(a.b * a.h);
+    const uint32_t slice = rest2 / heads;
+    const uint32_t bh = rest2 - slice * heads;
+    const int64_t v0 = static_cast<int64_t>(slice) * 16 * NDV;  // the slice's first dimension
+    const int64_t dvs = a.dv - v0;                               // the values' dimensions from it
     const int64_t k_begin = sp * key_len;
     const int64_t k_end = k_begin + key_len < a.lk ? k_begin + key_len : a.lk;
     const int64_t hi = bh % a.h;
@@ -285,7 +292,7 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
     const int64_t q0 = static_cast<int64_t>(qb) * kQueries;
     const int64_t qbase = bi * a.qnb3 + hi * a.qnb2;
     const int64_t kbase = bi * a.knb3 + kh * a.knb2;
-    const int64_t vbase = bi * a.vnb3 + kh * a.vnb2;
+    const int64_t vbase = bi * a.vnb3 + kh * a.vnb2 + v0;
 
     float4v o[NDV];
 #pragma unroll
@@ -359,7 +366,7 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
             const int j = idx / (16 * NDV), e = idx - j * (16 * NDV);
             const int64_t key = k0 + j;
             vs[j * a.ldv + e] =
-                (e < a.dv && key < k_end) ? bf16_operand(load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e), a.bf16) : 0.0f;
+                (e < dvs && key < k_end) ? bf16_operand(load_kv<VHALF>(a.v, vbase + key * a.vnb1 + e), a.bf16) : 0.0f;
         }
         __syncthreads();
 
@@ -398,28 +405,28 @@ __global__ __launch_bounds__(256) void attention_wide_kernel(AttentionArgs a, in
     if (i >= a.lq) return;
     if (part.o != nullptr) {
         const int64_t at = (static_cast<int64_t>(bh) * splits + sp) * a.lq + i;
-        if (lg == 0) {
+        if (lg == 0 && slice == 0) {
             part.m[at] = m;
             part.l[at] = l;
         }
-        float *po = part.o + at * a.dv;
+        float *po = part.o + at * a.dv + v0;
 #pragma unroll
         for (int c = 0; c < NDV; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int e = 16 * c + 4 * lg + r;
-                if (e < a.dv) po[e] = o[c][r];
+                if (e < dvs) po[e] = o[c][r];
             }
         return;
     }
     const float reciprocal = static_cast<float>(1.0 / l);
-    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1;
+    float *out = a.y + bi * a.ynb3 + i * a.ynb2 + hi * a.ynb1 + v0;
 #pragma unroll
     for (int c = 0; c < NDV; ++c)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int e = 16 * c + 4 * lg + r;
-            if (e < a.dv) out[e] = o[c][r] * reciprocal;
+            if (e < dvs) out[e] = o[c][r] * reciprocal;
         }
 }
 
@@ -1828,7 +1835,11 @@ hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
     const WideSplits w = wide_splits(a);
     const WidePartial part = w.splits > 1 ? wide_partial(work, a, w.splits) : WidePartial{nullptr, nullptr, nullptr};
     const size_t lds = sizeof(float) * (kQueries * kWideLd + kKeys * kWideLd + kKeys * a.ldv);
-    dim3 grid(static_cast<uint32_t>(a.qblocks * w.splits * a.h * a.b)), block(256);
+    // Values of more than 16 NDV dimensions (heads past 512) in slices.
+    const int64_t slices = ceil_div(a.dv, 16 * NDV);
+    const int64_t blocks = a.qblocks * w.splits * a.h * a.b * slices;
+    if (blocks >= (int64_t{1} << 24)) return hipErrorInvalidValue;  // 256-thread blocks of one dimension
+    dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     const auto launch = [&](auto kernel) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -1844,7 +1855,7 @@ hipError_t launch_wide(AttentionArgs a, void *work, hipStream_t stream) {
                        a.knb3 % 4 == 0 && a.vnb3 % 4 == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
     if (!a.khalf && !a.vhalf && a.dp > 384 && a.dp <= 512 && a.d % 4 == 0 && a.dv % 4 == 0 && rows4 && NDV == 32 &&
-        tuning().attention_generic == 0 && !a.bf16) {
+        slices == 1 && tuning().attention_generic == 0 && !a.bf16) {
         const size_t lds2 = sizeof(float) * (kKeys * (512 + 4) + kKeys * (16 * NDV + 4));
         hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(attention_wide2_kernel<512, NDV>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));

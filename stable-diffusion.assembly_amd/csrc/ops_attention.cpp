@@ -114,14 +114,17 @@ int sdhip_attention_supported(const sdhip_tensor *q, const sdhip_tensor *k, cons
     if (q == nullptr || k == nullptr || v == nullptr || y == nullptr) return 0;
     // No mask, ALiBi or soft cap; q single precision, k and v single
     // precision or FP16, each of elements one after another along ne[0]; the
-    // heads of q a multiple of those of k (attention.cc:828-845).  Heads of
-    // more than kAttentionMaxDims dimensions are left to the caller.
+    // heads of q a multiple of those of k (attention.cc:828-845), heads of
+    // any size.  The quantized form (the bits mode, from 256 keys) takes heads
+    // of up to kAttentionMaxDims dimensions; wider ones in that mode are left
+    // to the caller.
     const bool shapes = q->ne[0] == k->ne[0] && k->ne[1] == v->ne[1] && k->ne[2] == v->ne[2] && k->ne[2] > 0 &&
                         q->ne[2] % k->ne[2] == 0 && q->ne[3] == k->ne[3] && q->ne[3] == v->ne[3] && k->ne[1] >= 1 &&
                         y->ne[0] == v->ne[0] && y->ne[1] == q->ne[2] && y->ne[2] == q->ne[1] && y->ne[3] == q->ne[3];
     const bool taken = max_bias == 0.0f && softcap == 0.0f && holds_f32(q) && kv_type(k) && kv_type(v) &&
-                       holds_f32(y) && contiguous(y) && shapes && q->ne[0] <= kAttentionMaxDims &&
-                       v->ne[0] <= kAttentionMaxDims && q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 &&
+                       holds_f32(y) && contiguous(y) && shapes &&
+                       (!quantized_attention(k) || (q->ne[0] <= kAttentionMaxDims && v->ne[0] <= kAttentionMaxDims)) &&
+                       q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 &&
                        q->nb[3] % 4 == 0 && k->nb[1] % k->nb[0] == 0 && k->nb[2] % k->nb[0] == 0 &&
                        k->nb[3] % k->nb[0] == 0 && v->nb[1] % v->nb[0] == 0 && v->nb[2] % v->nb[0] == 0 &&
                        v->nb[3] % v->nb[0] == 0;

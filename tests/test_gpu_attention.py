@@ -32,6 +32,8 @@ CASES = [
     (300, 33, 47, 2, 2, 1, False),     # wide heads of no multiple of the chunk or of 16
     (320, 64, 1000, 1, 1, 1, False),   # wide heads, the keys in three splits (the last ragged) merged
     (288, 40, 700, 2, 1, 1, True),     # two splits, heads sharing FP16 keys and values
+    (640, 70, 300, 2, 1, 1, False),    # past 512: the values in two slices
+    (1100, 33, 1000, 1, 1, 1, True),   # three slices, the last ragged, keys in splits, FP16 keys and values
 ]
 
 
@@ -162,12 +164,23 @@ def test_attention_peaked_scores(gpu, d):
 
 @pytest.mark.gpu
 def test_attention_not_taken(gpu):
-    """Heads of more than 512 dimensions are left to the caller; so is a soft cap."""
-    q = torch.zeros((1, 40, 1, 640), device=gpu)
-    y = torch.zeros((1, 40, 1, 640), device=gpu)
-    with pytest.raises(sdhip.SdhipError) as e:
-        sdhip.attention(q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), q.permute(0, 2, 1, 3), y, 0.05)
+    """Heads of more than 512 dimensions that the bits mode would quantize
+    (256 keys or more) are left to the caller; so is a soft cap."""
+    q = torch.zeros((1, 300, 1, 640), device=gpu)
+    y = torch.zeros((1, 300, 1, 640), device=gpu)
+    qv = q.permute(0, 2, 1, 3)
+    sdhip.set_tuning("bits=8")
+    try:
+        with pytest.raises(sdhip.SdhipError) as e:
+            sdhip.attention(qv, qv, qv, y, 0.05)
+    finally:
+        sdhip.set_tuning("")
     assert e.value.status == sdhip.UNSUPPORTED
+    q40 = torch.zeros((1, 40, 1, 40), device=gpu)
+    y40 = torch.zeros((1, 40, 1, 40), device=gpu)
+    assert not sdhip.load().sdhip_attention_supported(sdhip.desc(q40.permute(0, 2, 1, 3)),
+                                                      sdhip.desc(q40.permute(0, 2, 1, 3)),
+                                                      sdhip.desc(q40.permute(0, 2, 1, 3)), sdhip.desc(y40), 0.0, 30.0)
 
 
 @pytest.mark.gpu

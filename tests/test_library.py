@@ -155,11 +155,22 @@ def test_attention_and_norm_predicates():
     assert lib.sdhip_attention_supported(q, q, q, y, 0.0, 0.0)
     assert not lib.sdhip_attention_supported(q, q, q, y, 0.0, 30.0)   # a soft cap
     assert not lib.sdhip_attention_supported(q, q, q, y, 8.0, 0.0)    # ALiBi
-    # Heads of 512 (the VAE's) are taken, by chunks of the dimensions; wider ones are left to the caller.
+    # Heads of any size are taken, as attention_supported takes them
+    # (attention.cc:828-845): 512 (the VAE's) by chunks of the dimensions,
+    # wider ones with their values in slices; in the bits mode, where the
+    # quantized form applies (256 keys or more), up to 512.
     vae = tensor(F32, (1, 1, 4096, 512))
     assert lib.sdhip_attention_supported(vae, vae, vae, tensor(F32, (1, 4096, 1, 512)), 0.0, 0.0)
     big = tensor(F32, (1, 1, 4096, 640))
-    assert not lib.sdhip_attention_supported(big, big, big, tensor(F32, (1, 4096, 1, 640)), 0.0, 0.0)
+    assert lib.sdhip_attention_supported(big, big, big, tensor(F32, (1, 4096, 1, 640)), 0.0, 0.0)
+    few = tensor(F32, (1, 1, 200, 640))
+    try:
+        sdhip.set_tuning("bits=8")
+        assert not lib.sdhip_attention_supported(big, big, big, tensor(F32, (1, 4096, 1, 640)), 0.0, 0.0)
+        assert lib.sdhip_attention_supported(big, few, few, tensor(F32, (1, 4096, 1, 640)), 0.0, 0.0)
+        assert lib.sdhip_attention_supported(vae, vae, vae, tensor(F32, (1, 4096, 1, 512)), 0.0, 0.0)
+    finally:
+        sdhip.set_tuning("")
     x = tensor(F32, (2, 1280, 8, 8))
     assert lib.sdhip_group_norm_supported(x, x, 32)
     assert not lib.sdhip_group_norm_supported(x, x, 0)
