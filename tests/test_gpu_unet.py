@@ -45,12 +45,16 @@ def test_unet_graph_replays_equal_eager(gpu):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("tuning,low,high", [("", 0.0, 1e-5), ("bits=8,weight_group=0", 1e-5, 1e-2),
-                                             ("bits=8", 1e-5, 1e-2)])
+                                             ("bits=8", 1e-5, 1e-2), ("bits=16", 2e-6, 1e-4),
+                                             ("bits=16,half_format=1", 5e-5, 1e-3)])
 def test_sdxl_block(gpu, tuning, low, high):
     """The SDXL transformer block at a reduced size -- 300
     tokens, so that its self-attention is quantized too -- against float64
     torch: in single precision within 1e-5 of the output's norm, in the bits
-    mode within the quantization's error (and measurably quantized)."""
+    mode within the quantization's error (and measurably quantized); with
+    products of 16 bits, the FP16 form (x rounded to FP16, attention single
+    precision) and the bfloat16 form (both operands and attention's rounded to
+    bfloat16), each measurably rounded and the bfloat16 one the coarser."""
     import sdhip
 
     block = u.SdxlBlock(gpu, channels=256, heads=4, seed=2)
