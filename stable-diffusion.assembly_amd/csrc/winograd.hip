@@ -1309,13 +1309,16 @@ WorkLayout work_layout(const WinogradArgs &a) {
     l.small = small_path(a);
     if (l.small) {
         // Splits of the input channels: as many as give every CU one block
-        // in a single round (a round and a fraction leaves most CUs idle
-        // through the fraction: measured, 1280 -> 1280 at 8x8 by F(2x2), 80
-        // blocks a split, 3 splits 50.4 us, 4 53.5, 5 50.1, 2 58.7);
-        // winograd_splits: that many instead.  Two steps or more a split.
+        // in a single round, two with F(2x2), whose blocks of four waves
+        // then hide each other's latency (a round and a fraction leaves most
+        // CUs idle through the fraction: measured, 1280 -> 1280 at 8x8 by
+        // F(2x2), 80 blocks a split, 3 splits 50.4 us, 4 53.5, 5 50.1, 2
+        // 58.7, 6 48.6); winograd_splits: that many instead.  Two steps or
+        // more a split.
         l.tp = round_up(a.tiles, 16);
         const int64_t oc_blocks = ceil_div(a.oc, 16);
-        int64_t sp = tuning().winograd_splits > 0 ? tuning().winograd_splits : compute_units() / oc_blocks;
+        const int64_t rounds = a.m == 2 ? 2 : 1;
+        int64_t sp = tuning().winograd_splits > 0 ? tuning().winograd_splits : rounds * compute_units() / oc_blocks;
         sp = sp < 1 ? 1 : (sp > l.kp / 64 ? l.kp / 64 : sp);
         sp = sp < 1 ? 1 : sp;
         l.split_len = round_up(ceil_div(l.kp, sp), 32);
