@@ -156,7 +156,7 @@ sdhip_status gated_after(const float *p, float *out, int64_t rows, int64_t half,
 // `source` bytes), made if the arena has room and the stream is not being
 // captured, or null; `ready` whether an earlier call filled it.  The call that
 // gets an entry not ready fills it on its stream, then store_publish()es it.
-enum StoreLayout : int32_t { kStoreQuantizedLinear = 1, kStoreWinograd = 2 };
+enum StoreLayout : int32_t { kStoreQuantizedLinear = 1, kStoreWinograd = 2, kStoreWinogradSmall = 3 };
 void *store_entry(const void *begin, int32_t type, const int64_t ne[4], const int64_t nb[4], int32_t layout,
                   uint64_t variant, size_t source, size_t bytes, hipStream_t stream, bool &ready);
 void store_publish(const void *entry);

@@ -1407,15 +1407,32 @@ sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
             SDHIP_LAUNCH((scales_kernel<M>), dim3(static_cast<uint32_t>(a.ic)), dim3(256), 0, stream, a, e,
                          a_oc);
         }
+        // Each split's exponents of the weights ([split][oc]) depend on the
+        // weights and the splits alone: kept in the store when it has room,
+        // as the reference keeps its weights' derived forms (store.cc:64-99),
+        // so that later calls read none of the weights for them.
+        const int64_t wne[4] = {3, 3, a.ic, a.oc};
+        const int64_t wnb[4] = {2, 6, 18, 18 * a.ic};
+        const uint64_t variant = static_cast<uint64_t>(M) | (static_cast<uint64_t>(l.splits) << 8) |
+                                 (static_cast<uint64_t>(l.split_len) << 32);
+        bool ready = false;
+        int32_t *ao_kept = static_cast<int32_t *>(
+            store_entry(a.w, SDHIP_TYPE_F16, wne, wnb, kStoreWinogradSmall, variant,
+                        static_cast<size_t>(a.oc * a.ic * 18), static_cast<size_t>(l.splits * a.oc * 4), stream,
+                        ready));
+        int32_t *ao = ao_kept != nullptr ? ao_kept : a_oc;
         _Float16 *vh = reinterpret_cast<_Float16 *>(v);
         {
-            // The inputs' transform, and beside it each split's exponents of
-            // the weights into a_oc ([split][oc]).
+            // The inputs' transform, and beside it, unless kept, each split's
+            // exponents of the weights.
             KernelScope scope(names[2].c_str(), stream);
             const int64_t iblocks = ceil_div(l.tp * l.kp, 256);
-            const int64_t wblocks = ceil_div(l.splits * a.oc, 4);
+            const int64_t wblocks = ready ? 0 : ceil_div(l.splits * a.oc, 4);
             SDHIP_LAUNCH((inputs_small_kernel<M>), dim3(static_cast<uint32_t>(iblocks + wblocks)), dim3(256), 0,
-                         stream, a, l.kp, l.tp, e, vh, iblocks, l.split_len, l.splits, a_oc);
+                         stream, a, l.kp, l.tp, e, vh, iblocks, l.split_len, l.splits, ao);
+            const hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return launched(err, "winograd inputs (small images)");
+            if (ao_kept != nullptr && !ready) store_publish(ao_kept);
         }
         {
             KernelScope scope(names[3].c_str(), stream);
@@ -1424,10 +1441,10 @@ sdhip_status run(const WinogradArgs &in, void *work, hipStream_t stream) {
             const dim3 block(64 * A);
             if (l.tp <= 16) {
                 SDHIP_LAUNCH((products_small_kernel<M, 1>), grid, block, 0, stream, a, l.kp, l.split_len,
-                             oc_blocks, e, vh, m, shift, a_oc);
+                             oc_blocks, e, vh, m, shift, ao);
             } else {
                 SDHIP_LAUNCH((products_small_kernel<M, 2>), grid, block, 0, stream, a, l.kp, l.split_len,
-                             oc_blocks, e, vh, m, shift, a_oc);
+                             oc_blocks, e, vh, m, shift, ao);
             }
         }
         KernelScope scope(names[4].c_str(), stream);

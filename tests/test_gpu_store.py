@@ -193,3 +193,32 @@ def test_kept_winograd_weights(gpu, arena, shape, path):
     assert orc.metric(y2, exact, mag) <= 2e-5
     sdhip.forget(k_d)
     assert sdhip.store_used() == (0, 0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ic,oc", [(64, 48), (1280, 1280)])
+def test_kept_small_images_weight_exponents(gpu, arena, ic, oc):
+    """The small images' path (8 x 8 maps, two images: 32 tiles) keeps each
+    split's exponents of the weights, which depend on the weights alone: the
+    first call fills the entry, later calls skip the weights' pass and give
+    the same outputs bit for bit as a call without a store; new inputs agree
+    with the oracle; sdhip_forget drops the entry."""
+    r = rng(ic + oc)
+    kh16, k32 = weights_f16(r, (oc, ic, 3, 3))
+    x = uniform(r, (2, ic, 8, 8), 1.0)
+    k_d, x_d = dev(kh16, gpu), dev(x, gpu)
+    assert sdhip.conv2d_path(k_d, x_d, unwritten((2, oc, 8, 8), gpu), sdhip.conv_params(1, 1, 1, 1, 1, 1)) == 2
+    sdhip.store_arena(None)
+    plain = convolve(gpu, k_d, x_d, 8, 8)
+    sdhip.store_arena(arena)
+    first = convolve(gpu, k_d, x_d, 8, 8)
+    assert sdhip.store_used()[1] == 1
+    again = convolve(gpu, k_d, x_d, 8, 8)
+    assert np.array_equal(first.view(np.uint32), plain.view(np.uint32))
+    assert np.array_equal(again.view(np.uint32), plain.view(np.uint32))
+    x2 = uniform(r, (2, ic, 8, 8), 4.0)
+    y2 = convolve(gpu, k_d, dev(x2, gpu), 8, 8)
+    exact, mag = orc.exact_conv2d(x2, k32, 1, 1, 1, 1, 1, 1)
+    assert orc.metric(y2, exact, mag) <= 2e-5
+    sdhip.forget(k_d)
+    assert sdhip.store_used() == (0, 0)
