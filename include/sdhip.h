@@ -135,7 +135,8 @@ void sdhip_forget(const void *begin, size_t size);
  * entries in (the quantized weights of the bits mode's MUL_MATs: bytes,
  * scales, offsets and sums; Winograd's transformed weights in single
  * precision with their exponents, which the reference keeps when its budget
- * allows, winograd.cc:2147-2149).  A NULL arena or 0 bytes keeps nothing (the
+ * allows, winograd.cc:2147-2149; for the small images' Winograd, each split's
+ * exponents of the weights).  A NULL arena or 0 bytes keeps nothing (the
  * default); a new arena forgets every entry of the last.  An entry is filled
  * by the first call that needs it, on that call's stream, and read by later
  * calls: they must be ordered after it on the device (one stream, or an
