@@ -379,16 +379,28 @@ __global__ __launch_bounds__(kThreads) void norm_resident_kernel(NormArgs a) {
     }
 }
 
-// NORM of rows of ne0 <= 256 Q, a multiple of 4, rows 16-byte aligned: one
-// wave per row, Q float4 a lane (lane + 64 u), x read once; the same
-// statistics as norm_kernel (sums in double, whose order moves no float
-// result).  A chain step whose operand runs along the row with stride 1 and
-// 16-byte aligned rows loads it a float4 at a time.
-template <int Q>
+// The sum of v over each group of L lanes (L a power of two up to 64).
+template <int L>
+__device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// NORM of rows of ne0 <= 4 L Q, a multiple of 4, rows 16-byte aligned: L
+// lanes per row (64, a wave; or 16, four rows a wave, for short rows, whose
+// lanes would idle and whose reductions would weigh on a wave to each), Q
+// float4 a lane (lane + L u), x read once; the same statistics as
+// norm_kernel (sums in double, whose order moves no float result).  A chain
+// step whose operand runs along the row with stride 1 and 16-byte aligned
+// rows loads it a float4 at a time.  A row's L lanes return together, so no
+// reduction reads a lane that has left.
+template <int Q, int L>
 __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(NormArgs a) {
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    const int64_t row =
+        (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6)) * (64 / L) + ((threadIdx.x & 63) / L);
     if (row >= a.rows) return;
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & (L - 1);
     const int64_t i1 = row % a.ne1;
     const int64_t i2 = (row / a.ne1) % a.ne2;
     const int64_t i3 = row / (a.ne1 * a.ne2);
@@ -398,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(NormArgs a) {
     float v[Q][4];
 #pragma unroll
     for (int u = 0; u < Q; ++u) {
-        const int j = lane + 64 * u;
+        const int j = lane + L * u;
         const float4v q4 = x[j < n4 ? j : n4 - 1];
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[u][k] = q4[k];
@@ -411,7 +423,7 @@ __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(NormArgs a) {
         const bool vec = st.nb[0] == 1 && (reinterpret_cast<uintptr_t>(base) & 15) == 0;
 #pragma unroll
         for (int u = 0; u < Q; ++u) {
-            const int j = lane + 64 * u;
+            const int j = lane + L * u;
             const int64_t e = 4 * static_cast<int64_t>(j < n4 ? j : n4 - 1);
             if (vec) {
                 const float4v o4 = *reinterpret_cast<const float4v *>(base + e);
@@ -431,21 +443,21 @@ __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(NormArgs a) {
     double s = 0.0;
 #pragma unroll
     for (int u = 0; u < Q; ++u)
-        if (lane + 64 * u < n4)
+        if (lane + L * u < n4)
 #pragma unroll
             for (int k = 0; k < 4; ++k) s += static_cast<double>(v[u][k]);
-    const float mean = static_cast<float>(wave_sum(s) / static_cast<double>(a.ne0));
+    const float mean = static_cast<float>(group_sum<L>(s) / static_cast<double>(a.ne0));
     double q = 0.0;
 #pragma unroll
     for (int u = 0; u < Q; ++u) {
-        if (lane + 64 * u >= n4) continue;
+        if (lane + L * u >= n4) continue;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float d = v[u][k] - mean;
             q += static_cast<double>(__fmul_rn(d, d));
         }
     }
-    const float variance = static_cast<float>(wave_sum(q) / static_cast<double>(a.ne0));
+    const float variance = static_cast<float>(group_sum<L>(q) / static_cast<double>(a.ne0));
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(variance + a.eps));
 #pragma unroll
     for (int u = 0; u < Q; ++u)
@@ -483,7 +495,7 @@ __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(NormArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < Q; ++u) {
-        const int j = lane + 64 * u;
+        const int j = lane + L * u;
         if (j < n4) y[j] = float4v{v[u][0], v[u][1], v[u][2], v[u][3]};
     }
 }
@@ -621,14 +633,22 @@ hipError_t launch_norm(const NormArgs &a, hipStream_t stream) {
                        (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.xnb1 % 4 == 0 && a.xnb2 % 4 == 0 &&
                        a.xnb3 % 4 == 0 && a.ynb1 % 4 == 0 && a.ynb2 % 4 == 0 && a.ynb3 % 4 == 0;
     const int64_t quads = ceil_div(a.ne0, 256);
-    if (rows4 && quads <= 2) {
-        SDHIP_LAUNCH(norm_rows4_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+    // Rows of up to 320 numbers: 16 lanes a row, four rows a wave (8192 rows
+    // of 320: 8.7 -> 6.7 us; rows of 640 by 32 lanes, two a wave, measured
+    // slower than a wave each: 5.5 -> 5.8 us).
+    const dim3 grid16(static_cast<uint32_t>(ceil_div(a.rows, 4 * (kThreads / 64))));
+    if (rows4 && a.ne0 <= 128) {
+        SDHIP_LAUNCH((norm_rows4_kernel<2, 16>), grid16, dim3(kThreads), 0, stream, a);
+    } else if (rows4 && a.ne0 <= 320) {
+        SDHIP_LAUNCH((norm_rows4_kernel<5, 16>), grid16, dim3(kThreads), 0, stream, a);
+    } else if (rows4 && quads <= 2) {
+        SDHIP_LAUNCH((norm_rows4_kernel<2, 64>), grid, dim3(kThreads), 0, stream, a);
     } else if (rows4 && quads <= 3) {
-        SDHIP_LAUNCH(norm_rows4_kernel<3>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH((norm_rows4_kernel<3, 64>), grid, dim3(kThreads), 0, stream, a);
     } else if (rows4 && quads <= 5) {
-        SDHIP_LAUNCH(norm_rows4_kernel<5>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH((norm_rows4_kernel<5, 64>), grid, dim3(kThreads), 0, stream, a);
     } else if (rows4 && quads <= 8) {
-        SDHIP_LAUNCH(norm_rows4_kernel<8>, grid, dim3(kThreads), 0, stream, a);
+        SDHIP_LAUNCH((norm_rows4_kernel<8, 64>), grid, dim3(kThreads), 0, stream, a);
     } else if (a.ne0 <= 64 * 8) {
         SDHIP_LAUNCH(norm_resident_kernel<8>, grid, dim3(kThreads), 0, stream, a);
     } else if (a.ne0 <= 64 * 16) {

@@ -94,11 +94,14 @@ def test_norm(gpu, shape):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape,view", [((2, 50, 4), False), ((1, 7, 2048), False), ((1, 9, 2052), False),
-                                        ((2, 300, 640), True), ((3, 33, 1280), True), ((2, 64, 320), False)],
+                                        ((2, 300, 640), True), ((3, 33, 1280), True), ((2, 64, 320), False),
+                                        ((1, 7, 128), False), ((2, 33, 200), True), ((2, 65, 320), True),
+                                        ((1, 5, 324), True), ((2, 33, 600), False)],
                          ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
 def test_norm_rows_and_operands(gpu, shape, view):
-    """NORM over rows of 4 .. 2048 numbers a float4 at a time (2052: the
-    general form), the input a view whose rows lie further apart where
+    """NORM over rows of 4 .. 2048 numbers a float4 at a time (up to 320:
+    four rows a wave, 16 lanes each, row counts no multiple of four among
+    them; 2052: the general form), the input a view whose rows lie further apart where
     `view`; the chain a per-column scale, a residual of the output's shape
     starting one number past a 16-byte boundary (read a number at a time), a
     per-row scale (broadcast along the row) and the SiLU."""
