@@ -663,8 +663,12 @@ constexpr PanelShape kPanelShapes[] = {{64, 160}, {64, 64}};
 
 __device__ __forceinline__ int panel_swizzle(int row) { return (row >> 1) & 7; }
 
+// With `part`, the panels split along K: block b takes split b / panels, of
+// split_chunks chunks, and writes its sums, no chain, to part[s][m][n] for
+// mul_mat_sum_kernel, as the 64 x 64 core's splits do.
 template <bool GENERIC, int BM, int BN>
-__global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
+__global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p, float *__restrict__ part,
+                                                            int64_t split_chunks) {
     constexpr int KC = kPanelK;
     constexpr int WR = BM / 32, WC = 4 / WR;        // waves along the tokens, the features
     constexpr int TMW = 2, TNW = BN / (16 * WC);    // tiles of 16 a wave
@@ -676,10 +680,16 @@ __global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
     __shared__ __attribute__((aligned(16))) _Float16 lw[2][BN * KC];     // [buffer][feature][k]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave / WC, wc = wave % WC;
-    const uint32_t b = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t b_all = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t panels = static_cast<uint32_t>(((p.M + BM - 1) / BM) * p.col_blocks);
+    const uint32_t split = part != nullptr ? b_all / panels : 0;
+    const uint32_t b = b_all - split * panels;
     const int64_t m0 = static_cast<int64_t>(b / p.col_blocks) * BM;
     const int64_t n0 = static_cast<int64_t>(b % p.col_blocks) * BN;
-    const int64_t chunks = p.K / KC;
+    const int64_t chunks_all = p.K / KC;
+    const int64_t c_begin = part != nullptr ? static_cast<int64_t>(split) * split_chunks : 0;
+    const int64_t chunks =
+        part != nullptr ? (c_begin + split_chunks < chunks_all ? c_begin + split_chunks : chunks_all) : chunks_all;
     const float *xs[XQ];
     int xoff[XQ];
 #pragma unroll
@@ -729,11 +739,11 @@ __global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
     for (int j = 0; j < TNW; ++j)
 #pragma unroll
         for (int i = 0; i < TMW; ++i) acc[j][i] = float4v{};
-    load(0);
+    load(c_begin);
     store(0);
     lds_barrier();
-    for (int64_t c = 0; c < chunks; ++c) {
-        const int buf = static_cast<int>(c & 1);
+    for (int64_t c = c_begin; c < chunks; ++c) {
+        const int buf = static_cast<int>((c - c_begin) & 1);
         if (c + 1 < chunks) load(c + 1);
 #pragma unroll
         for (int h = 0; h < KC / 32; ++h) {
@@ -795,6 +805,28 @@ __global__ __launch_bounds__(256) void mul_mat_panel_kernel(MulMatArgs p) {
         for (int j = 0; j < TNW; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[i][j][e] = acc[j][i][e] * kSplitUp;
+    if (part != nullptr) {
+        // A split's sums, rows of N, a float4 where the four lie inside N.
+        float *ps = part + static_cast<int64_t>(split) * p.M * p.N;
+        const bool v4 = p.N % 4 == 0;
+#pragma unroll
+        for (int i = 0; i < TMW; ++i) {
+            const int64_t m = m0 + wr * 16 * TMW + 16 * i + col;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) {
+                if (v4 && nf[j] + 3 < p.N) {
+                    *reinterpret_cast<float4v *>(ps + m * p.N + nf[j]) =
+                        float4v{v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (nf[j] + e < p.N) ps[m * p.N + nf[j] + e] = v[i][j][e];
+                }
+            }
+        }
+        return;
+    }
     // Element e of tile (i, j) of a tensor of the output's rows ld apart.
     const auto at = [&](int i, int j, int e) -> int64_t {
         const int64_t n = nf[j] + e;
@@ -1800,9 +1832,9 @@ hipError_t launch_panels(const MulMatArgs &p, hipStream_t stream) {
     const dim3 grid(static_cast<uint32_t>(((p.M + BM - 1) / BM) * a.col_blocks));
     KernelScope scope("mul_mat", stream);
     if (panel_chain_fast(a, BN)) {
-        SDHIP_LAUNCH((mul_mat_panel_kernel<false, BM, BN>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_panel_kernel<false, BM, BN>), grid, dim3(256), 0, stream, a, nullptr, 0);
     } else {
-        SDHIP_LAUNCH((mul_mat_panel_kernel<true, BM, BN>), grid, dim3(256), 0, stream, a);
+        SDHIP_LAUNCH((mul_mat_panel_kernel<true, BM, BN>), grid, dim3(256), 0, stream, a, nullptr, 0);
     }
     return hipGetLastError();
 }
@@ -1820,10 +1852,34 @@ hipError_t launch_mul_mat_panels(const MulMatArgs &p, int mode, hipStream_t stre
     }
 }
 
-hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hipStream_t stream) {
+hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, bool panels, hipStream_t stream) {
     const MulMatSplitPlan l = mul_mat_split_plan(p);
     float *part = static_cast<float *>(work);
     MulMatArgs a = p;
+    // Panels of 64 x 160 split along K in at most as many splits, where K is
+    // whole chunks of the panels' and N takes whole panels, and the splits
+    // are 5 chunks or more and the blocks 128 or more: the same partial sums,
+    // into the same buffer.  (Measured: 512 x 1280 x 1280 21.1 -> 20.1 us,
+    // 512 x 1280 x 5120 37.1 -> 33.7; with splits of 4 chunks, the cross-
+    // attention's 154 x 1280 x 768 and 128 x 1280 x 1280, 10.2 -> 12.4 and
+    // 11.1 -> 13.4: those keep the 64 x 64 core.)
+    const int64_t chunks = p.K / kPanelK;
+    const int64_t split_chunks = (chunks + l.splits - 1) / l.splits;
+    const int64_t splits = (chunks + split_chunks - 1) / split_chunks;
+    const int64_t panel_blocks = ((p.M + 63) / 64) * (p.N / 160) * splits;
+    if (panels && p.K % kPanelK == 0 && p.N % 160 == 0 && split_chunks >= 5 && panel_blocks >= 128) {
+        a.col_blocks = p.N / 160;
+        const int64_t panels = ((p.M + 63) / 64) * a.col_blocks;
+        {
+            KernelScope scope("mul_mat", stream);
+            SDHIP_LAUNCH((mul_mat_panel_kernel<false, 64, 160>), dim3(static_cast<uint32_t>(panels * splits)),
+                         dim3(256), 0, stream, a, part, split_chunks);
+        }
+        KernelScope scope("mul_mat.sum", stream);
+        SDHIP_LAUNCH(mul_mat_sum_kernel, dim3(static_cast<uint32_t>((p.M * p.N + 255) / 256)), dim3(256), 0,
+                     stream, a, part, splits);
+        return hipGetLastError();
+    }
     a.col_blocks = (p.N + 63) / 64;
     {
         KernelScope scope("mul_mat", stream);

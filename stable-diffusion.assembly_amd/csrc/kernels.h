@@ -116,7 +116,9 @@ hipError_t launch_conv_panels(const ConvArgs &c, hipStream_t stream);
 // splits' partial sums.
 bool mul_mat_split_taken(const MulMatArgs &p);
 size_t mul_mat_split_work_size(const MulMatArgs &p);
-hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, hipStream_t stream);
+// panels: the 64 x 160 panels split along K where K and N take them (the
+// mul_mat_panels tuning), else the 64 x 64 core's splits.
+hipError_t launch_mul_mat_split(const MulMatArgs &p, void *work, GemmShape g, bool panels, hipStream_t stream);
 
 // The direct convolution by columns (gemm.hip): taken for kernels other than
 // 1x1 whose K = IC KH KW is a multiple of 32 and whose FP16 weights are

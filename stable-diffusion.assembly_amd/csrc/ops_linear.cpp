@@ -126,7 +126,7 @@ sdhip_status sdhip_mul_mat(const sdhip_tensor *w, const sdhip_tensor *x, const s
     } else if (mul_mat_split_taken(a)) {
         const size_t need = mul_mat_split_work_size(a);
         if (const sdhip_status ws = check_work("mul_mat", work, work_size, need); ws != SDHIP_OK) return ws;
-        s = launched(launch_mul_mat_split(a, work, gemm_shape(), st), "mul_mat split along K");
+        s = launched(launch_mul_mat_split(a, work, gemm_shape(), tuning().mul_mat_panels != 0, st), "mul_mat split along K");
     } else {
         s = launched(launch_mul_mat(a, gemm_shape(), st), "mul_mat");
     }

@@ -89,17 +89,20 @@ def test_mul_mat_residual(gpu, from_redirect):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("K,M,B", [
-    (4096, 150, 2),  # 20 blocks of 64 x 64: 16 splits of 8 K-steps (256), all alike
-    (2336, 150, 1),  # 12 blocks, 73 K-steps: 8 splits of 9 steps and a last one of a single step
+@pytest.mark.parametrize("K,N,M,B", [
+    (4096, 200, 150, 2),   # 20 blocks of 64 x 64: 16 splits of 8 K-steps (256), all alike
+    (2336, 200, 150, 1),   # 12 blocks, 73 K-steps: 8 splits of 9 steps and a last one of a single step
+    (1280, 1280, 256, 2),  # panels of 64 x 160 split along K: 64 panels, 4 splits of 5 chunks of 64
+    (2560, 320, 77, 2),    # 6 panels, splits of chunks, rows past M in the last panel
+    (2240, 640, 100, 1),   # 35 chunks: splits of 5, the panels' last ragged in M
 ])
 @pytest.mark.parametrize("from_redirect", [False, True])
-def test_mul_mat_split_chain(gpu, from_redirect, K, M, B):
+def test_mul_mat_split_chain(gpu, from_redirect, K, N, M, B):
     """A product of few output blocks and long K, split along K (about 512
-    blocks, each split 8 K-steps of 32 or more, the last one what is left):
+    blocks, each split 8 K-steps of 32 or more, the last one what is left;
+    where K and N take them, panels of 64 x 160 split along K into as many):
     the splits' sums added with bias, a per-token scale and a residual (or
     begun from the residual), the epilogue of the single pass."""
-    N = 200
     r = rng(13 + K)
     bias = dev(uniform(r, (N,), 1.0), gpu)
     scale = dev(uniform(r, (B, M, 1), 1.0), gpu)
